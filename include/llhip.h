@@ -1,0 +1,115 @@
+/* libllhip -- MI355X (gfx950) kernels of llaccel's bit-exact integer decoder datapath.
+ *
+ * C ABI loaded with ctypes by llaccel_amd/_lib.py.  The reference has no FFI for this
+ * path: its "plugin API" is the Python surface of python/llaccel/golden.py.  Each entry
+ * point below replaces the golden.py function cited beside it, computing the same
+ * integers on the GPU.
+ *
+ * Conventions
+ *   - Every tensor pointer is a DEVICE pointer; the caller owns all memory.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream); work is stream-ordered
+ *     and asynchronous.
+ *   - Return 0 on success; -EINVAL (-22) for a bad shape or parameter (shift outside
+ *     [0,63], multiplier outside u32, ...), -ERANGE (-34) for a position or domain error,
+ *     -EIO (-5) for a HIP runtime error.  llhip_last_error() returns the thread's message.
+ *   - Positions: functions taking (pos, pos_dev) use *pos_dev when pos_dev is non-NULL
+ *     (device-resident decode state, e.g. inside a captured graph), else pos.
+ *   - `ws` is a caller-allocated workspace of llhip_workspace_bytes() bytes, zero-filled
+ *     once at allocation.  Every call leaves it zero-filled again, so it needs no clearing
+ *     between calls (and none inside a captured graph).  Calls that share one workspace
+ *     must be ordered on one stream.
+ */
+#ifndef LLHIP_H
+#define LLHIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLHIP_ABI_VERSION 1
+
+int llhip_abi_version(void);
+const char* llhip_last_error(void);
+/* bytes of the shared workspace used by llhip_linear / llhip_attention */
+int64_t llhip_workspace_bytes(void);
+
+/* ---- elementwise primitives over n int64 values (operands pre-broadcast by the host) ---- */
+/* golden.py:35-45  rshr(v, s), s in [0,63] */
+int llhip_rshr(const int64_t* v, const int64_t* s, int64_t n, int64_t* out, void* stream);
+/* golden.py:48-61  kind 0 sat8, 1 satu8, 2 sat16, 3 satu16 */
+int llhip_sat(const int64_t* v, int64_t n, int kind, int64_t* out, void* stream);
+/* golden.py:64-65  mulshift(v, M, S) = rshr(v*M, S), int64 wrapping product */
+int llhip_mulshift(const int64_t* v, const int64_t* M, const int64_t* S, int64_t n, int64_t* out, void* stream);
+/* golden.py:92-97  requant16 (bits 16) / requant8 (bits 8) */
+int llhip_requant(const int64_t* acc, const int64_t* M, const int64_t* S, int64_t n, int bits, int64_t* out,
+                  void* stream);
+/* golden.py:68-81  isqrt48; each t must be in [0, 2^48) */
+int llhip_isqrt48(const int64_t* t, int64_t n, int64_t* out, void* stream);
+/* golden.py:84-88  udiv(a, b) = (a // max(b,1)) & 0xFFFFFFFF; a, b >= 0 */
+int llhip_udiv(const int64_t* a, const int64_t* b, int64_t n, int64_t* out, void* stream);
+/* golden.py:101-107 silu16(x, Mi, Si, sh_out) on int64 values */
+int llhip_silu16_i64(const int64_t* x, int64_t n, int64_t Mi, int64_t Si, int64_t sh_out, int64_t* out,
+                     void* stream);
+/* golden.py:111-112 vmul on int64 values */
+int llhip_vmul_i64(const int64_t* a, const int64_t* b, int64_t n, int64_t sh, int64_t* out, void* stream);
+/* golden.py:115-116 vadd on int64 values */
+int llhip_vadd_i64(const int64_t* a, const int64_t* b, int64_t n, int64_t sh_b, int64_t* out, void* stream);
+/* golden.py:119-120 vquant on int64 values */
+int llhip_vquant_i64(const int64_t* x, int64_t n, int64_t M, int64_t S, int64_t* out, void* stream);
+
+/* ---- vec engine on datapath types (NUMERICS.md: x, g i16; quant out i8) ---- */
+/* golden.py:124-137  RMSNorm of `rows` rows of K i16 values (row strides ldx/ldy elements) */
+int llhip_rmsnorm(const int16_t* x, int64_t rows, int64_t K, int64_t ldx, const int16_t* g, int64_t eps_t, int64_t C,
+                  int64_t sh_post, int16_t* y, int64_t ldy, void* stream);
+/* golden.py:119-120  vquant i16 -> i8 over n values */
+int llhip_quant(const int16_t* x, int64_t n, int64_t M, int64_t S, int8_t* y, void* stream);
+/* golden.py:101-107  silu16 i16 -> i16 */
+int llhip_silu(const int16_t* x, int64_t n, int64_t Mi, int64_t Si, int64_t sh_out, int16_t* y, void* stream);
+/* golden.py:111-112  vmul */
+int llhip_vmul(const int16_t* a, const int16_t* b, int64_t n, int64_t sh, int16_t* y, void* stream);
+/* golden.py:115-116  vadd */
+int llhip_vadd(const int16_t* a, const int16_t* b, int64_t n, int64_t sh_b, int16_t* y, void* stream);
+/* golden.py:141-158  RoPE of x [M][H*D] (row stride ldx) with Q1.14 tables [max_seq][D/2]; row m at pos+m */
+int llhip_rope(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, const int16_t* cos_tab,
+               const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev, int16_t* y,
+               int64_t ldy, void* stream);
+
+/* ---- gemm engine ---- */
+/* golden.py:316-342  out[M][N] = epilogue(requant(A[M][K] . W[N][K]^T + bias)).
+ * A i8 (row stride lda), W i8 row-major [N][K], rq int32 pairs [N][2] = {M_n, S_n},
+ * bias int32 [N] or NULL, aux i16 [M][N] (row stride ldaux) for resadd/mul.
+ * epilogue: 0 none, 1 resadd, 2 silu, 3 mul.  out_i8 selects i8 output (epilogue 0 only),
+ * otherwise i16.  The rq table's S_n must lie in [0,63] (checked by the caller). */
+int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_t* W, int64_t N, const int32_t* rq,
+                 const int32_t* bias, int epilogue, const int16_t* aux, int64_t ldaux, int64_t aux_shift,
+                 int64_t silu_Mi, int64_t silu_Si, int64_t silu_sh, int out_i8, void* out, int64_t ldo, void* ws,
+                 void* stream);
+/* golden.py:217-240  exact integer A[M][K] (int64) . W[N][K]^T (int8) -> int64 [M][N] */
+int llhip_exact_matmul(const int64_t* A, int64_t M, int64_t K, const int8_t* W, int64_t N, int64_t* out,
+                       void* stream);
+
+/* ---- attn engine ---- */
+/* golden.py:344-351  K/V rows of M positions into caches [Hkv][max_seq][D] at pos+m */
+int llhip_kv_write(const int8_t* k, const int8_t* v, int64_t M, int64_t Hkv, int64_t D, int64_t ldk, int64_t ldv,
+                   int64_t pos, const int32_t* pos_dev, int8_t* kc, int8_t* vc, int64_t max_seq, void* stream);
+/* golden.py:353-366 (+ attention_head golden.py:162-180)  causal GQA attention of q [M][H*D]
+ * over caches [Hkv][max_seq][D]; row m sees keys 0..pos+m.  prob_bits 8 or 15. */
+int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
+                    const int32_t* pos_dev, const int8_t* kc, const int8_t* vc, int64_t max_seq, int64_t Ms,
+                    int64_t Ss, int64_t Mo, int64_t So, int64_t prob_bits, int8_t* out, int64_t ldo, void* ws,
+                    void* stream);
+
+/* ---- host-loop helpers ---- */
+/* golden.py:369-373  rows[m] = embed[tokens[m]] for m < n_tokens, zero for n_tokens <= m < M.
+ * tokens are int32 row indices already resolved by the caller to [0, vocab_rows). */
+int llhip_embed_rows(const int16_t* embed, int64_t vocab_rows, int64_t dim, const int32_t* tokens, int64_t n_tokens,
+                     int64_t M, int16_t* rows, void* stream);
+/* golden.py:376-377  idx[r] = first argmax of logits[r][0:vocab] (row stride ld) */
+int llhip_argmax_i16(const int16_t* logits, int64_t rows, int64_t ld, int64_t vocab, int32_t* idx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

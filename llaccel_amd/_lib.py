@@ -1,0 +1,93 @@
+"""ctypes binding of libllhip.so (C ABI declared in include/llhip.h).
+
+There is no fallback: if the shared object is missing the import of any compute entry
+point raises, naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+import errno
+import re
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libllhip.so"
+HEADER = PKG.parent / "include" / "llhip.h"
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+
+# name -> argument types (pointers as void*, integers as int64 unless the header says int)
+_SIGS = {
+    "llhip_abi_version": [],
+    "llhip_last_error": [],
+    "llhip_workspace_bytes": [],
+    "llhip_rshr": [_p, _p, _i64, _p, _p],
+    "llhip_sat": [_p, _i64, _i32, _p, _p],
+    "llhip_mulshift": [_p, _p, _p, _i64, _p, _p],
+    "llhip_requant": [_p, _p, _p, _i64, _i32, _p, _p],
+    "llhip_isqrt48": [_p, _i64, _p, _p],
+    "llhip_udiv": [_p, _p, _i64, _p, _p],
+    "llhip_silu16_i64": [_p, _i64, _i64, _i64, _i64, _p, _p],
+    "llhip_vmul_i64": [_p, _p, _i64, _i64, _p, _p],
+    "llhip_vadd_i64": [_p, _p, _i64, _i64, _p, _p],
+    "llhip_vquant_i64": [_p, _i64, _i64, _i64, _p, _p],
+    "llhip_rmsnorm": [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "llhip_quant": [_p, _i64, _i64, _i64, _p, _p],
+    "llhip_silu": [_p, _i64, _i64, _i64, _i64, _p, _p],
+    "llhip_vmul": [_p, _p, _i64, _i64, _p, _p],
+    "llhip_vadd": [_p, _p, _i64, _i64, _p, _p],
+    "llhip_rope": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _p],
+    "llhip_linear": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p,
+                     _i64, _p, _p],
+    "llhip_exact_matmul": [_p, _i64, _i64, _p, _i64, _p, _p],
+    "llhip_kv_write": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
+    "llhip_attention": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
+                        _i64, _p, _p],
+    "llhip_embed_rows": [_p, _i64, _i64, _p, _i64, _i64, _p, _p],
+    "llhip_argmax_i16": [_p, _i64, _i64, _i64, _p, _p],
+}
+_RESTYPES = {"llhip_last_error": ctypes.c_char_p, "llhip_workspace_bytes": _i64}
+
+_LIB = None
+
+
+class LibraryNotBuilt(RuntimeError):
+    pass
+
+
+def declared_symbols() -> list[str]:
+    """Every entry point declared in include/llhip.h."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(llhip_\w+)\s*\(", text)))
+
+
+def lib():
+    """The loaded library (raises LibraryNotBuilt if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise LibraryNotBuilt(f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+                                  f"g.build()'` (make -C llaccel_amd/csrc)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _LIB = L
+    return _LIB
+
+
+def check(rc: int, what: str) -> None:
+    """Map a negative errno return code to the exception the reference raises."""
+    if rc == 0:
+        return
+    msg = (lib().llhip_last_error() or b"").decode()
+    if rc in (-errno.EINVAL, -errno.ERANGE):
+        raise ValueError(msg or what)
+    raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)

@@ -1,0 +1,227 @@
+// attn engine of libllhip: KV-cache write (golden.py:344-351) and causal GQA
+// integer attention (golden.py:353-366 over attention_head golden.py:162-180,
+// NUMERICS.md "Attention").
+//
+// The integer softmax needs three reductions over all T keys in order -- the
+// maximum score, the sum of LUT exponentials (which depend on that maximum) and
+// the probability-weighted value sum (which depends on the sum through inv) --
+// so it cannot be computed online per tile.  Each of them is an exact integer
+// reduction, so any reduction order gives the reference's result.
+//
+// attention_rowhead: one 256-thread block per (row m, query head h).  Scores for
+// all T keys are staged in LDS (int32), block reductions give max and sum, and
+// the value pass splits the head dimension into 16-byte chunks across threads
+// and the keys across thread groups.
+#include "../../include/llhip.h"
+#include "common.h"
+
+namespace llhip {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int ATTN_MAX_T = 12000;  // scores + value partials stay within a 64 KiB block allocation
+
+struct AttnArgs {
+  const int8_t* q;
+  const int8_t* kc;
+  const int8_t* vc;
+  int8_t* out;
+  const int32_t* pos_dev;
+  int64_t ldq, ldo, max_seq;
+  int64_t Ms, Mo;
+  int Ss, So;
+  int H, Hkv, pos, pb;
+  int lds_T;  // score slots in LDS
+};
+
+__device__ __forceinline__ int32_t block_max_i32(int32_t v, int32_t* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, int32_t* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (int32_t)v;
+  __syncthreads();
+  return (uint32_t)red[0] + (uint32_t)red[1] + (uint32_t)red[2] + (uint32_t)red[3];
+}
+
+__device__ __forceinline__ int32_t sbyte(int w, int i) { return (int32_t)(int8_t)((uint32_t)w >> (8 * i)); }
+
+template <int D>
+__global__ __launch_bounds__(256) void attention_rowhead(AttnArgs p) {
+  extern __shared__ int32_t smem[];
+  __shared__ int32_t red[4];
+  constexpr int DC = D / 16;  // 16-byte chunks per key row
+  constexpr int TG = 256 / DC;
+  int32_t* sc = smem;              // [lds_T] scores, then probabilities
+  int32_t* part = smem + p.lds_T;  // [TG][D] value-pass partial sums
+
+  const int h = blockIdx.x;
+  const int m = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int pos0 = p.pos_dev ? *p.pos_dev : p.pos;
+  const int T = pos0 + m + 1;
+  const int g = h / (p.H / p.Hkv);
+  const int8_t* K = p.kc + (int64_t)g * p.max_seq * D;
+  const int8_t* V = p.vc + (int64_t)g * p.max_seq * D;
+  const int8_t* qr = p.q + (int64_t)m * p.ldq + (int64_t)h * D;
+
+  // scores s[t] = q . k[t] (int32, |s| <= D * 2^14)
+  v4i qv[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) qv[c] = *reinterpret_cast<const v4i*>(qr + 16 * c);
+  int32_t lmax = INT32_MIN;
+  for (int t = tid; t < T; t += 256) {
+    const v4i* kr = reinterpret_cast<const v4i*>(K + (int64_t)t * D);
+    int32_t s = 0;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const v4i kv = kr[c];
+      s = __builtin_amdgcn_sdot4(qv[c].x, kv.x, s, false);
+      s = __builtin_amdgcn_sdot4(qv[c].y, kv.y, s, false);
+      s = __builtin_amdgcn_sdot4(qv[c].z, kv.z, s, false);
+      s = __builtin_amdgcn_sdot4(qv[c].w, kv.w, s, false);
+    }
+    sc[t] = s;
+    lmax = max(lmax, s);
+  }
+  const int32_t mx = block_max_i32(lmax, red);
+
+  // p[t] = LUT(mulshift(mx - s[t], Ms, Ss)), sum
+  uint32_t lsum = 0;
+  for (int t = tid; t < T; t += 256) {
+    const uint32_t pr = lut_prob(mulshift((int64_t)mx - sc[t], p.Ms, p.Ss));
+    sc[t] = (int32_t)pr;
+    lsum += pr;
+  }
+  const uint32_t total = block_sum_u32(lsum, red);
+  const uint32_t inv = (uint32_t)((1ull << 31) / (uint64_t)(total > 1u ? total : 1u));
+  const int32_t cap = (1 << p.pb) - 1;
+  const int shp = 31 - p.pb;
+  for (int t = tid; t < T; t += 256) {
+    const int64_t pn = rshr((int64_t)sc[t] * (int64_t)inv, shp);
+    sc[t] = (int32_t)(pn < cap ? pn : cap);
+  }
+  __syncthreads();
+
+  // o[d] = sum_t pn[t] * v[t][d]
+  const int dc = tid % DC, tg = tid / DC;
+  int32_t acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0;
+  for (int t = tg; t < T; t += TG) {
+    const v4i vv = *reinterpret_cast<const v4i*>(V + (int64_t)t * D + 16 * dc);
+    const int32_t pn = sc[t];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i] += pn * sbyte(vv.x, i);
+      acc[4 + i] += pn * sbyte(vv.y, i);
+      acc[8 + i] += pn * sbyte(vv.z, i);
+      acc[12 + i] += pn * sbyte(vv.w, i);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) part[tg * D + 16 * dc + i] = acc[i];
+  __syncthreads();
+  for (int d = tid; d < D; d += 256) {
+    int32_t o = 0;
+    for (int j = 0; j < TG; ++j) o += part[j * D + d];
+    if (p.pb == 15) o = rshr32(o, 7);
+    p.out[(int64_t)m * p.ldo + (int64_t)h * D + d] = (int8_t)sat8(mulshift(o, p.Mo, p.So));
+  }
+}
+
+__global__ void kv_write_kernel(const int8_t* __restrict__ k, const int8_t* __restrict__ v, int64_t M, int Hkv, int D,
+                                int64_t ldk, int64_t ldv, int pos, const int32_t* __restrict__ pos_dev,
+                                int8_t* __restrict__ kc, int8_t* __restrict__ vc, int64_t max_seq) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_row = (int64_t)Hkv * D;
+  if (idx >= M * per_row) return;
+  const int64_t m = idx / per_row;
+  const int rem = (int)(idx % per_row);
+  const int h = rem / D, d = rem % D;
+  const int p0 = pos_dev ? *pos_dev : pos;
+  const int64_t dst = ((int64_t)h * max_seq + p0 + m) * D + d;
+  kc[dst] = k[m * ldk + rem];
+  vc[dst] = v[m * ldv + rem];
+}
+
+}  // namespace llhip
+
+using namespace llhip;
+
+extern "C" {
+
+int llhip_kv_write(const int8_t* k, const int8_t* v, int64_t M, int64_t Hkv, int64_t D, int64_t ldk, int64_t ldv,
+                   int64_t pos, const int32_t* pos_dev, int8_t* kc, int8_t* vc, int64_t max_seq, void* stream) {
+  if (M < 0 || Hkv <= 0 || D <= 0) return fail(-EINVAL, "kv_write: bad geometry");
+  if (ldk < Hkv * D || ldv < Hkv * D) return fail(-EINVAL, "kv_write: leading dimension too small");
+  if (!pos_dev && (pos < 0 || pos + M > max_seq))
+    return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)pos, (long long)(pos + M - 1),
+                (long long)max_seq);
+  const int64_t total = M * Hkv * D;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(kv_write_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, k, v, M,
+                     (int)Hkv, (int)D, ldk, ldv, (int)pos, pos_dev, kc, vc, max_seq);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
+                    const int32_t* pos_dev, const int8_t* kc, const int8_t* vc, int64_t max_seq, int64_t Ms,
+                    int64_t Ss, int64_t Mo, int64_t So, int64_t prob_bits, int8_t* out, int64_t ldo, void* ws,
+                    void* stream) {
+  (void)ws;
+  if (prob_bits != 8 && prob_bits != 15) return fail(-EINVAL, "attention prob_bits must be 8 or 15");
+  if (M < 0 || H <= 0 || Hkv <= 0 || H % Hkv) return fail(-EINVAL, "attention: H must be a multiple of Hkv");
+  if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256)
+    return fail(-EINVAL, "attention: head_dim %lld not in {16,32,64,128,256}", (long long)D);
+  if (!u32_ok(Ms) || !u32_ok(Mo) || !shift_ok(Ss) || !shift_ok(So))
+    return fail(-EINVAL, "attention: multipliers must be u32, shifts in [0,63]");
+  if (ldq < H * D || ldo < H * D) return fail(-EINVAL, "attention: leading dimension too small");
+  if (!pos_dev && (pos < 0 || pos + M > max_seq))
+    return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)pos, (long long)(pos + M - 1),
+                (long long)max_seq);
+  if (M == 0) return 0;
+  const int64_t tmax = pos_dev ? max_seq : pos + M;
+  if (tmax > ATTN_MAX_T) return fail(-EINVAL, "attention: context %lld exceeds %d", (long long)tmax, ATTN_MAX_T);
+  AttnArgs p{};
+  p.q = q;
+  p.kc = kc;
+  p.vc = vc;
+  p.out = out;
+  p.pos_dev = pos_dev;
+  p.ldq = ldq;
+  p.ldo = ldo;
+  p.max_seq = max_seq;
+  p.Ms = Ms;
+  p.Mo = Mo;
+  p.Ss = (int)Ss;
+  p.So = (int)So;
+  p.H = (int)H;
+  p.Hkv = (int)Hkv;
+  p.pos = (int)pos;
+  p.pb = (int)prob_bits;
+  p.lds_T = (int)((tmax + 3) / 4 * 4);
+  const size_t lds = sizeof(int32_t) * ((size_t)p.lds_T + 256 * 16);
+  dim3 grid((unsigned)H, (unsigned)M);
+  hipStream_t s = (hipStream_t)stream;
+  switch (D) {
+    case 16: hipLaunchKernelGGL(attention_rowhead<16>, grid, dim3(256), lds, s, p); break;
+    case 32: hipLaunchKernelGGL(attention_rowhead<32>, grid, dim3(256), lds, s, p); break;
+    case 64: hipLaunchKernelGGL(attention_rowhead<64>, grid, dim3(256), lds, s, p); break;
+    case 128: hipLaunchKernelGGL(attention_rowhead<128>, grid, dim3(256), lds, s, p); break;
+    default: hipLaunchKernelGGL(attention_rowhead<256>, grid, dim3(256), lds, s, p); break;
+  }
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+}  // extern "C"

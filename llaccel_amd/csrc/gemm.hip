@@ -1,0 +1,370 @@
+// gemm engine of libllhip: out = epilogue(requant(A . W^T + bias)) with int8
+// operands, exact int32 accumulation and the i64 requant of golden.py:316-342
+// (NUMERICS.md "GEMM").
+//
+// Two kernels:
+//  * linear_skinny: M <= 16 rows per z-block.  One wave computes a 16(M) x 16(N)
+//    tile with v_mfma_i32_16x16x64_i8; the A rows beyond M are zeros supplied in
+//    registers.  W [N][K] row-major is streamed once with 16-byte loads.  The K
+//    range is split over gridDim.y so that small-N projections still put enough
+//    waves on the chip; split partials are summed with int32 atomics into the
+//    workspace and the last-arriving wave of a tile (arrival counter) applies the
+//    epilogue and leaves the workspace zeroed.  Integer addition is associative,
+//    so the split never changes a result.
+//  * linear_tiled: M > 16.  128x128x64 block tiles, four waves in 2x2, each wave
+//    64x64 with v_mfma_i32_32x32x32_i8; A and W tiles double-buffered in LDS.
+//    Blocks are numbered XCD-major so the blocks that share a W panel run on one
+//    XCD and share its L2.
+#include "../../include/llhip.h"
+#include "common.h"
+
+namespace llhip {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+enum Epi : int { EPI_NONE = 0, EPI_RESADD = 1, EPI_SILU = 2, EPI_MUL = 3 };
+
+// workspace layout (bytes)
+constexpr int64_t WS_GEMM_PARTIALS = 0;          // int32 [16][N], N <= 65536
+constexpr int64_t WS_GEMM_COUNTERS = 4 << 20;    // uint32 per column tile
+constexpr int64_t GEMM_SPLIT_MAX_N = 65536;
+
+struct LinearArgs {
+  const int8_t* A;
+  const int8_t* W;
+  const int32_t* rq;
+  const int32_t* bias;
+  const int16_t* aux;
+  void* out;
+  int32_t* ws;
+  uint32_t* cnt;
+  int64_t lda, ldaux, ldo;
+  int64_t Mi;
+  int M, K, N;
+  int aux_shift, Si, sh;
+  int steps;            // ceil(K / 64)
+  int steps_per_split;  // linear_skinny
+  int splits;
+};
+
+// requant + epilogue of one output element (golden.py:323-342)
+template <int EPI, bool OUT8>
+__device__ __forceinline__ void finish(const LinearArgs& p, int m, int n, int64_t acc) {
+  if (p.bias) acc += p.bias[n];
+  const int64_t Mn = p.rq[2 * n];
+  const int Sn = p.rq[2 * n + 1];
+  const int64_t r = mulshift(acc, Mn, Sn);
+  if (OUT8) {
+    static_cast<int8_t*>(p.out)[(int64_t)m * p.ldo + n] = (int8_t)sat8(r);
+    return;
+  }
+  int64_t t = sat16(r);
+  if (EPI == EPI_RESADD) {
+    t = sat16(t + p.aux[(int64_t)m * p.ldaux + n]);
+  } else if (EPI == EPI_SILU) {
+    t = silu16(t, p.Mi, p.Si, p.sh);
+  } else if (EPI == EPI_MUL) {
+    t = sat16(rshr(wmul(t, p.aux[(int64_t)m * p.ldaux + n]), p.aux_shift));
+  }
+  static_cast<int16_t*>(p.out)[(int64_t)m * p.ldo + n] = (int16_t)t;
+}
+
+// 16 bytes of a K-contiguous row starting at k (zeros past K)
+template <bool ALIGNED>
+__device__ __forceinline__ v4i load16(const int8_t* row, int k, int K, bool valid) {
+  if (ALIGNED) {
+    if (valid && k < K) return *reinterpret_cast<const v4i*>(row + k);
+    return v4i{0, 0, 0, 0};
+  } else {
+    uint32_t w[4] = {0, 0, 0, 0};
+    if (valid) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        int kk = k + i;
+        uint32_t b = kk < K ? (uint8_t)row[kk] : 0u;
+        w[i >> 2] |= b << (8 * (i & 3));
+      }
+    }
+    return v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// M <= 16 (per z-block): one wave per 16-column tile and K split
+// ---------------------------------------------------------------------------------------
+template <int EPI, bool OUT8, bool ALIGNED>
+__global__ __launch_bounds__(64) void linear_skinny(LinearArgs p) {
+  const int lane = threadIdx.x;
+  const int col = lane & 15;
+  const int kg = lane >> 4;
+  const int tile = blockIdx.x;
+  const int split = blockIdx.y;
+  const int m0 = blockIdx.z * 16;
+  const int n = tile * 16 + col;
+  const bool nvalid = n < p.N;
+  const bool avalid = m0 + col < p.M;
+  const int8_t* wrow = p.W + (int64_t)(nvalid ? n : 0) * p.K;
+  const int8_t* arow = p.A + (int64_t)(avalid ? m0 + col : 0) * p.lda;
+
+  const int s_begin = split * p.steps_per_split;
+  const int s_end = min(s_begin + p.steps_per_split, p.steps);
+  v4i acc = {0, 0, 0, 0};
+  int s = s_begin;
+  constexpr int U = 4;
+  for (; s + U <= s_end; s += U) {
+    v4i b[U], a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (s + u) * 64 + kg * 16;
+      b[u] = load16<ALIGNED>(wrow, k, p.K, nvalid);
+      a[u] = load16<ALIGNED>(arow, k, p.K, avalid);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+  }
+  for (; s < s_end; ++s) {
+    const int k = s * 64 + kg * 16;
+    v4i b = load16<ALIGNED>(wrow, k, p.K, nvalid);
+    v4i a = load16<ALIGNED>(arow, k, p.K, avalid);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+  }
+
+  // acc[r] = C[4*kg + r][col] of this 16x16 tile
+  if (p.splits == 1) {
+    if (nvalid) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 4 * kg + r;
+        if (m < p.M) finish<EPI, OUT8>(p, m, n, acc[r]);
+      }
+    }
+    return;
+  }
+  // split-K: partial sums into the workspace, last arrival finishes the tile
+  int32_t* part = p.ws + (int64_t)blockIdx.z * 16 * p.N;
+  if (nvalid) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 4 * kg + r;
+      if (m < p.M) atomicAdd(&part[(int64_t)(4 * kg + r) * p.N + n], acc[r]);
+    }
+  }
+  __threadfence();
+  uint32_t* counter = p.cnt + (int64_t)blockIdx.z * gridDim.x + tile;
+  uint32_t prev = 0;
+  if (lane == 0) prev = atomicAdd(counter, 1u);
+  prev = __shfl(prev, 0);
+  if (prev != (uint32_t)(p.splits - 1)) return;
+  __threadfence();
+  if (nvalid) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 4 * kg + r;
+      if (m < p.M) {
+        const int32_t v = atomicExch(&part[(int64_t)(4 * kg + r) * p.N + n], 0);
+        finish<EPI, OUT8>(p, m, n, v);
+      }
+    }
+  }
+  if (lane == 0) atomicExch(counter, 0u);
+}
+
+// ---------------------------------------------------------------------------------------
+// M > 16: LDS-tiled 128x128x64 MFMA GEMM (K % 16 == 0)
+// ---------------------------------------------------------------------------------------
+constexpr int TBM = 128, TBN = 128, TBK = 64;
+constexpr int TLD = TBK + 16;  // LDS row stride in bytes (pad against bank conflicts)
+
+template <int EPI, bool OUT8>
+__global__ __launch_bounds__(256) void linear_tiled(LinearArgs p, int mblocks, int nblocks) {
+  __shared__ __attribute__((aligned(16))) int8_t As[2][TBM * TLD];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[2][TBN * TLD];
+
+  // XCD-major block numbering: hardware dispatches block b to XCD b % 8
+  const int nb_total = mblocks * nblocks;
+  const int b = blockIdx.x;
+  int logical = b;
+  if (nb_total % 8 == 0) logical = (b % 8) * (nb_total / 8) + b / 8;
+  const int mb = logical % mblocks;
+  const int nbk = logical / mblocks;
+  const int m0 = mb * TBM, n0 = nbk * TBN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+
+  // global -> LDS staging: each thread moves 2 x 16 B of A and 2 x 16 B of W per K tile
+  v4i ra[2], rb[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 2, kc = (c & 3) * 16;
+      const int gm = m0 + row, gn = n0 + row, gk = k0 + kc;
+      ra[i] = (gm < p.M && gk < p.K) ? *reinterpret_cast<const v4i*>(p.A + (int64_t)gm * p.lda + gk) : v4i{0, 0, 0, 0};
+      rb[i] = (gn < p.N && gk < p.K) ? *reinterpret_cast<const v4i*>(p.W + (int64_t)gn * p.K + gk) : v4i{0, 0, 0, 0};
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 2, kc = (c & 3) * 16;
+      *reinterpret_cast<v4i*>(&As[buf][row * TLD + kc]) = ra[i];
+      *reinterpret_cast<v4i*>(&Bs[buf][row * TLD + kc]) = rb[i];
+    }
+  };
+
+  v16i acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+
+  const int ktiles = (p.K + TBK - 1) / TBK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < ktiles) gload((kt + 1) * TBK);
+#pragma unroll
+    for (int ks = 0; ks < TBK; ks += 32) {
+      v4i fa[2], fb[2];
+      const int koff = ks + 16 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        fa[i] = *reinterpret_cast<const v4i*>(&As[buf][(wm + 32 * i + (lane & 31)) * TLD + koff]);
+        fb[i] = *reinterpret_cast<const v4i*>(&Bs[buf][(wn + 32 * i + (lane & 31)) * TLD + koff]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < ktiles) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn + 32 * j + (lane & 31);
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (m < p.M) finish<EPI, OUT8>(p, m, n, acc[i][j][r]);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// dispatch
+// ---------------------------------------------------------------------------------------
+template <int EPI, bool OUT8>
+static int launch_linear(LinearArgs& p, hipStream_t stream) {
+  const bool aligned = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.W % 16 == 0);
+  if (p.M > 16 && aligned) {
+    const int mblocks = (int)ceil_div(p.M, TBM), nblocks = (int)ceil_div(p.N, TBN);
+    hipLaunchKernelGGL((linear_tiled<EPI, OUT8>), dim3(mblocks * nblocks), dim3(256), 0, stream, p, mblocks, nblocks);
+    LLHIP_LAUNCH_CHECK();
+    return 0;
+  }
+  const int tiles = (int)ceil_div(p.N, 16);
+  const int zblocks = (int)ceil_div(p.M, 16);
+  int splits = 1;
+  const int target_waves = 8 * current_cu_count();
+  if (p.ws && p.N <= GEMM_SPLIT_MAX_N && zblocks == 1 && tiles < target_waves) {
+    splits = (int)ceil_div(target_waves, tiles);
+    const int max_splits = (int)ceil_div(p.steps, 2);  // keep >= 2 MFMA steps per wave
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+  }
+  p.steps_per_split = (int)ceil_div(p.steps, splits);
+  p.splits = (int)ceil_div(p.steps, p.steps_per_split);
+  dim3 grid(tiles, p.splits, zblocks);
+  if (aligned)
+    hipLaunchKernelGGL((linear_skinny<EPI, OUT8, true>), grid, dim3(64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((linear_skinny<EPI, OUT8, false>), grid, dim3(64), 0, stream, p);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+// exact int64 A . int8 W^T (golden.py:217-240 computes the same integers through FP64 BLAS)
+__global__ void exact_matmul_kernel(const int64_t* A, int64_t M, int64_t K, const int8_t* W, int64_t N, int64_t* out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * N) return;
+  const int64_t m = idx / N, n = idx % N;
+  int64_t acc = 0;
+  for (int64_t k = 0; k < K; ++k) acc += wmul(A[m * K + k], (int64_t)W[n * K + k]);
+  out[idx] = acc;
+}
+
+}  // namespace llhip
+
+using namespace llhip;
+
+extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_t* W, int64_t N,
+                            const int32_t* rq, const int32_t* bias, int epilogue, const int16_t* aux, int64_t ldaux,
+                            int64_t aux_shift, int64_t silu_Mi, int64_t silu_Si, int64_t silu_sh, int out_i8,
+                            void* out, int64_t ldo, void* ws, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail(-EINVAL, "linear: negative shape");
+  if (M == 0 || N == 0) return 0;
+  if (K > 65535) return fail(-EINVAL, "linear: K=%lld exceeds the int32 accumulator bound 65535", (long long)K);
+  if (M > INT32_MAX || N > INT32_MAX) return fail(-EINVAL, "linear: shape too large");
+  if (lda < K || ldo < N) return fail(-EINVAL, "linear: leading dimension too small");
+  if (!A || !W || !rq || !out) return fail(-EINVAL, "linear: null operand");
+  if (epilogue < 0 || epilogue > 3) return fail(-EINVAL, "linear: unknown epilogue %d", epilogue);
+  if (out_i8 && epilogue != EPI_NONE) return fail(-EINVAL, "i8 output is only valid with epilogue none");
+  if ((epilogue == EPI_RESADD || epilogue == EPI_MUL) && (!aux || ldaux < N))
+    return fail(-EINVAL, "linear: epilogue needs aux [M][N]");
+  if (epilogue == EPI_MUL && !shift_ok(aux_shift)) return fail(-EINVAL, "linear: aux_shift out of [0,63]");
+  if (epilogue == EPI_SILU && (!shift_ok(silu_Si) || !shift_ok(silu_sh)))
+    return fail(-EINVAL, "linear: silu shift out of [0,63]");
+  LinearArgs p{};
+  p.A = A;
+  p.W = W;
+  p.rq = rq;
+  p.bias = bias;
+  p.aux = aux;
+  p.out = out;
+  p.ws = ws ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_GEMM_PARTIALS) : nullptr;
+  p.cnt = ws ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + WS_GEMM_COUNTERS) : nullptr;
+  p.lda = lda;
+  p.ldaux = ldaux;
+  p.ldo = ldo;
+  p.Mi = silu_Mi;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.N = (int)N;
+  p.aux_shift = (int)aux_shift;
+  p.Si = (int)silu_Si;
+  p.sh = (int)silu_sh;
+  p.steps = (int)ceil_div(K, 64);
+  if (p.steps == 0) p.steps = 1;
+  hipStream_t s = (hipStream_t)stream;
+  if (out_i8) return launch_linear<EPI_NONE, true>(p, s);
+  switch (epilogue) {
+    case EPI_RESADD: return launch_linear<EPI_RESADD, false>(p, s);
+    case EPI_SILU: return launch_linear<EPI_SILU, false>(p, s);
+    case EPI_MUL: return launch_linear<EPI_MUL, false>(p, s);
+    default: return launch_linear<EPI_NONE, false>(p, s);
+  }
+}
+
+extern "C" int llhip_exact_matmul(const int64_t* A, int64_t M, int64_t K, const int8_t* W, int64_t N, int64_t* out,
+                                  void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail(-EINVAL, "exact_matmul: negative shape");
+  if (M == 0 || N == 0) return 0;
+  const int64_t total = M * N;
+  hipLaunchKernelGGL(exact_matmul_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, A, M,
+                     K, W, N, out);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}

@@ -1,0 +1,899 @@
+"""Drop-in GPU twin of the reference's python/llaccel/golden.py.
+
+Same names, signatures, argument meaning, records and error behaviour as the reference
+module; every integer is computed by the gfx950 kernels of libllhip.so (include/llhip.h)
+through ctypes.  PyTorch-ROCm only allocates device memory and supplies the stream.
+
+    python -m llaccel_amd.golden --qgraph build/q/ --prompt-ids 1,2,3 --tokens 64 -o golden.json
+
+Primitives (golden.py:35-180) take NumPy arrays / Python ints and return int64 NumPy
+arrays (Python ints for isqrt48/udiv), like the reference.  Inputs of the datapath
+primitives must fit the types NUMERICS.md gives them (rmsnorm/rope operands i16,
+attention operands i8); the reference would also compute out-of-type values, this module
+raises ValueError for them instead.
+
+`GoldenModel` keeps the quantized weights, the KV caches and every activation resident in
+HBM; `run_chunk` uploads the input rows and downloads the logits (and, when asked, every
+activation).  `kv` returns host snapshots of the device caches; `set_kv` uploads one.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+
+from . import _lib
+from .luts import exp_frac_lut, exp_int_lut, sigmoid_lut
+
+I64 = np.int64
+SIG = sigmoid_lut().astype(I64)
+EXPI = exp_int_lut().astype(I64)
+EXPF = exp_frac_lut().astype(I64)
+PREFILL_M = 16
+
+_torch = None
+
+
+def _t():
+    global _torch
+    if _torch is None:
+        import torch
+
+        if not torch.cuda.is_available():
+            raise RuntimeError("llaccel_amd needs a ROCm GPU: torch.cuda.is_available() is False")
+        _torch = torch
+    return _torch
+
+
+def _dev():
+    torch = _t()
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _stream():
+    return ctypes.c_void_p(_t().cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _up(a: np.ndarray, dtype=np.int64):
+    """Host array -> contiguous device tensor of `dtype`."""
+    torch = _t()
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=dtype)).to(_dev())
+
+
+def _down(t) -> np.ndarray:
+    return t.cpu().numpy()
+
+
+def _check_range(a: np.ndarray, lo: int, hi: int, what: str) -> None:
+    if a.size and (a.min() < lo or a.max() > hi):
+        raise ValueError(f"{what} must lie in [{lo}, {hi}]")
+
+
+def _check_shift(s, what="shift") -> None:
+    s = np.asarray(s, dtype=I64)
+    if s.size and (s.min() < 0 or s.max() > 63):
+        raise ValueError(f"{what} must be in [0, 63]")
+
+
+def _check_u32(v, what) -> None:
+    v = np.asarray(v, dtype=I64)
+    if v.size and (v.min() < 0 or v.max() > 0xFFFFFFFF):
+        raise ValueError(f"{what} must be an unsigned 32-bit value")
+
+
+def _elementwise(fn: str, arrays: list, *scalars) -> np.ndarray:
+    """Broadcast int64 operands on the host, run one elementwise kernel, return int64."""
+    arrs = np.broadcast_arrays(*[np.asarray(a, dtype=I64) for a in arrays])
+    shape = arrs[0].shape
+    n = int(np.prod(shape)) if shape else 1
+    if n == 0:
+        return np.zeros(shape, I64)
+    dev = [_up(a.reshape(-1)) for a in arrs]
+    out = _t().empty(n, dtype=_t().int64, device=_dev())
+    ptrs = [_ptr(d) for d in dev]
+    if fn in ("llhip_silu16_i64", "llhip_vquant_i64"):
+        _lib.call(fn, ptrs[0], n, *scalars, _ptr(out), _stream())
+    elif fn in ("llhip_vmul_i64", "llhip_vadd_i64"):
+        _lib.call(fn, ptrs[0], ptrs[1], n, *scalars, _ptr(out), _stream())
+    elif fn == "llhip_sat":
+        _lib.call(fn, ptrs[0], n, *scalars, _ptr(out), _stream())
+    elif fn == "llhip_requant":
+        _lib.call(fn, ptrs[0], ptrs[1], ptrs[2], n, *scalars, _ptr(out), _stream())
+    else:
+        _lib.call(fn, *ptrs, n, _ptr(out), _stream())
+    return _down(out).reshape(shape)
+
+
+# --------------------------------------------------------------------------------------
+# Primitives (golden.py:35-180)
+# --------------------------------------------------------------------------------------
+def rshr(v, s):
+    """Round-half-up arithmetic right shift (golden.py:35-45); s in [0, 63]."""
+    _check_shift(s)
+    return _elementwise("llhip_rshr", [v, s])
+
+
+def sat8(v):
+    """golden.py:48-49"""
+    return _elementwise("llhip_sat", [v], 0)
+
+
+def satu8(v):
+    """golden.py:52-53"""
+    return _elementwise("llhip_sat", [v], 1)
+
+
+def sat16(v):
+    """golden.py:56-57"""
+    return _elementwise("llhip_sat", [v], 2)
+
+
+def satu16(v):
+    """golden.py:60-61"""
+    return _elementwise("llhip_sat", [v], 3)
+
+
+def mulshift(v, M, S):
+    """rshr(v*M, S) with a wrapping int64 product (golden.py:64-65)."""
+    _check_shift(S)
+    return _elementwise("llhip_mulshift", [v, M, S])
+
+
+def isqrt48(t: int) -> int:
+    """floor(sqrt(t)) for t < 2^48 (golden.py:68-81)."""
+    t = int(t)
+    if not 0 <= t < (1 << 48):
+        raise ValueError(f"isqrt48 input out of range: {t}")
+    return int(_elementwise("llhip_isqrt48", [np.array([t])])[0])
+
+
+def udiv(a: int, b: int) -> int:
+    """(a // max(b, 1)) & 0xFFFFFFFF (golden.py:84-88)."""
+    a, b = int(a), int(b)
+    if a < 0 or b < 0:
+        raise ValueError("udiv operands must be unsigned")
+    if a >= 1 << 63 or b >= 1 << 63:
+        raise ValueError("udiv operands must fit int64")
+    return int(_elementwise("llhip_udiv", [np.array([a]), np.array([b])])[0])
+
+
+def requant16(acc, M, S):
+    """golden.py:92-93"""
+    _check_shift(S)
+    return _elementwise("llhip_requant", [acc, M, S], 16)
+
+
+def requant8(acc, M, S):
+    """golden.py:96-97"""
+    _check_shift(S)
+    return _elementwise("llhip_requant", [acc, M, S], 8)
+
+
+def silu16(x, Mi: int, Si: int, sh_out: int):
+    """golden.py:101-107"""
+    _check_shift(Si, "Si")
+    _check_shift(sh_out, "sh_out")
+    return _elementwise("llhip_silu16_i64", [x], int(Mi), int(Si), int(sh_out))
+
+
+def vmul(a, b, sh: int):
+    """golden.py:111-112"""
+    _check_shift(sh)
+    return _elementwise("llhip_vmul_i64", [a, b], int(sh))
+
+
+def vadd(a, b, sh_b: int):
+    """golden.py:115-116"""
+    _check_shift(sh_b)
+    return _elementwise("llhip_vadd_i64", [a, b], int(sh_b))
+
+
+def vquant(x, M: int, S: int):
+    """golden.py:119-120"""
+    _check_shift(S)
+    return _elementwise("llhip_vquant_i64", [x], int(M), int(S))
+
+
+def rmsnorm(x, g, eps_t: int, C: int, sh_post: int):
+    """Row-wise integer RMSNorm of x [rows][K] with gamma g [K] (golden.py:124-137)."""
+    x = np.asarray(x, dtype=I64)
+    g = np.asarray(g, dtype=I64).reshape(-1)
+    if x.ndim != 2 or x.shape[1] != g.shape[0]:
+        raise ValueError("rmsnorm: x must be [rows][K] with K = len(g)")
+    _check_range(x, -32768, 32767, "rmsnorm input")
+    _check_range(g, -32768, 32767, "rmsnorm gamma")
+    _check_u32(eps_t, "eps_t")
+    _check_u32(C, "C")
+    _check_shift(sh_post, "sh_post")
+    rows, K = x.shape
+    if rows == 0:
+        return np.zeros((0, K), I64)
+    xd, gd = _up(x, np.int16), _up(g, np.int16)
+    yd = _t().empty_like(xd)
+    _lib.call("llhip_rmsnorm", _ptr(xd), rows, K, K, _ptr(gd), int(eps_t), int(C), int(sh_post), _ptr(yd), K, _stream())
+    return _down(yd).astype(I64)
+
+
+def rmsnorm_row(x, g, eps_t: int, C: int, sh_post: int):
+    """golden.py:124-132"""
+    return rmsnorm(np.asarray(x, dtype=I64)[None, :], g, eps_t, C, sh_post)[0]
+
+
+def rope(x, H: int, D: int, cos_tab, sin_tab, pos: int):
+    """x [M][H*D]; row m uses table row pos+m (golden.py:155-158)."""
+    x = np.asarray(x, dtype=I64)
+    cos_tab = np.asarray(cos_tab, dtype=I64)
+    sin_tab = np.asarray(sin_tab, dtype=I64)
+    H, D, pos = int(H), int(D), int(pos)
+    if x.ndim != 2 or x.shape[1] != H * D or D % 2:
+        raise ValueError("rope: x must be [M][H*D] with even D")
+    if cos_tab.ndim != 2 or cos_tab.shape[1] != D // 2 or cos_tab.shape != sin_tab.shape:
+        raise ValueError("rope: tables must be [rows][D/2]")
+    if pos < 0 or pos + x.shape[0] > cos_tab.shape[0]:
+        raise IndexError("rope: table rows pos..pos+M-1 out of range")
+    for a, w in ((x, "rope input"), (cos_tab, "rope cos table"), (sin_tab, "rope sin table")):
+        _check_range(a, -32768, 32767, w)
+    M = x.shape[0]
+    if M == 0:
+        return np.zeros_like(x)
+    xd = _up(x, np.int16)
+    cd, sd = _up(cos_tab, np.int16), _up(sin_tab, np.int16)
+    yd = _t().empty_like(xd)
+    _lib.call("llhip_rope", _ptr(xd), M, H, D, H * D, _ptr(cd), _ptr(sd), cos_tab.shape[0], pos, None, _ptr(yd), H * D,
+              _stream())
+    return _down(yd).astype(I64)
+
+
+def rope_row(x, H: int, D: int, cosv, sinv):
+    """golden.py:141-152"""
+    return rope(np.asarray(x, dtype=I64)[None, :], H, D, np.asarray(cosv)[None, :], np.asarray(sinv)[None, :], 0)[0]
+
+
+def attention_head(q, keys, vals, Ms: int, Ss: int, Mo: int, So: int, prob_bits: int = 8):
+    """q [D] i8; keys/vals [T][D] i8 -> out [D] (golden.py:162-180)."""
+    if prob_bits not in (8, 15):
+        raise ValueError("attention prob_bits must be 8 or 15")
+    q = np.asarray(q, dtype=I64).reshape(-1)
+    keys = np.asarray(keys, dtype=I64)
+    vals = np.asarray(vals, dtype=I64)
+    D = q.shape[0]
+    if keys.ndim != 2 or keys.shape[1] != D or vals.shape != keys.shape or keys.shape[0] < 1:
+        raise ValueError("attention_head: keys/vals must be [T][D], T >= 1")
+    for a, w in ((q, "q"), (keys, "keys"), (vals, "vals")):
+        _check_range(a, -128, 127, w)
+    T = keys.shape[0]
+    qd = _up(q[None, :], np.int8)
+    kd, vd = _up(keys, np.int8), _up(vals, np.int8)
+    out = _t().empty((1, D), dtype=_t().int8, device=_dev())
+    _lib.call("llhip_attention", _ptr(qd), 1, 1, 1, D, D, T - 1, None, _ptr(kd), _ptr(vd), T, int(Ms), int(Ss),
+              int(Mo), int(So), int(prob_bits), _ptr(out), D, None, _stream())
+    return _down(out)[0].astype(I64)
+
+
+# --------------------------------------------------------------------------------------
+# Quantized graph loading (golden.py:186-214)
+# --------------------------------------------------------------------------------------
+_DT = {"i8": (np.int8, 1), "i16": (np.dtype("<i2"), 2), "i32": (np.dtype("<i4"), 4), "rq": (np.dtype("<i4"), 8)}
+
+
+class QGraph:
+    """qgraph.json + memory-mapped qweights.bin (golden.py:189-214)."""
+
+    def __init__(self, qdir: Path | str) -> None:
+        self.dir = Path(qdir)
+        with open(self.dir / "qgraph.json") as f:
+            self.g = json.load(f)
+        self.model = self.g["model"]
+        self.ops = self.g["ops"]
+        self.blob = np.memmap(self.dir / self.g["weights_file"], dtype=np.uint8, mode="r")
+        self.tensors: dict[str, np.ndarray] = {}
+        self.tensor_exp: dict[str, int] = {}
+        self.specs: dict[str, dict] = {}
+        for name, spec in self.g["tensors"].items():
+            dt, _ = _DT[spec["dtype"]]
+            count = int(np.prod(spec["shape"]))
+            if spec["dtype"] == "rq":
+                arr = np.frombuffer(self.blob, dtype=dt, count=2 * count, offset=spec["offset"]).reshape(count, 2)
+            else:
+                arr = np.frombuffer(self.blob, dtype=dt, count=count, offset=spec["offset"]).reshape(spec["shape"])
+            self.tensors[name] = arr
+            self.specs[name] = spec
+            if "exp" in spec:
+                self.tensor_exp[name] = spec["exp"]
+        self.exps: dict[str, int] = dict(self.g.get("exps", {}))
+        self.scales: dict[str, float] = dict(self.g.get("scales", {}))
+        self.input_name = self.g.get("input", "input")
+        self.output_name = self.g.get("output", "logits")
+
+
+def exact_blas_matmul(a: np.ndarray, w: np.ndarray, chunk_rows: int = 1024) -> np.ndarray:
+    """Exact integer A @ W.T (golden.py:217-240): same argument checks and errors as the
+    reference, computed with integer arithmetic on the GPU (no floating point)."""
+    if a.ndim != 2 or w.ndim != 2 or a.shape[1] != w.shape[1]:
+        raise ValueError("invalid matrix dimensions")
+    if a.dtype.kind not in "iu" or w.dtype.kind not in "iu" or chunk_rows < 1:
+        raise ValueError("exact BLAS requires integer inputs and positive chunks")
+    amax = max(abs(int(a.min(initial=0))), abs(int(a.max(initial=0))))
+    wi = np.iinfo(w.dtype)
+    wmax = max(abs(int(wi.min)), abs(int(wi.max)))
+    if a.shape[1] * amax * wmax > (1 << 53):
+        raise ValueError("integer dot product exceeds exact FP64 accumulation bound")
+    if w.dtype != np.int8:
+        raise ValueError("exact_blas_matmul: weights must be int8 (NUMERICS.md i8pc)")
+    M, K = a.shape
+    N = w.shape[0]
+    out = _t().empty((M, N), dtype=_t().int64, device=_dev())
+    ad, wd = _up(a), _up(w, np.int8)
+    _lib.call("llhip_exact_matmul", _ptr(ad), M, K, _ptr(wd), N, _ptr(out), _stream())
+    return _down(out)
+
+
+# --------------------------------------------------------------------------------------
+# Golden model
+# --------------------------------------------------------------------------------------
+_EPI = {"none": 0, "resadd": 1, "silu": 2, "mul": 3}
+_TDT = {"i8": "int8", "i16": "int16"}
+
+
+class _Deferred:
+    """A graph error that the reference raises when the op executes; raised at the same point."""
+
+    def __init__(self, exc: Exception) -> None:
+        self.exc = exc
+
+    def __call__(self, M, pos):
+        raise self.exc
+
+
+class GoldenModel:
+    """Device-resident twin of golden.py:246-440 (same attributes, methods and record)."""
+
+    def __init__(self, qgraph_dir: Path | str, *, fast_matmul: bool = False) -> None:
+        self.fast_matmul = fast_matmul  # accepted for API parity: every path here is exact integer arithmetic
+        self.q = QGraph(qgraph_dir)
+        m = self.q.model
+        self.dim = int(m["dim"])
+        self.n_layers = int(m["n_layers"])
+        self.vocab = int(m["vocab"])
+        self.vocab_padded = int(m.get("vocab_padded", self.vocab))
+        self.max_seq = int(m["max_seq"])
+        self.prefill_m = int(m.get("prefill_m", PREFILL_M))
+        if not 1 <= self.prefill_m <= 16 or self.max_seq % self.prefill_m:
+            raise ValueError("max_seq must be divisible by prefill_m in [1,16]")
+        self.E_RES = int(m["E_RES"])
+        self.E_LOGIT = int(m["E_LOGIT"])
+        self.embed = self.q.tensors["embed"]
+        self.rope_cos = self.q.tensors["rope_cos"]
+        self.rope_sin = self.q.tensors["rope_sin"]
+        torch = _t()
+        self.device = _dev()
+        # one upload of the whole weight blob; every tensor is a view of it
+        self._blob = torch.from_numpy(np.asarray(self.q.blob)).to(self.device)
+        self._dt: dict[str, object] = {}
+        for name, spec in self.q.specs.items():
+            self._dt[name] = self._tensor_view(spec)
+        self._ws = torch.zeros(int(_lib.lib().llhip_workspace_bytes()), dtype=torch.uint8, device=self.device)
+        self._act: dict[str, object] = {}
+        self._cap = 0
+        self._act_spec: dict[str, tuple[str, int]] = {}
+        self._plan = self._compile()
+        self.reset()
+
+    # ---- device tensors ---------------------------------------------------------------------
+    def _tensor_view(self, spec: dict):
+        torch = _t()
+        dt = spec["dtype"]
+        count = int(np.prod(spec["shape"]))
+        nbytes = {"i8": 1, "i16": 2, "i32": 4, "rq": 8}[dt] * count
+        raw = self._blob[int(spec["offset"]):int(spec["offset"]) + nbytes]
+        tdt = {"i8": torch.int8, "i16": torch.int16, "i32": torch.int32, "rq": torch.int32}[dt]
+        v = raw.view(tdt)
+        return v.view(count, 2) if dt == "rq" else v.view(*spec["shape"]) if spec["shape"] else v
+
+    def _buf(self, name: str):
+        return self._act[name]
+
+    def _ensure_capacity(self, M: int) -> None:
+        if M <= self._cap:
+            return
+        torch = _t()
+        cap = max(M, self.prefill_m)
+        for name, (dt, cols) in self._act_spec.items():
+            self._act[name] = torch.zeros((cap, cols), dtype=getattr(torch, _TDT[dt]), device=self.device)
+        self._cap = cap
+
+    def reset(self) -> None:
+        """Zero every layer's (Hkv, max_seq, D) int8 K and V caches (golden.py:266-272)."""
+        torch = _t()
+        self._kv: dict[int, tuple] = {}
+        for op in self.q.ops:
+            if op["op"] == "kv_write":
+                L, Hkv, D = int(op["layer"]), int(op["Hkv"]), int(op["D"])
+                shape = (Hkv, self.max_seq, D)
+                self._kv[L] = (torch.zeros(shape, dtype=torch.int8, device=self.device),
+                               torch.zeros(shape, dtype=torch.int8, device=self.device))
+
+    @property
+    def kv(self) -> dict[int, tuple[np.ndarray, np.ndarray]]:
+        """Host snapshots {layer: (K, V)} of the device caches, int8 (Hkv, max_seq, D)."""
+        return {L: (_down(k), _down(v)) for L, (k, v) in self._kv.items()}
+
+    def set_kv(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
+        """Upload a (Hkv, max_seq, D) int8 K/V state for `layer` (preinitialised-state runs)."""
+        kc, vc = self._kv[int(layer)]
+        for src, dst in ((k, kc), (v, vc)):
+            a = np.asarray(src)
+            if tuple(a.shape) != tuple(dst.shape):
+                raise ValueError(f"KV shape {a.shape} != {tuple(dst.shape)}")
+            dst.copy_(_up(a, np.int8))
+
+    # ---- graph compilation ----------------------------------------------------------------
+    def _compile(self) -> list:
+        """Typecheck the op list and turn every op into one (or a few) kernel launches."""
+        spec = self._act_spec
+        spec[self.q.input_name] = ("i16", self.dim)
+        plan = []
+        T = self.q.tensors
+
+        def need(name, dt=None):
+            if name not in spec:
+                raise ValueError(f"activation {name!r} is used before it is produced")
+            if dt is not None and spec[name][0] != dt:
+                raise ValueError(f"activation {name!r} is {spec[name][0]}, this op needs {dt}")
+            return spec[name]
+
+        for op in self.q.ops:
+            k = op["op"]
+            try:
+                if k == "rmsnorm":
+                    plan.append(self._c_rmsnorm(op, need, T))
+                elif k == "quant":
+                    _, cols = need(op["in"], "i16")
+                    _check_u32(op["M"], "quant M")
+                    _check_shift(op["S"], "quant S")
+                    spec[op["out"]] = ("i8", cols)
+                    plan.append(self._c_quant(op))
+                elif k == "linear":
+                    plan.append(self._c_linear(op, need, T))
+                elif k == "rope":
+                    _, cols = need(op["in"], "i16")
+                    H, D = int(op["H"]), int(op["D"])
+                    if cols != H * D or D % 2:
+                        raise ValueError(f"rope {op['out']}: {cols} columns != H*D = {H * D}")
+                    if self.rope_cos.shape[1] != D // 2:
+                        raise ValueError("rope table width != D/2")
+                    spec[op["out"]] = ("i16", cols)
+                    plan.append(self._c_rope(op))
+                elif k == "kv_write":
+                    plan.append(self._c_kv_write(op, need))
+                elif k == "attention":
+                    plan.append(self._c_attention(op, need))
+                elif k in ("add", "mul"):
+                    _, ca = need(op["a"], "i16")
+                    _, cb = need(op["b"], "i16")
+                    if ca != cb:
+                        raise ValueError(f"{k} {op['out']}: operand widths differ")
+                    _check_shift(op["sh_b" if k == "add" else "sh"], "shift")
+                    spec[op["out"]] = ("i16", ca)
+                    plan.append(self._c_binary(op, k))
+                elif k == "silu":
+                    _, cols = need(op["in"], "i16")
+                    _check_u32(op["Mi"], "silu Mi")
+                    _check_shift(op["Si"], "silu Si")
+                    _check_shift(op["sh_out"], "silu sh_out")
+                    spec[op["out"]] = ("i16", cols)
+                    plan.append(self._c_silu(op))
+                else:
+                    raise ValueError(f"unknown qgraph op {k!r}")
+            except (ValueError, KeyError) as e:
+                exc = e if isinstance(e, ValueError) else ValueError(f"missing tensor or field {e}")
+                plan.append(_Deferred(exc))
+                break
+        if self.q.output_name not in spec and not any(isinstance(p, _Deferred) for p in plan):
+            plan.append(_Deferred(ValueError(f"output {self.q.output_name!r} is never produced")))
+        return plan
+
+    def _c_rmsnorm(self, op, need, T):
+        _, cols = need(op["in"], "i16")
+        g = self._dt[op["gamma"]]
+        K = int(g.shape[0])
+        heads = int(op.get("heads", 1))
+        if heads < 1 or cols != heads * K:
+            raise ValueError("RMSNorm head geometry mismatch")
+        _check_u32(op["eps_t"], "rmsnorm eps_t")
+        _check_u32(op["C"], "rmsnorm C")
+        _check_shift(op["sh_post"], "rmsnorm sh_post")
+        self._act_spec[op["out"]] = ("i16", cols)
+        src, dst = op["in"], op["out"]
+        eps_t, C, sh = int(op["eps_t"]), int(op["C"]), int(op["sh_post"])
+
+        def run(M, pos):
+            x, y = self._buf(src), self._buf(dst)
+            _lib.call("llhip_rmsnorm", _ptr(x), M * heads, K, K, _ptr(g), eps_t, C, sh, _ptr(y), K, _stream())
+        return run
+
+    def _c_quant(self, op):
+        src, dst, Mq, Sq = op["in"], op["out"], int(op["M"]), int(op["S"])
+        cols = self._act_spec[src][1]
+
+        def run(M, pos):
+            _lib.call("llhip_quant", _ptr(self._buf(src)), M * cols, Mq, Sq, _ptr(self._buf(dst)), _stream())
+        return run
+
+    def _c_linear(self, op, need, T):
+        a_dt, a_cols = need(op["in"])
+        w = T[op["w"]]
+        rq = T[op["rq"]]
+        N, K = int(op["N"]), int(op["K"])
+        if tuple(w.shape) != (N, K) or a_cols != K:
+            raise ValueError(f"linear {op['out']}: shapes A(M, {a_cols}) W{tuple(w.shape)} vs N={N} K={K}")
+        if a_dt != "i8":
+            raise ValueError(f"linear {op['out']}: input {op['in']!r} must be an i8 activation")
+        if rq.shape != (N, 2):
+            raise ValueError(f"linear {op['out']}: rq table shape {rq.shape}")
+        if rq.size and (rq[:, 1].min() < 0 or rq[:, 1].max() > 63):
+            raise ValueError(f"linear {op['out']}: rq shifts must be in [0, 63]")
+        out_i8 = op.get("out_dtype", "i16") == "i8"
+        ep = op.get("epilogue", "none") or "none"
+        if out_i8 and ep != "none":
+            raise ValueError("i8 output is only valid with epilogue none")
+        if ep not in _EPI:
+            raise ValueError(f"unknown epilogue {ep!r}")
+        bias = self._dt[op["bias"]] if op.get("bias") else None
+        if bias is not None and tuple(bias.shape) != (N,):
+            raise ValueError(f"linear {op['out']}: bias shape {tuple(bias.shape)}")
+        aux = None
+        aux_shift = int(op.get("aux_shift", 0) or 0)
+        if ep in ("resadd", "mul"):
+            aux = op["aux"]
+            _, c = need(aux, "i16")
+            if c != N:
+                raise ValueError(f"linear {op['out']}: aux width {c} != N={N}")
+            if ep == "mul":
+                _check_shift(aux_shift, "aux_shift")
+        Mi = Si = sh = 0
+        if ep == "silu":
+            s = op["silu"]
+            Mi, Si, sh = int(s["Mi"]), int(s["Si"]), int(s["sh_out"])
+            _check_u32(Mi, "silu Mi")
+            _check_shift(Si, "silu Si")
+            _check_shift(sh, "silu sh_out")
+        self._act_spec[op["out"]] = ("i8" if out_i8 else "i16", N)
+        src, dst = op["in"], op["out"]
+        wd, rqd = self._dt[op["w"]], self._dt[op["rq"]]
+        epi = _EPI[ep]
+
+        def run(M, pos):
+            a = self._buf(src)
+            auxd = self._buf(aux) if aux is not None else None
+            _lib.call("llhip_linear", _ptr(a), M, K, K, _ptr(wd), N, _ptr(rqd), _ptr(bias), epi, _ptr(auxd), N,
+                      aux_shift, Mi, Si, sh, int(out_i8), _ptr(self._buf(dst)), N, _ptr(self._ws), _stream())
+        return run
+
+    def _c_rope(self, op):
+        src, dst, H, D = op["in"], op["out"], int(op["H"]), int(op["D"])
+        cos_t, sin_t = self._dt["rope_cos"], self._dt["rope_sin"]
+        rows = int(cos_t.shape[0])
+
+        def run(M, pos):
+            _lib.call("llhip_rope", _ptr(self._buf(src)), M, H, D, H * D, _ptr(cos_t), _ptr(sin_t), rows, pos, None,
+                      _ptr(self._buf(dst)), H * D, _stream())
+        return run
+
+    def _c_kv_write(self, op, need):
+        Hkv, D = int(op["Hkv"]), int(op["D"])
+        _, ck = need(op["k"], "i8")
+        _, cv = need(op["v"], "i8")
+        if ck < Hkv * D or cv < Hkv * D:
+            raise ValueError("kv_write: K/V activations narrower than Hkv*D")
+        layer = int(op["layer"])
+        ksrc, vsrc = op["k"], op["v"]
+
+        def run(M, pos):
+            kc, vc = self._kv[layer]
+            _lib.call("llhip_kv_write", _ptr(self._buf(ksrc)), _ptr(self._buf(vsrc)), M, Hkv, D, ck, cv, pos, None,
+                      _ptr(kc), _ptr(vc), self.max_seq, _stream())
+        return run
+
+    def _c_attention(self, op, need):
+        H, Hkv, D = int(op["H"]), int(op["Hkv"]), int(op["D"])
+        _, cq = need(op["q"], "i8")
+        if Hkv < 1 or H % Hkv:
+            raise ValueError("attention: H must be a multiple of Hkv")
+        if cq != H * D:
+            raise ValueError(f"attention {op['out']}: q width {cq} != H*D")
+        pb = op.get("prob_bits", 8)
+        if pb not in (8, 15):
+            raise ValueError("attention prob_bits must be 8 or 15")
+        for f in ("Ms", "Mo"):
+            _check_u32(op[f], f"attention {f}")
+        for f in ("Ss", "So"):
+            _check_shift(op[f], f"attention {f}")
+        layer = int(op["layer"])
+        self._act_spec[op["out"]] = ("i8", H * D)
+        src, dst = op["q"], op["out"]
+        Ms, Ss, Mo, So = (int(op[f]) for f in ("Ms", "Ss", "Mo", "So"))
+
+        def run(M, pos):
+            if layer not in self._kv:
+                raise KeyError(layer)
+            kc, vc = self._kv[layer]
+            _lib.call("llhip_attention", _ptr(self._buf(src)), M, H, Hkv, D, H * D, pos, None, _ptr(kc), _ptr(vc),
+                      self.max_seq, Ms, Ss, Mo, So, pb, _ptr(self._buf(dst)), H * D, _ptr(self._ws), _stream())
+        return run
+
+    def _c_binary(self, op, kind):
+        a, b, dst = op["a"], op["b"], op["out"]
+        sh = int(op["sh_b"] if kind == "add" else op["sh"])
+        cols = self._act_spec[a][1]
+        fn = "llhip_vadd" if kind == "add" else "llhip_vmul"
+
+        def run(M, pos):
+            _lib.call(fn, _ptr(self._buf(a)), _ptr(self._buf(b)), M * cols, sh, _ptr(self._buf(dst)), _stream())
+        return run
+
+    def _c_silu(self, op):
+        src, dst = op["in"], op["out"]
+        Mi, Si, sh = int(op["Mi"]), int(op["Si"]), int(op["sh_out"])
+        cols = self._act_spec[src][1]
+
+        def run(M, pos):
+            _lib.call("llhip_silu", _ptr(self._buf(src)), M * cols, Mi, Si, sh, _ptr(self._buf(dst)), _stream())
+        return run
+
+    # ---- one device launch --------------------------------------------------------------
+    def _execute(self, M: int, pos: int) -> None:
+        for step in self._plan:
+            step(M, pos)
+
+    def _collect(self, M: int) -> dict:
+        out = {}
+        for name in self._act_spec:
+            out[name] = _down(self._act[name][:M]).astype(I64)
+        return out
+
+    def run_chunk(self, rows: np.ndarray, pos: int, acts: dict | None = None) -> np.ndarray:
+        """Execute the op list for `rows` [M][dim] (i16 at E_RES) at positions pos..pos+M-1
+        (golden.py:275-314).  Returns logits [M][vocab_padded]; `acts` collects every activation."""
+        rows = np.asarray(rows, dtype=I64)
+        M = rows.shape[0]
+        if pos < 0 or pos + M > self.max_seq:
+            raise ValueError(f"positions {pos}..{pos + M - 1} exceed max_seq={self.max_seq}")
+        if rows.ndim != 2 or rows.shape[1] != self.dim:
+            raise ValueError(f"rows must be [M][{self.dim}]")
+        _check_range(rows, -32768, 32767, "input rows")
+        self._ensure_capacity(M)
+        self._act[self.q.input_name][:M].copy_(_up(rows, np.int16))
+        self._execute(M, int(pos))
+        if acts is not None:
+            got = self._collect(M)
+            got[self.q.input_name] = rows
+            acts.update(got)
+        return _down(self._act[self.q.output_name][:M]).astype(I64)
+
+    def linear(self, op: dict, act: dict) -> np.ndarray:
+        """One gemm-engine op on host activations (golden.py:316-342)."""
+        a = np.asarray(act[op["in"]], dtype=I64)
+        w = self.q.tensors[op["w"]]
+        N, K = int(op["N"]), int(op["K"])
+        if w.shape != (N, K) or a.shape[1] != K:
+            raise ValueError(f"linear {op['out']}: shapes A{a.shape} W{w.shape} vs N={N} K={K}")
+        _check_range(a, -128, 127, "linear input")
+        out_i8 = op.get("out_dtype", "i16") == "i8"
+        ep = op.get("epilogue", "none") or "none"
+        if out_i8 and ep != "none":
+            raise ValueError("i8 output is only valid with epilogue none")
+        if ep not in _EPI:
+            raise ValueError(f"unknown epilogue {ep!r}")
+        rq = self.q.tensors[op["rq"]]
+        if rq.size and (rq[:, 1].min() < 0 or rq[:, 1].max() > 63):
+            raise ValueError("rq shifts must be in [0, 63]")
+        M = a.shape[0]
+        ad = _up(a, np.int8)
+        auxd = None
+        if ep in ("resadd", "mul"):
+            aux = np.asarray(act[op["aux"]], dtype=I64)
+            _check_range(aux, -32768, 32767, "aux")
+            auxd = _up(aux, np.int16)
+        torch = _t()
+        out = torch.empty((M, N), dtype=torch.int8 if out_i8 else torch.int16, device=self.device)
+        s = op.get("silu") or {}
+        bias = self._dt[op["bias"]] if op.get("bias") else None
+        if M:
+            _lib.call("llhip_linear", _ptr(ad), M, K, K, _ptr(self._dt[op["w"]]), N, _ptr(self._dt[op["rq"]]),
+                      _ptr(bias), _EPI[ep], _ptr(auxd), N, int(op.get("aux_shift", 0) or 0), int(s.get("Mi", 0)),
+                      int(s.get("Si", 0)), int(s.get("sh_out", 0)), int(out_i8), _ptr(out), N, _ptr(self._ws),
+                      _stream())
+        return _down(out).astype(I64)
+
+    def kv_write(self, op: dict, act: dict, pos: int) -> None:
+        """Write M rows of K/V into the caches at pos+m (golden.py:344-351)."""
+        Hkv, D = int(op["Hkv"]), int(op["D"])
+        k = np.asarray(act[op["k"]], dtype=I64)
+        v = np.asarray(act[op["v"]], dtype=I64)
+        _check_range(k, -128, 127, "k")
+        _check_range(v, -128, 127, "v")
+        kc, vc = self._kv[int(op["layer"])]
+        M = k.shape[0]
+        kd, vd = _up(k, np.int8), _up(v, np.int8)
+        _lib.call("llhip_kv_write", _ptr(kd), _ptr(vd), M, Hkv, D, k.shape[1], v.shape[1], pos, None, _ptr(kc),
+                  _ptr(vc), self.max_seq, _stream())
+
+    def attention(self, op: dict, act: dict, pos: int) -> np.ndarray:
+        """Causal GQA attention of host q rows over the device caches (golden.py:353-366)."""
+        q = np.asarray(act[op["q"]], dtype=I64)
+        _check_range(q, -128, 127, "q")
+        H, Hkv, D = int(op["H"]), int(op["Hkv"]), int(op["D"])
+        kc, vc = self._kv[int(op["layer"])]
+        M = q.shape[0]
+        qd = _up(q, np.int8)
+        out = _t().empty((M, H * D), dtype=_t().int8, device=self.device)
+        _lib.call("llhip_attention", _ptr(qd), M, H, Hkv, D, q.shape[1], pos, None, _ptr(kc), _ptr(vc), self.max_seq,
+                  int(op["Ms"]), int(op["Ss"]), int(op["Mo"]), int(op["So"]), int(op.get("prob_bits", 8)), _ptr(out),
+                  H * D, _ptr(self._ws), _stream())
+        return _down(out).astype(I64)
+
+    # ---- host side --------------------------------------------------------------------------
+    def _token_rows(self, tokens) -> np.ndarray:
+        rows = []
+        n = self.embed.shape[0]
+        for t in tokens:
+            t = int(t)
+            if not -n <= t < n:
+                raise IndexError(f"index {t} is out of bounds for axis 0 with size {n}")
+            rows.append(t % n)
+        return np.array(rows, dtype=np.int32)
+
+    def embed_rows(self, tokens, M: int) -> np.ndarray:
+        """Embedding rows of `tokens`, zero pad rows up to M (golden.py:369-373)."""
+        idx = self._token_rows(tokens)
+        if len(idx) > M:
+            raise ValueError(f"{len(idx)} tokens do not fit {M} rows")
+        torch = _t()
+        out = torch.empty((M, self.dim), dtype=torch.int16, device=self.device)
+        td = _up(idx if len(idx) else np.zeros(1, np.int32), np.int32)
+        _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, _ptr(td), len(idx), M,
+                  _ptr(out), _stream())
+        return _down(out).astype(I64)
+
+    @staticmethod
+    def argmax(logits_row: np.ndarray, vocab: int) -> int:
+        """First maximum over the first `vocab` logits (golden.py:376-377)."""
+        row = np.asarray(logits_row, dtype=I64)[:vocab]
+        if row.size == 0:
+            raise ValueError("attempt to get argmax of an empty sequence")
+        _check_range(row, -32768, 32767, "logits")
+        d = _up(row[None, :], np.int16)
+        idx = _t().empty(1, dtype=_t().int32, device=_dev())
+        _lib.call("llhip_argmax_i16", _ptr(d), 1, row.size, row.size, _ptr(idx), _stream())
+        return int(_down(idx)[0])
+
+    def _launch_tokens(self, tokens, pos: int, M: int) -> None:
+        """Embedding gather on the device + one launch (rows stay resident)."""
+        idx = self._token_rows(tokens)
+        if pos < 0 or pos + M > self.max_seq:
+            raise ValueError(f"positions {pos}..{pos + M - 1} exceed max_seq={self.max_seq}")
+        self._ensure_capacity(M)
+        td = _up(idx if len(idx) else np.zeros(1, np.int32), np.int32)
+        _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, _ptr(td), len(idx), M,
+                  _ptr(self._act[self.q.input_name]), _stream())
+        self._execute(M, int(pos))
+
+    def prefill(self, tokens, acts: list | None = None) -> list[np.ndarray]:
+        """Chunked prefill with model.prefill_m rows per launch (golden.py:379-390)."""
+        tokens = [int(t) for t in tokens]
+        rows_out = []
+        for start in range(0, len(tokens), self.prefill_m):
+            chunk = tokens[start:start + self.prefill_m]
+            self._launch_tokens(chunk, start, self.prefill_m)
+            if acts is not None:
+                acts.append({"kind": "prefill", "pos": start, "rows": self.prefill_m, "valid_rows": len(chunk),
+                             "acts": self._collect(self.prefill_m)})
+            logits = _down(self._act[self.q.output_name][:len(chunk)]).astype(I64)
+            rows_out.extend(logits)
+        return rows_out
+
+    def decode(self, token: int, pos: int, acts: list | None = None) -> np.ndarray:
+        """One M=1 launch (golden.py:392-397)."""
+        self._launch_tokens([token], pos, 1)
+        if acts is not None:
+            acts.append({"kind": "decode", "pos": pos, "rows": 1, "valid_rows": 1, "acts": self._collect(1)})
+        return _down(self._act[self.q.output_name][0]).astype(I64)
+
+    def generate(self, prompt_tokens, n_tokens: int, acts: list | None = None) -> dict:
+        """Greedy generation with the launch sequence of golden.py:399-440; returns the golden.json record."""
+        if not isinstance(n_tokens, int) or n_tokens < 0:
+            raise ValueError("n_tokens must be a nonnegative integer")
+        prompt_tokens = [int(t) for t in prompt_tokens]
+        if not prompt_tokens:
+            raise ValueError("empty prompt")
+        if len(prompt_tokens) + n_tokens > self.max_seq:
+            raise ValueError(f"prompt + tokens = {len(prompt_tokens) + n_tokens} exceeds max_seq={self.max_seq}")
+        self.reset()
+        steps, argmax_per_step, logits_rows = [], [], []
+
+        def record(kind: str, pos: int, valid: int, row: np.ndarray) -> int:
+            steps.append({"kind": kind, "pos": pos, "rows": self.prefill_m if kind == "prefill" else 1,
+                          "valid_rows": valid})
+            argmax_per_step.append(self.argmax(row, self.vocab))
+            logits_rows.append([int(v) for v in row[:self.vocab]])
+            return argmax_per_step[-1]
+
+        rows = self.prefill(prompt_tokens, acts)
+        L = len(prompt_tokens)
+        n_chunks = math.ceil(L / self.prefill_m)
+        nxt = -1
+        for c in range(n_chunks):
+            last = min(L, (c + 1) * self.prefill_m) - 1
+            nxt = record("prefill", c * self.prefill_m, last + 1 - c * self.prefill_m, rows[last])
+        generated: list[int] = []
+        for i in range(n_tokens):
+            generated.append(nxt)
+            if L + i + 1 >= self.max_seq:
+                break
+            nxt = record("decode", L + i, 1, self.decode(nxt, L + i, acts))
+        return {"prompt_tokens": prompt_tokens, "generated": generated, "argmax_per_step": argmax_per_step,
+                "logits_last_rows": logits_rows, "steps": steps,
+                "model": {"vocab": self.vocab, "vocab_padded": self.vocab_padded, "E_LOGIT": self.E_LOGIT,
+                          "E_RES": self.E_RES, "max_seq": self.max_seq}}
+
+
+def dump_acts(acts: list, out_dir: Path) -> int:
+    """step{i:03d}_{kind}_pos{P}_{name}.npy as int32 for every activation (golden.py:443-450)."""
+    out_dir = Path(out_dir)
+    out_dir.mkdir(parents=True, exist_ok=True)
+    n = 0
+    for i, step in enumerate(acts):
+        for name, arr in step["acts"].items():
+            np.save(out_dir / f"step{i:03d}_{step['kind']}_pos{step['pos']}_{name}.npy", np.asarray(arr).astype(np.int32))
+            n += 1
+    return n
+
+
+def main(argv=None) -> None:
+    """CLI of golden.py:453-477.  A char-level tokenizer.json ({"itos": [...]}) next to the qgraph
+    is used as in the reference; --prompt-ids bypasses it with explicit token ids."""
+    ap = argparse.ArgumentParser(description="GPU golden model (integer datapath on MI355X)")
+    ap.add_argument("--qgraph", required=True)
+    ap.add_argument("--prompt", default="ROMEO:")
+    ap.add_argument("--prompt-ids", default=None, help="comma-separated token ids (instead of --prompt)")
+    ap.add_argument("--tokens", type=int, default=64)
+    ap.add_argument("--tokenizer", default=None, help="tokenizer.json (default: <qgraph>/tokenizer.json)")
+    ap.add_argument("-o", "--out", default="build/golden.json")
+    ap.add_argument("--dump-acts", default=None)
+    args = ap.parse_args(argv)
+    itos = None
+    if args.prompt_ids is not None:
+        prompt = [int(t) for t in args.prompt_ids.split(",") if t.strip()]
+    else:
+        tok_path = Path(args.tokenizer) if args.tokenizer else Path(args.qgraph) / "tokenizer.json"
+        itos = json.loads(Path(tok_path).read_text())["itos"]
+        stoi = {c: i for i, c in enumerate(itos)}
+        prompt = [stoi[c] for c in args.prompt]
+    g = GoldenModel(args.qgraph)
+    acts = [] if args.dump_acts else None
+    rec = g.generate(prompt, args.tokens, acts)
+    if itos is not None:
+        rec["prompt"] = args.prompt
+        rec["text"] = "".join(itos[t] for t in rec["generated"])
+    Path(args.out).parent.mkdir(parents=True, exist_ok=True)
+    with open(args.out, "w") as f:
+        json.dump(rec, f)
+    print(f"wrote {args.out}: {len(rec['steps'])} launches, {len(rec['generated'])} tokens")
+    if itos is not None:
+        print(args.prompt + rec["text"])
+    if acts is not None:
+        n = dump_acts(acts, Path(args.dump_acts))
+        print(f"dumped {n} activation arrays to {args.dump_acts}")
+
+
+if __name__ == "__main__":
+    main()

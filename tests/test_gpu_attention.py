@@ -1,0 +1,91 @@
+"""GPU parity of the attn engine (kv_write + causal GQA attention) against the CPU oracle,
+bit-exact, including BASELINE config 5's long-context shapes (T = 4096 = 16 tiles of 256,
+head_dim 128 and the head_dim-256 extra case)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from llaccel_amd import _lib
+from oracle import golden_np as O
+from tests.gpu_helpers import down, ptr, stream, up, workspace
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_attention(q, kc, vc, pos, H, Hkv, D, Ms, Ss, Mo, So, pb):
+    t = __import__("torch")
+    M = q.shape[0]
+    qd, kd, vd = up(q, np.int8), up(kc, np.int8), up(vc, np.int8)
+    out = t.empty((M, H * D), dtype=t.int8, device="cuda")
+    _lib.call("llhip_attention", ptr(qd), M, H, Hkv, D, H * D, pos, None, ptr(kd), ptr(vd), kc.shape[1], Ms, Ss, Mo,
+              So, pb, ptr(out), H * D, ptr(workspace()), stream())
+    return down(out)
+
+
+CASES = [
+    # M, H, Hkv, D, pos, max_seq
+    (1, 4, 2, 16, 47, 64),
+    (16, 4, 2, 16, 0, 64),
+    (16, 9, 3, 64, 112, 256),
+    (1, 14, 2, 64, 767, 1024),
+    (16, 14, 2, 64, 496, 1024),
+    (1, 16, 8, 128, 4095, 4096),
+    (1, 8, 2, 256, 4095, 4096),
+    (16, 8, 2, 256, 4080, 4096),
+    (3, 2, 1, 32, 254, 260),
+]
+
+
+@pytest.mark.parametrize("M,H,Hkv,D,pos,max_seq", CASES)
+def test_attention_matches_oracle(M, H, Hkv, D, pos, max_seq):
+    rng = np.random.default_rng(M * 1000 + H * 10 + D + pos)
+    kc = rng.integers(-128, 128, (Hkv, max_seq, D)).astype(np.int8)
+    vc = rng.integers(-128, 128, (Hkv, max_seq, D)).astype(np.int8)
+    q = rng.integers(-128, 128, (M, H * D))
+    # score scale chosen so softmax is neither one-hot nor flat: z ~ (mx - s) * 2^-k
+    Ms, Ss = int(rng.integers(1 << 30, 1 << 31)), 31 + int(np.log2(D)) + 4
+    Mo, So = int(rng.integers(1 << 30, 1 << 31)), 38
+    for pb in (15, 8):
+        got = gpu_attention(q, kc, vc, pos, H, Hkv, D, Ms, Ss, Mo, So, pb)
+        want = O.attention_c(q, kc, vc, pos, H, Hkv, D, Ms, Ss, Mo, So, pb)
+        assert np.array_equal(got, want), pb
+    assert np.abs(got).max() > 0
+
+
+def test_kv_write_and_positions():
+    rng = np.random.default_rng(3)
+    t = __import__("torch")
+    Hkv, D, max_seq, M = 3, 64, 256, 16
+    k = rng.integers(-128, 128, (M, Hkv * D))
+    v = rng.integers(-128, 128, (M, Hkv * D))
+    kc = t.zeros((Hkv, max_seq, D), dtype=t.int8, device="cuda")
+    vc = t.zeros_like(kc)
+    kd, vd = up(k, np.int8), up(v, np.int8)
+    _lib.call("llhip_kv_write", ptr(kd), ptr(vd), M, Hkv, D, Hkv * D, Hkv * D, 100, None, ptr(kc), ptr(vc), max_seq,
+              stream())
+    want = np.zeros((Hkv, max_seq, D), np.int64)
+    want[:, 100:116] = k.reshape(M, Hkv, D).transpose(1, 0, 2)
+    assert np.array_equal(down(kc), want)
+    want[:, 100:116] = v.reshape(M, Hkv, D).transpose(1, 0, 2)
+    assert np.array_equal(down(vc), want)
+    with pytest.raises(ValueError, match="max_seq"):
+        _lib.call("llhip_kv_write", ptr(kd), ptr(vd), M, Hkv, D, Hkv * D, Hkv * D, 250, None, ptr(kc), ptr(vc),
+                  max_seq, stream())
+
+
+def test_device_position():
+    """pos read from device memory (decode state inside a captured graph) == host pos."""
+    t = __import__("torch")
+    rng = np.random.default_rng(11)
+    H, Hkv, D, max_seq = 14, 2, 64, 1024
+    kc = rng.integers(-128, 128, (Hkv, max_seq, D))
+    vc = rng.integers(-128, 128, (Hkv, max_seq, D))
+    q = rng.integers(-128, 128, (1, H * D))
+    qd, kd, vd = up(q, np.int8), up(kc, np.int8), up(vc, np.int8)
+    posd = t.tensor([600], dtype=t.int32, device="cuda")
+    out = t.empty((1, H * D), dtype=t.int8, device="cuda")
+    _lib.call("llhip_attention", ptr(qd), 1, H, Hkv, D, H * D, 0, ptr(posd), ptr(kd), ptr(vd), max_seq, 1 << 30, 40,
+              1 << 30, 38, 15, ptr(out), H * D, ptr(workspace()), stream())
+    assert np.array_equal(down(out), O.attention_c(q, kc.astype(np.int8), vc.astype(np.int8), 600, H, Hkv, D,
+                                                   1 << 30, 40, 1 << 30, 38, 15))

@@ -1,0 +1,102 @@
+"""GPU parity of the gemm engine (llhip_linear) against the CPU oracle, bit-exact.
+
+Covers BASELINE config 2 (M in {1,16,128,2048} x (K,N) in {(896,896),(896,4864),(4864,896),
+(896,151936)}) plus every epilogue, bias, i8/i16 output, ragged K/N/M, split-K on and off.
+At M=2048 x N=151936 the oracle checks 8 sampled rows over all columns and 96 sampled
+columns over all rows (an output element depends only on its A row and W row)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import golden_np as O
+from tests.gpu_helpers import gpu_linear, random_rq
+
+pytestmark = pytest.mark.gpu
+SHAPES_KN = [(896, 896), (896, 4864), (4864, 896), (896, 151936)]
+
+
+def _operands(rng, M, K, N, out_i8=True):
+    a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    return a, w, random_rq(rng, N, K, out_i8)
+
+
+@pytest.mark.parametrize("K,N", SHAPES_KN)
+@pytest.mark.parametrize("M", [1, 16, 128, 2048])
+def test_config2_sweep(M, K, N):
+    rng = np.random.default_rng(M * 7 + K + N)
+    a, w, rq = _operands(rng, M, K, N)
+    got = gpu_linear(a, w, rq, out_i8=True)
+    if M * N * K <= 20e9:
+        want = O.linear_c(a, w, rq, None, True, "none", None, 0, None)
+        assert np.array_equal(got, want)
+    else:
+        rows = np.sort(rng.choice(M, 8, replace=False))
+        cols = np.sort(rng.choice(N, 96, replace=False))
+        want_r = O.linear_c(a[rows], w, rq, None, True, "none", None, 0, None)
+        want_c = O.linear_c(a, w[cols], rq[cols], None, True, "none", None, 0, None)
+        assert np.array_equal(got[rows], want_r)
+        assert np.array_equal(got[:, cols], want_c)
+    # outputs are not degenerate (the requant spans the i8 range)
+    assert got.min() < -60 and got.max() > 60 and np.mean(np.abs(got) == 127) < 0.2
+
+
+@pytest.mark.parametrize("epilogue", ["none", "resadd", "silu", "mul"])
+@pytest.mark.parametrize("M", [1, 3, 16, 40, 200])
+def test_epilogues_and_bias(M, epilogue):
+    rng = np.random.default_rng(M + len(epilogue))
+    K, N = 896, 1152
+    a, w, rq = _operands(rng, M, K, N, out_i8=False)
+    bias = rng.integers(-(2**31), 2**31 - 1, N) if M != 3 else rng.integers(-3000, 3000, N)
+    aux = rng.integers(-32768, 32768, (M, N))
+    silu = {"Mi": 1 << 30, "Si": 30, "sh_out": 16}
+    kw = dict(bias=bias, out_i8=False, epilogue=epilogue, aux=aux if epilogue in ("resadd", "mul") else None,
+              aux_shift=11 if epilogue == "mul" else 0, silu=silu if epilogue == "silu" else None)
+    got = gpu_linear(a, w, rq, **kw)
+    want = O.linear_c(a, w, rq, bias, False, epilogue, kw["aux"], kw["aux_shift"], kw["silu"])
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 64, 64), (16, 64, 172), (16, 172, 64), (5, 16, 3), (1, 4864, 896),
+                                   (17, 172, 33), (33, 96, 130), (2, 1, 5), (16, 65, 17), (300, 64, 1000)])
+def test_ragged_shapes(M, K, N):
+    rng = np.random.default_rng(M * 131 + K * 7 + N)
+    a, w, rq = _operands(rng, M, K, N, out_i8=False)
+    bias = rng.integers(-5000, 5000, N)
+    got = gpu_linear(a, w, rq, bias=bias)
+    assert np.array_equal(got, O.linear_c(a, w, rq, bias, False, "none", None, 0, None))
+
+
+def test_split_k_matches_unsplit_and_self_cleans():
+    """The split-K path (workspace) and the one-wave-per-tile path give identical results, and
+    repeated calls stay exact (the workspace is left zeroed)."""
+    rng = np.random.default_rng(5)
+    a, w, rq = _operands(rng, 1, 4864, 896)
+    r1 = gpu_linear(a, w, rq, out_i8=True, ws=True)
+    r2 = gpu_linear(a, w, rq, out_i8=True, ws=False)
+    r3 = gpu_linear(a, w, rq, out_i8=True, ws=True)
+    want = O.linear_c(a, w, rq, None, True, "none", None, 0, None)
+    assert np.array_equal(r1, want) and np.array_equal(r2, want) and np.array_equal(r3, want)
+
+
+def test_extreme_operands():
+    """All -128 operands: |acc| = K * 2^14 at K=4864, full-range bias, M = 2^31 - 1."""
+    K, N = 4864, 64
+    a = np.full((16, K), -128, np.int8)
+    w = np.full((N, K), -128, np.int8)
+    w[1::2] = 127
+    rq = np.stack([np.full(N, 2**31 - 1), np.arange(N) % 64], 1).astype(np.int32)
+    bias = np.where(np.arange(N) % 3 == 0, 2**31 - 1, -(2**31))
+    for out_i8 in (True, False):
+        got = gpu_linear(a, w, rq, bias=bias, out_i8=out_i8)
+        assert np.array_equal(got, O.linear_c(a, w, rq, bias, out_i8, "none", None, 0, None))
+
+
+def test_error_paths():
+    rng = np.random.default_rng(1)
+    a, w, rq = _operands(rng, 2, 64, 16)
+    with pytest.raises(ValueError, match="i8 output"):
+        gpu_linear(a, w, rq, out_i8=True, epilogue="resadd", aux=np.zeros((2, 16)))
+    with pytest.raises(ValueError):
+        gpu_linear(a, w, rq, out_i8=False, epilogue="mul", aux=np.zeros((2, 16)), aux_shift=64)

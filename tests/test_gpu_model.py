@@ -1,0 +1,112 @@
+"""GPU GoldenModel (llaccel_amd.golden) against the outputs of the reference's own
+golden.py (tests/golden/ref_tiny_*), the CPU oracle, and the invariants of the reference's
+tests/python/test_golden_e2e.py."""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+from llaccel_amd import golden as G
+from llaccel_amd import synth
+from oracle import golden_np as O
+
+pytestmark = pytest.mark.gpu
+CASES = ["ref_tiny_v2", "ref_tiny_v1", "ref_tiny_v2_pad", "ref_tiny_v2_m4"]
+
+
+def _load(golden_dir, name):
+    d = golden_dir / name
+    return (d / "qgraph", json.loads((d / "meta.json").read_text()), json.loads((d / "record.json").read_text()),
+            np.load(d / "kv_final.npz"), np.load(d / "acts.npz"))
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_reproduces_reference_golden_run(golden_dir, name):
+    qdir, meta, rec, kv, acts = _load(golden_dir, name)
+    g = G.GoldenModel(qdir)
+    got_acts: list = []
+    got = g.generate(meta["prompt"], meta["n_tokens"], got_acts)
+    assert got == rec
+    for layer, (k, v) in g.kv.items():
+        assert np.array_equal(k, kv[f"k{layer}"]) and np.array_equal(v, kv[f"v{layer}"]), layer
+    assert [{k: a[k] for k in ("kind", "pos", "rows", "valid_rows")} for a in got_acts] == meta["steps"]
+    for i in meta["acts_steps"]:
+        names = {key.split("/", 1)[1] for key in acts.files if key.startswith(f"step{i}/")}
+        assert names == set(got_acts[i]["acts"])
+        for n in names:
+            assert np.array_equal(got_acts[i]["acts"][n], acts[f"step{i}/{n}"]), (i, n)
+
+
+def test_run_chunk_acts_and_determinism(golden_dir):
+    qdir = golden_dir / "ref_tiny_v2" / "qgraph"
+    g = G.GoldenModel(qdir)
+    o = O.OracleModel(qdir)
+    rows = g.embed_rows([1, 2, 3], 16)
+    assert np.array_equal(rows, o.embed_rows([1, 2, 3], 16))
+    a1, a2 = {}, {}
+    l1 = g.run_chunk(rows, 0, a1)
+    l2 = o.run_chunk(rows, 0, a2)
+    assert np.array_equal(l1, l2) and set(a1) == set(a2)
+    for n in a1:
+        assert np.array_equal(a1[n], a2[n]), n
+    g.reset()
+    assert np.array_equal(g.run_chunk(rows, 0), l1)
+
+
+def test_chunked_prefill_equals_sequential_decode(golden_dir):
+    qdir = golden_dir / "ref_tiny_v2" / "qgraph"
+    toks = np.random.default_rng(3).integers(0, 256, 21).tolist()
+    a = G.GoldenModel(qdir).prefill(toks)
+    g2 = G.GoldenModel(qdir)
+    b = [g2.decode(t, i) for i, t in enumerate(toks)]
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
+
+
+def test_errors(golden_dir, tmp_path):
+    qdir = golden_dir / "ref_tiny_v2" / "qgraph"
+    with pytest.raises(ValueError, match="max_seq"):
+        G.GoldenModel(qdir).generate(list(range(10)), 64)
+    r = G.GoldenModel(qdir).generate(list(range(10)), 54)
+    assert len(r["generated"]) == 54 and r["steps"][-1]["pos"] == 62
+    with pytest.raises(ValueError, match="max_seq"):
+        G.GoldenModel(qdir).run_chunk(np.zeros((16, 64)), 60)
+    for pm in (0, 3, 17):
+        d = tmp_path / f"q{pm}"
+        d.mkdir()
+        g = json.loads((qdir / "qgraph.json").read_text())
+        g["model"]["prefill_m"] = pm
+        (d / "qgraph.json").write_text(json.dumps(g))
+        (d / "qweights.bin").write_bytes((qdir / "qweights.bin").read_bytes())
+        with pytest.raises(ValueError, match="max_seq must be divisible by prefill_m"):
+            G.GoldenModel(d)
+
+
+def test_kv_snapshot_and_preinitialised_state(golden_dir):
+    """Preinitialised-KV boundary launch (regress_pretrained_boundaries.py:55-69 pattern)."""
+    qdir = golden_dir / "ref_tiny_v2" / "qgraph"
+    rng = np.random.default_rng(9)
+    g, o = G.GoldenModel(qdir), O.OracleModel(qdir)
+    for layer in g.kv:
+        k = rng.integers(-128, 128, o.kv[layer][0].shape).astype(np.int8)
+        v = rng.integers(-128, 128, o.kv[layer][1].shape).astype(np.int8)
+        g.set_kv(layer, k, v)
+        o.kv[layer][0][...] = k
+        o.kv[layer][1][...] = v
+    assert np.array_equal(g.decode(17, 50), o.decode(17, 50))
+    for layer in g.kv:
+        assert np.array_equal(g.kv[layer][0], o.kv[layer][0]) and np.array_equal(g.kv[layer][1], o.kv[layer][1])
+
+
+@pytest.mark.parametrize("fusion", [True, False])
+def test_smol_shape_prefill_decode(tmp_path, fusion):
+    """SmolLM2-135M shape (config 3, 30 layers, 9/3 heads): 20-token prompt + 4 decode
+    launches, GPU == C oracle on the record and the whole KV state."""
+    qdir = synth.build_qgraph(tmp_path / "smol", "smol", seed=3, fusion=fusion)
+    prompt = synth.seeded_prompt("smol", 20, 1)
+    g = G.GoldenModel(qdir)
+    o = O.OracleModel(qdir, backend="c")
+    assert g.generate(prompt, 4) == o.generate(prompt, 4)
+    for layer in (0, 17, 29):
+        assert np.array_equal(g.kv[layer][0], o.kv[layer][0]) and np.array_equal(g.kv[layer][1], o.kv[layer][1])

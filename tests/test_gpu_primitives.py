@@ -1,0 +1,150 @@
+"""GPU parity of the elementwise primitives and vec-engine kernels against the CPU oracle
+(bit-exact).  Calls go through llaccel_amd.golden, i.e. through the libllhip C ABI."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from llaccel_amd import golden as G
+from oracle import golden_np as O
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(7)
+
+
+def test_rshr_full_domain():
+    vals = np.concatenate([np.array([-(1 << 63), (1 << 63) - 1, -1, 0, 1], np.int64),
+                           RNG.integers(-(1 << 63), (1 << 63) - 1, 500, dtype=np.int64)])
+    for s in (0, 1, 2, 7, 14, 31, 32, 62, 63):
+        assert np.array_equal(G.rshr(vals, s), O.rshr(vals, s))
+    shifts = RNG.integers(0, 64, vals.shape[0])
+    assert np.array_equal(G.rshr(vals, shifts), O.rshr(vals, shifts))
+    assert G.rshr(np.array([5]), 1)[0] == 3 and G.rshr(np.array([-5]), 1)[0] == -2
+    with pytest.raises(ValueError):
+        G.rshr(np.array([1]), 64)
+
+
+def test_saturation_and_mulshift():
+    v = np.array([-10**9, -32769, -32768, -129, -128, 0, 127, 128, 255, 256, 32767, 32768, 65535, 65536, 10**9])
+    for f in ("sat8", "satu8", "sat16", "satu16"):
+        assert np.array_equal(getattr(G, f)(v), getattr(O, f)(v)), f
+    x = RNG.integers(-(1 << 40), 1 << 40, 4000)
+    M = RNG.integers(0, 1 << 32, 4000)
+    S = RNG.integers(0, 64, 4000)
+    assert np.array_equal(G.mulshift(x, M, S), O.mulshift(x, M, S))
+    assert np.array_equal(G.requant16(x >> 10, M, S), O.requant16(x >> 10, M, S))
+    assert np.array_equal(G.requant8(x >> 10, M, S), O.requant8(x >> 10, M, S))
+    # broadcasting of per-channel parameters like golden.py:329
+    acc = RNG.integers(-(1 << 30), 1 << 30, (5, 7))
+    Mn, Sn = RNG.integers(1 << 30, 1 << 31, 7)[None, :], RNG.integers(20, 50, 7)[None, :]
+    assert np.array_equal(G.requant16(acc, Mn, Sn), O.requant16(acc, Mn, Sn))
+
+
+def test_isqrt_udiv():
+    for t in [0, 1, 2, 3, (1 << 48) - 1, 1 << 47, 65535**2] + RNG.integers(0, 1 << 48, 20).tolist():
+        assert G.isqrt48(t) == math.isqrt(t)
+    with pytest.raises(ValueError):
+        G.isqrt48(1 << 48)
+    assert G.udiv(10, 3) == 3 and G.udiv(10, 0) == 10 and G.udiv(2**31, 65534) == 32769
+    assert G.udiv(2**40, 1) == (2**40) & 0xFFFFFFFF
+    with pytest.raises(ValueError):
+        G.udiv(-1, 2)
+
+
+def test_silu_vmul_vadd_vquant():
+    x = np.arange(-32768, 32768, 3)
+    for Mi, Si, sh in ((2**30, 30, 16), (1518500250, 31, 15), (2**31 - 1, 33, 14)):
+        assert np.array_equal(G.silu16(x, Mi, Si, sh), O.silu16(x, Mi, Si, sh))
+    a = RNG.integers(-32768, 32768, 5000)
+    b = RNG.integers(-32768, 32768, 5000)
+    for sh in (0, 1, 10, 15, 31):
+        assert np.array_equal(G.vmul(a, b, sh), O.vmul(a, b, sh))
+        assert np.array_equal(G.vadd(a, b, sh), O.vadd(a, b, sh))
+    assert np.array_equal(G.vquant(a, 2**30, 38), O.vquant(a, 2**30, 38))
+    assert G.vmul(np.array([1000, -1000, 32767]), np.array([1000, 1000, 32767]), 10).tolist() == [977, -977, 32767]
+
+
+@pytest.mark.parametrize("K", [16, 64, 128, 172, 576, 896, 1024, 4864])
+def test_rmsnorm(K):
+    x = RNG.integers(-32768, 32768, (9, K)) >> RNG.integers(0, 12, (9, 1))
+    x[0] = 0
+    g = RNG.integers(-32768, 32768, K)
+    for eps_t, C, sh in ((0, 2**32 - 1, 40), (12345, int(2**24 * math.sqrt(K)), 24), (2**32 - 1, 1, 0)):
+        assert np.array_equal(G.rmsnorm(x, g, eps_t, C, sh), O.rmsnorm(x, g, eps_t, C, sh))
+
+
+@pytest.mark.parametrize("H,D", [(4, 16), (2, 64), (14, 64), (16, 128), (8, 256)])
+def test_rope(H, D):
+    inv = 1e6 ** (-np.arange(0, D, 2) / D)
+    ang = np.outer(np.arange(300), inv)
+    c = np.round(np.cos(ang) * 16384).astype(np.int64)
+    s = np.round(np.sin(ang) * 16384).astype(np.int64)
+    x = RNG.integers(-32768, 32768, (16, H * D))
+    for pos in (0, 17, 284):
+        assert np.array_equal(G.rope(x, H, D, c, s, pos), O.rope(x, H, D, c, s, pos))
+
+
+def test_attention_head_known_answers():
+    """test_golden_primitives.py:141-155, 197-231 and test_rounding_boundaries.py:19-29 on the GPU."""
+    D = 16
+    v = RNG.integers(-127, 128, (1, D))
+    out = G.attention_head(RNG.integers(-127, 128, D), RNG.integers(-127, 128, (1, D)), v, 2**30, 40, 2155905153, 39)
+    assert np.array_equal(out, v[0])
+    for pb in (8, 15):
+        for dim in (16, 32, 64):
+            q = np.zeros(dim, np.int64)
+            q[0] = 127
+            vals = np.zeros((2, dim), np.int64)
+            vals[:, 0] = [-127, 127]
+            outs = []
+            for off in (0, 126, -128):
+                keys = np.zeros((2, dim), np.int64)
+                keys[:, 0] = [off, off + 1]
+                outs.append(G.attention_head(q, keys, vals, 1 << 30, 24, 1 << 30, 38, pb))
+            assert all(np.array_equal(o, outs[0]) for o in outs) and outs[0][0] == 127
+            q.fill(127)
+            keys = np.array([[-128] * dim, [127] * dim], np.int64)
+            assert G.attention_head(q, keys, vals, 2**32 - 1, 0, 1 << 30, 38, pb)[0] == 127
+    for T in (1, 2, 100, 171, 255, 256):
+        for val in (-128, -1, 0, 127):
+            got = G.attention_head(np.zeros(16), np.zeros((T, 16)), np.full((T, 16), val), 1, 0, 1 << 30, 38, 15)
+            assert np.max(np.abs(got - val)) <= 1
+    assert int(G.attention_head(np.zeros(16), np.zeros((171, 16)), np.full((171, 16), 127), 1, 0, 1 << 30, 38)[0]) == 85
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+def test_attention_head_random(D):
+    for T in (1, 3, 255, 256, 257, 1000):
+        q = RNG.integers(-128, 128, D)
+        k = RNG.integers(-128, 128, (T, D))
+        v = RNG.integers(-128, 128, (T, D))
+        Ms, Ss = int(RNG.integers(1 << 30, 1 << 31)), int(RNG.integers(30, 40))
+        Mo, So = int(RNG.integers(1 << 30, 1 << 31)), int(RNG.integers(36, 42))
+        for pb in (8, 15):
+            assert np.array_equal(G.attention_head(q, k, v, Ms, Ss, Mo, So, pb),
+                                  O.attention_head(q, k, v, Ms, Ss, Mo, So, pb)), (T, pb)
+
+
+def test_exact_blas_matmul():
+    """test_exact_blas.py:6-19 on the GPU."""
+    for m, n, k in ((1, 17, 16), (4, 33, 4096), (16, 257, 512), (3, 1025, 32)):
+        a = RNG.integers(-32768, 32768, (m, k), dtype=np.int64)
+        w = RNG.integers(-128, 128, (n, k), dtype=np.int8)
+        a[0, :] = -32768
+        w[0, :] = -128
+        assert np.array_equal(G.exact_blas_matmul(a, w, 17), a @ w.astype(np.int64).T)
+    with pytest.raises(ValueError, match="bound"):
+        G.exact_blas_matmul(np.array([[2**53]], np.int64), np.array([[127]], np.int8))
+    with pytest.raises(ValueError, match="integer"):
+        G.exact_blas_matmul(np.ones((1, 1)), np.ones((1, 1), np.int8))
+
+
+def test_argmax_lowest_index_on_ties():
+    row = np.zeros(151936, np.int64)
+    row[[5, 100, 151935]] = 7
+    assert G.GoldenModel.argmax(row, 151936) == 5
+    row = RNG.integers(-32768, 32768, 49152)
+    assert G.GoldenModel.argmax(row, 49152) == int(np.argmax(row))
+    assert G.GoldenModel.argmax(row, 1000) == int(np.argmax(row[:1000]))
