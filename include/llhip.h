@@ -109,6 +109,14 @@ int llhip_embed_rows(const int16_t* embed, int64_t vocab_rows, int64_t dim, cons
 /* golden.py:376-377  idx[r] = first argmax of logits[r][0:vocab] (row stride ld) */
 int llhip_argmax_i16(const int16_t* logits, int64_t rows, int64_t ld, int64_t vocab, int32_t* idx, void* stream);
 
+/* golden.py:376-377 + the launch record of golden.py:411-414, in decode-loop form: first argmax
+ * of logits[0:vocab] -> *token; when *step < ring_cap the row is copied to ring_rows[*step]
+ * (row stride ring_ld) and the token to ring_tokens[*step]; then *pos += 1 and *step += 1.
+ * Everything stays on the device, so a captured decode launch needs no host round trip. */
+int llhip_greedy_step(const int16_t* logits, int64_t vocab, int32_t* token, int32_t* pos, int32_t* step,
+                      int16_t* ring_rows, int64_t ring_ld, int32_t* ring_tokens, int64_t ring_cap, void* ws,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

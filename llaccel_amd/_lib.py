@@ -47,6 +47,7 @@ _SIGS = {
                         _i64, _p, _p],
     "llhip_embed_rows": [_p, _i64, _i64, _p, _i64, _i64, _p, _p],
     "llhip_argmax_i16": [_p, _i64, _i64, _i64, _p, _p],
+    "llhip_greedy_step": [_p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],
 }
 _RESTYPES = {"llhip_last_error": ctypes.c_char_p, "llhip_workspace_bytes": _i64}
 
@@ -67,6 +68,10 @@ def lib():
     """The loaded library (raises LibraryNotBuilt if it has not been built)."""
     global _LIB
     if _LIB is None:
+        try:  # load PyTorch's HIP runtime first so the library binds to the same runtime instance
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not LIB_PATH.exists():
             raise LibraryNotBuilt(f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
                                   f"g.build()'` (make -C llaccel_amd/csrc)")

@@ -25,9 +25,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 enum Epi : int { EPI_NONE = 0, EPI_RESADD = 1, EPI_SILU = 2, EPI_MUL = 3 };
 
-// workspace layout (bytes)
-constexpr int64_t WS_GEMM_PARTIALS = 0;          // int32 [16][N], N <= 65536
-constexpr int64_t WS_GEMM_COUNTERS = 4 << 20;    // uint32 per column tile
 constexpr int64_t GEMM_SPLIT_MAX_N = 65536;
 
 struct LinearArgs {

@@ -143,6 +143,53 @@ __global__ __launch_bounds__(256) void argmax_kernel(const int16_t* __restrict__
   }
 }
 
+// Decode-loop step on the device: first argmax of logits[0:vocab] -> *token, the row and the
+// token stored in record slot *step, then *pos += 1 and *step += 1.  Blocks reduce their slice
+// to a 64-bit key (value, then lowest index) with one atomicMax; the last block to arrive
+// publishes the token, advances the state and clears the workspace slots.
+__global__ __launch_bounds__(256) void greedy_step_kernel(const int16_t* __restrict__ logits, int64_t vocab,
+                                                          int32_t* token, int32_t* pos, int32_t* step,
+                                                          int16_t* __restrict__ ring_rows, int64_t ring_ld,
+                                                          int32_t* ring_tok, int64_t ring_cap,
+                                                          unsigned long long* key_slot, uint32_t* counter) {
+  __shared__ uint64_t best[4];
+  const int s = *step;
+  const bool rec = s < ring_cap;
+  int16_t* dst = ring_rows + (int64_t)s * ring_ld;
+  uint64_t key = 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < vocab; i += stride) {
+    const int16_t v = logits[i];
+    if (rec) dst[i] = v;
+    const uint64_t k = amax_key(v, i);
+    key = k > key ? k : key;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    uint32_t lo = __shfl_xor((uint32_t)key, off);
+    uint32_t hi = __shfl_xor((uint32_t)(key >> 32), off);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    key = o > key ? o : key;
+  }
+  if ((threadIdx.x & 63) == 0) best[threadIdx.x >> 6] = key;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  uint64_t k = best[0];
+  for (int w = 1; w < 4; ++w) k = best[w] > k ? best[w] : k;
+  atomicMax(key_slot, (unsigned long long)k);
+  __threadfence();
+  const uint32_t prev = atomicAdd(counter, 1u);
+  if (prev != gridDim.x - 1) return;
+  __threadfence();
+  const unsigned long long win = atomicExch(key_slot, 0ull);
+  const int32_t idx = (int32_t)(0xFFFFFFFFu - (uint32_t)(win & 0xFFFFFFFFull));
+  *token = idx;
+  if (rec) ring_tok[s] = idx;
+  *pos = *pos + 1;
+  *step = s + 1;
+  atomicExch(counter, 0u);
+}
+
 }  // namespace llhip
 
 using namespace llhip;
@@ -215,6 +262,21 @@ int llhip_embed_rows(const int16_t* embed, int64_t vocab_rows, int64_t dim, cons
   if (M * dim == 0) return 0;
   hipLaunchKernelGGL(embed_kernel, dim3((unsigned)ceil_div(M * dim, 256)), dim3(256), 0, (hipStream_t)stream, embed, dim,
                      tokens, n_tokens, M, rows);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+int llhip_greedy_step(const int16_t* logits, int64_t vocab, int32_t* token, int32_t* pos, int32_t* step,
+                      int16_t* ring_rows, int64_t ring_ld, int32_t* ring_tokens, int64_t ring_cap, void* ws,
+                      void* stream) {
+  if (vocab <= 0 || vocab > 0x7FFFFFFF || ring_ld < vocab || ring_cap < 0 || !ws || !token || !pos || !step)
+    return fail(-EINVAL, "greedy_step: bad arguments");
+  char* w = static_cast<char*>(ws) + WS_GREEDY;
+  int64_t blocks = ceil_div(vocab, 256 * 8);
+  if (blocks > 120) blocks = 120;
+  hipLaunchKernelGGL(greedy_step_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, logits, vocab, token,
+                     pos, step, ring_rows, ring_ld, ring_tokens, ring_cap, reinterpret_cast<unsigned long long*>(w),
+                     reinterpret_cast<uint32_t*>(w + 8));
   LLHIP_LAUNCH_CHECK();
   return 0;
 }

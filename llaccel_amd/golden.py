@@ -346,11 +346,24 @@ _TDT = {"i8": "int8", "i16": "int16"}
 class _Deferred:
     """A graph error that the reference raises when the op executes; raised at the same point."""
 
+    kind = "error"
+
     def __init__(self, exc: Exception) -> None:
         self.exc = exc
 
-    def __call__(self, M, pos):
+    def __call__(self, M, pos, pd=None):
         raise self.exc
+
+
+class _Step:
+    """One compiled op: `fn(M, pos, pos_dev)` launches its kernel(s); `bytes_fn(M)` gives the
+    algorithmic HBM bytes of one launch (operands read once, results written once)."""
+
+    def __init__(self, kind: str, fn, bytes_fn=None, name: str = "") -> None:
+        self.kind, self.fn, self.bytes_fn, self.name = kind, fn, bytes_fn, name
+
+    def __call__(self, M, pos, pd=None):
+        self.fn(M, pos, pd)
 
 
 class GoldenModel:
@@ -385,6 +398,10 @@ class GoldenModel:
         self._cap = 0
         self._act_spec: dict[str, tuple[str, int]] = {}
         self._plan = self._compile()
+        self._ensure_capacity(self.prefill_m)
+        self._graph = None
+        self._ring_cap = 0
+        self.use_graph = True
         self.reset()
 
     # ---- device tensors ---------------------------------------------------------------------
@@ -406,6 +423,7 @@ class GoldenModel:
             return
         torch = _t()
         cap = max(M, self.prefill_m)
+        self._graph = None  # captured pointers would dangle
         for name, (dt, cols) in self._act_spec.items():
             self._act[name] = torch.zeros((cap, cols), dtype=getattr(torch, _TDT[dt]), device=self.device)
         self._cap = cap
@@ -413,6 +431,11 @@ class GoldenModel:
     def reset(self) -> None:
         """Zero every layer's (Hkv, max_seq, D) int8 K and V caches (golden.py:266-272)."""
         torch = _t()
+        if getattr(self, "_kv", None):
+            for kc, vc in self._kv.values():  # in place: a captured decode graph holds these addresses
+                kc.zero_()
+                vc.zero_()
+            return
         self._kv: dict[int, tuple] = {}
         for op in self.q.ops:
             if op["op"] == "kv_write":
@@ -454,15 +477,15 @@ class GoldenModel:
             k = op["op"]
             try:
                 if k == "rmsnorm":
-                    plan.append(self._c_rmsnorm(op, need, T))
+                    plan.append(_Step("rmsnorm", self._c_rmsnorm(op, need, T), name=op["out"]))
                 elif k == "quant":
                     _, cols = need(op["in"], "i16")
                     _check_u32(op["M"], "quant M")
                     _check_shift(op["S"], "quant S")
                     spec[op["out"]] = ("i8", cols)
-                    plan.append(self._c_quant(op))
+                    plan.append(_Step("quant", self._c_quant(op), name=op["out"]))
                 elif k == "linear":
-                    plan.append(self._c_linear(op, need, T))
+                    plan.append(_Step("linear", *self._c_linear(op, need, T), name=op["out"]))
                 elif k == "rope":
                     _, cols = need(op["in"], "i16")
                     H, D = int(op["H"]), int(op["D"])
@@ -471,11 +494,11 @@ class GoldenModel:
                     if self.rope_cos.shape[1] != D // 2:
                         raise ValueError("rope table width != D/2")
                     spec[op["out"]] = ("i16", cols)
-                    plan.append(self._c_rope(op))
+                    plan.append(_Step("rope", self._c_rope(op), name=op["out"]))
                 elif k == "kv_write":
-                    plan.append(self._c_kv_write(op, need))
+                    plan.append(_Step("kv_write", self._c_kv_write(op, need), name=str(op["layer"])))
                 elif k == "attention":
-                    plan.append(self._c_attention(op, need))
+                    plan.append(_Step("attention", *self._c_attention(op, need), name=op["out"]))
                 elif k in ("add", "mul"):
                     _, ca = need(op["a"], "i16")
                     _, cb = need(op["b"], "i16")
@@ -483,14 +506,14 @@ class GoldenModel:
                         raise ValueError(f"{k} {op['out']}: operand widths differ")
                     _check_shift(op["sh_b" if k == "add" else "sh"], "shift")
                     spec[op["out"]] = ("i16", ca)
-                    plan.append(self._c_binary(op, k))
+                    plan.append(_Step(k, self._c_binary(op, k), name=op["out"]))
                 elif k == "silu":
                     _, cols = need(op["in"], "i16")
                     _check_u32(op["Mi"], "silu Mi")
                     _check_shift(op["Si"], "silu Si")
                     _check_shift(op["sh_out"], "silu sh_out")
                     spec[op["out"]] = ("i16", cols)
-                    plan.append(self._c_silu(op))
+                    plan.append(_Step("silu", self._c_silu(op), name=op["out"]))
                 else:
                     raise ValueError(f"unknown qgraph op {k!r}")
             except (ValueError, KeyError) as e:
@@ -515,7 +538,7 @@ class GoldenModel:
         src, dst = op["in"], op["out"]
         eps_t, C, sh = int(op["eps_t"]), int(op["C"]), int(op["sh_post"])
 
-        def run(M, pos):
+        def run(M, pos, pd=None):
             x, y = self._buf(src), self._buf(dst)
             _lib.call("llhip_rmsnorm", _ptr(x), M * heads, K, K, _ptr(g), eps_t, C, sh, _ptr(y), K, _stream())
         return run
@@ -524,7 +547,7 @@ class GoldenModel:
         src, dst, Mq, Sq = op["in"], op["out"], int(op["M"]), int(op["S"])
         cols = self._act_spec[src][1]
 
-        def run(M, pos):
+        def run(M, pos, pd=None):
             _lib.call("llhip_quant", _ptr(self._buf(src)), M * cols, Mq, Sq, _ptr(self._buf(dst)), _stream())
         return run
 
@@ -571,20 +594,25 @@ class GoldenModel:
         wd, rqd = self._dt[op["w"]], self._dt[op["rq"]]
         epi = _EPI[ep]
 
-        def run(M, pos):
+        def run(M, pos, pd=None):
             a = self._buf(src)
             auxd = self._buf(aux) if aux is not None else None
             _lib.call("llhip_linear", _ptr(a), M, K, K, _ptr(wd), N, _ptr(rqd), _ptr(bias), epi, _ptr(auxd), N,
                       aux_shift, Mi, Si, sh, int(out_i8), _ptr(self._buf(dst)), N, _ptr(self._ws), _stream())
-        return run
+
+        def nbytes(M):
+            # W + rq + bias + A + out (+ aux)  (linear(M,N,K) bytes of the measurement plan)
+            return (N * K + 8 * N + (4 * N if bias is not None else 0) + M * K + M * N * (1 if out_i8 else 2)
+                    + (2 * M * N if aux is not None else 0))
+        return run, nbytes
 
     def _c_rope(self, op):
         src, dst, H, D = op["in"], op["out"], int(op["H"]), int(op["D"])
         cos_t, sin_t = self._dt["rope_cos"], self._dt["rope_sin"]
         rows = int(cos_t.shape[0])
 
-        def run(M, pos):
-            _lib.call("llhip_rope", _ptr(self._buf(src)), M, H, D, H * D, _ptr(cos_t), _ptr(sin_t), rows, pos, None,
+        def run(M, pos, pd=None):
+            _lib.call("llhip_rope", _ptr(self._buf(src)), M, H, D, H * D, _ptr(cos_t), _ptr(sin_t), rows, pos, pd,
                       _ptr(self._buf(dst)), H * D, _stream())
         return run
 
@@ -597,9 +625,9 @@ class GoldenModel:
         layer = int(op["layer"])
         ksrc, vsrc = op["k"], op["v"]
 
-        def run(M, pos):
+        def run(M, pos, pd=None):
             kc, vc = self._kv[layer]
-            _lib.call("llhip_kv_write", _ptr(self._buf(ksrc)), _ptr(self._buf(vsrc)), M, Hkv, D, ck, cv, pos, None,
+            _lib.call("llhip_kv_write", _ptr(self._buf(ksrc)), _ptr(self._buf(vsrc)), M, Hkv, D, ck, cv, pos, pd,
                       _ptr(kc), _ptr(vc), self.max_seq, _stream())
         return run
 
@@ -622,13 +650,17 @@ class GoldenModel:
         src, dst = op["q"], op["out"]
         Ms, Ss, Mo, So = (int(op[f]) for f in ("Ms", "Ss", "Mo", "So"))
 
-        def run(M, pos):
+        def run(M, pos, pd=None):
             if layer not in self._kv:
                 raise KeyError(layer)
             kc, vc = self._kv[layer]
-            _lib.call("llhip_attention", _ptr(self._buf(src)), M, H, Hkv, D, H * D, pos, None, _ptr(kc), _ptr(vc),
+            _lib.call("llhip_attention", _ptr(self._buf(src)), M, H, Hkv, D, H * D, pos, pd, _ptr(kc), _ptr(vc),
                       self.max_seq, Ms, Ss, Mo, So, pb, _ptr(self._buf(dst)), H * D, _ptr(self._ws), _stream())
-        return run
+
+        def nbytes(M, T):
+            # K and V rows read once per GQA group + q in + out
+            return 2 * Hkv * T * D + 2 * M * H * D
+        return run, nbytes
 
     def _c_binary(self, op, kind):
         a, b, dst = op["a"], op["b"], op["out"]
@@ -636,7 +668,7 @@ class GoldenModel:
         cols = self._act_spec[a][1]
         fn = "llhip_vadd" if kind == "add" else "llhip_vmul"
 
-        def run(M, pos):
+        def run(M, pos, pd=None):
             _lib.call(fn, _ptr(self._buf(a)), _ptr(self._buf(b)), M * cols, sh, _ptr(self._buf(dst)), _stream())
         return run
 
@@ -645,14 +677,14 @@ class GoldenModel:
         Mi, Si, sh = int(op["Mi"]), int(op["Si"]), int(op["sh_out"])
         cols = self._act_spec[src][1]
 
-        def run(M, pos):
+        def run(M, pos, pd=None):
             _lib.call("llhip_silu", _ptr(self._buf(src)), M * cols, Mi, Si, sh, _ptr(self._buf(dst)), _stream())
         return run
 
     # ---- one device launch --------------------------------------------------------------
-    def _execute(self, M: int, pos: int) -> None:
+    def _execute(self, M: int, pos: int, pd=None) -> None:
         for step in self._plan:
-            step(M, pos)
+            step(M, pos, pd)
 
     def _collect(self, M: int) -> dict:
         out = {}
@@ -787,6 +819,92 @@ class GoldenModel:
                   _ptr(self._act[self.q.input_name]), _stream())
         self._execute(M, int(pos))
 
+    # ---- device-resident greedy decode ----------------------------------------------------
+    def _decode_state(self, ring_cap: int) -> None:
+        torch = _t()
+        if ring_cap > self._ring_cap:
+            cap = max(ring_cap, 64)
+            self._ring_rows = torch.zeros((cap, self.vocab), dtype=torch.int16, device=self.device)
+            self._ring_tok = torch.zeros(cap, dtype=torch.int32, device=self.device)
+            self._ring_cap = cap
+            self._graph = None
+        if not hasattr(self, "_st"):
+            self._st = torch.zeros(3, dtype=torch.int32, device=self.device)  # token, pos, step
+
+    def _decode_launch(self) -> None:
+        """Embedding gather of the device token, the op list at the device position, greedy step."""
+        st = self._st
+        tok, pos, step = (ctypes.c_void_p(st.data_ptr() + 4 * i) for i in range(3))
+        _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, tok, 1, 1,
+                  _ptr(self._act[self.q.input_name]), _stream())
+        self._execute(1, 0, pos)
+        _lib.call("llhip_greedy_step", _ptr(self._act[self.q.output_name]), self.vocab, tok, pos, step,
+                  _ptr(self._ring_rows), self.vocab, _ptr(self._ring_tok), self._ring_cap, _ptr(self._ws), _stream())
+
+    def _capture(self) -> None:
+        torch = _t()
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(g, stream=side):
+            self._decode_launch()
+        torch.cuda.current_stream().wait_stream(side)
+        self._graph = g
+
+    def decode_loop(self, token: int, pos: int, n: int, *, sync: bool = True):
+        """Run `n` greedy M=1 decode launches from (token, pos) entirely on the device.
+
+        Launch i decodes at pos + i; its argmax feeds launch i + 1.  Returns the n argmax tokens
+        and the n recorded logits rows ([n][vocab] int16) -- the decode part of the golden.json
+        record.  With `use_graph` each launch is one replay of a captured HIP graph."""
+        if n <= 0:
+            return np.zeros(0, np.int64), np.zeros((0, self.vocab), np.int16)
+        if pos < 0 or pos + n > self.max_seq:
+            raise ValueError(f"positions {pos}..{pos + n - 1} exceed max_seq={self.max_seq}")
+        torch = _t()
+        self._decode_state(n)
+        self._st.copy_(torch.tensor([int(self._token_rows([token])[0]), pos, 0], dtype=torch.int32))
+        if self.use_graph and self._graph is None:
+            self._capture()
+        for _ in range(n):
+            if self.use_graph:
+                self._graph.replay()
+            else:
+                self._decode_launch()
+        if not sync:
+            return None
+        return _down(self._ring_tok[:n]).astype(np.int64), self._ring_rows[:n].cpu().numpy()
+
+    # ---- measurement aids ------------------------------------------------------------------
+    def capture_steps(self, kinds, pos: int):
+        """HIP graph of the M=1 launches of the plan steps whose kind is in `kinds`, reading the
+        position from the device decode state (set to `pos`).  Used to time kernel families."""
+        torch = _t()
+        self._decode_state(1)
+        self._st.copy_(torch.tensor([0, pos, 0], dtype=torch.int32))
+        pd = ctypes.c_void_p(self._st.data_ptr() + 4)
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(g, stream=side):
+            for st in self._plan:
+                if st.kind in kinds:
+                    st(1, 0, pd)
+        torch.cuda.current_stream().wait_stream(side)
+        return g
+
+    def step_bytes(self, kind: str, M: int = 1, T: int = 1) -> int:
+        """Algorithmic HBM bytes of all plan steps of `kind` for one launch of M rows at context T."""
+        total = 0
+        for st in self._plan:
+            if st.kind != kind or st.bytes_fn is None:
+                continue
+            total += st.bytes_fn(M, T) if kind == "attention" else st.bytes_fn(M)
+        return total
+
+    def count_steps(self, kind: str) -> int:
+        return sum(1 for st in self._plan if st.kind == kind)
+
     def prefill(self, tokens, acts: list | None = None) -> list[np.ndarray]:
         """Chunked prefill with model.prefill_m rows per launch (golden.py:379-390)."""
         tokens = [int(t) for t in tokens]
@@ -835,11 +953,24 @@ class GoldenModel:
             last = min(L, (c + 1) * self.prefill_m) - 1
             nxt = record("prefill", c * self.prefill_m, last + 1 - c * self.prefill_m, rows[last])
         generated: list[int] = []
-        for i in range(n_tokens):
-            generated.append(nxt)
-            if L + i + 1 >= self.max_seq:
-                break
-            nxt = record("decode", L + i, 1, self.decode(nxt, L + i, acts))
+        n_dec = min(n_tokens, self.max_seq - L - 1)
+        if acts is None and self.use_graph and n_dec > 0:
+            # device-resident decode: one captured graph per launch, the record kept in a device ring
+            toks, rows_dev = self.decode_loop(nxt, L, n_dec)
+            for i in range(n_tokens):
+                generated.append(nxt)
+                if L + i + 1 >= self.max_seq:
+                    break
+                steps.append({"kind": "decode", "pos": L + i, "rows": 1, "valid_rows": 1})
+                argmax_per_step.append(int(toks[i]))
+                logits_rows.append(rows_dev[i].tolist())
+                nxt = int(toks[i])
+        else:
+            for i in range(n_tokens):
+                generated.append(nxt)
+                if L + i + 1 >= self.max_seq:
+                    break
+                nxt = record("decode", L + i, 1, self.decode(nxt, L + i, acts))
         return {"prompt_tokens": prompt_tokens, "generated": generated, "argmax_per_step": argmax_per_step,
                 "logits_last_rows": logits_rows, "steps": steps,
                 "model": {"vocab": self.vocab, "vocab_padded": self.vocab_padded, "E_LOGIT": self.E_LOGIT,

@@ -110,3 +110,39 @@ def test_smol_shape_prefill_decode(tmp_path, fusion):
     assert g.generate(prompt, 4) == o.generate(prompt, 4)
     for layer in (0, 17, 29):
         assert np.array_equal(g.kv[layer][0], o.kv[layer][0]) and np.array_equal(g.kv[layer][1], o.kv[layer][1])
+
+
+def test_graph_decode_equals_eager_and_reference(golden_dir):
+    """The captured-graph decode loop (default generate path) reproduces the reference record;
+    replays are interleaved with eager launches and checked every time."""
+    qdir, meta, rec, kv, _ = _load(golden_dir, "ref_tiny_v2")
+    g = G.GoldenModel(qdir)
+    assert g.generate(meta["prompt"], meta["n_tokens"]) == rec
+    for layer, (k, v) in g.kv.items():
+        assert np.array_equal(k, kv[f"k{layer}"]) and np.array_equal(v, kv[f"v{layer}"]), layer
+    g.use_graph = False
+    assert g.generate(meta["prompt"], meta["n_tokens"]) == rec
+    g.use_graph = True
+    o = O.OracleModel(qdir, backend="c")
+    for seed in range(3):
+        prompt = synth.seeded_prompt("tiny", 5 + 7 * seed, 100 + seed)
+        assert g.generate(prompt, 20) == o.generate(prompt, 20), seed
+        rows = g.embed_rows([seed], 16)
+        g.reset()
+        o.reset()
+        assert np.array_equal(g.run_chunk(rows, 0), o.run_chunk(rows, 0))
+
+
+def test_decode_loop_matches_sequential_decode(golden_dir):
+    qdir = golden_dir / "ref_tiny_v2_pad" / "qgraph"
+    prompt = list(range(20))
+    g1, g2 = G.GoldenModel(qdir), G.GoldenModel(qdir)
+    r1, r2 = g1.prefill(prompt), g2.prefill(prompt)
+    nxt = G.GoldenModel.argmax(r1[-1], g1.vocab)
+    toks, rows = g1.decode_loop(nxt, 20, 12)
+    t = nxt
+    for i in range(12):
+        row = g2.decode(t, 20 + i)
+        assert np.array_equal(rows[i], row[:g2.vocab]), i
+        t = G.GoldenModel.argmax(row, g2.vocab)
+        assert t == toks[i]
