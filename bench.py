@@ -113,9 +113,9 @@ def gemm_sweep(reps: int = 10):
                           torch.full((N,), 42, dtype=torch.int32, device="cuda")], 1).contiguous()
         o = torch.empty((M, N), dtype=torch.int8, device="cuda")
         p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
         def launch():
+            s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # the capture stream inside the graph
             _lib.call("llhip_linear", p(a), M, K, K, p(w), N, p(rq), None, 0, None, N, 0, 0, 0, 0, 1, p(o), N, p(ws), s)
 
         graph = torch.cuda.CUDAGraph()

@@ -117,6 +117,67 @@ int llhip_greedy_step(const int16_t* logits, int64_t vocab, int32_t* token, int3
                       int16_t* ring_rows, int64_t ring_ld, int32_t* ring_tokens, int64_t ring_cap, void* ws,
                       void* stream);
 
+/* ---- fused decoder blocks (M <= 16 rows per launch) ----
+ * Each computes a run of consecutive qgraph ops in one launch and writes every activation
+ * those ops name, with the values the separate entry points above produce.  Row strides of
+ * the i16 rows are ldx elements; i8 rows are K (or N) elements.  K % 8 == 0. */
+typedef struct llhip_norm_quant_desc {
+  const void* x;     /* i16 [M][ldx] input rows */
+  const void* gamma; /* i16 [K] */
+  void* h_out;       /* i16 [M][ldx] normalised rows, or NULL */
+  void* hq_out;      /* i8 [M][K] quantised rows, or NULL */
+  int64_t ldx, K, eps_t, C, sh_post, Mq, Sq;
+} llhip_norm_quant_desc;
+
+typedef struct llhip_attn_in_desc {
+  llhip_norm_quant_desc pre;
+  const void* W[3];    /* q, k, v weights i8 [N][K] */
+  const void* rq[3];   /* int32 [N][2] */
+  const void* bias[3]; /* int32 [N] or NULL */
+  void* lin_out[3];    /* q i16 [M][H*D], k i16 [M][Hkv*D], v i8 [M][Hkv*D] */
+  const void* nrm_gamma[2]; /* Q/K RMSNorm gamma i16 [D] (has_norm) */
+  void* nrm_out[2];
+  int64_t nrm_eps[2], nrm_C[2], nrm_sh[2];
+  const void* cos_tab; /* i16 [max_seq][D/2] */
+  const void* sin_tab;
+  const void* pos_dev; /* int32 device position or NULL */
+  void* rope_out[2];   /* i16 rows */
+  void* quant_out[2];  /* i8 rows */
+  int64_t quant_M[2], quant_S[2];
+  void* kc; /* int8 caches [Hkv][max_seq][D] */
+  void* vc;
+  int64_t max_seq, M, H, Hkv, D, pos, has_norm;
+} llhip_attn_in_desc;
+
+/* golden.py:286-300 -- rmsnorm, quant, linear q/k/v (+bias), [rmsnorm heads q/k], rope q/k,
+ * quant q/k, kv_write: one workgroup per head block. */
+int llhip_attn_in(const llhip_attn_in_desc* d, void* stream);
+
+typedef struct llhip_mlp_in_desc {
+  llhip_norm_quant_desc pre;
+  const void* Wg; const void* Wu;   /* i8 [N][K] */
+  const void* rqg; const void* rqu; /* int32 [N][2] */
+  const void* bg; const void* bu;   /* int32 [N] or NULL */
+  void* g_out; void* u_out;         /* i16 [M][N] (unfused graphs) or NULL */
+  void* sg_out; void* f_out;        /* i16 [M][N] */
+  void* fq_out;                     /* i8 [M][N] */
+  int64_t silu_Mi, silu_Si, silu_sh, mul_sh, fq_M, fq_S, M, N;
+} llhip_mlp_in_desc;
+
+/* golden.py:286-309 + 332-342 -- rmsnorm, quant, linear gate (silu epilogue) and up (mul
+ * epilogue) [or linear g, linear u, silu, mul], quant. */
+int llhip_mlp_in(const llhip_mlp_in_desc* d, void* stream);
+
+typedef struct llhip_norm_linear_desc {
+  llhip_norm_quant_desc pre;
+  const void* W; const void* rq; const void* bias; const void* aux;
+  void* out; /* [M][N] i16 or i8 */
+  int64_t epilogue, aux_shift, silu_Mi, silu_Si, silu_sh, out_i8, M, N;
+} llhip_norm_linear_desc;
+
+/* golden.py:286-296 + 316-342 -- rmsnorm, quant, one linear with any epilogue. */
+int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

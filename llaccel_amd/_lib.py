@@ -96,3 +96,38 @@ def check(rc: int, what: str) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args), name)
+
+
+# ---- descriptors of the fused entry points (include/llhip.h) -------------------------------
+class NormQuantDesc(ctypes.Structure):
+    _fields_ = [("x", _p), ("gamma", _p), ("h_out", _p), ("hq_out", _p), ("ldx", _i64), ("K", _i64), ("eps_t", _i64),
+                ("C", _i64), ("sh_post", _i64), ("Mq", _i64), ("Sq", _i64)]
+
+
+class AttnInDesc(ctypes.Structure):
+    _fields_ = [("pre", NormQuantDesc), ("W", _p * 3), ("rq", _p * 3), ("bias", _p * 3), ("lin_out", _p * 3),
+                ("nrm_gamma", _p * 2), ("nrm_out", _p * 2), ("nrm_eps", _i64 * 2), ("nrm_C", _i64 * 2),
+                ("nrm_sh", _i64 * 2), ("cos_tab", _p), ("sin_tab", _p), ("pos_dev", _p), ("rope_out", _p * 2),
+                ("quant_out", _p * 2), ("quant_M", _i64 * 2), ("quant_S", _i64 * 2), ("kc", _p), ("vc", _p),
+                ("max_seq", _i64), ("M", _i64), ("H", _i64), ("Hkv", _i64), ("D", _i64), ("pos", _i64),
+                ("has_norm", _i64)]
+
+
+class MlpInDesc(ctypes.Structure):
+    _fields_ = [("pre", NormQuantDesc), ("Wg", _p), ("Wu", _p), ("rqg", _p), ("rqu", _p), ("bg", _p), ("bu", _p),
+                ("g_out", _p), ("u_out", _p), ("sg_out", _p), ("f_out", _p), ("fq_out", _p), ("silu_Mi", _i64),
+                ("silu_Si", _i64), ("silu_sh", _i64), ("mul_sh", _i64), ("fq_M", _i64), ("fq_S", _i64), ("M", _i64),
+                ("N", _i64)]
+
+
+class NormLinearDesc(ctypes.Structure):
+    _fields_ = [("pre", NormQuantDesc), ("W", _p), ("rq", _p), ("bias", _p), ("aux", _p), ("out", _p),
+                ("epilogue", _i64), ("aux_shift", _i64), ("silu_Mi", _i64), ("silu_Si", _i64), ("silu_sh", _i64),
+                ("out_i8", _i64), ("M", _i64), ("N", _i64)]
+
+
+_SIGS.update({
+    "llhip_attn_in": [ctypes.POINTER(AttnInDesc), _p],
+    "llhip_mlp_in": [ctypes.POINTER(MlpInDesc), _p],
+    "llhip_norm_linear": [ctypes.POINTER(NormLinearDesc), _p],
+})

@@ -8,16 +8,16 @@
 // so it cannot be computed online per tile.  Each of them is an exact integer
 // reduction, so any reduction order gives the reference's result.
 //
-// attention_rowhead: one 256-thread block per (row m, query head h).  Scores for
+// attention_rowhead: one 512-thread block per (row m, query head h).  Scores for
 // all T keys are staged in LDS (int32), block reductions give max and sum, and
 // the value pass splits the head dimension into 16-byte chunks across threads
-// and the keys across thread groups.
+// and the keys across thread groups (four keys in flight per thread); partial
+// sums are folded across lanes with shuffles, then across waves in LDS.
 #include "../../include/llhip.h"
 #include "common.h"
 
 namespace llhip {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int ATTN_MAX_T = 12000;  // scores + value partials stay within a 64 KiB block allocation
 
@@ -34,13 +34,19 @@ struct AttnArgs {
   int lds_T;  // score slots in LDS
 };
 
+constexpr int ATTN_THREADS = 512;
+constexpr int ATTN_WAVES = ATTN_THREADS / 64;
+
 __device__ __forceinline__ int32_t block_max_i32(int32_t v, int32_t* red) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off));
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return max(max(red[0], red[1]), max(red[2], red[3]));
+  int32_t r = red[0];
+#pragma unroll
+  for (int w = 1; w < ATTN_WAVES; ++w) r = max(r, red[w]);
+  return r;
 }
 
 __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, int32_t* red) {
@@ -49,19 +55,36 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, int32_t* red) {
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (int32_t)v;
   __syncthreads();
-  return (uint32_t)red[0] + (uint32_t)red[1] + (uint32_t)red[2] + (uint32_t)red[3];
+  uint32_t r = 0;
+#pragma unroll
+  for (int w = 0; w < ATTN_WAVES; ++w) r += (uint32_t)red[w];
+  return r;
 }
 
 __device__ __forceinline__ int32_t sbyte(int w, int i) { return (int32_t)(int8_t)((uint32_t)w >> (8 * i)); }
 
 template <int D>
-__global__ __launch_bounds__(256) void attention_rowhead(AttnArgs p) {
-  extern __shared__ int32_t smem[];
-  __shared__ int32_t red[4];
+__device__ __forceinline__ int32_t dot_row(const v4i* qv, const v4i* kr) {
+  constexpr int DC = D / 16;
+  int32_t s = 0;
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    const v4i kv = kr[c];
+    s = __builtin_amdgcn_sdot4(qv[c].x, kv.x, s, false);
+    s = __builtin_amdgcn_sdot4(qv[c].y, kv.y, s, false);
+    s = __builtin_amdgcn_sdot4(qv[c].z, kv.z, s, false);
+    s = __builtin_amdgcn_sdot4(qv[c].w, kv.w, s, false);
+  }
+  return s;
+}
+
+template <int D>
+__global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
+  extern __shared__ int32_t sc[];  // [lds_T] scores, then probabilities
+  __shared__ int32_t red[ATTN_WAVES];
+  __shared__ int32_t wpart[ATTN_WAVES][D];
   constexpr int DC = D / 16;  // 16-byte chunks per key row
-  constexpr int TG = 256 / DC;
-  int32_t* sc = smem;              // [lds_T] scores, then probabilities
-  int32_t* part = smem + p.lds_T;  // [TG][D] value-pass partial sums
+  constexpr int TG = ATTN_THREADS / DC;
 
   const int h = blockIdx.x;
   const int m = blockIdx.y;
@@ -73,30 +96,25 @@ __global__ __launch_bounds__(256) void attention_rowhead(AttnArgs p) {
   const int8_t* V = p.vc + (int64_t)g * p.max_seq * D;
   const int8_t* qr = p.q + (int64_t)m * p.ldq + (int64_t)h * D;
 
-  // scores s[t] = q . k[t] (int32, |s| <= D * 2^14)
+  // scores s[t] = q . k[t] (int32, |s| <= D * 2^14), two keys in flight per thread
   v4i qv[DC];
 #pragma unroll
   for (int c = 0; c < DC; ++c) qv[c] = *reinterpret_cast<const v4i*>(qr + 16 * c);
   int32_t lmax = INT32_MIN;
-  for (int t = tid; t < T; t += 256) {
-    const v4i* kr = reinterpret_cast<const v4i*>(K + (int64_t)t * D);
-    int32_t s = 0;
-#pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      const v4i kv = kr[c];
-      s = __builtin_amdgcn_sdot4(qv[c].x, kv.x, s, false);
-      s = __builtin_amdgcn_sdot4(qv[c].y, kv.y, s, false);
-      s = __builtin_amdgcn_sdot4(qv[c].z, kv.z, s, false);
-      s = __builtin_amdgcn_sdot4(qv[c].w, kv.w, s, false);
-    }
-    sc[t] = s;
-    lmax = max(lmax, s);
+  for (int t0 = tid; t0 < T; t0 += 2 * ATTN_THREADS) {
+    const int t1 = t0 + ATTN_THREADS;
+    const int32_t s0 = dot_row<D>(qv, reinterpret_cast<const v4i*>(K + (int64_t)t0 * D));
+    int32_t s1 = INT32_MIN;
+    if (t1 < T) s1 = dot_row<D>(qv, reinterpret_cast<const v4i*>(K + (int64_t)t1 * D));
+    sc[t0] = s0;
+    if (t1 < T) sc[t1] = s1;
+    lmax = max(lmax, max(s0, s1));
   }
   const int32_t mx = block_max_i32(lmax, red);
 
-  // p[t] = LUT(mulshift(mx - s[t], Ms, Ss)), sum
+  // p[t] = LUT(mulshift(mx - s[t], Ms, Ss)), then the sum
   uint32_t lsum = 0;
-  for (int t = tid; t < T; t += 256) {
+  for (int t = tid; t < T; t += ATTN_THREADS) {
     const uint32_t pr = lut_prob(mulshift((int64_t)mx - sc[t], p.Ms, p.Ss));
     sc[t] = (int32_t)pr;
     lsum += pr;
@@ -105,34 +123,52 @@ __global__ __launch_bounds__(256) void attention_rowhead(AttnArgs p) {
   const uint32_t inv = (uint32_t)((1ull << 31) / (uint64_t)(total > 1u ? total : 1u));
   const int32_t cap = (1 << p.pb) - 1;
   const int shp = 31 - p.pb;
-  for (int t = tid; t < T; t += 256) {
+  for (int t = tid; t < T; t += ATTN_THREADS) {
     const int64_t pn = rshr((int64_t)sc[t] * (int64_t)inv, shp);
     sc[t] = (int32_t)(pn < cap ? pn : cap);
   }
   __syncthreads();
 
-  // o[d] = sum_t pn[t] * v[t][d]
+  // o[d] = sum_t pn[t] * v[t][d]: thread (tg, dc) takes keys tg, tg+TG, ... (four in flight)
   const int dc = tid % DC, tg = tid / DC;
   int32_t acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0;
-  for (int t = tg; t < T; t += TG) {
-    const v4i vv = *reinterpret_cast<const v4i*>(V + (int64_t)t * D + 16 * dc);
-    const int32_t pn = sc[t];
+  for (int t0 = tg; t0 < T; t0 += 4 * TG) {
+    v4i vv[4];
+    int32_t pn[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[i] += pn * sbyte(vv.x, i);
-      acc[4 + i] += pn * sbyte(vv.y, i);
-      acc[8 + i] += pn * sbyte(vv.z, i);
-      acc[12 + i] += pn * sbyte(vv.w, i);
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u * TG;
+      const bool ok = t < T;
+      vv[u] = ok ? *reinterpret_cast<const v4i*>(V + (int64_t)t * D + 16 * dc) : v4i{0, 0, 0, 0};
+      pn[u] = ok ? sc[t] : 0;
     }
-  }
 #pragma unroll
-  for (int i = 0; i < 16; ++i) part[tg * D + 16 * dc + i] = acc[i];
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[i] += pn[u] * sbyte(vv[u].x, i);
+        acc[4 + i] += pn[u] * sbyte(vv[u].y, i);
+        acc[8 + i] += pn[u] * sbyte(vv[u].z, i);
+        acc[12 + i] += pn[u] * sbyte(vv[u].w, i);
+      }
+  }
+  // lanes l and l ^ (DC * j) hold the same 16 columns: fold them, then across waves in LDS
+#pragma unroll
+  for (int off = DC; off < 64; off <<= 1)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] += __shfl_xor(acc[i], off);
+  const int lane = tid & 63, wave = tid >> 6;
+  if (lane < DC) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) wpart[wave][16 * lane + i] = acc[i];
+  }
   __syncthreads();
-  for (int d = tid; d < D; d += 256) {
+  for (int d = tid; d < D; d += ATTN_THREADS) {
     int32_t o = 0;
-    for (int j = 0; j < TG; ++j) o += part[j * D + d];
+#pragma unroll
+    for (int w = 0; w < ATTN_WAVES; ++w) o += wpart[w][d];
     if (p.pb == 15) o = rshr32(o, 7);
     p.out[(int64_t)m * p.ldo + (int64_t)h * D + d] = (int8_t)sat8(mulshift(o, p.Mo, p.So));
   }
@@ -210,15 +246,16 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   p.pos = (int)pos;
   p.pb = (int)prob_bits;
   p.lds_T = (int)((tmax + 3) / 4 * 4);
-  const size_t lds = sizeof(int32_t) * ((size_t)p.lds_T + 256 * 16);
+  const size_t lds = sizeof(int32_t) * (size_t)p.lds_T;
   dim3 grid((unsigned)H, (unsigned)M);
+  dim3 block(ATTN_THREADS);
   hipStream_t s = (hipStream_t)stream;
   switch (D) {
-    case 16: hipLaunchKernelGGL(attention_rowhead<16>, grid, dim3(256), lds, s, p); break;
-    case 32: hipLaunchKernelGGL(attention_rowhead<32>, grid, dim3(256), lds, s, p); break;
-    case 64: hipLaunchKernelGGL(attention_rowhead<64>, grid, dim3(256), lds, s, p); break;
-    case 128: hipLaunchKernelGGL(attention_rowhead<128>, grid, dim3(256), lds, s, p); break;
-    default: hipLaunchKernelGGL(attention_rowhead<256>, grid, dim3(256), lds, s, p); break;
+    case 16: hipLaunchKernelGGL(attention_rowhead<16>, grid, block, lds, s, p); break;
+    case 32: hipLaunchKernelGGL(attention_rowhead<32>, grid, block, lds, s, p); break;
+    case 64: hipLaunchKernelGGL(attention_rowhead<64>, grid, block, lds, s, p); break;
+    case 128: hipLaunchKernelGGL(attention_rowhead<128>, grid, block, lds, s, p); break;
+    default: hipLaunchKernelGGL(attention_rowhead<256>, grid, block, lds, s, p); break;
   }
   LLHIP_LAUNCH_CHECK();
   return 0;

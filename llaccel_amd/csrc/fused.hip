@@ -1,0 +1,549 @@
+// Fused decoder-block kernels of libllhip.  Each kernel computes a run of
+// consecutive qgraph ops in one launch and writes every intermediate activation
+// those ops name, so its results are those of the separate ops (golden.py:275-314
+// executes them one by one):
+//
+//  attn_in : rmsnorm -> quant -> linear q, k, v (+bias) [-> rmsnorm heads (Qwen3 Q/K norm)]
+//            -> rope q, k -> quant q, k -> kv_write
+//            One workgroup per head block (H query heads, Hkv key heads, Hkv value heads).
+//            The workgroup normalises and quantises the M input rows into LDS, computes the
+//            block's D output columns with v_mfma_i32_16x16x64_i8 (K split across waves,
+//            partials summed in LDS), then runs the head-local tail: requant, Q/K RMSNorm over
+//            the head, RoPE (needs columns i and i + D/2 of the same head), quant and the
+//            KV-cache write of the key/value rows.
+//  mlp_in  : rmsnorm -> quant -> linear gate (silu) + linear up (mul) -> quant
+//            (or the unfused linear g, linear u, silu, mul forms).  One workgroup per 16
+//            FFN columns computes the gate and the up tile of those columns.
+//  norm_gemv: rmsnorm -> quant -> linear (any epilogue), e.g. the final norm + lm_head.
+//
+// No workgroup depends on another inside a launch (no device-scope synchronisation).
+#include "../../include/llhip.h"
+#include "common.h"
+
+namespace llhip {
+
+constexpr int FUSED_MAX_WAVES = 16;
+
+struct NormQuant {
+  const int16_t* x;
+  const int16_t* gamma;
+  int16_t* h_out;   // normalised rows (i16), written by workgroup 0
+  int8_t* hq_out;   // quantised rows (i8), written by workgroup 0
+  int64_t ldx;      // row stride of x and of the outputs (elements)
+  int64_t Mq;       // quant multiplier
+  uint32_t eps_t, C;
+  int sh_post, Sq, K;
+};
+
+// RMSNorm + quant of M rows (K % 8 == 0) into LDS rows of stride lda bytes (golden.py:124-137,
+// 119-120).  Wave w takes rows w, w + nw, ...
+__device__ void norm_quant_rows(const NormQuant& pr, int M, int8_t* a_lds, int lda, bool write_global) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int nch = pr.K >> 3;
+  const v4i* gv = reinterpret_cast<const v4i*>(pr.gamma);
+  for (int m = wave; m < M; m += nw) {
+    const v4i* xv = reinterpret_cast<const v4i*>(pr.x + (int64_t)m * pr.ldx);
+    uint64_t ss = 0;
+    for (int c0 = lane; c0 < nch; c0 += 128) {
+      const int c1 = c0 + 64;
+      const v4i b0 = xv[c0];
+      const v4i b1 = c1 < nch ? xv[c1] : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int32_t a = lo16(b0[j]), c = hi16(b0[j]);
+        ss += (uint64_t)(uint32_t)(a * a) + (uint64_t)(uint32_t)(c * c);
+        a = lo16(b1[j]);
+        c = hi16(b1[j]);
+        ss += (uint64_t)(uint32_t)(a * a) + (uint64_t)(uint32_t)(c * c);
+      }
+    }
+    ss = wave_sum_u64(ss);
+    const uint32_t inv = rms_inv(ss, pr.eps_t, pr.C);
+    for (int c = lane; c < nch; c += 64) {
+      const v4i b = xv[c], g = gv[c];
+      v4i y;
+      uint32_t qw[2] = {0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int16_t y0 = rms_apply(lo16(b[j]), lo16(g[j]), inv, pr.sh_post);
+        const int16_t y1 = rms_apply(hi16(b[j]), hi16(g[j]), inv, pr.sh_post);
+        y[j] = pack16(y0, y1);
+        const uint32_t q0 = (uint8_t)sat8(mulshift(y0, pr.Mq, pr.Sq));
+        const uint32_t q1 = (uint8_t)sat8(mulshift(y1, pr.Mq, pr.Sq));
+        qw[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
+      }
+      int2 q2;
+      q2.x = (int)qw[0];
+      q2.y = (int)qw[1];
+      *reinterpret_cast<int2*>(a_lds + m * lda + 8 * c) = q2;
+      if (write_global) {
+        if (pr.h_out) *reinterpret_cast<v4i*>(pr.h_out + (int64_t)m * pr.ldx + 8 * c) = y;
+        if (pr.hq_out) *reinterpret_cast<int2*>(pr.hq_out + (int64_t)m * pr.K + 8 * c) = q2;
+      }
+    }
+  }
+}
+
+// partial 16x16 tile over K steps [s_begin, s_end) with A rows from LDS (rows >= M are zeros)
+__device__ __forceinline__ v4i gemv_lds_partial(const int8_t* __restrict__ wrow, bool nvalid, const int8_t* a_lds,
+                                                int lda, int M, int K, int kg, int s_begin, int s_end) {
+  const int lane = threadIdx.x & 63;
+  const int m = lane & 15;
+  const bool avalid = m < M;
+  const int8_t* arow = a_lds + m * lda;
+  v4i acc = {0, 0, 0, 0};
+  int s = s_begin;
+  constexpr int U = 4;
+  for (; s + U <= s_end; s += U) {
+    v4i b[U], a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (s + u) * 64 + kg * 16;
+      const bool ok = k < K;
+      b[u] = (nvalid && ok) ? *reinterpret_cast<const v4i*>(wrow + k) : v4i{0, 0, 0, 0};
+      a[u] = (avalid && ok) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+  }
+  for (; s < s_end; ++s) {
+    const int k = s * 64 + kg * 16;
+    const bool ok = k < K;
+    const v4i b = (nvalid && ok) ? *reinterpret_cast<const v4i*>(wrow + k) : v4i{0, 0, 0, 0};
+    const v4i a = (avalid && ok) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ int64_t requant_raw(int64_t acc, const int32_t* bias, const int32_t* rq, int n) {
+  if (bias) acc += bias[n];
+  return mulshift(acc, rq[2 * n], rq[2 * n + 1]);
+}
+
+__device__ __forceinline__ void v4_add(v4i& a, const v4i& b) {
+  a.x += b.x;
+  a.y += b.y;
+  a.z += b.z;
+  a.w += b.w;
+}
+
+// ---------------------------------------------------------------------------------------
+// attn_in
+// ---------------------------------------------------------------------------------------
+struct AttnInArgs {
+  NormQuant pre;
+  const int8_t* W[3];
+  const int32_t* rq[3];
+  const int32_t* bias[3];
+  void* lin_out[3];  // q i16 [M][H*D], k i16 [M][Hkv*D], v i8 [M][Hkv*D]
+  const int16_t* nrm_gamma[2];
+  int16_t* nrm_out[2];
+  int64_t nrm_eps[2], nrm_C[2], nrm_sh[2];
+  const int16_t* cos_tab;
+  const int16_t* sin_tab;
+  const int32_t* pos_dev;
+  int16_t* rope_out[2];
+  int8_t* quant_out[2];
+  int64_t quant_M[2], quant_S[2];
+  int8_t* kc;
+  int8_t* vc;
+  int64_t max_seq;
+  int M, H, Hkv, D, K, pos, KS, has_norm;
+};
+
+__global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArgs p) {
+  extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
+  __shared__ v4i red[FUSED_MAX_WAVES][64];
+  const int lda = p.K + 16;
+  int8_t* a_lds = dyn;                                                      // [M][lda] i8
+  int32_t* hres = reinterpret_cast<int32_t*>(dyn + ((p.M * lda + 15) & ~15));  // [M][D] i32
+
+  const int b = blockIdx.x;
+  const int role = b < p.H ? 0 : (b < p.H + p.Hkv ? 1 : 2);
+  const int hh = role == 0 ? b : (role == 1 ? b - p.H : b - p.H - p.Hkv);
+  const int D = p.D, M = p.M;
+  const int Nrole = (role == 0 ? p.H : p.Hkv) * D;
+  const int base = hh * D;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tiles = D >> 4;
+
+  norm_quant_rows(p.pre, M, a_lds, lda, b == 0);
+  __syncthreads();
+
+  // D columns = `tiles` 16-column tiles x KS K-splits
+  {
+    const int t = wave % tiles, ks = wave / tiles;
+    const int col = lane & 15, kg = lane >> 4;
+    const int n = base + t * 16 + col;
+    const int steps = (p.K + 63) >> 6;
+    const int spw = (steps + p.KS - 1) / p.KS;
+    const int s0 = min(ks * spw, steps), s1 = min(s0 + spw, steps);
+    const int8_t* wrow = p.W[role] + (int64_t)n * p.K;
+    const v4i acc = gemv_lds_partial(wrow, true, a_lds, lda, M, p.K, kg, s0, s1);
+    red[wave][lane] = acc;
+  }
+  __syncthreads();
+  if (wave < tiles) {
+    v4i acc = red[wave][lane];
+    for (int ks = 1; ks < p.KS; ++ks) v4_add(acc, red[wave + ks * tiles][lane]);
+    const int col = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * kg + r;
+      if (m < M) hres[m * D + wave * 16 + col] = acc[r];
+    }
+  }
+  __syncthreads();
+
+  const int pos0 = p.pos_dev ? *p.pos_dev : p.pos;
+  if (role == 2) {  // v: requant8 -> v activation and V cache
+    for (int i = tid; i < M * D; i += blockDim.x) {
+      const int m = i / D, d = i % D, n = base + d;
+      const int8_t y = (int8_t)sat8(requant_raw(hres[i], p.bias[2], p.rq[2], n));
+      static_cast<int8_t*>(p.lin_out[2])[(int64_t)m * Nrole + n] = y;
+      p.vc[((int64_t)hh * p.max_seq + pos0 + m) * D + d] = y;
+    }
+    return;
+  }
+  // q / k: requant16 -> activation; head values kept in hres as int32
+  for (int i = tid; i < M * D; i += blockDim.x) {
+    const int m = i / D, d = i % D, n = base + d;
+    const int16_t y = (int16_t)sat16(requant_raw(hres[i], p.bias[role], p.rq[role], n));
+    static_cast<int16_t*>(p.lin_out[role])[(int64_t)m * Nrole + n] = y;
+    hres[i] = y;
+  }
+  __syncthreads();
+  if (p.has_norm) {  // RMSNorm over each D-wide head (golden.py:287-293, heads > 1)
+    const int16_t* g = p.nrm_gamma[role];
+    const int nw = blockDim.x >> 6;
+    for (int m = wave; m < M; m += nw) {
+      uint64_t ss = 0;
+      for (int d = lane; d < D; d += 64) ss += (uint64_t)(uint32_t)(hres[m * D + d] * hres[m * D + d]);
+      ss = wave_sum_u64(ss);
+      const uint32_t inv = rms_inv(ss, (uint32_t)p.nrm_eps[role], (uint32_t)p.nrm_C[role]);
+      for (int d = lane; d < D; d += 64) {
+        const int16_t y = rms_apply(hres[m * D + d], g[d], inv, (int)p.nrm_sh[role]);
+        p.nrm_out[role][(int64_t)m * Nrole + base + d] = y;
+        hres[m * D + d] = y;
+      }
+    }
+    __syncthreads();
+  }
+  // RoPE (golden.py:141-158) -> quant (golden.py:119-120) -> K cache for keys
+  const int half = D >> 1;
+  for (int i = tid; i < M * half; i += blockDim.x) {
+    const int m = i / half, j = i % half;
+    const int64_t prow = (int64_t)(pos0 + m) * half;
+    const int64_t c = p.cos_tab[prow + j], s = p.sin_tab[prow + j];
+    const int64_t x1 = hres[m * D + j], x2 = hres[m * D + half + j];
+    const int16_t y1 = (int16_t)sat16(rshr(x1 * c - x2 * s, 14));
+    const int16_t y2 = (int16_t)sat16(rshr(x2 * c + x1 * s, 14));
+    const int64_t o = (int64_t)m * Nrole + base;
+    p.rope_out[role][o + j] = y1;
+    p.rope_out[role][o + half + j] = y2;
+    const int8_t q1 = (int8_t)sat8(mulshift(y1, p.quant_M[role], (int)p.quant_S[role]));
+    const int8_t q2 = (int8_t)sat8(mulshift(y2, p.quant_M[role], (int)p.quant_S[role]));
+    p.quant_out[role][o + j] = q1;
+    p.quant_out[role][o + half + j] = q2;
+    if (role == 1) {
+      int8_t* kr = p.kc + ((int64_t)hh * p.max_seq + pos0 + m) * D;
+      kr[j] = q1;
+      kr[half + j] = q2;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// mlp_in
+// ---------------------------------------------------------------------------------------
+struct MlpInArgs {
+  NormQuant pre;
+  const int8_t* Wg;
+  const int8_t* Wu;
+  const int32_t* rqg;
+  const int32_t* rqu;
+  const int32_t* bg;
+  const int32_t* bu;
+  int16_t* g_out;  // unfused graphs only
+  int16_t* u_out;  // unfused graphs only
+  int16_t* sg_out;
+  int16_t* f_out;
+  int8_t* fq_out;
+  int64_t silu_Mi, fq_M;
+  int silu_Si, silu_sh, mul_sh, fq_S;
+  int M, N, K, KS;
+};
+
+__global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void mlp_in_kernel(MlpInArgs p) {
+  extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
+  __shared__ v4i red[FUSED_MAX_WAVES][64];
+  const int lda = p.K + 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  norm_quant_rows(p.pre, p.M, dyn, lda, blockIdx.x == 0);
+  __syncthreads();
+  const int col = lane & 15, kg = lane >> 4;
+  const int n = blockIdx.x * 16 + col;
+  const bool nvalid = n < p.N;
+  {
+    const int up = wave >= p.KS;  // waves [0, KS): gate, [KS, 2KS): up
+    const int ks = up ? wave - p.KS : wave;
+    const int steps = (p.K + 63) >> 6;
+    const int spw = (steps + p.KS - 1) / p.KS;
+    const int s0 = min(ks * spw, steps), s1 = min(s0 + spw, steps);
+    const int8_t* wrow = (up ? p.Wu : p.Wg) + (int64_t)(nvalid ? n : 0) * p.K;
+    red[wave][lane] = gemv_lds_partial(wrow, nvalid, dyn, lda, p.M, p.K, kg, s0, s1);
+  }
+  __syncthreads();
+  if (wave != 0 || !nvalid) return;
+  v4i ag = red[0][lane], au = red[p.KS][lane];
+  for (int ks = 1; ks < p.KS; ++ks) {
+    v4_add(ag, red[ks][lane]);
+    v4_add(au, red[p.KS + ks][lane]);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * kg + r;
+    if (m >= p.M) continue;
+    const int64_t o = (int64_t)m * p.N + n;
+    const int64_t tg = sat16(requant_raw(ag[r], p.bg, p.rqg, n));
+    const int64_t tu = sat16(requant_raw(au[r], p.bu, p.rqu, n));
+    if (p.g_out) p.g_out[o] = (int16_t)tg;
+    if (p.u_out) p.u_out[o] = (int16_t)tu;
+    const int64_t sg = silu16(tg, p.silu_Mi, p.silu_Si, p.silu_sh);
+    const int64_t f = sat16(rshr(tu * sg, p.mul_sh));
+    p.sg_out[o] = (int16_t)sg;
+    p.f_out[o] = (int16_t)f;
+    p.fq_out[o] = (int8_t)sat8(mulshift(f, p.fq_M, p.fq_S));
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// norm_gemv: rmsnorm -> quant -> one linear with any epilogue (TPW 16-column tiles per
+// workgroup, KS K-splits per tile)
+// ---------------------------------------------------------------------------------------
+struct NormGemvArgs {
+  NormQuant pre;
+  const int8_t* W;
+  const int32_t* rq;
+  const int32_t* bias;
+  const int16_t* aux;
+  void* out;
+  int64_t Mi;
+  int aux_shift, Si, sh, epilogue, out_i8;
+  int M, N, K, KS, TPW;
+};
+
+__global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void norm_gemv_kernel(NormGemvArgs p) {
+  extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
+  __shared__ v4i red[FUSED_MAX_WAVES][64];
+  const int lda = p.K + 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  norm_quant_rows(p.pre, p.M, dyn, lda, blockIdx.x == 0);
+  __syncthreads();
+  const int col = lane & 15, kg = lane >> 4;
+  const int t = wave % p.TPW, ks = wave / p.TPW;
+  const int n = (blockIdx.x * p.TPW + t) * 16 + col;
+  const bool nvalid = n < p.N;
+  const int steps = (p.K + 63) >> 6;
+  const int spw = (steps + p.KS - 1) / p.KS;
+  const int s0 = min(ks * spw, steps), s1 = min(s0 + spw, steps);
+  v4i acc = gemv_lds_partial(p.W + (int64_t)(nvalid ? n : 0) * p.K, nvalid, dyn, lda, p.M, p.K, kg, s0, s1);
+  if (p.KS > 1) {
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (ks != 0) return;
+    for (int j = 1; j < p.KS; ++j) v4_add(acc, red[t + j * p.TPW][lane]);
+  }
+  if (!nvalid) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * kg + r;
+    if (m >= p.M) continue;
+    const int64_t o = (int64_t)m * p.N + n;
+    const int64_t v = requant_raw(acc[r], p.bias, p.rq, n);
+    if (p.out_i8) {
+      static_cast<int8_t*>(p.out)[o] = (int8_t)sat8(v);
+      continue;
+    }
+    int64_t y = sat16(v);
+    if (p.epilogue == 1) y = sat16(y + p.aux[o]);
+    else if (p.epilogue == 2) y = silu16(y, p.Mi, p.Si, p.sh);
+    else if (p.epilogue == 3) y = sat16(rshr(y * p.aux[o], p.aux_shift));
+    static_cast<int16_t*>(p.out)[o] = (int16_t)y;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------------------
+static int fill_pre(NormQuant& pr, const llhip_norm_quant_desc& d) {
+  if (d.K <= 0 || d.K % 8 || d.ldx < d.K || d.ldx % 8) return fail(-EINVAL, "fused rmsnorm: K and ldx must be multiples of 8");
+  if (!u32_ok(d.eps_t) || !u32_ok(d.C) || !shift_ok(d.sh_post) || !u32_ok(d.Mq) || !shift_ok(d.Sq))
+    return fail(-EINVAL, "fused rmsnorm/quant parameter out of range");
+  if (d.K >= (int64_t)((1ull << 48) - (1ull << 32)) >> 30) return fail(-ERANGE, "isqrt48 input out of range");
+  if ((uintptr_t)d.x % 16 || (uintptr_t)d.gamma % 16 || (d.h_out && (uintptr_t)d.h_out % 16) ||
+      (d.hq_out && (uintptr_t)d.hq_out % 8))
+    return fail(-EINVAL, "fused rmsnorm: misaligned operands");
+  pr.x = static_cast<const int16_t*>(d.x);
+  pr.gamma = static_cast<const int16_t*>(d.gamma);
+  pr.h_out = static_cast<int16_t*>(d.h_out);
+  pr.hq_out = static_cast<int8_t*>(d.hq_out);
+  pr.ldx = d.ldx;
+  pr.Mq = d.Mq;
+  pr.eps_t = (uint32_t)d.eps_t;
+  pr.C = (uint32_t)d.C;
+  pr.sh_post = (int)d.sh_post;
+  pr.Sq = (int)d.Sq;
+  pr.K = (int)d.K;
+  return 0;
+}
+
+static int pick_ks(int64_t blocks, int per_split_waves, int steps, int max_waves) {
+  const int target = 8 * current_cu_count();
+  int ks = 1;
+  while (per_split_waves * ks * 2 <= max_waves && blocks * per_split_waves * ks * 2 <= target && ks * 2 <= steps)
+    ks *= 2;
+  return ks;
+}
+
+}  // namespace llhip
+
+using namespace llhip;
+
+extern "C" int llhip_attn_in(const llhip_attn_in_desc* d, void* stream) {
+  if (!d) return fail(-EINVAL, "attn_in: null descriptor");
+  AttnInArgs p{};
+  int rc = fill_pre(p.pre, d->pre);
+  if (rc) return rc;
+  const int64_t M = d->M, H = d->H, Hkv = d->Hkv, D = d->D, K = d->pre.K;
+  if (M < 1 || M > 16 || H < 1 || Hkv < 1 || H % Hkv || D < 16 || D > 256 || D % 16)
+    return fail(-EINVAL, "attn_in: bad geometry (M <= 16, D multiple of 16 up to 256)");
+  if (!d->pos_dev && (d->pos < 0 || d->pos + M > d->max_seq))
+    return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)d->pos, (long long)(d->pos + M - 1),
+                (long long)d->max_seq);
+  for (int i = 0; i < 2; ++i)
+    if (!u32_ok(d->quant_M[i]) || !shift_ok(d->quant_S[i]) ||
+        (d->has_norm && (!u32_ok(d->nrm_eps[i]) || !u32_ok(d->nrm_C[i]) || !shift_ok(d->nrm_sh[i]))))
+      return fail(-EINVAL, "attn_in: parameter out of range");
+  for (int i = 0; i < 3; ++i) {
+    p.W[i] = static_cast<const int8_t*>(d->W[i]);
+    p.rq[i] = static_cast<const int32_t*>(d->rq[i]);
+    p.bias[i] = static_cast<const int32_t*>(d->bias[i]);
+    p.lin_out[i] = d->lin_out[i];
+    if ((uintptr_t)p.W[i] % 16) return fail(-EINVAL, "attn_in: misaligned weights");
+  }
+  for (int i = 0; i < 2; ++i) {
+    p.nrm_gamma[i] = static_cast<const int16_t*>(d->nrm_gamma[i]);
+    p.nrm_out[i] = static_cast<int16_t*>(d->nrm_out[i]);
+    p.nrm_eps[i] = d->nrm_eps[i];
+    p.nrm_C[i] = d->nrm_C[i];
+    p.nrm_sh[i] = d->nrm_sh[i];
+    p.rope_out[i] = static_cast<int16_t*>(d->rope_out[i]);
+    p.quant_out[i] = static_cast<int8_t*>(d->quant_out[i]);
+    p.quant_M[i] = d->quant_M[i];
+    p.quant_S[i] = d->quant_S[i];
+  }
+  p.cos_tab = static_cast<const int16_t*>(d->cos_tab);
+  p.sin_tab = static_cast<const int16_t*>(d->sin_tab);
+  p.pos_dev = static_cast<const int32_t*>(d->pos_dev);
+  p.kc = static_cast<int8_t*>(d->kc);
+  p.vc = static_cast<int8_t*>(d->vc);
+  p.max_seq = d->max_seq;
+  p.M = (int)M;
+  p.H = (int)H;
+  p.Hkv = (int)Hkv;
+  p.D = (int)D;
+  p.K = (int)K;
+  p.pos = (int)d->pos;
+  p.has_norm = d->has_norm ? 1 : 0;
+  const int tiles = (int)(D / 16);
+  const int steps = (int)ceil_div(K, 64);
+  p.KS = pick_ks(H + 2 * Hkv, tiles, steps, FUSED_MAX_WAVES);
+  const size_t lds = (size_t)((M * (K + 16) + 15) & ~15) + sizeof(int32_t) * (size_t)(M * D);
+  if (lds > 48 * 1024) return fail(-EINVAL, "attn_in: M*K too large for the LDS staging");
+  hipLaunchKernelGGL(attn_in_kernel, dim3((unsigned)(H + 2 * Hkv)), dim3(64 * tiles * p.KS), lds, (hipStream_t)stream,
+                     p);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int llhip_mlp_in(const llhip_mlp_in_desc* d, void* stream) {
+  if (!d) return fail(-EINVAL, "mlp_in: null descriptor");
+  MlpInArgs p{};
+  int rc = fill_pre(p.pre, d->pre);
+  if (rc) return rc;
+  const int64_t M = d->M, N = d->N, K = d->pre.K;
+  if (M < 1 || M > 16 || N < 1) return fail(-EINVAL, "mlp_in: bad geometry (M <= 16)");
+  if (!u32_ok(d->silu_Mi) || !shift_ok(d->silu_Si) || !shift_ok(d->silu_sh) || !shift_ok(d->mul_sh) ||
+      !u32_ok(d->fq_M) || !shift_ok(d->fq_S))
+    return fail(-EINVAL, "mlp_in: parameter out of range");
+  if ((uintptr_t)d->Wg % 16 || (uintptr_t)d->Wu % 16) return fail(-EINVAL, "mlp_in: misaligned weights");
+  p.Wg = static_cast<const int8_t*>(d->Wg);
+  p.Wu = static_cast<const int8_t*>(d->Wu);
+  p.rqg = static_cast<const int32_t*>(d->rqg);
+  p.rqu = static_cast<const int32_t*>(d->rqu);
+  p.bg = static_cast<const int32_t*>(d->bg);
+  p.bu = static_cast<const int32_t*>(d->bu);
+  p.g_out = static_cast<int16_t*>(d->g_out);
+  p.u_out = static_cast<int16_t*>(d->u_out);
+  p.sg_out = static_cast<int16_t*>(d->sg_out);
+  p.f_out = static_cast<int16_t*>(d->f_out);
+  p.fq_out = static_cast<int8_t*>(d->fq_out);
+  p.silu_Mi = d->silu_Mi;
+  p.silu_Si = (int)d->silu_Si;
+  p.silu_sh = (int)d->silu_sh;
+  p.mul_sh = (int)d->mul_sh;
+  p.fq_M = d->fq_M;
+  p.fq_S = (int)d->fq_S;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  const int tiles = (int)ceil_div(N, 16);
+  p.KS = pick_ks(tiles, 2, (int)ceil_div(K, 64), FUSED_MAX_WAVES);
+  const size_t lds = (size_t)(M * (K + 16));
+  if (lds > 48 * 1024) return fail(-EINVAL, "mlp_in: M*K too large for the LDS staging");
+  hipLaunchKernelGGL(mlp_in_kernel, dim3((unsigned)tiles), dim3(64 * 2 * p.KS), lds, (hipStream_t)stream, p);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream) {
+  if (!d) return fail(-EINVAL, "norm_linear: null descriptor");
+  NormGemvArgs p{};
+  int rc = fill_pre(p.pre, d->pre);
+  if (rc) return rc;
+  const int64_t M = d->M, N = d->N, K = d->pre.K;
+  if (M < 1 || M > 16 || N < 1) return fail(-EINVAL, "norm_linear: bad geometry (M <= 16)");
+  if (d->epilogue < 0 || d->epilogue > 3 || (d->out_i8 && d->epilogue != 0))
+    return fail(-EINVAL, "norm_linear: bad epilogue");
+  if ((d->epilogue == 1 || d->epilogue == 3) && !d->aux) return fail(-EINVAL, "norm_linear: epilogue needs aux");
+  if (!shift_ok(d->aux_shift) || !shift_ok(d->silu_Si) || !shift_ok(d->silu_sh))
+    return fail(-EINVAL, "norm_linear: shift out of [0,63]");
+  if ((uintptr_t)d->W % 16) return fail(-EINVAL, "norm_linear: misaligned weights");
+  p.W = static_cast<const int8_t*>(d->W);
+  p.rq = static_cast<const int32_t*>(d->rq);
+  p.bias = static_cast<const int32_t*>(d->bias);
+  p.aux = static_cast<const int16_t*>(d->aux);
+  p.out = d->out;
+  p.Mi = d->silu_Mi;
+  p.aux_shift = (int)d->aux_shift;
+  p.Si = (int)d->silu_Si;
+  p.sh = (int)d->silu_sh;
+  p.epilogue = (int)d->epilogue;
+  p.out_i8 = d->out_i8 ? 1 : 0;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  const int tiles = (int)ceil_div(N, 16);
+  const int steps = (int)ceil_div(K, 64);
+  // wide outputs: several tiles per workgroup share one prologue; narrow ones split K
+  p.TPW = tiles >= 4096 ? 4 : 1;
+  p.KS = p.TPW == 1 ? pick_ks(tiles, 1, steps, FUSED_MAX_WAVES) : 1;
+  const int blocks = (int)ceil_div(tiles, p.TPW);
+  const size_t lds = (size_t)(M * (K + 16));
+  if (lds > 48 * 1024) return fail(-EINVAL, "norm_linear: M*K too large for the LDS staging");
+  hipLaunchKernelGGL(norm_gemv_kernel, dim3((unsigned)blocks), dim3(64 * p.TPW * p.KS), lds, (hipStream_t)stream, p);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}

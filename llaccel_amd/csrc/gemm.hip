@@ -3,14 +3,12 @@
 // (NUMERICS.md "GEMM").
 //
 // Two kernels:
-//  * linear_skinny: M <= 16 rows per z-block.  One wave computes a 16(M) x 16(N)
-//    tile with v_mfma_i32_16x16x64_i8; the A rows beyond M are zeros supplied in
-//    registers.  W [N][K] row-major is streamed once with 16-byte loads.  The K
-//    range is split over gridDim.y so that small-N projections still put enough
-//    waves on the chip; split partials are summed with int32 atomics into the
-//    workspace and the last-arriving wave of a tile (arrival counter) applies the
-//    epilogue and leaves the workspace zeroed.  Integer addition is associative,
-//    so the split never changes a result.
+//  * linear_gemv: M <= 16 rows per z-block (decode GEMV, prefill chunks).  One workgroup
+//    per 16-column tile; its waves split the K range and each computes a 16(M) x 16(N)
+//    partial tile with v_mfma_i32_16x16x64_i8 (A rows beyond M are zeros supplied in
+//    registers); the partials are summed in LDS.  W [N][K] row-major is streamed once
+//    with 16-byte loads, four K steps in flight per wave.  Integer addition is
+//    associative, so the split never changes a result.
 //  * linear_tiled: M > 16.  128x128x64 block tiles, four waves in 2x2, each wave
 //    64x64 with v_mfma_i32_32x32x32_i8; A and W tiles double-buffered in LDS.
 //    Blocks are numbered XCD-major so the blocks that share a W panel run on one
@@ -20,12 +18,10 @@
 
 namespace llhip {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 enum Epi : int { EPI_NONE = 0, EPI_RESADD = 1, EPI_SILU = 2, EPI_MUL = 3 };
 
-constexpr int64_t GEMM_SPLIT_MAX_N = 65536;
 
 struct LinearArgs {
   const int8_t* A;
@@ -34,15 +30,11 @@ struct LinearArgs {
   const int32_t* bias;
   const int16_t* aux;
   void* out;
-  int32_t* ws;
-  uint32_t* cnt;
   int64_t lda, ldaux, ldo;
   int64_t Mi;
   int M, K, N;
   int aux_shift, Si, sh;
-  int steps;            // ceil(K / 64)
-  int steps_per_split;  // linear_skinny
-  int splits;
+  int steps;  // ceil(K / 64)
 };
 
 // requant + epilogue of one output element (golden.py:323-342)
@@ -88,24 +80,17 @@ __device__ __forceinline__ v4i load16(const int8_t* row, int k, int K, bool vali
 }
 
 // ---------------------------------------------------------------------------------------
-// M <= 16 (per z-block): one wave per 16-column tile and K split
+// M <= 16 (per z-block): one workgroup per 16-column tile, K split across its waves
 // ---------------------------------------------------------------------------------------
-template <int EPI, bool OUT8, bool ALIGNED>
-__global__ __launch_bounds__(64) void linear_skinny(LinearArgs p) {
-  const int lane = threadIdx.x;
-  const int col = lane & 15;
-  const int kg = lane >> 4;
-  const int tile = blockIdx.x;
-  const int split = blockIdx.y;
-  const int m0 = blockIdx.z * 16;
-  const int n = tile * 16 + col;
-  const bool nvalid = n < p.N;
-  const bool avalid = m0 + col < p.M;
-  const int8_t* wrow = p.W + (int64_t)(nvalid ? n : 0) * p.K;
-  const int8_t* arow = p.A + (int64_t)(avalid ? m0 + col : 0) * p.lda;
+// Wave w of the workgroup accumulates the K steps [w*spw, (w+1)*spw) of the tile with
+// v_mfma_i32_16x16x64_i8; the per-wave 16x16 partial tiles are summed through LDS by wave 0,
+// which applies the epilogue.  No workgroup depends on another, so the kernel needs no
+// device-scope synchronisation (on the multi-XCD part those fences flush the XCD's L2).
+constexpr int GEMV_MAX_WAVES = 16;
 
-  const int s_begin = split * p.steps_per_split;
-  const int s_end = min(s_begin + p.steps_per_split, p.steps);
+template <bool ALIGNED>
+__device__ __forceinline__ v4i gemv_tile_partial(const LinearArgs& p, const int8_t* wrow, bool nvalid,
+                                                 const int8_t* arow, bool avalid, int kg, int s_begin, int s_end) {
   v4i acc = {0, 0, 0, 0};
   int s = s_begin;
   constexpr int U = 4;
@@ -122,49 +107,53 @@ __global__ __launch_bounds__(64) void linear_skinny(LinearArgs p) {
   }
   for (; s < s_end; ++s) {
     const int k = s * 64 + kg * 16;
-    v4i b = load16<ALIGNED>(wrow, k, p.K, nvalid);
-    v4i a = load16<ALIGNED>(arow, k, p.K, avalid);
+    const v4i b = load16<ALIGNED>(wrow, k, p.K, nvalid);
+    const v4i a = load16<ALIGNED>(arow, k, p.K, avalid);
     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
   }
+  return acc;
+}
 
+template <int EPI, bool OUT8, bool ALIGNED>
+__global__ __launch_bounds__(64 * GEMV_MAX_WAVES) void linear_gemv(LinearArgs p) {
+  __shared__ v4i red[GEMV_MAX_WAVES - 1][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const int col = lane & 15;
+  const int kg = lane >> 4;
+  const int tile = blockIdx.x;
+  const int m0 = blockIdx.z * 16;
+  const int n = tile * 16 + col;
+  const bool nvalid = n < p.N;
+  const bool avalid = m0 + col < p.M;
+  const int8_t* wrow = p.W + (int64_t)(nvalid ? n : 0) * p.K;
+  const int8_t* arow = p.A + (int64_t)(avalid ? m0 + col : 0) * p.lda;
+
+  const int spw = (p.steps + nw - 1) / nw;
+  const int s_begin = min(wave * spw, p.steps);
+  const int s_end = min(s_begin + spw, p.steps);
+  v4i acc = gemv_tile_partial<ALIGNED>(p, wrow, nvalid, arow, avalid, kg, s_begin, s_end);
+  if (nw > 1) {
+    if (wave > 0) red[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave > 0) return;
+    for (int w = 0; w < nw - 1; ++w) {
+      const v4i o = red[w][lane];
+      acc.x += o.x;
+      acc.y += o.y;
+      acc.z += o.z;
+      acc.w += o.w;
+    }
+  }
   // acc[r] = C[4*kg + r][col] of this 16x16 tile
-  if (p.splits == 1) {
-    if (nvalid) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 4 * kg + r;
-        if (m < p.M) finish<EPI, OUT8>(p, m, n, acc[r]);
-      }
-    }
-    return;
-  }
-  // split-K: partial sums into the workspace, last arrival finishes the tile
-  int32_t* part = p.ws + (int64_t)blockIdx.z * 16 * p.N;
   if (nvalid) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = m0 + 4 * kg + r;
-      if (m < p.M) atomicAdd(&part[(int64_t)(4 * kg + r) * p.N + n], acc[r]);
+      if (m < p.M) finish<EPI, OUT8>(p, m, n, acc[r]);
     }
   }
-  __threadfence();
-  uint32_t* counter = p.cnt + (int64_t)blockIdx.z * gridDim.x + tile;
-  uint32_t prev = 0;
-  if (lane == 0) prev = atomicAdd(counter, 1u);
-  prev = __shfl(prev, 0);
-  if (prev != (uint32_t)(p.splits - 1)) return;
-  __threadfence();
-  if (nvalid) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m0 + 4 * kg + r;
-      if (m < p.M) {
-        const int32_t v = atomicExch(&part[(int64_t)(4 * kg + r) * p.N + n], 0);
-        finish<EPI, OUT8>(p, m, n, v);
-      }
-    }
-  }
-  if (lane == 0) atomicExch(counter, 0u);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -274,21 +263,15 @@ static int launch_linear(LinearArgs& p, hipStream_t stream) {
   }
   const int tiles = (int)ceil_div(p.N, 16);
   const int zblocks = (int)ceil_div(p.M, 16);
-  int splits = 1;
+  // waves per workgroup: enough waves on the chip to keep HBM busy, never more than K steps
   const int target_waves = 8 * current_cu_count();
-  if (p.ws && p.N <= GEMM_SPLIT_MAX_N && zblocks == 1 && tiles < target_waves) {
-    splits = (int)ceil_div(target_waves, tiles);
-    const int max_splits = (int)ceil_div(p.steps, 2);  // keep >= 2 MFMA steps per wave
-    if (splits > max_splits) splits = max_splits;
-    if (splits < 1) splits = 1;
-  }
-  p.steps_per_split = (int)ceil_div(p.steps, splits);
-  p.splits = (int)ceil_div(p.steps, p.steps_per_split);
-  dim3 grid(tiles, p.splits, zblocks);
+  int nw = 1;
+  while (nw < GEMV_MAX_WAVES && (int64_t)tiles * zblocks * nw * 2 <= target_waves && nw * 2 <= p.steps) nw *= 2;
+  dim3 grid(tiles, 1, zblocks);
   if (aligned)
-    hipLaunchKernelGGL((linear_skinny<EPI, OUT8, true>), grid, dim3(64), 0, stream, p);
+    hipLaunchKernelGGL((linear_gemv<EPI, OUT8, true>), grid, dim3(64 * nw), 0, stream, p);
   else
-    hipLaunchKernelGGL((linear_skinny<EPI, OUT8, false>), grid, dim3(64), 0, stream, p);
+    hipLaunchKernelGGL((linear_gemv<EPI, OUT8, false>), grid, dim3(64 * nw), 0, stream, p);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
@@ -331,8 +314,7 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
   p.bias = bias;
   p.aux = aux;
   p.out = out;
-  p.ws = ws ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_GEMM_PARTIALS) : nullptr;
-  p.cnt = ws ? reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + WS_GEMM_COUNTERS) : nullptr;
+  (void)ws;  // the GEMM kernels need no workspace
   p.lda = lda;
   p.ldaux = ldaux;
   p.ldo = ldo;

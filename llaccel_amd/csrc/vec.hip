@@ -7,71 +7,134 @@
 
 namespace llhip {
 
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    uint32_t lo = __shfl_xor((uint32_t)v, off);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off);
-    v += ((uint64_t)hi << 32) | lo;
-  }
-  return v;
-}
-
 // ---------------------------------------------------------------------------------------
-// RMSNorm (golden.py:124-137): one wave per row
+// RMSNorm (golden.py:124-137): one wave per row.  Rows whose K and stride are multiples of 8
+// move 16 bytes (8 values) per lane per load, four loads in flight.
 // ---------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const int16_t* __restrict__ x, int64_t rows, int K, int64_t ldx,
                                                       const int16_t* __restrict__ g, uint32_t eps_t, uint32_t C, int sh,
-                                                      int16_t* __restrict__ y, int64_t ldy) {
+                                                      int16_t* __restrict__ y, int64_t ldy, int vec) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int16_t* xr = x + row * ldx;
+  int16_t* yr = y + row * ldy;
   uint64_t ss = 0;
+  if (vec) {
+    const int nch = K >> 3;
+    const v4i* xv = reinterpret_cast<const v4i*>(xr);
+    for (int c0 = lane; c0 < nch; c0 += 256) {
+      v4i b[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) b[u] = c0 + 64 * u < nch ? xv[c0 + 64 * u] : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int32_t a = lo16(b[u][j]), c = hi16(b[u][j]);
+          ss += (uint64_t)(uint32_t)(a * a) + (uint64_t)(uint32_t)(c * c);
+        }
+    }
+    ss = wave_sum_u64(ss);
+    const uint32_t inv = rms_inv(ss, eps_t, C);
+    const v4i* gv = reinterpret_cast<const v4i*>(g);
+    v4i* yv = reinterpret_cast<v4i*>(yr);
+    for (int c0 = lane; c0 < nch; c0 += 256) {
+      v4i b[4], gg[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool ok = c0 + 64 * u < nch;
+        b[u] = ok ? xv[c0 + 64 * u] : v4i{0, 0, 0, 0};
+        gg[u] = ok ? gv[c0 + 64 * u] : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (c0 + 64 * u >= nch) break;
+        v4i o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = pack16(rms_apply(lo16(b[u][j]), lo16(gg[u][j]), inv, sh), rms_apply(hi16(b[u][j]), hi16(gg[u][j]), inv, sh));
+        yv[c0 + 64 * u] = o;
+      }
+    }
+    return;
+  }
   for (int k = lane; k < K; k += 64) {
     const int32_t v = xr[k];
-    ss += (uint64_t)(int64_t)(v * v);  // |v| <= 2^15: v*v <= 2^30 fits int32
+    ss += (uint64_t)(uint32_t)(v * v);
   }
   ss = wave_sum_u64(ss);
-  const uint64_t tt = ss + eps_t;  // < 2^48: the host bounds K so that K * 2^30 + 2^32 < 2^48
-  const uint32_t r = isqrt48(tt);
-  const uint32_t d = r > 1 ? r : 1u;
-  uint32_t inv = C / d;  // C < 2^32, so the quotient already fits u32
-  if (inv > 65535u) inv = 65535u;
-  int16_t* yr = y + row * ldy;
-  for (int k = lane; k < K; k += 64) {
-    const int64_t xg = (int64_t)((int32_t)xr[k] * (int32_t)g[k]);
-    yr[k] = (int16_t)sat16(rshr(xg * (int64_t)inv, sh));
+  const uint32_t inv = rms_inv(ss, eps_t, C);
+  for (int k = lane; k < K; k += 64) yr[k] = rms_apply(xr[k], g[k], inv, sh);
+}
+
+// ---------------------------------------------------------------------------------------
+// elementwise: 8 consecutive values per thread, 16-byte accesses when aligned
+// ---------------------------------------------------------------------------------------
+struct EwArgs {
+  const int16_t* a;
+  const int16_t* b;
+  void* y;
+  int64_t n;
+  int64_t M;  // multiplier (quant M / silu Mi)
+  int s0, s1; // shifts
+  int aligned;
+};
+
+template <int OP>  // 0 quant, 1 silu, 2 vmul, 3 vadd
+__device__ __forceinline__ int64_t ew_one(const EwArgs& p, int64_t a, int64_t b) {
+  if (OP == 0) return sat8(mulshift(a, p.M, p.s0));
+  if (OP == 1) return silu16(a, p.M, p.s0, p.s1);
+  if (OP == 2) return sat16(rshr(a * b, p.s0));
+  return sat16(a + rshr(b, p.s0));
+}
+
+template <int OP>
+__global__ __launch_bounds__(256) void ew_kernel(EwArgs p) {
+  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i0 >= p.n) return;
+  if (p.aligned && i0 + 8 <= p.n) {
+    const v4i av = *reinterpret_cast<const v4i*>(p.a + i0);
+    v4i bv = {0, 0, 0, 0};
+    if (OP >= 2) bv = *reinterpret_cast<const v4i*>(p.b + i0);
+    int64_t r[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      r[2 * j] = ew_one<OP>(p, lo16(av[j]), lo16(bv[j]));
+      r[2 * j + 1] = ew_one<OP>(p, hi16(av[j]), hi16(bv[j]));
+    }
+    if (OP == 0) {
+      int2 o;
+      o.x = (int)((uint32_t)(uint8_t)r[0] | (uint32_t)(uint8_t)r[1] << 8 | (uint32_t)(uint8_t)r[2] << 16 |
+                  (uint32_t)(uint8_t)r[3] << 24);
+      o.y = (int)((uint32_t)(uint8_t)r[4] | (uint32_t)(uint8_t)r[5] << 8 | (uint32_t)(uint8_t)r[6] << 16 |
+                  (uint32_t)(uint8_t)r[7] << 24);
+      *reinterpret_cast<int2*>(static_cast<int8_t*>(p.y) + i0) = o;
+    } else {
+      v4i o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = pack16(r[2 * j], r[2 * j + 1]);
+      *reinterpret_cast<v4i*>(static_cast<int16_t*>(p.y) + i0) = o;
+    }
+    return;
+  }
+  for (int64_t i = i0; i < p.n && i < i0 + 8; ++i) {
+    const int64_t r = ew_one<OP>(p, p.a[i], OP >= 2 ? p.b[i] : 0);
+    if (OP == 0)
+      static_cast<int8_t*>(p.y)[i] = (int8_t)r;
+    else
+      static_cast<int16_t*>(p.y)[i] = (int16_t)r;
   }
 }
 
-// ---------------------------------------------------------------------------------------
-// elementwise
-// ---------------------------------------------------------------------------------------
-__global__ void quant_kernel(const int16_t* __restrict__ x, int64_t n, int64_t M, int S, int8_t* __restrict__ y) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    y[i] = (int8_t)sat8(mulshift(x[i], M, S));
-}
-
-__global__ void silu_kernel(const int16_t* __restrict__ x, int64_t n, int64_t Mi, int Si, int sh, int16_t* __restrict__ y) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    y[i] = (int16_t)silu16(x[i], Mi, Si, sh);
-}
-
-__global__ void vmul_kernel(const int16_t* __restrict__ a, const int16_t* __restrict__ b, int64_t n, int sh,
-                            int16_t* __restrict__ y) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    y[i] = (int16_t)sat16(rshr((int64_t)((int32_t)a[i] * (int32_t)b[i]), sh));
-}
-
-__global__ void vadd_kernel(const int16_t* __restrict__ a, const int16_t* __restrict__ b, int64_t n, int sh,
-                            int16_t* __restrict__ y) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    y[i] = (int16_t)sat16((int64_t)a[i] + rshr(b[i], sh));
+template <int OP>
+static int launch_ew(EwArgs p, hipStream_t stream) {
+  if (p.n <= 0) return p.n < 0 ? fail(-EINVAL, "negative element count") : 0;
+  p.aligned = ((uintptr_t)p.a % 16 == 0) && (!p.b || (uintptr_t)p.b % 16 == 0) && ((uintptr_t)p.y % 16 == 0);
+  const int64_t threads = ceil_div(p.n, 8);
+  hipLaunchKernelGGL(ew_kernel<OP>, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, stream, p);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
 }
 
 static unsigned ew_blocks(int64_t n) {
@@ -204,42 +267,32 @@ int llhip_rmsnorm(const int16_t* x, int64_t rows, int64_t K, int64_t ldx, const 
   // isqrt48 domain: sum of K squares of i16 (each <= 2^30) plus eps_t must stay below 2^48
   if (K >= (int64_t)((1ull << 48) - (1ull << 32)) >> 30) return fail(-ERANGE, "isqrt48 input out of range: K=%lld", (long long)K);
   if (ldx < K || ldy < K) return fail(-EINVAL, "rmsnorm: leading dimension too small");
+  const int vec = (K % 8 == 0) && (ldx % 8 == 0) && (ldy % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
+                  ((uintptr_t)y % 16 == 0) && ((uintptr_t)g % 16 == 0);
   hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, (hipStream_t)stream, x, rows,
-                     (int)K, ldx, g, (uint32_t)eps_t, (uint32_t)C, (int)sh_post, y, ldy);
+                     (int)K, ldx, g, (uint32_t)eps_t, (uint32_t)C, (int)sh_post, y, ldy, vec);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
 
 int llhip_quant(const int16_t* x, int64_t n, int64_t M, int64_t S, int8_t* y, void* stream) {
   if (!u32_ok(M) || !shift_ok(S)) return fail(-EINVAL, "quant: M must be u32, S in [0,63]");
-  if (n <= 0) return n < 0 ? fail(-EINVAL, "quant: negative count") : 0;
-  hipLaunchKernelGGL(quant_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t)stream, x, n, M, (int)S, y);
-  LLHIP_LAUNCH_CHECK();
-  return 0;
+  return launch_ew<0>(EwArgs{x, nullptr, y, n, M, (int)S, 0, 0}, (hipStream_t)stream);
 }
 
 int llhip_silu(const int16_t* x, int64_t n, int64_t Mi, int64_t Si, int64_t sh_out, int16_t* y, void* stream) {
   if (!u32_ok(Mi) || !shift_ok(Si) || !shift_ok(sh_out)) return fail(-EINVAL, "silu: Mi must be u32, shifts in [0,63]");
-  if (n <= 0) return n < 0 ? fail(-EINVAL, "silu: negative count") : 0;
-  hipLaunchKernelGGL(silu_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t)stream, x, n, Mi, (int)Si, (int)sh_out, y);
-  LLHIP_LAUNCH_CHECK();
-  return 0;
+  return launch_ew<1>(EwArgs{x, nullptr, y, n, Mi, (int)Si, (int)sh_out, 0}, (hipStream_t)stream);
 }
 
 int llhip_vmul(const int16_t* a, const int16_t* b, int64_t n, int64_t sh, int16_t* y, void* stream) {
   if (!shift_ok(sh)) return fail(-EINVAL, "mul: sh out of [0,63]");
-  if (n <= 0) return n < 0 ? fail(-EINVAL, "mul: negative count") : 0;
-  hipLaunchKernelGGL(vmul_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t)stream, a, b, n, (int)sh, y);
-  LLHIP_LAUNCH_CHECK();
-  return 0;
+  return launch_ew<2>(EwArgs{a, b, y, n, 0, (int)sh, 0, 0}, (hipStream_t)stream);
 }
 
 int llhip_vadd(const int16_t* a, const int16_t* b, int64_t n, int64_t sh_b, int16_t* y, void* stream) {
   if (!shift_ok(sh_b)) return fail(-EINVAL, "add: sh_b out of [0,63]");
-  if (n <= 0) return n < 0 ? fail(-EINVAL, "add: negative count") : 0;
-  hipLaunchKernelGGL(vadd_kernel, dim3(ew_blocks(n)), dim3(256), 0, (hipStream_t)stream, a, b, n, (int)sh_b, y);
-  LLHIP_LAUNCH_CHECK();
-  return 0;
+  return launch_ew<3>(EwArgs{a, b, y, n, 0, (int)sh_b, 0, 0}, (hipStream_t)stream);
 }
 
 int llhip_rope(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, const int16_t* cos_tab,

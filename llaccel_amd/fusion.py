@@ -1,0 +1,305 @@
+"""Op-list fusion for GoldenModel: replaces runs of consecutive qgraph ops with one fused
+launch (include/llhip.h: llhip_attn_in, llhip_mlp_in, llhip_norm_linear).
+
+A fused step writes every activation its ops name, with the values the separate ops give
+(the kernels compute the same integer formulas), so `acts`, later consumers and the launch
+record are unaffected.  It keeps the per-op steps it replaces and runs those instead when
+its shape limits do not hold (more than 16 rows per launch, an LDS staging overflow), so
+every graph runs; graphs that do not match a pattern simply keep their per-op steps.
+
+Recognised runs (the op order the reference's quantizer and compiler emit, refquant.py:426-467):
+  attn_in : rmsnorm, quant, linear q, linear k, linear v, [rmsnorm heads q, rmsnorm heads k],
+            rope q, rope k, quant q, quant k, kv_write
+  mlp_in  : rmsnorm, quant, linear(silu), linear(mul aux=silu out), quant          (fused graph)
+            rmsnorm, quant, linear g, linear u, silu(g), mul(sg, u), quant         (unfused graph)
+  norm_linear: rmsnorm, quant, linear (any epilogue)                               (e.g. lm_head)
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import _lib
+
+LDS_LIMIT = 48 * 1024
+
+
+def _vp(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+class FusedStep:
+    """`kind` names the fused kernel; `fallback` are the per-op steps it replaces."""
+
+    def __init__(self, model, kind, fallback, fill, entry, desc_cls, K, bytes_fn, name, ops):
+        self.model, self.kind, self.fallback, self.fill = model, kind, fallback, fill
+        self.entry, self.desc = entry, desc_cls()
+        self.K, self.bytes_fn, self.name, self.ops = K, bytes_fn, name, ops
+
+    def __call__(self, M, pos, pd=None):
+        if M > 16 or M * (self.K + 16) > LDS_LIMIT:
+            for st in self.fallback:
+                st(M, pos, pd)
+            return
+        self.fill(self.desc, M, pos, pd)
+        m = self.model
+        _lib.call(self.entry, ctypes.byref(self.desc), m._stream_handle())
+
+
+def _pre(model, d, op_norm, op_quant):
+    """Fill a NormQuantDesc for rmsnorm(op_norm) -> quant(op_quant)."""
+    x = model._buf(op_norm["in"])
+    d.x = _vp(x)
+    d.gamma = _vp(model._dt[op_norm["gamma"]])
+    d.h_out = _vp(model._buf(op_norm["out"]))
+    d.hq_out = _vp(model._buf(op_quant["out"]))
+    d.ldx = x.shape[1]
+    d.K = int(model._dt[op_norm["gamma"]].shape[0])
+    d.eps_t, d.C, d.sh_post = int(op_norm["eps_t"]), int(op_norm["C"]), int(op_norm["sh_post"])
+    d.Mq, d.Sq = int(op_quant["M"]), int(op_quant["S"])
+
+
+def _is(op, kind, **kw):
+    if op.get("op") != kind:
+        return False
+    return all(op.get(k, None) == v for k, v in kw.items())
+
+
+def _plain_linear(op):
+    return op.get("op") == "linear" and (op.get("epilogue", "none") or "none") == "none"
+
+
+def _norm_quant_head(ops, i, spec):
+    """ops[i], ops[i+1] = rmsnorm (one head) -> quant of its output, with K % 8 == 0."""
+    if i + 1 >= len(ops):
+        return None
+    a, b = ops[i], ops[i + 1]
+    if not _is(a, "rmsnorm") or int(a.get("heads", 1)) != 1 or not _is(b, "quant") or b["in"] != a["out"]:
+        return None
+    if a["in"] not in spec or spec[a["in"]][0] != "i16" or spec[a["in"]][1] % 8:
+        return None
+    return a, b
+
+
+def match_attn_in(model, ops, i, steps):
+    spec = model._act_spec
+    head = _norm_quant_head(ops, i, spec)
+    if head is None:
+        return None
+    rn, qu = head
+    j = i + 2
+    lin = ops[j:j + 3]
+    if len(lin) < 3 or not all(_plain_linear(o) and o["in"] == qu["out"] for o in lin):
+        return None
+    q_op, k_op, v_op = lin
+    if q_op.get("out_dtype", "i16") != "i16" or k_op.get("out_dtype", "i16") != "i16" or v_op.get("out_dtype") != "i8":
+        return None
+    j += 3
+    has_norm = False
+    nq = nk = None
+    if j + 1 < len(ops) and _is(ops[j], "rmsnorm") and _is(ops[j + 1], "rmsnorm"):
+        nq, nk = ops[j], ops[j + 1]
+        if nq["in"] != q_op["out"] or nk["in"] != k_op["out"]:
+            return None
+        has_norm = True
+        j += 2
+    qs = nq["out"] if has_norm else q_op["out"]
+    ks = nk["out"] if has_norm else k_op["out"]
+    if j + 4 >= len(ops):
+        return None
+    rq_, rk_, qq_, kq_, kvw = ops[j:j + 5]
+    if not (_is(rq_, "rope") and _is(rk_, "rope") and _is(qq_, "quant") and _is(kq_, "quant") and _is(kvw, "kv_write")):
+        return None
+    if rq_["in"] != qs or rk_["in"] != ks or qq_["in"] != rq_["out"] or kq_["in"] != rk_["out"]:
+        return None
+    if kvw["k"] != kq_["out"] or kvw["v"] != v_op["out"]:
+        return None
+    H, D = int(rq_["H"]), int(rq_["D"])
+    Hkv = int(rk_["H"])
+    if int(rk_["D"]) != D or int(kvw["Hkv"]) != Hkv or int(kvw["D"]) != D or Hkv < 1 or H % Hkv:
+        return None
+    K = int(model._dt[rn["gamma"]].shape[0])
+    if D % 16 or D > 256 or int(q_op["N"]) != H * D or int(k_op["N"]) != Hkv * D or int(v_op["N"]) != Hkv * D:
+        return None
+    if any(int(o["K"]) != K for o in lin):
+        return None
+    if has_norm and (int(nq.get("heads", 1)) != H or int(nk.get("heads", 1)) != Hkv
+                     or int(model._dt[nq["gamma"]].shape[0]) != D or int(model._dt[nk["gamma"]].shape[0]) != D):
+        return None
+    if model.rope_cos.shape[0] < model.max_seq or model.rope_cos.shape[1] != D // 2:
+        return None
+    n_ops = j + 5 - i
+    layer = int(kvw["layer"])
+    dt = model._dt
+
+    def fill(d, M, pos, pd):
+        _pre(model, d.pre, rn, qu)
+        for r, o in enumerate(lin):
+            d.W[r] = _vp(dt[o["w"]])
+            d.rq[r] = _vp(dt[o["rq"]])
+            d.bias[r] = _vp(dt[o["bias"]]) if o.get("bias") else None
+            d.lin_out[r] = _vp(model._buf(o["out"]))
+        if has_norm:
+            for r, o in enumerate((nq, nk)):
+                d.nrm_gamma[r] = _vp(dt[o["gamma"]])
+                d.nrm_out[r] = _vp(model._buf(o["out"]))
+                d.nrm_eps[r], d.nrm_C[r], d.nrm_sh[r] = int(o["eps_t"]), int(o["C"]), int(o["sh_post"])
+        d.cos_tab, d.sin_tab = _vp(dt["rope_cos"]), _vp(dt["rope_sin"])
+        d.pos_dev = pd
+        for r, (ro, qo) in enumerate(((rq_, qq_), (rk_, kq_))):
+            d.rope_out[r] = _vp(model._buf(ro["out"]))
+            d.quant_out[r] = _vp(model._buf(qo["out"]))
+            d.quant_M[r], d.quant_S[r] = int(qo["M"]), int(qo["S"])
+        kc, vc = model._kv[layer]
+        d.kc, d.vc = _vp(kc), _vp(vc)
+        d.max_seq, d.M, d.H, d.Hkv, d.D, d.pos, d.has_norm = model.max_seq, M, H, Hkv, D, pos, int(has_norm)
+
+    n_all = (H + 2 * Hkv) * D
+    n_bias = sum(int(o["N"]) for o in lin if o.get("bias"))
+
+    def nbytes(M):
+        # q/k/v weights + rq + bias, the x rows in, q/k (i16, before and after RoPE), v and
+        # the quantised q/k rows out, the K/V cache rows written
+        return (n_all * K + 8 * n_all + 4 * n_bias + 2 * M * K + M * (H + Hkv) * D * (2 + 2 + 1) + M * Hkv * D
+                + 2 * M * Hkv * D)
+
+    return n_ops, FusedStep(model, "attn_in", steps[i:i + n_ops], fill, "llhip_attn_in", _lib.AttnInDesc, K, nbytes,
+                            q_op["out"], ops[i:i + n_ops])
+
+
+def match_mlp_in(model, ops, i, steps):
+    spec = model._act_spec
+    head = _norm_quant_head(ops, i, spec)
+    if head is None:
+        return None
+    rn, qu = head
+    K = int(model._dt[rn["gamma"]].shape[0])
+    j = i + 2
+    if j + 2 >= len(ops):
+        return None
+    a, b = ops[j], ops[j + 1]
+    if not (a.get("op") == "linear" and b.get("op") == "linear" and a["in"] == qu["out"] and b["in"] == qu["out"]):
+        return None
+    if a.get("out_dtype", "i16") != "i16" or b.get("out_dtype", "i16") != "i16":
+        return None
+    N = int(a["N"])
+    if int(b["N"]) != N or int(a["K"]) != K or int(b["K"]) != K:
+        return None
+    ea, eb = a.get("epilogue", "none") or "none", b.get("epilogue", "none") or "none"
+    fused_graph = ea == "silu" and eb == "mul" and b.get("aux") == a["out"]
+    unfused_graph = ea == "none" and eb == "none"
+    if fused_graph:
+        silu, sh_mul = a["silu"], int(b["aux_shift"])
+        sg_name, f_name, g_name, u_name = a["out"], b["out"], None, None
+        j += 2
+    elif unfused_graph:
+        if j + 3 >= len(ops):
+            return None
+        si, mu = ops[j + 2], ops[j + 3]
+        if not (_is(si, "silu") and _is(mu, "mul") and si["in"] == a["out"]):
+            return None
+        if {mu["a"], mu["b"]} != {si["out"], b["out"]}:
+            return None
+        silu, sh_mul = {"Mi": si["Mi"], "Si": si["Si"], "sh_out": si["sh_out"]}, int(mu["sh"])
+        sg_name, f_name, g_name, u_name = si["out"], mu["out"], a["out"], b["out"]
+        j += 4
+    else:
+        return None
+    if j >= len(ops) or not _is(ops[j], "quant") or ops[j]["in"] != f_name:
+        return None
+    fq = ops[j]
+    n_ops = j + 1 - i
+    dt = model._dt
+
+    def fill(d, M, pos, pd):
+        _pre(model, d.pre, rn, qu)
+        d.Wg, d.Wu = _vp(dt[a["w"]]), _vp(dt[b["w"]])
+        d.rqg, d.rqu = _vp(dt[a["rq"]]), _vp(dt[b["rq"]])
+        d.bg = _vp(dt[a["bias"]]) if a.get("bias") else None
+        d.bu = _vp(dt[b["bias"]]) if b.get("bias") else None
+        d.g_out = _vp(model._buf(g_name)) if g_name else None
+        d.u_out = _vp(model._buf(u_name)) if u_name else None
+        d.sg_out, d.f_out, d.fq_out = _vp(model._buf(sg_name)), _vp(model._buf(f_name)), _vp(model._buf(fq["out"]))
+        d.silu_Mi, d.silu_Si, d.silu_sh = int(silu["Mi"]), int(silu["Si"]), int(silu["sh_out"])
+        d.mul_sh, d.fq_M, d.fq_S, d.M, d.N = sh_mul, int(fq["M"]), int(fq["S"]), M, N
+
+    n_bias = (N if a.get("bias") else 0) + (N if b.get("bias") else 0)
+    n_out = 5 + (4 if g_name else 0)  # sg, f (i16) and f.q (i8) per element, g and u for unfused graphs
+
+    def nbytes(M):
+        # gate + up weights, rq, bias, the x rows in, the outputs
+        return 2 * N * K + 16 * N + 4 * n_bias + 2 * M * K + M * N * n_out
+
+    return n_ops, FusedStep(model, "mlp_in", steps[i:i + n_ops], fill, "llhip_mlp_in", _lib.MlpInDesc, K, nbytes,
+                            f_name, ops[i:i + n_ops])
+
+
+_EPI = {"none": 0, "resadd": 1, "silu": 2, "mul": 3}
+
+
+def match_norm_linear(model, ops, i, steps):
+    spec = model._act_spec
+    head = _norm_quant_head(ops, i, spec)
+    if head is None or i + 2 >= len(ops):
+        return None
+    rn, qu = head
+    lo = ops[i + 2]
+    if lo.get("op") != "linear" or lo["in"] != qu["out"]:
+        return None
+    K = int(model._dt[rn["gamma"]].shape[0])
+    if int(lo["K"]) != K:
+        return None
+    ep = lo.get("epilogue", "none") or "none"
+    out_i8 = lo.get("out_dtype", "i16") == "i8"
+    N = int(lo["N"])
+    dt = model._dt
+    s = lo.get("silu") or {}
+
+    def fill(d, M, pos, pd):
+        _pre(model, d.pre, rn, qu)
+        d.W, d.rq = _vp(dt[lo["w"]]), _vp(dt[lo["rq"]])
+        d.bias = _vp(dt[lo["bias"]]) if lo.get("bias") else None
+        d.aux = _vp(model._buf(lo["aux"])) if ep in ("resadd", "mul") else None
+        d.out = _vp(model._buf(lo["out"]))
+        d.epilogue, d.aux_shift = _EPI[ep], int(lo.get("aux_shift", 0) or 0)
+        d.silu_Mi, d.silu_Si, d.silu_sh = int(s.get("Mi", 0)), int(s.get("Si", 0)), int(s.get("sh_out", 0))
+        d.out_i8, d.M, d.N = int(out_i8), M, N
+
+    has_aux = ep in ("resadd", "mul")
+
+    def nbytes(M):
+        # weights, rq, bias, the x rows in (i16), outputs (+ aux rows)
+        return (N * K + 8 * N + (4 * N if lo.get("bias") else 0) + 2 * M * K + M * N * (1 if out_i8 else 2)
+                + (2 * M * N if has_aux else 0))
+
+    return 3, FusedStep(model, "norm_linear", steps[i:i + 3], fill, "llhip_norm_linear", _lib.NormLinearDesc, K,
+                        nbytes, lo["out"], ops[i:i + 3])
+
+
+MATCHERS = (match_attn_in, match_mlp_in, match_norm_linear)
+
+
+def fuse(model, ops, steps):
+    """New plan: matched runs of `ops` (steps[i] is op i's per-op step) become FusedSteps."""
+    out = []
+    i = 0
+    while i < len(ops):
+        if i >= len(steps):
+            break
+        got = None
+        for m in MATCHERS:
+            got = m(model, ops, i, steps)
+            if got is not None:
+                n = got[0]
+                # never swallow a deferred graph error: the reference raises it at that op
+                if i + n > len(steps) or any(getattr(s, "kind", "") == "error" for s in steps[i:i + n]):
+                    got = None
+                break
+        if got is None:
+            out.append(steps[i])
+            i += 1
+        else:
+            n, st = got
+            out.append(st)
+            i += n
+    out.extend(steps[len(ops):])
+    return out

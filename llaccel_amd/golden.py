@@ -369,8 +369,9 @@ class _Step:
 class GoldenModel:
     """Device-resident twin of golden.py:246-440 (same attributes, methods and record)."""
 
-    def __init__(self, qgraph_dir: Path | str, *, fast_matmul: bool = False) -> None:
+    def __init__(self, qgraph_dir: Path | str, *, fast_matmul: bool = False, fuse: bool = True) -> None:
         self.fast_matmul = fast_matmul  # accepted for API parity: every path here is exact integer arithmetic
+        self.fuse = fuse  # run matched op runs as fused launches (llaccel_amd.fusion); results are identical
         self.q = QGraph(qgraph_dir)
         m = self.q.model
         self.dim = int(m["dim"])
@@ -389,7 +390,7 @@ class GoldenModel:
         torch = _t()
         self.device = _dev()
         # one upload of the whole weight blob; every tensor is a view of it
-        self._blob = torch.from_numpy(np.asarray(self.q.blob)).to(self.device)
+        self._blob = torch.from_numpy(np.array(self.q.blob, copy=True)).to(self.device)
         self._dt: dict[str, object] = {}
         for name, spec in self.q.specs.items():
             self._dt[name] = self._tensor_view(spec)
@@ -522,7 +523,15 @@ class GoldenModel:
                 break
         if self.q.output_name not in spec and not any(isinstance(p, _Deferred) for p in plan):
             plan.append(_Deferred(ValueError(f"output {self.q.output_name!r} is never produced")))
+        self._plan_unfused = plan
+        if self.fuse:
+            from . import fusion
+
+            plan = fusion.fuse(self, self.q.ops, plan)
         return plan
+
+    def _stream_handle(self):
+        return _stream()
 
     def _c_rmsnorm(self, op, need, T):
         _, cols = need(op["in"], "i16")

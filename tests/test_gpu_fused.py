@@ -1,0 +1,99 @@
+"""Fused decoder-block launches (llaccel_amd.fusion -> llhip_attn_in / llhip_mlp_in /
+llhip_norm_linear) against the per-op path and the CPU oracle, bit-exact, on every
+configuration shape: tiny Llama (fused and unfused graphs), SmolLM2-135M, Qwen2.5-0.5B
+(QKV bias) and Qwen3-0.6B (head_dim 128, Q/K RMSNorm)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from llaccel_amd import golden as G
+from llaccel_amd import synth
+from oracle import golden_np as O
+
+pytestmark = pytest.mark.gpu
+
+_CACHE = {}
+
+
+def _qgraph(tmp_path_factory, cfg, fusion=True, seed=1):
+    key = (cfg, fusion, seed)
+    if key not in _CACHE:
+        d = tmp_path_factory.mktemp(f"{cfg}_{int(fusion)}")
+        _CACHE[key] = synth.build_qgraph(d, cfg, seed=seed, fusion=fusion)
+    return _CACHE[key]
+
+
+def _kinds(g):
+    return [getattr(s, "kind", "?") for s in g._plan]
+
+
+@pytest.mark.parametrize("name", ["ref_tiny_v2", "ref_tiny_v1"])
+def test_tiny_plan_is_fused_and_exact(golden_dir, name):
+    qdir = golden_dir / name / "qgraph"
+    g = G.GoldenModel(qdir)
+    k = _kinds(g)
+    assert k.count("attn_in") == 2 and k.count("mlp_in") == 2 and k.count("norm_linear") == 1
+    u = G.GoldenModel(qdir, fuse=False)
+    prompt = list(range(3, 23))
+    a1, a2 = [], []
+    assert g.generate(prompt, 6, a1) == u.generate(prompt, 6, a2)
+    for s1, s2 in zip(a1, a2):
+        assert set(s1["acts"]) == set(s2["acts"])
+        for n in s1["acts"]:
+            assert np.array_equal(s1["acts"][n], s2["acts"][n]), (s1["kind"], s1["pos"], n)
+
+
+@pytest.mark.parametrize("cfg,fusion", [("smol", True), ("smol", False), ("qwen25", True), ("qwen3", True)])
+def test_model_shapes_fused_vs_oracle(tmp_path_factory, cfg, fusion):
+    qdir = _qgraph(tmp_path_factory, cfg, fusion)
+    g = G.GoldenModel(qdir)
+    k = _kinds(g)
+    L = g.n_layers
+    assert k.count("attn_in") == L and k.count("mlp_in") == L and k.count("norm_linear") == 1, k[:20]
+    o = O.OracleModel(qdir, backend="c")
+    prompt = synth.seeded_prompt(cfg, 19, 5)
+    acts_g, acts_o = [], []
+    rg = g.generate(prompt, 3, acts_g)      # eager launches (activations collected)
+    ro = o.generate(prompt, 3, acts_o)
+    assert rg == ro
+    for sg, so in zip(acts_g, acts_o):
+        for n in so["acts"]:
+            assert np.array_equal(sg["acts"][n], so["acts"][n]), (sg["kind"], sg["pos"], n)
+    for layer in (0, L - 1):
+        assert np.array_equal(g.kv[layer][0], o.kv[layer][0]) and np.array_equal(g.kv[layer][1], o.kv[layer][1])
+    # graph decode path (no activations requested) gives the same record
+    assert g.generate(prompt, 3) == ro
+
+
+def test_qwen3_preinitialised_long_context(tmp_path_factory):
+    """Config 5: KV of every layer filled with seeded int8 at positions 0..4094, one decode
+    launch at position 4095 (T = 4096 = 16 tiles of 256 keys)."""
+    qdir = _qgraph(tmp_path_factory, "qwen3", True)
+    g = G.GoldenModel(qdir)
+    o = O.OracleModel(qdir, backend="c")
+    rng = np.random.default_rng(4095)
+    for layer in g.kv:
+        shape = o.kv[layer][0].shape
+        k = np.zeros(shape, np.int8)
+        v = np.zeros(shape, np.int8)
+        k[:, :4095] = rng.integers(-128, 128, (shape[0], 4095, shape[2]))
+        v[:, :4095] = rng.integers(-128, 128, (shape[0], 4095, shape[2]))
+        g.set_kv(layer, k, v)
+        o.kv[layer][0][...] = k
+        o.kv[layer][1][...] = v
+    tok = 12345
+    want = o.decode(tok, 4095)
+    assert np.array_equal(g.decode(tok, 4095), want)
+    for layer in (0, 13, 27):
+        assert np.array_equal(g.kv[layer][0], o.kv[layer][0]) and np.array_equal(g.kv[layer][1], o.kv[layer][1])
+    # the graph decode launch at the same position rewrites the same KV row and gives the same logits
+    toks, rows = g.decode_loop(tok, 4095, 1)
+    assert np.array_equal(rows[0], want[:g.vocab]) and toks[0] == int(np.argmax(want[:g.vocab]))
+
+
+def test_fused_and_unfused_graph_decode_agree(tmp_path_factory):
+    qdir = _qgraph(tmp_path_factory, "smol", True)
+    prompt = synth.seeded_prompt("smol", 33, 9)
+    g, u = G.GoldenModel(qdir), G.GoldenModel(qdir, fuse=False)
+    assert g.generate(prompt, 24) == u.generate(prompt, 24)
