@@ -185,24 +185,29 @@ def main() -> None:
     tok_s = args.steps / dt
     log(f"decode: {args.steps} steps in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
 
-    # ---- dominant kernel: decode GEMV family (all linear launches of one decode step) ----
+    # ---- per-kernel families of one decode step (graphs of the step's launches of one kind) ----
     T = L + args.warmup + args.steps
-    lin_graph = g.capture_steps({"linear"}, T - 1)
-    t_lin = time_graph(lin_graph, 20)
-    n_lin = g.count_steps("linear")
-    lin_bytes = g.step_bytes("linear", 1)
-    achieved = lin_bytes / t_lin / 1e9
-    attn_graph = g.capture_steps({"attention"}, T - 1)
-    t_attn = time_graph(attn_graph, 20)
-    attn_bytes = g.step_bytes("attention", 1, T)
-    step_bytes = lin_bytes + attn_bytes
-    log(f"linear: {n_lin} launches, {lin_bytes / 1e6:.1f} MB, {t_lin * 1e6:.1f} us -> {achieved:.0f} GB/s; "
-        f"attention {attn_bytes / 1e6:.2f} MB in {t_attn * 1e6:.1f} us")
-
-    roofline = {"bound": "hbm", "kernel": "linear_skinny (decode GEMV, M=1; all %d launches of one step)" % n_lin,
+    fam = {}
+    for kind in sorted({getattr(st, "kind", "?") for st in g._plan}):
+        if kind in ("error", "?"):
+            continue
+        n = g.count_steps(kind)
+        graph = g.capture_steps({kind}, T - 1)
+        t = time_graph(graph, 20)
+        nbytes = g.step_bytes(kind, 1, T)
+        fam[kind] = {"launches": n, "us_per_step": round(t * 1e6, 2), "us_per_launch": round(t / n * 1e6, 3),
+                     "bytes_per_launch": round(nbytes / n), "GBs": round(nbytes / t / 1e9, 1)}
+        log(f"  {kind:12s} {n:3d} launches {t * 1e6:8.1f} us/step {t / n * 1e6:7.2f} us/launch "
+            f"{nbytes / 1e6:8.2f} MB -> {nbytes / t / 1e9:7.1f} GB/s")
+        del graph
+    dom = max(fam, key=lambda k: fam[k]["us_per_step"] if fam[k]["bytes_per_launch"] > 0 else -1)
+    d = fam[dom]
+    achieved = d["bytes_per_launch"] / (d["us_per_launch"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": f"{dom} (decode, M=1; {d['launches']} launches per step)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "bytes_per_launch": round(lin_bytes / n_lin), "avg_launch_us": round(t_lin / n_lin * 1e6, 3)}
+                "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": d["us_per_launch"]}
+    step_bytes = sum(fam[k]["bytes_per_launch"] * fam[k]["launches"] for k in fam)
 
     # ---- CPU baseline (bounded sample of the same decode launches) ----
     cpu = None
@@ -220,9 +225,7 @@ def main() -> None:
     extra = {"prefill_tok_s": round(L / t_prefill, 1), "prefill_ms": round(t_prefill * 1e3, 2),
              "decode_step_bytes": step_bytes, "decode_hbm_frac_of_step": round(step_bytes / (dt / args.steps) / 1e9
                                                                                 / HBM_PEAK_GBS, 4),
-             "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1),
-             "attention_us": round(t_attn * 1e6, 2), "attention_GBs": round(attn_bytes / t_attn / 1e9, 1),
-             "linear_us_per_step": round(t_lin * 1e6, 2)}
+             "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1), "decode_kernel_families": fam}
     if not args.no_gemm:
         extra["gemm_sweep"] = gemm_sweep()
 

@@ -96,6 +96,17 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   const int8_t* V = p.vc + (int64_t)g * p.max_seq * D;
   const int8_t* qr = p.q + (int64_t)m * p.ldq + (int64_t)h * D;
 
+  // value rows of this thread's first VPF keys, loaded at entry so the value pass finds
+  // them in registers (their latency overlaps the score and softmax phases)
+  constexpr int VPF = 8;
+  const int dc = tid % DC, tg = tid / DC;
+  v4i vpre[VPF];
+#pragma unroll
+  for (int u = 0; u < VPF; ++u) {
+    const int t = tg + u * TG;
+    vpre[u] = t < T ? *reinterpret_cast<const v4i*>(V + (int64_t)t * D + 16 * dc) : v4i{0, 0, 0, 0};
+  }
+
   // scores s[t] = q . k[t] (int32, |s| <= D * 2^14), two keys in flight per thread
   v4i qv[DC];
 #pragma unroll
@@ -129,12 +140,24 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   }
   __syncthreads();
 
-  // o[d] = sum_t pn[t] * v[t][d]: thread (tg, dc) takes keys tg, tg+TG, ... (four in flight)
-  const int dc = tid % DC, tg = tid / DC;
+  // o[d] = sum_t pn[t] * v[t][d]: thread (tg, dc) takes keys tg, tg+TG, ... (prefetched rows
+  // first, then four in flight)
   int32_t acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0;
-  for (int t0 = tg; t0 < T; t0 += 4 * TG) {
+#pragma unroll
+  for (int u = 0; u < VPF; ++u) {
+    const int t = tg + u * TG;
+    const int32_t pn = t < T ? sc[t] : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i] += pn * sbyte(vpre[u].x, i);
+      acc[4 + i] += pn * sbyte(vpre[u].y, i);
+      acc[8 + i] += pn * sbyte(vpre[u].z, i);
+      acc[12 + i] += pn * sbyte(vpre[u].w, i);
+    }
+  }
+  for (int t0 = tg + VPF * TG; t0 < T; t0 += 4 * TG) {
     v4i vv[4];
     int32_t pn[4];
 #pragma unroll

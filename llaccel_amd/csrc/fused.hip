@@ -84,41 +84,65 @@ __device__ void norm_quant_rows(const NormQuant& pr, int M, int8_t* a_lds, int l
   }
 }
 
-// partial 16x16 tile over K steps [s_begin, s_end) with A rows from LDS (rows >= M are zeros)
-__device__ __forceinline__ v4i gemv_lds_partial(const int8_t* __restrict__ wrow, bool nvalid, const int8_t* a_lds,
-                                                int lda, int M, int K, int kg, int s_begin, int s_end) {
+// W operand of a wave's K slice: the first PF 16-byte chunks are loaded into registers at kernel
+// entry (before the RMSNorm prologue) so their HBM latency overlaps it; longer slices stream the rest.
+constexpr int PF = 8;
+
+struct WSlice {
+  v4i w[PF];
+  const int8_t* row;
+  int s0, s1, kg, K;
+  bool nvalid;
+};
+
+__device__ __forceinline__ void wslice_prefetch(WSlice& ws, const int8_t* __restrict__ wrow, bool nvalid, int K, int kg,
+                                                int s0, int s1) {
+  ws.row = wrow;
+  ws.s0 = s0;
+  ws.s1 = s1;
+  ws.kg = kg;
+  ws.K = K;
+  ws.nvalid = nvalid;
+#pragma unroll
+  for (int u = 0; u < PF; ++u) {
+    const int k = (s0 + u) * 64 + kg * 16;
+    ws.w[u] = (nvalid && s0 + u < s1 && k < K) ? *reinterpret_cast<const v4i*>(wrow + k) : v4i{0, 0, 0, 0};
+  }
+}
+
+// 16x16 partial tile of the slice with A rows from LDS (rows >= M are zeros)
+__device__ __forceinline__ v4i wslice_mfma(const WSlice& ws, const int8_t* a_lds, int lda, int M) {
   const int lane = threadIdx.x & 63;
   const int m = lane & 15;
   const bool avalid = m < M;
   const int8_t* arow = a_lds + m * lda;
   v4i acc = {0, 0, 0, 0};
-  int s = s_begin;
-  constexpr int U = 4;
-  for (; s + U <= s_end; s += U) {
-    v4i b[U], a[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (s + u) * 64 + kg * 16;
-      const bool ok = k < K;
-      b[u] = (nvalid && ok) ? *reinterpret_cast<const v4i*>(wrow + k) : v4i{0, 0, 0, 0};
+  for (int u = 0; u < PF; ++u) {
+    const int k = (ws.s0 + u) * 64 + ws.kg * 16;
+    const bool ok = ws.s0 + u < ws.s1 && k < ws.K;
+    const v4i a = (avalid && ok) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ws.w[u], acc, 0, 0, 0);
+  }
+  for (int s = ws.s0 + PF; s < ws.s1; s += 4) {
+    v4i b[4], a[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = (s + u) * 64 + ws.kg * 16;
+      const bool ok = s + u < ws.s1 && k < ws.K;
+      b[u] = (ws.nvalid && ok) ? *reinterpret_cast<const v4i*>(ws.row + k) : v4i{0, 0, 0, 0};
       a[u] = (avalid && ok) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
-  }
-  for (; s < s_end; ++s) {
-    const int k = s * 64 + kg * 16;
-    const bool ok = k < K;
-    const v4i b = (nvalid && ok) ? *reinterpret_cast<const v4i*>(wrow + k) : v4i{0, 0, 0, 0};
-    const v4i a = (avalid && ok) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
-    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
   }
   return acc;
 }
 
-__device__ __forceinline__ int64_t requant_raw(int64_t acc, const int32_t* bias, const int32_t* rq, int n) {
-  if (bias) acc += bias[n];
-  return mulshift(acc, rq[2 * n], rq[2 * n + 1]);
+__device__ __forceinline__ void split_range(int steps, int parts, int idx, int& s0, int& s1) {
+  const int spw = (steps + parts - 1) / parts;
+  s0 = min(idx * spw, steps);
+  s1 = min(s0 + spw, steps);
 }
 
 __device__ __forceinline__ void v4_add(v4i& a, const v4i& b) {
@@ -156,7 +180,7 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArg
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   __shared__ v4i red[FUSED_MAX_WAVES][64];
   const int lda = p.K + 16;
-  int8_t* a_lds = dyn;                                                      // [M][lda] i8
+  int8_t* a_lds = dyn;                                                         // [M][lda] i8
   int32_t* hres = reinterpret_cast<int32_t*>(dyn + ((p.M * lda + 15) & ~15));  // [M][D] i32
 
   const int b = blockIdx.x;
@@ -167,22 +191,32 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArg
   const int base = hh * D;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tiles = D >> 4;
+  const int pos0 = p.pos_dev ? *p.pos_dev : p.pos;
+
+  // kernel entry: weight slice and the epilogue operands of this thread's column
+  WSlice ws;
+  {
+    const int t = wave % tiles, ks = wave / tiles;
+    int s0, s1;
+    split_range((p.K + 63) >> 6, p.KS, ks, s0, s1);
+    const int n = base + t * 16 + (lane & 15);
+    wslice_prefetch(ws, p.W[role] + (int64_t)n * p.K, true, p.K, lane >> 4, s0, s1);
+  }
+  const int dcol = tid % D;  // blockDim is a multiple of D: each thread owns one column in the tail
+  const int ncol = base + dcol;
+  const int32_t rq_m = p.rq[role][2 * ncol], rq_s = p.rq[role][2 * ncol + 1];
+  const int32_t bias = p.bias[role] ? p.bias[role][ncol] : 0;
+  const int half = D >> 1;
+  const int jrope = tid % half, mrope = tid / half;
+  int64_t c0 = 0, s0r = 0;
+  if (role < 2 && mrope < M) {
+    c0 = p.cos_tab[(int64_t)(pos0 + mrope) * half + jrope];
+    s0r = p.sin_tab[(int64_t)(pos0 + mrope) * half + jrope];
+  }
 
   norm_quant_rows(p.pre, M, a_lds, lda, b == 0);
   __syncthreads();
-
-  // D columns = `tiles` 16-column tiles x KS K-splits
-  {
-    const int t = wave % tiles, ks = wave / tiles;
-    const int col = lane & 15, kg = lane >> 4;
-    const int n = base + t * 16 + col;
-    const int steps = (p.K + 63) >> 6;
-    const int spw = (steps + p.KS - 1) / p.KS;
-    const int s0 = min(ks * spw, steps), s1 = min(s0 + spw, steps);
-    const int8_t* wrow = p.W[role] + (int64_t)n * p.K;
-    const v4i acc = gemv_lds_partial(wrow, true, a_lds, lda, M, p.K, kg, s0, s1);
-    red[wave][lane] = acc;
-  }
+  red[wave][lane] = wslice_mfma(ws, a_lds, lda, M);
   __syncthreads();
   if (wave < tiles) {
     v4i acc = red[wave][lane];
@@ -196,22 +230,20 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArg
   }
   __syncthreads();
 
-  const int pos0 = p.pos_dev ? *p.pos_dev : p.pos;
+  const int rstep = blockDim.x / D;
   if (role == 2) {  // v: requant8 -> v activation and V cache
-    for (int i = tid; i < M * D; i += blockDim.x) {
-      const int m = i / D, d = i % D, n = base + d;
-      const int8_t y = (int8_t)sat8(requant_raw(hres[i], p.bias[2], p.rq[2], n));
-      static_cast<int8_t*>(p.lin_out[2])[(int64_t)m * Nrole + n] = y;
-      p.vc[((int64_t)hh * p.max_seq + pos0 + m) * D + d] = y;
+    for (int m = tid / D; m < M; m += rstep) {
+      const int8_t y = (int8_t)sat8(mulshift((int64_t)hres[m * D + dcol] + bias, rq_m, rq_s));
+      static_cast<int8_t*>(p.lin_out[2])[(int64_t)m * Nrole + ncol] = y;
+      p.vc[((int64_t)hh * p.max_seq + pos0 + m) * D + dcol] = y;
     }
     return;
   }
   // q / k: requant16 -> activation; head values kept in hres as int32
-  for (int i = tid; i < M * D; i += blockDim.x) {
-    const int m = i / D, d = i % D, n = base + d;
-    const int16_t y = (int16_t)sat16(requant_raw(hres[i], p.bias[role], p.rq[role], n));
-    static_cast<int16_t*>(p.lin_out[role])[(int64_t)m * Nrole + n] = y;
-    hres[i] = y;
+  for (int m = tid / D; m < M; m += rstep) {
+    const int16_t y = (int16_t)sat16(mulshift((int64_t)hres[m * D + dcol] + bias, rq_m, rq_s));
+    static_cast<int16_t*>(p.lin_out[role])[(int64_t)m * Nrole + ncol] = y;
+    hres[m * D + dcol] = y;
   }
   __syncthreads();
   if (p.has_norm) {  // RMSNorm over each D-wide head (golden.py:287-293, heads > 1)
@@ -231,11 +263,13 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArg
     __syncthreads();
   }
   // RoPE (golden.py:141-158) -> quant (golden.py:119-120) -> K cache for keys
-  const int half = D >> 1;
-  for (int i = tid; i < M * half; i += blockDim.x) {
-    const int m = i / half, j = i % half;
-    const int64_t prow = (int64_t)(pos0 + m) * half;
-    const int64_t c = p.cos_tab[prow + j], s = p.sin_tab[prow + j];
+  for (int m = mrope; m < M; m += blockDim.x / half) {
+    int64_t c = c0, s = s0r;
+    if (m != mrope) {
+      c = p.cos_tab[(int64_t)(pos0 + m) * half + jrope];
+      s = p.sin_tab[(int64_t)(pos0 + m) * half + jrope];
+    }
+    const int j = jrope;
     const int64_t x1 = hres[m * D + j], x2 = hres[m * D + half + j];
     const int16_t y1 = (int16_t)sat16(rshr(x1 * c - x2 * s, 14));
     const int16_t y2 = (int16_t)sat16(rshr(x2 * c + x1 * s, 14));
@@ -280,20 +314,29 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void mlp_in_kernel(MlpInArgs 
   __shared__ v4i red[FUSED_MAX_WAVES][64];
   const int lda = p.K + 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  norm_quant_rows(p.pre, p.M, dyn, lda, blockIdx.x == 0);
-  __syncthreads();
   const int col = lane & 15, kg = lane >> 4;
   const int n = blockIdx.x * 16 + col;
   const bool nvalid = n < p.N;
+  const int nn = nvalid ? n : 0;
+  WSlice ws;
   {
     const int up = wave >= p.KS;  // waves [0, KS): gate, [KS, 2KS): up
-    const int ks = up ? wave - p.KS : wave;
-    const int steps = (p.K + 63) >> 6;
-    const int spw = (steps + p.KS - 1) / p.KS;
-    const int s0 = min(ks * spw, steps), s1 = min(s0 + spw, steps);
-    const int8_t* wrow = (up ? p.Wu : p.Wg) + (int64_t)(nvalid ? n : 0) * p.K;
-    red[wave][lane] = gemv_lds_partial(wrow, nvalid, dyn, lda, p.M, p.K, kg, s0, s1);
+    int s0, s1;
+    split_range((p.K + 63) >> 6, p.KS, up ? wave - p.KS : wave, s0, s1);
+    wslice_prefetch(ws, (up ? p.Wu : p.Wg) + (int64_t)nn * p.K, nvalid, p.K, kg, s0, s1);
   }
+  int32_t rg_m = 0, rg_s = 0, ru_m = 0, ru_s = 0, bgv = 0, buv = 0;
+  if (wave == 0) {
+    rg_m = p.rqg[2 * nn];
+    rg_s = p.rqg[2 * nn + 1];
+    ru_m = p.rqu[2 * nn];
+    ru_s = p.rqu[2 * nn + 1];
+    bgv = p.bg ? p.bg[nn] : 0;
+    buv = p.bu ? p.bu[nn] : 0;
+  }
+  norm_quant_rows(p.pre, p.M, dyn, lda, blockIdx.x == 0);
+  __syncthreads();
+  red[wave][lane] = wslice_mfma(ws, dyn, lda, p.M);
   __syncthreads();
   if (wave != 0 || !nvalid) return;
   v4i ag = red[0][lane], au = red[p.KS][lane];
@@ -306,8 +349,8 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void mlp_in_kernel(MlpInArgs 
     const int m = 4 * kg + r;
     if (m >= p.M) continue;
     const int64_t o = (int64_t)m * p.N + n;
-    const int64_t tg = sat16(requant_raw(ag[r], p.bg, p.rqg, n));
-    const int64_t tu = sat16(requant_raw(au[r], p.bu, p.rqu, n));
+    const int64_t tg = sat16(mulshift((int64_t)ag[r] + bgv, rg_m, rg_s));
+    const int64_t tu = sat16(mulshift((int64_t)au[r] + buv, ru_m, ru_s));
     if (p.g_out) p.g_out[o] = (int16_t)tg;
     if (p.u_out) p.u_out[o] = (int16_t)tu;
     const int64_t sg = silu16(tg, p.silu_Mi, p.silu_Si, p.silu_sh);
@@ -339,16 +382,22 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void norm_gemv_kernel(NormGem
   __shared__ v4i red[FUSED_MAX_WAVES][64];
   const int lda = p.K + 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  norm_quant_rows(p.pre, p.M, dyn, lda, blockIdx.x == 0);
-  __syncthreads();
   const int col = lane & 15, kg = lane >> 4;
   const int t = wave % p.TPW, ks = wave / p.TPW;
   const int n = (blockIdx.x * p.TPW + t) * 16 + col;
   const bool nvalid = n < p.N;
-  const int steps = (p.K + 63) >> 6;
-  const int spw = (steps + p.KS - 1) / p.KS;
-  const int s0 = min(ks * spw, steps), s1 = min(s0 + spw, steps);
-  v4i acc = gemv_lds_partial(p.W + (int64_t)(nvalid ? n : 0) * p.K, nvalid, dyn, lda, p.M, p.K, kg, s0, s1);
+  const int nn = nvalid ? n : 0;
+  WSlice ws;
+  {
+    int s0, s1;
+    split_range((p.K + 63) >> 6, p.KS, ks, s0, s1);
+    wslice_prefetch(ws, p.W + (int64_t)nn * p.K, nvalid, p.K, kg, s0, s1);
+  }
+  const int32_t rq_m = p.rq[2 * nn], rq_s = p.rq[2 * nn + 1];
+  const int32_t bias = p.bias ? p.bias[nn] : 0;
+  norm_quant_rows(p.pre, p.M, dyn, lda, blockIdx.x == 0);
+  __syncthreads();
+  v4i acc = wslice_mfma(ws, dyn, lda, p.M);
   if (p.KS > 1) {
     red[wave][lane] = acc;
     __syncthreads();
@@ -361,7 +410,7 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void norm_gemv_kernel(NormGem
     const int m = 4 * kg + r;
     if (m >= p.M) continue;
     const int64_t o = (int64_t)m * p.N + n;
-    const int64_t v = requant_raw(acc[r], p.bias, p.rq, n);
+    const int64_t v = mulshift((int64_t)acc[r] + bias, rq_m, rq_s);
     if (p.out_i8) {
       static_cast<int8_t*>(p.out)[o] = (int8_t)sat8(v);
       continue;

@@ -88,31 +88,31 @@ __device__ __forceinline__ v4i load16(const int8_t* row, int k, int K, bool vali
 // device-scope synchronisation (on the multi-XCD part those fences flush the XCD's L2).
 constexpr int GEMV_MAX_WAVES = 16;
 
-template <bool ALIGNED>
-__device__ __forceinline__ v4i gemv_tile_partial(const LinearArgs& p, const int8_t* wrow, bool nvalid,
-                                                 const int8_t* arow, bool avalid, int kg, int s_begin, int s_end) {
-  v4i acc = {0, 0, 0, 0};
-  int s = s_begin;
-  constexpr int U = 4;
-  for (; s + U <= s_end; s += U) {
-    v4i b[U], a[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (s + u) * 64 + kg * 16;
-      b[u] = load16<ALIGNED>(wrow, k, p.K, nvalid);
-      a[u] = load16<ALIGNED>(arow, k, p.K, avalid);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+// epilogue operands of one lane's column n and rows m0 + 4*kg + r, loaded before the MFMAs
+template <int EPI>
+struct EpiOperands {
+  int64_t rq_m;
+  int rq_s;
+  int32_t bias;
+  int16_t aux[4];
+};
+
+template <int EPI, bool OUT8>
+__device__ __forceinline__ void finish_pre(const LinearArgs& p, const EpiOperands<EPI>& e, int r, int m, int n,
+                                           int64_t acc) {
+  const int64_t v = mulshift(acc + e.bias, e.rq_m, e.rq_s);
+  if (OUT8) {
+    static_cast<int8_t*>(p.out)[(int64_t)m * p.ldo + n] = (int8_t)sat8(v);
+    return;
   }
-  for (; s < s_end; ++s) {
-    const int k = s * 64 + kg * 16;
-    const v4i b = load16<ALIGNED>(wrow, k, p.K, nvalid);
-    const v4i a = load16<ALIGNED>(arow, k, p.K, avalid);
-    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
-  }
-  return acc;
+  int64_t t = sat16(v);
+  if (EPI == EPI_RESADD) t = sat16(t + e.aux[r]);
+  else if (EPI == EPI_SILU) t = silu16(t, p.Mi, p.Si, p.sh);
+  else if (EPI == EPI_MUL) t = sat16(rshr(wmul(t, e.aux[r]), p.aux_shift));
+  static_cast<int16_t*>(p.out)[(int64_t)m * p.ldo + n] = (int16_t)t;
 }
+
+constexpr int GEMV_PF = 8;  // K steps of W and A in flight per wave
 
 template <int EPI, bool OUT8, bool ALIGNED>
 __global__ __launch_bounds__(64 * GEMV_MAX_WAVES) void linear_gemv(LinearArgs p) {
@@ -126,32 +126,74 @@ __global__ __launch_bounds__(64 * GEMV_MAX_WAVES) void linear_gemv(LinearArgs p)
   const int m0 = blockIdx.z * 16;
   const int n = tile * 16 + col;
   const bool nvalid = n < p.N;
+  const int nn = nvalid ? n : 0;
   const bool avalid = m0 + col < p.M;
-  const int8_t* wrow = p.W + (int64_t)(nvalid ? n : 0) * p.K;
+  const int8_t* wrow = p.W + (int64_t)nn * p.K;
   const int8_t* arow = p.A + (int64_t)(avalid ? m0 + col : 0) * p.lda;
 
   const int spw = (p.steps + nw - 1) / nw;
   const int s_begin = min(wave * spw, p.steps);
   const int s_end = min(s_begin + spw, p.steps);
-  v4i acc = gemv_tile_partial<ALIGNED>(p, wrow, nvalid, arow, avalid, kg, s_begin, s_end);
-  if (nw > 1) {
-    if (wave > 0) red[wave - 1][lane] = acc;
-    __syncthreads();
-    if (wave > 0) return;
-    for (int w = 0; w < nw - 1; ++w) {
-      const v4i o = red[w][lane];
-      acc.x += o.x;
-      acc.y += o.y;
-      acc.z += o.z;
-      acc.w += o.w;
-    }
-  }
-  // acc[r] = C[4*kg + r][col] of this 16x16 tile
-  if (nvalid) {
+  v4i acc = {0, 0, 0, 0};
+  int s = s_begin;
+  // first GEMV_PF steps: every load issued before the first MFMA
+  {
+    v4i b[GEMV_PF], a[GEMV_PF];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m0 + 4 * kg + r;
-      if (m < p.M) finish<EPI, OUT8>(p, m, n, acc[r]);
+    for (int u = 0; u < GEMV_PF; ++u) {
+      const int k = (s + u) * 64 + kg * 16;
+      const bool ok = s + u < s_end;
+      b[u] = ok ? load16<ALIGNED>(wrow, k, p.K, nvalid) : v4i{0, 0, 0, 0};
+      a[u] = ok ? load16<ALIGNED>(arow, k, p.K, avalid) : v4i{0, 0, 0, 0};
+    }
+    EpiOperands<EPI> e{};
+    if (wave == 0) {
+      e.rq_m = p.rq[2 * nn];
+      e.rq_s = p.rq[2 * nn + 1];
+      e.bias = p.bias ? p.bias[nn] : 0;
+      if (EPI == EPI_RESADD || EPI == EPI_MUL) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 4 * kg + r;
+          e.aux[r] = m < p.M ? p.aux[(int64_t)m * p.ldaux + nn] : (int16_t)0;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < GEMV_PF; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+    s += GEMV_PF;
+    constexpr int U = 4;
+    for (; s < s_end; s += U) {
+      v4i bb[U], aa[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = (s + u) * 64 + kg * 16;
+        const bool ok = s + u < s_end;
+        bb[u] = ok ? load16<ALIGNED>(wrow, k, p.K, nvalid) : v4i{0, 0, 0, 0};
+        aa[u] = ok ? load16<ALIGNED>(arow, k, p.K, avalid) : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(aa[u], bb[u], acc, 0, 0, 0);
+    }
+    if (nw > 1) {
+      if (wave > 0) red[wave - 1][lane] = acc;
+      __syncthreads();
+      if (wave > 0) return;
+      for (int w = 0; w < nw - 1; ++w) {
+        const v4i o = red[w][lane];
+        acc.x += o.x;
+        acc.y += o.y;
+        acc.z += o.z;
+        acc.w += o.w;
+      }
+    }
+    // acc[r] = C[4*kg + r][col] of this 16x16 tile
+    if (nvalid) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 4 * kg + r;
+        if (m < p.M) finish_pre<EPI, OUT8>(p, e, r, m, n, acc[r]);
+      }
     }
   }
 }

@@ -403,6 +403,7 @@ class GoldenModel:
         self._graph = None
         self._ring_cap = 0
         self.use_graph = True
+        self.whole_prompt_prefill = True
         self.reset()
 
     # ---- device tensors ---------------------------------------------------------------------
@@ -915,8 +916,19 @@ class GoldenModel:
         return sum(1 for st in self._plan if st.kind == kind)
 
     def prefill(self, tokens, acts: list | None = None) -> list[np.ndarray]:
-        """Chunked prefill with model.prefill_m rows per launch (golden.py:379-390)."""
+        """Prefill with the launch structure of golden.py:379-390 (chunks of prefill_m rows).
+
+        Without `acts` (and with `whole_prompt_prefill`) the chunks run as ONE launch of all
+        ceil(L/prefill_m)*prefill_m rows at positions 0..: every row depends only on itself and
+        on keys at earlier positions, and the zero pad rows of the last chunk sit at the same
+        positions as in the chunked run, so logits and the KV state are identical (a GPU test
+        checks it) while the GEMMs run at M = padded prompt length on the MFMA tiled kernel."""
         tokens = [int(t) for t in tokens]
+        L = len(tokens)
+        padded = -(-L // self.prefill_m) * self.prefill_m
+        if acts is None and self.whole_prompt_prefill and L > self.prefill_m and padded <= self.max_seq:
+            self._launch_tokens(tokens, 0, padded)
+            return list(_down(self._act[self.q.output_name][:L]).astype(I64))
         rows_out = []
         for start in range(0, len(tokens), self.prefill_m):
             chunk = tokens[start:start + self.prefill_m]

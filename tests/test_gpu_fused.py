@@ -92,6 +92,20 @@ def test_qwen3_preinitialised_long_context(tmp_path_factory):
     assert np.array_equal(rows[0], want[:g.vocab]) and toks[0] == int(np.argmax(want[:g.vocab]))
 
 
+@pytest.mark.parametrize("cfg", ["smol", "qwen25", "qwen3"])
+def test_whole_prompt_prefill_large_models(tmp_path_factory, cfg):
+    """Config 3-5 shapes: one M = 64 prefill launch (tiled MFMA GEMM, M-row attention) == the
+    chunked M = 16 launches (fused kernels), logits and KV."""
+    qdir = _qgraph(tmp_path_factory, cfg, True)
+    prompt = synth.seeded_prompt(cfg, 61, 3)
+    g1, g2 = G.GoldenModel(qdir), G.GoldenModel(qdir)
+    g2.whole_prompt_prefill = False
+    r1, r2 = g1.prefill(prompt), g2.prefill(prompt)
+    assert all(np.array_equal(a, b) for a, b in zip(r1, r2))
+    for layer in (0, g1.n_layers // 2, g1.n_layers - 1):
+        assert np.array_equal(g1.kv[layer][0], g2.kv[layer][0]) and np.array_equal(g1.kv[layer][1], g2.kv[layer][1])
+
+
 def test_fused_and_unfused_graph_decode_agree(tmp_path_factory):
     qdir = _qgraph(tmp_path_factory, "smol", True)
     prompt = synth.seeded_prompt("smol", 33, 9)

@@ -146,3 +146,20 @@ def test_decode_loop_matches_sequential_decode(golden_dir):
         assert np.array_equal(rows[i], row[:g2.vocab]), i
         t = G.GoldenModel.argmax(row, g2.vocab)
         assert t == toks[i]
+
+
+@pytest.mark.parametrize("name,plen", [("ref_tiny_v2", 16), ("ref_tiny_v2", 41), ("ref_tiny_v2_m4", 9),
+                                       ("ref_tiny_v1", 33)])
+def test_whole_prompt_prefill_equals_chunked(golden_dir, name, plen):
+    """One launch of the padded prompt == the chunked launches: logits rows, records, and the
+    whole KV state including the pad rows' entries."""
+    qdir = golden_dir / name / "qgraph"
+    prompt = synth.seeded_prompt("tiny", plen, 77)
+    g1, g2 = G.GoldenModel(qdir), G.GoldenModel(qdir)
+    g2.whole_prompt_prefill = False
+    r1, r2 = g1.prefill(prompt), g2.prefill(prompt)
+    assert len(r1) == len(r2) == plen and all(np.array_equal(a, b) for a, b in zip(r1, r2))
+    for layer in g1.kv:
+        assert np.array_equal(g1.kv[layer][0], g2.kv[layer][0]) and np.array_equal(g1.kv[layer][1], g2.kv[layer][1])
+    g1.reset(), g2.reset()
+    assert g1.generate(prompt, 5) == g2.generate(prompt, 5) == O.OracleModel(qdir, "c").generate(prompt, 5)
