@@ -9,10 +9,12 @@
 //    registers); the partials are summed in LDS.  W [N][K] row-major is streamed once
 //    with 16-byte loads, four K steps in flight per wave.  Integer addition is
 //    associative, so the split never changes a result.
-//  * linear_tiled: M > 16.  128x128x64 block tiles, four waves in 2x2, each wave
-//    64x64 with v_mfma_i32_32x32x32_i8; A and W tiles double-buffered in LDS.
+//  * linear_tiled: M > 16.  128x256 (or 128x128) x 64 block tiles, four waves in 2x2,
+//    each wave 64x128 (64x64) with v_mfma_i32_32x32x32_i8; A and W double-buffered in LDS.
 //    Blocks are numbered XCD-major so the blocks that share a W panel run on one
 //    XCD and share its L2.
+#include <type_traits>
+
 #include "../../include/llhip.h"
 #include "common.h"
 
@@ -199,15 +201,35 @@ __global__ __launch_bounds__(64 * GEMV_MAX_WAVES) void linear_gemv(LinearArgs p)
 }
 
 // ---------------------------------------------------------------------------------------
-// M > 16: LDS-tiled 128x128x64 MFMA GEMM (K % 16 == 0)
+// M > 16: LDS-tiled MFMA GEMM (K % 16 == 0)
 // ---------------------------------------------------------------------------------------
-constexpr int TBM = 128, TBN = 128, TBK = 64;
+// Block = 2 x 2 waves; a wave owns a (32*WM) x (32*WN) tile of v_mfma_i32_32x32x32_i8 blocks.
+// Per 64-deep K tile the block stages A [BM][64] and W [BN][64] in LDS (rows padded to 80 B,
+// conflict-free 16-byte reads), double-buffered: the global loads of tile k+1 are in flight while
+// tile k feeds the MFMAs.  Epilogue: per output column the requant multiplier M_n, shift S_n and
+// bias*M_n are loaded once, so (acc + bias) * M_n is one 32x32->64 multiply-add per element.
+constexpr int TBK = 64;
 constexpr int TLD = TBK + 16;  // LDS row stride in bytes (pad against bank conflicts)
 
 template <int EPI, bool OUT8>
+__device__ __forceinline__ void store_out(const LinearArgs& p, int m, int n, int64_t v, int16_t aux) {
+  if (OUT8) {
+    static_cast<int8_t*>(p.out)[(int64_t)m * p.ldo + n] = (int8_t)sat8(v);
+    return;
+  }
+  int64_t t = sat16(v);
+  if (EPI == EPI_RESADD) t = sat16(t + aux);
+  else if (EPI == EPI_SILU) t = silu16(t, p.Mi, p.Si, p.sh);
+  else if (EPI == EPI_MUL) t = sat16(rshr(wmul(t, aux), p.aux_shift));
+  static_cast<int16_t*>(p.out)[(int64_t)m * p.ldo + n] = (int16_t)t;
+}
+
+template <int EPI, bool OUT8, int WM, int WN>
 __global__ __launch_bounds__(256) void linear_tiled(LinearArgs p, int mblocks, int nblocks) {
-  __shared__ __attribute__((aligned(16))) int8_t As[2][TBM * TLD];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[2][TBN * TLD];
+  constexpr int BM = 64 * WM, BN = 64 * WN;
+  constexpr int ACH = BM * 4 / 256, BCH = BN * 4 / 256;  // 16-byte chunks per thread per K tile
+  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * TLD];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * TLD];
 
   // XCD-major block numbering: hardware dispatches block b to XCD b % 8
   const int nb_total = mblocks * nblocks;
@@ -216,40 +238,46 @@ __global__ __launch_bounds__(256) void linear_tiled(LinearArgs p, int mblocks, i
   if (nb_total % 8 == 0) logical = (b % 8) * (nb_total / 8) + b / 8;
   const int mb = logical % mblocks;
   const int nbk = logical / mblocks;
-  const int m0 = mb * TBM, n0 = nbk * TBN;
+  const int m0 = mb * BM, n0 = nbk * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+  const int wm = (wave & 1) * 32 * WM, wn = (wave >> 1) * 32 * WN;
 
-  // global -> LDS staging: each thread moves 2 x 16 B of A and 2 x 16 B of W per K tile
-  v4i ra[2], rb[2];
+  v4i ra[ACH], rb[BCH];
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < ACH; ++i) {
       const int c = tid + 256 * i;
-      const int row = c >> 2, kc = (c & 3) * 16;
-      const int gm = m0 + row, gn = n0 + row, gk = k0 + kc;
+      const int row = c >> 2, gk = k0 + (c & 3) * 16, gm = m0 + row;
       ra[i] = (gm < p.M && gk < p.K) ? *reinterpret_cast<const v4i*>(p.A + (int64_t)gm * p.lda + gk) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 2, gk = k0 + (c & 3) * 16, gn = n0 + row;
       rb[i] = (gn < p.N && gk < p.K) ? *reinterpret_cast<const v4i*>(p.W + (int64_t)gn * p.K + gk) : v4i{0, 0, 0, 0};
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < ACH; ++i) {
       const int c = tid + 256 * i;
-      const int row = c >> 2, kc = (c & 3) * 16;
-      *reinterpret_cast<v4i*>(&As[buf][row * TLD + kc]) = ra[i];
-      *reinterpret_cast<v4i*>(&Bs[buf][row * TLD + kc]) = rb[i];
+      *reinterpret_cast<v4i*>(&As[buf][(c >> 2) * TLD + (c & 3) * 16]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<v4i*>(&Bs[buf][(c >> 2) * TLD + (c & 3) * 16]) = rb[i];
     }
   };
 
-  v16i acc[2][2];
+  v16i acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+    for (int j = 0; j < WN; ++j) acc[i][j] = v16i{};
 
   const int ktiles = (p.K + TBK - 1) / TBK;
   gload(0);
@@ -260,17 +288,18 @@ __global__ __launch_bounds__(256) void linear_tiled(LinearArgs p, int mblocks, i
     if (kt + 1 < ktiles) gload((kt + 1) * TBK);
 #pragma unroll
     for (int ks = 0; ks < TBK; ks += 32) {
-      v4i fa[2], fb[2];
+      v4i fa[WM], fb[WN];
       const int koff = ks + 16 * (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < WM; ++i)
         fa[i] = *reinterpret_cast<const v4i*>(&As[buf][(wm + 32 * i + (lane & 31)) * TLD + koff]);
-        fb[i] = *reinterpret_cast<const v4i*>(&Bs[buf][(wn + 32 * i + (lane & 31)) * TLD + koff]);
-      }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < WN; ++j)
+        fb[j] = *reinterpret_cast<const v4i*>(&Bs[buf][(wn + 32 * j + (lane & 31)) * TLD + koff]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
     if (kt + 1 < ktiles) sstore(buf ^ 1);
     __syncthreads();
@@ -278,17 +307,240 @@ __global__ __launch_bounds__(256) void linear_tiled(LinearArgs p, int mblocks, i
 
   // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < WN; ++j) {
+    const int n = n0 + wn + 32 * j + (lane & 31);
+    if (n >= p.N) continue;
+    const int32_t Mn = p.rq[2 * n];
+    const int Sn = p.rq[2 * n + 1];
+    const int64_t bM = (int64_t)(p.bias ? p.bias[n] : 0) * Mn;  // (acc + bias) * M = acc * M + bias * M
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn + 32 * j + (lane & 31);
-      if (n >= p.N) continue;
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (m < p.M) finish<EPI, OUT8>(p, m, n, acc[i][j][r]);
+        if (m >= p.M) continue;
+        const int64_t v = rshr((int64_t)acc[i][j][r] * Mn + bM, Sn);
+        const int16_t aux = (EPI == EPI_RESADD || EPI == EPI_MUL) ? p.aux[(int64_t)m * p.ldaux + n] : (int16_t)0;
+        store_out<EPI, OUT8>(p, m, n, v, aux);
+      }
+  }
+}
+
+// Requant of one accumulator, rshr((int64)acc * M + bias * M, S) (= golden.py's
+// mulshift(acc + bias, M, S)), returned clamped to int32 (every later step saturates to 8 or 16
+// bits, so the clamp changes no output).  With v = hi:lo and S >= 32 the shifted value is
+// hi >> (S - 32) and its rounding bit, bit S-1 of v, is bit 31 of alignbit(hi, lo, S - 32): six
+// 32-bit operations after one v_mad_i64_i32.  |v| < 2^62.6, so hi >> (S-32) + 1 cannot overflow.
+struct ColRq {
+  int32_t M;
+  int S;
+  int64_t bM;  // bias * M
+};
+
+__device__ __forceinline__ ColRq make_colrq(int32_t M, int S, int32_t bias) {
+  ColRq c;
+  c.M = M;
+  c.S = S;
+  c.bM = (int64_t)bias * M;
+  // opaque to the optimiser (emits nothing): otherwise acc * M + bias * M is refactored into
+  // (acc + bias) * M, a 64 x 32-bit product, instead of one v_mad_i64_i32 per element
+  __asm__ volatile("" : "+v"(c.bM));
+  return c;
+}
+
+template <bool FAST>
+__device__ __forceinline__ int32_t requant_col(int32_t acc, const ColRq& c) {
+  const int64_t v = (int64_t)acc * (int64_t)c.M + c.bM;
+  if (FAST) {
+    const uint32_t sh = (uint32_t)(c.S - 32);
+    const int32_t hi = (int32_t)(v >> 32);
+    const uint32_t lo = (uint32_t)v;
+    return (hi >> sh) + (int32_t)(__builtin_amdgcn_alignbit((uint32_t)hi, lo, sh) >> 31);
+  }
+  return (int32_t)clamp64(rshr(v, c.S), INT32_MIN, INT32_MAX);
+}
+
+__device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) { return min(max(v, lo), hi); }
+
+// ---------------------------------------------------------------------------------------
+// Large GEMM (M >= 128, K % 64 == 0): 256x256x64 block tile, 8 waves, 3-stage LDS ring fed by
+// direct global->LDS loads (global_load_lds_dwordx4)
+// ---------------------------------------------------------------------------------------
+// Each wave instruction moves 64 x 16 B into 1 KiB of LDS (16 rows of 64 B).  Lane L of it
+// writes slot L of that KiB (row L/4, slot L%4) and fetches K chunk (L%4) ^ swz(row), so a row's
+// four 16-byte chunks are stored XOR-permuted: fragment reads of 8 (or 16) consecutive rows at one
+// K chunk then fall into distinct LDS banks without padding.  Tiles k+1 and k+2 are in flight
+// while tile k feeds the MFMAs.  Rows past M/N read a clamped valid row (their outputs are
+// discarded); K is a multiple of 64, so no K chunk is partial.
+constexpr int GB = 256;      // block tile rows (A) and columns (W)
+constexpr int GSTAGES = 3;
+constexpr int GSTAGE_BYTES = 2 * GB * 64;  // A + W of one K tile
+
+__device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+template <int EPI, bool OUT8>
+__global__ __launch_bounds__(512) void linear_mfma(LinearArgs p, int mblocks, int nblocks) {
+  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A 256x64 | W 256x64]
+  const int nb_total = mblocks * nblocks;
+  const int b = blockIdx.x;
+  int logical = b;
+  if (nb_total % 8 == 0) logical = (b % 8) * (nb_total / 8) + b / 8;  // XCD-major (block b runs on XCD b % 8)
+  const int mb = logical % mblocks;
+  const int nbk = logical / mblocks;
+  const int m0 = mb * GB, n0 = nbk * GB;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave & 1) * 128, wn = (wave >> 1) * 64;  // 2 x 4 waves, 128 x 64 each
+
+  // this lane's source rows for the two A and two W load instructions of a stage
+  const int8_t* asrc[2];
+  const int8_t* wsrc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (wave * 2 + i) * 16 + (lane >> 2);
+    const int chunk = (lane & 3) ^ lds_swz(r);
+    const int gm = min(m0 + r, p.M - 1), gn = min(n0 + r, p.N - 1);
+    asrc[i] = p.A + (int64_t)gm * p.lda + chunk * 16;
+    wsrc[i] = p.W + (int64_t)gn * p.K + chunk * 16;
+  }
+  auto issue = [&](int kt) {
+    int8_t* st = ring + (kt % GSTAGES) * GSTAGE_BYTES;
+    const int k0 = kt * 64;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_global_load_lds(asrc[i] + k0, st + (wave * 2 + i) * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(wsrc[i] + k0, st + GB * 64 + (wave * 2 + i) * 1024, 16, 0, 0);
+    }
+  };
+
+  v16i acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+
+  const int ktiles = p.K / 64;
+  issue(0);
+  if (ktiles > 1) issue(1);
+  for (int kt = 0; kt < ktiles; ++kt) {
+    // tile kt landed once at most the next tile's 4 loads are outstanding
+    if (kt + 1 < ktiles)
+      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4), expcnt/lgkmcnt don't-care
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // Every wave has its own tile-kt copies in LDS; after the barrier all of them are, and every
+    // wave has finished reading stage (kt-1) % 3, which issue(kt + 2) overwrites.  A bare
+    // s_barrier: __syncthreads() would also drain the tile-(kt+1) copies still in flight.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (kt + 2 < ktiles) issue(kt + 2);
+    const int8_t* st = ring + (kt % GSTAGES) * GSTAGE_BYTES;
+    const int8_t* As = st;
+    const int8_t* Ws = st + GB * 64;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 2 + (lane >> 5);  // 16-byte K chunk of this lane's fragment
+      v4i fa[4], fb[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = wm + 32 * i + (lane & 31);
+        fa[i] = *reinterpret_cast<const v4i*>(As + r * 64 + ((c ^ lds_swz(r)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = wn + 32 * j + (lane & 31);
+        fb[j] = *reinterpret_cast<const v4i*>(Ws + r * 64 + ((c ^ lds_swz(r)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Epilogue through LDS: the requantised block tile is staged row-major in the (now idle) ring and
+  // written back with 16-byte stores along whole 256-column rows; stores straight from the MFMA
+  // layout would be single bytes per lane (partial-line HBM writes).  i16 outputs take two passes
+  // of 128 rows (64 KiB each).
+  constexpr int OB = OUT8 ? 1 : 2;
+  constexpr int PASS_ROWS = OUT8 ? 256 : 128;
+  constexpr int ROWB = GB * OB;  // staged row bytes
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();  // every wave is done reading the ring (the last DMA was waited for)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const bool vec_ok = ((p.ldo * OB) % 16 == 0) && ((uintptr_t)p.out % 16 == 0);
+  ColRq cq[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = min(n0 + wn + 32 * j + (lane & 31), p.N - 1);
+    cq[j] = make_colrq(p.rq[2 * n], p.rq[2 * n + 1], p.bias ? p.bias[n] : 0);  // (acc+bias)*M = acc*M + bias*M
+  }
+  // one wave-uniform choice of the requant form
+  const bool fast = __all(cq[0].S >= 32 && cq[1].S >= 32);
+  auto stage = [&](auto fast_tag, int pass) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int cl = wn + 32 * j + (lane & 31);
+      const int n = n0 + cl;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rl = wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+          const int m = m0 + rl;
+          const int32_t v = requant_col<FAST>(acc[i][j][r], cq[j]);
+          int8_t* slot = ring + (rl - pass * PASS_ROWS) * ROWB + cl * OB;
+          if (OUT8) {
+            *slot = (int8_t)clamp32(v, -128, 127);
+          } else {
+            int32_t t = clamp32(v, -32768, 32767);
+            if (EPI == EPI_RESADD || EPI == EPI_MUL) {
+              const int32_t aux = (m < p.M && n < p.N) ? p.aux[(int64_t)m * p.ldaux + n] : 0;
+              if (EPI == EPI_RESADD) t = clamp32(t + aux, -32768, 32767);
+              else t = (int32_t)sat16(rshr((int64_t)(t * aux), p.aux_shift));
+            } else if (EPI == EPI_SILU) {
+              t = (int32_t)silu16(t, p.Mi, p.Si, p.sh);
+            }
+            *reinterpret_cast<int16_t*>(slot) = (int16_t)t;
+          }
+        }
+    }
+  };
+#pragma unroll
+  for (int pass = 0; pass < GB / PASS_ROWS; ++pass) {
+    if (wm / PASS_ROWS == pass) {
+      if (fast)
+        stage(std::true_type{}, pass);
+      else
+        stage(std::false_type{}, pass);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    constexpr int CPR = ROWB / 16;  // 16-byte chunks per staged row
+    for (int idx = tid; idx < PASS_ROWS * CPR; idx += 512) {
+      const int rl = idx / CPR, ch = idx % CPR;
+      const int m = m0 + pass * PASS_ROWS + rl;
+      const int nc = n0 + ch * (16 / OB);
+      if (m >= p.M || nc >= p.N) continue;
+      const int8_t* src = ring + rl * ROWB + ch * 16;
+      char* dst = static_cast<char*>(p.out) + ((int64_t)m * p.ldo + nc) * OB;
+      if (vec_ok && nc + 16 / OB <= p.N) {
+        *reinterpret_cast<v4i*>(dst) = *reinterpret_cast<const v4i*>(src);
+      } else {
+        for (int e = 0; e < 16 / OB && nc + e < p.N; ++e)
+          for (int q = 0; q < OB; ++q) dst[e * OB + q] = src[e * OB + q];
       }
     }
+    if (pass + 1 < GB / PASS_ROWS) {
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -297,9 +549,22 @@ __global__ __launch_bounds__(256) void linear_tiled(LinearArgs p, int mblocks, i
 template <int EPI, bool OUT8>
 static int launch_linear(LinearArgs& p, hipStream_t stream) {
   const bool aligned = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.W % 16 == 0);
+  if (p.M >= 128 && p.K % 64 == 0 && aligned &&
+      (int64_t)ceil_div(p.M, GB) * ceil_div(p.N, GB) >= current_cu_count()) {
+    const int mblocks = (int)ceil_div(p.M, GB), nblocks = (int)ceil_div(p.N, GB);
+    hipLaunchKernelGGL((linear_mfma<EPI, OUT8>), dim3(mblocks * nblocks), dim3(512), GSTAGES * GSTAGE_BYTES, stream,
+                       p, mblocks, nblocks);
+    LLHIP_LAUNCH_CHECK();
+    return 0;
+  }
   if (p.M > 16 && aligned) {
-    const int mblocks = (int)ceil_div(p.M, TBM), nblocks = (int)ceil_div(p.N, TBN);
-    hipLaunchKernelGGL((linear_tiled<EPI, OUT8>), dim3(mblocks * nblocks), dim3(256), 0, stream, p, mblocks, nblocks);
+    // 128x256 block tiles when they still fill the chip, else 128x128
+    const int mblocks = (int)ceil_div(p.M, 128);
+    const int nb256 = (int)ceil_div(p.N, 256), nb128 = (int)ceil_div(p.N, 128);
+    if ((int64_t)mblocks * nb256 >= 2 * current_cu_count())
+      hipLaunchKernelGGL((linear_tiled<EPI, OUT8, 2, 4>), dim3(mblocks * nb256), dim3(256), 0, stream, p, mblocks, nb256);
+    else
+      hipLaunchKernelGGL((linear_tiled<EPI, OUT8, 2, 2>), dim3(mblocks * nb128), dim3(256), 0, stream, p, mblocks, nb128);
     LLHIP_LAUNCH_CHECK();
     return 0;
   }

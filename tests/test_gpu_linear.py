@@ -100,3 +100,26 @@ def test_error_paths():
         gpu_linear(a, w, rq, out_i8=True, epilogue="resadd", aux=np.zeros((2, 16)))
     with pytest.raises(ValueError):
         gpu_linear(a, w, rq, out_i8=False, epilogue="mul", aux=np.zeros((2, 16)), aux_shift=64)
+
+
+@pytest.mark.parametrize("epilogue,out_i8", [("none", True), ("none", False), ("resadd", False), ("silu", False),
+                                             ("mul", False)])
+def test_large_gemm_path_ragged_with_epilogues(epilogue, out_i8):
+    """Shapes large enough for the 256x256 LDS-ring MFMA kernel, with M and N not multiples of
+    the block tile, a full-range bias and every epilogue; sampled rows x all columns and all
+    rows x sampled columns against the oracle."""
+    rng = np.random.default_rng(len(epilogue) + out_i8)
+    M, K, N = 300, 896, 76000
+    a, w, rq = _operands(rng, M, K, N, out_i8=out_i8)
+    bias = rng.integers(-(2**31), 2**31 - 1, N)
+    aux = rng.integers(-32768, 32768, (M, N)) if epilogue in ("resadd", "mul") else None
+    silu = {"Mi": 1 << 30, "Si": 30, "sh_out": 16} if epilogue == "silu" else None
+    sh = 11 if epilogue == "mul" else 0
+    got = gpu_linear(a, w, rq, bias=bias, out_i8=out_i8, epilogue=epilogue, aux=aux, aux_shift=sh, silu=silu)
+    rows = np.array([0, 1, 127, 128, 255, 256, 298, 299])
+    cols = np.concatenate([np.arange(0, 40), np.arange(75900, 76000), rng.choice(N, 60, replace=False)])
+    want_r = O.linear_c(a[rows], w, rq, bias, out_i8, epilogue, None if aux is None else aux[rows], sh, silu)
+    want_c = O.linear_c(a, w[cols], rq[cols], bias[cols], out_i8, epilogue, None if aux is None else aux[:, cols], sh,
+                        silu)
+    assert np.array_equal(got[rows], want_r)
+    assert np.array_equal(got[:, cols], want_c)
