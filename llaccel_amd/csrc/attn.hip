@@ -19,7 +19,7 @@
 namespace llhip {
 
 
-constexpr int ATTN_MAX_T = 12000;  // scores + value partials stay within a 64 KiB block allocation
+constexpr int ATTN_MAX_T = 12000;  // 48 KB of scores + 32 KB of value partials (D = 256) in LDS
 
 struct AttnArgs {
   const int8_t* q;
@@ -37,101 +37,148 @@ struct AttnArgs {
 constexpr int ATTN_THREADS = 512;
 constexpr int ATTN_WAVES = ATTN_THREADS / 64;
 
-__device__ __forceinline__ int32_t block_max_i32(int32_t v, int32_t* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off));
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  int32_t r = red[0];
-#pragma unroll
-  for (int w = 1; w < ATTN_WAVES; ++w) r = max(r, red[w]);
-  return r;
-}
-
-__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, int32_t* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = (int32_t)v;
-  __syncthreads();
-  uint32_t r = 0;
-#pragma unroll
-  for (int w = 0; w < ATTN_WAVES; ++w) r += (uint32_t)red[w];
-  return r;
-}
-
 __device__ __forceinline__ int32_t sbyte(int w, int i) { return (int32_t)(int8_t)((uint32_t)w >> (8 * i)); }
 
 template <int D>
-__device__ __forceinline__ int32_t dot_row(const v4i* qv, const v4i* kr) {
+__device__ __forceinline__ int32_t dot_row(const v4i* qv, const v4i* kv) {
   constexpr int DC = D / 16;
   int32_t s = 0;
 #pragma unroll
   for (int c = 0; c < DC; ++c) {
-    const v4i kv = kr[c];
-    s = __builtin_amdgcn_sdot4(qv[c].x, kv.x, s, false);
-    s = __builtin_amdgcn_sdot4(qv[c].y, kv.y, s, false);
-    s = __builtin_amdgcn_sdot4(qv[c].z, kv.z, s, false);
-    s = __builtin_amdgcn_sdot4(qv[c].w, kv.w, s, false);
+    s = __builtin_amdgcn_sdot4(qv[c].x, kv[c].x, s, false);
+    s = __builtin_amdgcn_sdot4(qv[c].y, kv[c].y, s, false);
+    s = __builtin_amdgcn_sdot4(qv[c].z, kv[c].z, s, false);
+    s = __builtin_amdgcn_sdot4(qv[c].w, kv[c].w, s, false);
   }
   return s;
 }
 
+// sum over the lanes of a 16-lane row that share lane % DC (DC divides 16)
+template <int DC>
+__device__ __forceinline__ int32_t row_fold(int32_t v) {
+  if constexpr (DC <= 1) v += dpp_mov<DPP_ROW_ROR + 1>(v);
+  if constexpr (DC <= 2) v += dpp_mov<DPP_ROW_ROR + 2>(v);
+  if constexpr (DC <= 4) v += dpp_mov<DPP_ROW_ROR + 4>(v);
+  if constexpr (DC <= 8) v += dpp_mov<DPP_ROW_ROR + 8>(v);
+  return v;
+}
+
+// exp LUTs staged in LDS: kExpI (16 u16 = 8 dwords) then kExpF (256 u16 = 128 dwords)
+constexpr int LUT_DW = 136;
+
+__device__ __forceinline__ uint32_t lut_prob_lds(int64_t z, const uint16_t* ei, const uint16_t* ef) {
+  if (z >= 4096 || z < 0) return 0u;
+  const uint32_t zi = (uint32_t)z;
+  return ((uint32_t)ei[zi >> 8] * (uint32_t)ef[zi & 255] + 32768u) >> 16;
+}
+
+// Loads at entry, in order of use: q and the keys of the first score pass, the LUT dwords (wave
+// 0), then the value rows of this thread's first VPF keys, so each phase waits only for its own
+// group and the value latency hides behind the score and softmax phases.  Keys >= T read zeros.
 template <int D>
 __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   extern __shared__ int32_t sc[];  // [lds_T] scores, then probabilities
-  __shared__ int32_t red[ATTN_WAVES];
-  __shared__ int32_t wpart[ATTN_WAVES][D];
+  __shared__ int32_t redmax[ATTN_WAVES], redsum[ATTN_WAVES];
+  __shared__ uint32_t lut32[LUT_DW];
+  __shared__ int32_t wpart[4 * ATTN_WAVES][D];
   constexpr int DC = D / 16;  // 16-byte chunks per key row
   constexpr int TG = ATTN_THREADS / DC;
+  constexpr int VPF = 8;
 
   const int h = blockIdx.x;
   const int m = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int pos0 = p.pos_dev ? *p.pos_dev : p.pos;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int pos0 = load_pos(p.pos_dev, p.pos);
   const int T = pos0 + m + 1;
   const int g = h / (p.H / p.Hkv);
-  const int8_t* K = p.kc + (int64_t)g * p.max_seq * D;
-  const int8_t* V = p.vc + (int64_t)g * p.max_seq * D;
-  const int8_t* qr = p.q + (int64_t)m * p.ldq + (int64_t)h * D;
+  const Rsrc kr = rsrc(p.kc + (int64_t)g * p.max_seq * D, (int64_t)T * D);
+  const Rsrc vr = rsrc(p.vc + (int64_t)g * p.max_seq * D, (int64_t)T * D);
+  const Rsrc qr = rsrc(p.q + (int64_t)m * p.ldq + (int64_t)h * D, D);
 
-  // value rows of this thread's first VPF keys, loaded at entry so the value pass finds
-  // them in registers (their latency overlaps the score and softmax phases)
-  constexpr int VPF = 8;
+  v4i qv[DC], k0[DC], k1[DC];
+  const int t0 = tid, t1 = tid + ATTN_THREADS;
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    qv[c] = ld16(qr, 16 * c);
+    k0[c] = ld16(kr, (uint32_t)(t0 * D + 16 * c));
+    k1[c] = ld16(kr, (uint32_t)(t1 * D + 16 * c));
+  }
+  issue_fence();
+  uint32_t lw[3];
+  {
+    const Rsrc ir = rsrc(kExpI, sizeof(kExpI)), fr = rsrc(kExpF, sizeof(kExpF));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int idx = lane + 64 * i;
+      const bool mine = wave == 0 && idx < LUT_DW;
+      // one of the two reads is out of range (zero)
+      lw[i] = (uint32_t)ld4(ir, mine && idx < 8 ? 4 * idx : LD_OOB) |
+              (uint32_t)ld4(fr, mine && idx >= 8 ? 4 * (idx - 8) : LD_OOB);
+    }
+  }
+  issue_fence();
   const int dc = tid % DC, tg = tid / DC;
   v4i vpre[VPF];
 #pragma unroll
-  for (int u = 0; u < VPF; ++u) {
-    const int t = tg + u * TG;
-    vpre[u] = t < T ? *reinterpret_cast<const v4i*>(V + (int64_t)t * D + 16 * dc) : v4i{0, 0, 0, 0};
-  }
+  for (int u = 0; u < VPF; ++u) vpre[u] = ld16(vr, (uint32_t)((tg + u * TG) * D + 16 * dc));
+  issue_fence();
 
-  // scores s[t] = q . k[t] (int32, |s| <= D * 2^14), two keys in flight per thread
-  v4i qv[DC];
-#pragma unroll
-  for (int c = 0; c < DC; ++c) qv[c] = *reinterpret_cast<const v4i*>(qr + 16 * c);
+  // scores s[t] = q . k[t] (int32, |s| <= D * 2^14)
   int32_t lmax = INT32_MIN;
-  for (int t0 = tid; t0 < T; t0 += 2 * ATTN_THREADS) {
-    const int t1 = t0 + ATTN_THREADS;
-    const int32_t s0 = dot_row<D>(qv, reinterpret_cast<const v4i*>(K + (int64_t)t0 * D));
-    int32_t s1 = INT32_MIN;
-    if (t1 < T) s1 = dot_row<D>(qv, reinterpret_cast<const v4i*>(K + (int64_t)t1 * D));
-    sc[t0] = s0;
-    if (t1 < T) sc[t1] = s1;
-    lmax = max(lmax, max(s0, s1));
+  {
+    const int32_t s0 = dot_row<D>(qv, k0), s1 = dot_row<D>(qv, k1);
+    if (t0 < T) {
+      sc[t0] = s0;
+      lmax = s0;
+    }
+    if (t1 < T) {
+      sc[t1] = s1;
+      lmax = max(lmax, s1);
+    }
   }
-  const int32_t mx = block_max_i32(lmax, red);
+  for (int ta = tid + 2 * ATTN_THREADS; ta < T; ta += 2 * ATTN_THREADS) {
+    const int tb = ta + ATTN_THREADS;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      k0[c] = ld16(kr, (uint32_t)(ta * D + 16 * c));
+      k1[c] = ld16(kr, (uint32_t)(tb * D + 16 * c));
+    }
+    const int32_t s0 = dot_row<D>(qv, k0), s1 = dot_row<D>(qv, k1);
+    sc[ta] = s0;
+    lmax = max(lmax, s0);
+    if (tb < T) {
+      sc[tb] = s1;
+      lmax = max(lmax, s1);
+    }
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (lane + 64 * i < LUT_DW) lut32[lane + 64 * i] = lw[i];
+  }
+  lmax = wave_max_i32(lmax);
+  if (lane == 0) redmax[wave] = lmax;
+  __syncthreads();
+  int32_t mx = redmax[0];
+#pragma unroll
+  for (int w = 1; w < ATTN_WAVES; ++w) mx = max(mx, redmax[w]);
 
   // p[t] = LUT(mulshift(mx - s[t], Ms, Ss)), then the sum
+  const uint16_t* ei = reinterpret_cast<const uint16_t*>(lut32);
+  const uint16_t* ef = ei + 16;
   uint32_t lsum = 0;
   for (int t = tid; t < T; t += ATTN_THREADS) {
-    const uint32_t pr = lut_prob(mulshift((int64_t)mx - sc[t], p.Ms, p.Ss));
+    const uint32_t pr = lut_prob_lds(mulshift((int64_t)mx - sc[t], p.Ms, p.Ss), ei, ef);
     sc[t] = (int32_t)pr;
     lsum += pr;
   }
-  const uint32_t total = block_sum_u32(lsum, red);
-  const uint32_t inv = (uint32_t)((1ull << 31) / (uint64_t)(total > 1u ? total : 1u));
+  lsum = (uint32_t)wave_sum_i32((int)lsum);  // T * 65535 < 2^31
+  if (lane == 0) redsum[wave] = (int32_t)lsum;
+  __syncthreads();
+  uint32_t total = 0;
+#pragma unroll
+  for (int w = 0; w < ATTN_WAVES; ++w) total += (uint32_t)redsum[w];
+  const uint32_t inv = 0x80000000u / (total > 1u ? total : 1u);  // 2^31 / total (golden.py:174)
   const int32_t cap = (1 << p.pb) - 1;
   const int shp = 31 - p.pb;
   for (int t = tid; t < T; t += ATTN_THREADS) {
@@ -157,15 +204,14 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
       acc[12 + i] += pn * sbyte(vpre[u].w, i);
     }
   }
-  for (int t0 = tg + VPF * TG; t0 < T; t0 += 4 * TG) {
+  for (int ta = tg + VPF * TG; ta < T; ta += 4 * TG) {
     v4i vv[4];
     int32_t pn[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int t = t0 + u * TG;
-      const bool ok = t < T;
-      vv[u] = ok ? *reinterpret_cast<const v4i*>(V + (int64_t)t * D + 16 * dc) : v4i{0, 0, 0, 0};
-      pn[u] = ok ? sc[t] : 0;
+      const int t = ta + u * TG;
+      vv[u] = ld16(vr, (uint32_t)(t * D + 16 * dc));
+      pn[u] = t < T ? sc[t] : 0;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -177,21 +223,19 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
         acc[12 + i] += pn[u] * sbyte(vv[u].w, i);
       }
   }
-  // lanes l and l ^ (DC * j) hold the same 16 columns: fold them, then across waves in LDS
+  // the lanes of a 16-lane row with equal lane % DC hold the same 16 columns: fold them with
+  // row rotations, then the 4 rows x ATTN_WAVES partials in LDS
 #pragma unroll
-  for (int off = DC; off < 64; off <<= 1)
+  for (int i = 0; i < 16; ++i) acc[i] = row_fold<DC>(acc[i]);
+  if ((lane & 15) < DC) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] += __shfl_xor(acc[i], off);
-  const int lane = tid & 63, wave = tid >> 6;
-  if (lane < DC) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) wpart[wave][16 * lane + i] = acc[i];
+    for (int i = 0; i < 16; ++i) wpart[wave * 4 + (lane >> 4)][16 * (lane & 15) + i] = acc[i];
   }
   __syncthreads();
   for (int d = tid; d < D; d += ATTN_THREADS) {
     int32_t o = 0;
 #pragma unroll
-    for (int w = 0; w < ATTN_WAVES; ++w) o += wpart[w][d];
+    for (int w = 0; w < 4 * ATTN_WAVES; ++w) o += wpart[w][d];
     if (p.pb == 15) o = rshr32(o, 7);
     p.out[(int64_t)m * p.ldo + (int64_t)h * D + d] = (int8_t)sat8(mulshift(o, p.Mo, p.So));
   }
@@ -206,7 +250,7 @@ __global__ void kv_write_kernel(const int8_t* __restrict__ k, const int8_t* __re
   const int64_t m = idx / per_row;
   const int rem = (int)(idx % per_row);
   const int h = rem / D, d = rem % D;
-  const int p0 = pos_dev ? *pos_dev : pos;
+  const int p0 = load_pos(pos_dev, pos);
   const int64_t dst = ((int64_t)h * max_seq + p0 + m) * D + d;
   kc[dst] = k[m * ldk + rem];
   vc[dst] = v[m * ldv + rem];

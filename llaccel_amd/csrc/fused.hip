@@ -16,14 +16,20 @@
 //            FFN columns computes the gate and the up tile of those columns.
 //  norm_gemv: rmsnorm -> quant -> linear (any epilogue), e.g. the final norm + lm_head.
 //
-// No workgroup depends on another inside a launch (no device-scope synchronisation).
+// Decode launches are latency-bound (M = 1, a few MB of weights), so every kernel issues all of
+// its independent loads at entry in the order they are needed -- RMSNorm operands, LUTs, the
+// weight slice, the epilogue operands -- as branch-free buffer loads (out-of-range lanes read
+// zeros), and waits for each group only where it is used: the RMSNorm prologue runs while the
+// weights are in flight.  No workgroup depends on another inside a launch (no device-scope
+// synchronisation).
 #include "../../include/llhip.h"
 #include "common.h"
 
 namespace llhip {
 
-constexpr int FUSED_MAX_WAVES = 16;
-
+// ---------------------------------------------------------------------------------------
+// RMSNorm + quant prologue (golden.py:124-137, 119-120)
+// ---------------------------------------------------------------------------------------
 struct NormQuant {
   const int16_t* x;
   const int16_t* gamma;
@@ -35,103 +41,186 @@ struct NormQuant {
   int sh_post, Sq, K;
 };
 
-// RMSNorm + quant of M rows (K % 8 == 0) into LDS rows of stride lda bytes (golden.py:124-137,
-// 119-120).  Wave w takes rows w, w + nw, ...
-__device__ void norm_quant_rows(const NormQuant& pr, int M, int8_t* a_lds, int lda, bool write_global) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int nch = pr.K >> 3;
-  const v4i* gv = reinterpret_cast<const v4i*>(pr.gamma);
-  for (int m = wave; m < M; m += nw) {
-    const v4i* xv = reinterpret_cast<const v4i*>(pr.x + (int64_t)m * pr.ldx);
-    uint64_t ss = 0;
-    for (int c0 = lane; c0 < nch; c0 += 128) {
-      const int c1 = c0 + 64;
-      const v4i b0 = xv[c0];
-      const v4i b1 = c1 < nch ? xv[c1] : v4i{0, 0, 0, 0};
+constexpr int NORM_MAX_K = 1024;  // a row's sum of squares takes chunks lane and lane + 64
+
+// Rows and 4-element output units of this wave.  With M < nw several waves share a row: each
+// computes the row's sum of squares (the row is 2 KiB at most) and applies the scale to its own
+// units, so no cross-wave reduction is needed.  With M >= nw wave w takes rows w, w + nw, ...
+struct NormMap {
+  int m0, step, j, G;  // rows m0, m0 + step, ...; units j*64 + lane + i*G*64
+};
+
+__device__ __forceinline__ NormMap norm_map(int M) {
+  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  NormMap r;
+  r.m0 = wave % M;
+  if (M < nw) {
+    r.step = M;
+    r.j = wave / M;
+    r.G = (nw - r.m0 + M - 1) / M;
+  } else {
+    r.step = nw;
+    r.j = 0;
+    r.G = 1;
+  }
+  return r;
+}
+
+// operands of the wave's first row, loaded at kernel entry
+struct NormRegs {
+  v4i xs[2];  // 8-element chunks lane and lane + 64 (sum of squares)
+  v2i xu, gu; // x and gamma of the first output unit
+};
+
+__device__ __forceinline__ void norm_prefetch(const NormQuant& pr, int M, const NormMap& nm, NormRegs& r) {
+  const int lane = threadIdx.x & 63, nch = pr.K >> 3, nu = pr.K >> 2;
+  const Rsrc xr = rsrc(pr.x, (int64_t)M * pr.ldx * 2), gr = rsrc(pr.gamma, (int64_t)pr.K * 2);
+  const uint32_t row = (uint32_t)(nm.m0 * pr.ldx * 2);
+  r.xs[0] = ld16(xr, lane < nch ? row + 16 * lane : LD_OOB);
+  r.xs[1] = ld16(xr, lane + 64 < nch ? row + 16 * (lane + 64) : LD_OOB);
+  const int u = nm.j * 64 + lane;
+  r.xu = ld8(xr, u < nu ? row + 8 * u : LD_OOB);
+  r.gu = ld8(gr, u < nu ? 8 * u : LD_OOB);
+}
+
+__device__ __forceinline__ uint32_t norm_row_inv(const NormQuant& pr, const v4i& xs0, const v4i& xs1) {
+  uint64_t ss = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int32_t a = lo16(b0[j]), c = hi16(b0[j]);
-        ss += (uint64_t)(uint32_t)(a * a) + (uint64_t)(uint32_t)(c * c);
-        a = lo16(b1[j]);
-        c = hi16(b1[j]);
-        ss += (uint64_t)(uint32_t)(a * a) + (uint64_t)(uint32_t)(c * c);
-      }
+  for (int j = 0; j < 4; ++j) {
+    int32_t a = lo16(xs0[j]), c = hi16(xs0[j]);
+    ss += (uint32_t)(a * a) + (uint32_t)(c * c);  // each square <= 2^30: the pair fits u32
+    a = lo16(xs1[j]);
+    c = hi16(xs1[j]);
+    ss += (uint32_t)(a * a) + (uint32_t)(c * c);
+  }
+  return rms_inv(wave_sum_u64(ss), pr.eps_t, pr.C);
+}
+
+// normalise + quantise output unit u (elements 4u..4u+3) of row m
+__device__ __forceinline__ void norm_apply_unit(const NormQuant& pr, int m, int u, uint32_t inv, const v2i& xu,
+                                                const v2i& gu, int8_t* a_lds, int lda, bool write_global) {
+  if (u >= (pr.K >> 2)) return;
+  const int16_t y0 = rms_apply(lo16(xu.x), lo16(gu.x), inv, pr.sh_post);
+  const int16_t y1 = rms_apply(hi16(xu.x), hi16(gu.x), inv, pr.sh_post);
+  const int16_t y2 = rms_apply(lo16(xu.y), lo16(gu.y), inv, pr.sh_post);
+  const int16_t y3 = rms_apply(hi16(xu.y), hi16(gu.y), inv, pr.sh_post);
+  const uint32_t q = (uint32_t)(uint8_t)sat8(mulshift(y0, pr.Mq, pr.Sq)) |
+                     ((uint32_t)(uint8_t)sat8(mulshift(y1, pr.Mq, pr.Sq)) << 8) |
+                     ((uint32_t)(uint8_t)sat8(mulshift(y2, pr.Mq, pr.Sq)) << 16) |
+                     ((uint32_t)(uint8_t)sat8(mulshift(y3, pr.Mq, pr.Sq)) << 24);
+  *reinterpret_cast<uint32_t*>(a_lds + m * lda + 4 * u) = q;
+  if (write_global) {
+    if (pr.h_out) {
+      v2i y;
+      y.x = pack16(y0, y1);
+      y.y = pack16(y2, y3);
+      *reinterpret_cast<v2i*>(pr.h_out + (int64_t)m * pr.ldx + 4 * u) = y;
     }
-    ss = wave_sum_u64(ss);
-    const uint32_t inv = rms_inv(ss, pr.eps_t, pr.C);
-    for (int c = lane; c < nch; c += 64) {
-      const v4i b = xv[c], g = gv[c];
-      v4i y;
-      uint32_t qw[2] = {0u, 0u};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int16_t y0 = rms_apply(lo16(b[j]), lo16(g[j]), inv, pr.sh_post);
-        const int16_t y1 = rms_apply(hi16(b[j]), hi16(g[j]), inv, pr.sh_post);
-        y[j] = pack16(y0, y1);
-        const uint32_t q0 = (uint8_t)sat8(mulshift(y0, pr.Mq, pr.Sq));
-        const uint32_t q1 = (uint8_t)sat8(mulshift(y1, pr.Mq, pr.Sq));
-        qw[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
-      }
-      int2 q2;
-      q2.x = (int)qw[0];
-      q2.y = (int)qw[1];
-      *reinterpret_cast<int2*>(a_lds + m * lda + 8 * c) = q2;
-      if (write_global) {
-        if (pr.h_out) *reinterpret_cast<v4i*>(pr.h_out + (int64_t)m * pr.ldx + 8 * c) = y;
-        if (pr.hq_out) *reinterpret_cast<int2*>(pr.hq_out + (int64_t)m * pr.K + 8 * c) = q2;
-      }
+    if (pr.hq_out) *reinterpret_cast<uint32_t*>(pr.hq_out + (int64_t)m * pr.K + 4 * u) = q;
+  }
+}
+
+// The wave's first row and first unit use the registers loaded at entry in straight-line code,
+// so their waits cover those loads only; further rows and units (M > waves, or K > 256 * waves
+// sharing a row) load inside loops.
+__device__ void norm_quant_rows(const NormQuant& pr, const NormRegs& r, int M, const NormMap& nm, int8_t* a_lds,
+                                int lda, bool write_global) {
+  const int lane = threadIdx.x & 63, nch = pr.K >> 3, nu = pr.K >> 2;
+  const Rsrc xr = rsrc(pr.x, (int64_t)M * pr.ldx * 2), gr = rsrc(pr.gamma, (int64_t)pr.K * 2);
+  const int ustep = nm.G * 64;
+  {
+    const int m = nm.m0;
+    const uint32_t row = (uint32_t)(m * pr.ldx * 2);
+    const uint32_t inv = norm_row_inv(pr, r.xs[0], r.xs[1]);
+    norm_apply_unit(pr, m, nm.j * 64 + lane, inv, r.xu, r.gu, a_lds, lda, write_global);
+    for (int u0 = nm.j * 64 + ustep; u0 < nu; u0 += ustep) {
+      const int u = u0 + lane;
+      const v2i xu = ld8(xr, u < nu ? row + 8 * u : LD_OOB), gu = ld8(gr, u < nu ? 8 * u : LD_OOB);
+      norm_apply_unit(pr, m, u, inv, xu, gu, a_lds, lda, write_global);
+    }
+  }
+  for (int m = nm.m0 + nm.step; m < M; m += nm.step) {
+    const uint32_t row = (uint32_t)(m * pr.ldx * 2);
+    const v4i xs0 = ld16(xr, lane < nch ? row + 16 * lane : LD_OOB);
+    const v4i xs1 = ld16(xr, lane + 64 < nch ? row + 16 * (lane + 64) : LD_OOB);
+    const uint32_t inv = norm_row_inv(pr, xs0, xs1);
+    for (int u0 = nm.j * 64; u0 < nu; u0 += ustep) {
+      const int u = u0 + lane;
+      const v2i xu = ld8(xr, u < nu ? row + 8 * u : LD_OOB), gu = ld8(gr, u < nu ? 8 * u : LD_OOB);
+      norm_apply_unit(pr, m, u, inv, xu, gu, a_lds, lda, write_global);
     }
   }
 }
 
-// W operand of a wave's K slice: the first PF 16-byte chunks are loaded into registers at kernel
-// entry (before the RMSNorm prologue) so their HBM latency overlaps it; longer slices stream the rest.
+// SIG table (258 u16 = 129 dwords) staged into LDS by wave 0: three dword loads per lane at
+// kernel entry, stored once the prologue waits anyway
+struct SigRegs {
+  uint32_t w[3];
+};
+
+__device__ __forceinline__ void sig_prefetch(SigRegs& r) {
+  const int tid = threadIdx.x;
+  const Rsrc sr = rsrc(kSig, sizeof(kSig));
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int idx = tid + 64 * i;
+    r.w[i] = (uint32_t)ld4(sr, (tid < 64 && idx < 129) ? 4 * idx : LD_OOB);
+  }
+}
+
+__device__ __forceinline__ void sig_store(const SigRegs& r, uint32_t* sig32) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (tid + 64 * i < 129) sig32[tid + 64 * i] = r.w[i];
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// weight slices: W [N][K] i8, 16 columns x one wave's K steps
+// ---------------------------------------------------------------------------------------
+// The first PF 64-deep K steps of a wave's slice are loaded at kernel entry; longer slices stream
+// the rest four steps at a time.  Lane (col, kg) holds K bytes [s*64 + kg*16, +16) of column col.
 constexpr int PF = 8;
 
 struct WSlice {
   v4i w[PF];
-  const int8_t* row;
-  int s0, s1, kg, K;
-  bool nvalid;
+  uint32_t rowoff;
+  int s0, s1, kg;
 };
 
-__device__ __forceinline__ void wslice_prefetch(WSlice& ws, const int8_t* __restrict__ wrow, bool nvalid, int K, int kg,
-                                                int s0, int s1) {
-  ws.row = wrow;
+__device__ __forceinline__ void wslice_prefetch(WSlice& ws, Rsrc wr, int n, int K, int kg, int s0, int s1) {
+  ws.rowoff = (uint32_t)n * (uint32_t)K;  // rows n >= N fall past the range and read zeros
   ws.s0 = s0;
   ws.s1 = s1;
   ws.kg = kg;
-  ws.K = K;
-  ws.nvalid = nvalid;
 #pragma unroll
   for (int u = 0; u < PF; ++u) {
     const int k = (s0 + u) * 64 + kg * 16;
-    ws.w[u] = (nvalid && s0 + u < s1 && k < K) ? *reinterpret_cast<const v4i*>(wrow + k) : v4i{0, 0, 0, 0};
+    ws.w[u] = ld16(wr, (s0 + u < s1 && k < K) ? ws.rowoff + k : LD_OOB);
   }
 }
 
-// 16x16 partial tile of the slice with A rows from LDS (rows >= M are zeros)
-__device__ __forceinline__ v4i wslice_mfma(const WSlice& ws, const int8_t* a_lds, int lda, int M) {
+// 16x16 partial tile of the slice; A rows from LDS.  A rows >= M are read from row M - 1: output
+// row m depends only on A row m, so those rows only produce discarded outputs.  Steps past the
+// slice have zero weights, so their A reads only need to stay inside the LDS rows.
+__device__ __forceinline__ v4i wslice_mfma(const WSlice& ws, Rsrc wr, const int8_t* a_lds, int lda, int M, int K) {
   const int lane = threadIdx.x & 63;
-  const int m = lane & 15;
-  const bool avalid = m < M;
-  const int8_t* arow = a_lds + m * lda;
+  const int8_t* arow = a_lds + min(lane & 15, M - 1) * lda;
   v4i acc = {0, 0, 0, 0};
 #pragma unroll
   for (int u = 0; u < PF; ++u) {
-    const int k = (ws.s0 + u) * 64 + ws.kg * 16;
-    const bool ok = ws.s0 + u < ws.s1 && k < ws.K;
-    const v4i a = (avalid && ok) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
-    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ws.w[u], acc, 0, 0, 0);
+    const int k = min((ws.s0 + u) * 64 + ws.kg * 16, K - 16);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const v4i*>(arow + k), ws.w[u], acc, 0, 0, 0);
   }
   for (int s = ws.s0 + PF; s < ws.s1; s += 4) {
     v4i b[4], a[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int k = (s + u) * 64 + ws.kg * 16;
-      const bool ok = s + u < ws.s1 && k < ws.K;
-      b[u] = (ws.nvalid && ok) ? *reinterpret_cast<const v4i*>(ws.row + k) : v4i{0, 0, 0, 0};
-      a[u] = (avalid && ok) ? *reinterpret_cast<const v4i*>(arow + k) : v4i{0, 0, 0, 0};
+      b[u] = ld16(wr, (s + u < ws.s1 && k < K) ? ws.rowoff + k : LD_OOB);
+      a[u] = *reinterpret_cast<const v4i*>(arow + min(k, K - 16));
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
@@ -176,9 +265,18 @@ struct AttnInArgs {
   int M, H, Hkv, D, K, pos, KS, has_norm;
 };
 
-__global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArgs p) {
+// per-role kernel arguments chosen by scalar selects of the three values (an indexed read of the
+// argument array would wait on the role before the load could issue)
+template <class T>
+__device__ __forceinline__ T pick3(int role, const T (&v)[3]) {
+  const T a = v[0], b = v[1], c = v[2];
+  return role == 0 ? a : (role == 1 ? b : c);
+}
+
+template <int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
-  __shared__ v4i red[FUSED_MAX_WAVES][64];
+  __shared__ v4i red[MAXW][64];
   const int lda = p.K + 16;
   int8_t* a_lds = dyn;                                                         // [M][lda] i8
   int32_t* hres = reinterpret_cast<int32_t*>(dyn + ((p.M * lda + 15) & ~15));  // [M][D] i32
@@ -189,34 +287,52 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArg
   const int D = p.D, M = p.M;
   const int Nrole = (role == 0 ? p.H : p.Hkv) * D;
   const int base = hh * D;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int tiles = D >> 4;
-  const int pos0 = p.pos_dev ? *p.pos_dev : p.pos;
+  const int pos0 = load_pos(p.pos_dev, p.pos);
 
-  // kernel entry: weight slice and the epilogue operands of this thread's column
+  // kernel entry, in order of use: RMSNorm operands, weight slice, epilogue operands of this
+  // thread's column, head-norm gamma, RoPE factors
+  const NormMap nm = norm_map(M);
+  NormRegs nr;
+  norm_prefetch(p.pre, M, nm, nr);
+  issue_fence();
+  const Rsrc wr = rsrc(pick3(role, p.W), (int64_t)Nrole * p.K);
   WSlice ws;
   {
     const int t = wave % tiles, ks = wave / tiles;
     int s0, s1;
     split_range((p.K + 63) >> 6, p.KS, ks, s0, s1);
-    const int n = base + t * 16 + (lane & 15);
-    wslice_prefetch(ws, p.W[role] + (int64_t)n * p.K, true, p.K, lane >> 4, s0, s1);
+    wslice_prefetch(ws, wr, base + t * 16 + (lane & 15), p.K, lane >> 4, s0, s1);
   }
+  issue_fence();
   const int dcol = tid % D;  // blockDim is a multiple of D: each thread owns one column in the tail
   const int ncol = base + dcol;
-  const int32_t rq_m = p.rq[role][2 * ncol], rq_s = p.rq[role][2 * ncol + 1];
-  const int32_t bias = p.bias[role] ? p.bias[role][ncol] : 0;
+  const v2i rq = ld8(rsrc(pick3(role, p.rq), (int64_t)Nrole * 8), 8 * ncol);
+  const int32_t bias = ld4(rsrc(pick3(role, p.bias), (int64_t)Nrole * 4), 4 * ncol);
+  const bool hn = p.has_norm && role < 2;
+  int32_t hg[4];  // head-norm gamma of dims lane + 64 i (the per-row norm runs wave-wide)
+  {
+    const Rsrc gr = rsrc(hn ? (role == 0 ? p.nrm_gamma[0] : p.nrm_gamma[1]) : nullptr, (int64_t)D * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hg[i] = ld2s(gr, lane + 64 * i < D ? 2 * (lane + 64 * i) : LD_OOB);
+  }
+  issue_fence();
   const int half = D >> 1;
   const int jrope = tid % half, mrope = tid / half;
-  int64_t c0 = 0, s0r = 0;
-  if (role < 2 && mrope < M) {
-    c0 = p.cos_tab[(int64_t)(pos0 + mrope) * half + jrope];
-    s0r = p.sin_tab[(int64_t)(pos0 + mrope) * half + jrope];
+  int32_t c0 = 0, s0r = 0;
+  {
+    const bool rok = role < 2 && mrope < M;
+    const int64_t tab = (int64_t)p.max_seq * half * 2;
+    const uint32_t off = rok ? (uint32_t)(((int64_t)(pos0 + mrope) * half + jrope) * 2) : LD_OOB;
+    c0 = ld2s(rsrc(p.cos_tab, tab), off);
+    s0r = ld2s(rsrc(p.sin_tab, tab), off);
   }
+  issue_fence();
 
-  norm_quant_rows(p.pre, M, a_lds, lda, b == 0);
+  norm_quant_rows(p.pre, nr, M, nm, a_lds, lda, b == 0);
   __syncthreads();
-  red[wave][lane] = wslice_mfma(ws, a_lds, lda, M);
+  red[wave][lane] = wslice_mfma(ws, wr, a_lds, lda, M, p.K);
   __syncthreads();
   if (wave < tiles) {
     v4i acc = red[wave][lane];
@@ -233,7 +349,7 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArg
   const int rstep = blockDim.x / D;
   if (role == 2) {  // v: requant8 -> v activation and V cache
     for (int m = tid / D; m < M; m += rstep) {
-      const int8_t y = (int8_t)sat8(mulshift((int64_t)hres[m * D + dcol] + bias, rq_m, rq_s));
+      const int8_t y = (int8_t)sat8(mulshift((int64_t)hres[m * D + dcol] + bias, rq.x, rq.y));
       static_cast<int8_t*>(p.lin_out[2])[(int64_t)m * Nrole + ncol] = y;
       p.vc[((int64_t)hh * p.max_seq + pos0 + m) * D + dcol] = y;
     }
@@ -241,21 +357,23 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void attn_in_kernel(AttnInArg
   }
   // q / k: requant16 -> activation; head values kept in hres as int32
   for (int m = tid / D; m < M; m += rstep) {
-    const int16_t y = (int16_t)sat16(mulshift((int64_t)hres[m * D + dcol] + bias, rq_m, rq_s));
+    const int16_t y = (int16_t)sat16(mulshift((int64_t)hres[m * D + dcol] + bias, rq.x, rq.y));
     static_cast<int16_t*>(p.lin_out[role])[(int64_t)m * Nrole + ncol] = y;
     hres[m * D + dcol] = y;
   }
   __syncthreads();
-  if (p.has_norm) {  // RMSNorm over each D-wide head (golden.py:287-293, heads > 1)
-    const int16_t* g = p.nrm_gamma[role];
+  if (hn) {  // RMSNorm over each D-wide head (golden.py:287-293, heads > 1)
     const int nw = blockDim.x >> 6;
     for (int m = wave; m < M; m += nw) {
       uint64_t ss = 0;
       for (int d = lane; d < D; d += 64) ss += (uint64_t)(uint32_t)(hres[m * D + d] * hres[m * D + d]);
       ss = wave_sum_u64(ss);
       const uint32_t inv = rms_inv(ss, (uint32_t)p.nrm_eps[role], (uint32_t)p.nrm_C[role]);
-      for (int d = lane; d < D; d += 64) {
-        const int16_t y = rms_apply(hres[m * D + d], g[d], inv, (int)p.nrm_sh[role]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = lane + 64 * i;
+        if (d >= D) break;
+        const int16_t y = rms_apply(hres[m * D + d], hg[i], inv, (int)p.nrm_sh[role]);
         p.nrm_out[role][(int64_t)m * Nrole + base + d] = y;
         hres[m * D + d] = y;
       }
@@ -309,51 +427,61 @@ struct MlpInArgs {
   int M, N, K, KS;
 };
 
-__global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void mlp_in_kernel(MlpInArgs p) {
+template <int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
-  __shared__ v4i red[FUSED_MAX_WAVES][64];
+  __shared__ v4i red[MAXW][64];
+  __shared__ uint32_t sig32[129];
   const int lda = p.K + 16;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int col = lane & 15, kg = lane >> 4;
   const int n = blockIdx.x * 16 + col;
-  const bool nvalid = n < p.N;
-  const int nn = nvalid ? n : 0;
+
+  const NormMap nm = norm_map(p.M);
+  NormRegs nr;
+  norm_prefetch(p.pre, p.M, nm, nr);
+  issue_fence();
+  SigRegs sr;
+  sig_prefetch(sr);
+  issue_fence();
+  const int up = wave >= p.KS;  // waves [0, KS): gate, [KS, 2KS): up
+  const Rsrc wr = rsrc(up ? p.Wu : p.Wg, (int64_t)p.N * p.K);
   WSlice ws;
   {
-    const int up = wave >= p.KS;  // waves [0, KS): gate, [KS, 2KS): up
     int s0, s1;
     split_range((p.K + 63) >> 6, p.KS, up ? wave - p.KS : wave, s0, s1);
-    wslice_prefetch(ws, (up ? p.Wu : p.Wg) + (int64_t)nn * p.K, nvalid, p.K, kg, s0, s1);
+    wslice_prefetch(ws, wr, n, p.K, kg, s0, s1);
   }
-  int32_t rg_m = 0, rg_s = 0, ru_m = 0, ru_s = 0, bgv = 0, buv = 0;
-  if (wave == 0) {
-    rg_m = p.rqg[2 * nn];
-    rg_s = p.rqg[2 * nn + 1];
-    ru_m = p.rqu[2 * nn];
-    ru_s = p.rqu[2 * nn + 1];
-    bgv = p.bg ? p.bg[nn] : 0;
-    buv = p.bu ? p.bu[nn] : 0;
-  }
-  norm_quant_rows(p.pre, p.M, dyn, lda, blockIdx.x == 0);
+  issue_fence();
+  const uint32_t o8 = n < p.N ? 8 * n : LD_OOB, o4 = n < p.N ? 4 * n : LD_OOB;
+  const v2i rg = ld8(rsrc(p.rqg, (int64_t)p.N * 8), o8);
+  const v2i ru = ld8(rsrc(p.rqu, (int64_t)p.N * 8), o8);
+  const int32_t bgv = ld4(rsrc(p.bg, (int64_t)p.N * 4), o4);
+  const int32_t buv = ld4(rsrc(p.bu, (int64_t)p.N * 4), o4);
+  issue_fence();
+
+  norm_quant_rows(p.pre, nr, p.M, nm, dyn, lda, blockIdx.x == 0);
+  sig_store(sr, sig32);
   __syncthreads();
-  red[wave][lane] = wslice_mfma(ws, dyn, lda, p.M);
+  red[wave][lane] = wslice_mfma(ws, wr, dyn, lda, p.M, p.K);
   __syncthreads();
-  if (wave != 0 || !nvalid) return;
+  if (wave != 0 || n >= p.N) return;
   v4i ag = red[0][lane], au = red[p.KS][lane];
   for (int ks = 1; ks < p.KS; ++ks) {
     v4_add(ag, red[ks][lane]);
     v4_add(au, red[p.KS + ks][lane]);
   }
+  const uint16_t* sig = reinterpret_cast<const uint16_t*>(sig32);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * kg + r;
     if (m >= p.M) continue;
     const int64_t o = (int64_t)m * p.N + n;
-    const int64_t tg = sat16(mulshift((int64_t)ag[r] + bgv, rg_m, rg_s));
-    const int64_t tu = sat16(mulshift((int64_t)au[r] + buv, ru_m, ru_s));
+    const int64_t tg = sat16(mulshift((int64_t)ag[r] + bgv, rg.x, rg.y));
+    const int64_t tu = sat16(mulshift((int64_t)au[r] + buv, ru.x, ru.y));
     if (p.g_out) p.g_out[o] = (int16_t)tg;
     if (p.u_out) p.u_out[o] = (int16_t)tu;
-    const int64_t sg = silu16(tg, p.silu_Mi, p.silu_Si, p.silu_sh);
+    const int64_t sg = silu16_lds(tg, p.silu_Mi, p.silu_Si, p.silu_sh, sig);
     const int64_t f = sat16(rshr(tu * sg, p.mul_sh));
     p.sg_out[o] = (int16_t)sg;
     p.f_out[o] = (int16_t)f;
@@ -377,48 +505,72 @@ struct NormGemvArgs {
   int M, N, K, KS, TPW;
 };
 
-__global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void norm_gemv_kernel(NormGemvArgs p) {
+template <int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
-  __shared__ v4i red[FUSED_MAX_WAVES][64];
+  __shared__ v4i red[MAXW][64];
+  __shared__ uint32_t sig32[129];
   const int lda = p.K + 16;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int col = lane & 15, kg = lane >> 4;
   const int t = wave % p.TPW, ks = wave / p.TPW;
   const int n = (blockIdx.x * p.TPW + t) * 16 + col;
-  const bool nvalid = n < p.N;
-  const int nn = nvalid ? n : 0;
+
+  const NormMap nm = norm_map(p.M);
+  NormRegs nr;
+  norm_prefetch(p.pre, p.M, nm, nr);
+  issue_fence();
+  SigRegs sr;
+  sig_prefetch(sr);
+  issue_fence();
+  const Rsrc wr = rsrc(p.W, (int64_t)p.N * p.K);
   WSlice ws;
   {
     int s0, s1;
     split_range((p.K + 63) >> 6, p.KS, ks, s0, s1);
-    wslice_prefetch(ws, p.W + (int64_t)nn * p.K, nvalid, p.K, kg, s0, s1);
+    wslice_prefetch(ws, wr, n, p.K, kg, s0, s1);
   }
-  const int32_t rq_m = p.rq[2 * nn], rq_s = p.rq[2 * nn + 1];
-  const int32_t bias = p.bias ? p.bias[nn] : 0;
-  norm_quant_rows(p.pre, p.M, dyn, lda, blockIdx.x == 0);
+  issue_fence();
+  const v2i rq = ld8(rsrc(p.rq, (int64_t)p.N * 8), n < p.N ? 8 * n : LD_OOB);
+  const int32_t bias = ld4(rsrc(p.bias, (int64_t)p.N * 4), n < p.N ? 4 * n : LD_OOB);
+  int32_t aux[4];
+  {
+    const bool use = p.epilogue == 1 || p.epilogue == 3;
+    const Rsrc ar = rsrc(use ? p.aux : nullptr, (int64_t)p.M * p.N * 2);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * kg + r;
+      aux[r] = ld2s(ar, (m < p.M && n < p.N) ? (uint32_t)(2 * ((int64_t)m * p.N + n)) : LD_OOB);
+    }
+  }
+  issue_fence();
+
+  norm_quant_rows(p.pre, nr, p.M, nm, dyn, lda, blockIdx.x == 0);
+  sig_store(sr, sig32);
   __syncthreads();
-  v4i acc = wslice_mfma(ws, dyn, lda, p.M);
+  v4i acc = wslice_mfma(ws, wr, dyn, lda, p.M, p.K);
   if (p.KS > 1) {
     red[wave][lane] = acc;
     __syncthreads();
     if (ks != 0) return;
     for (int j = 1; j < p.KS; ++j) v4_add(acc, red[t + j * p.TPW][lane]);
   }
-  if (!nvalid) return;
+  if (n >= p.N) return;
+  const uint16_t* sig = reinterpret_cast<const uint16_t*>(sig32);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * kg + r;
     if (m >= p.M) continue;
     const int64_t o = (int64_t)m * p.N + n;
-    const int64_t v = mulshift((int64_t)acc[r] + bias, rq_m, rq_s);
+    const int64_t v = mulshift((int64_t)acc[r] + bias, rq.x, rq.y);
     if (p.out_i8) {
       static_cast<int8_t*>(p.out)[o] = (int8_t)sat8(v);
       continue;
     }
     int64_t y = sat16(v);
-    if (p.epilogue == 1) y = sat16(y + p.aux[o]);
-    else if (p.epilogue == 2) y = silu16(y, p.Mi, p.Si, p.sh);
-    else if (p.epilogue == 3) y = sat16(rshr(y * p.aux[o], p.aux_shift));
+    if (p.epilogue == 1) y = sat16(y + aux[r]);
+    else if (p.epilogue == 2) y = silu16_lds(y, p.Mi, p.Si, p.sh, sig);
+    else if (p.epilogue == 3) y = sat16(rshr(y * aux[r], p.aux_shift));
     static_cast<int16_t*>(p.out)[o] = (int16_t)y;
   }
 }
@@ -427,7 +579,9 @@ __global__ __launch_bounds__(64 * FUSED_MAX_WAVES) void norm_gemv_kernel(NormGem
 // host side
 // ---------------------------------------------------------------------------------------
 static int fill_pre(NormQuant& pr, const llhip_norm_quant_desc& d) {
-  if (d.K <= 0 || d.K % 8 || d.ldx < d.K || d.ldx % 8) return fail(-EINVAL, "fused rmsnorm: K and ldx must be multiples of 8");
+  if (d.K <= 0 || d.K % 16 || d.ldx < d.K || d.ldx % 8)
+    return fail(-EINVAL, "fused rmsnorm: K must be a multiple of 16 and ldx of 8");
+  if (d.K > NORM_MAX_K) return fail(-EINVAL, "fused rmsnorm: K=%lld above %d", (long long)d.K, NORM_MAX_K);
   if (!u32_ok(d.eps_t) || !u32_ok(d.C) || !shift_ok(d.sh_post) || !u32_ok(d.Mq) || !shift_ok(d.Sq))
     return fail(-EINVAL, "fused rmsnorm/quant parameter out of range");
   if (d.K >= (int64_t)((1ull << 48) - (1ull << 32)) >> 30) return fail(-ERANGE, "isqrt48 input out of range");
@@ -447,6 +601,13 @@ static int fill_pre(NormQuant& pr, const llhip_norm_quant_desc& d) {
   pr.K = (int)d.K;
   return 0;
 }
+
+// Waves per workgroup are capped at 8 (512 threads, 256 VGPRs per lane) unless one split
+// alone needs more (attn_in with D = 256): 16-wave workgroups leave 128 VGPRs per lane.
+constexpr int FUSED_WAVES = 8;
+
+// weight matrices are addressed with 32-bit buffer offsets
+static bool w_ok(int64_t N, int64_t K) { return N * K < (1ll << 31); }
 
 static int pick_ks(int64_t blocks, int per_split_waves, int steps, int max_waves) {
   const int target = 8 * current_cu_count();
@@ -508,11 +669,17 @@ extern "C" int llhip_attn_in(const llhip_attn_in_desc* d, void* stream) {
   p.has_norm = d->has_norm ? 1 : 0;
   const int tiles = (int)(D / 16);
   const int steps = (int)ceil_div(K, 64);
-  p.KS = pick_ks(H + 2 * Hkv, tiles, steps, FUSED_MAX_WAVES);
+  if (!w_ok(H * D, K) || d->max_seq * D >= (1ll << 31)) return fail(-EINVAL, "attn_in: operand above 2 GiB");
+  p.KS = pick_ks(H + 2 * Hkv, tiles, steps, tiles > FUSED_WAVES ? 16 : FUSED_WAVES);
   const size_t lds = (size_t)((M * (K + 16) + 15) & ~15) + sizeof(int32_t) * (size_t)(M * D);
   if (lds > 48 * 1024) return fail(-EINVAL, "attn_in: M*K too large for the LDS staging");
-  hipLaunchKernelGGL(attn_in_kernel, dim3((unsigned)(H + 2 * Hkv)), dim3(64 * tiles * p.KS), lds, (hipStream_t)stream,
-                     p);
+  const int waves = tiles * p.KS;
+  if (waves <= FUSED_WAVES)
+    hipLaunchKernelGGL(attn_in_kernel<FUSED_WAVES>, dim3((unsigned)(H + 2 * Hkv)), dim3(64 * waves), lds,
+                       (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(attn_in_kernel<16>, dim3((unsigned)(H + 2 * Hkv)), dim3(64 * waves), lds, (hipStream_t)stream,
+                       p);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
@@ -549,10 +716,12 @@ extern "C" int llhip_mlp_in(const llhip_mlp_in_desc* d, void* stream) {
   p.N = (int)N;
   p.K = (int)K;
   const int tiles = (int)ceil_div(N, 16);
-  p.KS = pick_ks(tiles, 2, (int)ceil_div(K, 64), FUSED_MAX_WAVES);
+  if (!w_ok(N, K)) return fail(-EINVAL, "mlp_in: weights above 2 GiB");
+  p.KS = pick_ks(tiles, 2, (int)ceil_div(K, 64), FUSED_WAVES);
   const size_t lds = (size_t)(M * (K + 16));
   if (lds > 48 * 1024) return fail(-EINVAL, "mlp_in: M*K too large for the LDS staging");
-  hipLaunchKernelGGL(mlp_in_kernel, dim3((unsigned)tiles), dim3(64 * 2 * p.KS), lds, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(mlp_in_kernel<FUSED_WAVES>, dim3((unsigned)tiles), dim3(64 * 2 * p.KS), lds, (hipStream_t)stream,
+                     p);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
@@ -586,13 +755,16 @@ extern "C" int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream) 
   p.K = (int)K;
   const int tiles = (int)ceil_div(N, 16);
   const int steps = (int)ceil_div(K, 64);
-  // wide outputs: several tiles per workgroup share one prologue; narrow ones split K
+  if (!w_ok(N, K) || M * N * 2 >= (1ll << 31)) return fail(-EINVAL, "norm_linear: operand above 2 GiB");
+  // wide outputs: several tiles per workgroup share one prologue, K split in two so every step of
+  // a wave's slice is loaded at entry; narrow ones split K further
   p.TPW = tiles >= 4096 ? 4 : 1;
-  p.KS = p.TPW == 1 ? pick_ks(tiles, 1, steps, FUSED_MAX_WAVES) : 1;
+  p.KS = p.TPW == 1 ? pick_ks(tiles, 1, steps, FUSED_WAVES) : (steps > PF ? 2 : 1);
   const int blocks = (int)ceil_div(tiles, p.TPW);
   const size_t lds = (size_t)(M * (K + 16));
   if (lds > 48 * 1024) return fail(-EINVAL, "norm_linear: M*K too large for the LDS staging");
-  hipLaunchKernelGGL(norm_gemv_kernel, dim3((unsigned)blocks), dim3(64 * p.TPW * p.KS), lds, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(norm_gemv_kernel<FUSED_WAVES>, dim3((unsigned)blocks), dim3(64 * p.TPW * p.KS), lds,
+                     (hipStream_t)stream, p);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }

@@ -201,6 +201,78 @@ __global__ __launch_bounds__(64 * GEMV_MAX_WAVES) void linear_gemv(LinearArgs p)
 }
 
 // ---------------------------------------------------------------------------------------
+// M = 1 with few output columns (decode projections): VALU dot products, one wave per CPW
+// columns, no LDS and no barrier
+// ---------------------------------------------------------------------------------------
+// With 16-column MFMA tiles an N = 896 projection has 56 workgroups, so a quarter of the CUs
+// carry all of its weight traffic.  Here lane l of a wave works on column l / LPC of the wave's
+// CPW = 64 / LPC columns and on the 16-byte K chunks l % LPC + i*LPC, with v_dot4_i32_i8; the
+// LPC partial sums of a column are folded with lane shuffles and its first lane applies the
+// epilogue.  Every load of a lane (up to G1_PF chunks of W and of A, and the epilogue operands)
+// is issued at entry.
+constexpr int G1_PF = 8;
+
+template <int EPI, bool OUT8, int LPC>
+__global__ __launch_bounds__(64) void linear_gemv1(LinearArgs p) {
+  constexpr int CPW = 64 / LPC;
+  const int lane = threadIdx.x;
+  const int c = lane / LPC, j = lane % LPC;
+  const int n = blockIdx.x * CPW + c;
+  const int nch = p.K >> 4;
+  const Rsrc wr = rsrc(p.W, (int64_t)p.N * p.K), ar = rsrc(p.A, p.K);
+  const uint32_t row = (uint32_t)n * (uint32_t)p.K;  // columns n >= N read zeros
+  v4i w[G1_PF], a[G1_PF];
+#pragma unroll
+  for (int u = 0; u < G1_PF; ++u) {
+    const int ch = j + u * LPC;
+    w[u] = ld16(wr, ch < nch ? row + 16 * ch : LD_OOB);
+    a[u] = ld16(ar, ch < nch ? 16 * ch : LD_OOB);
+  }
+  issue_fence();
+  const bool lead = j == 0 && n < p.N;
+  const v2i rq = ld8(rsrc(p.rq, (int64_t)p.N * 8), lead ? 8 * n : LD_OOB);
+  const int32_t bias = ld4(rsrc(p.bias, (int64_t)p.N * 4), lead ? 4 * n : LD_OOB);
+  const int32_t aux =
+      (EPI == EPI_RESADD || EPI == EPI_MUL) ? ld2s(rsrc(p.aux, (int64_t)p.N * 2), lead ? 2 * n : LD_OOB) : 0;
+  issue_fence();
+  int32_t acc = 0;
+#pragma unroll
+  for (int u = 0; u < G1_PF; ++u) {
+    acc = __builtin_amdgcn_sdot4(w[u].x, a[u].x, acc, false);
+    acc = __builtin_amdgcn_sdot4(w[u].y, a[u].y, acc, false);
+    acc = __builtin_amdgcn_sdot4(w[u].z, a[u].z, acc, false);
+    acc = __builtin_amdgcn_sdot4(w[u].w, a[u].w, acc, false);
+  }
+  for (int ch0 = G1_PF * LPC; ch0 < nch; ch0 += G1_PF * LPC) {
+#pragma unroll
+    for (int u = 0; u < G1_PF; ++u) {
+      const int ch = ch0 + j + u * LPC;
+      w[u] = ld16(wr, ch < nch ? row + 16 * ch : LD_OOB);
+      a[u] = ld16(ar, ch < nch ? 16 * ch : LD_OOB);
+    }
+#pragma unroll
+    for (int u = 0; u < G1_PF; ++u) {
+      acc = __builtin_amdgcn_sdot4(w[u].x, a[u].x, acc, false);
+      acc = __builtin_amdgcn_sdot4(w[u].y, a[u].y, acc, false);
+      acc = __builtin_amdgcn_sdot4(w[u].z, a[u].z, acc, false);
+      acc = __builtin_amdgcn_sdot4(w[u].w, a[u].w, acc, false);
+    }
+  }
+  acc = group_sum_i32<LPC>(acc);
+  if (!lead) return;
+  const int64_t v = mulshift((int64_t)acc + bias, rq.x, rq.y);
+  if (OUT8) {
+    static_cast<int8_t*>(p.out)[n] = (int8_t)sat8(v);
+    return;
+  }
+  int64_t t = sat16(v);
+  if (EPI == EPI_RESADD) t = sat16(t + aux);
+  else if (EPI == EPI_SILU) t = silu16(t, p.Mi, p.Si, p.sh);
+  else if (EPI == EPI_MUL) t = sat16(rshr(wmul(t, aux), p.aux_shift));
+  static_cast<int16_t*>(p.out)[n] = (int16_t)t;
+}
+
+// ---------------------------------------------------------------------------------------
 // M > 16: LDS-tiled MFMA GEMM (K % 16 == 0)
 // ---------------------------------------------------------------------------------------
 // Block = 2 x 2 waves; a wave owns a (32*WM) x (32*WN) tile of v_mfma_i32_32x32x32_i8 blocks.
@@ -363,8 +435,8 @@ __device__ __forceinline__ int32_t requant_col(int32_t acc, const ColRq& c) {
 __device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) { return min(max(v, lo), hi); }
 
 // ---------------------------------------------------------------------------------------
-// Large GEMM (M >= 128, K % 64 == 0): 256x256x64 block tile, 8 waves, 3-stage LDS ring fed by
-// direct global->LDS loads (global_load_lds_dwordx4)
+// Large GEMM (M >= 128, K % 64 == 0): GB x GB x 64 block tile (GB = 256 with 8 waves, 128 with 4),
+// 3-stage LDS ring fed by direct global->LDS loads (global_load_lds_dwordx4)
 // ---------------------------------------------------------------------------------------
 // Each wave instruction moves 64 x 16 B into 1 KiB of LDS (16 rows of 64 B).  Lane L of it
 // writes slot L of that KiB (row L/4, slot L%4) and fetches K chunk (L%4) ^ swz(row), so a row's
@@ -372,15 +444,26 @@ __device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) { 
 // K chunk then fall into distinct LDS banks without padding.  Tiles k+1 and k+2 are in flight
 // while tile k feeds the MFMAs.  Rows past M/N read a clamped valid row (their outputs are
 // discarded); K is a multiple of 64, so no K chunk is partial.
-constexpr int GB = 256;      // block tile rows (A) and columns (W)
 constexpr int GSTAGES = 3;
-constexpr int GSTAGE_BYTES = 2 * GB * 64;  // A + W of one K tile
 
 __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-template <int EPI, bool OUT8>
-__global__ __launch_bounds__(512) void linear_mfma(LinearArgs p, int mblocks, int nblocks) {
-  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A 256x64 | W 256x64]
+template <int GB, int NW>
+struct MfmaTile {
+  static constexpr int NT = 64 * NW;
+  static constexpr int STAGE_BYTES = 2 * GB * 64;     // A + W of one K tile
+  static constexpr int LDS_BYTES = GSTAGES * STAGE_BYTES;
+  static constexpr int WROWS = GB / 2;                // wave tile: 2 x NW/2 waves
+  static constexpr int WCOLS = 2 * GB / NW;
+  static constexpr int WM = WROWS / 32, WN = WCOLS / 32;  // 32x32 MFMA tiles per wave
+  static constexpr int LOADS = GB / (16 * NW);        // 1 KiB A (and W) loads per wave per stage
+  static_assert(LOADS == 2, "the vmcnt(4) wait assumes 2 A + 2 W loads per wave per stage");
+};
+
+template <int EPI, bool OUT8, int GB, int NW>
+__global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks) {
+  using T = MfmaTile<GB, NW>;
+  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A GBx64 | W GBx64]
   const int nb_total = mblocks * nblocks;
   const int b = blockIdx.x;
   int logical = b;
@@ -390,7 +473,7 @@ __global__ __launch_bounds__(512) void linear_mfma(LinearArgs p, int mblocks, in
   const int m0 = mb * GB, n0 = nbk * GB;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave & 1) * 128, wn = (wave >> 1) * 64;  // 2 x 4 waves, 128 x 64 each
+  const int wm = (wave & 1) * T::WROWS, wn = (wave >> 1) * T::WCOLS;
 
   // this lane's source rows for the two A and two W load instructions of a stage
   const int8_t* asrc[2];
@@ -404,7 +487,7 @@ __global__ __launch_bounds__(512) void linear_mfma(LinearArgs p, int mblocks, in
     wsrc[i] = p.W + (int64_t)gn * p.K + chunk * 16;
   }
   auto issue = [&](int kt) {
-    int8_t* st = ring + (kt % GSTAGES) * GSTAGE_BYTES;
+    int8_t* st = ring + (kt % GSTAGES) * T::STAGE_BYTES;
     const int k0 = kt * 64;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -413,11 +496,11 @@ __global__ __launch_bounds__(512) void linear_mfma(LinearArgs p, int mblocks, in
     }
   };
 
-  v16i acc[4][2];
+  v16i acc[T::WM][T::WN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < T::WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+    for (int j = 0; j < T::WN; ++j) acc[i][j] = v16i{};
 
   const int ktiles = p.K / 64;
   issue(0);
@@ -435,58 +518,61 @@ __global__ __launch_bounds__(512) void linear_mfma(LinearArgs p, int mblocks, in
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (kt + 2 < ktiles) issue(kt + 2);
-    const int8_t* st = ring + (kt % GSTAGES) * GSTAGE_BYTES;
+    const int8_t* st = ring + (kt % GSTAGES) * T::STAGE_BYTES;
     const int8_t* As = st;
     const int8_t* Ws = st + GB * 64;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int c = ks * 2 + (lane >> 5);  // 16-byte K chunk of this lane's fragment
-      v4i fa[4], fb[2];
+      v4i fa[T::WM], fb[T::WN];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < T::WM; ++i) {
         const int r = wm + 32 * i + (lane & 31);
         fa[i] = *reinterpret_cast<const v4i*>(As + r * 64 + ((c ^ lds_swz(r)) << 4));
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < T::WN; ++j) {
         const int r = wn + 32 * j + (lane & 31);
         fb[j] = *reinterpret_cast<const v4i*>(Ws + r * 64 + ((c ^ lds_swz(r)) << 4));
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < T::WM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
   }
 
   // Epilogue through LDS: the requantised block tile is staged row-major in the (now idle) ring and
-  // written back with 16-byte stores along whole 256-column rows; stores straight from the MFMA
-  // layout would be single bytes per lane (partial-line HBM writes).  i16 outputs take two passes
-  // of 128 rows (64 KiB each).
+  // written back with 16-byte stores along whole GB-column rows; stores straight from the MFMA
+  // layout would be single bytes per lane (partial-line HBM writes).  A block tile larger than the
+  // ring (i16 output at GB = 256) is staged in two passes of GB/2 rows.
   constexpr int OB = OUT8 ? 1 : 2;
-  constexpr int PASS_ROWS = OUT8 ? 256 : 128;
+  constexpr int PASS_ROWS = (GB * GB * OB <= T::LDS_BYTES) ? GB : GB / 2;
   constexpr int ROWB = GB * OB;  // staged row bytes
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();  // every wave is done reading the ring (the last DMA was waited for)
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   const bool vec_ok = ((p.ldo * OB) % 16 == 0) && ((uintptr_t)p.out % 16 == 0);
-  ColRq cq[2];
+  ColRq cq[T::WN];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < T::WN; ++j) {
     const int n = min(n0 + wn + 32 * j + (lane & 31), p.N - 1);
     cq[j] = make_colrq(p.rq[2 * n], p.rq[2 * n + 1], p.bias ? p.bias[n] : 0);  // (acc+bias)*M = acc*M + bias*M
   }
   // one wave-uniform choice of the requant form
-  const bool fast = __all(cq[0].S >= 32 && cq[1].S >= 32);
+  bool col_fast = true;
+#pragma unroll
+  for (int j = 0; j < T::WN; ++j) col_fast = col_fast && cq[j].S >= 32;
+  const bool fast = __all(col_fast);
   auto stage = [&](auto fast_tag, int pass) {
     constexpr bool FAST = decltype(fast_tag)::value;
     // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < T::WN; ++j) {
       const int cl = wn + 32 * j + (lane & 31);
       const int n = n0 + cl;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < T::WM; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int rl = wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
@@ -521,7 +607,7 @@ __global__ __launch_bounds__(512) void linear_mfma(LinearArgs p, int mblocks, in
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     constexpr int CPR = ROWB / 16;  // 16-byte chunks per staged row
-    for (int idx = tid; idx < PASS_ROWS * CPR; idx += 512) {
+    for (int idx = tid; idx < PASS_ROWS * CPR; idx += T::NT) {
       const int rl = idx / CPR, ch = idx % CPR;
       const int m = m0 + pass * PASS_ROWS + rl;
       const int nc = n0 + ch * (16 / OB);
@@ -549,11 +635,23 @@ __global__ __launch_bounds__(512) void linear_mfma(LinearArgs p, int mblocks, in
 template <int EPI, bool OUT8>
 static int launch_linear(LinearArgs& p, hipStream_t stream) {
   const bool aligned = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.W % 16 == 0);
-  if (p.M >= 128 && p.K % 64 == 0 && aligned &&
-      (int64_t)ceil_div(p.M, GB) * ceil_div(p.N, GB) >= current_cu_count()) {
-    const int mblocks = (int)ceil_div(p.M, GB), nblocks = (int)ceil_div(p.N, GB);
-    hipLaunchKernelGGL((linear_mfma<EPI, OUT8>), dim3(mblocks * nblocks), dim3(512), GSTAGES * GSTAGE_BYTES, stream,
-                       p, mblocks, nblocks);
+  if (p.M >= 128 && p.K % 64 == 0 && aligned) {
+    // 256x256 tiles when they fill every CU, else 128x128.  The 256x256 kernel keeps 128
+    // accumulators per lane at two waves per SIMD; the aux-reading epilogues would spill there.
+    if constexpr (EPI == EPI_NONE) {
+      if ((int64_t)ceil_div(p.M, 256) * ceil_div(p.N, 256) >= current_cu_count()) {
+        using T = MfmaTile<256, 8>;
+        const int mblocks = (int)ceil_div(p.M, 256), nblocks = (int)ceil_div(p.N, 256);
+        hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 256, 8>), dim3(mblocks * nblocks), dim3(T::NT), T::LDS_BYTES,
+                           stream, p, mblocks, nblocks);
+        LLHIP_LAUNCH_CHECK();
+        return 0;
+      }
+    }
+    using T = MfmaTile<128, 4>;
+    const int mblocks = (int)ceil_div(p.M, 128), nblocks = (int)ceil_div(p.N, 128);
+    hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 128, 4>), dim3(mblocks * nblocks), dim3(T::NT), T::LDS_BYTES, stream, p,
+                       mblocks, nblocks);
     LLHIP_LAUNCH_CHECK();
     return 0;
   }
@@ -569,6 +667,23 @@ static int launch_linear(LinearArgs& p, hipStream_t stream) {
     return 0;
   }
   const int tiles = (int)ceil_div(p.N, 16);
+  if (p.M == 1 && aligned && tiles < 2 * current_cu_count() && (int64_t)p.N * p.K < (1ll << 31)) {
+    // lanes per column: enough chunks per lane to amortise the fold, at most G1_PF in flight
+    const int nch = p.K / 16;
+    if (nch >= 128) {
+      hipLaunchKernelGGL((linear_gemv1<EPI, OUT8, 64>), dim3(p.N), dim3(64), 0, stream, p);
+    } else if (nch >= 64) {
+      hipLaunchKernelGGL((linear_gemv1<EPI, OUT8, 32>), dim3(ceil_div(p.N, 2)), dim3(64), 0, stream, p);
+    } else if (nch >= 32) {
+      hipLaunchKernelGGL((linear_gemv1<EPI, OUT8, 16>), dim3(ceil_div(p.N, 4)), dim3(64), 0, stream, p);
+    } else if (nch >= 16) {
+      hipLaunchKernelGGL((linear_gemv1<EPI, OUT8, 8>), dim3(ceil_div(p.N, 8)), dim3(64), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((linear_gemv1<EPI, OUT8, 4>), dim3(ceil_div(p.N, 16)), dim3(64), 0, stream, p);
+    }
+    LLHIP_LAUNCH_CHECK();
+    return 0;
+  }
   const int zblocks = (int)ceil_div(p.M, 16);
   // waves per workgroup: enough waves on the chip to keep HBM busy, never more than K steps
   const int target_waves = 8 * current_cu_count();

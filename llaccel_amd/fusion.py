@@ -4,8 +4,9 @@ launch (include/llhip.h: llhip_attn_in, llhip_mlp_in, llhip_norm_linear).
 A fused step writes every activation its ops name, with the values the separate ops give
 (the kernels compute the same integer formulas), so `acts`, later consumers and the launch
 record are unaffected.  It keeps the per-op steps it replaces and runs those instead when
-its shape limits do not hold (more than 16 rows per launch, an LDS staging overflow), so
-every graph runs; graphs that do not match a pattern simply keep their per-op steps.
+its shape limits do not hold (more than 16 rows per launch, an LDS staging overflow, a
+normalised width above 1024), so every graph runs; graphs that do not match a pattern simply
+keep their per-op steps.
 
 Recognised runs (the op order the reference's quantizer and compiler emit, refquant.py:426-467):
   attn_in : rmsnorm, quant, linear q, linear k, linear v, [rmsnorm heads q, rmsnorm heads k],
@@ -21,6 +22,7 @@ import ctypes
 from . import _lib
 
 LDS_LIMIT = 48 * 1024
+NORM_MAX_K = 1024  # the fused RMSNorm prologue holds a row in two 8-element chunks per lane
 
 
 def _vp(t):
@@ -36,7 +38,7 @@ class FusedStep:
         self.K, self.bytes_fn, self.name, self.ops = K, bytes_fn, name, ops
 
     def __call__(self, M, pos, pd=None):
-        if M > 16 or M * (self.K + 16) > LDS_LIMIT:
+        if M > 16 or M * (self.K + 16) > LDS_LIMIT or self.K > NORM_MAX_K:
             for st in self.fallback:
                 st(M, pos, pd)
             return

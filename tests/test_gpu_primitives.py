@@ -45,6 +45,13 @@ def test_saturation_and_mulshift():
 def test_isqrt_udiv():
     for t in [0, 1, 2, 3, (1 << 48) - 1, 1 << 47, 65535**2] + RNG.integers(0, 1 << 48, 20).tolist():
         assert G.isqrt48(t) == math.isqrt(t)
+    # perfect squares and their neighbours, where a rounded floating-point root can land on
+    # either side of the integer root
+    n = np.concatenate([np.arange(1, 3000), (1 << 24) - np.arange(1, 3000), RNG.integers(1, 1 << 24, 6000)])
+    t = np.concatenate([n * n - 1, n * n, n * n + 1, n * n + 2 * n])
+    t = t[(t >= 0) & (t < (1 << 48))]
+    want = np.array([math.isqrt(int(v)) for v in t])
+    assert np.array_equal(G._elementwise("llhip_isqrt48", [t.astype(np.int64)]), want)
     with pytest.raises(ValueError):
         G.isqrt48(1 << 48)
     assert G.udiv(10, 3) == 3 and G.udiv(10, 0) == 10 and G.udiv(2**31, 65534) == 32769
