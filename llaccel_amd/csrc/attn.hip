@@ -77,6 +77,7 @@ __device__ __forceinline__ uint32_t lut_prob_lds(int64_t z, const uint16_t* ei, 
 // group and the value latency hides behind the score and softmax phases.  Keys >= T read zeros.
 template <int D>
 __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
+  kernarg_warm<sizeof(AttnArgs)>();
   extern __shared__ int32_t sc[];  // [lds_T] scores, then probabilities
   __shared__ int32_t redmax[ATTN_WAVES], redsum[ATTN_WAVES];
   __shared__ uint32_t lut32[LUT_DW];
@@ -88,13 +89,14 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   const int h = blockIdx.x;
   const int m = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int pos0 = load_pos(p.pos_dev, p.pos);
-  const int T = pos0 + m + 1;
   const int g = h / (p.H / p.Hkv);
-  const Rsrc kr = rsrc(p.kc + (int64_t)g * p.max_seq * D, (int64_t)T * D);
-  const Rsrc vr = rsrc(p.vc + (int64_t)g * p.max_seq * D, (int64_t)T * D);
+  // Loads in order of use: q and the keys of the first score pass, the LUT dwords (wave 0), the
+  // value rows of this thread's first VPF keys.  Key rows at or past T read zeros.
+  const int T = load_pos(p.pos_dev, p.pos) + m + 1;
+  const int8_t* kbase = p.kc + (int64_t)g * p.max_seq * D;
+  const int8_t* vbase = p.vc + (int64_t)g * p.max_seq * D;
   const Rsrc qr = rsrc(p.q + (int64_t)m * p.ldq + (int64_t)h * D, D);
-
+  const Rsrc kr = rsrc(kbase, (int64_t)T * D), vr = rsrc(vbase, (int64_t)T * D);
   v4i qv[DC], k0[DC], k1[DC];
   const int t0 = tid, t1 = tid + ATTN_THREADS;
 #pragma unroll

@@ -275,6 +275,7 @@ __device__ __forceinline__ T pick3(int role, const T (&v)[3]) {
 
 template <int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
+  kernarg_warm<sizeof(AttnInArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   __shared__ v4i red[MAXW][64];
   const int lda = p.K + 16;
@@ -289,10 +290,13 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   const int base = hh * D;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int tiles = D >> 4;
-  const int pos0 = load_pos(p.pos_dev, p.pos);
 
-  // kernel entry, in order of use: RMSNorm operands, weight slice, epilogue operands of this
-  // thread's column, head-norm gamma, RoPE factors
+  // kernel entry, in order of use: the device position, RMSNorm operands, weight slice, epilogue
+  // operands of this thread's column, head-norm gamma.  The position is a vector load issued
+  // first (the previous launch wrote it, so it comes from memory): it has arrived once the
+  // RMSNorm operands have, and only then are the RoPE factors at that position requested.
+  const int32_t posv = ld4(rsrc(p.pos_dev, 4), 0);
+  issue_fence();
   const NormMap nm = norm_map(M);
   NormRegs nr;
   norm_prefetch(p.pre, M, nm, nr);
@@ -318,6 +322,9 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     for (int i = 0; i < 4; ++i) hg[i] = ld2s(gr, lane + 64 * i < D ? 2 * (lane + 64 * i) : LD_OOB);
   }
   issue_fence();
+
+  norm_quant_rows(p.pre, nr, M, nm, a_lds, lda, b == 0);
+  const int pos0 = p.pos_dev ? __builtin_amdgcn_readfirstlane(posv) : p.pos;
   const int half = D >> 1;
   const int jrope = tid % half, mrope = tid / half;
   int32_t c0 = 0, s0r = 0;
@@ -329,8 +336,6 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     s0r = ld2s(rsrc(p.sin_tab, tab), off);
   }
   issue_fence();
-
-  norm_quant_rows(p.pre, nr, M, nm, a_lds, lda, b == 0);
   __syncthreads();
   red[wave][lane] = wslice_mfma(ws, wr, a_lds, lda, M, p.K);
   __syncthreads();
@@ -429,6 +434,7 @@ struct MlpInArgs {
 
 template <int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
+  kernarg_warm<sizeof(MlpInArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   __shared__ v4i red[MAXW][64];
   __shared__ uint32_t sig32[129];
@@ -507,6 +513,7 @@ struct NormGemvArgs {
 
 template <int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
+  kernarg_warm<sizeof(NormGemvArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   __shared__ v4i red[MAXW][64];
   __shared__ uint32_t sig32[129];

@@ -214,6 +214,7 @@ constexpr int G1_PF = 8;
 
 template <int EPI, bool OUT8, int LPC>
 __global__ __launch_bounds__(64) void linear_gemv1(LinearArgs p) {
+  kernarg_warm<sizeof(LinearArgs)>();
   constexpr int CPW = 64 / LPC;
   const int lane = threadIdx.x;
   const int c = lane / LPC, j = lane % LPC;
