@@ -54,6 +54,37 @@ def build_workload(cfg_name: str, seed: int) -> Path:
     return qdir
 
 
+def batch_decode(qdir: Path, args, single_tokens) -> dict:
+    """Config 4 at batch B: sequence b has the seeded prompt of seed + b and its own KV slot; after
+    the B prefills, every decode launch runs the B sequences as B rows.  Sequence 0 has the batch-1
+    run's prompt, so its tokens must equal the batch-1 warmup tokens."""
+    import torch
+
+    from llaccel_amd import golden as G
+    from llaccel_amd import synth
+
+    B = args.batch
+    g = G.GoldenModel(qdir)
+    prompts = [synth.seeded_prompt("qwen25", args.prompt, args.seed + b) for b in range(B)]
+    L = len(prompts[0])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    rows = g.prefill_batch(prompts)
+    torch.cuda.synchronize()
+    t_pre = time.perf_counter() - t0
+    nxt = [G.GoldenModel.argmax(r[-1], g.vocab) for r in rows]
+    toks_w, _ = g.decode_batch_loop(nxt, [L] * B, args.warmup)
+    same = bool(np.array_equal(toks_w[:, 0], np.asarray(single_tokens)))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.decode_batch_loop([int(t) for t in toks_w[-1]], [L + args.warmup] * B, args.steps, sync=False)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return {"batch": B, "tok_s": round(B * args.steps / dt, 1), "ms_per_step": round(dt / args.steps * 1e3, 4),
+            "steps": args.steps, "prefill_ms_all": round(t_pre * 1e3, 1),
+            "sequence0_tokens_equal_batch1": same}
+
+
 def time_graph(graph, reps: int) -> float:
     """Average seconds per replay, HIP events on the current stream."""
     import torch
@@ -144,6 +175,7 @@ def main() -> None:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--batch", type=int, default=16, help="also time config 4's batch decode (1 = skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs the datapath on a "
@@ -222,10 +254,17 @@ def main() -> None:
         if not exact:
             raise SystemExit("CPU oracle and GPU decode launches differ")
 
+    batch = None
+    if args.batch > 1:
+        batch = batch_decode(qdir, args, toks_w)
+        log("batch decode", batch)
+
     extra = {"prefill_tok_s": round(L / t_prefill, 1), "prefill_ms": round(t_prefill * 1e3, 2),
              "decode_step_bytes": step_bytes, "decode_hbm_frac_of_step": round(step_bytes / (dt / args.steps) / 1e9
                                                                                 / HBM_PEAK_GBS, 4),
              "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1), "decode_kernel_families": fam}
+    if batch is not None:
+        extra[f"decode_batch{args.batch}"] = batch
     if not args.no_gemm:
         extra["gemm_sweep"] = gemm_sweep()
 

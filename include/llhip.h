@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define LLHIP_ABI_VERSION 1
+#define LLHIP_ABI_VERSION 2
 
 int llhip_abi_version(void);
 const char* llhip_last_error(void);
@@ -71,10 +71,12 @@ int llhip_silu(const int16_t* x, int64_t n, int64_t Mi, int64_t Si, int64_t sh_o
 int llhip_vmul(const int16_t* a, const int16_t* b, int64_t n, int64_t sh, int16_t* y, void* stream);
 /* golden.py:115-116  vadd */
 int llhip_vadd(const int16_t* a, const int16_t* b, int64_t n, int64_t sh_b, int16_t* y, void* stream);
-/* golden.py:141-158  RoPE of x [M][H*D] (row stride ldx) with Q1.14 tables [max_seq][D/2]; row m at pos+m */
+/* golden.py:141-158  RoPE of x [M][H*D] (row stride ldx) with Q1.14 tables [max_seq][D/2]; row m at
+ * pos+m (pos read from pos_dev when non-NULL), or at row_pos[m] when row_pos (int32 [M], device)
+ * is non-NULL (one sequence per row). */
 int llhip_rope(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, const int16_t* cos_tab,
-               const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev, int16_t* y,
-               int64_t ldy, void* stream);
+               const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev,
+               const int32_t* row_pos, int16_t* y, int64_t ldy, void* stream);
 
 /* ---- gemm engine ---- */
 /* golden.py:316-342  out[M][N] = epilogue(requant(A[M][K] . W[N][K]^T + bias)).
@@ -91,15 +93,19 @@ int llhip_exact_matmul(const int64_t* A, int64_t M, int64_t K, const int8_t* W, 
                        void* stream);
 
 /* ---- attn engine ---- */
+/* Batch decode (row_pos non-NULL, int32 [M] on the device): row m is its own sequence at position
+ * row_pos[m], with its caches at kc/vc + m * slot_stride (slot_stride >= Hkv * max_seq * D).
+ * Otherwise row m sits at pos + m (pos read from pos_dev when non-NULL) in the caches at kc/vc. */
 /* golden.py:344-351  K/V rows of M positions into caches [Hkv][max_seq][D] at pos+m */
 int llhip_kv_write(const int8_t* k, const int8_t* v, int64_t M, int64_t Hkv, int64_t D, int64_t ldk, int64_t ldv,
-                   int64_t pos, const int32_t* pos_dev, int8_t* kc, int8_t* vc, int64_t max_seq, void* stream);
+                   int64_t pos, const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, int8_t* kc,
+                   int8_t* vc, int64_t max_seq, void* stream);
 /* golden.py:353-366 (+ attention_head golden.py:162-180)  causal GQA attention of q [M][H*D]
  * over caches [Hkv][max_seq][D]; row m sees keys 0..pos+m.  prob_bits 8 or 15. */
 int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
-                    const int32_t* pos_dev, const int8_t* kc, const int8_t* vc, int64_t max_seq, int64_t Ms,
-                    int64_t Ss, int64_t Mo, int64_t So, int64_t prob_bits, int8_t* out, int64_t ldo, void* ws,
-                    void* stream);
+                    const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
+                    const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
+                    int64_t prob_bits, int8_t* out, int64_t ldo, void* ws, void* stream);
 
 /* ---- host-loop helpers ---- */
 /* golden.py:369-373  rows[m] = embed[tokens[m]] for m < n_tokens, zero for n_tokens <= m < M.
@@ -116,6 +122,15 @@ int llhip_argmax_i16(const int16_t* logits, int64_t rows, int64_t ld, int64_t vo
 int llhip_greedy_step(const int16_t* logits, int64_t vocab, int32_t* token, int32_t* pos, int32_t* step,
                       int16_t* ring_rows, int64_t ring_ld, int32_t* ring_tokens, int64_t ring_cap, void* ws,
                       void* stream);
+
+/* golden.py:376-377 + the launch record of golden.py:411-414 for a batch decode launch, one
+ * sequence per row: tokens[r] = first argmax of logits[r][0:vocab], rows ld elements apart.  With
+ * s = positions[r] - base[r], when 0 <= s < ring_cap the row goes to ring_rows[s][r] (rows of
+ * ring_ld elements, [ring_cap][rows] of them) and the token to ring_tokens[s][r]; then
+ * positions[r] += 1. */
+int llhip_greedy_rows(const int16_t* logits, int64_t rows, int64_t ld, int64_t vocab, int32_t* tokens,
+                      int32_t* positions, const int32_t* base, int16_t* ring_rows, int64_t ring_ld,
+                      int32_t* ring_tokens, int64_t ring_cap, void* stream);
 
 /* ---- fused decoder blocks (M <= 16 rows per launch) ----
  * Each computes a run of consecutive qgraph ops in one launch and writes every activation
@@ -147,6 +162,8 @@ typedef struct llhip_attn_in_desc {
   void* kc; /* int8 caches [Hkv][max_seq][D] */
   void* vc;
   int64_t max_seq, M, H, Hkv, D, pos, has_norm;
+  const void* row_pos; /* int32 [M] device positions, one sequence per row (batch decode), or NULL */
+  int64_t slot_stride; /* with row_pos: elements between the caches of rows m and m + 1 */
 } llhip_attn_in_desc;
 
 /* golden.py:286-300 -- rmsnorm, quant, linear q/k/v (+bias), [rmsnorm heads q/k], rope q/k,

@@ -38,16 +38,17 @@ _SIGS = {
     "llhip_silu": [_p, _i64, _i64, _i64, _i64, _p, _p],
     "llhip_vmul": [_p, _p, _i64, _i64, _p, _p],
     "llhip_vadd": [_p, _p, _i64, _i64, _p, _p],
-    "llhip_rope": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i64, _p],
+    "llhip_rope": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _p],
     "llhip_linear": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p,
                      _i64, _p, _p],
     "llhip_exact_matmul": [_p, _i64, _i64, _p, _i64, _p, _p],
-    "llhip_kv_write": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p],
-    "llhip_attention": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p,
-                        _i64, _p, _p],
+    "llhip_kv_write": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p],
+    "llhip_attention": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                        _i64, _p, _i64, _p, _p],
     "llhip_embed_rows": [_p, _i64, _i64, _p, _i64, _i64, _p, _p],
     "llhip_argmax_i16": [_p, _i64, _i64, _i64, _p, _p],
     "llhip_greedy_step": [_p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],
+    "llhip_greedy_rows": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p],
 }
 _RESTYPES = {"llhip_last_error": ctypes.c_char_p, "llhip_workspace_bytes": _i64}
 
@@ -110,7 +111,7 @@ class AttnInDesc(ctypes.Structure):
                 ("nrm_sh", _i64 * 2), ("cos_tab", _p), ("sin_tab", _p), ("pos_dev", _p), ("rope_out", _p * 2),
                 ("quant_out", _p * 2), ("quant_M", _i64 * 2), ("quant_S", _i64 * 2), ("kc", _p), ("vc", _p),
                 ("max_seq", _i64), ("M", _i64), ("H", _i64), ("Hkv", _i64), ("D", _i64), ("pos", _i64),
-                ("has_norm", _i64)]
+                ("has_norm", _i64), ("row_pos", _p), ("slot_stride", _i64)]
 
 
 class MlpInDesc(ctypes.Structure):

@@ -27,6 +27,8 @@ struct AttnArgs {
   const int8_t* vc;
   int8_t* out;
   const int32_t* pos_dev;
+  const int32_t* row_pos;  // per-row positions (row m in cache slot m), or null
+  int64_t slot_stride;
   int64_t ldq, ldo, max_seq;
   int64_t Ms, Mo;
   int Ss, So;
@@ -92,9 +94,14 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   const int g = h / (p.H / p.Hkv);
   // Loads in order of use: q and the keys of the first score pass, the LUT dwords (wave 0), the
   // value rows of this thread's first VPF keys.  Key rows at or past T read zeros.
-  const int T = load_pos(p.pos_dev, p.pos) + m + 1;
-  const int8_t* kbase = p.kc + (int64_t)g * p.max_seq * D;
-  const int8_t* vbase = p.vc + (int64_t)g * p.max_seq * D;
+  // row m's context: T = position + 1 (row m of a launch at pos sits at pos + m; with per-row
+  // positions, row m is its own sequence in cache slot m), never past the cache
+  const int T = min((p.row_pos ? *(const __attribute__((address_space(4))) int32_t*)(p.row_pos + m)
+                               : load_pos(p.pos_dev, p.pos) + m) + 1,
+                    (int)p.max_seq);
+  const int64_t slot = p.row_pos ? m * p.slot_stride : 0;
+  const int8_t* kbase = p.kc + slot + (int64_t)g * p.max_seq * D;
+  const int8_t* vbase = p.vc + slot + (int64_t)g * p.max_seq * D;
   const Rsrc qr = rsrc(p.q + (int64_t)m * p.ldq + (int64_t)h * D, D);
   const Rsrc kr = rsrc(kbase, (int64_t)T * D), vr = rsrc(vbase, (int64_t)T * D);
   v4i qv[DC], k0[DC], k1[DC];
@@ -245,15 +252,17 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
 
 __global__ void kv_write_kernel(const int8_t* __restrict__ k, const int8_t* __restrict__ v, int64_t M, int Hkv, int D,
                                 int64_t ldk, int64_t ldv, int pos, const int32_t* __restrict__ pos_dev,
-                                int8_t* __restrict__ kc, int8_t* __restrict__ vc, int64_t max_seq) {
+                                const int32_t* __restrict__ row_pos, int64_t slot_stride, int8_t* __restrict__ kc,
+                                int8_t* __restrict__ vc, int64_t max_seq) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t per_row = (int64_t)Hkv * D;
   if (idx >= M * per_row) return;
   const int64_t m = idx / per_row;
   const int rem = (int)(idx % per_row);
   const int h = rem / D, d = rem % D;
-  const int p0 = load_pos(pos_dev, pos);
-  const int64_t dst = ((int64_t)h * max_seq + p0 + m) * D + d;
+  const int64_t pm = row_pos ? (int64_t)row_pos[m] : (int64_t)load_pos(pos_dev, pos) + m;
+  if (pm < 0 || pm >= max_seq) return;  // device positions are checked by the caller; never write past a cache
+  const int64_t dst = (row_pos ? m * slot_stride : 0) + ((int64_t)h * max_seq + pm) * D + d;
   kc[dst] = k[m * ldk + rem];
   vc[dst] = v[m * ldv + rem];
 }
@@ -265,22 +274,25 @@ using namespace llhip;
 extern "C" {
 
 int llhip_kv_write(const int8_t* k, const int8_t* v, int64_t M, int64_t Hkv, int64_t D, int64_t ldk, int64_t ldv,
-                   int64_t pos, const int32_t* pos_dev, int8_t* kc, int8_t* vc, int64_t max_seq, void* stream) {
+                   int64_t pos, const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, int8_t* kc,
+                   int8_t* vc, int64_t max_seq, void* stream) {
   if (M < 0 || Hkv <= 0 || D <= 0) return fail(-EINVAL, "kv_write: bad geometry");
   if (ldk < Hkv * D || ldv < Hkv * D) return fail(-EINVAL, "kv_write: leading dimension too small");
-  if (!pos_dev && (pos < 0 || pos + M > max_seq))
+  if (row_pos && slot_stride < Hkv * max_seq * D) return fail(-EINVAL, "kv_write: cache slots overlap");
+  if (!pos_dev && !row_pos && (pos < 0 || pos + M > max_seq))
     return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)pos, (long long)(pos + M - 1),
                 (long long)max_seq);
   const int64_t total = M * Hkv * D;
   if (total == 0) return 0;
   hipLaunchKernelGGL(kv_write_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, k, v, M,
-                     (int)Hkv, (int)D, ldk, ldv, (int)pos, pos_dev, kc, vc, max_seq);
+                     (int)Hkv, (int)D, ldk, ldv, (int)pos, pos_dev, row_pos, slot_stride, kc, vc, max_seq);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
 
 int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
-                    const int32_t* pos_dev, const int8_t* kc, const int8_t* vc, int64_t max_seq, int64_t Ms,
+                    const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
+                    const int8_t* vc, int64_t max_seq, int64_t Ms,
                     int64_t Ss, int64_t Mo, int64_t So, int64_t prob_bits, int8_t* out, int64_t ldo, void* ws,
                     void* stream) {
   (void)ws;
@@ -291,11 +303,12 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   if (!u32_ok(Ms) || !u32_ok(Mo) || !shift_ok(Ss) || !shift_ok(So))
     return fail(-EINVAL, "attention: multipliers must be u32, shifts in [0,63]");
   if (ldq < H * D || ldo < H * D) return fail(-EINVAL, "attention: leading dimension too small");
-  if (!pos_dev && (pos < 0 || pos + M > max_seq))
+  if (row_pos && slot_stride < Hkv * max_seq * D) return fail(-EINVAL, "attention: cache slots overlap");
+  if (!pos_dev && !row_pos && (pos < 0 || pos + M > max_seq))
     return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)pos, (long long)(pos + M - 1),
                 (long long)max_seq);
   if (M == 0) return 0;
-  const int64_t tmax = pos_dev ? max_seq : pos + M;
+  const int64_t tmax = (pos_dev || row_pos) ? max_seq : pos + M;
   if (tmax > ATTN_MAX_T) return fail(-EINVAL, "attention: context %lld exceeds %d", (long long)tmax, ATTN_MAX_T);
   AttnArgs p{};
   p.q = q;
@@ -303,6 +316,8 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   p.vc = vc;
   p.out = out;
   p.pos_dev = pos_dev;
+  p.row_pos = row_pos;
+  p.slot_stride = slot_stride;
   p.ldq = ldq;
   p.ldo = ldo;
   p.max_seq = max_seq;

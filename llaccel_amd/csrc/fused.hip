@@ -256,6 +256,8 @@ struct AttnInArgs {
   const int16_t* cos_tab;
   const int16_t* sin_tab;
   const int32_t* pos_dev;
+  const int32_t* row_pos;  // per-row positions (row m in cache slot m), or null
+  int64_t slot_stride;
   int16_t* rope_out[2];
   int8_t* quant_out[2];
   int64_t quant_M[2], quant_S[2];
@@ -278,6 +280,7 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   kernarg_warm<sizeof(AttnInArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   __shared__ v4i red[MAXW][64];
+  __shared__ int32_t rowpos[16];
   const int lda = p.K + 16;
   int8_t* a_lds = dyn;                                                         // [M][lda] i8
   int32_t* hres = reinterpret_cast<int32_t*>(dyn + ((p.M * lda + 15) & ~15));  // [M][D] i32
@@ -296,6 +299,11 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   // first (the previous launch wrote it, so it comes from memory): it has arrived once the
   // RMSNorm operands have, and only then are the RoPE factors at that position requested.
   const int32_t posv = ld4(rsrc(p.pos_dev, 4), 0);
+  // per-row positions: the row of this thread's RoPE pair and row tid (staged in LDS for the tail)
+  const int half = D >> 1;
+  const int jrope = tid % half, mrope = tid / half;
+  const Rsrc rpr = rsrc(p.row_pos, 4 * M);
+  const int32_t rp_rope = ld4(rpr, mrope < M ? 4 * mrope : LD_OOB), rp_own = ld4(rpr, tid < M ? 4 * tid : LD_OOB);
   issue_fence();
   const NormMap nm = norm_map(M);
   NormRegs nr;
@@ -325,13 +333,14 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
 
   norm_quant_rows(p.pre, nr, M, nm, a_lds, lda, b == 0);
   const int pos0 = p.pos_dev ? __builtin_amdgcn_readfirstlane(posv) : p.pos;
-  const int half = D >> 1;
-  const int jrope = tid % half, mrope = tid / half;
+  const bool rows = p.row_pos != nullptr;
+  if (tid < M) rowpos[tid] = rows ? rp_own : pos0 + tid;
   int32_t c0 = 0, s0r = 0;
   {
-    const bool rok = role < 2 && mrope < M;
+    const int pr = rows ? rp_rope : pos0 + mrope;
+    const bool rok = role < 2 && mrope < M && pr >= 0 && pr < p.max_seq;
     const int64_t tab = (int64_t)p.max_seq * half * 2;
-    const uint32_t off = rok ? (uint32_t)(((int64_t)(pos0 + mrope) * half + jrope) * 2) : LD_OOB;
+    const uint32_t off = rok ? (uint32_t)(((int64_t)pr * half + jrope) * 2) : LD_OOB;
     c0 = ld2s(rsrc(p.cos_tab, tab), off);
     s0r = ld2s(rsrc(p.sin_tab, tab), off);
   }
@@ -356,7 +365,9 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     for (int m = tid / D; m < M; m += rstep) {
       const int8_t y = (int8_t)sat8(mulshift((int64_t)hres[m * D + dcol] + bias, rq.x, rq.y));
       static_cast<int8_t*>(p.lin_out[2])[(int64_t)m * Nrole + ncol] = y;
-      p.vc[((int64_t)hh * p.max_seq + pos0 + m) * D + dcol] = y;
+      const int pm = rowpos[m];
+      if (pm >= 0 && pm < p.max_seq)  // device positions are checked by the caller; never write past a cache
+        p.vc[(rows ? m * p.slot_stride : 0) + ((int64_t)hh * p.max_seq + pm) * D + dcol] = y;
     }
     return;
   }
@@ -388,9 +399,11 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   // RoPE (golden.py:141-158) -> quant (golden.py:119-120) -> K cache for keys
   for (int m = mrope; m < M; m += blockDim.x / half) {
     int64_t c = c0, s = s0r;
+    const int pm = rowpos[m];
+    if (pm < 0 || pm >= p.max_seq) continue;
     if (m != mrope) {
-      c = p.cos_tab[(int64_t)(pos0 + m) * half + jrope];
-      s = p.sin_tab[(int64_t)(pos0 + m) * half + jrope];
+      c = p.cos_tab[(int64_t)pm * half + jrope];
+      s = p.sin_tab[(int64_t)pm * half + jrope];
     }
     const int j = jrope;
     const int64_t x1 = hres[m * D + j], x2 = hres[m * D + half + j];
@@ -404,7 +417,7 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     p.quant_out[role][o + j] = q1;
     p.quant_out[role][o + half + j] = q2;
     if (role == 1) {
-      int8_t* kr = p.kc + ((int64_t)hh * p.max_seq + pos0 + m) * D;
+      int8_t* kr = p.kc + (rows ? m * p.slot_stride : 0) + ((int64_t)hh * p.max_seq + pm) * D;
       kr[j] = q1;
       kr[half + j] = q2;
     }
@@ -636,7 +649,7 @@ extern "C" int llhip_attn_in(const llhip_attn_in_desc* d, void* stream) {
   const int64_t M = d->M, H = d->H, Hkv = d->Hkv, D = d->D, K = d->pre.K;
   if (M < 1 || M > 16 || H < 1 || Hkv < 1 || H % Hkv || D < 16 || D > 256 || D % 16)
     return fail(-EINVAL, "attn_in: bad geometry (M <= 16, D multiple of 16 up to 256)");
-  if (!d->pos_dev && (d->pos < 0 || d->pos + M > d->max_seq))
+  if (!d->pos_dev && !d->row_pos && (d->pos < 0 || d->pos + M > d->max_seq))
     return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)d->pos, (long long)(d->pos + M - 1),
                 (long long)d->max_seq);
   for (int i = 0; i < 2; ++i)
@@ -664,6 +677,9 @@ extern "C" int llhip_attn_in(const llhip_attn_in_desc* d, void* stream) {
   p.cos_tab = static_cast<const int16_t*>(d->cos_tab);
   p.sin_tab = static_cast<const int16_t*>(d->sin_tab);
   p.pos_dev = static_cast<const int32_t*>(d->pos_dev);
+  p.row_pos = static_cast<const int32_t*>(d->row_pos);
+  p.slot_stride = d->slot_stride;
+  if (p.row_pos && p.slot_stride < Hkv * d->max_seq * D) return fail(-EINVAL, "attn_in: cache slots overlap");
   p.kc = static_cast<int8_t*>(d->kc);
   p.vc = static_cast<int8_t*>(d->vc);
   p.max_seq = d->max_seq;

@@ -147,8 +147,9 @@ static unsigned ew_blocks(int64_t n) {
 // RoPE (golden.py:141-158): thread per (row, head, i < D/2)
 // ---------------------------------------------------------------------------------------
 __global__ void rope_kernel(const int16_t* __restrict__ x, int64_t M, int H, int D, int64_t ldx,
-                            const int16_t* __restrict__ cos_tab, const int16_t* __restrict__ sin_tab, int pos,
-                            const int32_t* __restrict__ pos_dev, int16_t* __restrict__ y, int64_t ldy) {
+                            const int16_t* __restrict__ cos_tab, const int16_t* __restrict__ sin_tab,
+                            int64_t table_rows, int pos, const int32_t* __restrict__ pos_dev,
+                            const int32_t* __restrict__ row_pos, int16_t* __restrict__ y, int64_t ldy) {
   const int half = D / 2;
   const int64_t total = M * H * half;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -156,8 +157,9 @@ __global__ void rope_kernel(const int16_t* __restrict__ x, int64_t M, int H, int
   const int64_t m = idx / ((int64_t)H * half);
   const int rem = (int)(idx % ((int64_t)H * half));
   const int h = rem / half, i = rem % half;
-  const int p0 = pos_dev ? *pos_dev : pos;
-  const int64_t trow = (int64_t)(p0 + m) * half;
+  const int64_t pm = row_pos ? (int64_t)row_pos[m] : (int64_t)(pos_dev ? *pos_dev : pos) + m;
+  if (pm < 0 || pm >= table_rows) return;  // device positions are checked by the caller; never read past the table
+  const int64_t trow = pm * half;
   const int64_t c = cos_tab[trow + i], s = sin_tab[trow + i];
   const int64_t a = x[m * ldx + h * D + i], b = x[m * ldx + h * D + half + i];
   y[m * ldy + h * D + i] = (int16_t)sat16(rshr(a * c - b * s, 14));
@@ -253,6 +255,69 @@ __global__ __launch_bounds__(256) void greedy_step_kernel(const int16_t* __restr
   atomicExch(counter, 0u);
 }
 
+// Batch decode step on the device: one workgroup per row (sequence).  Each thread scans 8-element
+// chunks keeping its first maximum (strictly greater replaces), then the workgroup keeps the
+// largest value and, among equal values, the lowest index -- the first argmax of golden.py:376-377.
+constexpr int GR_THREADS = 1024;
+
+__device__ __forceinline__ void block_argmax(int32_t& v, int32_t& i, int32_t* sv, int32_t* si) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int32_t wv = wave_max_i32(v);
+  const int32_t wi = -wave_max_i32(v == wv ? -i : INT32_MIN + 1);  // lowest index holding the maximum
+  if (lane == 0) {
+    sv[wave] = wv;
+    si[wave] = wi;
+  }
+  __syncthreads();
+  v = sv[0];
+  i = si[0];
+  for (int w = 1; w < nw; ++w)
+    if (sv[w] > v || (sv[w] == v && si[w] < i)) {
+      v = sv[w];
+      i = si[w];
+    }
+}
+
+__global__ __launch_bounds__(GR_THREADS) void greedy_rows_kernel(const int16_t* __restrict__ logits, int64_t ld,
+                                                                 int64_t vocab, int32_t* tokens, int32_t* positions,
+                                                                 const int32_t* __restrict__ base,
+                                                                 int16_t* __restrict__ ring_rows, int64_t ring_ld,
+                                                                 int32_t* ring_tok, int64_t ring_cap, int64_t rows) {
+  __shared__ int32_t sv[GR_THREADS / 64], si[GR_THREADS / 64];
+  const int r = blockIdx.x;
+  const int64_t s = (int64_t)positions[r] - base[r];
+  const bool rec = s >= 0 && s < ring_cap;
+  const int16_t* lr = logits + (int64_t)r * ld;
+  int16_t* dst = ring_rows + (s * rows + r) * ring_ld;
+  const Rsrc lrs = rsrc(lr, (vocab + 1) / 2 * 4);  // whole dwords: the range check is per dword
+  int32_t best = INT32_MIN, bi = 0;
+  for (int64_t c = threadIdx.x; c * 8 < vocab; c += GR_THREADS) {
+    const v4i w = ld16(lrs, (uint32_t)(c * 16));  // elements past vocab read zero and are skipped
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t i = c * 8 + e;
+      const int32_t v = (e & 1) ? hi16(w[e >> 1]) : lo16(w[e >> 1]);
+      if (i < vocab && v > best) {
+        best = v;
+        bi = (int32_t)i;
+      }
+    }
+    if (rec) {
+      if (c * 8 + 8 <= vocab && ring_ld % 8 == 0) {
+        *reinterpret_cast<v4i*>(dst + c * 8) = w;
+      } else {
+        for (int e = 0; e < 8 && c * 8 + e < vocab; ++e)
+          dst[c * 8 + e] = (int16_t)((e & 1) ? hi16(w[e >> 1]) : lo16(w[e >> 1]));
+      }
+    }
+  }
+  block_argmax(best, bi, sv, si);
+  if (threadIdx.x != 0) return;
+  tokens[r] = bi;
+  if (rec) ring_tok[s * rows + r] = bi;
+  positions[r] = positions[r] + 1;
+}
+
 }  // namespace llhip
 
 using namespace llhip;
@@ -296,15 +361,15 @@ int llhip_vadd(const int16_t* a, const int16_t* b, int64_t n, int64_t sh_b, int1
 }
 
 int llhip_rope(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, const int16_t* cos_tab,
-               const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev, int16_t* y,
-               int64_t ldy, void* stream) {
+               const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev,
+               const int32_t* row_pos, int16_t* y, int64_t ldy, void* stream) {
   if (M < 0 || H < 0 || D < 0 || D % 2) return fail(-EINVAL, "rope: bad geometry (D must be even)");
   if (ldx < H * D || ldy < H * D) return fail(-EINVAL, "rope: leading dimension too small");
-  if (!pos_dev && (pos < 0 || pos + M > table_rows)) return fail(-ERANGE, "rope: positions exceed the table");
+  if (!pos_dev && !row_pos && (pos < 0 || pos + M > table_rows)) return fail(-ERANGE, "rope: positions exceed the table");
   const int64_t total = M * H * (D / 2);
   if (total == 0) return 0;
   hipLaunchKernelGGL(rope_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, x, M, (int)H,
-                     (int)D, ldx, cos_tab, sin_tab, (int)pos, pos_dev, y, ldy);
+                     (int)D, ldx, cos_tab, sin_tab, table_rows, (int)pos, pos_dev, row_pos, y, ldy);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
@@ -330,6 +395,21 @@ int llhip_greedy_step(const int16_t* logits, int64_t vocab, int32_t* token, int3
   hipLaunchKernelGGL(greedy_step_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, logits, vocab, token,
                      pos, step, ring_rows, ring_ld, ring_tokens, ring_cap, reinterpret_cast<unsigned long long*>(w),
                      reinterpret_cast<uint32_t*>(w + 8));
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+int llhip_greedy_rows(const int16_t* logits, int64_t rows, int64_t ld, int64_t vocab, int32_t* tokens,
+                      int32_t* positions, const int32_t* base, int16_t* ring_rows, int64_t ring_ld,
+                      int32_t* ring_tokens, int64_t ring_cap, void* stream) {
+  if (rows < 0 || vocab <= 0 || vocab >= (1ll << 30) || ld < (vocab + 1) / 2 * 2 || ring_ld < vocab || ring_cap < 0)
+    return fail(-EINVAL, "greedy_rows: bad arguments");
+  if (rows == 0) return 0;
+  if (!logits || !tokens || !positions || !base || (ring_cap && (!ring_rows || !ring_tokens)))
+    return fail(-EINVAL, "greedy_rows: null operand");
+  if ((uintptr_t)ring_rows % 16) return fail(-EINVAL, "greedy_rows: misaligned record rows");
+  hipLaunchKernelGGL(greedy_rows_kernel, dim3((unsigned)rows), dim3(GR_THREADS), 0, (hipStream_t)stream, logits, ld,
+                     vocab, tokens, positions, base, ring_rows, ring_ld, ring_tokens, ring_cap, rows);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }

@@ -146,13 +146,12 @@ def match_attn_in(model, ops, i, steps):
                 d.nrm_out[r] = _vp(model._buf(o["out"]))
                 d.nrm_eps[r], d.nrm_C[r], d.nrm_sh[r] = int(o["eps_t"]), int(o["C"]), int(o["sh_post"])
         d.cos_tab, d.sin_tab = _vp(dt["rope_cos"]), _vp(dt["rope_sin"])
-        d.pos_dev = pd
+        kcp, vcp, d.pos_dev, d.row_pos, d.slot_stride = model._kv_args(layer, pd)
         for r, (ro, qo) in enumerate(((rq_, qq_), (rk_, kq_))):
             d.rope_out[r] = _vp(model._buf(ro["out"]))
             d.quant_out[r] = _vp(model._buf(qo["out"]))
             d.quant_M[r], d.quant_S[r] = int(qo["M"]), int(qo["S"])
-        kc, vc = model._kv[layer]
-        d.kc, d.vc = _vp(kc), _vp(vc)
+        d.kc, d.vc = kcp, vcp
         d.max_seq, d.M, d.H, d.Hkv, d.D, d.pos, d.has_norm = model.max_seq, M, H, Hkv, D, pos, int(has_norm)
 
     n_all = (H + 2 * Hkv) * D

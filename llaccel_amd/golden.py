@@ -247,8 +247,8 @@ def rope(x, H: int, D: int, cos_tab, sin_tab, pos: int):
     xd = _up(x, np.int16)
     cd, sd = _up(cos_tab, np.int16), _up(sin_tab, np.int16)
     yd = _t().empty_like(xd)
-    _lib.call("llhip_rope", _ptr(xd), M, H, D, H * D, _ptr(cd), _ptr(sd), cos_tab.shape[0], pos, None, _ptr(yd), H * D,
-              _stream())
+    _lib.call("llhip_rope", _ptr(xd), M, H, D, H * D, _ptr(cd), _ptr(sd), cos_tab.shape[0], pos, None, None, _ptr(yd),
+              H * D, _stream())
     return _down(yd).astype(I64)
 
 
@@ -273,8 +273,8 @@ def attention_head(q, keys, vals, Ms: int, Ss: int, Mo: int, So: int, prob_bits:
     qd = _up(q[None, :], np.int8)
     kd, vd = _up(keys, np.int8), _up(vals, np.int8)
     out = _t().empty((1, D), dtype=_t().int8, device=_dev())
-    _lib.call("llhip_attention", _ptr(qd), 1, 1, 1, D, D, T - 1, None, _ptr(kd), _ptr(vd), T, int(Ms), int(Ss),
-              int(Mo), int(So), int(prob_bits), _ptr(out), D, None, _stream())
+    _lib.call("llhip_attention", _ptr(qd), 1, 1, 1, D, D, T - 1, None, None, 0, _ptr(kd), _ptr(vd), T, int(Ms),
+              int(Ss), int(Mo), int(So), int(prob_bits), _ptr(out), D, None, _stream())
     return _down(out)[0].astype(I64)
 
 
@@ -355,6 +355,21 @@ class _Deferred:
         raise self.exc
 
 
+class _RowPos:
+    """Position context of a batch decode launch: row m is its own sequence, at the device position
+    rows[m], with its K/V caches in slot m (`stride` elements after slot m - 1)."""
+
+    def __init__(self, ptr, stride: int) -> None:
+        self.ptr, self.stride = ptr, stride
+
+
+def _pos_args(pd):
+    """(pos_dev, row_pos, slot_stride) kernel arguments of a step's position context."""
+    if isinstance(pd, _RowPos):
+        return None, pd.ptr, pd.stride
+    return pd, None, 0
+
+
 class _Step:
     """One compiled op: `fn(M, pos, pos_dev)` launches its kernel(s); `bytes_fn(M)` gives the
     algorithmic HBM bytes of one launch (operands read once, results written once)."""
@@ -420,12 +435,20 @@ class GoldenModel:
     def _buf(self, name: str):
         return self._act[name]
 
+    def _kv_args(self, layer: int, pd):
+        """(K cache, V cache, pos_dev, row_pos, slot_stride) kernel arguments of one layer."""
+        kc, vc = self._kv[layer]
+        if isinstance(pd, _RowPos):
+            return _ptr(kc), _ptr(vc), None, pd.ptr, pd.stride
+        return _ptr(kc[self._slot]), _ptr(vc[self._slot]), pd, None, 0
+
     def _ensure_capacity(self, M: int) -> None:
         if M <= self._cap:
             return
         torch = _t()
         cap = max(M, self.prefill_m)
         self._graph = None  # captured pointers would dangle
+        self._graph_b = None
         for name, (dt, cols) in self._act_spec.items():
             self._act[name] = torch.zeros((cap, cols), dtype=getattr(torch, _TDT[dt]), device=self.device)
         self._cap = cap
@@ -438,23 +461,32 @@ class GoldenModel:
                 kc.zero_()
                 vc.zero_()
             return
+        self._alloc_kv(1)
+
+    def _alloc_kv(self, slots: int) -> None:
+        """KV caches of `slots` independent sequences: per layer (slots, Hkv, max_seq, D) int8,
+        zero-filled.  Single-sequence calls use slot `_slot` (0 unless a batch API selects one)."""
+        torch = _t()
+        self._graph = None
+        self._graph_b = None
+        self._slot = 0
         self._kv: dict[int, tuple] = {}
         for op in self.q.ops:
             if op["op"] == "kv_write":
                 L, Hkv, D = int(op["layer"]), int(op["Hkv"]), int(op["D"])
-                shape = (Hkv, self.max_seq, D)
+                shape = (slots, Hkv, self.max_seq, D)
                 self._kv[L] = (torch.zeros(shape, dtype=torch.int8, device=self.device),
                                torch.zeros(shape, dtype=torch.int8, device=self.device))
 
     @property
     def kv(self) -> dict[int, tuple[np.ndarray, np.ndarray]]:
         """Host snapshots {layer: (K, V)} of the device caches, int8 (Hkv, max_seq, D)."""
-        return {L: (_down(k), _down(v)) for L, (k, v) in self._kv.items()}
+        return {L: (_down(k[self._slot]), _down(v[self._slot])) for L, (k, v) in self._kv.items()}
 
     def set_kv(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
         """Upload a (Hkv, max_seq, D) int8 K/V state for `layer` (preinitialised-state runs)."""
         kc, vc = self._kv[int(layer)]
-        for src, dst in ((k, kc), (v, vc)):
+        for src, dst in ((k, kc[self._slot]), (v, vc[self._slot])):
             a = np.asarray(src)
             if tuple(a.shape) != tuple(dst.shape):
                 raise ValueError(f"KV shape {a.shape} != {tuple(dst.shape)}")
@@ -622,8 +654,9 @@ class GoldenModel:
         rows = int(cos_t.shape[0])
 
         def run(M, pos, pd=None):
-            _lib.call("llhip_rope", _ptr(self._buf(src)), M, H, D, H * D, _ptr(cos_t), _ptr(sin_t), rows, pos, pd,
-                      _ptr(self._buf(dst)), H * D, _stream())
+            pdev, rpos, _ = _pos_args(pd)
+            _lib.call("llhip_rope", _ptr(self._buf(src)), M, H, D, H * D, _ptr(cos_t), _ptr(sin_t), rows, pos, pdev,
+                      rpos, _ptr(self._buf(dst)), H * D, _stream())
         return run
 
     def _c_kv_write(self, op, need):
@@ -636,9 +669,9 @@ class GoldenModel:
         ksrc, vsrc = op["k"], op["v"]
 
         def run(M, pos, pd=None):
-            kc, vc = self._kv[layer]
-            _lib.call("llhip_kv_write", _ptr(self._buf(ksrc)), _ptr(self._buf(vsrc)), M, Hkv, D, ck, cv, pos, pd,
-                      _ptr(kc), _ptr(vc), self.max_seq, _stream())
+            kcp, vcp, pdev, rpos, stride = self._kv_args(layer, pd)
+            _lib.call("llhip_kv_write", _ptr(self._buf(ksrc)), _ptr(self._buf(vsrc)), M, Hkv, D, ck, cv, pos, pdev,
+                      rpos, stride, kcp, vcp, self.max_seq, _stream())
         return run
 
     def _c_attention(self, op, need):
@@ -663,8 +696,8 @@ class GoldenModel:
         def run(M, pos, pd=None):
             if layer not in self._kv:
                 raise KeyError(layer)
-            kc, vc = self._kv[layer]
-            _lib.call("llhip_attention", _ptr(self._buf(src)), M, H, Hkv, D, H * D, pos, pd, _ptr(kc), _ptr(vc),
+            kcp, vcp, pdev, rpos, stride = self._kv_args(layer, pd)
+            _lib.call("llhip_attention", _ptr(self._buf(src)), M, H, Hkv, D, H * D, pos, pdev, rpos, stride, kcp, vcp,
                       self.max_seq, Ms, Ss, Mo, So, pb, _ptr(self._buf(dst)), H * D, _ptr(self._ws), _stream())
 
         def nbytes(M, T):
@@ -763,22 +796,22 @@ class GoldenModel:
         v = np.asarray(act[op["v"]], dtype=I64)
         _check_range(k, -128, 127, "k")
         _check_range(v, -128, 127, "v")
-        kc, vc = self._kv[int(op["layer"])]
+        kcp, vcp, _, _, _ = self._kv_args(int(op["layer"]), None)
         M = k.shape[0]
         kd, vd = _up(k, np.int8), _up(v, np.int8)
-        _lib.call("llhip_kv_write", _ptr(kd), _ptr(vd), M, Hkv, D, k.shape[1], v.shape[1], pos, None, _ptr(kc),
-                  _ptr(vc), self.max_seq, _stream())
+        _lib.call("llhip_kv_write", _ptr(kd), _ptr(vd), M, Hkv, D, k.shape[1], v.shape[1], pos, None, None, 0, kcp,
+                  vcp, self.max_seq, _stream())
 
     def attention(self, op: dict, act: dict, pos: int) -> np.ndarray:
         """Causal GQA attention of host q rows over the device caches (golden.py:353-366)."""
         q = np.asarray(act[op["q"]], dtype=I64)
         _check_range(q, -128, 127, "q")
         H, Hkv, D = int(op["H"]), int(op["Hkv"]), int(op["D"])
-        kc, vc = self._kv[int(op["layer"])]
+        kcp, vcp, _, _, _ = self._kv_args(int(op["layer"]), None)
         M = q.shape[0]
         qd = _up(q, np.int8)
         out = _t().empty((M, H * D), dtype=_t().int8, device=self.device)
-        _lib.call("llhip_attention", _ptr(qd), M, H, Hkv, D, q.shape[1], pos, None, _ptr(kc), _ptr(vc), self.max_seq,
+        _lib.call("llhip_attention", _ptr(qd), M, H, Hkv, D, q.shape[1], pos, None, None, 0, kcp, vcp, self.max_seq,
                   int(op["Ms"]), int(op["Ss"]), int(op["Mo"]), int(op["So"]), int(op.get("prob_bits", 8)), _ptr(out),
                   H * D, _ptr(self._ws), _stream())
         return _down(out).astype(I64)
@@ -884,6 +917,126 @@ class GoldenModel:
         if not sync:
             return None
         return _down(self._ring_tok[:n]).astype(np.int64), self._ring_rows[:n].cpu().numpy()
+
+    # ---- batch decode: B independent sequences, one per row -------------------------------
+    def _batch_state(self, B: int, ring_cap: int) -> None:
+        torch = _t()
+        if self._kv and next(iter(self._kv.values()))[0].shape[0] < B:
+            raise ValueError(f"{B} sequences need {B} KV slots (generate_batch allocates them)")
+        if getattr(self, "_b_rows", None) != B or ring_cap > self._b_cap:
+            cap = max(ring_cap, 16)
+            self._b_ring_rows = torch.zeros((cap, B, self.vocab), dtype=torch.int16, device=self.device)
+            self._b_ring_tok = torch.zeros((cap, B), dtype=torch.int32, device=self.device)
+            self._b_st = torch.zeros(3 * B, dtype=torch.int32, device=self.device)  # tokens, positions, base
+            self._b_rows, self._b_cap = B, cap
+            self._graph_b = None
+
+    def _decode_batch_launch(self) -> None:
+        """Embedding gather of the B device tokens, the op list with one sequence per row, greedy step."""
+        B = self._b_rows
+        st = self._b_st
+        tok, posp, base = (ctypes.c_void_p(st.data_ptr() + 4 * B * i) for i in range(3))
+        _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, tok, B, B,
+                  _ptr(self._act[self.q.input_name]), _stream())
+        kc0 = next(iter(self._kv.values()))[0]
+        self._execute(B, 0, _RowPos(posp, kc0[0].numel()))
+        out = self._act[self.q.output_name]
+        _lib.call("llhip_greedy_rows", _ptr(out), B, out.shape[1], self.vocab, tok, posp, base,
+                  _ptr(self._b_ring_rows), self.vocab, _ptr(self._b_ring_tok), self._b_cap, _stream())
+
+    def decode_batch_loop(self, tokens, positions, n: int, *, sync: bool = True):
+        """Run `n` greedy decode launches of B = len(tokens) sequences together: row b is sequence b,
+        at position positions[b] + i in launch i, with its KV caches in slot b.  Every row is
+        computed exactly as its own single-sequence decode launch.  Returns tokens [n][B] and
+        logits rows [n][B][vocab]."""
+        B = len(tokens)
+        if B < 1 or len(positions) != B:
+            raise ValueError("tokens and positions must be nonempty and of equal length")
+        if n <= 0:
+            return np.zeros((0, B), np.int64), np.zeros((0, B, self.vocab), np.int16)
+        pos = [int(p) for p in positions]
+        if min(pos) < 0 or max(pos) + n > self.max_seq:
+            raise ValueError(f"positions up to {max(pos) + n - 1} exceed max_seq={self.max_seq}")
+        torch = _t()
+        self._ensure_capacity(B)
+        self._batch_state(B, n)
+        idx = [int(t) for t in self._token_rows(tokens)]
+        self._b_st.copy_(torch.tensor(idx + pos + pos, dtype=torch.int32))
+        if self.use_graph and self._graph_b is None:
+            g = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.graph(g, stream=side):
+                self._decode_batch_launch()
+            torch.cuda.current_stream().wait_stream(side)
+            self._graph_b = g
+        for _ in range(n):
+            if self.use_graph:
+                self._graph_b.replay()
+            else:
+                self._decode_batch_launch()
+        if not sync:
+            return None
+        return (_down(self._b_ring_tok[:n]).astype(np.int64), self._b_ring_rows[:n].cpu().numpy())
+
+    def prefill_batch(self, prompts) -> list[list[np.ndarray]]:
+        """Reallocate the KV caches with B = len(prompts) slots and prefill prompt b into slot b
+        (the launches of prefill()); returns each prompt's prefill logits rows."""
+        self._alloc_kv(len(prompts))
+        out = []
+        for b, p in enumerate(prompts):
+            self._slot = b
+            out.append(self.prefill(p))
+        self._slot = 0
+        return out
+
+    def generate_batch(self, prompts, n_tokens: int) -> list[dict]:
+        """Greedy generation of B = len(prompts) independent sequences of one prompt length: each
+        prompt is prefilled into its own KV-cache slot, then every decode launch runs the B
+        sequences together as B rows.  Record b equals generate(prompts[b], n_tokens) run alone
+        (the same golden.json record).  Reallocates the KV caches with B slots."""
+        if not isinstance(n_tokens, int) or n_tokens < 0:
+            raise ValueError("n_tokens must be a nonnegative integer")
+        prompts = [[int(t) for t in p] for p in prompts]
+        if not prompts or any(not p for p in prompts):
+            raise ValueError("empty prompt")
+        L = len(prompts[0])
+        if any(len(p) != L for p in prompts):
+            raise ValueError("generate_batch needs prompts of one length")
+        if L + n_tokens > self.max_seq:
+            raise ValueError(f"prompt + tokens = {L + n_tokens} exceeds max_seq={self.max_seq}")
+        B = len(prompts)
+        recs, nxt = [], []
+        for b, (p, rows) in enumerate(zip(prompts, self.prefill_batch(prompts))):
+            steps, argm, lrows = [], [], []
+            for c in range(math.ceil(L / self.prefill_m)):
+                last = min(L, (c + 1) * self.prefill_m) - 1
+                steps.append({"kind": "prefill", "pos": c * self.prefill_m, "rows": self.prefill_m,
+                              "valid_rows": last + 1 - c * self.prefill_m})
+                argm.append(self.argmax(rows[last], self.vocab))
+                lrows.append([int(v) for v in rows[last][:self.vocab]])
+            recs.append((steps, argm, lrows))
+            nxt.append(argm[-1])
+        n_dec = min(n_tokens, self.max_seq - L - 1)
+        toks = rows_dev = None
+        if n_dec > 0:
+            toks, rows_dev = self.decode_batch_loop(nxt, [L] * B, n_dec)
+        out = []
+        for b, (steps, argm, lrows) in enumerate(recs):
+            generated, cur = [], nxt[b]
+            for i in range(n_tokens):
+                generated.append(cur)
+                if L + i + 1 >= self.max_seq:
+                    break
+                steps.append({"kind": "decode", "pos": L + i, "rows": 1, "valid_rows": 1})
+                argm.append(int(toks[i][b]))
+                lrows.append(rows_dev[i][b].tolist())
+                cur = int(toks[i][b])
+            out.append({"prompt_tokens": prompts[b], "generated": generated, "argmax_per_step": argm,
+                        "logits_last_rows": lrows, "steps": steps,
+                        "model": {"vocab": self.vocab, "vocab_padded": self.vocab_padded, "E_LOGIT": self.E_LOGIT,
+                                  "E_RES": self.E_RES, "max_seq": self.max_seq}})
+        return out
 
     # ---- measurement aids ------------------------------------------------------------------
     def capture_steps(self, kinds, pos: int):

@@ -23,7 +23,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_workspace():
     L = _lib.lib()
-    assert L.llhip_abi_version() == 1
+    assert L.llhip_abi_version() == 2
     assert L.llhip_workspace_bytes() >= 8 << 20
 
 
@@ -53,7 +53,8 @@ def test_errors_are_reported_without_a_gpu():
     assert rc == -22
     assert b"shift" in L.llhip_last_error()
     with pytest.raises(ValueError, match="prob_bits"):
-        _lib.call("llhip_attention", None, 1, 1, 1, 16, 16, 0, None, None, None, 1, 1, 0, 1, 0, 9, None, 16, None, None)
+        _lib.call("llhip_attention", None, 1, 1, 1, 16, 16, 0, None, None, 0, None, None, 1, 1, 0, 1, 0, 9, None, 16, None,
+                  None)
 
 
 def test_product_does_not_import_the_oracle():

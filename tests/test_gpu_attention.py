@@ -18,8 +18,8 @@ def gpu_attention(q, kc, vc, pos, H, Hkv, D, Ms, Ss, Mo, So, pb):
     M = q.shape[0]
     qd, kd, vd = up(q, np.int8), up(kc, np.int8), up(vc, np.int8)
     out = t.empty((M, H * D), dtype=t.int8, device="cuda")
-    _lib.call("llhip_attention", ptr(qd), M, H, Hkv, D, H * D, pos, None, ptr(kd), ptr(vd), kc.shape[1], Ms, Ss, Mo,
-              So, pb, ptr(out), H * D, ptr(workspace()), stream())
+    _lib.call("llhip_attention", ptr(qd), M, H, Hkv, D, H * D, pos, None, None, 0, ptr(kd), ptr(vd), kc.shape[1], Ms,
+              Ss, Mo, So, pb, ptr(out), H * D, ptr(workspace()), stream())
     return down(out)
 
 
@@ -63,16 +63,16 @@ def test_kv_write_and_positions():
     kc = t.zeros((Hkv, max_seq, D), dtype=t.int8, device="cuda")
     vc = t.zeros_like(kc)
     kd, vd = up(k, np.int8), up(v, np.int8)
-    _lib.call("llhip_kv_write", ptr(kd), ptr(vd), M, Hkv, D, Hkv * D, Hkv * D, 100, None, ptr(kc), ptr(vc), max_seq,
-              stream())
+    _lib.call("llhip_kv_write", ptr(kd), ptr(vd), M, Hkv, D, Hkv * D, Hkv * D, 100, None, None, 0, ptr(kc), ptr(vc),
+              max_seq, stream())
     want = np.zeros((Hkv, max_seq, D), np.int64)
     want[:, 100:116] = k.reshape(M, Hkv, D).transpose(1, 0, 2)
     assert np.array_equal(down(kc), want)
     want[:, 100:116] = v.reshape(M, Hkv, D).transpose(1, 0, 2)
     assert np.array_equal(down(vc), want)
     with pytest.raises(ValueError, match="max_seq"):
-        _lib.call("llhip_kv_write", ptr(kd), ptr(vd), M, Hkv, D, Hkv * D, Hkv * D, 250, None, ptr(kc), ptr(vc),
-                  max_seq, stream())
+        _lib.call("llhip_kv_write", ptr(kd), ptr(vd), M, Hkv, D, Hkv * D, Hkv * D, 250, None, None, 0, ptr(kc),
+                  ptr(vc), max_seq, stream())
 
 
 def test_device_position():
@@ -86,7 +86,45 @@ def test_device_position():
     qd, kd, vd = up(q, np.int8), up(kc, np.int8), up(vc, np.int8)
     posd = t.tensor([600], dtype=t.int32, device="cuda")
     out = t.empty((1, H * D), dtype=t.int8, device="cuda")
-    _lib.call("llhip_attention", ptr(qd), 1, H, Hkv, D, H * D, 0, ptr(posd), ptr(kd), ptr(vd), max_seq, 1 << 30, 40,
-              1 << 30, 38, 15, ptr(out), H * D, ptr(workspace()), stream())
+    _lib.call("llhip_attention", ptr(qd), 1, H, Hkv, D, H * D, 0, ptr(posd), None, 0, ptr(kd), ptr(vd), max_seq,
+              1 << 30, 40, 1 << 30, 38, 15, ptr(out), H * D, ptr(workspace()), stream())
     assert np.array_equal(down(out), O.attention_c(q, kc.astype(np.int8), vc.astype(np.int8), 600, H, Hkv, D,
                                                    1 << 30, 40, 1 << 30, 38, 15))
+
+
+@pytest.mark.parametrize("D,H,Hkv", [(64, 14, 2), (128, 16, 8), (16, 4, 2)])
+def test_rows_as_sequences(D, H, Hkv):
+    """Batch decode form: row m is its own sequence at position row_pos[m] with its caches in slot m.
+    Each row equals a single-row launch over its own caches (oracle), and kv_write stores each row
+    in its own slot at its own position."""
+    t = __import__("torch")
+    rng = np.random.default_rng(D + H)
+    B, max_seq = 5, 300
+    positions = np.array([0, 17, 299, 128, 63], np.int32)
+    kc = rng.integers(-128, 128, (B, Hkv, max_seq, D))
+    vc = rng.integers(-128, 128, (B, Hkv, max_seq, D))
+    q = rng.integers(-128, 128, (B, H * D))
+    kd, vd, qd = up(kc, np.int8), up(vc, np.int8), up(q, np.int8)
+    rp = t.tensor(positions, dtype=t.int32, device="cuda")
+    stride = Hkv * max_seq * D
+    # the new K/V rows go to each sequence's slot at its position
+    knew = rng.integers(-128, 128, (B, Hkv * D))
+    vnew = rng.integers(-128, 128, (B, Hkv * D))
+    knd, vnd = up(knew, np.int8), up(vnew, np.int8)  # held until the launch has run
+    _lib.call("llhip_kv_write", ptr(knd), ptr(vnd), B, Hkv, D, Hkv * D, Hkv * D, 0, None, ptr(rp), stride, ptr(kd),
+              ptr(vd), max_seq, stream())
+    for b in range(B):
+        kc[b][:, positions[b]] = knew[b].reshape(Hkv, D)
+        vc[b][:, positions[b]] = vnew[b].reshape(Hkv, D)
+    assert np.array_equal(down(kd), kc) and np.array_equal(down(vd), vc)
+    out = t.empty((B, H * D), dtype=t.int8, device="cuda")
+    _lib.call("llhip_attention", ptr(qd), B, H, Hkv, D, H * D, 0, None, ptr(rp), stride, ptr(kd), ptr(vd), max_seq,
+              1 << 30, 40, 1 << 30, 38, 8, ptr(out), H * D, ptr(workspace()), stream())
+    got = down(out)
+    for b in range(B):
+        want = O.attention_c(q[b:b + 1], kc[b].astype(np.int8), vc[b].astype(np.int8), int(positions[b]), H, Hkv, D,
+                             1 << 30, 40, 1 << 30, 38, 8)
+        assert np.array_equal(got[b:b + 1], want), b
+    with pytest.raises(ValueError, match="slots overlap"):
+        _lib.call("llhip_attention", ptr(qd), B, H, Hkv, D, H * D, 0, None, ptr(rp), stride - 1, ptr(kd), ptr(vd),
+                  max_seq, 1 << 30, 40, 1 << 30, 38, 8, ptr(out), H * D, ptr(workspace()), stream())

@@ -163,3 +163,52 @@ def test_whole_prompt_prefill_equals_chunked(golden_dir, name, plen):
         assert np.array_equal(g1.kv[layer][0], g2.kv[layer][0]) and np.array_equal(g1.kv[layer][1], g2.kv[layer][1])
     g1.reset(), g2.reset()
     assert g1.generate(prompt, 5) == g2.generate(prompt, 5) == O.OracleModel(qdir, "c").generate(prompt, 5)
+
+
+@pytest.mark.parametrize("name,B,L,n", [("ref_tiny_v2", 4, 10, 30), ("ref_tiny_v2_pad", 16, 17, 12),
+                                        ("ref_tiny_v1", 3, 5, 58)])
+def test_generate_batch_equals_single_sequences(golden_dir, name, B, L, n):
+    """Batch decode (config 4's batch-16 form): B sequences with their own prompts, KV slots and
+    positions run as the B rows of one launch; every record equals the sequence's own generate()
+    run alone and the oracle's.  n reaches max_seq in the last case (the record stops there)."""
+    qdir = golden_dir / name / "qgraph"
+    prompts = [synth.seeded_prompt("tiny", L, 40 + b) for b in range(B)]
+    g = G.GoldenModel(qdir)
+    recs = g.generate_batch(prompts, n)
+    single = G.GoldenModel(qdir)
+    o = O.OracleModel(qdir, backend="c")
+    for b in range(B):
+        want = single.generate(prompts[b], n)
+        assert recs[b] == want, b
+        if b in (0, B - 1):
+            assert want == o.generate(prompts[b], n), b
+    # the KV slot of the last sequence equals its single-sequence caches
+    g._slot = B - 1
+    for layer, (k, v) in g.kv.items():
+        assert np.array_equal(k, single.kv[layer][0]) and np.array_equal(v, single.kv[layer][1]), layer
+    g._slot = 0
+    # eager batch launches (no graph) give the same records
+    g.use_graph = False
+    assert g.generate_batch(prompts[:2], 6) == [single.generate(p, 6) for p in prompts[:2]]
+
+
+def test_generate_batch_qwen_shape(tmp_path):
+    """Qwen2.5 GQA shape with QKV bias (reduced to 2 layers, vocab 4096): batch of 4 sequences of
+    24 tokens + 6 decode launches, each equal to its single-sequence run."""
+    import dataclasses
+
+    cfg = dataclasses.replace(synth.CONFIGS["qwen25"], n_layers=2, vocab=4096, max_seq=64, name="q25s")
+    qdir = synth.build_qgraph(tmp_path / "q25s", cfg, seed=5)
+    prompts = [synth.seeded_prompt(cfg, 24, 7 + b) for b in range(4)]
+    g, single = G.GoldenModel(qdir), G.GoldenModel(qdir)
+    recs = g.generate_batch(prompts, 6)
+    for b in range(4):
+        assert recs[b] == single.generate(prompts[b], 6), b
+
+
+def test_generate_batch_errors(golden_dir):
+    g = G.GoldenModel(golden_dir / "ref_tiny_v2" / "qgraph")
+    with pytest.raises(ValueError, match="one length"):
+        g.generate_batch([[1, 2], [3]], 2)
+    with pytest.raises(ValueError, match="max_seq"):
+        g.generate_batch([[1, 2]], 63)
