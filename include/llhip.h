@@ -142,7 +142,13 @@ typedef struct llhip_norm_quant_desc {
   void* h_out;       /* i16 [M][ldx] normalised rows, or NULL */
   void* hq_out;      /* i8 [M][K] quantised rows, or NULL */
   int64_t ldx, K, eps_t, C, sh_post, Mq, Sq;
+  int64_t prequant;  /* fused kernels: nonzero when h_out/hq_out already hold the rows (written by
+                      * llhip_rmsnorm_quant); the kernel then reads hq_out instead of normalising x */
 } llhip_norm_quant_desc;
+
+/* golden.py:124-137 + 119-120  rmsnorm then quant of M rows in one launch (one workgroup per row):
+ * h_out = rmsnorm(x), hq_out = quant(h_out).  Multi-row fused launches run it first (prequant). */
+int llhip_rmsnorm_quant(const llhip_norm_quant_desc* d, int64_t M, void* stream);
 
 typedef struct llhip_attn_in_desc {
   llhip_norm_quant_desc pre;

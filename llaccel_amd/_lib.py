@@ -49,6 +49,7 @@ _SIGS = {
     "llhip_argmax_i16": [_p, _i64, _i64, _i64, _p, _p],
     "llhip_greedy_step": [_p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],
     "llhip_greedy_rows": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p],
+    "llhip_rmsnorm_quant": [_p, _i64, _p],
 }
 _RESTYPES = {"llhip_last_error": ctypes.c_char_p, "llhip_workspace_bytes": _i64}
 
@@ -102,7 +103,7 @@ def call(name: str, *args) -> None:
 # ---- descriptors of the fused entry points (include/llhip.h) -------------------------------
 class NormQuantDesc(ctypes.Structure):
     _fields_ = [("x", _p), ("gamma", _p), ("h_out", _p), ("hq_out", _p), ("ldx", _i64), ("K", _i64), ("eps_t", _i64),
-                ("C", _i64), ("sh_post", _i64), ("Mq", _i64), ("Sq", _i64)]
+                ("C", _i64), ("sh_post", _i64), ("Mq", _i64), ("Sq", _i64), ("prequant", _i64)]
 
 
 class AttnInDesc(ctypes.Structure):

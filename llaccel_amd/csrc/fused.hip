@@ -39,6 +39,7 @@ struct NormQuant {
   int64_t Mq;       // quant multiplier
   uint32_t eps_t, C;
   int sh_post, Sq, K;
+  int prequant;     // rows already normalised + quantised into h_out/hq_out
 };
 
 constexpr int NORM_MAX_K = 1024;  // a row's sum of squares takes chunks lane and lane + 64
@@ -148,6 +149,87 @@ __device__ void norm_quant_rows(const NormQuant& pr, const NormRegs& r, int M, c
       const int u = u0 + lane;
       const v2i xu = ld8(xr, u < nu ? row + 8 * u : LD_OOB), gu = ld8(gr, u < nu ? 8 * u : LD_OOB);
       norm_apply_unit(pr, m, u, inv, xu, gu, a_lds, lda, write_global);
+    }
+  }
+}
+
+// Rows already quantised by llhip_rmsnorm_quant (multi-row launches): the i8 rows [M][K] are
+// loaded at kernel entry (16-byte chunks, PRE_CHUNKS per thread) and staged in LDS.
+// Normalising M > 1 rows in every workgroup would repeat the whole row prologue per workgroup.
+constexpr int PRE_CHUNKS = 8;
+
+struct PreRows {
+  v4i c[PRE_CHUNKS];
+};
+
+__device__ __forceinline__ void prerows_load(const NormQuant& pr, int M, PreRows& r) {
+  const int nt = blockDim.x, tid = threadIdx.x, total = M * (pr.K >> 4);
+  const Rsrc q = rsrc(pr.hq_out, (int64_t)M * pr.K);
+#pragma unroll
+  for (int i = 0; i < PRE_CHUNKS; ++i) {
+    const int c = tid + i * nt;
+    r.c[i] = ld16(q, c < total ? 16 * c : LD_OOB);
+  }
+}
+
+__device__ __forceinline__ void prerows_store(const NormQuant& pr, int M, const PreRows& r, int8_t* a_lds, int lda) {
+  const int nt = blockDim.x, tid = threadIdx.x, nch = pr.K >> 4, total = M * nch;
+#pragma unroll
+  for (int i = 0; i < PRE_CHUNKS; ++i) {
+    const int c = tid + i * nt;
+    if (c < total) *reinterpret_cast<v4i*>(a_lds + (c / nch) * lda + 16 * (c % nch)) = r.c[i];
+  }
+  // small workgroups: the chunks beyond the prefetched ones
+  const Rsrc q = rsrc(pr.hq_out, (int64_t)M * pr.K);
+  for (int c = tid + PRE_CHUNKS * nt; c < total; c += nt)
+    *reinterpret_cast<v4i*>(a_lds + (c / nch) * lda + 16 * (c % nch)) = ld16(q, 16 * c);
+}
+
+// standalone rmsnorm + quant, one workgroup (256 threads) per row: thread t takes chunk t
+__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(NormQuant pr) {
+  __shared__ uint64_t part[4];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nch = pr.K >> 3;
+  const Rsrc xr = rsrc(pr.x + (int64_t)m * pr.ldx, (int64_t)pr.K * 2), gr = rsrc(pr.gamma, (int64_t)pr.K * 2);
+  v4i x[NORM_MAX_K / 8 / 256 + 1], g[NORM_MAX_K / 8 / 256 + 1];
+  uint64_t ss = 0;
+#pragma unroll
+  for (int i = 0; i < NORM_MAX_K / 8 / 256 + 1; ++i) {
+    const int c = tid + 256 * i;
+    x[i] = ld16(xr, c < nch ? 16 * c : LD_OOB);
+    g[i] = ld16(gr, c < nch ? 16 * c : LD_OOB);
+  }
+#pragma unroll
+  for (int i = 0; i < NORM_MAX_K / 8 / 256 + 1; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t a = lo16(x[i][j]), c = hi16(x[i][j]);
+      ss += (uint32_t)(a * a) + (uint32_t)(c * c);
+    }
+  ss = wave_sum_u64(ss);
+  if (lane == 0) part[wave] = ss;
+  __syncthreads();
+  const uint32_t inv = rms_inv(part[0] + part[1] + part[2] + part[3], pr.eps_t, pr.C);
+#pragma unroll
+  for (int i = 0; i < NORM_MAX_K / 8 / 256 + 1; ++i) {
+    const int c = tid + 256 * i;
+    if (c >= nch) break;
+    v4i y;
+    uint32_t qw[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int16_t y0 = rms_apply(lo16(x[i][j]), lo16(g[i][j]), inv, pr.sh_post);
+      const int16_t y1 = rms_apply(hi16(x[i][j]), hi16(g[i][j]), inv, pr.sh_post);
+      y[j] = pack16(y0, y1);
+      const uint32_t q0 = (uint8_t)sat8(mulshift(y0, pr.Mq, pr.Sq));
+      const uint32_t q1 = (uint8_t)sat8(mulshift(y1, pr.Mq, pr.Sq));
+      qw[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
+    }
+    if (pr.h_out) *reinterpret_cast<v4i*>(pr.h_out + (int64_t)m * pr.ldx + 8 * c) = y;
+    if (pr.hq_out) {
+      v2i q2;
+      q2.x = (int)qw[0];
+      q2.y = (int)qw[1];
+      *reinterpret_cast<v2i*>(pr.hq_out + (int64_t)m * pr.K + 8 * c) = q2;
     }
   }
 }
@@ -307,7 +389,11 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   issue_fence();
   const NormMap nm = norm_map(M);
   NormRegs nr;
-  norm_prefetch(p.pre, M, nm, nr);
+  PreRows pq;
+  if (p.pre.prequant)
+    prerows_load(p.pre, M, pq);
+  else
+    norm_prefetch(p.pre, M, nm, nr);
   issue_fence();
   const Rsrc wr = rsrc(pick3(role, p.W), (int64_t)Nrole * p.K);
   WSlice ws;
@@ -331,7 +417,10 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   }
   issue_fence();
 
-  norm_quant_rows(p.pre, nr, M, nm, a_lds, lda, b == 0);
+  if (p.pre.prequant)
+    prerows_store(p.pre, M, pq, a_lds, lda);
+  else
+    norm_quant_rows(p.pre, nr, M, nm, a_lds, lda, b == 0);
   const int pos0 = p.pos_dev ? __builtin_amdgcn_readfirstlane(posv) : p.pos;
   const bool rows = p.row_pos != nullptr;
   if (tid < M) rowpos[tid] = rows ? rp_own : pos0 + tid;
@@ -458,7 +547,11 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
 
   const NormMap nm = norm_map(p.M);
   NormRegs nr;
-  norm_prefetch(p.pre, p.M, nm, nr);
+  PreRows pq;
+  if (p.pre.prequant)
+    prerows_load(p.pre, p.M, pq);
+  else
+    norm_prefetch(p.pre, p.M, nm, nr);
   issue_fence();
   SigRegs sr;
   sig_prefetch(sr);
@@ -479,7 +572,10 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   const int32_t buv = ld4(rsrc(p.bu, (int64_t)p.N * 4), o4);
   issue_fence();
 
-  norm_quant_rows(p.pre, nr, p.M, nm, dyn, lda, blockIdx.x == 0);
+  if (p.pre.prequant)
+    prerows_store(p.pre, p.M, pq, dyn, lda);
+  else
+    norm_quant_rows(p.pre, nr, p.M, nm, dyn, lda, blockIdx.x == 0);
   sig_store(sr, sig32);
   __syncthreads();
   red[wave][lane] = wslice_mfma(ws, wr, dyn, lda, p.M, p.K);
@@ -538,7 +634,11 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
 
   const NormMap nm = norm_map(p.M);
   NormRegs nr;
-  norm_prefetch(p.pre, p.M, nm, nr);
+  PreRows pq;
+  if (p.pre.prequant)
+    prerows_load(p.pre, p.M, pq);
+  else
+    norm_prefetch(p.pre, p.M, nm, nr);
   issue_fence();
   SigRegs sr;
   sig_prefetch(sr);
@@ -565,7 +665,10 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
   }
   issue_fence();
 
-  norm_quant_rows(p.pre, nr, p.M, nm, dyn, lda, blockIdx.x == 0);
+  if (p.pre.prequant)
+    prerows_store(p.pre, p.M, pq, dyn, lda);
+  else
+    norm_quant_rows(p.pre, nr, p.M, nm, dyn, lda, blockIdx.x == 0);
   sig_store(sr, sig32);
   __syncthreads();
   v4i acc = wslice_mfma(ws, wr, dyn, lda, p.M, p.K);
@@ -619,6 +722,8 @@ static int fill_pre(NormQuant& pr, const llhip_norm_quant_desc& d) {
   pr.sh_post = (int)d.sh_post;
   pr.Sq = (int)d.Sq;
   pr.K = (int)d.K;
+  pr.prequant = d.prequant ? 1 : 0;
+  if (pr.prequant && !d.hq_out) return fail(-EINVAL, "fused rmsnorm: prequant needs the quantised rows (hq_out)");
   return 0;
 }
 
@@ -640,6 +745,19 @@ static int pick_ks(int64_t blocks, int per_split_waves, int steps, int max_waves
 }  // namespace llhip
 
 using namespace llhip;
+
+extern "C" int llhip_rmsnorm_quant(const llhip_norm_quant_desc* d, int64_t M, void* stream) {
+  if (!d) return fail(-EINVAL, "rmsnorm_quant: null descriptor");
+  NormQuant pr{};
+  int rc = fill_pre(pr, *d);
+  if (rc) return rc;
+  if (M < 0 || M > INT32_MAX) return fail(-EINVAL, "rmsnorm_quant: bad row count");
+  if (!d->hq_out && !d->h_out) return fail(-EINVAL, "rmsnorm_quant: no output");
+  if (M == 0) return 0;
+  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream, pr);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
 
 extern "C" int llhip_attn_in(const llhip_attn_in_desc* d, void* stream) {
   if (!d) return fail(-EINVAL, "attn_in: null descriptor");

@@ -13,6 +13,7 @@
 //    each wave 64x128 (64x64) with v_mfma_i32_32x32x32_i8; A and W double-buffered in LDS.
 //    Blocks are numbered XCD-major so the blocks that share a W panel run on one
 //    XCD and share its L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "../../include/llhip.h"
@@ -37,6 +38,7 @@ struct LinearArgs {
   int M, K, N;
   int aux_shift, Si, sh;
   int steps;  // ceil(K / 64)
+  int cpb;    // linear_gemv: output columns per workgroup (16, or 8 / 4 to spread narrow outputs)
 };
 
 // requant + epilogue of one output element (golden.py:323-342)
@@ -124,10 +126,10 @@ __global__ __launch_bounds__(64 * GEMV_MAX_WAVES) void linear_gemv(LinearArgs p)
   const int nw = blockDim.x >> 6;
   const int col = lane & 15;
   const int kg = lane >> 4;
-  const int tile = blockIdx.x;
+  const int tile = blockIdx.x;  // columns [tile * cpb, tile * cpb + cpb): lanes col >= cpb carry zero weights
   const int m0 = blockIdx.z * 16;
-  const int n = tile * 16 + col;
-  const bool nvalid = n < p.N;
+  const int n = tile * p.cpb + col;
+  const bool nvalid = col < p.cpb && n < p.N;
   const int nn = nvalid ? n : 0;
   const bool avalid = m0 + col < p.M;
   const int8_t* wrow = p.W + (int64_t)nn * p.K;
@@ -686,11 +688,19 @@ static int launch_linear(LinearArgs& p, hipStream_t stream) {
     return 0;
   }
   const int zblocks = (int)ceil_div(p.M, 16);
-  // waves per workgroup: enough waves on the chip to keep HBM busy, never more than K steps
-  const int target_waves = 8 * current_cu_count();
+  const int cus = current_cu_count();
   int nw = 1;
-  while (nw < GEMV_MAX_WAVES && (int64_t)tiles * zblocks * nw * 2 <= target_waves && nw * 2 <= p.steps) nw *= 2;
-  dim3 grid(tiles, 1, zblocks);
+  p.cpb = 16;
+  if ((int64_t)tiles * zblocks >= cus) {
+    // waves per workgroup: enough waves on the chip to keep HBM busy, never more than K steps
+    while (nw < GEMV_MAX_WAVES && (int64_t)tiles * zblocks * nw * 2 <= 8 * cus && nw * 2 <= p.steps) nw *= 2;
+  } else {
+    // narrow output (a decode projection of a few rows): fewer columns per workgroup so that every
+    // CU streams a share of W, and enough waves that each wave's K slice is loaded at entry
+    while (p.cpb > 4 && ceil_div(p.N, p.cpb) * zblocks < cus) p.cpb /= 2;
+    nw = (int)std::min<int64_t>(GEMV_MAX_WAVES, ceil_div(p.steps, GEMV_PF));
+  }
+  dim3 grid((unsigned)ceil_div(p.N, p.cpb), 1, zblocks);
   if (aligned)
     hipLaunchKernelGGL((linear_gemv<EPI, OUT8, true>), grid, dim3(64 * nw), 0, stream, p);
   else

@@ -44,6 +44,10 @@ class FusedStep:
             return
         self.fill(self.desc, M, pos, pd)
         m = self.model
+        # several rows: normalise them once (one launch) instead of in every workgroup's prologue
+        self.desc.pre.prequant = int(M > 1)
+        if M > 1:
+            _lib.call("llhip_rmsnorm_quant", ctypes.byref(self.desc.pre), M, m._stream_handle())
         _lib.call(self.entry, ctypes.byref(self.desc), m._stream_handle())
 
 
