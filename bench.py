@@ -8,15 +8,19 @@ batch 1, after a 512-token prefill.  One step = one M=1 decode launch of the who
 graph, with weights, KV cache and activations resident in HBM.
 
 The JSON line also carries
-  roofline     : the decode GEMV kernel family (llhip linear_skinny), algorithmic bytes per
-                 launch / average launch duration measured with HIP events on its stream,
-                 against 8 TB/s;
+  roofline     : the decode kernel family with the most time per step: algorithmic bytes per
+                 launch / average launch duration (HIP events around a graph of that family's
+                 launches), against 8 TB/s; `traffic` is the HBM bytes per launch measured with
+                 rocprofv3 counters (profiles/decode_traffic.json, copy-kernel calibrated);
   cpu_baseline : the CPU oracle's numpy restatement of golden.py (int64 `a @ w.T`, Python
                  attention loop -- the reference's own structure) timed on a bounded sample
                  of the same decode launches on this host, and checked equal to the GPU's;
-  extra        : prefill tok/s, attention bytes/s, config-2 GEMM TOPS and GB/s.
+  extra        : prefill tok/s, per-family decode timings, config 4 at batch 16, config-2
+                 GEMM TOPS and GB/s.
 
     python bench.py [--gpus 1] [--steps 64] [--warmup 8]
+    python bench.py --profile decode   # prefill + decode launches only (for rocprofv3)
+    python bench.py --profile copy     # 256 MiB device copies (counter calibration)
 """
 from __future__ import annotations
 
@@ -83,6 +87,21 @@ def batch_decode(qdir: Path, args, single_tokens) -> dict:
     return {"batch": B, "tok_s": round(B * args.steps / dt, 1), "ms_per_step": round(dt / args.steps * 1e3, 4),
             "steps": args.steps, "prefill_ms_all": round(t_pre * 1e3, 1),
             "sequence0_tokens_equal_batch1": same}
+
+
+# decode kernel of each plan-step family (rocprofv3 kernel names)
+FAMILY_KERNEL = {"attn_in": "attn_in_kernel", "attention": "attention_rowhead", "mlp_in": "mlp_in_kernel",
+                 "linear": "linear_gemv1", "norm_linear": "norm_gemv_kernel"}
+
+
+def measured_traffic(family: str):
+    """HBM bytes (fetched + written) per launch of a decode kernel family, from the committed
+    rocprofv3 counter summary (profiles/decode_traffic.json), or None when not measured."""
+    f = REPO / "profiles" / "decode_traffic.json"
+    if not f.exists():
+        return None
+    k = json.loads(f.read_text()).get("kernels", {}).get(FAMILY_KERNEL.get(family, ""))
+    return None if k is None else int(k["fetch_bytes"] + k["write_bytes"])
 
 
 def time_graph(graph, reps: int) -> float:
@@ -176,6 +195,7 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--batch", type=int, default=16, help="also time config 4's batch decode (1 = skip)")
+    ap.add_argument("--profile", choices=("decode", "copy"), help="workload-only runs for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs the datapath on a "
@@ -183,6 +203,17 @@ def main() -> None:
         sys.exit(2)
 
     import torch
+
+    if args.profile == "copy":
+        # counter calibration: device-to-device copies of a known size
+        n = 256 << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {n} bytes x 10")
+        return
 
     from llaccel_amd import golden as G
 
@@ -216,6 +247,8 @@ def main() -> None:
     dt = time.perf_counter() - t0
     tok_s = args.steps / dt
     log(f"decode: {args.steps} steps in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
+    if args.profile == "decode":
+        return
 
     # ---- per-kernel families of one decode step (graphs of the step's launches of one kind) ----
     T = L + args.warmup + args.steps
@@ -237,7 +270,7 @@ def main() -> None:
     achieved = d["bytes_per_launch"] / (d["us_per_launch"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": f"{dom} (decode, M=1; {d['launches']} launches per step)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                 "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": d["us_per_launch"]}
     step_bytes = sum(fam[k]["bytes_per_launch"] * fam[k]["launches"] for k in fam)
 

@@ -88,10 +88,15 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   constexpr int TG = ATTN_THREADS / DC;
   constexpr int VPF = 8;
 
-  const int h = blockIdx.x;
+  // GQA group g runs on XCD g % 8 (workgroup b is dispatched to XCD b % 8), so the G = H/Hkv
+  // query heads that read one group's K/V share that XCD's L2: block b -> group
+  // (b % 8) + 8 * ((b / 8) / G), head j = (b / 8) % G of it.  Blocks past the groups exit.
+  const int G = p.H / p.Hkv;
+  const int g = (int)(blockIdx.x % 8) + 8 * (int)((blockIdx.x / 8) / G);
+  if (g >= p.Hkv) return;
+  const int h = g * G + (int)((blockIdx.x / 8) % G);
   const int m = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int g = h / (p.H / p.Hkv);
   // Loads in order of use: q and the keys of the first score pass, the LUT dwords (wave 0), the
   // value rows of this thread's first VPF keys.  Key rows at or past T read zeros.
   // row m's context: T = position + 1 (row m of a launch at pos sits at pos + m; with per-row
@@ -331,7 +336,7 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   p.pb = (int)prob_bits;
   p.lds_T = (int)((tmax + 3) / 4 * 4);
   const size_t lds = sizeof(int32_t) * (size_t)p.lds_T;
-  dim3 grid((unsigned)H, (unsigned)M);
+  dim3 grid((unsigned)(8 * (H / Hkv) * ceil_div(Hkv, 8)), (unsigned)M);
   dim3 block(ATTN_THREADS);
   hipStream_t s = (hipStream_t)stream;
   switch (D) {
