@@ -34,6 +34,7 @@ struct AttnArgs {
   int Ss, So;
   int H, Hkv, pos, pb;
   int lds_T;  // score slots in LDS
+  int M;
 };
 
 constexpr int ATTN_THREADS = 512;
@@ -255,6 +256,213 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// attention_tiled: M >= 2 rows at consecutive positions pos.. (prefill, chunked prefill)
+// ---------------------------------------------------------------------------------------
+// One workgroup per (block of 16 query rows, query head); its waves split the 64-key tiles of the
+// block's context.  Each of the three reductions is one pass over the tiles, and every pass
+// recomputes the tile's scores with v_mfma_i32_16x16x64_i8 (cheap next to a round trip of the
+// scores through LDS):
+//   S^T = K . Q^T : A = 16 key rows, B = the 16 query rows, so lane (lg = lane / 16, lr = lane % 16)
+//                   holds query row lr's scores of keys 16j + 4lg + r (subtile j, register r);
+//   O = P . V     : A = P with row lr and byte 4j + r <-> key 16j + 4lg + r -- exactly the score
+//                   layout, so the probabilities never leave the lane -- and B = V^T in the same key
+//                   order, made by multiplying 16-key blocks of V (as A) by 0/1 selection matrices:
+//                   C[key][n] = V[key][16e + n], which lands key 16b + 4lg + r, column 16e + lr in
+//                   lane (lg, lr) register r.
+// The probabilities pn < 2^15 enter the int8 MFMA as base-128 digits (pn = d0 + 128 d1 + 16384 d2,
+// each digit in [0, 127]), so O = O0 + 128 O1 + 16384 O2 is the exact integer sum.  The operand
+// byte order inside a lane (which K index a byte feeds) is the same for A and B, so neither
+// product depends on it.  Keys at or past a row's T get probability 0; keys past the block's last
+// row read zeros.
+constexpr int AT_ROWS = 16;
+constexpr int AT_MIN_M = 2;       // launches of fewer rows use attention_rowhead
+constexpr int AT_MAX_T = 32767;   // per-row sum of T probabilities < 2^31
+
+template <int D>
+struct AttnTileCfg {
+  static constexpr int DK = (D + 63) / 64;  // 64-byte K chunks of a key row
+  static constexpr int DB = D / 16;         // 16-column blocks of the output
+  static constexpr int MAXW = D <= 64 ? 16 : (D == 128 ? 8 : 4);
+};
+
+__device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000c0cu);
+  return lo | hi;
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(AttnArgs p) {
+  using C = AttnTileCfg<D>;
+  constexpr int DK = C::DK, DB = C::DB;
+  __shared__ uint32_t lut32[LUT_DW];
+  __shared__ int32_t red[C::MAXW][AT_ROWS];
+  __shared__ int32_t osum[AT_ROWS][D];
+  const int G = p.H / p.Hkv;
+  const int g = (int)(blockIdx.x % 8) + 8 * (int)((blockIdx.x / 8) / G);
+  if (g >= p.Hkv) return;
+  const int h = g * G + (int)((blockIdx.x / 8) % G);
+  const int m0 = blockIdx.y * AT_ROWS;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int nw = blockDim.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int pos = load_pos(p.pos_dev, p.pos);
+  const int mlast = min(m0 + AT_ROWS, p.M) - 1;
+  const int Tb = min(pos + mlast + 1, (int)p.max_seq);  // keys any row of the block sees
+  const int ntiles = (Tb + 63) >> 6;
+  const int m = m0 + lr;  // this lane's query row
+  const int tlim = m < p.M ? min(pos + m + 1, (int)p.max_seq) : 0;
+  const int8_t* kbase = p.kc + (int64_t)g * p.max_seq * D;
+  const int8_t* vbase = p.vc + (int64_t)g * p.max_seq * D;
+  const Rsrc kr = rsrc(kbase, (int64_t)Tb * D), vr = rsrc(vbase, (int64_t)Tb * D);
+
+  v4i qf[DK];
+  {
+    const Rsrc qr = rsrc(p.q + (int64_t)m0 * p.ldq + (int64_t)h * D, (int64_t)AT_ROWS * p.ldq);
+#pragma unroll
+    for (int c = 0; c < DK; ++c)
+      qf[c] = ld16(qr, (m < p.M && 64 * c + 16 * lg < D) ? (uint32_t)(lr * p.ldq + 64 * c + 16 * lg) : LD_OOB);
+  }
+  {
+    const Rsrc ir = rsrc(kExpI, sizeof(kExpI)), fr = rsrc(kExpF, sizeof(kExpF));
+    for (int idx = tid; idx < LUT_DW; idx += blockDim.x)
+      lut32[idx] = (uint32_t)ld4(ir, idx < 8 ? 4 * idx : LD_OOB) | (uint32_t)ld4(fr, idx >= 8 ? 4 * (idx - 8) : LD_OOB);
+    for (int idx = tid; idx < AT_ROWS * D; idx += blockDim.x) (&osum[0][0])[idx] = 0;
+  }
+  // K (or V) fragment of 16-key block j of tile kt: key kt*64 + 16j + lr, bytes [64c + 16lg, +16)
+  auto frag_off = [&](int kt, int j, int c) -> uint32_t {
+    return 64 * c + 16 * lg < D ? (uint32_t)((kt * 64 + 16 * j + lr) * D + 64 * c + 16 * lg) : LD_OOB;
+  };
+  auto scores = [&](int kt, v4i (&st)[4]) {
+    v4i kf[4][DK];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) kf[j][c] = ld16(kr, frag_off(kt, j, c));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      st[j] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int c = 0; c < DK; ++c) st[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[j][c], qf[c], st[j], 0, 0, 0);
+    }
+  };
+  // key of subtile j, register r of tile kt in this lane
+  auto key = [&](int kt, int j, int r) { return kt * 64 + 16 * j + 4 * lg + r; };
+
+  // pass 1: row maxima
+  int32_t vmax = INT32_MIN;
+  for (int kt = wave; kt < ntiles; kt += nw) {
+    v4i st[4];
+    scores(kt, st);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (key(kt, j, r) < tlim) vmax = max(vmax, st[j][r]);
+  }
+  vmax = max(vmax, __shfl_xor(vmax, 16));
+  vmax = max(vmax, __shfl_xor(vmax, 32));
+  if (lg == 0) red[wave][lr] = vmax;
+  __syncthreads();
+  int32_t mx = red[0][lr];
+  for (int w = 1; w < nw; ++w) mx = max(mx, red[w][lr]);
+  __syncthreads();
+
+  // pass 2: sums of the LUT exponentials
+  const uint16_t* ei = reinterpret_cast<const uint16_t*>(lut32);
+  const uint16_t* ef = ei + 16;
+  auto prob = [&](int32_t s) -> uint32_t { return lut_prob_lds(mulshift((int64_t)mx - s, p.Ms, p.Ss), ei, ef); };
+  uint32_t vsum = 0;
+  for (int kt = wave; kt < ntiles; kt += nw) {
+    v4i st[4];
+    scores(kt, st);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (key(kt, j, r) < tlim) vsum += prob(st[j][r]);
+  }
+  vsum += (uint32_t)__shfl_xor((int)vsum, 16);
+  vsum += (uint32_t)__shfl_xor((int)vsum, 32);
+  if (lg == 0) red[wave][lr] = (int32_t)vsum;
+  __syncthreads();
+  uint32_t total = 0;
+  for (int w = 0; w < nw; ++w) total += (uint32_t)red[w][lr];
+  const uint32_t inv = 0x80000000u / (total > 1u ? total : 1u);  // 2^31 / total (golden.py:174)
+  const int64_t cap = (1 << p.pb) - 1;
+  const int shp = 31 - p.pb;
+  const bool three = p.pb > 14;  // pn >= 2^14 possible: a third digit
+
+  // 0/1 selection matrix e: lane (lg, lr) has byte lr set when lg == e
+  v4i sel[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t bit = lg == e ? 1u << (8 * (lr & 3)) : 0u;
+    sel[e] = v4i{(lr >> 2) == 0 ? (int)bit : 0, (lr >> 2) == 1 ? (int)bit : 0, (lr >> 2) == 2 ? (int)bit : 0,
+                 (lr >> 2) == 3 ? (int)bit : 0};
+  }
+
+  // pass 3: O = P . V
+  v4i oacc[DB];
+#pragma unroll
+  for (int e = 0; e < DB; ++e) oacc[e] = v4i{0, 0, 0, 0};
+  for (int kt = wave; kt < ntiles; kt += nw) {
+    v4i vf[4][DK];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) vf[b][c] = ld16(vr, frag_off(kt, b, c));
+    v4i st[4];
+    scores(kt, st);
+    v4i pd[3];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int32_t pn[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int64_t v = 0;
+        if (key(kt, j, r) < tlim) {
+          v = rshr((int64_t)prob(st[j][r]) * (int64_t)inv, shp);
+          v = v < cap ? v : cap;
+        }
+        pn[r] = (int32_t)v;
+      }
+      pd[0][j] = (int)pack4(pn[0] & 127, pn[1] & 127, pn[2] & 127, pn[3] & 127);
+      pd[1][j] = (int)pack4((pn[0] >> 7) & 127, (pn[1] >> 7) & 127, (pn[2] >> 7) & 127, (pn[3] >> 7) & 127);
+      pd[2][j] = (int)pack4(pn[0] >> 14, pn[1] >> 14, pn[2] >> 14, pn[3] >> 14);
+    }
+#pragma unroll
+    for (int e = 0; e < DB; ++e) {
+      const int c = e >> 2;
+      v4i vt;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const v4i t = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[b][c], sel[e & 3], v4i{0, 0, 0, 0}, 0, 0, 0);
+        vt[b] = (int)pack4(t[0], t[1], t[2], t[3]);
+      }
+      v4i a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[0], vt, v4i{0, 0, 0, 0}, 0, 0, 0);
+      v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[1], vt, v4i{0, 0, 0, 0}, 0, 0, 0);
+      v4i a2 = three ? __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[2], vt, v4i{0, 0, 0, 0}, 0, 0, 0) : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) oacc[e][r] += a0[r] + 128 * a1[r] + 16384 * a2[r];
+    }
+  }
+  // C layout of O: lane (lg, lr) register r = row 4lg + r, column 16e + lr
+#pragma unroll
+  for (int e = 0; e < DB; ++e)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) atomicAdd(&osum[4 * lg + r][16 * e + lr], oacc[e][r]);
+  __syncthreads();
+  for (int idx = tid; idx < AT_ROWS * D; idx += blockDim.x) {
+    const int row = idx / D, d = idx % D;
+    if (m0 + row >= p.M) break;
+    int32_t o = osum[row][d];
+    if (p.pb == 15) o = rshr32(o, 7);
+    p.out[(int64_t)(m0 + row) * p.ldo + (int64_t)h * D + d] = (int8_t)sat8(mulshift(o, p.Mo, p.So));
+  }
+}
+
 __global__ void kv_write_kernel(const int8_t* __restrict__ k, const int8_t* __restrict__ v, int64_t M, int Hkv, int D,
                                 int64_t ldk, int64_t ldv, int pos, const int32_t* __restrict__ pos_dev,
                                 const int32_t* __restrict__ row_pos, int64_t slot_stride, int8_t* __restrict__ kc,
@@ -314,7 +522,10 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
                 (long long)max_seq);
   if (M == 0) return 0;
   const int64_t tmax = (pos_dev || row_pos) ? max_seq : pos + M;
-  if (tmax > ATTN_MAX_T) return fail(-EINVAL, "attention: context %lld exceeds %d", (long long)tmax, ATTN_MAX_T);
+  const bool tiled = !row_pos && M >= AT_MIN_M;
+  if (tmax > (tiled ? AT_MAX_T : ATTN_MAX_T))
+    return fail(-EINVAL, "attention: context %lld exceeds %d", (long long)tmax, tiled ? AT_MAX_T : ATTN_MAX_T);
+  if (max_seq * D * Hkv >= (1ll << 31)) return fail(-EINVAL, "attention: KV cache above 2 GiB");
   AttnArgs p{};
   p.q = q;
   p.kc = kc;
@@ -335,10 +546,31 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   p.pos = (int)pos;
   p.pb = (int)prob_bits;
   p.lds_T = (int)((tmax + 3) / 4 * 4);
+  p.M = (int)M;
+  hipStream_t s = (hipStream_t)stream;
+  if (tiled) {
+    // waves per workgroup: up to the register-file limit while the chip is not yet full and
+    // every wave still gets a 64-key tile
+    const int64_t blocks = H * ceil_div(M, AT_ROWS);
+    const int maxw = D <= 64 ? AttnTileCfg<64>::MAXW : (D == 128 ? AttnTileCfg<128>::MAXW : AttnTileCfg<256>::MAXW);
+    const int64_t tiles = ceil_div(tmax, 64);
+    int nw = 1;
+    while (nw < maxw && nw * 2 <= tiles && blocks * nw < 8 * (int64_t)current_cu_count()) nw *= 2;
+    dim3 grid((unsigned)(8 * (H / Hkv) * ceil_div(Hkv, 8)), (unsigned)ceil_div(M, AT_ROWS));
+    dim3 block(64 * nw);
+    switch (D) {
+      case 16: hipLaunchKernelGGL(attention_tiled<16>, grid, block, 0, s, p); break;
+      case 32: hipLaunchKernelGGL(attention_tiled<32>, grid, block, 0, s, p); break;
+      case 64: hipLaunchKernelGGL(attention_tiled<64>, grid, block, 0, s, p); break;
+      case 128: hipLaunchKernelGGL(attention_tiled<128>, grid, block, 0, s, p); break;
+      default: hipLaunchKernelGGL(attention_tiled<256>, grid, block, 0, s, p); break;
+    }
+    LLHIP_LAUNCH_CHECK();
+    return 0;
+  }
   const size_t lds = sizeof(int32_t) * (size_t)p.lds_T;
   dim3 grid((unsigned)(8 * (H / Hkv) * ceil_div(Hkv, 8)), (unsigned)M);
   dim3 block(ATTN_THREADS);
-  hipStream_t s = (hipStream_t)stream;
   switch (D) {
     case 16: hipLaunchKernelGGL(attention_rowhead<16>, grid, block, lds, s, p); break;
     case 32: hipLaunchKernelGGL(attention_rowhead<32>, grid, block, lds, s, p); break;

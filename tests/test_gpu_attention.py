@@ -34,6 +34,13 @@ CASES = [
     (1, 8, 2, 256, 4095, 4096),
     (16, 8, 2, 256, 4080, 4096),
     (3, 2, 1, 32, 254, 260),
+    # multi-row launches (the 16-row MFMA kernel): prompt-sized blocks, ragged row counts, every D
+    (200, 14, 2, 64, 0, 256),
+    (512, 14, 2, 64, 0, 512),
+    (33, 16, 8, 128, 100, 256),
+    (17, 4, 2, 32, 40, 64),
+    (2, 8, 2, 256, 61, 128),
+    (45, 2, 2, 16, 3, 64),
 ]
 
 
@@ -128,3 +135,27 @@ def test_rows_as_sequences(D, H, Hkv):
     with pytest.raises(ValueError, match="slots overlap"):
         _lib.call("llhip_attention", ptr(qd), B, H, Hkv, D, H * D, 0, None, ptr(rp), stride - 1, ptr(kd), ptr(vd),
                   max_seq, 1 << 30, 40, 1 << 30, 38, 8, ptr(out), H * D, ptr(workspace()), stream())
+
+
+@pytest.mark.parametrize("M,D", [(16, 64), (1, 64), (40, 128), (5, 256)])
+@pytest.mark.parametrize("regime", ["onehot", "flat", "extreme"])
+def test_softmax_regimes(M, D, regime):
+    """Saturating probabilities (one key gets 2^pb - 1, so every base-128 digit of pn is used),
+    a flat softmax (Ms = 0: every p = 65534) and all-(-128) operands (maximal scores)."""
+    rng = np.random.default_rng(M + D + len(regime))
+    H, Hkv, pos, max_seq = 4, 2, 70, 128
+    kc = rng.integers(-128, 128, (Hkv, max_seq, D)).astype(np.int8)
+    vc = rng.integers(-128, 128, (Hkv, max_seq, D)).astype(np.int8)
+    q = rng.integers(-128, 128, (M, H * D))
+    Ms, Ss, Mo, So = (1 << 31) + 12345, 20, (1 << 31) - 1, 40
+    if regime == "flat":
+        Ms = 0
+    elif regime == "extreme":
+        kc[:] = -128
+        vc[:] = -128
+        q[:] = -128
+        Ms, Ss = 1 << 20, 24
+    for pb in (15, 8):
+        got = gpu_attention(q, kc, vc, pos, H, Hkv, D, Ms, Ss, Mo, So, pb)
+        want = O.attention_c(q, kc, vc, pos, H, Hkv, D, Ms, Ss, Mo, So, pb)
+        assert np.array_equal(got, want), pb
