@@ -403,13 +403,15 @@ __global__ __launch_bounds__(256) void linear_tiled(LinearArgs p, int mblocks, i
 
 // Requant of one accumulator, rshr((int64)acc * M + bias * M, S) (= golden.py's
 // mulshift(acc + bias, M, S)), returned clamped to int32 (every later step saturates to 8 or 16
-// bits, so the clamp changes no output).  With v = hi:lo and S >= 32 the shifted value is
-// hi >> (S - 32) and its rounding bit, bit S-1 of v, is bit 31 of alignbit(hi, lo, S - 32): six
-// 32-bit operations after one v_mad_i64_i32.  |v| < 2^62.6, so hi >> (S-32) + 1 cannot overflow.
+// bits, so the clamp changes no output).  Round-half-up is floor((v + 2^(S-1)) / 2^S), so with the
+// constant bR = bias * M + 2^(S-1) folded in and 32 <= S <= 62 the result is the high word of
+// acc * M + bR shifted right by S - 32: one v_mad_i64_i32 and one shift.  |acc| < 2^30 and
+// |M|, |bias| <= 2^31 keep acc * M + bR below 2^63.
 struct ColRq {
   int32_t M;
   int S;
   int64_t bM;  // bias * M
+  int64_t bR;  // bias * M + 2^(S-1)
 };
 
 __device__ __forceinline__ ColRq make_colrq(int32_t M, int S, int32_t bias) {
@@ -417,21 +419,20 @@ __device__ __forceinline__ ColRq make_colrq(int32_t M, int S, int32_t bias) {
   c.M = M;
   c.S = S;
   c.bM = (int64_t)bias * M;
+  c.bR = c.bM + (S > 0 ? (int64_t)1 << (S - 1) : 0);
   // opaque to the optimiser (emits nothing): otherwise acc * M + bias * M is refactored into
   // (acc + bias) * M, a 64 x 32-bit product, instead of one v_mad_i64_i32 per element
   __asm__ volatile("" : "+v"(c.bM));
+  __asm__ volatile("" : "+v"(c.bR));
   return c;
 }
 
+__device__ __forceinline__ bool colrq_fast(const ColRq& c) { return c.S >= 32 && c.S <= 62; }
+
 template <bool FAST>
 __device__ __forceinline__ int32_t requant_col(int32_t acc, const ColRq& c) {
+  if (FAST) return (int32_t)(((int64_t)acc * (int64_t)c.M + c.bR) >> 32) >> (c.S - 32);
   const int64_t v = (int64_t)acc * (int64_t)c.M + c.bM;
-  if (FAST) {
-    const uint32_t sh = (uint32_t)(c.S - 32);
-    const int32_t hi = (int32_t)(v >> 32);
-    const uint32_t lo = (uint32_t)v;
-    return (hi >> sh) + (int32_t)(__builtin_amdgcn_alignbit((uint32_t)hi, lo, sh) >> 31);
-  }
   return (int32_t)clamp64(rshr(v, c.S), INT32_MIN, INT32_MAX);
 }
 
@@ -439,15 +440,17 @@ __device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) { 
 
 // ---------------------------------------------------------------------------------------
 // Large GEMM (M >= 128, K % 64 == 0): GB x GB x 64 block tile (GB = 256 with 8 waves, 128 with 4),
-// 3-stage LDS ring fed by direct global->LDS loads (global_load_lds_dwordx4)
+// 4-stage LDS ring fed by direct global->LDS loads (global_load_lds_dwordx4)
 // ---------------------------------------------------------------------------------------
 // Each wave instruction moves 64 x 16 B into 1 KiB of LDS (16 rows of 64 B).  Lane L of it
 // writes slot L of that KiB (row L/4, slot L%4) and fetches K chunk (L%4) ^ swz(row), so a row's
 // four 16-byte chunks are stored XOR-permuted: fragment reads of 8 (or 16) consecutive rows at one
-// K chunk then fall into distinct LDS banks without padding.  Tiles k+1 and k+2 are in flight
-// while tile k feeds the MFMAs.  Rows past M/N read a clamped valid row (their outputs are
-// discarded); K is a multiple of 64, so no K chunk is partial.
-constexpr int GSTAGES = 3;
+// K chunk then fall into distinct LDS banks without padding.  Tiles k+1..k+3 are in flight while
+// tile k feeds the MFMAs, and the fragments of the next 32-byte K step are read while the MFMAs of
+// this one run (one barrier per tile, in the middle of the tile's MFMA stream).  Rows past M/N
+// read a clamped valid row (their outputs are discarded); K is a multiple of 64, so no K chunk is
+// partial.
+constexpr int GSTAGES = 4;
 
 __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
@@ -463,14 +466,71 @@ struct MfmaTile {
   static_assert(LOADS == 2, "the vmcnt(4) wait assumes 2 A + 2 W loads per wave per stage");
 };
 
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// interleave the MFMAs of one K step with the DS reads of the next (scheduling hint only)
+template <int NMFMA, int NREAD>
+__device__ __forceinline__ void mfma_ds_interleave() {
+#pragma unroll
+  for (int q = 0; q < NREAD; ++q) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+  }
+  if constexpr (NMFMA > NREAD) __builtin_amdgcn_sched_group_barrier(0x008, NMFMA - NREAD, 0);
+}
+
+// i8-output epilogue straight from the accumulators: requant, then a 4x4 byte transpose across
+// each lane quad (the 32x32 C layout gives lane l rows (r/4)*8 + (l/32)*4 + r%4 of column l%32;
+// afterwards lane 4q+t of a half-wave holds row (r/4)*8 + (l/32)*4 + t, columns 4q..4q+3) and one
+// dword store per four outputs.
+template <bool FAST, int WM, int WN>
+__device__ __forceinline__ void store_i8_tile(const LinearArgs& p, const v16i (&acc)[WM][WN], const ColRq (&cq)[WN],
+                                              int mrow0, int ncol0, bool full) {
+  const int lane = threadIdx.x & 63;
+  const int t = lane & 3;
+  const uint32_t sel1 = (t & 1) ? 0x03070105u : 0x06020400u;  // pair swap: bytes [x1 d1 x3 d3] / [d0 x0 d2 x2]
+  const uint32_t sel2 = (t & 2) ? 0x03020706u : 0x05040100u;  // half swap: [y2 y3 d2 d3] / [d0 d1 y0 y1]
+  int8_t* out = static_cast<int8_t*>(p.out);
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int nq = ncol0 + 32 * j + 4 * ((lane & 31) >> 2);
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        int32_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = clamp32(requant_col<FAST>(acc[i][j][4 * g + q], cq[j]), -128, 127);
+        const uint32_t d = __builtin_amdgcn_perm((uint32_t)v[1], (uint32_t)v[0], 0x0c0c0400u) |
+                           __builtin_amdgcn_perm((uint32_t)v[3], (uint32_t)v[2], 0x04000c0cu);
+        const uint32_t d1 = __builtin_amdgcn_perm((uint32_t)dpp_mov<DPP_QUAD_XOR1>((int)d), d, sel1);
+        const uint32_t e = __builtin_amdgcn_perm((uint32_t)dpp_mov<DPP_QUAD_XOR2>((int)d1), d1, sel2);
+        const int m = mrow0 + 32 * i + g * 8 + (lane >> 5) * 4 + t;
+        int8_t* dst = out + (int64_t)m * p.ldo + nq;
+        if (full) {
+          *reinterpret_cast<uint32_t*>(dst) = e;
+        } else if (m < p.M) {
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if (nq + b < p.N) dst[b] = (int8_t)(e >> (8 * b));
+        }
+      }
+  }
+}
+
 template <int EPI, bool OUT8, int GB, int NW>
 __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks) {
   using T = MfmaTile<GB, NW>;
   extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A GBx64 | W GBx64]
-  const int nb_total = mblocks * nblocks;
+  // The grid is padded to a multiple of 8 and workgroup b runs on XCD b % 8, which takes a
+  // contiguous range of tiles (M fastest): the M-blocks that share a W panel share that XCD's L2.
   const int b = blockIdx.x;
-  int logical = b;
-  if (nb_total % 8 == 0) logical = (b % 8) * (nb_total / 8) + b / 8;  // XCD-major (block b runs on XCD b % 8)
+  const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
+  if (logical >= mblocks * nblocks) return;
   const int mb = logical % mblocks;
   const int nbk = logical / mblocks;
   const int m0 = mb * GB, n0 = nbk * GB;
@@ -498,6 +558,29 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
       __builtin_amdgcn_global_load_lds(wsrc[i] + k0, st + GB * 64 + (wave * 2 + i) * 1024, 16, 0, 0);
     }
   };
+  // LDS offsets of this lane's fragments for the two 32-byte K steps of a tile
+  int aoff[T::WM][2], woff[T::WN][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int c = ks * 2 + (lane >> 5);  // 16-byte K chunk of this lane's fragment
+#pragma unroll
+    for (int i = 0; i < T::WM; ++i) {
+      const int r = wm + 32 * i + (lane & 31);
+      aoff[i][ks] = r * 64 + ((c ^ lds_swz(r)) << 4);
+    }
+#pragma unroll
+    for (int j = 0; j < T::WN; ++j) {
+      const int r = wn + 32 * j + (lane & 31);
+      woff[j][ks] = GB * 64 + r * 64 + ((c ^ lds_swz(r)) << 4);
+    }
+  }
+  // epilogue column parameters, loaded while the first tiles stream in
+  ColRq cq[T::WN];
+#pragma unroll
+  for (int j = 0; j < T::WN; ++j) {
+    const int n = min(n0 + wn + 32 * j + (lane & 31), p.N - 1);
+    cq[j] = make_colrq(p.rq[2 * n], p.rq[2 * n + 1], p.bias ? p.bias[n] : 0);  // (acc+bias)*M = acc*M + bias*M
+  }
 
   v16i acc[T::WM][T::WN];
 #pragma unroll
@@ -506,67 +589,79 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
     for (int j = 0; j < T::WN; ++j) acc[i][j] = v16i{};
 
   const int ktiles = p.K / 64;
-  issue(0);
-  if (ktiles > 1) issue(1);
+  for (int s0 = 0; s0 < GSTAGES - 1; ++s0)
+    if (s0 < ktiles) issue(s0);
+  // tile 0 landed: at most the next two tiles' 2 x 4 loads are outstanding
+  if (ktiles > 2)
+    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+  else
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  lds_barrier();
+  v4i fa0[T::WM], fb0[T::WN], fa1[T::WM], fb1[T::WN];
+#pragma unroll
+  for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(ring + aoff[i][0]);
+#pragma unroll
+  for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(ring + woff[j][0]);
   for (int kt = 0; kt < ktiles; ++kt) {
-    // tile kt landed once at most the next tile's 4 loads are outstanding
-    if (kt + 1 < ktiles)
-      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4), expcnt/lgkmcnt don't-care
+    const int8_t* st = ring + (kt % GSTAGES) * T::STAGE_BYTES;
+    // first K step of tile kt (fragments already in registers) while the second one's are read
+#pragma unroll
+    for (int i = 0; i < T::WM; ++i) fa1[i] = *reinterpret_cast<const v4i*>(st + aoff[i][1]);
+#pragma unroll
+    for (int j = 0; j < T::WN; ++j) fb1[j] = *reinterpret_cast<const v4i*>(st + woff[j][1]);
+#pragma unroll
+    for (int i = 0; i < T::WM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
+    mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
+    // Tile kt+1 landed once at most tile kt+2's 4 loads are outstanding; after the barrier every
+    // wave's copies of it are visible and every wave has finished reading stage (kt-1) % 4, which
+    // issue(kt + 3) overwrites.  A bare s_barrier: __syncthreads() would also drain the later
+    // tiles still in flight.
+    if (kt + 2 < ktiles)
+      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
     else
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    // Every wave has its own tile-kt copies in LDS; after the barrier all of them are, and every
-    // wave has finished reading stage (kt-1) % 3, which issue(kt + 2) overwrites.  A bare
-    // s_barrier: __syncthreads() would also drain the tile-(kt+1) copies still in flight.
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (kt + 2 < ktiles) issue(kt + 2);
-    const int8_t* st = ring + (kt % GSTAGES) * T::STAGE_BYTES;
-    const int8_t* As = st;
-    const int8_t* Ws = st + GB * 64;
+    lds_barrier();
+    if (kt + GSTAGES - 1 < ktiles) issue(kt + GSTAGES - 1);
+    // second K step of tile kt while the next tile's first-step fragments are read (after the
+    // last tile they come from a stale stage and are never used)
+    const int8_t* sn = ring + ((kt + 1) % GSTAGES) * T::STAGE_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int c = ks * 2 + (lane >> 5);  // 16-byte K chunk of this lane's fragment
-      v4i fa[T::WM], fb[T::WN];
+    for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(sn + aoff[i][0]);
 #pragma unroll
-      for (int i = 0; i < T::WM; ++i) {
-        const int r = wm + 32 * i + (lane & 31);
-        fa[i] = *reinterpret_cast<const v4i*>(As + r * 64 + ((c ^ lds_swz(r)) << 4));
-      }
+    for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(sn + woff[j][0]);
 #pragma unroll
-      for (int j = 0; j < T::WN; ++j) {
-        const int r = wn + 32 * j + (lane & 31);
-        fb[j] = *reinterpret_cast<const v4i*>(Ws + r * 64 + ((c ^ lds_swz(r)) << 4));
-      }
+    for (int i = 0; i < T::WM; ++i)
 #pragma unroll
-      for (int i = 0; i < T::WM; ++i)
-#pragma unroll
-        for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
+      for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
+    mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
   }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stale fragment reads have returned
 
-  // Epilogue through LDS: the requantised block tile is staged row-major in the (now idle) ring and
-  // written back with 16-byte stores along whole GB-column rows; stores straight from the MFMA
-  // layout would be single bytes per lane (partial-line HBM writes).  A block tile larger than the
-  // ring (i16 output at GB = 256) is staged in two passes of GB/2 rows.
-  constexpr int OB = OUT8 ? 1 : 2;
-  constexpr int PASS_ROWS = (GB * GB * OB <= T::LDS_BYTES) ? GB : GB / 2;
-  constexpr int ROWB = GB * OB;  // staged row bytes
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();  // every wave is done reading the ring (the last DMA was waited for)
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  const bool vec_ok = ((p.ldo * OB) % 16 == 0) && ((uintptr_t)p.out % 16 == 0);
-  ColRq cq[T::WN];
-#pragma unroll
-  for (int j = 0; j < T::WN; ++j) {
-    const int n = min(n0 + wn + 32 * j + (lane & 31), p.N - 1);
-    cq[j] = make_colrq(p.rq[2 * n], p.rq[2 * n + 1], p.bias ? p.bias[n] : 0);  // (acc+bias)*M = acc*M + bias*M
-  }
   // one wave-uniform choice of the requant form
   bool col_fast = true;
 #pragma unroll
-  for (int j = 0; j < T::WN; ++j) col_fast = col_fast && cq[j].S >= 32;
+  for (int j = 0; j < T::WN; ++j) col_fast = col_fast && colrq_fast(cq[j]);
   const bool fast = __all(col_fast);
+
+  if constexpr (OUT8) {
+    const bool full = m0 + GB <= p.M && n0 + GB <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 4 == 0;
+    if (fast)
+      store_i8_tile<true>(p, acc, cq, m0 + wm, n0 + wn, full);
+    else
+      store_i8_tile<false>(p, acc, cq, m0 + wm, n0 + wn, full);
+    return;
+  }
+
+  // i16 epilogue through LDS: the requantised block tile is staged row-major in the (now idle) ring
+  // and written back with 16-byte stores along whole GB-column rows; stores straight from the MFMA
+  // layout would be 2-byte pieces per lane.
+  constexpr int OB = 2;
+  constexpr int PASS_ROWS = (GB * GB * OB <= T::LDS_BYTES) ? GB : GB / 2;
+  constexpr int ROWB = GB * OB;  // staged row bytes
+  lds_barrier();  // every wave is done reading the ring (the last DMA was waited for)
+  const bool vec_ok = ((p.ldo * OB) % 16 == 0) && ((uintptr_t)p.out % 16 == 0);
   auto stage = [&](auto fast_tag, int pass) {
     constexpr bool FAST = decltype(fast_tag)::value;
     // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32
@@ -582,19 +677,15 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
           const int m = m0 + rl;
           const int32_t v = requant_col<FAST>(acc[i][j][r], cq[j]);
           int8_t* slot = ring + (rl - pass * PASS_ROWS) * ROWB + cl * OB;
-          if (OUT8) {
-            *slot = (int8_t)clamp32(v, -128, 127);
-          } else {
-            int32_t t = clamp32(v, -32768, 32767);
-            if (EPI == EPI_RESADD || EPI == EPI_MUL) {
-              const int32_t aux = (m < p.M && n < p.N) ? p.aux[(int64_t)m * p.ldaux + n] : 0;
-              if (EPI == EPI_RESADD) t = clamp32(t + aux, -32768, 32767);
-              else t = (int32_t)sat16(rshr((int64_t)(t * aux), p.aux_shift));
-            } else if (EPI == EPI_SILU) {
-              t = (int32_t)silu16(t, p.Mi, p.Si, p.sh);
-            }
-            *reinterpret_cast<int16_t*>(slot) = (int16_t)t;
+          int32_t t = clamp32(v, -32768, 32767);
+          if (EPI == EPI_RESADD || EPI == EPI_MUL) {
+            const int32_t aux = (m < p.M && n < p.N) ? p.aux[(int64_t)m * p.ldaux + n] : 0;
+            if (EPI == EPI_RESADD) t = clamp32(t + aux, -32768, 32767);
+            else t = (int32_t)sat16(rshr((int64_t)(t * aux), p.aux_shift));
+          } else if (EPI == EPI_SILU) {
+            t = (int32_t)silu16(t, p.Mi, p.Si, p.sh);
           }
+          *reinterpret_cast<int16_t*>(slot) = (int16_t)t;
         }
     }
   };
@@ -606,9 +697,7 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
       else
         stage(std::false_type{}, pass);
     }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    lds_barrier();
     constexpr int CPR = ROWB / 16;  // 16-byte chunks per staged row
     for (int idx = tid; idx < PASS_ROWS * CPR; idx += T::NT) {
       const int rl = idx / CPR, ch = idx % CPR;
@@ -624,11 +713,7 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
           for (int q = 0; q < OB; ++q) dst[e * OB + q] = src[e * OB + q];
       }
     }
-    if (pass + 1 < GB / PASS_ROWS) {
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_s_barrier();
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    }
+    if (pass + 1 < GB / PASS_ROWS) lds_barrier();
   }
 }
 
@@ -639,22 +724,22 @@ template <int EPI, bool OUT8>
 static int launch_linear(LinearArgs& p, hipStream_t stream) {
   const bool aligned = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.W % 16 == 0);
   if (p.M >= 128 && p.K % 64 == 0 && aligned) {
-    // 256x256 tiles when they fill every CU, else 128x128.  The 256x256 kernel keeps 128
+    // 256x256 tiles when M fills them and they fill every CU, else 128x128.  The 256x256 kernel keeps 128
     // accumulators per lane at two waves per SIMD; the aux-reading epilogues would spill there.
     if constexpr (EPI == EPI_NONE) {
-      if ((int64_t)ceil_div(p.M, 256) * ceil_div(p.N, 256) >= current_cu_count()) {
+      if (p.M >= 256 && (int64_t)ceil_div(p.M, 256) * ceil_div(p.N, 256) >= current_cu_count()) {
         using T = MfmaTile<256, 8>;
         const int mblocks = (int)ceil_div(p.M, 256), nblocks = (int)ceil_div(p.N, 256);
-        hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 256, 8>), dim3(mblocks * nblocks), dim3(T::NT), T::LDS_BYTES,
-                           stream, p, mblocks, nblocks);
+        hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 256, 8>), dim3(ceil_div(mblocks * nblocks, 8) * 8), dim3(T::NT),
+                           T::LDS_BYTES, stream, p, mblocks, nblocks);
         LLHIP_LAUNCH_CHECK();
         return 0;
       }
     }
     using T = MfmaTile<128, 4>;
     const int mblocks = (int)ceil_div(p.M, 128), nblocks = (int)ceil_div(p.N, 128);
-    hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 128, 4>), dim3(mblocks * nblocks), dim3(T::NT), T::LDS_BYTES, stream, p,
-                       mblocks, nblocks);
+    hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 128, 4>), dim3(ceil_div(mblocks * nblocks, 8) * 8), dim3(T::NT),
+                       T::LDS_BYTES, stream, p, mblocks, nblocks);
     LLHIP_LAUNCH_CHECK();
     return 0;
   }
