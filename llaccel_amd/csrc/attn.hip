@@ -283,7 +283,8 @@ template <int D>
 struct AttnTileCfg {
   static constexpr int DK = (D + 63) / 64;  // 64-byte K chunks of a key row
   static constexpr int DB = D / 16;         // 16-column blocks of the output
-  static constexpr int MAXW = D <= 64 ? 16 : (D == 128 ? 8 : 4);
+  static constexpr int MAXW = D <= 128 ? 8 : 4;
+  static constexpr int SC = D <= 64 ? 2 : 1;  // tiles per wave whose scores stay in registers
 };
 
 __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
@@ -292,17 +293,41 @@ __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32
   return lo | hi;
 }
 
+// Probability of a key x = mx - s >= 0 below the row maximum (golden.py:170-172):
+// z = rshr(x * Ms, Ss) = (x * Ms + 2^(Ss-1)) >> Ss for x >= 0 (x < 2^24, Ms < 2^32: one 32x32->64
+// multiply-add), p = 0 past the 4096-entry exponent range, else the rounded LUT product.
+struct ProbParams {
+  uint32_t Ms;
+  int Ss;
+  uint64_t zc;  // 2^(Ss-1), or 0 when Ss = 0
+};
+
+__device__ __forceinline__ uint32_t prob_lds(int32_t x, const ProbParams& q, const uint16_t* ei, const uint16_t* ef) {
+  const uint64_t z = ((uint64_t)(uint32_t)x * q.Ms + q.zc) >> q.Ss;
+  if (z >= 4096) return 0u;
+  const uint32_t zi = (uint32_t)z;
+  return ((uint32_t)ei[zi >> 8] * (uint32_t)ef[zi & 255] + 32768u) >> 16;
+}
+
 template <int D>
 __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(AttnArgs p) {
   using C = AttnTileCfg<D>;
-  constexpr int DK = C::DK, DB = C::DB;
+  constexpr int DK = C::DK, DB = C::DB, SC = C::SC;
   __shared__ uint32_t lut32[LUT_DW];
   __shared__ int32_t red[C::MAXW][AT_ROWS];
   __shared__ int32_t osum[AT_ROWS][D];
+  // With Hkv a multiple of 8, GQA group g runs on XCD g % 8 (workgroup b is dispatched to XCD
+  // b % 8) so its query heads share that XCD's L2; otherwise heads are numbered in order (an
+  // XCD-per-group mapping would leave most workgroups empty).
   const int G = p.H / p.Hkv;
-  const int g = (int)(blockIdx.x % 8) + 8 * (int)((blockIdx.x / 8) / G);
-  if (g >= p.Hkv) return;
-  const int h = g * G + (int)((blockIdx.x / 8) % G);
+  int h;
+  if (p.Hkv % 8 == 0) {
+    const int g = (int)(blockIdx.x % 8) + 8 * (int)((blockIdx.x / 8) / G);
+    h = g * G + (int)((blockIdx.x / 8) % G);
+  } else {
+    h = (int)blockIdx.x;
+  }
+  const int g = h / G;
   const int m0 = blockIdx.y * AT_ROWS;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int nw = blockDim.x >> 6;
@@ -350,9 +375,25 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
   // key of subtile j, register r of tile kt in this lane
   auto key = [&](int kt, int j, int r) { return kt * 64 + 16 * j + 4 * lg + r; };
 
+  // Tiles wave + it * nw (it < SC) keep their scores, later their probabilities, in registers
+  // across the three passes; further tiles are recomputed in each pass.
+  v4i cache[SC][4];
+
   // pass 1: row maxima
   int32_t vmax = INT32_MIN;
-  for (int kt = wave; kt < ntiles; kt += nw) {
+#pragma unroll
+  for (int it = 0; it < SC; ++it) {
+    const int kt = wave + it * nw;
+    if (kt < ntiles) {
+      scores(kt, cache[it]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (key(kt, j, r) < tlim) vmax = max(vmax, cache[it][j][r]);
+    }
+  }
+  for (int kt = wave + SC * nw; kt < ntiles; kt += nw) {
     v4i st[4];
     scores(kt, st);
 #pragma unroll
@@ -369,19 +410,47 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
   for (int w = 1; w < nw; ++w) mx = max(mx, red[w][lr]);
   __syncthreads();
 
-  // pass 2: sums of the LUT exponentials
+  // values of the cached tiles: loaded now, used in pass 3
+  v4i vcache[SC][4][DK];
+#pragma unroll
+  for (int it = 0; it < SC; ++it) {
+    const int kt = wave + it * nw;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) vcache[it][b][c] = ld16(vr, kt < ntiles ? frag_off(kt, b, c) : LD_OOB);
+  }
+
+  // pass 2: sums of the LUT exponentials (cached tiles keep p in place of s)
   const uint16_t* ei = reinterpret_cast<const uint16_t*>(lut32);
   const uint16_t* ef = ei + 16;
-  auto prob = [&](int32_t s) -> uint32_t { return lut_prob_lds(mulshift((int64_t)mx - s, p.Ms, p.Ss), ei, ef); };
+  ProbParams pq;
+  pq.Ms = (uint32_t)p.Ms;
+  pq.Ss = p.Ss;
+  pq.zc = p.Ss > 0 ? 1ull << (p.Ss - 1) : 0ull;
   uint32_t vsum = 0;
-  for (int kt = wave; kt < ntiles; kt += nw) {
+#pragma unroll
+  for (int it = 0; it < SC; ++it) {
+    const int kt = wave + it * nw;
+    if (kt < ntiles) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t pr = key(kt, j, r) < tlim ? prob_lds(mx - cache[it][j][r], pq, ei, ef) : 0u;
+          cache[it][j][r] = (int32_t)pr;
+          vsum += pr;
+        }
+    }
+  }
+  for (int kt = wave + SC * nw; kt < ntiles; kt += nw) {
     v4i st[4];
     scores(kt, st);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        if (key(kt, j, r) < tlim) vsum += prob(st[j][r]);
+        if (key(kt, j, r) < tlim) vsum += prob_lds(mx - st[j][r], pq, ei, ef);
   }
   vsum += (uint32_t)__shfl_xor((int)vsum, 16);
   vsum += (uint32_t)__shfl_xor((int)vsum, 32);
@@ -390,9 +459,10 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
   uint32_t total = 0;
   for (int w = 0; w < nw; ++w) total += (uint32_t)red[w][lr];
   const uint32_t inv = 0x80000000u / (total > 1u ? total : 1u);  // 2^31 / total (golden.py:174)
-  const int64_t cap = (1 << p.pb) - 1;
+  const uint32_t cap = (1u << p.pb) - 1u;
   const int shp = 31 - p.pb;
-  const bool three = p.pb > 14;  // pn >= 2^14 possible: a third digit
+  const uint64_t pc = 1ull << (shp - 1);  // rounding constant of rshr(p * inv, 31 - pb), shp >= 16
+  const bool three = p.pb > 14;           // pn >= 2^14 possible: a third digit
 
   // 0/1 selection matrix e: lane (lg, lr) has byte lr set when lg == e
   v4i sel[4];
@@ -407,26 +477,16 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
   v4i oacc[DB];
 #pragma unroll
   for (int e = 0; e < DB; ++e) oacc[e] = v4i{0, 0, 0, 0};
-  for (int kt = wave; kt < ntiles; kt += nw) {
-    v4i vf[4][DK];
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int c = 0; c < DK; ++c) vf[b][c] = ld16(vr, frag_off(kt, b, c));
-    v4i st[4];
-    scores(kt, st);
+  // probabilities (already zero for keys a row does not see) -> base-128 digits -> MFMAs
+  auto pv_tile = [&](const v4i (&pr)[4], const v4i (&vf)[4][DK]) {
     v4i pd[3];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      int32_t pn[4];
+      uint32_t pn[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        int64_t v = 0;
-        if (key(kt, j, r) < tlim) {
-          v = rshr((int64_t)prob(st[j][r]) * (int64_t)inv, shp);
-          v = v < cap ? v : cap;
-        }
-        pn[r] = (int32_t)v;
+        const uint32_t v = (uint32_t)(((uint64_t)(uint32_t)pr[j][r] * inv + pc) >> shp);
+        pn[r] = v < cap ? v : cap;
       }
       pd[0][j] = (int)pack4(pn[0] & 127, pn[1] & 127, pn[2] & 127, pn[3] & 127);
       pd[1][j] = (int)pack4((pn[0] >> 7) & 127, (pn[1] >> 7) & 127, (pn[2] >> 7) & 127, (pn[3] >> 7) & 127);
@@ -441,12 +501,30 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
         const v4i t = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[b][c], sel[e & 3], v4i{0, 0, 0, 0}, 0, 0, 0);
         vt[b] = (int)pack4(t[0], t[1], t[2], t[3]);
       }
-      v4i a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[0], vt, v4i{0, 0, 0, 0}, 0, 0, 0);
-      v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[1], vt, v4i{0, 0, 0, 0}, 0, 0, 0);
-      v4i a2 = three ? __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[2], vt, v4i{0, 0, 0, 0}, 0, 0, 0) : v4i{0, 0, 0, 0};
+      const v4i a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[0], vt, v4i{0, 0, 0, 0}, 0, 0, 0);
+      const v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[1], vt, v4i{0, 0, 0, 0}, 0, 0, 0);
+      const v4i a2 = three ? __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[2], vt, v4i{0, 0, 0, 0}, 0, 0, 0) : v4i{0, 0, 0, 0};
 #pragma unroll
       for (int r = 0; r < 4; ++r) oacc[e][r] += a0[r] + 128 * a1[r] + 16384 * a2[r];
     }
+  };
+#pragma unroll
+  for (int it = 0; it < SC; ++it)
+    if (wave + it * nw < ntiles) pv_tile(cache[it], vcache[it]);
+  for (int kt = wave + SC * nw; kt < ntiles; kt += nw) {
+    v4i vf[4][DK];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) vf[b][c] = ld16(vr, frag_off(kt, b, c));
+    v4i st[4];
+    scores(kt, st);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        st[j][r] = key(kt, j, r) < tlim ? (int32_t)prob_lds(mx - st[j][r], pq, ei, ef) : 0;
+    pv_tile(st, vf);
   }
   // C layout of O: lane (lg, lr) register r = row 4lg + r, column 16e + lr
 #pragma unroll
@@ -549,14 +627,15 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   p.M = (int)M;
   hipStream_t s = (hipStream_t)stream;
   if (tiled) {
-    // waves per workgroup: up to the register-file limit while the chip is not yet full and
-    // every wave still gets a 64-key tile
+    // waves per workgroup: enough that every wave's tiles stay in registers across the three
+    // passes, more (up to the register-file limit) while the chip would otherwise be idle
     const int64_t blocks = H * ceil_div(M, AT_ROWS);
-    const int maxw = D <= 64 ? AttnTileCfg<64>::MAXW : (D == 128 ? AttnTileCfg<128>::MAXW : AttnTileCfg<256>::MAXW);
+    const int maxw = D <= 128 ? AttnTileCfg<128>::MAXW : AttnTileCfg<256>::MAXW;
+    const int sc = D <= 64 ? AttnTileCfg<64>::SC : 1;
     const int64_t tiles = ceil_div(tmax, 64);
     int nw = 1;
-    while (nw < maxw && nw * 2 <= tiles && blocks * nw < 8 * (int64_t)current_cu_count()) nw *= 2;
-    dim3 grid((unsigned)(8 * (H / Hkv) * ceil_div(Hkv, 8)), (unsigned)ceil_div(M, AT_ROWS));
+    while (nw < maxw && nw * 2 <= tiles && (nw * sc < tiles || blocks * nw < 4 * (int64_t)current_cu_count())) nw *= 2;
+    dim3 grid((unsigned)H, (unsigned)ceil_div(M, AT_ROWS));
     dim3 block(64 * nw);
     switch (D) {
       case 16: hipLaunchKernelGGL(attention_tiled<16>, grid, block, 0, s, p); break;
