@@ -15,9 +15,11 @@
  *   - Positions: functions taking (pos, pos_dev) use *pos_dev when pos_dev is non-NULL
  *     (device-resident decode state, e.g. inside a captured graph), else pos.
  *   - `ws` is a caller-allocated workspace of llhip_workspace_bytes() bytes, zero-filled
- *     once at allocation.  Every call leaves it zero-filled again, so it needs no clearing
- *     between calls (and none inside a captured graph).  Calls that share one workspace
- *     must be ordered on one stream.
+ *     once at allocation.  Every call leaves the parts that must start at zero zero-filled
+ *     again, so it needs no clearing between calls (and none inside a captured graph).
+ *     Calls that share one workspace must be ordered on one stream.  llhip_linear uses it
+ *     for split-K partial sums when the output has too few tiles to fill the GPU (a NULL ws
+ *     only disables that split).
  */
 #ifndef LLHIP_H
 #define LLHIP_H

@@ -522,8 +522,11 @@ __device__ __forceinline__ void store_i8_tile(const LinearArgs& p, const v16i (&
   }
 }
 
+// Split-K (part != NULL): workgroup (tile, z = blockIdx.y) accumulates K tiles [z*kps, z*kps + kps)
+// and stores its int32 partial tile into plane z of part [splits][M][N]; linear_splitk_finish
+// sums the planes (integer addition: any split gives the same sum) and applies the epilogue.
 template <int EPI, bool OUT8, int GB, int NW>
-__global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks) {
+__global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part) {
   using T = MfmaTile<GB, NW>;
   extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A GBx64 | W GBx64]
   // The grid is padded to a multiple of 8 and workgroup b runs on XCD b % 8, which takes a
@@ -546,8 +549,9 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
     const int r = (wave * 2 + i) * 16 + (lane >> 2);
     const int chunk = (lane & 3) ^ lds_swz(r);
     const int gm = min(m0 + r, p.M - 1), gn = min(n0 + r, p.N - 1);
-    asrc[i] = p.A + (int64_t)gm * p.lda + chunk * 16;
-    wsrc[i] = p.W + (int64_t)gn * p.K + chunk * 16;
+    const int kbase = (int)blockIdx.y * kps * 64;  // first K byte of this split
+    asrc[i] = p.A + (int64_t)gm * p.lda + kbase + chunk * 16;
+    wsrc[i] = p.W + (int64_t)gn * p.K + kbase + chunk * 16;
   }
   auto issue = [&](int kt) {
     int8_t* st = ring + (kt % GSTAGES) * T::STAGE_BYTES;
@@ -588,7 +592,7 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
 #pragma unroll
     for (int j = 0; j < T::WN; ++j) acc[i][j] = v16i{};
 
-  const int ktiles = p.K / 64;
+  const int ktiles = min(kps, p.K / 64 - (int)blockIdx.y * kps);
   for (int s0 = 0; s0 < GSTAGES - 1; ++s0)
     if (s0 < ktiles) issue(s0);
   // tile 0 landed: at most the next two tiles' 2 x 4 loads are outstanding
@@ -638,6 +642,24 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
     mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stale fragment reads have returned
+
+  if (part) {
+    // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32; each
+    // element store of the wave writes 2 rows x 128 contiguous bytes
+    int32_t* plane = part + (int64_t)blockIdx.y * p.M * p.N;
+#pragma unroll
+    for (int j = 0; j < T::WN; ++j) {
+      const int n = n0 + wn + 32 * j + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < T::WM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+          if (m < p.M && n < p.N) plane[(int64_t)m * p.N + n] = acc[i][j][r];
+        }
+    }
+    return;
+  }
 
   // one wave-uniform choice of the requant form
   bool col_fast = true;
@@ -717,11 +739,34 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
   }
 }
 
+// sum of the split-K planes + bias, requant and epilogue; four columns per thread
+template <int EPI, bool OUT8>
+__global__ __launch_bounds__(256) void linear_splitk_finish(LinearArgs p, const int32_t* part, int splits) {
+  const int64_t plane = (int64_t)p.M * p.N;
+  const int64_t quads = plane / 4;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += (int64_t)gridDim.x * blockDim.x) {
+    v4i a = *reinterpret_cast<const v4i*>(part + 4 * q);
+    for (int z = 1; z < splits; ++z) {
+      const v4i b = *reinterpret_cast<const v4i*>(part + z * plane + 4 * q);
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+    }
+    const int64_t e = 4 * q;
+    const int m = (int)(e / p.N), n = (int)(e % p.N);  // N % 4 == 0: the quad stays in one row
+    finish<EPI, OUT8>(p, m, n, a.x);
+    finish<EPI, OUT8>(p, m, n + 1, a.y);
+    finish<EPI, OUT8>(p, m, n + 2, a.z);
+    finish<EPI, OUT8>(p, m, n + 3, a.w);
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------------------
 template <int EPI, bool OUT8>
-static int launch_linear(LinearArgs& p, hipStream_t stream) {
+static int launch_linear(LinearArgs& p, void* ws, hipStream_t stream) {
   const bool aligned = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.W % 16 == 0);
   if (p.M >= 128 && p.K % 64 == 0 && aligned) {
     // 256x256 tiles when M fills them and they fill every CU, else 128x128.  The 256x256 kernel keeps 128
@@ -731,16 +776,46 @@ static int launch_linear(LinearArgs& p, hipStream_t stream) {
         using T = MfmaTile<256, 8>;
         const int mblocks = (int)ceil_div(p.M, 256), nblocks = (int)ceil_div(p.N, 256);
         hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 256, 8>), dim3(ceil_div(mblocks * nblocks, 8) * 8), dim3(T::NT),
-                           T::LDS_BYTES, stream, p, mblocks, nblocks);
+                           T::LDS_BYTES, stream, p, mblocks, nblocks, p.K / 64, (int32_t*)nullptr);
         LLHIP_LAUNCH_CHECK();
         return 0;
       }
     }
     using T = MfmaTile<128, 4>;
     const int mblocks = (int)ceil_div(p.M, 128), nblocks = (int)ceil_div(p.N, 128);
-    hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 128, 4>), dim3(ceil_div(mblocks * nblocks, 8) * 8), dim3(T::NT),
-                       T::LDS_BYTES, stream, p, mblocks, nblocks);
+    // Too few output tiles for the CUs (narrow projections of a prompt): split K into ranges of at
+    // least 4 K tiles whose int32 partial tiles fit the workspace, then sum them.  The split count
+    // maximises (K-loop time saved) - (partial-plane traffic + one more launch), with the measured
+    // ~0.5 us per K tile of a workgroup and ~4 TB/s for the planes.
+    const int64_t tiles = (int64_t)mblocks * nblocks;
+    const int ktiles = (int)(p.K / 64);
+    const int cus = current_cu_count();
+    int splits = 1;
+    if (ws && p.N % 4 == 0 && tiles < cus) {
+      const int smax = (int)std::min<int64_t>(std::min<int64_t>(8, ceil_div(2 * cus, tiles)), ktiles / 4);
+      double best = 0.0;
+      for (int sp = 2; sp <= smax; ++sp) {
+        const double plane_bytes = (double)sp * p.M * p.N * 4;
+        if (plane_bytes > (double)WS_GEMM_SPLIT_BYTES) break;
+        const double gain = 0.5 * ktiles * (sp - 1) / sp - (2.0 + plane_bytes / 4e6);
+        if (gain > best) {
+          best = gain;
+          splits = sp;
+        }
+      }
+    }
+    const int kps = (int)ceil_div(ktiles, splits);
+    splits = (int)ceil_div(ktiles, kps);
+    int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_GEMM_SPLIT) : nullptr;
+    hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 128, 4>), dim3(ceil_div(mblocks * nblocks, 8) * 8, splits), dim3(T::NT),
+                       T::LDS_BYTES, stream, p, mblocks, nblocks, kps, part);
     LLHIP_LAUNCH_CHECK();
+    if (part) {
+      const int64_t quads = (int64_t)p.M * p.N / 4;
+      hipLaunchKernelGGL((linear_splitk_finish<EPI, OUT8>), dim3((unsigned)std::min<int64_t>(ceil_div(quads, 256), 8 * cus)),
+                         dim3(256), 0, stream, p, part, splits);
+      LLHIP_LAUNCH_CHECK();
+    }
     return 0;
   }
   if (p.M > 16 && aligned) {
@@ -832,7 +907,6 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
   p.bias = bias;
   p.aux = aux;
   p.out = out;
-  (void)ws;  // the GEMM kernels need no workspace
   p.lda = lda;
   p.ldaux = ldaux;
   p.ldo = ldo;
@@ -846,12 +920,12 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
   p.steps = (int)ceil_div(K, 64);
   if (p.steps == 0) p.steps = 1;
   hipStream_t s = (hipStream_t)stream;
-  if (out_i8) return launch_linear<EPI_NONE, true>(p, s);
+  if (out_i8) return launch_linear<EPI_NONE, true>(p, ws, s);
   switch (epilogue) {
-    case EPI_RESADD: return launch_linear<EPI_RESADD, false>(p, s);
-    case EPI_SILU: return launch_linear<EPI_SILU, false>(p, s);
-    case EPI_MUL: return launch_linear<EPI_MUL, false>(p, s);
-    default: return launch_linear<EPI_NONE, false>(p, s);
+    case EPI_RESADD: return launch_linear<EPI_RESADD, false>(p, ws, s);
+    case EPI_SILU: return launch_linear<EPI_SILU, false>(p, ws, s);
+    case EPI_MUL: return launch_linear<EPI_MUL, false>(p, ws, s);
+    default: return launch_linear<EPI_NONE, false>(p, ws, s);
   }
 }
 

@@ -123,3 +123,24 @@ def test_large_gemm_path_ragged_with_epilogues(epilogue, out_i8):
                         silu)
     assert np.array_equal(got[rows], want_r)
     assert np.array_equal(got[:, cols], want_c)
+
+
+@pytest.mark.parametrize("epilogue,out_i8", [("none", True), ("none", False), ("resadd", False), ("silu", False),
+                                             ("mul", False)])
+@pytest.mark.parametrize("M,K,N", [(512, 4864, 896), (300, 896, 900), (2048, 4864, 896), (130, 4864, 130)])
+def test_split_k_gemm(M, K, N, epilogue, out_i8):
+    """Prompt-sized GEMMs with too few output tiles for the GPU take the split-K path (int32
+    partial planes in the workspace, summed by a second kernel): equal to the oracle and to the
+    unsplit kernel (no workspace), with a full-range bias and every epilogue; ragged M and N."""
+    rng = np.random.default_rng(M + K + N + len(epilogue) + out_i8)
+    a, w, rq = _operands(rng, M, K, N, out_i8=out_i8)
+    bias = rng.integers(-(2**31), 2**31 - 1, N)
+    aux = rng.integers(-32768, 32768, (M, N)) if epilogue in ("resadd", "mul") else None
+    silu = {"Mi": 1 << 30, "Si": 30, "sh_out": 16} if epilogue == "silu" else None
+    sh = 11 if epilogue == "mul" else 0
+    kw = dict(bias=bias, out_i8=out_i8, epilogue=epilogue, aux=aux, aux_shift=sh, silu=silu)
+    got = gpu_linear(a, w, rq, **kw)
+    assert np.array_equal(got, gpu_linear(a, w, rq, ws=False, **kw))
+    rows = np.unique(np.concatenate([np.arange(4), np.arange(M - 4, M), rng.choice(M, 12, replace=False)]))
+    want = O.linear_c(a[rows], w, rq, bias, out_i8, epilogue, None if aux is None else aux[rows], sh, silu)
+    assert np.array_equal(got[rows], want)
