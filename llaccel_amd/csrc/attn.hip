@@ -89,14 +89,16 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   constexpr int TG = ATTN_THREADS / DC;
   constexpr int VPF = 8;
 
-  // GQA group g runs on XCD g % 8 (workgroup b is dispatched to XCD b % 8), so the G = H/Hkv
-  // query heads that read one group's K/V share that XCD's L2: block b -> group
-  // (b % 8) + 8 * ((b / 8) / G), head j = (b / 8) % G of it.  Blocks past the groups exit.
+  // The G = H/Hkv query heads that read one (row, GQA group)'s K/V run on one XCD and share its
+  // L2 (workgroup b is dispatched to XCD b % 8): pair u = m * Hkv + g goes to XCD u % 8, as
+  // workgroups b = u % 8 + 8 * ((u / 8) * G + j) for its heads j.  The grid is
+  // 8 * ceil(M * Hkv / 8) * G; workgroups past the last pair exit.
   const int G = p.H / p.Hkv;
-  const int g = (int)(blockIdx.x % 8) + 8 * (int)((blockIdx.x / 8) / G);
-  if (g >= p.Hkv) return;
-  const int h = g * G + (int)((blockIdx.x / 8) % G);
-  const int m = blockIdx.y;
+  const int xk = (int)(blockIdx.x / 8);
+  const int u = (int)(blockIdx.x % 8) + 8 * (xk / G);
+  if (u >= p.M * p.Hkv) return;
+  const int m = u / p.Hkv, g = u % p.Hkv;
+  const int h = g * G + xk % G;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   // Loads in order of use: q and the keys of the first score pass, the LUT dwords (wave 0), the
   // value rows of this thread's first VPF keys.  Key rows at or past T read zeros.
@@ -648,7 +650,8 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
     return 0;
   }
   const size_t lds = sizeof(int32_t) * (size_t)p.lds_T;
-  dim3 grid((unsigned)(8 * (H / Hkv) * ceil_div(Hkv, 8)), (unsigned)M);
+  if (M * Hkv > (int64_t)INT32_MAX / 8 / (H / Hkv)) return fail(-EINVAL, "attention: too many rows");
+  dim3 grid((unsigned)(8 * ceil_div(M * Hkv, 8) * (H / Hkv)));
   dim3 block(ATTN_THREADS);
   switch (D) {
     case 16: hipLaunchKernelGGL(attention_rowhead<16>, grid, block, lds, s, p); break;
