@@ -156,6 +156,7 @@ def gemm_sweep(min_reps: int = 8):
     import torch
 
     from llaccel_amd import _lib
+    from llaccel_amd.golden import capture_graph
 
     ws = torch.zeros(int(_lib.lib().llhip_workspace_bytes()), dtype=torch.uint8, device="cuda")
     out = []
@@ -177,12 +178,9 @@ def gemm_sweep(min_reps: int = 8):
             _lib.call("llhip_linear", p(a), M, K, K, p(w), N, p(rq), None, 0, None, N, 0, 0, 0, 0, 1, p(o), N, p(ws), s)
 
         graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.graph(graph, stream=side):
+        with capture_graph(graph):
             for r in range(reps):
                 launch(ws_w[r % copies])
-        torch.cuda.current_stream().wait_stream(side)
         dt = time_graph(graph, 3) / reps
         nbytes = N * K + M * K + 8 * N + M * N
         out.append({"M": M, "K": K, "N": N, "us": round(dt * 1e6, 2), "TOPS": round(2 * M * N * K / dt / 1e12, 1),

@@ -13,6 +13,8 @@
 // the value pass splits the head dimension into 16-byte chunks across threads
 // and the keys across thread groups (four keys in flight per thread); partial
 // sums are folded across lanes with shuffles, then across waves in LDS.
+#include <algorithm>
+
 #include "../../include/llhip.h"
 #include "common.h"
 
@@ -280,6 +282,8 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
 constexpr int AT_ROWS = 16;
 constexpr int AT_MIN_M = 2;       // launches of fewer rows use attention_rowhead
 constexpr int AT_MAX_T = 32767;   // per-row sum of T probabilities < 2^31
+constexpr int AT_SPLIT_MIN_TILES = 32;  // contexts of >= 2048 keys may be split across workgroups
+constexpr int AT_SPLIT_MAXS = 128;      // splits per (row block, head) pair
 
 template <int D>
 struct AttnTileCfg {
@@ -543,6 +547,244 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// attention_split: long contexts with few (row block, head) pairs.  The 64-key tiles of the
+// context are split over S workgroups per pair and the three reductions become three launches
+// (PHASE 1: row maxima, 2: sums of the LUT exponentials, 3: probability-weighted value sums),
+// each writing per-split partials to the workspace, then attention_split_finish adds the value
+// partials and requantises.  Every partial is an exact integer max or sum, so the split changes
+// no result.  The per-tile arithmetic is that of attention_tiled (16 query rows per workgroup,
+// S^T = K . Q^T, V^T by selection MFMAs, base-128 probability digits).
+// ---------------------------------------------------------------------------------------
+struct SplitWs {
+  int32_t* maxv;  // [pairs][S][16]
+  int32_t* sumv;  // [pairs][S][16]
+  int32_t* outv;  // [pairs][S][16][D]
+};
+
+template <int D>
+__device__ __forceinline__ SplitWs split_ws(int32_t* ws, int64_t pairs, int S) {
+  SplitWs w;
+  w.maxv = ws;
+  w.sumv = ws + pairs * S * AT_ROWS;
+  w.outv = ws + 2 * pairs * S * AT_ROWS;
+  return w;
+}
+
+template <int D, int PHASE>
+__global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_split(AttnArgs p, int S, int tps, int32_t* ws) {
+  using C = AttnTileCfg<D>;
+  constexpr int DK = C::DK, DB = C::DB;
+  __shared__ uint32_t lut32[LUT_DW];
+  __shared__ int32_t red[C::MAXW][AT_ROWS];
+  __shared__ int32_t osum[PHASE == 3 ? AT_ROWS : 1][PHASE == 3 ? D : 1];
+  __shared__ int32_t spart[PHASE >= 2 ? AT_SPLIT_MAXS : 1][AT_ROWS];  // every split's maxima (then sums)
+  const int G = p.H / p.Hkv;
+  int h;
+  if (p.Hkv % 8 == 0) {
+    const int g = (int)(blockIdx.x % 8) + 8 * (int)((blockIdx.x / 8) / G);
+    h = g * G + (int)((blockIdx.x / 8) % G);
+  } else {
+    h = (int)blockIdx.x;
+  }
+  const int g = h / G;
+  const int rb = blockIdx.y, z = blockIdx.z;
+  const int64_t pairs = (int64_t)p.H * gridDim.y;
+  const int64_t pair = (int64_t)h * gridDim.y + rb;
+  const SplitWs w = split_ws<D>(ws, pairs, S);
+  const int m0 = rb * AT_ROWS;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int nw = blockDim.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int pos = load_pos(p.pos_dev, p.pos);
+  const int mlast = min(m0 + AT_ROWS, p.M) - 1;
+  const int Tb = min(pos + mlast + 1, (int)p.max_seq);
+  const int ntiles = (Tb + 63) >> 6;
+  const int kt0 = z * tps, kt1 = min(kt0 + tps, ntiles);  // this split's tiles (possibly none)
+  const int m = m0 + lr;
+  const int tlim = m < p.M ? min(pos + m + 1, (int)p.max_seq) : 0;
+  const int8_t* kbase = p.kc + (int64_t)g * p.max_seq * D;
+  const int8_t* vbase = p.vc + (int64_t)g * p.max_seq * D;
+  const Rsrc kr = rsrc(kbase, (int64_t)Tb * D), vr = rsrc(vbase, (int64_t)Tb * D);
+
+  v4i qf[DK];
+  {
+    const Rsrc qr = rsrc(p.q + (int64_t)m0 * p.ldq + (int64_t)h * D, (int64_t)AT_ROWS * p.ldq);
+#pragma unroll
+    for (int c = 0; c < DK; ++c)
+      qf[c] = ld16(qr, (m < p.M && 64 * c + 16 * lg < D) ? (uint32_t)(lr * p.ldq + 64 * c + 16 * lg) : LD_OOB);
+  }
+  if (PHASE >= 2) {
+    const Rsrc ir = rsrc(kExpI, sizeof(kExpI)), fr = rsrc(kExpF, sizeof(kExpF));
+    for (int idx = tid; idx < LUT_DW; idx += blockDim.x)
+      lut32[idx] = (uint32_t)ld4(ir, idx < 8 ? 4 * idx : LD_OOB) | (uint32_t)ld4(fr, idx >= 8 ? 4 * (idx - 8) : LD_OOB);
+  }
+  if (PHASE == 3)
+    for (int idx = tid; idx < AT_ROWS * D; idx += blockDim.x) (&osum[0][0])[idx] = 0;
+  auto frag_off = [&](int kt, int j, int c) -> uint32_t {
+    return 64 * c + 16 * lg < D ? (uint32_t)((kt * 64 + 16 * j + lr) * D + 64 * c + 16 * lg) : LD_OOB;
+  };
+  auto scores = [&](int kt, v4i (&st)[4]) {
+    v4i kf[4][DK];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) kf[j][c] = ld16(kr, frag_off(kt, j, c));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      st[j] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int c = 0; c < DK; ++c) st[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[j][c], qf[c], st[j], 0, 0, 0);
+    }
+  };
+  auto key = [&](int kt, int j, int r) { return kt * 64 + 16 * j + 4 * lg + r; };
+
+  if (PHASE == 1) {
+    int32_t vmax = INT32_MIN;
+    for (int kt = kt0 + wave; kt < kt1; kt += nw) {
+      v4i st[4];
+      scores(kt, st);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (key(kt, j, r) < tlim) vmax = max(vmax, st[j][r]);
+    }
+    vmax = max(vmax, __shfl_xor(vmax, 16));
+    vmax = max(vmax, __shfl_xor(vmax, 32));
+    if (lg == 0) red[wave][lr] = vmax;
+    __syncthreads();
+    if (tid < AT_ROWS) {
+      int32_t mx = red[0][tid];
+      for (int q = 1; q < nw; ++q) mx = max(mx, red[q][tid]);
+      w.maxv[(pair * S + z) * AT_ROWS + tid] = mx;
+    }
+    return;
+  }
+
+  // row maximum over all splits (the S x 16 partials staged in LDS by the whole workgroup)
+  for (int idx = tid; idx < S * AT_ROWS; idx += blockDim.x) (&spart[0][0])[idx] = w.maxv[pair * S * AT_ROWS + idx];
+  __syncthreads();  // partials and LUT staged
+  int32_t mx = INT32_MIN;
+  for (int q = 0; q < S; ++q) mx = max(mx, spart[q][lr]);
+  const uint16_t* ei = reinterpret_cast<const uint16_t*>(lut32);
+  const uint16_t* ef = ei + 16;
+  ProbParams pq;
+  pq.Ms = (uint32_t)p.Ms;
+  pq.Ss = p.Ss;
+  pq.zc = p.Ss > 0 ? 1ull << (p.Ss - 1) : 0ull;
+
+  if (PHASE == 2) {
+    uint32_t vsum = 0;
+    for (int kt = kt0 + wave; kt < kt1; kt += nw) {
+      v4i st[4];
+      scores(kt, st);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (key(kt, j, r) < tlim) vsum += prob_lds(mx - st[j][r], pq, ei, ef);
+    }
+    vsum += (uint32_t)__shfl_xor((int)vsum, 16);
+    vsum += (uint32_t)__shfl_xor((int)vsum, 32);
+    if (lg == 0) red[wave][lr] = (int32_t)vsum;
+    __syncthreads();
+    if (tid < AT_ROWS) {
+      uint32_t t = 0;
+      for (int q = 0; q < nw; ++q) t += (uint32_t)red[q][tid];
+      w.sumv[(pair * S + z) * AT_ROWS + tid] = (int32_t)t;
+    }
+    return;
+  }
+
+  // PHASE 3: the row's total over all splits -> inv, then this split's P . V
+  __syncthreads();  // every lane has its maximum
+  for (int idx = tid; idx < S * AT_ROWS; idx += blockDim.x) (&spart[0][0])[idx] = w.sumv[pair * S * AT_ROWS + idx];
+  __syncthreads();
+  uint32_t total = 0;
+  for (int q = 0; q < S; ++q) total += (uint32_t)spart[q][lr];
+  const uint32_t inv = 0x80000000u / (total > 1u ? total : 1u);  // 2^31 / total (golden.py:174)
+  const uint32_t cap = (1u << p.pb) - 1u;
+  const int shp = 31 - p.pb;
+  const uint64_t pc = 1ull << (shp - 1);
+  const bool three = p.pb > 14;
+  v4i sel[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t bit = lg == e ? 1u << (8 * (lr & 3)) : 0u;
+    sel[e] = v4i{(lr >> 2) == 0 ? (int)bit : 0, (lr >> 2) == 1 ? (int)bit : 0, (lr >> 2) == 2 ? (int)bit : 0,
+                 (lr >> 2) == 3 ? (int)bit : 0};
+  }
+  v4i oacc[DB];
+#pragma unroll
+  for (int e = 0; e < DB; ++e) oacc[e] = v4i{0, 0, 0, 0};
+  for (int kt = kt0 + wave; kt < kt1; kt += nw) {
+    v4i vf[4][DK];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) vf[b][c] = ld16(vr, frag_off(kt, b, c));
+    v4i st[4];
+    scores(kt, st);
+    v4i pd[3];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t pn[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t pr = key(kt, j, r) < tlim ? prob_lds(mx - st[j][r], pq, ei, ef) : 0u;
+        const uint32_t v = (uint32_t)(((uint64_t)pr * inv + pc) >> shp);
+        pn[r] = v < cap ? v : cap;
+      }
+      pd[0][j] = (int)pack4(pn[0] & 127, pn[1] & 127, pn[2] & 127, pn[3] & 127);
+      pd[1][j] = (int)pack4((pn[0] >> 7) & 127, (pn[1] >> 7) & 127, (pn[2] >> 7) & 127, (pn[3] >> 7) & 127);
+      pd[2][j] = (int)pack4(pn[0] >> 14, pn[1] >> 14, pn[2] >> 14, pn[3] >> 14);
+    }
+#pragma unroll
+    for (int e = 0; e < DB; ++e) {
+      const int c = e >> 2;
+      v4i vt;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const v4i t = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[b][c], sel[e & 3], v4i{0, 0, 0, 0}, 0, 0, 0);
+        vt[b] = (int)pack4(t[0], t[1], t[2], t[3]);
+      }
+      const v4i a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[0], vt, v4i{0, 0, 0, 0}, 0, 0, 0);
+      const v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[1], vt, v4i{0, 0, 0, 0}, 0, 0, 0);
+      const v4i a2 = three ? __builtin_amdgcn_mfma_i32_16x16x64_i8(pd[2], vt, v4i{0, 0, 0, 0}, 0, 0, 0) : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) oacc[e][r] += a0[r] + 128 * a1[r] + 16384 * a2[r];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < DB; ++e)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) atomicAdd(&osum[PHASE == 3 ? 4 * lg + r : 0][PHASE == 3 ? 16 * e + lr : 0], oacc[e][r]);
+  __syncthreads();
+  // the block's valid rows only (the finishing kernel reads no others)
+  int32_t* dst = w.outv + (pair * S + z) * AT_ROWS * D;
+  const int nrows = min(AT_ROWS, p.M - m0);
+  for (int idx = tid; idx < nrows * D; idx += blockDim.x) dst[idx] = (&osum[0][0])[idx];
+}
+
+// sum of the S value partials of each (row block, head) pair, then the output requant: one
+// thread per output element (grid z covers the block's rows in groups of 256 / D)
+template <int D>
+__global__ __launch_bounds__(256) void attention_split_finish(AttnArgs p, int S, const int32_t* ws) {
+  const int h = blockIdx.x, rb = blockIdx.y;
+  const int64_t pairs = (int64_t)p.H * gridDim.y;
+  const int64_t pair = (int64_t)h * gridDim.y + rb;
+  const int32_t* outv = ws + 2 * pairs * S * AT_ROWS + pair * S * AT_ROWS * D;
+  const int idx = (int)blockIdx.z * 256 + (int)threadIdx.x;
+  const int row = idx / D, d = idx % D;
+  if (row >= AT_ROWS || rb * AT_ROWS + row >= p.M) return;
+  int32_t o = 0;
+#pragma unroll 8
+  for (int q = 0; q < S; ++q) o += outv[(int64_t)q * AT_ROWS * D + idx];
+  if (p.pb == 15) o = rshr32(o, 7);
+  p.out[(int64_t)(rb * AT_ROWS + row) * p.ldo + (int64_t)h * D + d] = (int8_t)sat8(mulshift(o, p.Mo, p.So));
+}
+
 __global__ void kv_write_kernel(const int8_t* __restrict__ k, const int8_t* __restrict__ v, int64_t M, int Hkv, int D,
                                 int64_t ldk, int64_t ldv, int pos, const int32_t* __restrict__ pos_dev,
                                 const int32_t* __restrict__ row_pos, int64_t slot_stride, int8_t* __restrict__ kc,
@@ -588,7 +830,6 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
                     const int8_t* vc, int64_t max_seq, int64_t Ms,
                     int64_t Ss, int64_t Mo, int64_t So, int64_t prob_bits, int8_t* out, int64_t ldo, void* ws,
                     void* stream) {
-  (void)ws;
   if (prob_bits != 8 && prob_bits != 15) return fail(-EINVAL, "attention prob_bits must be 8 or 15");
   if (M < 0 || H <= 0 || Hkv <= 0 || H % Hkv) return fail(-EINVAL, "attention: H must be a multiple of Hkv");
   if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256)
@@ -628,6 +869,36 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   p.lds_T = (int)((tmax + 3) / 4 * 4);
   p.M = (int)M;
   hipStream_t s = (hipStream_t)stream;
+  const int cus = current_cu_count();
+  // Long contexts with few (row block, head) pairs: split the key tiles over S workgroups per pair
+  // (three reduction launches + a finishing one) so every CU streams a share of K and V.
+  const int64_t rblocks = ceil_div(M, AT_ROWS), pairs = H * rblocks, ktiles = ceil_div(tmax, 64);
+  if (!row_pos && ws && tmax <= AT_MAX_T && ktiles >= AT_SPLIT_MIN_TILES && pairs * 4 <= cus) {
+    int S = (int)std::min<int64_t>(std::min<int64_t>(ceil_div(cus, pairs), ceil_div(ktiles, 4)), AT_SPLIT_MAXS);
+    while (S > 1 && pairs * S * AT_ROWS * (2 + D) * 4 > WS_SCRATCH_BYTES) --S;
+    const int tps = (int)ceil_div(ktiles, S);
+    S = (int)ceil_div(ktiles, tps);
+    const int maxw = D <= 128 ? AttnTileCfg<128>::MAXW : AttnTileCfg<256>::MAXW;
+    const int nw = std::min(maxw, tps);
+    int32_t* sw = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH);
+    dim3 grid((unsigned)H, (unsigned)rblocks, (unsigned)S), block(64 * nw);
+    dim3 fgrid((unsigned)H, (unsigned)rblocks, (unsigned)ceil_div(std::min<int64_t>(M, AT_ROWS) * D, 256));
+#define LLHIP_SPLIT(DD)                                                                      \
+  hipLaunchKernelGGL((attention_split<DD, 1>), grid, block, 0, s, p, S, tps, sw);           \
+  hipLaunchKernelGGL((attention_split<DD, 2>), grid, block, 0, s, p, S, tps, sw);           \
+  hipLaunchKernelGGL((attention_split<DD, 3>), grid, block, 0, s, p, S, tps, sw);           \
+  hipLaunchKernelGGL((attention_split_finish<DD>), fgrid, dim3(256), 0, s, p, S, sw);
+    switch (D) {
+      case 16: LLHIP_SPLIT(16) break;
+      case 32: LLHIP_SPLIT(32) break;
+      case 64: LLHIP_SPLIT(64) break;
+      case 128: LLHIP_SPLIT(128) break;
+      default: LLHIP_SPLIT(256) break;
+    }
+#undef LLHIP_SPLIT
+    LLHIP_LAUNCH_CHECK();
+    return 0;
+  }
   if (tiled) {
     // waves per workgroup: enough that every wave's tiles stay in registers across the three
     // passes, more (up to the register-file limit) while the chip would otherwise be idle

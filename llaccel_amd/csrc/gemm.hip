@@ -796,7 +796,7 @@ static int launch_linear(LinearArgs& p, void* ws, hipStream_t stream) {
       double best = 0.0;
       for (int sp = 2; sp <= smax; ++sp) {
         const double plane_bytes = (double)sp * p.M * p.N * 4;
-        if (plane_bytes > (double)WS_GEMM_SPLIT_BYTES) break;
+        if (plane_bytes > (double)WS_SCRATCH_BYTES) break;
         const double gain = 0.5 * ktiles * (sp - 1) / sp - (2.0 + plane_bytes / 4e6);
         if (gain > best) {
           best = gain;
@@ -806,7 +806,7 @@ static int launch_linear(LinearArgs& p, void* ws, hipStream_t stream) {
     }
     const int kps = (int)ceil_div(ktiles, splits);
     splits = (int)ceil_div(ktiles, kps);
-    int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_GEMM_SPLIT) : nullptr;
+    int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
     hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 128, 4>), dim3(ceil_div(mblocks * nblocks, 8) * 8, splits), dim3(T::NT),
                        T::LDS_BYTES, stream, p, mblocks, nblocks, kps, part);
     LLHIP_LAUNCH_CHECK();

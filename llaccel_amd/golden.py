@@ -19,7 +19,9 @@ activation).  `kv` returns host snapshots of the device caches; `set_kv` uploads
 from __future__ import annotations
 
 import argparse
+import contextlib
 import ctypes
+import gc
 import json
 import math
 from pathlib import Path
@@ -56,6 +58,26 @@ def _dev():
 
 def _stream():
     return ctypes.c_void_p(_t().cuda.current_stream().cuda_stream)
+
+
+@contextlib.contextmanager
+def capture_graph(graph):
+    """torch.cuda.graph on a side stream with the Python garbage collector paused: a collection
+    during capture could destroy an unreferenced graph or free device memory of an earlier model,
+    runtime calls that are not permitted while a stream is being captured."""
+    torch = _t()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    gc.collect()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph, stream=side):
+            yield
+    finally:
+        if enabled:
+            gc.enable()
+    torch.cuda.current_stream().wait_stream(side)
 
 
 def _ptr(t):
@@ -887,11 +909,8 @@ class GoldenModel:
     def _capture(self) -> None:
         torch = _t()
         g = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.graph(g, stream=side):
+        with capture_graph(g):
             self._decode_launch()
-        torch.cuda.current_stream().wait_stream(side)
         self._graph = g
 
     def decode_loop(self, token: int, pos: int, n: int, *, sync: bool = True):
@@ -964,11 +983,8 @@ class GoldenModel:
         self._b_st.copy_(torch.tensor(idx + pos + pos, dtype=torch.int32))
         if self.use_graph and self._graph_b is None:
             g = torch.cuda.CUDAGraph()
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.graph(g, stream=side):
+            with capture_graph(g):
                 self._decode_batch_launch()
-            torch.cuda.current_stream().wait_stream(side)
             self._graph_b = g
         for _ in range(n):
             if self.use_graph:
@@ -1047,13 +1063,10 @@ class GoldenModel:
         self._st.copy_(torch.tensor([0, pos, 0], dtype=torch.int32))
         pd = ctypes.c_void_p(self._st.data_ptr() + 4)
         g = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.graph(g, stream=side):
+        with capture_graph(g):
             for st in self._plan:
                 if st.kind in kinds:
                     st(1, 0, pd)
-        torch.cuda.current_stream().wait_stream(side)
         return g
 
     def step_bytes(self, kind: str, M: int = 1, T: int = 1) -> int:

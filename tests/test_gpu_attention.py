@@ -41,6 +41,11 @@ CASES = [
     (17, 4, 2, 32, 40, 64),
     (2, 8, 2, 256, 61, 128),
     (45, 2, 2, 16, 3, 64),
+    # long contexts with few (row block, head) pairs: the key tiles split over workgroups
+    (16, 16, 8, 128, 4080, 4096),
+    (20, 8, 2, 64, 3000, 4096),
+    (3, 4, 2, 32, 2500, 3000),
+    (1, 2, 1, 16, 2047, 2048),
 ]
 
 
@@ -97,6 +102,26 @@ def test_device_position():
               1 << 30, 40, 1 << 30, 38, 15, ptr(out), H * D, ptr(workspace()), stream())
     assert np.array_equal(down(out), O.attention_c(q, kc.astype(np.int8), vc.astype(np.int8), 600, H, Hkv, D,
                                                    1 << 30, 40, 1 << 30, 38, 15))
+
+
+@pytest.mark.parametrize("pos", [0, 5, 2100, 4095])
+def test_device_position_long_context(pos):
+    """Device position with a long cache (the split-context path sizes its grid for max_seq):
+    splits past the position find no keys and contribute nothing."""
+    t = __import__("torch")
+    rng = np.random.default_rng(12 + pos)
+    H, Hkv, D, max_seq = 16, 8, 128, 4096
+    kc = rng.integers(-128, 128, (Hkv, max_seq, D))
+    vc = rng.integers(-128, 128, (Hkv, max_seq, D))
+    q = rng.integers(-128, 128, (1, H * D))
+    qd, kd, vd = up(q, np.int8), up(kc, np.int8), up(vc, np.int8)
+    posd = t.tensor([pos], dtype=t.int32, device="cuda")
+    out = t.empty((1, H * D), dtype=t.int8, device="cuda")
+    for pb in (15, 8):
+        _lib.call("llhip_attention", ptr(qd), 1, H, Hkv, D, H * D, 0, ptr(posd), None, 0, ptr(kd), ptr(vd), max_seq,
+                  1 << 30, 41, 1 << 30, 38, pb, ptr(out), H * D, ptr(workspace()), stream())
+        want = O.attention_c(q, kc.astype(np.int8), vc.astype(np.int8), pos, H, Hkv, D, 1 << 30, 41, 1 << 30, 38, pb)
+        assert np.array_equal(down(out), want), pb
 
 
 @pytest.mark.parametrize("D,H,Hkv", [(64, 14, 2), (128, 16, 8), (16, 4, 2)])
