@@ -22,6 +22,8 @@ The JSON line also carries
 
     python bench.py [--gpus 1] [--steps 64] [--warmup 8]
     python bench.py --profile decode   # prefill + decode launches only (for rocprofv3)
+    python bench.py --profile prefill  # prefill() once, then three one-launch 512-row prefills
+    python bench.py --profile gemm     # config 2's M=2048 x K=896 x N=151936 GEMM, 7 launches
     python bench.py --profile copy     # 256 MiB device copies (counter calibration)
 """
 from __future__ import annotations
@@ -201,7 +203,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--batch", type=int, default=16, help="also time config 4's batch decode (1 = skip)")
-    ap.add_argument("--profile", choices=("decode", "copy"), help="workload-only runs for rocprofv3")
+    ap.add_argument("--profile", choices=("decode", "copy", "prefill", "gemm"),
+                    help="workload-only runs for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs the datapath on a "
@@ -219,6 +222,29 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copied {n} bytes x 10")
+        return
+
+    if args.profile == "gemm":
+        # config 2's largest shape, i8 output: 2 warm-up + 5 launches, weights rotated over 4 copies
+        import ctypes
+
+        from llaccel_amd import _lib
+
+        M, K, N = 2048, 896, 151936
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=g)
+        ws_w = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g) for _ in range(4)]
+        rq = torch.stack([torch.full((N,), 1 << 30, dtype=torch.int32, device="cuda"),
+                          torch.full((N,), 42, dtype=torch.int32, device="cuda")], 1).contiguous()
+        o = torch.empty((M, N), dtype=torch.int8, device="cuda")
+        ws = torch.zeros(int(_lib.lib().llhip_workspace_bytes()), dtype=torch.uint8, device="cuda")
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for r in range(7):
+            _lib.call("llhip_linear", p(a), M, K, K, p(ws_w[r % 4]), N, p(rq), None, 0, None, N, 0, 0, 0, 0, 1, p(o), N,
+                      p(ws), s)
+        torch.cuda.synchronize()
+        log(f"gemm {M}x{K}x{N}: 7 launches")
         return
 
     from llaccel_amd import golden as G
@@ -254,6 +280,8 @@ def main() -> None:
         t_dev.append(time.perf_counter() - t0)
     t_prefill_dev = min(t_dev)
     log(f"prefill {L} tokens: {t_prefill * 1e3:.1f} ms through prefill(), {t_prefill_dev * 1e3:.2f} ms on the GPU")
+    if args.profile == "prefill":
+        return
 
     # ---- decode: warmup (captures the graph), then the timed steps ----
     toks_w, rows_w = g.decode_loop(nxt, L, args.warmup)
