@@ -522,6 +522,69 @@ __device__ __forceinline__ void store_i8_tile(const LinearArgs& p, const v16i (&
   }
 }
 
+// i16-output epilogue straight from the accumulators: requant + sat16 in the C layout, a 4x4
+// transpose of 16-bit values across each lane quad (an exchange of dwords with lane ^ 2, then of
+// halves with lane ^ 1), after which lane 4q+t of a half-wave holds row (r/4)*8 + (l/32)*4 + t,
+// columns 4q..4q+3: the aux operand is read and the result written 8 bytes at a time.
+template <int EPI, bool FAST, int WM, int WN>
+__device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (&acc)[WM][WN], const ColRq (&cq)[WN],
+                                               int mrow0, int ncol0, bool full, const uint16_t* sig) {
+  const int lane = threadIdx.x & 63;
+  const int t = lane & 3;
+  const bool lo2 = t < 2;
+  const uint32_t selh = (t & 1) ? 0x03020706u : 0x05040100u;  // odd: [x.hi | own.hi], even: [own.lo | x.lo]
+  int16_t* out = static_cast<int16_t*>(p.out);
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int nq = ncol0 + 32 * j + 4 * ((lane & 31) >> 2);
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        int32_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = clamp32(requant_col<FAST>(acc[i][j][4 * g + q], cq[j]), -32768, 32767);
+        // E[lane][row]: d0 = rows 0,1, d1 = rows 2,3 of this lane's column
+        const uint32_t d0 = __builtin_amdgcn_perm((uint32_t)v[1], (uint32_t)v[0], 0x05040100u);
+        const uint32_t d1 = __builtin_amdgcn_perm((uint32_t)v[3], (uint32_t)v[2], 0x05040100u);
+        const uint32_t r = (uint32_t)dpp_mov<DPP_QUAD_XOR2>((int)(lo2 ? d1 : d0));
+        const uint32_t a = lo2 ? d0 : r, b = lo2 ? r : d1;  // rows {0,1} or {2,3} of lanes t and t^2
+        const uint32_t t0 = __builtin_amdgcn_perm((uint32_t)dpp_mov<DPP_QUAD_XOR1>((int)a), a, selh);
+        const uint32_t t1 = __builtin_amdgcn_perm((uint32_t)dpp_mov<DPP_QUAD_XOR1>((int)b), b, selh);
+        const int m = mrow0 + 32 * i + g * 8 + (lane >> 5) * 4 + t;
+        int32_t o[4] = {lo16((int)t0), hi16((int)t0), lo16((int)t1), hi16((int)t1)};
+        if (full) {
+          if (EPI == EPI_RESADD || EPI == EPI_MUL) {
+            const v2i ax = *reinterpret_cast<const v2i*>(p.aux + (int64_t)m * p.ldaux + nq);
+            const int32_t av[4] = {lo16(ax.x), hi16(ax.x), lo16(ax.y), hi16(ax.y)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              o[e] = EPI == EPI_RESADD ? clamp32(o[e] + av[e], -32768, 32767)
+                                       : (int32_t)sat16(rshr((int64_t)(o[e] * av[e]), p.aux_shift));
+          } else if (EPI == EPI_SILU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = silu16_i16(o[e], (uint32_t)p.Mi, p.Si, p.sh, sig);
+          }
+          *reinterpret_cast<v2i*>(out + (int64_t)m * p.ldo + nq) = v2i{pack16(o[0], o[1]), pack16(o[2], o[3])};
+        } else if (m < p.M) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int n = nq + e;
+            if (n >= p.N) break;
+            int32_t x = o[e];
+            if (EPI == EPI_RESADD || EPI == EPI_MUL) {
+              const int32_t aux = p.aux[(int64_t)m * p.ldaux + n];
+              x = EPI == EPI_RESADD ? clamp32(x + aux, -32768, 32767) : (int32_t)sat16(rshr((int64_t)(x * aux), p.aux_shift));
+            } else if (EPI == EPI_SILU) {
+              x = silu16_i16(x, (uint32_t)p.Mi, p.Si, p.sh, sig);
+            }
+            out[(int64_t)m * p.ldo + n] = (int16_t)x;
+          }
+        }
+      }
+  }
+}
+
 // Split-K (part != NULL): workgroup (tile, z = blockIdx.y) accumulates K tiles [z*kps, z*kps + kps)
 // and stores its int32 partial tile into plane z of part [splits][M][N]; linear_splitk_finish
 // sums the planes (integer addition: any split gives the same sum) and applies the epilogue.
@@ -578,6 +641,10 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
       woff[j][ks] = GB * 64 + r * 64 + ((c ^ lds_swz(r)) << 4);
     }
   }
+  // SiLU table for the silu epilogue, staged in LDS (visible after the main loop's barriers)
+  __shared__ uint32_t sig32[EPI == EPI_SILU ? 129 : 1];
+  if (EPI == EPI_SILU && tid < 129) sig32[tid] = reinterpret_cast<const uint32_t*>(kSig)[tid];
+  const uint16_t* sig16 = reinterpret_cast<const uint16_t*>(sig32);
   // epilogue column parameters, loaded while the first tiles stream in
   ColRq cq[T::WN];
 #pragma unroll
@@ -676,67 +743,13 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
     return;
   }
 
-  // i16 epilogue through LDS: the requantised block tile is staged row-major in the (now idle) ring
-  // and written back with 16-byte stores along whole GB-column rows; stores straight from the MFMA
-  // layout would be 2-byte pieces per lane.
-  constexpr int OB = 2;
-  constexpr int PASS_ROWS = (GB * GB * OB <= T::LDS_BYTES) ? GB : GB / 2;
-  constexpr int ROWB = GB * OB;  // staged row bytes
-  lds_barrier();  // every wave is done reading the ring (the last DMA was waited for)
-  const bool vec_ok = ((p.ldo * OB) % 16 == 0) && ((uintptr_t)p.out % 16 == 0);
-  auto stage = [&](auto fast_tag, int pass) {
-    constexpr bool FAST = decltype(fast_tag)::value;
-    // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32
-#pragma unroll
-    for (int j = 0; j < T::WN; ++j) {
-      const int cl = wn + 32 * j + (lane & 31);
-      const int n = n0 + cl;
-#pragma unroll
-      for (int i = 0; i < T::WM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rl = wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-          const int m = m0 + rl;
-          const int32_t v = requant_col<FAST>(acc[i][j][r], cq[j]);
-          int8_t* slot = ring + (rl - pass * PASS_ROWS) * ROWB + cl * OB;
-          int32_t t = clamp32(v, -32768, 32767);
-          if (EPI == EPI_RESADD || EPI == EPI_MUL) {
-            const int32_t aux = (m < p.M && n < p.N) ? p.aux[(int64_t)m * p.ldaux + n] : 0;
-            if (EPI == EPI_RESADD) t = clamp32(t + aux, -32768, 32767);
-            else t = (int32_t)sat16(rshr((int64_t)(t * aux), p.aux_shift));
-          } else if (EPI == EPI_SILU) {
-            t = (int32_t)silu16(t, p.Mi, p.Si, p.sh);
-          }
-          *reinterpret_cast<int16_t*>(slot) = (int16_t)t;
-        }
-    }
-  };
-#pragma unroll
-  for (int pass = 0; pass < GB / PASS_ROWS; ++pass) {
-    if (wm / PASS_ROWS == pass) {
-      if (fast)
-        stage(std::true_type{}, pass);
-      else
-        stage(std::false_type{}, pass);
-    }
-    lds_barrier();
-    constexpr int CPR = ROWB / 16;  // 16-byte chunks per staged row
-    for (int idx = tid; idx < PASS_ROWS * CPR; idx += T::NT) {
-      const int rl = idx / CPR, ch = idx % CPR;
-      const int m = m0 + pass * PASS_ROWS + rl;
-      const int nc = n0 + ch * (16 / OB);
-      if (m >= p.M || nc >= p.N) continue;
-      const int8_t* src = ring + rl * ROWB + ch * 16;
-      char* dst = static_cast<char*>(p.out) + ((int64_t)m * p.ldo + nc) * OB;
-      if (vec_ok && nc + 16 / OB <= p.N) {
-        *reinterpret_cast<v4i*>(dst) = *reinterpret_cast<const v4i*>(src);
-      } else {
-        for (int e = 0; e < 16 / OB && nc + e < p.N; ++e)
-          for (int q = 0; q < OB; ++q) dst[e * OB + q] = src[e * OB + q];
-      }
-    }
-    if (pass + 1 < GB / PASS_ROWS) lds_barrier();
-  }
+  // i16 output (with the aux-reading epilogues) from registers as well
+  const bool full = m0 + GB <= p.M && n0 + GB <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 8 == 0 &&
+                    ((EPI != EPI_RESADD && EPI != EPI_MUL) || (p.ldaux % 4 == 0 && (uintptr_t)p.aux % 8 == 0));
+  if (fast)
+    store_i16_tile<EPI, true>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
+  else
+    store_i16_tile<EPI, false>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
 }
 
 // sum of the split-K planes + bias, requant and epilogue; four columns per thread
@@ -900,6 +913,7 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
   if (epilogue == EPI_MUL && !shift_ok(aux_shift)) return fail(-EINVAL, "linear: aux_shift out of [0,63]");
   if (epilogue == EPI_SILU && (!shift_ok(silu_Si) || !shift_ok(silu_sh)))
     return fail(-EINVAL, "linear: silu shift out of [0,63]");
+  if (epilogue == EPI_SILU && !u32_ok(silu_Mi)) return fail(-EINVAL, "linear: silu Mi must be u32");
   LinearArgs p{};
   p.A = A;
   p.W = W;
