@@ -85,7 +85,7 @@ int llhip_rope(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, c
  * A i8 (row stride lda), W i8 row-major [N][K], rq int32 pairs [N][2] = {M_n, S_n},
  * bias int32 [N] or NULL, aux i16 [M][N] (row stride ldaux) for resadd/mul.
  * epilogue: 0 none, 1 resadd, 2 silu, 3 mul.  out_i8 selects i8 output (epilogue 0 only),
- * otherwise i16.  The rq table's S_n must lie in [0,63] (checked by the caller); the silu
+ * otherwise i16.  The rq table's S_n must lie in [0,63], which the caller checks.  The silu
  * multiplier silu_Mi is u32 and its shifts lie in [0,63], as for llhip_silu. */
 int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_t* W, int64_t N, const int32_t* rq,
                  const int32_t* bias, int epilogue, const int16_t* aux, int64_t ldaux, int64_t aux_shift,
