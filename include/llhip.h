@@ -135,6 +135,16 @@ int llhip_greedy_rows(const int16_t* logits, int64_t rows, int64_t ld, int64_t v
                       int32_t* positions, const int32_t* base, int16_t* ring_rows, int64_t ring_ld,
                       int32_t* ring_tokens, int64_t ring_cap, void* stream);
 
+/* ---- record verification on the device (a long run checked without downloading its rows) ---- */
+/* verify.py:80-104 (compare_sim: records equal element by element) on device-resident i16 rows:
+ * *out = smallest flat index r * cols + c with a[r][c] != b[r][c], or -1 when the row sets are
+ * equal (out is an int64 in device memory) */
+int llhip_rows_first_mismatch_i16(const int16_t* a, int64_t lda, const int16_t* b, int64_t ldb, int64_t rows,
+                                  int64_t cols, int64_t* out, void* stream);
+/* verify.py:80-104 by checksum: out[r] = sum_c (c + 1) * (uint16)x[r][c] modulo 2^64, so two runs
+ * are compared by rows * 8 bytes (llaccel_amd/verify.py computes the same on the host) */
+int llhip_rows_checksum_i16(const int16_t* x, int64_t ld, int64_t rows, int64_t cols, uint64_t* out, void* stream);
+
 /* ---- fused decoder blocks (M <= 16 rows per launch) ----
  * Each computes a run of consecutive qgraph ops in one launch and writes every activation
  * those ops name, with the values the separate entry points above produce.  Row strides of

@@ -2,6 +2,8 @@
 // types (i16 in, i16/i8 out; NUMERICS.md "RMSNorm", "RoPE", "SiLU",
 // "Elementwise"), plus the host-loop helpers embedding gather and argmax
 // (golden.py:369-377).
+#include <algorithm>
+
 #include "../../include/llhip.h"
 #include "common.h"
 
@@ -318,6 +320,66 @@ __global__ __launch_bounds__(GR_THREADS) void greedy_rows_kernel(const int16_t* 
   positions[r] = positions[r] + 1;
 }
 
+
+// ---------------------------------------------------------------------------------------
+// record verification on the device (long runs checked without downloading every logits row)
+// ---------------------------------------------------------------------------------------
+// first mismatching element of two i16 row sets: smallest flat index r * cols + c, -1 if none.
+// Three stream-ordered launches (set, compare with atomicMin, finish): no memset, so they can be
+// captured in a graph.
+__global__ void mismatch_init_kernel(unsigned long long* out) { *out = ~0ull; }
+
+__global__ __launch_bounds__(256) void mismatch_kernel(const int16_t* __restrict__ a, int64_t lda,
+                                                       const int16_t* __restrict__ b, int64_t ldb, int64_t rows,
+                                                       int64_t cols, unsigned long long* out) {
+  const int64_t n = rows * cols;
+  unsigned long long first = ~0ull;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cols, c = i % cols;
+    if (a[r * lda + c] != b[r * ldb + c]) {
+      first = (unsigned long long)i;
+      break;  // later indices of this thread are larger
+    }
+  }
+  // wave minimum, then one atomic per wave
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)first, off), hi = __shfl_xor((uint32_t)(first >> 32), off);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    first = o < first ? o : first;
+  }
+  if ((threadIdx.x & 63) == 0 && first != ~0ull) atomicMin(out, first);
+}
+
+__global__ void mismatch_finish_kernel(unsigned long long* out) {
+  if (*out == ~0ull) *reinterpret_cast<int64_t*>(out) = -1;
+}
+
+// sum over the wave modulo 2^64 (any 64-bit lane values)
+__device__ __forceinline__ uint64_t wave_sum_u64_full(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, off), hi = __shfl_xor((uint32_t)(v >> 32), off);
+    v += ((uint64_t)hi << 32) | lo;
+  }
+  return v;
+}
+
+// per-row checksum sum_c (c + 1) * (uint16)x[r][c] modulo 2^64: exact, order-independent, and
+// position-weighted (a swap of two unequal values changes it); one workgroup per row
+__global__ __launch_bounds__(256) void row_checksum_kernel(const int16_t* __restrict__ x, int64_t ld, int64_t cols,
+                                                           uint64_t* __restrict__ out) {
+  __shared__ uint64_t part[4];
+  const int64_t r = blockIdx.x;
+  uint64_t acc = 0;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x)
+    acc += (uint64_t)(c + 1) * (uint64_t)(uint16_t)x[r * ld + c];
+  acc = wave_sum_u64_full(acc);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) out[r] = part[0] + part[1] + part[2] + part[3];
+}
+
 }  // namespace llhip
 
 using namespace llhip;
@@ -418,6 +480,32 @@ int llhip_argmax_i16(const int16_t* logits, int64_t rows, int64_t ld, int64_t vo
   if (rows < 0 || vocab <= 0 || ld < vocab) return fail(-EINVAL, "argmax: bad shape");
   if (rows == 0) return 0;
   hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, logits, ld, vocab, idx);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+int llhip_rows_first_mismatch_i16(const int16_t* a, int64_t lda, const int16_t* b, int64_t ldb, int64_t rows,
+                                  int64_t cols, int64_t* out, void* stream) {
+  if (rows < 0 || cols < 0 || lda < cols || ldb < cols || !out || ((rows && cols) && (!a || !b)))
+    return fail(-EINVAL, "rows_first_mismatch: bad arguments");
+  hipStream_t s = (hipStream_t)stream;
+  unsigned long long* o = reinterpret_cast<unsigned long long*>(out);
+  hipLaunchKernelGGL(mismatch_init_kernel, dim3(1), dim3(1), 0, s, o);
+  if (rows && cols) {
+    const int64_t n = rows * cols;
+    hipLaunchKernelGGL(mismatch_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 4096)), dim3(256), 0, s, a, lda,
+                       b, ldb, rows, cols, o);
+  }
+  hipLaunchKernelGGL(mismatch_finish_kernel, dim3(1), dim3(1), 0, s, o);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+int llhip_rows_checksum_i16(const int16_t* x, int64_t ld, int64_t rows, int64_t cols, uint64_t* out, void* stream) {
+  if (rows < 0 || cols < 0 || ld < cols || (rows && (!x || !out)) || rows > INT32_MAX)
+    return fail(-EINVAL, "rows_checksum: bad arguments");
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(row_checksum_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x, ld, cols, out);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }

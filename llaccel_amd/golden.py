@@ -937,6 +937,14 @@ class GoldenModel:
             return None
         return _down(self._ring_tok[:n]).astype(np.int64), self._ring_rows[:n].cpu().numpy()
 
+    def decode_ring(self, n: int):
+        """Device tensors of the last decode_loop's record (valid until the next one): the argmax
+        tokens (int32 [n]) and logits rows (int16 [n][vocab]) -- for checks on the device
+        (llaccel_amd.verify.first_mismatch / row_checksums) without downloading the rows."""
+        if not 0 <= n <= self._ring_cap:
+            raise ValueError(f"the decode ring holds {self._ring_cap} steps")
+        return self._ring_tok[:n], self._ring_rows[:n]
+
     # ---- batch decode: B independent sequences, one per row -------------------------------
     def _batch_state(self, B: int, ring_cap: int) -> None:
         torch = _t()
