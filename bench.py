@@ -17,8 +17,9 @@ The JSON line also carries
                  of the same decode launches on this host, and checked equal to the GPU's;
   extra        : prefill tok/s (GPU time of the one-launch 512-row prefill; prefill_api_ms adds
                  the host side of prefill(): all L logits rows downloaded and widened to int64),
-                 per-family decode timings, config 4 at batch 16, config-2 GEMM TOPS and GB/s
-                 (weights rotated through copies larger than the memory-side cache).
+                 per-family decode timings, config 4 at batch 16, config 5 (Qwen3 shape, T = 4096)
+                 decode launch time, config-2 GEMM TOPS and GB/s (weights rotated through copies
+                 larger than the memory-side cache).
 
     python bench.py [--gpus 1] [--steps 64] [--warmup 8]
     python bench.py --profile decode   # prefill + decode launches only (for rocprofv3)
@@ -91,6 +92,30 @@ def batch_decode(qdir: Path, args, single_tokens) -> dict:
     return {"batch": B, "tok_s": round(B * args.steps / dt, 1), "ms_per_step": round(dt / args.steps * 1e3, 4),
             "steps": args.steps, "prefill_ms_all": round(t_pre * 1e3, 1),
             "sequence0_tokens_equal_batch1": same}
+
+
+def config5_decode(args) -> dict:
+    """Config 5: Qwen3-0.6B shape (28 layers, dim 1024, 16/8 heads, head_dim 128, Q/K norm, vocab
+    151936), every layer's KV filled with seeded int8 at positions 0..4094, then the 28 layers +
+    lm_head of one decode launch at position 4095 (T = 4096 keys per head) captured as one graph
+    and replayed (the embedding gather and greedy step, ~12 us, are not in it)."""
+    import torch
+
+    from llaccel_amd import golden as G
+
+    qdir = build_workload("qwen3", args.seed)
+    g = G.GoldenModel(qdir)
+    gen = torch.Generator(device="cuda").manual_seed(4095 + args.seed)
+    for kc, vc in g._kv.values():
+        for t in (kc, vc):
+            t.copy_(torch.randint(-128, 128, tuple(t.shape), dtype=torch.int8, device="cuda", generator=gen))
+            t[:, :, 4095:] = 0
+    T = 4096
+    graph = g.capture_steps({getattr(st, "kind", "?") for st in g._plan}, T - 1)
+    dt = time_graph(graph, 20)
+    kv_bytes = sum(2 * kc[0].numel() for kc, _ in g._kv.values())
+    return {"T": T, "layers": g.n_layers, "ms_per_step": round(dt * 1e3, 4), "tok_s": round(1 / dt, 1),
+            "kv_bytes_read": kv_bytes, "note": "layers + lm_head of one M=1 decode launch at position 4095"}
 
 
 # decode kernel of each plan-step family (rocprofv3 kernel names)
@@ -202,6 +227,7 @@ def main() -> None:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-config5", action="store_true", help="skip the Qwen3 T=4096 decode timing")
     ap.add_argument("--batch", type=int, default=16, help="also time config 4's batch decode (1 = skip)")
     ap.add_argument("--profile", choices=("decode", "copy", "prefill", "gemm"),
                     help="workload-only runs for rocprofv3")
@@ -344,6 +370,9 @@ def main() -> None:
              "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1), "decode_kernel_families": fam}
     if batch is not None:
         extra[f"decode_batch{args.batch}"] = batch
+    if not args.no_config5:
+        extra["config5_decode_T4096"] = config5_decode(args)
+        log("config 5 decode", extra["config5_decode_T4096"])
     if not args.no_gemm:
         extra["gemm_sweep"] = gemm_sweep()
 

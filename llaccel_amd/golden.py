@@ -918,13 +918,15 @@ class GoldenModel:
 
         Launch i decodes at pos + i; its argmax feeds launch i + 1.  Returns the n argmax tokens
         and the n recorded logits rows ([n][vocab] int16) -- the decode part of the golden.json
-        record.  With `use_graph` each launch is one replay of a captured HIP graph."""
+        record.  With `use_graph` each launch is one replay of a captured HIP graph.  With
+        sync=False the device ring keeps its capacity (at least 64 launches) when that is smaller
+        than n: the later launches run but are not recorded, and no graph is captured again."""
         if n <= 0:
             return np.zeros(0, np.int64), np.zeros((0, self.vocab), np.int16)
         if pos < 0 or pos + n > self.max_seq:
             raise ValueError(f"positions {pos}..{pos + n - 1} exceed max_seq={self.max_seq}")
         torch = _t()
-        self._decode_state(n)
+        self._decode_state(n if sync else min(n, max(self._ring_cap, 64)))
         self._st.copy_(torch.tensor([int(self._token_rows([token])[0]), pos, 0], dtype=torch.int32))
         if self.use_graph and self._graph is None:
             self._capture()
@@ -951,7 +953,7 @@ class GoldenModel:
         if self._kv and next(iter(self._kv.values()))[0].shape[0] < B:
             raise ValueError(f"{B} sequences need {B} KV slots (generate_batch allocates them)")
         if getattr(self, "_b_rows", None) != B or ring_cap > self._b_cap:
-            cap = max(ring_cap, 16)
+            cap = max(ring_cap, 64)
             self._b_ring_rows = torch.zeros((cap, B, self.vocab), dtype=torch.int16, device=self.device)
             self._b_ring_tok = torch.zeros((cap, B), dtype=torch.int32, device=self.device)
             self._b_st = torch.zeros(3 * B, dtype=torch.int32, device=self.device)  # tokens, positions, base
@@ -975,7 +977,8 @@ class GoldenModel:
         """Run `n` greedy decode launches of B = len(tokens) sequences together: row b is sequence b,
         at position positions[b] + i in launch i, with its KV caches in slot b.  Every row is
         computed exactly as its own single-sequence decode launch.  Returns tokens [n][B] and
-        logits rows [n][B][vocab]."""
+        logits rows [n][B][vocab].  With sync=False the ring keeps its capacity (at least 64
+        launches), as in decode_loop."""
         B = len(tokens)
         if B < 1 or len(positions) != B:
             raise ValueError("tokens and positions must be nonempty and of equal length")
@@ -986,7 +989,7 @@ class GoldenModel:
             raise ValueError(f"positions up to {max(pos) + n - 1} exceed max_seq={self.max_seq}")
         torch = _t()
         self._ensure_capacity(B)
-        self._batch_state(B, n)
+        self._batch_state(B, n if sync else min(n, max(getattr(self, "_b_cap", 0), 64)))
         idx = [int(t) for t in self._token_rows(tokens)]
         self._b_st.copy_(torch.tensor(idx + pos + pos, dtype=torch.int32))
         if self.use_graph and self._graph_b is None:
