@@ -439,8 +439,8 @@ __device__ __forceinline__ int32_t requant_col(int32_t acc, const ColRq& c) {
 __device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) { return min(max(v, lo), hi); }
 
 // ---------------------------------------------------------------------------------------
-// Large GEMM (M >= 128, K % 64 == 0): GB x GB x 64 block tile (GB = 256 with 8 waves, 128 with 4),
-// 4-stage LDS ring fed by direct global->LDS loads (global_load_lds_dwordx4)
+// Large GEMM (M >= 128, K % 64 == 0): GM x GN x 64 block tile (256 x 256 with 8 waves, 128 x 128
+// or 64 x 128 with 4), 4-stage LDS ring fed by direct global->LDS loads (global_load_lds_dwordx4)
 // ---------------------------------------------------------------------------------------
 // Each wave instruction moves 64 x 16 B into 1 KiB of LDS (16 rows of 64 B).  Lane L of it
 // writes slot L of that KiB (row L/4, slot L%4) and fetches K chunk (L%4) ^ swz(row), so a row's
@@ -454,17 +454,38 @@ constexpr int GSTAGES = 4;
 
 __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-template <int GB, int NW>
+template <int GM, int GN, int NW>
 struct MfmaTile {
   static constexpr int NT = 64 * NW;
-  static constexpr int STAGE_BYTES = 2 * GB * 64;     // A + W of one K tile
+  static constexpr int STAGE_BYTES = (GM + GN) * 64;  // A + W of one K tile
   static constexpr int LDS_BYTES = GSTAGES * STAGE_BYTES;
-  static constexpr int WROWS = GB / 2;                // wave tile: 2 x NW/2 waves
-  static constexpr int WCOLS = 2 * GB / NW;
+  static constexpr int WROWS = GM / 2;                // wave tile: 2 x NW/2 waves
+  static constexpr int WCOLS = 2 * GN / NW;
   static constexpr int WM = WROWS / 32, WN = WCOLS / 32;  // 32x32 MFMA tiles per wave
-  static constexpr int LOADS = GB / (16 * NW);        // 1 KiB A (and W) loads per wave per stage
-  static_assert(LOADS == 2, "the vmcnt(4) wait assumes 2 A + 2 W loads per wave per stage");
+  static constexpr int LA = GM / (16 * NW);           // 1 KiB A loads per wave per stage
+  static constexpr int LW = GN / (16 * NW);           // 1 KiB W loads per wave per stage
+  static constexpr int LOADS = LA + LW;
+  static_assert(WM >= 1 && WN >= 1 && LA >= 1 && LW >= 1 && LA * 16 * NW == GM && LW * 16 * NW == GN, "tile shape");
+  static_assert(2 * LOADS <= 15, "vmcnt waits are encoded in the low 4 bits");
+  static_assert(LA <= 4 && LW <= 4, "load source arrays");
 };
+
+// s_waitcnt vmcnt(N), expcnt and lgkmcnt not waited for.  Each builtin call takes a literal: a
+// template-dependent argument keeps the host pass from emitting the kernels' launch stubs.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N == 0 || N == 3 || N == 4 || N == 6 || N == 8, "vmcnt values of the tile shapes");
+  if constexpr (N == 0)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  else if constexpr (N == 3)
+    __builtin_amdgcn_s_waitcnt(0x0F73);
+  else if constexpr (N == 4)
+    __builtin_amdgcn_s_waitcnt(0x0F74);
+  else if constexpr (N == 6)
+    __builtin_amdgcn_s_waitcnt(0x0F76);
+  else
+    __builtin_amdgcn_s_waitcnt(0x0F78);
+}
 
 __device__ __forceinline__ void lds_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -534,6 +555,23 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
   const bool lo2 = t < 2;
   const uint32_t selh = (t & 1) ? 0x03020706u : 0x05040100u;  // odd: [x.hi | own.hi], even: [own.lo | x.lo]
   int16_t* out = static_cast<int16_t*>(p.out);
+  // aux of every output group loaded before the first store: a load after a store to a pointer
+  // that may alias it would wait for the store, one memory round trip per group
+  constexpr bool AUX = EPI == EPI_RESADD || EPI == EPI_MUL;
+  v2i axr[AUX ? WM : 1][AUX ? WN : 1][4];
+  if (AUX && full) {
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int nq = ncol0 + 32 * j + 4 * ((lane & 31) >> 2);
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int m = mrow0 + 32 * i + g * 8 + (lane >> 5) * 4 + t;
+          axr[AUX ? i : 0][AUX ? j : 0][g] = *reinterpret_cast<const v2i*>(p.aux + (int64_t)m * p.ldaux + nq);
+        }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < WN; ++j) {
     const int nq = ncol0 + 32 * j + 4 * ((lane & 31) >> 2);
@@ -554,8 +592,8 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
         const int m = mrow0 + 32 * i + g * 8 + (lane >> 5) * 4 + t;
         int32_t o[4] = {lo16((int)t0), hi16((int)t0), lo16((int)t1), hi16((int)t1)};
         if (full) {
-          if (EPI == EPI_RESADD || EPI == EPI_MUL) {
-            const v2i ax = *reinterpret_cast<const v2i*>(p.aux + (int64_t)m * p.ldaux + nq);
+          if (AUX) {
+            const v2i ax = axr[AUX ? i : 0][AUX ? j : 0][g];
             const int32_t av[4] = {lo16(ax.x), hi16(ax.x), lo16(ax.y), hi16(ax.y)};
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -588,10 +626,10 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
 // Split-K (part != NULL): workgroup (tile, z = blockIdx.y) accumulates K tiles [z*kps, z*kps + kps)
 // and stores its int32 partial tile into plane z of part [splits][M][N]; linear_splitk_finish
 // sums the planes (integer addition: any split gives the same sum) and applies the epilogue.
-template <int EPI, bool OUT8, int GB, int NW>
+template <int EPI, bool OUT8, int GM, int GN, int NW>
 __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part) {
-  using T = MfmaTile<GB, NW>;
-  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A GBx64 | W GBx64]
+  using T = MfmaTile<GM, GN, NW>;
+  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A GMx64 | W GNx64]
   // The grid is padded to a multiple of 8 and workgroup b runs on XCD b % 8, which takes a
   // contiguous range of tiles (M fastest): the M-blocks that share a W panel share that XCD's L2.
   const int b = blockIdx.x;
@@ -599,30 +637,43 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
   if (logical >= mblocks * nblocks) return;
   const int mb = logical % mblocks;
   const int nbk = logical / mblocks;
-  const int m0 = mb * GB, n0 = nbk * GB;
+  const int m0 = mb * GM, n0 = nbk * GN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave & 1) * T::WROWS, wn = (wave >> 1) * T::WCOLS;
 
-  // this lane's source rows for the two A and two W load instructions of a stage
-  const int8_t* asrc[2];
-  const int8_t* wsrc[2];
+  // this lane's source rows for the LA A and LW W load instructions of a stage
+  const int8_t* asrc[4];  // fixed sizes (see wait_vmcnt)
+  const int8_t* wsrc[4];
+  const int kbase = (int)blockIdx.y * kps * 64;  // first K byte of this split
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (wave * 2 + i) * 16 + (lane >> 2);
-    const int chunk = (lane & 3) ^ lds_swz(r);
-    const int gm = min(m0 + r, p.M - 1), gn = min(n0 + r, p.N - 1);
-    const int kbase = (int)blockIdx.y * kps * 64;  // first K byte of this split
-    asrc[i] = p.A + (int64_t)gm * p.lda + kbase + chunk * 16;
-    wsrc[i] = p.W + (int64_t)gn * p.K + kbase + chunk * 16;
+  for (int i = 0; i < T::LA; ++i) {
+    const int r = (wave * T::LA + i) * 16 + (lane >> 2);
+    const int gm = min(m0 + r, p.M - 1);
+    asrc[i] = p.A + (int64_t)gm * p.lda + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < T::LW; ++i) {
+    const int r = (wave * T::LW + i) * 16 + (lane >> 2);
+    const int gn = min(n0 + r, p.N - 1);
+    wsrc[i] = p.W + (int64_t)gn * p.K + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
   }
   auto issue = [&](int kt) {
     int8_t* st = ring + (kt % GSTAGES) * T::STAGE_BYTES;
     const int k0 = kt * 64;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      __builtin_amdgcn_global_load_lds(asrc[i] + k0, st + (wave * 2 + i) * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(wsrc[i] + k0, st + GB * 64 + (wave * 2 + i) * 1024, 16, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      // explicitly typed operands (see wait_vmcnt)
+      if (i < T::LA) {
+        const int8_t* src = asrc[i] + k0;
+        int8_t* dst = st + (wave * T::LA + i) * 1024;
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      }
+      if (i < T::LW) {
+        const int8_t* src = wsrc[i] + k0;
+        int8_t* dst = st + GM * 64 + (wave * T::LW + i) * 1024;
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      }
     }
   };
   // LDS offsets of this lane's fragments for the two 32-byte K steps of a tile
@@ -638,7 +689,7 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
 #pragma unroll
     for (int j = 0; j < T::WN; ++j) {
       const int r = wn + 32 * j + (lane & 31);
-      woff[j][ks] = GB * 64 + r * 64 + ((c ^ lds_swz(r)) << 4);
+      woff[j][ks] = GM * 64 + r * 64 + ((c ^ lds_swz(r)) << 4);
     }
   }
   // SiLU table for the silu epilogue, staged in LDS (visible after the main loop's barriers)
@@ -662,11 +713,11 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
   const int ktiles = min(kps, p.K / 64 - (int)blockIdx.y * kps);
   for (int s0 = 0; s0 < GSTAGES - 1; ++s0)
     if (s0 < ktiles) issue(s0);
-  // tile 0 landed: at most the next two tiles' 2 x 4 loads are outstanding
+  // tile 0 landed: at most the next two tiles' loads are outstanding
   if (ktiles > 2)
-    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    wait_vmcnt<2 * T::LOADS>();
   else
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    wait_vmcnt<0>();
   lds_barrier();
   v4i fa0[T::WM], fb0[T::WN], fa1[T::WM], fb1[T::WN];
 #pragma unroll
@@ -685,14 +736,14 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
 #pragma unroll
       for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
     mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
-    // Tile kt+1 landed once at most tile kt+2's 4 loads are outstanding; after the barrier every
+    // Tile kt+1 landed once at most tile kt+2's loads are outstanding; after the barrier every
     // wave's copies of it are visible and every wave has finished reading stage (kt-1) % 4, which
     // issue(kt + 3) overwrites.  A bare s_barrier: __syncthreads() would also drain the later
     // tiles still in flight.
     if (kt + 2 < ktiles)
-      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+      wait_vmcnt<T::LOADS>();
     else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      wait_vmcnt<0>();
     lds_barrier();
     if (kt + GSTAGES - 1 < ktiles) issue(kt + GSTAGES - 1);
     // second K step of tile kt while the next tile's first-step fragments are read (after the
@@ -735,7 +786,7 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
   const bool fast = __all(col_fast);
 
   if constexpr (OUT8) {
-    const bool full = m0 + GB <= p.M && n0 + GB <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 4 == 0;
+    const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 4 == 0;
     if (fast)
       store_i8_tile<true>(p, acc, cq, m0 + wm, n0 + wn, full);
     else
@@ -744,7 +795,7 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
   }
 
   // i16 output (with the aux-reading epilogues) from registers as well
-  const bool full = m0 + GB <= p.M && n0 + GB <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 8 == 0 &&
+  const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 8 == 0 &&
                     ((EPI != EPI_RESADD && EPI != EPI_MUL) || (p.ldaux % 4 == 0 && (uintptr_t)p.aux % 8 == 0));
   if (fast)
     store_i16_tile<EPI, true>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
@@ -778,58 +829,62 @@ __global__ __launch_bounds__(256) void linear_splitk_finish(LinearArgs p, const 
 // ---------------------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------------------
+// One MFMA GEMM launch with GM x GN tiles.  Too few output tiles for the CUs (narrow projections of
+// a prompt): split K into ranges of at least 4 K tiles whose int32 partial tiles fit the workspace,
+// then sum them.  The split count maximises (K-loop time saved) - (partial-plane traffic + the
+// finishing launch), with measured costs: ~0.5 us (128x128) or ~0.4 us (64x128) per K tile of a
+// workgroup, ~5 us for the finishing launch and ~4 TB/s for the planes.
+template <int EPI, bool OUT8, int GM, int GN, int NW>
+static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
+  using T = MfmaTile<GM, GN, NW>;
+  const int mblocks = (int)ceil_div(p.M, GM), nblocks = (int)ceil_div(p.N, GN);
+  const int64_t tiles = (int64_t)mblocks * nblocks;
+  const int ktiles = (int)(p.K / 64);
+  const int cus = current_cu_count();
+  int splits = 1;
+  if (ws && p.N % 4 == 0 && tiles < cus) {
+    const int smax = (int)std::min<int64_t>(std::min<int64_t>(8, ceil_div(2 * cus, tiles)), ktiles / 4);
+    double best = 0.0;
+    for (int sp = 2; sp <= smax; ++sp) {
+      const double plane_bytes = (double)sp * p.M * p.N * 4;
+      if (plane_bytes > (double)WS_SCRATCH_BYTES) break;
+      const double gain = (GM * GN >= 128 * 128 ? 0.5 : 0.4) * ktiles * (sp - 1) / sp - (5.0 + plane_bytes / 4e6);
+      if (gain > best) {
+        best = gain;
+        splits = sp;
+      }
+    }
+  }
+  const int kps = (int)ceil_div(ktiles, splits);
+  splits = (int)ceil_div(ktiles, kps);
+  int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
+  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW>), dim3(ceil_div(mblocks * nblocks, 8) * 8, splits),
+                     dim3(T::NT), T::LDS_BYTES, stream, p, mblocks, nblocks, kps, part);
+  LLHIP_LAUNCH_CHECK();
+  if (part) {
+    const int64_t quads = (int64_t)p.M * p.N / 4;
+    hipLaunchKernelGGL((linear_splitk_finish<EPI, OUT8>), dim3((unsigned)std::min<int64_t>(ceil_div(quads, 256), 8 * cus)),
+                       dim3(256), 0, stream, p, part, splits);
+    LLHIP_LAUNCH_CHECK();
+  }
+  return 0;
+}
+
 template <int EPI, bool OUT8>
 static int launch_linear(LinearArgs& p, void* ws, hipStream_t stream) {
   const bool aligned = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.W % 16 == 0);
   if (p.M >= 128 && p.K % 64 == 0 && aligned) {
-    // 256x256 tiles when M fills them and they fill every CU, else 128x128.  The 256x256 kernel keeps 128
+    // 256x256 tiles when M fills them and they fill every CU.  The 256x256 kernel keeps 128
     // accumulators per lane at two waves per SIMD; the aux-reading epilogues would spill there.
     if constexpr (EPI == EPI_NONE) {
-      if (p.M >= 256 && (int64_t)ceil_div(p.M, 256) * ceil_div(p.N, 256) >= current_cu_count()) {
-        using T = MfmaTile<256, 8>;
-        const int mblocks = (int)ceil_div(p.M, 256), nblocks = (int)ceil_div(p.N, 256);
-        hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 256, 8>), dim3(ceil_div(mblocks * nblocks, 8) * 8), dim3(T::NT),
-                           T::LDS_BYTES, stream, p, mblocks, nblocks, p.K / 64, (int32_t*)nullptr);
-        LLHIP_LAUNCH_CHECK();
-        return 0;
-      }
+      if (p.M >= 256 && (int64_t)ceil_div(p.M, 256) * ceil_div(p.N, 256) >= current_cu_count())
+        return launch_mfma<EPI, OUT8, 256, 256, 8>(p, ws, stream);
     }
-    using T = MfmaTile<128, 4>;
-    const int mblocks = (int)ceil_div(p.M, 128), nblocks = (int)ceil_div(p.N, 128);
-    // Too few output tiles for the CUs (narrow projections of a prompt): split K into ranges of at
-    // least 4 K tiles whose int32 partial tiles fit the workspace, then sum them.  The split count
-    // maximises (K-loop time saved) - (partial-plane traffic + one more launch), with the measured
-    // ~0.5 us per K tile of a workgroup and ~4 TB/s for the planes.
-    const int64_t tiles = (int64_t)mblocks * nblocks;
-    const int ktiles = (int)(p.K / 64);
-    const int cus = current_cu_count();
-    int splits = 1;
-    if (ws && p.N % 4 == 0 && tiles < cus) {
-      const int smax = (int)std::min<int64_t>(std::min<int64_t>(8, ceil_div(2 * cus, tiles)), ktiles / 4);
-      double best = 0.0;
-      for (int sp = 2; sp <= smax; ++sp) {
-        const double plane_bytes = (double)sp * p.M * p.N * 4;
-        if (plane_bytes > (double)WS_SCRATCH_BYTES) break;
-        const double gain = 0.5 * ktiles * (sp - 1) / sp - (2.0 + plane_bytes / 4e6);
-        if (gain > best) {
-          best = gain;
-          splits = sp;
-        }
-      }
-    }
-    const int kps = (int)ceil_div(ktiles, splits);
-    splits = (int)ceil_div(ktiles, kps);
-    int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
-    hipLaunchKernelGGL((linear_mfma<EPI, OUT8, 128, 4>), dim3(ceil_div(mblocks * nblocks, 8) * 8, splits), dim3(T::NT),
-                       T::LDS_BYTES, stream, p, mblocks, nblocks, kps, part);
-    LLHIP_LAUNCH_CHECK();
-    if (part) {
-      const int64_t quads = (int64_t)p.M * p.N / 4;
-      hipLaunchKernelGGL((linear_splitk_finish<EPI, OUT8>), dim3((unsigned)std::min<int64_t>(ceil_div(quads, 256), 8 * cus)),
-                         dim3(256), 0, stream, p, part, splits);
-      LLHIP_LAUNCH_CHECK();
-    }
-    return 0;
+    // 128x128 tiles while they fill the CUs, else 64x128 tiles (twice as many workgroups, three per
+    // CU), split along K when even those are too few
+    if ((int64_t)ceil_div(p.M, 128) * ceil_div(p.N, 128) >= current_cu_count())
+      return launch_mfma<EPI, OUT8, 128, 128, 4>(p, ws, stream);
+    return launch_mfma<EPI, OUT8, 64, 128, 4>(p, ws, stream);
   }
   if (p.M > 16 && aligned) {
     // 128x256 block tiles when they still fill the chip, else 128x128

@@ -21,6 +21,15 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(_lib._SIGS), "ctypes signature table out of sync with include/llhip.h"
 
 
+def test_library_resolves_every_symbol_at_load():
+    """Every symbol the library references resolves when it is bound eagerly: a kernel template the
+    host compilation pass failed to instantiate leaves its launch stub undefined, which a lazy load
+    only reports at the first launch."""
+    import os
+
+    ctypes.CDLL(str(_lib.LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+
+
 def test_abi_version_and_workspace():
     L = _lib.lib()
     assert L.llhip_abi_version() == 2
