@@ -145,6 +145,16 @@ int llhip_rows_first_mismatch_i16(const int16_t* a, int64_t lda, const int16_t* 
  * are compared by rows * 8 bytes (llaccel_amd/verify.py computes the same on the host) */
 int llhip_rows_checksum_i16(const int16_t* x, int64_t ld, int64_t rows, int64_t cols, uint64_t* out, void* stream);
 
+/* ---- quantizer (the float -> integer conversions of the qgraph producer) ----
+ * refquant.py:137-141 + 119-125  per-output-channel int8 weights of w f32 [N][K] (row stride ldw):
+ * scales[n] = max|w[n,:]| / 127 as a double (1 for an all-zero row), q[n][k] = llround(clip(w[n][k] /
+ * scales[n], -128, 127)), llround rounding halves away from zero (refquant.py:61-72).  A non-finite
+ * weight sets *status to 1 (status is an int32 in device memory, zeroed by the caller). */
+int llhip_quant_rows_i8(const float* w, int64_t N, int64_t K, int64_t ldw, int8_t* q, int64_t ldq, double* scales,
+                        int32_t* status, void* stream);
+/* refquant.py:128-134  i16 tensor at exponent e: y = llround(clip(x * 2^-e, -32768, 32767)). */
+int llhip_quant_i16(const float* x, int64_t n, int64_t e, int16_t* y, int32_t* status, void* stream);
+
 /* ---- fused decoder blocks (M <= 16 rows per launch) ----
  * Each computes a run of consecutive qgraph ops in one launch and writes every activation
  * those ops name, with the values the separate entry points above produce.  Row strides of

@@ -421,6 +421,40 @@ def build_qgraph(out_dir, cfg: ModelConfig | str, *, seed: int = 0, fusion: bool
     return out
 
 
+def write_export(out_dir, cfg: ModelConfig | str, *, seed: int = 0, calib_len: int = 32,
+                 weights: dict | None = None) -> Path:
+    """A model export directory in the reference's format (read by refquant.py:275-301 and by
+    llaccel_amd.quantize.load_export) for the seeded float model of `cfg`: `model.mlir` with the
+    `llaccel.model` attribute and the weight declarations, `weights.bin` (little-endian f32) +
+    `weights.json` (name, shape, byte offset), and `calib.json` (abs-max of every named activation
+    over the seeded calibration sequence).  Returns out_dir."""
+    if isinstance(cfg, str):
+        cfg = CONFIGS[cfg]
+    out = Path(out_dir)
+    out.mkdir(parents=True, exist_ok=True)
+    W = weights if weights is not None else float_weights(cfg, seed)
+    crng = np.random.default_rng(seed + 1000)
+    amax = calibrate(cfg, W, crng.integers(0, cfg.vocab, min(calib_len, cfg.max_seq)).tolist())
+    attrs = {"dim": cfg.dim, "n_layers": cfg.n_layers, "n_heads": cfg.n_heads, "n_kv_heads": cfg.n_kv_heads,
+             "head_dim": cfg.head_dim, "ffn": cfg.ffn, "vocab": cfg.vocab, "max_seq": cfg.max_seq}
+    body = ", ".join(f"{k} = {v} : i64" for k, v in attrs.items())
+    body += f", rope_base = {float(cfg.rope_base)!r} : f64, rms_eps = {float(cfg.rms_eps)!r} : f64"
+    lines = [f"module attributes {{llaccel.model = {{{body}}}}} {{"]
+    index, off = [], 0
+    with open(out / "weights.bin", "wb") as f:
+        for name, arr in W.items():
+            a = np.ascontiguousarray(arr, dtype="<f4")
+            lines.append(f"  llaccel.weight @{name} : tensor<{'x'.join(str(s) for s in a.shape)}xf32>")
+            index.append({"name": name, "shape": [int(s) for s in a.shape], "offset": off})
+            f.write(a.tobytes())
+            off += a.nbytes
+    lines.append("}")
+    (out / "model.mlir").write_text("\n".join(lines) + "\n")
+    (out / "weights.json").write_text(json.dumps(index, indent=1))
+    (out / "calib.json").write_text(json.dumps(amax, indent=1))
+    return out
+
+
 def seeded_prompt(cfg: ModelConfig | str, length: int, seed: int = 0) -> list[int]:
     """Prompt ids uniform over [0, vocab) from numpy's default_rng(seed)."""
     if isinstance(cfg, str):

@@ -42,10 +42,11 @@ def test_header_declarations_cite_the_reference():
         if name in ("llhip_abi_version", "llhip_last_error", "llhip_workspace_bytes"):
             continue
         # the comment block directly above each compute entry point cites the reference function it
-        # replaces: golden.py:<lines> (the datapath) or verify.py:<lines> (record verification)
+        # replaces: golden.py:<lines> (the datapath), verify.py:<lines> (record verification) or
+        # refquant.py:<lines> (the qgraph producer)
         idx = text.index(name + "(")
         before = text[:idx].rsplit(");", 1)[-1]
-        assert re.search(r"(golden|verify)\.py:\d+", before), name
+        assert re.search(r"(golden|verify|refquant)\.py:\d+", before), name
 
 
 def test_hip_luts_are_current_and_equal_reference(golden_dir):
