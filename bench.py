@@ -19,13 +19,15 @@ The JSON line also carries
                  the host side of prefill(): all L logits rows downloaded and widened to int64),
                  per-family decode timings, config 4 at batch 16, config 5 (Qwen3 shape, T = 4096)
                  decode launch time, config-2 GEMM TOPS and GB/s (weights rotated through copies
-                 larger than the memory-side cache).
+                 larger than the memory-side cache), the qgraph producer's weight conversion
+                 (llhip_quant_rows_i8, lm_head-shaped f32) against HBM and its numpy baseline.
 
     python bench.py [--gpus 1] [--steps 64] [--warmup 8]
     python bench.py --profile decode   # prefill + decode launches only (for rocprofv3)
     python bench.py --profile prefill  # prefill() once, then three one-launch 512-row prefills
     python bench.py --profile gemm     # config 2's M=2048 x K=896 x N=151936 GEMM, 7 launches
     python bench.py --profile copy     # 256 MiB device copies (counter calibration)
+    python bench.py --profile quant    # llhip_quant_rows_i8 on a 151936 x 896 f32 matrix, 7 launches
 """
 from __future__ import annotations
 
@@ -217,6 +219,53 @@ def gemm_sweep(min_reps: int = 8):
     return out
 
 
+def quantizer_bench(cpu_rows: int = 2048) -> dict:
+    """The qgraph producer's weight conversion (llhip_quant_rows_i8) on an lm_head-shaped f32
+    matrix (151936 x 896, 544 MB, larger than the memory-side cache): HIP events over a graph of
+    launches; algorithmic bytes 4NK read + NK + 8N written.  CPU baseline: the float64 numpy
+    restatement (oracle/quant_np.py) on the first `cpu_rows` rows, checked equal to the GPU's."""
+    import ctypes
+
+    import torch
+
+    from llaccel_amd import _lib
+    from llaccel_amd.golden import capture_graph
+    from oracle import quant_np as QN
+
+    N, K, reps = 151936, 896, 10
+    g = torch.Generator(device="cuda").manual_seed(17)
+    w = torch.randn((N, K), dtype=torch.float32, device="cuda", generator=g) * 0.02
+    q = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    sc = torch.empty(N, dtype=torch.float64, device="cuda")
+    st = torch.zeros(1, dtype=torch.int32, device="cuda")
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def launch():
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.call("llhip_quant_rows_i8", p(w), N, K, K, p(q), K, p(sc), p(st), s)
+
+    graph = torch.cuda.CUDAGraph()
+    with capture_graph(graph):
+        for _ in range(reps):
+            launch()
+    dt = time_graph(graph, 3) / reps
+    nbytes = 5 * N * K + 8 * N
+    wh = w[:cpu_rows].cpu().numpy().astype(np.float64)
+    t0 = time.perf_counter()
+    cq, cs = QN.quant_rows_i8(wh)
+    cdt = time.perf_counter() - t0
+    same = bool(np.array_equal(cq, q[:cpu_rows].cpu().numpy()) and np.array_equal(cs, sc[:cpu_rows].cpu().numpy())
+                and int(st.item()) == 0)
+    out = {"shape": [N, K], "us": round(dt * 1e6, 2), "GBs": round(nbytes / dt / 1e9, 1),
+           "frac_hbm": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes,
+           "cpu_baseline": {"rows_per_s": round(cpu_rows / cdt, 1), "GBs": round(5 * cpu_rows * K / cdt / 1e9, 3),
+                            "cores": 1, "kind": "port",
+                            "sample": f"first {cpu_rows} rows, float64 numpy restatement; equal to the GPU: {same}"},
+           "gpu_rows_per_s": round(N / dt, 1)}
+    del graph, w, q
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,8 +277,9 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-config5", action="store_true", help="skip the Qwen3 T=4096 decode timing")
+    ap.add_argument("--no-quant", action="store_true", help="skip the weight-quantization kernel timing")
     ap.add_argument("--batch", type=int, default=16, help="also time config 4's batch decode (1 = skip)")
-    ap.add_argument("--profile", choices=("decode", "copy", "prefill", "gemm"),
+    ap.add_argument("--profile", choices=("decode", "copy", "prefill", "gemm", "quant"),
                     help="workload-only runs for rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -271,6 +321,26 @@ def main() -> None:
                       p(ws), s)
         torch.cuda.synchronize()
         log(f"gemm {M}x{K}x{N}: 7 launches")
+        return
+
+    if args.profile == "quant":
+        # the weight conversion of the qgraph producer on an lm_head-shaped f32 matrix, 7 launches
+        import ctypes
+
+        from llaccel_amd import _lib
+
+        N, K = 151936, 896
+        g = torch.Generator(device="cuda").manual_seed(17)
+        w = torch.randn((N, K), dtype=torch.float32, device="cuda", generator=g) * 0.02
+        q = torch.empty((N, K), dtype=torch.int8, device="cuda")
+        sc = torch.empty(N, dtype=torch.float64, device="cuda")
+        st = torch.zeros(1, dtype=torch.int32, device="cuda")
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for _ in range(7):
+            _lib.call("llhip_quant_rows_i8", p(w), N, K, K, p(q), K, p(sc), p(st), s)
+        torch.cuda.synchronize()
+        log(f"quant_rows_i8 {N}x{K}: 7 launches")
         return
 
     from llaccel_amd import golden as G
@@ -375,6 +445,9 @@ def main() -> None:
         log("config 5 decode", extra["config5_decode_T4096"])
     if not args.no_gemm:
         extra["gemm_sweep"] = gemm_sweep()
+    if not args.no_quant:
+        extra["quantize_rows_i8"] = quantizer_bench()
+        log("quantize", extra["quantize_rows_i8"])
 
     line = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True,

@@ -71,6 +71,30 @@ def test_quant_rows_i8_equals_oracle(N, K):
     assert np.array_equal(q2[:N], q) and not q2[N:].any() and s2[N:].tolist() == [1.0] * 3
 
 
+@pytest.mark.parametrize("K", [64, 896])
+def test_quant_rows_i8_ties_near_ties_and_tiny_rows(K):
+    """The wave kernel rounds from a float32 quotient and settles near-halves in float64: exact
+    halves (row max 127 * 2^-3, entries (k + 1/2) * 2^-3), entries one ulp either side of them,
+    rows whose abs-max is subnormal or just above 2^-100, and rows at the float32 maximum."""
+    rng = np.random.default_rng(K)
+    rows = []
+    k = rng.integers(-127, 127, K)
+    half = ((k + 0.5) * 0.125).astype(np.float32)
+    half[0] = 127 * 0.125
+    rows.append(half)
+    rows.append(np.nextafter(half, np.float32(np.inf)))
+    rows.append(np.nextafter(half, np.float32(-np.inf)))
+    for scale in (1e-39, 3e-45, 2.0**-99, 2.0**-101, 3.0e38, 1.7):
+        r = (np.clip(rng.standard_normal(K), -1.1, 1.1) * scale).astype(np.float32)  # finite at 3e38
+        r[1] = np.float32(scale)
+        rows.append(r)
+    w = np.stack(rows)
+    q, s, st = _rows_i8(w)
+    wq, ws = QN.quant_rows_i8(w.astype(np.float64))
+    assert st == 0 and np.array_equal(s, ws) and np.array_equal(q, wq)
+    assert np.array_equal(q[0, 1:], np.clip(np.where(k[1:] >= 0, k[1:] + 1, k[1:]), -128, 127))
+
+
 def test_quant_rows_i8_strided_and_non_finite():
     t = torch()
     rng = np.random.default_rng(3)
