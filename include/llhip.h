@@ -79,6 +79,14 @@ int llhip_vadd(const int16_t* a, const int16_t* b, int64_t n, int64_t sh_b, int1
 int llhip_rope(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, const int16_t* cos_tab,
                const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev,
                const int32_t* row_pos, int16_t* y, int64_t ldy, void* stream);
+/* golden.py:141-158 + 119-120 [+ 344-351]  RoPE of M rows of H heads, then quant (qM, qS) of the
+ * rotated rows: y i16 and yq i8, both [M][H*D].  With kc non-NULL the quantised rows also go to the
+ * K cache at their positions, and with vc non-NULL the v rows [M][ldv] to the V cache (the layer's
+ * kv_write; caches [slots][H][max_seq][D], slot m at m * slot_stride with row_pos). */
+int llhip_rope_quant(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, const int16_t* cos_tab,
+                     const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev,
+                     const int32_t* row_pos, int16_t* y, int8_t* yq, int64_t qM, int64_t qS, int8_t* kc,
+                     const int8_t* v, int64_t ldv, int8_t* vc, int64_t max_seq, int64_t slot_stride, void* stream);
 
 /* ---- gemm engine ---- */
 /* golden.py:316-342  out[M][N] = epilogue(requant(A[M][K] . W[N][K]^T + bias)).

@@ -51,6 +51,8 @@ _SIGS = {
     "llhip_greedy_rows": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p],
     "llhip_rows_first_mismatch_i16": [_p, _i64, _p, _i64, _i64, _i64, _p, _p],
     "llhip_rows_checksum_i16": [_p, _i64, _i64, _i64, _p, _p],
+    "llhip_rope_quant": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _p,
+                         _i64, _i64, _p],
     "llhip_quant_rows_i8": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
     "llhip_quant_i16": [_p, _i64, _i64, _p, _p, _p],
     "llhip_rmsnorm_quant": [_p, _i64, _p],

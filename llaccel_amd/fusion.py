@@ -30,16 +30,18 @@ def _vp(t):
 
 
 class FusedStep:
-    """`kind` names the fused kernel; `fallback` are the per-op steps it replaces."""
+    """`kind` names the fused kernel; `fallback` are the per-op steps it replaces, `wide` the
+    launches that run instead when the fused kernel does not take the rows (see wide_steps)."""
 
     def __init__(self, model, kind, fallback, fill, entry, desc_cls, K, bytes_fn, name, ops):
         self.model, self.kind, self.fallback, self.fill = model, kind, fallback, fill
         self.entry, self.desc = entry, desc_cls()
         self.K, self.bytes_fn, self.name, self.ops = K, bytes_fn, name, ops
+        self.wide = wide_steps(model, ops, fallback)
 
     def __call__(self, M, pos, pd=None):
         if M > 16 or M * (self.K + 16) > LDS_LIMIT or self.K > NORM_MAX_K:
-            for st in self.fallback:
+            for st in self.wide:
                 st(M, pos, pd)
             return
         self.fill(self.desc, M, pos, pd)
@@ -49,6 +51,75 @@ class FusedStep:
         if M > 1:
             _lib.call("llhip_rmsnorm_quant", ctypes.byref(self.desc.pre), M, m._stream_handle())
         _lib.call(self.entry, ctypes.byref(self.desc), m._stream_handle())
+
+
+class _NormQuantStep:
+    """rmsnorm -> quant of its output for any number of rows: one llhip_rmsnorm_quant launch (one
+    workgroup per row) writing both activations."""
+
+    def __init__(self, model, rn, qu):
+        self.model, self.rn, self.qu = model, rn, qu
+        self.desc = _lib.NormQuantDesc()
+
+    def __call__(self, M, pos, pd=None):
+        _pre(self.model, self.desc, self.rn, self.qu)
+        self.desc.prequant = 0
+        _lib.call("llhip_rmsnorm_quant", ctypes.byref(self.desc), M, self.model._stream_handle())
+
+
+class _RopeQuantStep:
+    """rope -> quant of the rotated rows in one llhip_rope_quant launch; for the key rows also the
+    layer's kv_write (quantised keys and the v rows into the caches)."""
+
+    def __init__(self, model, rope, quant, kvw=None):
+        self.model, self.rope, self.quant, self.kvw = model, rope, quant, kvw
+
+    def __call__(self, M, pos, pd=None):
+        m, ro, qu, kvw = self.model, self.rope, self.quant, self.kvw
+        H, D = int(ro["H"]), int(ro["D"])
+        cos_t, sin_t = m._dt["rope_cos"], m._dt["rope_sin"]
+        if kvw is None:
+            from .golden import _pos_args
+
+            pdev, rpos, stride = _pos_args(pd)
+            kc = vc = v = None
+            ldv = 0
+        else:
+            kc, vc, pdev, rpos, stride = m._kv_args(int(kvw["layer"]), pd)
+            vbuf = m._buf(kvw["v"])
+            v, ldv = _vp(vbuf), vbuf.shape[1]
+        _lib.call("llhip_rope_quant", _vp(m._buf(ro["in"])), M, H, D, H * D, _vp(cos_t), _vp(sin_t),
+                  int(cos_t.shape[0]), pos, pdev, rpos, _vp(m._buf(ro["out"])), _vp(m._buf(qu["out"])),
+                  int(qu["M"]), int(qu["S"]), kc, v, ldv, vc, m.max_seq, stride, m._stream_handle())
+
+
+def wide_steps(model, ops, steps):
+    """Launches of a fused run for more rows than its fused kernel takes (prompt chunks): the run's
+    per-op steps, with each rmsnorm + quant of its output as one launch and attn_in's group
+    rope q, rope k, quant q, quant k, kv_write as two.  The arithmetic of every op is unchanged."""
+    out, i = [], 0
+    while i < len(ops):
+        a = ops[i]
+        if (i + 1 < len(ops) and _is(a, "rmsnorm") and int(a.get("heads", 1)) == 1 and _is(ops[i + 1], "quant")
+                and ops[i + 1]["in"] == a["out"]):
+            K = int(model._dt[a["gamma"]].shape[0])
+            if K % 16 == 0 and K <= NORM_MAX_K:
+                out.append(_NormQuantStep(model, a, ops[i + 1]))
+                i += 2
+                continue
+        if i + 4 < len(ops):
+            rq_, rk_, qq_, kq_, kvw = ops[i:i + 5]
+            if (_is(rq_, "rope") and _is(rk_, "rope") and _is(qq_, "quant") and _is(kq_, "quant")
+                    and _is(kvw, "kv_write") and qq_["in"] == rq_["out"] and kq_["in"] == rk_["out"]
+                    and kvw["k"] == kq_["out"] and int(kvw["Hkv"]) == int(rk_["H"]) and int(kvw["D"]) == int(rk_["D"])
+                    and model._act_spec[kvw["v"]][1] >= int(rk_["H"]) * int(rk_["D"])):
+                out.append(_RopeQuantStep(model, rq_, qq_))
+                out.append(_RopeQuantStep(model, rk_, kq_, kvw))
+                i += 5
+                continue
+        out.append(steps[i])
+        i += 1
+    return out
 
 
 def _pre(model, d, op_norm, op_quant):

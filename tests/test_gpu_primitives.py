@@ -155,3 +155,52 @@ def test_argmax_lowest_index_on_ties():
     row = RNG.integers(-32768, 32768, 49152)
     assert G.GoldenModel.argmax(row, 49152) == int(np.argmax(row))
     assert G.GoldenModel.argmax(row, 1000) == int(np.argmax(row[:1000]))
+
+
+@pytest.mark.parametrize("H,D,rows", [(2, 64, False), (8, 128, False), (4, 16, True)])
+def test_rope_quant_with_cache_writes(H, D, rows):
+    """llhip_rope_quant (the prompt-chunk launch of rope -> quant [-> kv_write]) equals the oracle's
+    rope, vquant and cache write; with per-row positions each row writes its own cache slot."""
+    from llaccel_amd import _lib
+    from tests.gpu_helpers import ptr, stream, torch, up
+
+    t = torch()
+    M, max_seq, pos, qM, qS = 40, 96, 50, 1234567891, 40
+    inv = 1e6 ** (-np.arange(0, D, 2) / D)
+    ang = np.outer(np.arange(max_seq), inv)
+    c = np.round(np.cos(ang) * 16384).astype(np.int64)
+    s = np.round(np.sin(ang) * 16384).astype(np.int64)
+    x = RNG.integers(-32768, 32768, (M, H * D))
+    v = RNG.integers(-128, 128, (M, H * D + 8))
+    slots = M if rows else 1
+    kc0 = RNG.integers(-128, 128, (slots, H, max_seq, D))
+    vc0 = RNG.integers(-128, 128, (slots, H, max_seq, D))
+    rp = RNG.integers(0, max_seq, M) if rows else None
+    xd, cd, sd, vd = up(x, np.int16), up(c, np.int16), up(s, np.int16), up(v, np.int8)
+    kcd, vcd = up(kc0, np.int8), up(vc0, np.int8)
+    rpd = up(rp, np.int32) if rows else None
+    yd = t.zeros((M, H * D), dtype=t.int16, device="cuda")
+    yqd = t.zeros((M, H * D), dtype=t.int8, device="cuda")
+    stride = H * max_seq * D
+    _lib.call("llhip_rope_quant", ptr(xd), M, H, D, H * D, ptr(cd), ptr(sd), max_seq, pos, None, ptr(rpd), ptr(yd),
+              ptr(yqd), qM, qS, ptr(kcd), ptr(vd), H * D + 8, ptr(vcd), max_seq, stride if rows else 0, stream())
+    if rows:
+        want_y = np.stack([O.rope(x[m:m + 1], H, D, c, s, int(rp[m]))[0] for m in range(M)])
+    else:
+        want_y = O.rope(x, H, D, c, s, pos)
+    want_q = O.vquant(want_y, qM, qS)
+    assert np.array_equal(yd.cpu().numpy(), want_y) and np.array_equal(yqd.cpu().numpy(), want_q)
+    kc, vc = kc0.copy(), vc0.copy()
+    for m in range(M):
+        slot, pm = (m, int(rp[m])) if rows else (0, pos + m)
+        kc[slot, :, pm] = want_q[m].reshape(H, D)
+        vc[slot, :, pm] = v[m, :H * D].reshape(H, D)
+    assert np.array_equal(kcd.cpu().numpy(), kc) and np.array_equal(vcd.cpu().numpy(), vc)
+    # without caches: the query rows (y and yq only)
+    yqd.zero_()
+    _lib.call("llhip_rope_quant", ptr(xd), M, H, D, H * D, ptr(cd), ptr(sd), max_seq, 7, None, None, ptr(yd), ptr(yqd),
+              qM, qS, None, None, 0, None, max_seq, 0, stream())
+    assert np.array_equal(yqd.cpu().numpy(), O.vquant(O.rope(x, H, D, c, s, 7), qM, qS))
+    with pytest.raises(ValueError):
+        _lib.call("llhip_rope_quant", ptr(xd), M, H, D, H * D, ptr(cd), ptr(sd), max_seq, 60, None, None, ptr(yd),
+                  ptr(yqd), qM, qS, ptr(kcd), ptr(vd), H * D, ptr(vcd), max_seq, 0, stream())
