@@ -15,8 +15,10 @@ The JSON line also carries
   cpu_baseline : the CPU oracle's numpy restatement of golden.py (int64 `a @ w.T`, Python
                  attention loop -- the reference's own structure) timed on a bounded sample
                  of the same decode launches on this host, and checked equal to the GPU's;
-  extra        : prefill tok/s (GPU time of the one-launch 512-row prefill; prefill_api_ms adds
-                 the host side of prefill(): all L logits rows downloaded and widened to int64),
+  extra        : prefill tok/s (the one-launch 512-row prefill as the HIP graph prefill() replays
+                 from the second prompt of a shape on; prefill_eager_ms: its ~300 launches
+                 enqueued one by one, as the first prompt of a shape runs; prefill_api_ms adds the
+                 host side of prefill(): all L logits rows downloaded and widened to int64),
                  per-family decode timings, config 4 at batch 16, config 5 (Qwen3 shape, T = 4096)
                  decode launch time, config-2 GEMM TOPS and GB/s (weights rotated through copies
                  larger than the memory-side cache), the qgraph producer's weight conversion
@@ -365,17 +367,25 @@ def main() -> None:
     nxt = G.GoldenModel.argmax(rows[-1], g.vocab)
     kv0 = g.kv
     # the same launches without the host side of the API (the logits rows of all L positions,
-    # downloaded and widened to int64 numpy rows): the GPU's prefill time
+    # downloaded and widened to int64 numpy rows): eagerly enqueued, and as the replayed graph that
+    # prefill() captures on the second prompt of a shape
     padded = -(-L // g.prefill_m) * g.prefill_m
-    t_dev = []
-    for _ in range(3):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        g._launch_tokens(prompt, 0, padded)
-        torch.cuda.synchronize()
-        t_dev.append(time.perf_counter() - t0)
-    t_prefill_dev = min(t_dev)
-    log(f"prefill {L} tokens: {t_prefill * 1e3:.1f} ms through prefill(), {t_prefill_dev * 1e3:.2f} ms on the GPU")
+
+    def timed(fn):
+        t = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            t.append(time.perf_counter() - t0)
+        return min(t)
+
+    t_prefill_eager = timed(lambda: g._launch_tokens(prompt, 0, padded))
+    g._prefill_launch(prompt, padded)  # the second prefill of this shape: captured
+    t_prefill_dev = timed(lambda: g._prefill_launch(prompt, padded))
+    log(f"prefill {L} tokens: {t_prefill * 1e3:.1f} ms through prefill(), {t_prefill_dev * 1e3:.2f} ms on the GPU "
+        f"(graph replay; {t_prefill_eager * 1e3:.2f} ms eagerly enqueued)")
     if args.profile == "prefill":
         return
 
@@ -434,6 +444,7 @@ def main() -> None:
         log("batch decode", batch)
 
     extra = {"prefill_tok_s": round(L / t_prefill_dev, 1), "prefill_ms": round(t_prefill_dev * 1e3, 3),
+             "prefill_eager_ms": round(t_prefill_eager * 1e3, 3),
              "prefill_api_ms": round(t_prefill * 1e3, 2),
              "decode_step_bytes": step_bytes, "decode_hbm_frac_of_step": round(step_bytes / (dt / args.steps) / 1e9
                                                                                 / HBM_PEAK_GBS, 4),

@@ -435,6 +435,8 @@ class GoldenModel:
         self._act: dict[str, object] = {}
         self._cap = 0
         self._act_spec: dict[str, tuple[str, int]] = {}
+        self._pf_graphs: dict = {}  # whole-prompt prefill graphs by (rows, prompt length, KV slot)
+        self._pf_seen: dict = {}
         self._plan = self._compile()
         self._ensure_capacity(self.prefill_m)
         self._graph = None
@@ -471,6 +473,7 @@ class GoldenModel:
         cap = max(M, self.prefill_m)
         self._graph = None  # captured pointers would dangle
         self._graph_b = None
+        self._pf_graphs.clear()
         for name, (dt, cols) in self._act_spec.items():
             self._act[name] = torch.zeros((cap, cols), dtype=getattr(torch, _TDT[dt]), device=self.device)
         self._cap = cap
@@ -491,6 +494,7 @@ class GoldenModel:
         torch = _t()
         self._graph = None
         self._graph_b = None
+        getattr(self, "_pf_graphs", {}).clear()
         self._slot = 0
         self._kv: dict[int, tuple] = {}
         for op in self.q.ops:
@@ -884,6 +888,40 @@ class GoldenModel:
                   _ptr(self._act[self.q.input_name]), _stream())
         self._execute(M, int(pos))
 
+    PF_GRAPHS = 16  # whole-prompt prefill graphs kept (oldest dropped first)
+
+    def _prefill_launch(self, tokens, M: int) -> None:
+        """The whole-prompt prefill launch of `tokens` padded to M rows at positions 0..M-1.  Its
+        ~300 kernel launches are enqueued by the host in about as long as the GPU runs them, so
+        the second prefill of a (rows, prompt length, KV slot) shape captures them in a HIP graph
+        and every later one replays it, after copying the token ids into the graph's buffer."""
+        key = (M, len(tokens), self._slot)
+        if not self.use_graph:
+            self._launch_tokens(tokens, 0, M)
+            return
+        torch = _t()
+        idx = self._token_rows(tokens)
+        self._ensure_capacity(M)
+        g = self._pf_graphs.get(key)
+        if g is None:
+            self._pf_seen[key] = self._pf_seen.get(key, 0) + 1
+            if self._pf_seen[key] < 2:
+                self._launch_tokens(tokens, 0, M)
+                return
+            tok = torch.zeros(max(len(idx), 1), dtype=torch.int32, device=self.device)
+            graph = torch.cuda.CUDAGraph()
+            with capture_graph(graph):
+                _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, _ptr(tok),
+                          len(idx), M, _ptr(self._act[self.q.input_name]), _stream())
+                self._execute(M, 0)
+            while len(self._pf_graphs) >= self.PF_GRAPHS:
+                self._pf_graphs.pop(next(iter(self._pf_graphs)))
+            g = self._pf_graphs[key] = (graph, tok)
+        graph, tok = g
+        if len(idx):
+            tok.copy_(torch.from_numpy(np.ascontiguousarray(idx, dtype=np.int32)), non_blocking=False)
+        graph.replay()
+
     # ---- device-resident greedy decode ----------------------------------------------------
     def _decode_state(self, ring_cap: int) -> None:
         torch = _t()
@@ -1104,7 +1142,7 @@ class GoldenModel:
         L = len(tokens)
         padded = -(-L // self.prefill_m) * self.prefill_m
         if acts is None and self.whole_prompt_prefill and L > self.prefill_m and padded <= self.max_seq:
-            self._launch_tokens(tokens, 0, padded)
+            self._prefill_launch(tokens, padded)
             return list(_down(self._act[self.q.output_name][:L]).astype(I64))
         rows_out = []
         for start in range(0, len(tokens), self.prefill_m):

@@ -106,6 +106,27 @@ def test_whole_prompt_prefill_large_models(tmp_path_factory, cfg):
         assert np.array_equal(g1.kv[layer][0], g2.kv[layer][0]) and np.array_equal(g1.kv[layer][1], g2.kv[layer][1])
 
 
+def test_prefill_graph_replays_equal_eager_launches(tmp_path_factory):
+    """The second whole-prompt prefill of a shape is captured as a HIP graph and later ones replay
+    it: four prefills (eager, capture + replay, replay, replay of another prompt of the same
+    length), with eager decode launches between them, each equal to the eager model's logits and
+    KV; a prompt of another length runs eagerly again."""
+    qdir = _qgraph(tmp_path_factory, "qwen25", True)
+    g, e = G.GoldenModel(qdir), G.GoldenModel(qdir)
+    e.use_graph = False
+    prompts = [synth.seeded_prompt("qwen25", 40, 1)] * 3 + [synth.seeded_prompt("qwen25", 40, 2),
+                                                           synth.seeded_prompt("qwen25", 37, 3)]
+    for i, p in enumerate(prompts):
+        g.reset()
+        e.reset()
+        r1, r2 = g.prefill(p), e.prefill(p)
+        assert all(np.array_equal(a, b) for a, b in zip(r1, r2)), i
+        for layer in (0, g.n_layers - 1):
+            assert np.array_equal(g.kv[layer][0], e.kv[layer][0]) and np.array_equal(g.kv[layer][1], e.kv[layer][1])
+        assert np.array_equal(g.decode(5, len(p)), e.decode(5, len(p)))
+    assert len(g._pf_graphs) == 1
+
+
 def test_fused_and_unfused_graph_decode_agree(tmp_path_factory):
     qdir = _qgraph(tmp_path_factory, "smol", True)
     prompt = synth.seeded_prompt("smol", 33, 9)
