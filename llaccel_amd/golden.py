@@ -1143,7 +1143,8 @@ class GoldenModel:
         padded = -(-L // self.prefill_m) * self.prefill_m
         if acts is None and self.whole_prompt_prefill and L > self.prefill_m and padded <= self.max_seq:
             self._prefill_launch(tokens, padded)
-            return list(_down(self._act[self.q.output_name][:L]).astype(I64))
+            # int16 rows downloaded, widened to int64 by torch's multithreaded CPU copy
+            return list(self._act[self.q.output_name][:L].cpu().to(_t().int64).numpy())
         rows_out = []
         for start in range(0, len(tokens), self.prefill_m):
             chunk = tokens[start:start + self.prefill_m]
