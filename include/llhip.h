@@ -99,6 +99,20 @@ int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_
                  const int32_t* bias, int epilogue, const int16_t* aux, int64_t ldaux, int64_t aux_shift,
                  int64_t silu_Mi, int64_t silu_Si, int64_t silu_sh, int out_i8, void* out, int64_t ldo, void* ws,
                  void* stream);
+/* golden.py:316-342 for several linears of one input in one launch (the q, k, v projections of a
+ * prompt chunk): out_q = requant(A . W_q^T + bias_q), epilogue none, i8 or i16 output.  At most 4
+ * problems. */
+typedef struct llhip_linear_problem {
+  const void* W;     /* int8 [N][K] */
+  int64_t N;
+  const void* rq;    /* int32 [N][2] */
+  const void* bias;  /* int32 [N] or NULL */
+  void* out;         /* [M][ldo] i8 or i16 */
+  int64_t ldo, out_i8;
+} llhip_linear_problem;
+int llhip_linear_group(const int8_t* A, int64_t M, int64_t K, int64_t lda, int64_t count,
+                       const llhip_linear_problem* probs, void* ws, void* stream);
+
 /* golden.py:217-240  exact integer A[M][K] (int64) . W[N][K]^T (int8) -> int64 [M][N] */
 int llhip_exact_matmul(const int64_t* A, int64_t M, int64_t K, const int8_t* W, int64_t N, int64_t* out,
                        void* stream);

@@ -51,6 +51,7 @@ _SIGS = {
     "llhip_greedy_rows": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p],
     "llhip_rows_first_mismatch_i16": [_p, _i64, _p, _i64, _i64, _i64, _p, _p],
     "llhip_rows_checksum_i16": [_p, _i64, _i64, _i64, _p, _p],
+    "llhip_linear_group": [_p, _i64, _i64, _i64, _i64, _p, _p, _p],
     "llhip_rope_quant": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _p,
                          _i64, _i64, _p],
     "llhip_quant_rows_i8": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
@@ -110,6 +111,10 @@ def call(name: str, *args) -> None:
 class NormQuantDesc(ctypes.Structure):
     _fields_ = [("x", _p), ("gamma", _p), ("h_out", _p), ("hq_out", _p), ("ldx", _i64), ("K", _i64), ("eps_t", _i64),
                 ("C", _i64), ("sh_post", _i64), ("Mq", _i64), ("Sq", _i64), ("prequant", _i64)]
+
+
+class LinearProblem(ctypes.Structure):
+    _fields_ = [("W", _p), ("N", _i64), ("rq", _p), ("bias", _p), ("out", _p), ("ldo", _i64), ("out_i8", _i64)]
 
 
 class AttnInDesc(ctypes.Structure):

@@ -627,16 +627,9 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
 // and stores its int32 partial tile into plane z of part [splits][M][N]; linear_splitk_finish
 // sums the planes (integer addition: any split gives the same sum) and applies the epilogue.
 template <int EPI, bool OUT8, int GM, int GN, int NW>
-__global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part) {
+__device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, int kps, int32_t* part) {
   using T = MfmaTile<GM, GN, NW>;
   extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A GMx64 | W GNx64]
-  // The grid is padded to a multiple of 8 and workgroup b runs on XCD b % 8, which takes a
-  // contiguous range of tiles (M fastest): the M-blocks that share a W panel share that XCD's L2.
-  const int b = blockIdx.x;
-  const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
-  if (logical >= mblocks * nblocks) return;
-  const int mb = logical % mblocks;
-  const int nbk = logical / mblocks;
   const int m0 = mb * GM, n0 = nbk * GN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -803,6 +796,53 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks
     store_i16_tile<EPI, false>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
 }
 
+// The grid is padded to a multiple of 8 and workgroup b runs on XCD b % 8, which takes a
+// contiguous range of tiles (M fastest): the M-blocks that share a W panel share that XCD's L2.
+template <int EPI, bool OUT8, int GM, int GN, int NW>
+__global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part) {
+  const int b = blockIdx.x;
+  const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
+  if (logical >= mblocks * nblocks) return;
+  mfma_tile<EPI, OUT8, GM, GN, NW>(p, logical % mblocks, logical / mblocks, kps, part);
+}
+
+// Several linears of one input in one launch (the q, k, v projections of a prompt chunk): the
+// N-blocks of problem q are nb0[q] .. nb0[q+1]-1 of one grid; epilogue none, i8 or i16 output.
+constexpr int GROUP_MAX = 4;
+struct LinearGroup {
+  int count;
+  int nb0[GROUP_MAX + 1];
+  const int8_t* W[GROUP_MAX];
+  const int32_t* rq[GROUP_MAX];
+  const int32_t* bias[GROUP_MAX];
+  void* out[GROUP_MAX];
+  int64_t ldo[GROUP_MAX];
+  int N[GROUP_MAX];
+  int out8[GROUP_MAX];
+};
+
+template <int GM, int GN, int NW>
+__global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, LinearGroup g, int mblocks) {
+  const int b = blockIdx.x;
+  const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
+  if (logical >= mblocks * g.nb0[g.count]) return;
+  const int mb = logical % mblocks;
+  int nbk = logical / mblocks, q = 0;
+  while (q + 1 < g.count && nbk >= g.nb0[q + 1]) ++q;
+  LinearArgs pp = p;
+  pp.W = g.W[q];
+  pp.rq = g.rq[q];
+  pp.bias = g.bias[q];
+  pp.out = g.out[q];
+  pp.ldo = g.ldo[q];
+  pp.N = g.N[q];
+  nbk -= g.nb0[q];
+  if (g.out8[q])
+    mfma_tile<EPI_NONE, true, GM, GN, NW>(pp, mb, nbk, p.K / 64, nullptr);
+  else
+    mfma_tile<EPI_NONE, false, GM, GN, NW>(pp, mb, nbk, p.K / 64, nullptr);
+}
+
 // sum of the split-K planes + bias, requant and epilogue; four columns per thread
 template <int EPI, bool OUT8>
 __global__ __launch_bounds__(256) void linear_splitk_finish(LinearArgs p, const int32_t* part, int splits) {
@@ -937,6 +977,48 @@ static int launch_linear(LinearArgs& p, void* ws, hipStream_t stream) {
   return 0;
 }
 
+// grouped launch of up to GROUP_MAX linears of one input (64x128 tiles); other shapes run the
+// problems one by one through launch_linear
+static int launch_linear_group(const LinearArgs& base, const llhip_linear_problem* pr, int count, void* ws,
+                               hipStream_t s) {
+  const bool aligned = (base.K % 64 == 0) && (base.lda % 16 == 0) && ((uintptr_t)base.A % 16 == 0);
+  bool ok = aligned && count <= GROUP_MAX;
+  for (int q = 0; ok && q < count; ++q) ok = (uintptr_t)pr[q].W % 16 == 0;
+  if (!ok) {
+    for (int q = 0; q < count; ++q) {
+      LinearArgs p = base;
+      p.W = static_cast<const int8_t*>(pr[q].W);
+      p.rq = static_cast<const int32_t*>(pr[q].rq);
+      p.bias = static_cast<const int32_t*>(pr[q].bias);
+      p.out = pr[q].out;
+      p.ldo = pr[q].ldo;
+      p.N = (int)pr[q].N;
+      const int rc = pr[q].out_i8 ? launch_linear<EPI_NONE, true>(p, ws, s) : launch_linear<EPI_NONE, false>(p, ws, s);
+      if (rc) return rc;
+    }
+    return 0;
+  }
+  using T = MfmaTile<64, 128, 4>;
+  LinearGroup g{};
+  g.count = count;
+  g.nb0[0] = 0;
+  for (int q = 0; q < count; ++q) {
+    g.W[q] = static_cast<const int8_t*>(pr[q].W);
+    g.rq[q] = static_cast<const int32_t*>(pr[q].rq);
+    g.bias[q] = static_cast<const int32_t*>(pr[q].bias);
+    g.out[q] = pr[q].out;
+    g.ldo[q] = pr[q].ldo;
+    g.N[q] = (int)pr[q].N;
+    g.out8[q] = pr[q].out_i8 ? 1 : 0;
+    g.nb0[q + 1] = g.nb0[q] + (int)ceil_div(pr[q].N, 128);
+  }
+  const int mblocks = (int)ceil_div(base.M, 64);
+  hipLaunchKernelGGL((linear_mfma_group<64, 128, 4>), dim3(ceil_div((int64_t)mblocks * g.nb0[count], 8) * 8),
+                     dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
 // exact int64 A . int8 W^T (golden.py:217-240 computes the same integers through FP64 BLAS)
 __global__ void exact_matmul_kernel(const int64_t* A, int64_t M, int64_t K, const int8_t* W, int64_t N, int64_t* out) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -996,6 +1078,34 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
     case EPI_MUL: return launch_linear<EPI_MUL, false>(p, ws, s);
     default: return launch_linear<EPI_NONE, false>(p, ws, s);
   }
+}
+
+extern "C" int llhip_linear_group(const int8_t* A, int64_t M, int64_t K, int64_t lda, int64_t count,
+                                  const llhip_linear_problem* probs, void* ws, void* stream) {
+  if (M < 0 || K < 0 || count < 0) return fail(-EINVAL, "linear_group: negative shape");
+  if (count > GROUP_MAX) return fail(-EINVAL, "linear_group: at most %d problems", GROUP_MAX);
+  if (count && !probs) return fail(-EINVAL, "linear_group: null problems");
+  if (K > 65535) return fail(-EINVAL, "linear: K=%lld exceeds the int32 accumulator bound 65535", (long long)K);
+  if (M > INT32_MAX || lda < K || !A) return fail(-EINVAL, "linear_group: bad input rows");
+  for (int64_t q = 0; q < count; ++q) {
+    const llhip_linear_problem& r = probs[q];
+    if (r.N < 0 || r.N > INT32_MAX || r.ldo < r.N || !r.W || !r.rq || !r.out)
+      return fail(-EINVAL, "linear_group: bad problem %lld", (long long)q);
+  }
+  if (M == 0 || count == 0) return 0;
+  LinearArgs p{};
+  p.A = A;
+  p.lda = lda;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.steps = (int)std::max<int64_t>(ceil_div(K, 64), 1);
+  // problems with N = 0 take no tiles
+  llhip_linear_problem live[GROUP_MAX];
+  int n = 0;
+  for (int64_t q = 0; q < count; ++q)
+    if (probs[q].N > 0) live[n++] = probs[q];
+  if (n == 0) return 0;
+  return launch_linear_group(p, live, n, ws, (hipStream_t)stream);
 }
 
 extern "C" int llhip_exact_matmul(const int64_t* A, int64_t M, int64_t K, const int8_t* W, int64_t N, int64_t* out,

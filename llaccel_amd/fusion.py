@@ -93,10 +93,31 @@ class _RopeQuantStep:
                   int(qu["M"]), int(qu["S"]), kc, v, ldv, vc, m.max_seq, stride, m._stream_handle())
 
 
+class _GroupLinearStep:
+    """Linears of one input with epilogue none (the q, k, v projections) in one
+    llhip_linear_group launch."""
+
+    def __init__(self, model, lins):
+        self.model, self.lins = model, lins
+        self.probs = (_lib.LinearProblem * len(lins))()
+
+    def __call__(self, M, pos, pd=None):
+        m = self.model
+        for pr, o in zip(self.probs, self.lins):
+            out = m._buf(o["out"])
+            pr.W, pr.N, pr.rq = _vp(m._dt[o["w"]]), int(o["N"]), _vp(m._dt[o["rq"]])
+            pr.bias = _vp(m._dt[o["bias"]]) if o.get("bias") else None
+            pr.out, pr.ldo, pr.out_i8 = _vp(out), out.shape[1], int(o.get("out_dtype", "i16") == "i8")
+        a = self.lins[0]
+        _lib.call("llhip_linear_group", _vp(m._buf(a["in"])), M, int(a["K"]), int(a["K"]), len(self.lins), self.probs,
+                  _vp(m._ws), m._stream_handle())
+
+
 def wide_steps(model, ops, steps):
     """Launches of a fused run for more rows than its fused kernel takes (prompt chunks): the run's
-    per-op steps, with each rmsnorm + quant of its output as one launch and attn_in's group
-    rope q, rope k, quant q, quant k, kv_write as two.  The arithmetic of every op is unchanged."""
+    per-op steps, with each rmsnorm + quant of its output as one launch, three linears of one input
+    (q, k, v) as one grouped launch and attn_in's group rope q, rope k, quant q, quant k, kv_write
+    as two.  The arithmetic of every op is unchanged."""
     out, i = [], 0
     while i < len(ops):
         a = ops[i]
@@ -106,6 +127,13 @@ def wide_steps(model, ops, steps):
             if K % 16 == 0 and K <= NORM_MAX_K:
                 out.append(_NormQuantStep(model, a, ops[i + 1]))
                 i += 2
+                continue
+        if i + 2 < len(ops):
+            lins = ops[i:i + 3]
+            if (all(_plain_linear(o) for o in lins) and len({o["in"] for o in lins}) == 1
+                    and len({int(o["K"]) for o in lins}) == 1):
+                out.append(_GroupLinearStep(model, lins))
+                i += 3
                 continue
         if i + 4 < len(ops):
             rq_, rk_, qq_, kq_, kvw = ops[i:i + 5]

@@ -144,3 +144,38 @@ def test_split_k_gemm(M, K, N, epilogue, out_i8):
     rows = np.unique(np.concatenate([np.arange(4), np.arange(M - 4, M), rng.choice(M, 12, replace=False)]))
     want = O.linear_c(a[rows], w, rq, bias, out_i8, epilogue, None if aux is None else aux[rows], sh, silu)
     assert np.array_equal(got[rows], want)
+
+
+@pytest.mark.parametrize("M,K", [(512, 896), (300, 896), (37, 128), (64, 100)])
+def test_linear_group_equals_separate_launches(M, K):
+    """llhip_linear_group (q, k, v of a prompt chunk in one launch: i16, i16 and i8 outputs, bias
+    on two of them) equals one llhip_linear launch per problem; K = 100 runs the per-problem
+    fallback."""
+    import ctypes
+
+    from llaccel_amd import _lib
+    from tests.gpu_helpers import ptr, stream, torch, up, workspace
+
+    t = torch()
+    rng = np.random.default_rng(M + K)
+    a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    shapes = [(896, False, True), (128, False, True), (130, True, False)]
+    probs = (_lib.LinearProblem * 3)()
+    outs, want = [], []
+    ad = up(a, np.int8)
+    for pr, (N, out8, has_bias) in zip(probs, shapes):
+        w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+        rq = random_rq(rng, N, K, out8)
+        bias = rng.integers(-(2**20), 2**20, N) if has_bias else None
+        wd, rqd = up(w, np.int8), up(rq, np.int32)
+        bd = up(bias, np.int32) if has_bias else None
+        od = t.zeros((M, N + 3), dtype=t.int8 if out8 else t.int16, device="cuda")
+        pr.W, pr.N, pr.rq, pr.bias = ptr(wd), N, ptr(rqd), ptr(bd)
+        pr.out, pr.ldo, pr.out_i8 = ptr(od), N + 3, int(out8)
+        outs.append((od, wd, rqd, bd))
+        want.append(gpu_linear(a, w, rq, bias=bias, out_i8=out8))
+    _lib.call("llhip_linear_group", ptr(ad), M, K, K, 3, probs, ptr(workspace()), stream())
+    for (od, *_keep), (N, _, _), wnt in zip(outs, shapes, want):
+        assert np.array_equal(od.cpu().numpy()[:, :N], wnt) and not od.cpu().numpy()[:, N:].any()
+    with pytest.raises(ValueError):
+        _lib.call("llhip_linear_group", ptr(ad), M, K, K, 5, probs, ptr(workspace()), stream())
