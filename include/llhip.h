@@ -99,6 +99,21 @@ int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_
                  const int32_t* bias, int epilogue, const int16_t* aux, int64_t ldaux, int64_t aux_shift,
                  int64_t silu_Mi, int64_t silu_Si, int64_t silu_sh, int out_i8, void* out, int64_t ldo, void* ws,
                  void* stream);
+/* golden.py:316-342 (silu and mul epilogues) + 119-120  the gate and up projections of an MLP over
+ * M rows in one launch: sg = silu16(requant16(A . Wg^T + bg)), f = sat16(rshr(requant16(A . Wu^T +
+ * bu) * sg, mul_sh)), fq = quant(f), outputs [M][ld] (i16, i16, i8) -- the values of the gate
+ * linear, the up linear and the quant run one by one. */
+typedef struct llhip_gate_up_desc {
+  const void* A;  /* i8 [M][lda] */
+  int64_t M, K, lda;
+  const void* Wg; const void* rqg; const void* bg;  /* int8 [N][K], int32 [N][2], int32 [N] or NULL */
+  const void* Wu; const void* rqu; const void* bu;
+  int64_t N, ld;
+  int64_t silu_Mi, silu_Si, silu_sh, mul_sh, fq_M, fq_S;
+  void* sg_out; void* f_out; void* fq_out;
+} llhip_gate_up_desc;
+int llhip_gate_up(const llhip_gate_up_desc* d, void* stream);
+
 /* golden.py:316-342 for several linears of one input in one launch (the q, k, v projections of a
  * prompt chunk): out_q = requant(A . W_q^T + bias_q), epilogue none, i8 or i16 output.  At most 4
  * problems. */

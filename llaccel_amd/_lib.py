@@ -52,6 +52,7 @@ _SIGS = {
     "llhip_rows_first_mismatch_i16": [_p, _i64, _p, _i64, _i64, _i64, _p, _p],
     "llhip_rows_checksum_i16": [_p, _i64, _i64, _i64, _p, _p],
     "llhip_linear_group": [_p, _i64, _i64, _i64, _i64, _p, _p, _p],
+    "llhip_gate_up": [_p, _p],
     "llhip_rope_quant": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _p,
                          _i64, _i64, _p],
     "llhip_quant_rows_i8": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
@@ -111,6 +112,13 @@ def call(name: str, *args) -> None:
 class NormQuantDesc(ctypes.Structure):
     _fields_ = [("x", _p), ("gamma", _p), ("h_out", _p), ("hq_out", _p), ("ldx", _i64), ("K", _i64), ("eps_t", _i64),
                 ("C", _i64), ("sh_post", _i64), ("Mq", _i64), ("Sq", _i64), ("prequant", _i64)]
+
+
+class GateUpDesc(ctypes.Structure):
+    _fields_ = [("A", _p), ("M", _i64), ("K", _i64), ("lda", _i64), ("Wg", _p), ("rqg", _p), ("bg", _p), ("Wu", _p),
+                ("rqu", _p), ("bu", _p), ("N", _i64), ("ld", _i64), ("silu_Mi", _i64), ("silu_Si", _i64),
+                ("silu_sh", _i64), ("mul_sh", _i64), ("fq_M", _i64), ("fq_S", _i64), ("sg_out", _p), ("f_out", _p),
+                ("fq_out", _p)]
 
 
 class LinearProblem(ctypes.Structure):

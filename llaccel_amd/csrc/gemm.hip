@@ -474,17 +474,23 @@ struct MfmaTile {
 // template-dependent argument keeps the host pass from emitting the kernels' launch stubs.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N == 0 || N == 3 || N == 4 || N == 6 || N == 8, "vmcnt values of the tile shapes");
+  static_assert(N == 0 || N == 2 || N == 3 || N == 4 || N == 5 || N == 6 || N == 8 || N == 10, "vmcnt values");
   if constexpr (N == 0)
     __builtin_amdgcn_s_waitcnt(0x0F70);
+  else if constexpr (N == 2)
+    __builtin_amdgcn_s_waitcnt(0x0F72);
   else if constexpr (N == 3)
     __builtin_amdgcn_s_waitcnt(0x0F73);
   else if constexpr (N == 4)
     __builtin_amdgcn_s_waitcnt(0x0F74);
+  else if constexpr (N == 5)
+    __builtin_amdgcn_s_waitcnt(0x0F75);
   else if constexpr (N == 6)
     __builtin_amdgcn_s_waitcnt(0x0F76);
-  else
+  else if constexpr (N == 8)
     __builtin_amdgcn_s_waitcnt(0x0F78);
+  else
+    __builtin_amdgcn_s_waitcnt(0x0F7A);
 }
 
 __device__ __forceinline__ void lds_barrier() {
@@ -843,6 +849,183 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, Linea
     mfma_tile<EPI_NONE, false, GM, GN, NW>(pp, mb, nbk, p.K / 64, nullptr);
 }
 
+// ---------------------------------------------------------------------------------------
+// gate + up of an MLP over many rows in one launch (golden.py:316-342 with the silu and mul
+// epilogues, then quant golden.py:119-120): every 64x128 tile streams the gate and the up weight
+// panels through one LDS ring against the same A rows, keeps both accumulators, and writes
+// sg = silu16(requant16(A.Wg^T + bg)), f = sat16(rshr(requant16(A.Wu^T + bu) * sg, mul_sh)) and
+// fq = quant(f) -- the values of the gate linear, the up linear and the quant run one by one.
+// ---------------------------------------------------------------------------------------
+struct DualArgs {
+  const int8_t* Wu;
+  const int32_t* rqu;
+  const int32_t* bu;
+  int16_t* sg;
+  int16_t* f;
+  int8_t* fq;
+  int64_t ld;  // row stride of the three outputs (elements)
+  int64_t fqM;
+  int fqS, mul_sh;
+};
+
+// Eight waves: waves 0-3 accumulate the gate tile, waves 4-7 the up tile of the same 64x128
+// outputs from the same LDS stages (each wave the MFMA work of a 4-wave single GEMM tile, two waves
+// per SIMD); the up waves pass their requantised values to the gate waves through LDS for the
+// epilogue.  Stage loads: gate waves 1 A + 2 Wg instructions, up waves 2 Wu instructions.
+__global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d, int mblocks, int nblocks) {
+  constexpr int GM = 64, GN = 128, LW = 2;
+  constexpr int STAGE = (GM + 2 * GN) * 64;
+  constexpr int WN = 2;  // 32x32 tiles per wave along N (one along M)
+  // [GSTAGES][A | Wg | Wu]; after the k loop it holds the requantised up tile and the SiLU table
+  // (80 KB in all, so two workgroups share a CU)
+  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];
+  const int b = blockIdx.x;
+  const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
+  if (logical >= mblocks * nblocks) return;
+  const int mb = logical % mblocks, nbk = logical / mblocks;
+  const int m0 = mb * GM, n0 = nbk * GN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool upw = wave >= 4;  // wave-uniform role
+  const int wq = wave & 3;
+  const int wm = (wq & 1) * 32, wn = (wq >> 1) * 64;
+  const int8_t* Wsrc = upw ? d.Wu : p.W;
+
+  const int8_t* asrc;
+  const int8_t* wsrc[LW];
+  {
+    const int r = wq * 16 + (lane >> 2);
+    asrc = p.A + (int64_t)min(m0 + r, p.M - 1) * p.lda + (((lane & 3) ^ lds_swz(r)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < LW; ++i) {
+    const int r = (wq * LW + i) * 16 + (lane >> 2);
+    wsrc[i] = Wsrc + (int64_t)min(n0 + r, p.N - 1) * p.K + (((lane & 3) ^ lds_swz(r)) * 16);
+  }
+  const int wbase = (upw ? GM + GN : GM) * 64;  // this wave group's W panel in a stage
+  auto issue = [&](int kt) {
+    int8_t* st = ring + (kt % GSTAGES) * STAGE;
+    const int k0 = kt * 64;
+    if (!upw) {
+      const int8_t* src = asrc + k0;
+      int8_t* dst = st + wq * 1024;
+      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < LW; ++i) {
+      const int8_t* src = wsrc[i] + k0;
+      int8_t* dst = st + wbase + (wq * LW + i) * 1024;
+      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    }
+  };
+  // vmcnt waits by wave group: gate waves issue 3 loads per stage, up waves 2
+  auto wait_two = [&]() {
+    if (upw)
+      wait_vmcnt<4>();
+    else
+      wait_vmcnt<6>();
+  };
+  auto wait_one = [&]() {
+    if (upw)
+      wait_vmcnt<2>();
+    else
+      wait_vmcnt<3>();
+  };
+  int aoff[2], woff[WN][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int c = ks * 2 + (lane >> 5);
+    const int ra = wm + (lane & 31);
+    aoff[ks] = ra * 64 + ((c ^ lds_swz(ra)) << 4);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int r = wn + 32 * j + (lane & 31);
+      woff[j][ks] = wbase + r * 64 + ((c ^ lds_swz(r)) << 4);
+    }
+  }
+  const int32_t* rqp = upw ? d.rqu : p.rq;
+  const int32_t* bp = upw ? d.bu : p.bias;
+  ColRq cq[WN];
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int n = min(n0 + wn + 32 * j + (lane & 31), p.N - 1);
+    cq[j] = make_colrq(rqp[2 * n], rqp[2 * n + 1], bp ? bp[n] : 0);
+  }
+  v16i acc[WN];
+#pragma unroll
+  for (int j = 0; j < WN; ++j) acc[j] = v16i{};
+
+  const int ktiles = p.K / 64;
+  for (int s0 = 0; s0 < GSTAGES - 1; ++s0)
+    if (s0 < ktiles) issue(s0);
+  if (ktiles > 2)
+    wait_two();
+  else
+    wait_vmcnt<0>();
+  lds_barrier();
+  v4i fa0, fa1, fb0[WN], fb1[WN];
+  fa0 = *reinterpret_cast<const v4i*>(ring + aoff[0]);
+#pragma unroll
+  for (int j = 0; j < WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(ring + woff[j][0]);
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int8_t* st = ring + (kt % GSTAGES) * STAGE;
+    fa1 = *reinterpret_cast<const v4i*>(st + aoff[1]);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) fb1[j] = *reinterpret_cast<const v4i*>(st + woff[j][1]);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb0[j], acc[j], 0, 0, 0);
+    mfma_ds_interleave<WN, 1 + WN>();
+    if (kt + 2 < ktiles)
+      wait_one();
+    else
+      wait_vmcnt<0>();
+    lds_barrier();
+    if (kt + GSTAGES - 1 < ktiles) issue(kt + GSTAGES - 1);
+    const int8_t* sn = ring + ((kt + 1) % GSTAGES) * STAGE;
+    fa0 = *reinterpret_cast<const v4i*>(sn + aoff[0]);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(sn + woff[j][0]);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb1[j], acc[j], 0, 0, 0);
+    mfma_ds_interleave<WN, 1 + WN>();
+  }
+  __syncthreads();  // every wave's fragment reads have returned; no stage load is outstanding
+  int16_t* ubuf = reinterpret_cast<int16_t*>(ring);  // [GM][GN]
+  uint32_t* sig32 = reinterpret_cast<uint32_t*>(ring + GM * GN * 2);
+  if (tid < 129) sig32[tid] = reinterpret_cast<const uint32_t*>(kSig)[tid];
+  const uint16_t* sig16 = reinterpret_cast<const uint16_t*>(sig32);
+
+  // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, column l%32
+  if (upw) {
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ml = wm + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), nl = wn + 32 * j + (lane & 31);
+        ubuf[ml * GN + nl] = (int16_t)clamp32(requant_col<false>(acc[j][r], cq[j]), -32768, 32767);
+      }
+  }
+  __syncthreads();
+  if (upw) return;
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int nl = wn + 32 * j + (lane & 31), n = n0 + nl;
+    if (n >= p.N) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int ml = wm + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), m = m0 + ml;
+      if (m >= p.M) continue;
+      const int32_t g = clamp32(requant_col<false>(acc[j][r], cq[j]), -32768, 32767);
+      const int32_t sg = silu16_i16(g, (uint32_t)p.Mi, p.Si, p.sh, sig16);
+      const int32_t u = ubuf[ml * GN + nl];
+      const int32_t f = (int32_t)sat16(rshr((int64_t)(u * sg), d.mul_sh));
+      const int64_t o = (int64_t)m * d.ld + n;
+      d.sg[o] = (int16_t)sg;
+      d.f[o] = (int16_t)f;
+      d.fq[o] = (int8_t)sat8(mulshift(f, d.fqM, d.fqS));
+    }
+  }
+}
+
 // sum of the split-K planes + bias, requant and epilogue; four columns per thread
 template <int EPI, bool OUT8>
 __global__ __launch_bounds__(256) void linear_splitk_finish(LinearArgs p, const int32_t* part, int splits) {
@@ -1078,6 +1261,74 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
     case EPI_MUL: return launch_linear<EPI_MUL, false>(p, ws, s);
     default: return launch_linear<EPI_NONE, false>(p, ws, s);
   }
+}
+
+extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {
+  if (!d) return fail(-EINVAL, "gate_up: null descriptor");
+  const int64_t M = d->M, K = d->K, N = d->N;
+  if (M < 0 || K < 0 || N < 0 || M > INT32_MAX || N > INT32_MAX || d->lda < K || d->ld < N)
+    return fail(-EINVAL, "gate_up: bad shape");
+  if (K > 65535) return fail(-EINVAL, "linear: K=%lld exceeds the int32 accumulator bound 65535", (long long)K);
+  if (!d->A || !d->Wg || !d->Wu || !d->rqg || !d->rqu || !d->sg_out || !d->f_out || !d->fq_out)
+    return fail(-EINVAL, "gate_up: null operand");
+  if (!u32_ok(d->silu_Mi) || !shift_ok(d->silu_Si) || !shift_ok(d->silu_sh) || !shift_ok(d->mul_sh) ||
+      !u32_ok(d->fq_M) || !shift_ok(d->fq_S))
+    return fail(-EINVAL, "gate_up: parameter out of range");
+  if (M == 0 || N == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  LinearArgs p{};
+  p.A = static_cast<const int8_t*>(d->A);
+  p.lda = d->lda;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.N = (int)N;
+  p.steps = (int)std::max<int64_t>(ceil_div(K, 64), 1);
+  p.Mi = d->silu_Mi;
+  p.Si = (int)d->silu_Si;
+  p.sh = (int)d->silu_sh;
+  const bool fits = K % 64 == 0 && K > 0 && d->lda % 16 == 0 && (uintptr_t)d->A % 16 == 0 && (uintptr_t)d->Wg % 16 == 0 &&
+                    (uintptr_t)d->Wu % 16 == 0;
+  if (!fits) {  // the three ops one by one
+    p.W = static_cast<const int8_t*>(d->Wg);
+    p.rq = static_cast<const int32_t*>(d->rqg);
+    p.bias = static_cast<const int32_t*>(d->bg);
+    p.out = d->sg_out;
+    p.ldo = d->ld;
+    int rc = launch_linear<EPI_SILU, false>(p, nullptr, s);
+    if (rc) return rc;
+    p.W = static_cast<const int8_t*>(d->Wu);
+    p.rq = static_cast<const int32_t*>(d->rqu);
+    p.bias = static_cast<const int32_t*>(d->bu);
+    p.aux = static_cast<const int16_t*>(d->sg_out);
+    p.ldaux = d->ld;
+    p.aux_shift = (int)d->mul_sh;
+    p.out = d->f_out;
+    if ((rc = launch_linear<EPI_MUL, false>(p, nullptr, s))) return rc;
+    for (int64_t m = 0; m < M; ++m)
+      if ((rc = llhip_quant(static_cast<const int16_t*>(d->f_out) + m * d->ld, N, d->fq_M, d->fq_S,
+                            static_cast<int8_t*>(d->fq_out) + m * d->ld, stream)))
+        return rc;
+    return 0;
+  }
+  p.W = static_cast<const int8_t*>(d->Wg);
+  p.rq = static_cast<const int32_t*>(d->rqg);
+  p.bias = static_cast<const int32_t*>(d->bg);
+  DualArgs a{};
+  a.Wu = static_cast<const int8_t*>(d->Wu);
+  a.rqu = static_cast<const int32_t*>(d->rqu);
+  a.bu = static_cast<const int32_t*>(d->bu);
+  a.sg = static_cast<int16_t*>(d->sg_out);
+  a.f = static_cast<int16_t*>(d->f_out);
+  a.fq = static_cast<int8_t*>(d->fq_out);
+  a.ld = d->ld;
+  a.fqM = d->fq_M;
+  a.fqS = (int)d->fq_S;
+  a.mul_sh = (int)d->mul_sh;
+  const int mblocks = (int)ceil_div(M, 64), nblocks = (int)ceil_div(N, 128);
+  hipLaunchKernelGGL(linear_mfma_dual, dim3(ceil_div((int64_t)mblocks * nblocks, 8) * 8), dim3(512),
+                     GSTAGES * (64 + 2 * 128) * 64, s, p, a, mblocks, nblocks);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
 }
 
 extern "C" int llhip_linear_group(const int8_t* A, int64_t M, int64_t K, int64_t lda, int64_t count,

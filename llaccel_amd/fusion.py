@@ -113,11 +113,51 @@ class _GroupLinearStep:
                   _vp(m._ws), m._stream_handle())
 
 
+class _GateUpStep:
+    """The gate (silu epilogue) and up (mul epilogue on the gate's output) linears of one input
+    and the quant of the product in one llhip_gate_up launch."""
+
+    def __init__(self, model, g, u, q):
+        self.model, self.g, self.u, self.q = model, g, u, q
+        self.desc = _lib.GateUpDesc()
+
+    def __call__(self, M, pos, pd=None):
+        m, g, u, q, d = self.model, self.g, self.u, self.q, self.desc
+        dt, s = m._dt, g["silu"]
+        sg = m._buf(g["out"])
+        d.A, d.M, d.K, d.lda = _vp(m._buf(g["in"])), M, int(g["K"]), int(g["K"])
+        d.Wg, d.rqg = _vp(dt[g["w"]]), _vp(dt[g["rq"]])
+        d.bg = _vp(dt[g["bias"]]) if g.get("bias") else None
+        d.Wu, d.rqu = _vp(dt[u["w"]]), _vp(dt[u["rq"]])
+        d.bu = _vp(dt[u["bias"]]) if u.get("bias") else None
+        d.N, d.ld = int(g["N"]), sg.shape[1]
+        d.silu_Mi, d.silu_Si, d.silu_sh = int(s["Mi"]), int(s["Si"]), int(s["sh_out"])
+        d.mul_sh, d.fq_M, d.fq_S = int(u["aux_shift"]), int(q["M"]), int(q["S"])
+        d.sg_out, d.f_out, d.fq_out = _vp(sg), _vp(m._buf(u["out"])), _vp(m._buf(q["out"]))
+        _lib.call("llhip_gate_up", ctypes.byref(d), m._stream_handle())
+
+
+def _gate_up(model, ops, i):
+    """ops[i:i+3] = linear g (silu) -> linear u (mul by g's output) -> quant of u's output, one input."""
+    if i + 2 >= len(ops):
+        return None
+    g, u, q = ops[i:i + 3]
+    if not (_is(g, "linear") and _is(u, "linear") and _is(q, "quant")):
+        return None
+    if (g.get("epilogue") != "silu" or u.get("epilogue") != "mul" or u.get("aux") != g["out"] or g["in"] != u["in"]
+            or q["in"] != u["out"] or int(g["N"]) != int(u["N"]) or int(g["K"]) != int(u["K"])):
+        return None
+    if g.get("out_dtype", "i16") != "i16" or u.get("out_dtype", "i16") != "i16":
+        return None
+    return _GateUpStep(model, g, u, q)
+
+
 def wide_steps(model, ops, steps):
     """Launches of a fused run for more rows than its fused kernel takes (prompt chunks): the run's
     per-op steps, with each rmsnorm + quant of its output as one launch, three linears of one input
-    (q, k, v) as one grouped launch and attn_in's group rope q, rope k, quant q, quant k, kv_write
-    as two.  The arithmetic of every op is unchanged."""
+    (q, k, v) as one grouped launch, the gate and up linears and the quant of their product as
+    one launch, and attn_in's group rope q, rope k, quant q, quant k, kv_write as two.  The
+    arithmetic of every op is unchanged."""
     out, i = [], 0
     while i < len(ops):
         a = ops[i]
@@ -128,6 +168,11 @@ def wide_steps(model, ops, steps):
                 out.append(_NormQuantStep(model, a, ops[i + 1]))
                 i += 2
                 continue
+        gu = _gate_up(model, ops, i)
+        if gu is not None:
+            out.append(gu)
+            i += 3
+            continue
         if i + 2 < len(ops):
             lins = ops[i:i + 3]
             if (all(_plain_linear(o) for o in lins) and len({o["in"] for o in lins}) == 1

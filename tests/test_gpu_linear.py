@@ -6,6 +6,8 @@ At M=2048 x N=151936 the oracle checks 8 sampled rows over all columns and 96 sa
 columns over all rows (an output element depends only on its A row and W row)."""
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -179,3 +181,40 @@ def test_linear_group_equals_separate_launches(M, K):
         assert np.array_equal(od.cpu().numpy()[:, :N], wnt) and not od.cpu().numpy()[:, N:].any()
     with pytest.raises(ValueError):
         _lib.call("llhip_linear_group", ptr(ad), M, K, K, 5, probs, ptr(workspace()), stream())
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 896, 4864), (300, 128, 200), (40, 100, 64)])
+def test_gate_up_equals_the_three_ops(M, K, N):
+    """llhip_gate_up (gate linear with the silu epilogue, up linear with the mul epilogue on the
+    gate's output, quant of the product, in one launch) equals the three ops run one by one; K = 100
+    runs the op-by-op fallback inside the entry point."""
+    from llaccel_amd import _lib
+    from oracle import golden_np as OO
+    from tests.gpu_helpers import ptr, stream, torch, up
+
+    t = torch()
+    rng = np.random.default_rng(M + K + N)
+    a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    wg, wu = (rng.integers(-127, 128, (N, K)).astype(np.int8) for _ in range(2))
+    rqg, rqu = random_rq(rng, N, K, False), random_rq(rng, N, K, False)
+    bg, bu = rng.integers(-(2**20), 2**20, N), None
+    silu = {"Mi": 1 << 30, "Si": 30, "sh_out": 16}
+    mul_sh, fqM, fqS = 11, 1518500250, 38
+    sg = gpu_linear(a, wg, rqg, bias=bg, epilogue="silu", silu=silu)
+    f = gpu_linear(a, wu, rqu, epilogue="mul", aux=sg, aux_shift=mul_sh)
+    fq = OO.vquant(f, fqM, fqS)
+    d = _lib.GateUpDesc()
+    keep = [up(a, np.int8), up(wg, np.int8), up(rqg, np.int32), up(bg, np.int32), up(wu, np.int8), up(rqu, np.int32)]
+    ld = N + 5
+    outs = [t.zeros((M, ld), dtype=t.int16, device="cuda"), t.zeros((M, ld), dtype=t.int16, device="cuda"),
+            t.zeros((M, ld), dtype=t.int8, device="cuda")]
+    d.A, d.M, d.K, d.lda = ptr(keep[0]), M, K, K
+    d.Wg, d.rqg, d.bg, d.Wu, d.rqu, d.bu = ptr(keep[1]), ptr(keep[2]), ptr(keep[3]), ptr(keep[4]), ptr(keep[5]), None
+    d.N, d.ld = N, ld
+    d.silu_Mi, d.silu_Si, d.silu_sh, d.mul_sh, d.fq_M, d.fq_S = silu["Mi"], silu["Si"], silu["sh_out"], mul_sh, fqM, fqS
+    d.sg_out, d.f_out, d.fq_out = (ptr(o) for o in outs)
+    _lib.call("llhip_gate_up", ctypes.byref(d), stream())
+    got = [o.cpu().numpy() for o in outs]
+    for g_, w_ in zip(got, (sg, f, fq)):
+        assert np.array_equal(g_[:, :N], w_) and not g_[:, N:].any()
+    assert np.count_nonzero(f) > f.size // 2  # the products are not degenerate
