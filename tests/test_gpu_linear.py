@@ -129,7 +129,8 @@ def test_large_gemm_path_ragged_with_epilogues(epilogue, out_i8):
 
 @pytest.mark.parametrize("epilogue,out_i8", [("none", True), ("none", False), ("resadd", False), ("silu", False),
                                              ("mul", False)])
-@pytest.mark.parametrize("M,K,N", [(512, 4864, 896), (300, 2048, 900), (2048, 4864, 896), (130, 4864, 130)])
+@pytest.mark.parametrize("M,K,N", [(512, 4864, 896), (300, 2048, 900), (2048, 4864, 896), (130, 4864, 130),
+                                   (512, 896, 896), (33, 256, 130)])
 def test_split_k_gemm(M, K, N, epilogue, out_i8):
     """Prompt-sized GEMMs with too few output tiles for the GPU take the split-K path (int32
     partial planes in the workspace, summed by a second kernel): equal to the oracle and to the
