@@ -261,6 +261,36 @@ typedef struct llhip_norm_linear_desc {
 /* golden.py:286-296 + 316-342 -- rmsnorm, quant, one linear with any epilogue. */
 int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream);
 
+/* ---- the reference accelerator's instruction set on the GPU ----
+ * A device holding the ISA's DRAM and 1 MiB SRAM in GPU memory that runs .llbin programs (docs/ISA.md,
+ * binary version 2) with the functional simulator's semantics and performance counters.  Errors
+ * (the simulator's runtime_error conditions, with its messages) return a negative errno with the
+ * message in llhip_last_error(). */
+typedef struct llhip_device llhip_device;
+#define LLHIP_DEV_NUM_PERF 27
+
+/* runtime/include/llaccel/device.h:41 makeFuncSim (funcsim.cpp:24-27): a device with max(dram_bytes,
+ * 1 MiB) of zeroed DRAM; epilogue_fusion selects the v2 target (GEMM epilogues allowed).  NULL on
+ * failure. */
+llhip_device* llhip_dev_create(uint64_t dram_bytes, int epilogue_fusion);
+/* device.h:17 ~Device */
+void llhip_dev_destroy(llhip_device* dev);
+/* device.h:22 dramWrite (funcsim.cpp:29-33): host bytes into DRAM, which grows to addr + n */
+int llhip_dev_dram_write(llhip_device* dev, uint64_t addr, const void* src, uint64_t n);
+/* device.h:23 dramRead (funcsim.cpp:34-37) */
+int llhip_dev_dram_read(llhip_device* dev, uint64_t addr, void* dst, uint64_t n);
+/* device.h:24 dramSize */
+uint64_t llhip_dev_dram_size(const llhip_device* dev);
+/* device.h:26 run (funcsim.cpp:41-107, sequential policy): executes from pc until HALT with the POS
+ * register at pos; perf (27 counters, include/llaccel/isa.h:133-141) may be NULL. */
+int llhip_dev_run(llhip_device* dev, uint32_t pc, uint32_t pos, uint64_t* perf);
+/* device.h:28 sramSnapshot: the 1 MiB SRAM into dst */
+int llhip_dev_sram_snapshot(llhip_device* dev, void* dst);
+/* device.h:19 maxAttentionHeadDim (funcsim.cpp:24) */
+uint32_t llhip_dev_max_attention_head_dim(void);
+/* device.h:22 (device side): the DRAM's device address, valid until the DRAM next grows */
+void* llhip_dev_dram_ptr(llhip_device* dev);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,8 +58,19 @@ _SIGS = {
     "llhip_quant_rows_i8": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
     "llhip_quant_i16": [_p, _i64, _i64, _p, _p, _p],
     "llhip_rmsnorm_quant": [_p, _i64, _p],
+    "llhip_dev_create": [ctypes.c_uint64, _i32],
+    "llhip_dev_destroy": [_p],
+    "llhip_dev_dram_write": [_p, ctypes.c_uint64, _p, ctypes.c_uint64],
+    "llhip_dev_dram_read": [_p, ctypes.c_uint64, _p, ctypes.c_uint64],
+    "llhip_dev_dram_size": [_p],
+    "llhip_dev_run": [_p, ctypes.c_uint32, ctypes.c_uint32, _p],
+    "llhip_dev_sram_snapshot": [_p, _p],
+    "llhip_dev_max_attention_head_dim": [],
+    "llhip_dev_dram_ptr": [_p],
 }
-_RESTYPES = {"llhip_last_error": ctypes.c_char_p, "llhip_workspace_bytes": _i64}
+_RESTYPES = {"llhip_last_error": ctypes.c_char_p, "llhip_workspace_bytes": _i64, "llhip_dev_create": _p,
+             "llhip_dev_destroy": None, "llhip_dev_dram_size": ctypes.c_uint64,
+             "llhip_dev_max_attention_head_dim": ctypes.c_uint32, "llhip_dev_dram_ptr": _p}
 
 _LIB = None
 

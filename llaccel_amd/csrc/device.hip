@@ -1,0 +1,655 @@
+// A device for the reference accelerator's instruction set (docs/ISA.md, binary version 2) on the
+// GPU: the llaccel::Device contract of runtime/include/llaccel/device.h:15-29 with the semantics of
+// the functional simulator runtime/src/funcsim.cpp.
+//
+// DRAM and the 1 MiB SRAM are device buffers.  run() decodes the instruction stream on the host in
+// program order -- the simulator's sequential policy, funcsim.cpp:84-87: every instruction executes
+// before the next one issues, so a semaphore wait is satisfied exactly when earlier instructions
+// signalled enough -- checks each instruction as the simulator does (same conditions, same
+// messages), accumulates the same performance counters (functions of the operands and POS only) and
+// enqueues the instruction's kernels on one stream: DMA and KV_WRITE as strided copies, GEMM as the
+// tiled-weight relayout + llhip_linear, the VEC ops and ATTN through the datapath's own kernels.
+// Data-dependent faults (an invalid requant table entry) are flagged on the device and reported once
+// the program has drained.
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/llhip.h"
+#include "common.h"
+
+namespace llhip {
+namespace {
+
+constexpr uint32_t kSram = 1u << 20, kInstr = 64, kNumSem = 32, kTM = 16, kTMax = 4096, kBeat = 64;
+constexpr uint8_t kNoSem = 0xFF;
+constexpr uint64_t kMaxInstr = 50000000;
+constexpr uint64_t kDramPad = 64 << 10;  // zero bytes past the logical DRAM size (whole-tile reads)
+enum Op : uint8_t {
+  OP_NOP = 0x00, OP_HALT = 0x01, OP_DMA_LOAD = 0x10, OP_DMA_STORE = 0x11, OP_GEMM = 0x20, OP_RMSNORM = 0x30,
+  OP_ROPE = 0x31, OP_SILU = 0x32, OP_MUL = 0x33, OP_ADD = 0x34, OP_QUANT = 0x35, OP_ATTN = 0x40, OP_KV_WRITE = 0x41,
+};
+// performance counter indices (include/llaccel/isa.h:133-141)
+enum Perf {
+  P_CYCLES = 0, P_INSTR_ISSUED, P_CP_STALL_WAIT, P_CP_STALL_QFULL, P_CP_STALL_FETCH, P_GEMM_BUSY, P_GEMM_MAC,
+  P_GEMM_SRAM_STALL, P_GEMM_EPI, P_VEC_BUSY, P_VEC_SRAM_STALL, P_ATTN_BUSY, P_ATTN_SRAM_STALL, P_ATTN_MAC,
+  P_DMA_BUSY, P_DMA_SRAM_STALL, P_DMA_DRAM_WAIT, P_SRAM_RD, P_SRAM_WR, P_DRAM_RD, P_DRAM_WR, P_GEMM_IDLE,
+  P_VEC_IDLE, P_ATTN_IDLE, P_ATTN_DRAM_WAIT, P_ATTN_DRAM_RD, P_ATTN_DRAM_WR, P_NUM
+};
+static_assert(P_NUM == LLHIP_DEV_NUM_PERF, "27 performance counters");
+
+const char* op_name(uint8_t op) {
+  switch (op) {
+    case OP_NOP: return "NOP";
+    case OP_HALT: return "HALT";
+    case OP_DMA_LOAD: return "DMA_LOAD";
+    case OP_DMA_STORE: return "DMA_STORE";
+    case OP_GEMM: return "GEMM";
+    case OP_RMSNORM: return "VEC_RMSNORM";
+    case OP_ROPE: return "VEC_ROPE";
+    case OP_SILU: return "VEC_SILU";
+    case OP_MUL: return "VEC_MUL";
+    case OP_ADD: return "VEC_ADD";
+    case OP_QUANT: return "VEC_QUANT";
+    case OP_ATTN: return "ATTN";
+    case OP_KV_WRITE: return "KV_WRITE";
+  }
+  return "?";
+}
+int engine_of(uint8_t op) { return op < 0x10 ? 0 : op < 0x20 ? 1 : op < 0x30 ? 2 : op < 0x40 ? 3 : 4; }
+
+std::string hex(uint64_t v) {
+  char b[32];
+  std::snprintf(b, sizeof b, "%llx", (unsigned long long)v);
+  return b;
+}
+[[noreturn]] void bad(const std::string& m) { throw std::runtime_error(m); }
+void hip_ok(hipError_t e, const char* what) {
+  if (e != hipSuccess) bad(std::string(what) + ": " + hipGetErrorString(e));
+}
+void rc_ok(int rc) {
+  if (rc) bad(llhip_last_error());
+}
+
+// ---- kernels ----------------------------------------------------------------------------
+// rows x bytes strided copy; 16-byte units when every address and stride allows it
+__global__ void copy_rows16(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, uint32_t rows, uint32_t units,
+                            uint64_t ss, uint64_t ds) {
+  const uint64_t n = (uint64_t)rows * units;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t r = i / units, u = i % units;
+    *reinterpret_cast<uint4*>(dst + r * ds + 16 * u) = *reinterpret_cast<const uint4*>(src + r * ss + 16 * u);
+  }
+}
+__global__ void copy_rows8(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, uint32_t rows, uint32_t bytes,
+                           uint64_t ss, uint64_t ds) {
+  const uint64_t n = (uint64_t)rows * bytes;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t r = i / bytes, b = i % bytes;
+    dst[r * ds + b] = src[r * ss + b];
+  }
+}
+// destination rows that overlap each other: rows in order, one workgroup (later rows win)
+__global__ void copy_rows_ordered(uint8_t* dst, const uint8_t* src, uint32_t rows, uint32_t bytes, uint64_t ss,
+                                  uint64_t ds) {
+  for (uint32_t r = 0; r < rows; ++r) {
+    for (uint32_t b = threadIdx.x; b < bytes; b += blockDim.x) dst[r * ds + b] = src[r * ss + b];
+    __syncthreads();
+  }
+}
+// GEMM weights: tile (nt, kt) of 16x16 bytes at w + (nt*KT + kt)*256, byte n*16 + k = W[nt*16+n][kt*16+k]
+// (docs/ISA.md "GEMM details") -> row-major W [N][K]
+__global__ void untile_w(const uint8_t* __restrict__ w, int8_t* __restrict__ out, uint32_t N, uint32_t K) {
+  const uint64_t n_all = (uint64_t)N * K;
+  const uint32_t KT = K / 16;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_all; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t n = (uint32_t)(i / K), k = (uint32_t)(i % K);
+    out[i] = (int8_t)w[((uint64_t)(n / 16) * KT + k / 16) * 256 + (n % 16) * 16 + k % 16];
+  }
+}
+// requant table entries {M_n, S_n}: M_n >= 0 and S_n in [0, 63] (funcsim.cpp:214), else flag 1
+__global__ void check_rq(const int32_t* __restrict__ rq, uint32_t N, int32_t* status) {
+  const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n < N && (rq[2 * n] < 0 || rq[2 * n + 1] < 0 || rq[2 * n + 1] > 63)) atomicOr(status, 1);
+}
+// RoPE rows p = pos + m of the SRAM table [cos D/2][sin D/2] (row stride `stride` bytes) gathered
+// into cos/sin [M][D/2]
+__global__ void gather_rope(const uint8_t* __restrict__ sram, uint32_t table, uint32_t stride, uint32_t pos,
+                            uint32_t M, uint32_t D, int16_t* __restrict__ cs, int16_t* __restrict__ sn) {
+  const uint32_t h = D / 2;
+  for (uint32_t i = threadIdx.x; i < M * D; i += blockDim.x) {
+    const uint32_t m = i / D, j = i % D;
+    const uint64_t a = (uint64_t)table + (uint64_t)(pos + m) * stride + 2ull * j;
+    const int16_t v = (int16_t)(sram[a] | (sram[a + 1] << 8));
+    if (j < h)
+      cs[m * h + j] = v;
+    else
+      sn[m * h + j - h] = v;
+  }
+}
+// KV_WRITE: src [M][Hkv*D] -> base + kvh*stride + (pos+m)*D (funcsim.cpp:390-398)
+__global__ void kv_rows(uint8_t* __restrict__ dram, const uint8_t* __restrict__ src, uint64_t base, uint32_t M,
+                        uint32_t Hkv, uint32_t D, uint64_t stride, uint32_t pos) {
+  const uint64_t n = (uint64_t)M * Hkv * D;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t d = i % D, r = i / D, kvh = r % Hkv, m = r / Hkv;
+    dram[base + kvh * stride + (pos + m) * D + d] = src[i];
+  }
+}
+
+unsigned grid_for(uint64_t n) { return (unsigned)std::min<uint64_t>(std::max<uint64_t>(ceil_div((int64_t)n, 256), 1), 4096); }
+
+bool overlap(uint64_t a, uint64_t an, uint64_t b, uint64_t bn) { return an && bn && a < b + bn && b < a + an; }
+
+}  // namespace
+
+struct Device {
+  uint8_t* dram = nullptr;
+  uint64_t cap = 0, size = 0;  // allocation (without the pad) and the simulator's DRAM size
+  uint8_t* sram = nullptr;
+  uint8_t* scratch = nullptr;  // results of ops whose output aliases an input, copied back after
+  int8_t* wrm = nullptr;       // row-major GEMM weights
+  int16_t* rope_tab = nullptr;
+  void* ws = nullptr;
+  int32_t* status = nullptr;
+  hipStream_t stream = nullptr;
+  bool fusion = false;
+  uint32_t pos = 0;
+  uint64_t perf[P_NUM] = {};
+  uint32_t sem[kNumSem] = {};
+
+  ~Device() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (void* p : {(void*)dram, (void*)sram, (void*)scratch, (void*)wrm, (void*)rope_tab, ws, (void*)status})
+      if (p) (void)hipFree(p);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  void init(uint64_t dram_bytes, bool epilogue_fusion) {
+    fusion = epilogue_fusion;
+    hip_ok(hipStreamCreate(&stream), "hipStreamCreate");
+    hip_ok(hipMalloc(&sram, kSram), "hipMalloc");
+    hip_ok(hipMalloc(&scratch, kSram), "hipMalloc");
+    hip_ok(hipMalloc(&wrm, kSram), "hipMalloc");
+    hip_ok(hipMalloc(&rope_tab, 2 * kTM * 128 * sizeof(int16_t)), "hipMalloc");
+    hip_ok(hipMalloc(&ws, (size_t)llhip_workspace_bytes()), "hipMalloc");
+    hip_ok(hipMalloc(&status, 4), "hipMalloc");
+    hip_ok(hipMemset(sram, 0, kSram), "hipMemset");
+    hip_ok(hipMemset(ws, 0, (size_t)llhip_workspace_bytes()), "hipMemset");
+    hip_ok(hipMemset(status, 0, 4), "hipMemset");
+    grow(std::max<uint64_t>(dram_bytes, 1u << 20));
+  }
+
+  // the simulator's ensureDram: the DRAM grows (zero-filled) to n bytes
+  void grow(uint64_t n) {
+    if (n <= size) return;
+    if (n > cap) {
+      const uint64_t ncap = std::max<uint64_t>((n + (1u << 20) - 1) & ~uint64_t((1u << 20) - 1), 2 * cap);
+      uint8_t* nd = nullptr;
+      hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      hip_ok(hipMalloc(&nd, ncap + kDramPad), "hipMalloc (DRAM)");
+      hip_ok(hipMemset(nd, 0, ncap + kDramPad), "hipMemset");
+      if (dram) {
+        hip_ok(hipMemcpy(nd, dram, size, hipMemcpyDeviceToDevice), "hipMemcpy");
+        hip_ok(hipFree(dram), "hipFree");
+      }
+      dram = nd;
+      cap = ncap;
+    }
+    size = n;  // bytes past the old size are zero: nothing is ever written beyond `size`
+  }
+
+  void write(uint64_t addr, const void* src, uint64_t n) {
+    if (addr > UINT64_MAX - n) bad("dramWrite address overflow");
+    grow(addr + n);
+    hip_ok(hipMemcpyAsync(dram + addr, src, n, hipMemcpyHostToDevice, stream), "hipMemcpyAsync");
+    hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  }
+  void read(uint64_t addr, void* dst, uint64_t n) {
+    if (addr > size || n > size - addr) bad("dramRead out of range");
+    hip_ok(hipMemcpyAsync(dst, dram + addr, n, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
+    hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  }
+
+  // ---- checks (funcsim.cpp:124-132) ----
+  static void chk(uint64_t addr, uint64_t n, const char* what) {
+    if (addr + n > kSram) bad(std::string("SRAM access out of range in ") + what + " @0x" + hex(addr));
+  }
+  void chk_dram(uint64_t addr, uint64_t n, const char* what) const {
+    if (addr > size || n > size - addr || addr > UINT32_MAX || n > uint64_t(UINT32_MAX) + 1 - addr)
+      bad(std::string("DRAM access out of range in ") + what + " @0x" + hex(addr));
+  }
+  // SRAM operands of the datapath kernels: 16-byte aligned (docs/ISA.md "Opcodes")
+  static void aligned(uint64_t addr, const char* what) {
+    if (addr % 16) bad(std::string("SRAM operand not 16-B aligned in ") + what + " @0x" + hex(addr));
+  }
+  // An output that aliases an input: exactly (dst == src, the simulator's element-by-element loops
+  // read each element before writing it) -> computed into scratch and copied back; any other
+  // overlap would see partially updated inputs in the simulator's order -> rejected.
+  static bool alias(uint64_t dst, uint64_t dn, uint64_t src, uint64_t sn, const char* what) {
+    if (!overlap(dst, dn, src, sn)) return false;
+    if (dst != src) bad(std::string("overlapping operands in ") + what);
+    return true;
+  }
+
+  void copy(uint8_t* dst, const uint8_t* src, uint32_t rows, uint32_t bytes, uint64_t ss, uint64_t ds) {
+    if (!rows || !bytes) return;
+    if (rows > 1 && ds < bytes) {
+      hipLaunchKernelGGL(copy_rows_ordered, dim3(1), dim3(256), 0, stream, dst, src, rows, bytes, ss, ds);
+    } else if (((uintptr_t)dst | (uintptr_t)src | ss | ds | bytes) % 16 == 0) {
+      hipLaunchKernelGGL(copy_rows16, dim3(grid_for((uint64_t)rows * bytes / 16)), dim3(256), 0, stream, dst, src, rows,
+                         bytes / 16, ss, ds);
+    } else {
+      hipLaunchKernelGGL(copy_rows8, dim3(grid_for((uint64_t)rows * bytes)), dim3(256), 0, stream, dst, src, rows, bytes,
+                         ss, ds);
+    }
+    hip_ok(hipGetLastError(), "kernel launch");
+  }
+
+  // ---- instructions ----
+  void dma(const uint32_t* in, bool load) {
+    const uint32_t sramA = in[2], dramA = in[3], rows = in[4], rowBytes = in[5], srcStride = in[6], dstStride = in[7];
+    if (rowBytes % 16 || sramA % 16) bad("DMA row/addr not 16-B aligned");
+    uint64_t beats = 0, sramReadBytes = 0;
+    for (uint32_t r = 0; r < rows; ++r) {  // funcsim.cpp:162-186
+      const uint64_t dramRow = uint64_t(dramA) + uint64_t(r) * (load ? srcStride : dstStride);
+      beats += rowBytes ? ((dramRow % 64) + rowBytes + 63) / 64 : 0;
+      if (!load) {
+        uint64_t copied = 0;
+        while (copied < rowBytes) {
+          const uint64_t useful = std::min<uint64_t>(64 - ((dramRow + copied) % 64), rowBytes - copied);
+          const uint64_t source = uint64_t(sramA) + uint64_t(r) * srcStride + copied;
+          sramReadBytes += ((source % 64 + useful + 63) / 64) * 64;
+          copied += useful;
+        }
+      }
+      if (load) {
+        const uint64_t s = uint64_t(dramA) + uint64_t(r) * srcStride, d = uint64_t(sramA) + uint64_t(r) * dstStride;
+        if (s + rowBytes > size) bad("DMA_LOAD source out of DRAM range");
+        chk(d, rowBytes, "DMA_LOAD");
+      } else {
+        const uint64_t s = uint64_t(sramA) + uint64_t(r) * srcStride, d = uint64_t(dramA) + uint64_t(r) * dstStride;
+        chk(s, rowBytes, "DMA_STORE");
+        grow(d + rowBytes);
+      }
+    }
+    const uint64_t bytes = uint64_t(rows) * rowBytes;
+    perf[load ? P_SRAM_WR : P_SRAM_RD] += load ? bytes : sramReadBytes;
+    perf[load ? P_DRAM_RD : P_DRAM_WR] += beats * 64;
+    perf[P_DMA_BUSY] += beats;
+    if (load)
+      copy(sram + sramA, dram + dramA, rows, rowBytes, srcStride, dstStride);
+    else
+      copy(dram + dramA, sram + sramA, rows, rowBytes, srcStride, dstStride);
+  }
+
+  void gemm(const uint32_t* in) {
+    const uint32_t a = in[2], w = in[3], out = in[4], rq = in[5], bias = in[6], aux = in[7];
+    const uint32_t M = in[8], N = in[9], K = in[10], ep = in[11], siluMi = in[12], siluSi = in[13] & 0xFF,
+                   siluSh = (in[13] >> 8) & 0xFF;
+    const bool hasBias = (in[0] >> 8) & 1;
+    const uint32_t mode = ep & 0xF;
+    const bool outI8 = (ep >> 4) & 1;
+    const uint32_t auxShift = (ep >> 8) & 0xFF;
+    if (M == 0 || M > kTM || N % 16 || K % 16 || N == 0 || K == 0) bad("GEMM bad shape");
+    if (w % 256) bad("GEMM weight address not 256-B aligned");
+    if (outI8 && mode != 0) bad("GEMM i8 output with epilogue");
+    if (mode != 0 && !fusion) bad("GEMM epilogue used on a target without EPILOGUE_FUSION");
+    const uint32_t NT = N / 16, KT = K / 16, outRow = outI8 ? N : 2 * N;
+    chk(a, uint64_t(M) * K, "GEMM A");
+    chk(w, uint64_t(NT) * KT * 256, "GEMM W");
+    chk(rq, uint64_t(N) * 8, "GEMM rq");
+    chk(out, uint64_t(M) * outRow, "GEMM out");
+    if (hasBias) chk(bias, uint64_t(N) * 4, "GEMM bias");
+    const bool useAux = mode == 1 || mode == 3;
+    if (useAux) chk(aux, uint64_t(M) * 2 * N, "GEMM aux");
+    if (mode > 3) bad("GEMM bad epilogue mode");
+    for (uint32_t x : {a, out, rq}) aligned(x, "GEMM");
+    if (hasBias) aligned(bias, "GEMM");
+    if (useAux) aligned(aux, "GEMM");
+    const uint64_t on = uint64_t(M) * outRow;
+    if (overlap(out, on, a, uint64_t(M) * K) || overlap(out, on, w, uint64_t(NT) * KT * 256) ||
+        overlap(out, on, rq, uint64_t(N) * 8) || (hasBias && overlap(out, on, bias, uint64_t(N) * 4)))
+      bad("overlapping operands in GEMM");
+    const bool inplace = useAux && alias(out, on, aux, uint64_t(M) * 2 * N, "GEMM");
+    // counters of funcsim.cpp:202-239 in closed form
+    perf[P_SRAM_RD] += uint64_t(NT) * KT * (256 + uint64_t(M) * 16) + uint64_t(NT) * (128 + (hasBias ? 64 : 0)) +
+                       (useAux ? uint64_t(NT) * M * 32 : 0);
+    perf[P_GEMM_MAC] += uint64_t(NT) * KT * M;
+    perf[P_SRAM_WR] += uint64_t(NT) * M * (outI8 ? 16 : 32);
+    perf[P_GEMM_EPI] += uint64_t(NT) * M;
+    perf[P_GEMM_BUSY] += uint64_t(NT) * KT * (1 + M) + uint64_t(NT) * M;
+
+    hipLaunchKernelGGL(check_rq, dim3(ceil_div(N, 256)), dim3(256), 0, stream,
+                       reinterpret_cast<const int32_t*>(sram + rq), N, status);
+    hipLaunchKernelGGL(untile_w, dim3(grid_for(uint64_t(N) * K)), dim3(256), 0, stream, sram + w, wrm, N, K);
+    hip_ok(hipGetLastError(), "kernel launch");
+    uint8_t* dst = inplace ? scratch : sram + out;
+    rc_ok(llhip_linear(reinterpret_cast<const int8_t*>(sram + a), M, K, K, wrm, N,
+                       reinterpret_cast<const int32_t*>(sram + rq),
+                       hasBias ? reinterpret_cast<const int32_t*>(sram + bias) : nullptr, (int)mode,
+                       useAux ? reinterpret_cast<const int16_t*>(sram + aux) : nullptr, N, auxShift, siluMi, siluSi,
+                       siluSh, outI8 ? 1 : 0, dst, N, ws, stream));
+    if (inplace) copy(sram + out, scratch, 1, (uint32_t)on, 0, 0);
+  }
+
+  void rmsnorm(const uint32_t* in) {
+    const uint32_t src = in[2], gamma = in[3], dst = in[4], M = in[5], K = in[6], epsT = in[7], C = in[8], shPost = in[9];
+    if (K % 16 || K == 0) bad("RMSNORM K not a multiple of 16");
+    const uint64_t n = uint64_t(M) * K * 2;
+    chk(src, n, "RMSNORM src");
+    chk(gamma, uint64_t(K) * 2, "RMSNORM gamma");
+    chk(dst, n, "RMSNORM dst");
+    perf[P_SRAM_RD] += uint64_t(M) * (2 * K * 2 + K * 2);
+    perf[P_SRAM_WR] += uint64_t(M) * K * 2;
+    perf[P_VEC_BUSY] += uint64_t(M) * (2 * K / 16 + 24 + 32);
+    if (!M) return;
+    for (uint32_t x : {src, gamma, dst}) aligned(x, "VEC_RMSNORM");
+    if (overlap(dst, n, gamma, uint64_t(K) * 2)) bad("overlapping operands in VEC_RMSNORM");
+    const bool inplace = alias(dst, n, src, n, "VEC_RMSNORM");
+    int16_t* y = reinterpret_cast<int16_t*>(inplace ? scratch : sram + dst);
+    rc_ok(llhip_rmsnorm(reinterpret_cast<const int16_t*>(sram + src), M, K, K,
+                        reinterpret_cast<const int16_t*>(sram + gamma), epsT, C, shPost, y, K, stream));
+    if (inplace) copy(sram + dst, scratch, 1, (uint32_t)n, 0, 0);
+  }
+
+  void rope(const uint32_t* in) {
+    const uint32_t src = in[2], dst = in[3], M = in[4], H = in[5], D = in[6], table = in[7], stride = in[8];
+    if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256) bad("ROPE bad D");
+    if (M == 0 || M > kTM || H == 0 || H > 255 || pos >= kTMax || M > kTMax - pos || stride < 2 * D)
+      bad("ROPE invalid row/head/context dimensions");
+    const uint32_t row = H * D;
+    const uint64_t n = uint64_t(M) * row * 2;
+    chk(src, n, "ROPE src");
+    chk(dst, n, "ROPE dst");
+    for (uint32_t m = 0; m < M; ++m) chk(uint64_t(table) + uint64_t(pos + m) * stride, 2 * D, "ROPE table");
+    perf[P_SRAM_RD] += uint64_t(M) * (row * 2 + H * 2 * D);
+    perf[P_SRAM_WR] += uint64_t(M) * row * 2;
+    perf[P_VEC_BUSY] += uint64_t(M) * H * (D / 2 / 16 + 1);
+    aligned(src, "VEC_ROPE");
+    aligned(dst, "VEC_ROPE");
+    for (uint32_t m = 0; m < M; ++m)
+      if (overlap(dst, n, uint64_t(table) + uint64_t(pos + m) * stride, 2 * D)) bad("overlapping operands in VEC_ROPE");
+    const bool inplace = alias(dst, n, src, n, "VEC_ROPE");
+    int16_t* cs = rope_tab;
+    int16_t* sn = rope_tab + kTM * 128;
+    hipLaunchKernelGGL(gather_rope, dim3(1), dim3(256), 0, stream, sram, table, stride, pos, M, D, cs, sn);
+    hip_ok(hipGetLastError(), "kernel launch");
+    int16_t* y = reinterpret_cast<int16_t*>(inplace ? scratch : sram + dst);
+    rc_ok(llhip_rope(reinterpret_cast<const int16_t*>(sram + src), M, H, D, row, cs, sn, M, 0, nullptr, nullptr, y, row,
+                     stream));
+    if (inplace) copy(sram + dst, scratch, 1, (uint32_t)n, 0, 0);
+  }
+
+  // kind: 0 SILU(src,dst,count,Mi,Si,sh_out) 1 MUL(a,b,dst,count,sh) 2 ADD(a,b,dst,count,sh_b) 3 QUANT(src,dst,count,M,S)
+  void elementwise(const uint32_t* in, int kind) {
+    static const char* names[] = {"VEC_SILU", "VEC_MUL", "VEC_ADD", "VEC_QUANT"};
+    if (kind == 0 || kind == 3) {
+      const uint32_t src = in[2], dst = in[3], count = in[4], p0 = in[5], p1 = in[6], p2 = in[7];
+      if (count % 16) bad("VEC count not a multiple of 16");
+      const uint64_t dn = uint64_t(count) * (kind == 3 ? 1 : 2);
+      chk(src, uint64_t(count) * 2, "VEC src");
+      chk(dst, dn, "VEC dst");
+      perf[P_SRAM_RD] += uint64_t(count) * 2;
+      perf[P_SRAM_WR] += dn;
+      perf[P_VEC_BUSY] += count / 16;
+      if (!count) return;
+      aligned(src, names[kind]);
+      aligned(dst, names[kind]);
+      // dst at or before src: the simulator's ascending loop reads every element before it is overwritten
+      bool inplace = false;
+      if (overlap(dst, dn, src, uint64_t(count) * 2)) {
+        if (dst > src) bad(std::string("overlapping operands in ") + names[kind]);
+        inplace = true;
+      }
+      uint8_t* y = inplace ? scratch : sram + dst;
+      const int16_t* x = reinterpret_cast<const int16_t*>(sram + src);
+      if (kind == 0)
+        rc_ok(llhip_silu(x, count, p0, p1, p2, reinterpret_cast<int16_t*>(y), stream));
+      else
+        rc_ok(llhip_quant(x, count, p0, p1, reinterpret_cast<int8_t*>(y), stream));
+      if (inplace) copy(sram + dst, scratch, 1, (uint32_t)dn, 0, 0);
+    } else {
+      const uint32_t a = in[2], b = in[3], dst = in[4], count = in[5], sh = in[6];
+      if (count % 16) bad("VEC count not a multiple of 16");
+      const uint64_t n = uint64_t(count) * 2;
+      chk(a, n, "VEC a");
+      chk(b, n, "VEC b");
+      chk(dst, n, "VEC dst");
+      perf[P_SRAM_RD] += uint64_t(count) * 4;
+      perf[P_SRAM_WR] += n;
+      perf[P_VEC_BUSY] += count / 16;
+      if (!count) return;
+      for (uint32_t x : {a, b, dst}) aligned(x, names[kind]);
+      bool inplace = false;
+      for (uint32_t s : {a, b})
+        if (overlap(dst, n, s, n)) {
+          if (dst > s) bad(std::string("overlapping operands in ") + names[kind]);
+          inplace = true;
+        }
+      int16_t* y = reinterpret_cast<int16_t*>(inplace ? scratch : sram + dst);
+      const int16_t* x0 = reinterpret_cast<const int16_t*>(sram + a);
+      const int16_t* x1 = reinterpret_cast<const int16_t*>(sram + b);
+      if (kind == 1)
+        rc_ok(llhip_vmul(x0, x1, count, sh, y, stream));
+      else
+        rc_ok(llhip_vadd(x0, x1, count, sh, y, stream));
+      if (inplace) copy(sram + dst, scratch, 1, (uint32_t)n, 0, 0);
+    }
+  }
+
+  // DRAM beats of T key rows of D bytes from `base` (funcsim.cpp:364-369): one 64-byte beat per row,
+  // D/16 when the row crosses a beat; periodic in t with period at most 4, so counted per period
+  static uint64_t row_beats(uint64_t base, uint32_t T, uint32_t D) {
+    uint64_t per[4], period = 0;
+    for (uint32_t t = 0; t < 4; ++t) per[t] = ((base + uint64_t(t) * D) % kBeat + D > kBeat) ? D / 16 : 1;
+    uint64_t full = 0;
+    for (uint32_t t = 0; t < 4; ++t) full += per[t];
+    period = uint64_t(T / 4) * full;
+    for (uint32_t t = 0; t < T % 4; ++t) period += per[t];
+    return period;
+  }
+
+  void attn(const uint32_t* in) {
+    const uint32_t q = in[2], out = in[3], kbase = in[4], vbase = in[5], M = in[6], H = in[7], Hkv = in[8], D = in[9],
+                   kvStride = in[10], Ms = in[11], Ss = in[12], Mo = in[13], So = in[14];
+    if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256) bad("ATTN bad D");
+    if (M == 0 || M > kTM || H == 0 || H > 255 || Hkv == 0 || Hkv > 255 || H % Hkv)
+      bad("ATTN invalid row/head dimensions");
+    if (pos >= kTMax || M > kTMax - pos || uint64_t(pos + M) * D > kvStride || kvStride % 16 || kbase % 16 ||
+        vbase % 16)
+      bad("ATTN invalid context/DRAM cache stride");
+    const uint32_t row = H * D, grp = H / Hkv;
+    const uint64_t n = uint64_t(M) * row;
+    chk(q, n, "ATTN q");
+    chk(out, n, "ATTN out");
+    const uint32_t Tmax = pos + M;
+    for (uint32_t kvh = 0; kvh < Hkv; ++kvh) {  // the widest row's keys of every head group
+      chk_dram(uint64_t(kbase) + uint64_t(kvh) * kvStride, uint64_t(Tmax) * D, "ATTN K");
+      chk_dram(uint64_t(vbase) + uint64_t(kvh) * kvStride, uint64_t(Tmax) * D, "ATTN V");
+    }
+    if (kvStride % D) bad("ATTN kv_stride not a multiple of D is not supported by this device");
+    for (uint32_t m = 0; m < M; ++m) {
+      const uint32_t T = pos + m + 1;
+      for (uint32_t h = 0; h < H; ++h) {
+        const uint32_t kvh = h / grp;
+        const uint64_t kb = uint64_t(kbase) + uint64_t(kvh) * kvStride, vb = uint64_t(vbase) + uint64_t(kvh) * kvStride;
+        const uint64_t kvRead = (3 * row_beats(kb, T, D) + row_beats(vb, T, D)) * kBeat;
+        perf[P_SRAM_RD] += D;
+        perf[P_DRAM_RD] += kvRead;
+        perf[P_ATTN_DRAM_RD] += kvRead;
+        perf[P_SRAM_WR] += D;
+        perf[P_ATTN_MAC] += 4ull * T;
+        perf[P_ATTN_BUSY] += 7ull * T + 32;
+      }
+    }
+    aligned(q, "ATTN");
+    aligned(out, "ATTN");
+    const bool inplace = alias(out, n, q, n, "ATTN");
+    int8_t* o = reinterpret_cast<int8_t*>(inplace ? scratch : sram + out);
+    const int pb = ((in[0] >> 8) & 2) ? 15 : 8;
+    rc_ok(llhip_attention(reinterpret_cast<const int8_t*>(sram + q), M, H, Hkv, D, row, pos, nullptr, nullptr, 0,
+                          reinterpret_cast<const int8_t*>(dram + kbase), reinterpret_cast<const int8_t*>(dram + vbase),
+                          kvStride / D, Ms, Ss, Mo, So, pb, o, row, ws, stream));
+    if (inplace) copy(sram + out, scratch, 1, (uint32_t)n, 0, 0);
+  }
+
+  void kv_write(const uint32_t* in) {
+    const uint32_t src = in[2], base = in[3], M = in[4], Hkv = in[5], D = in[6], kvStride = in[7];
+    if ((D != 16 && D != 32 && D != 64 && D != 128 && D != 256) || M == 0 || M > kTM || Hkv == 0 || Hkv > 255 ||
+        pos >= kTMax || M > kTMax - pos || uint64_t(pos + M) * D > kvStride || kvStride % 16 || base % 16)
+      bad("KV_WRITE invalid dimensions/DRAM cache stride");
+    const uint32_t row = Hkv * D;
+    chk(src, uint64_t(M) * row, "KV_WRITE src");
+    for (uint32_t m = 0; m < M; ++m)
+      for (uint32_t kvh = 0; kvh < Hkv; ++kvh) {
+        const uint64_t d = uint64_t(base) + uint64_t(kvh) * kvStride + uint64_t(pos + m) * D;
+        chk_dram(d, D, "KV_WRITE dst");
+        const uint64_t wr = ((d % kBeat + D > kBeat) ? D / 16 : 1) * kBeat;
+        perf[P_DRAM_WR] += wr;
+        perf[P_ATTN_DRAM_WR] += wr;
+      }
+    perf[P_SRAM_RD] += uint64_t(M) * row;
+    perf[P_ATTN_BUSY] += uint64_t(M) * Hkv;
+    hipLaunchKernelGGL(kv_rows, dim3(grid_for(uint64_t(M) * row)), dim3(256), 0, stream, dram, sram + src, uint64_t(base),
+                       M, Hkv, D, uint64_t(kvStride), pos);
+    hip_ok(hipGetLastError(), "kernel launch");
+  }
+
+  void execute(const uint32_t* in) {
+    const uint8_t op = in[0] & 0xFF;
+    auto shift = [](uint32_t s) {
+      if (s > 63) bad("shift outside [0,63]");
+    };
+    switch (op) {  // funcsim.cpp:131-138
+      case OP_GEMM: shift((in[11] >> 8) & 0xFF); shift(in[13] & 255); shift((in[13] >> 8) & 255); break;
+      case OP_RMSNORM: shift(in[9]); break;
+      case OP_SILU: shift(in[6]); shift(in[7]); break;
+      case OP_QUANT: case OP_ADD: case OP_MUL: shift(in[6]); break;
+      case OP_ATTN: shift(in[12]); shift(in[14]); break;
+      default: break;
+    }
+    switch (op) {
+      case OP_DMA_LOAD: return dma(in, true);
+      case OP_DMA_STORE: return dma(in, false);
+      case OP_GEMM: return gemm(in);
+      case OP_RMSNORM: return rmsnorm(in);
+      case OP_ROPE: return rope(in);
+      case OP_SILU: return elementwise(in, 0);
+      case OP_MUL: return elementwise(in, 1);
+      case OP_ADD: return elementwise(in, 2);
+      case OP_QUANT: return elementwise(in, 3);
+      case OP_ATTN: return attn(in);
+      case OP_KV_WRITE: return kv_write(in);
+      default: bad("unexpected opcode " + std::to_string(int(op)));
+    }
+  }
+
+  // Fetches, checks and executes instructions from `pc` until HALT (funcsim.cpp:41-107, sequential).
+  void run(uint32_t pc, uint32_t p) {
+    std::memset(perf, 0, sizeof perf);
+    std::memset(sem, 0, sizeof sem);
+    pos = p;
+    hip_ok(hipMemsetAsync(status, 0, 4, stream), "hipMemsetAsync");
+    std::vector<uint32_t> window;  // instructions fetched from DRAM, 1024 at a time
+    uint64_t wbase = 0, fetchPc = pc, issued = 0;
+    for (;;) {
+      if (fetchPc + kInstr > size) bad("instruction fetch out of DRAM range");
+      if (window.empty() || fetchPc < wbase || fetchPc + kInstr > wbase + window.size() * 4) {
+        const uint64_t n = std::min<uint64_t>(1024 * kInstr, (size - fetchPc) / kInstr * kInstr);
+        window.assign(n / 4, 0);
+        wbase = fetchPc;
+        // ordered after every instruction enqueued so far: a program that stores over its own
+        // later instructions sees them as the simulator does
+        hip_ok(hipMemcpyAsync(window.data(), dram + fetchPc, n, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
+        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      }
+      const uint32_t* in = window.data() + (fetchPc - wbase) / 4;
+      const uint8_t op = in[0] & 0xFF, ws_ = (in[0] >> 16) & 0xFF, ss = (in[0] >> 24) & 0xFF;
+      if ((ws_ != kNoSem && ws_ >= kNumSem) || (ss != kNoSem && ss >= kNumSem)) bad("invalid semaphore index");
+      if (engine_of(op) == 0 && op != OP_NOP && op != OP_HALT) bad("invalid command processor opcode");
+      if (ws_ != kNoSem && sem[ws_] < in[1])
+        bad("deadlock at pc=0x" + hex(fetchPc) + " (" + op_name(op) + " waits sem " + std::to_string(ws_) +
+            " >= " + std::to_string(in[1]) + ", current " + std::to_string(sem[ws_]) + ")");
+      fetchPc += kInstr;
+      perf[P_INSTR_ISSUED]++;
+      perf[P_DRAM_RD] += kInstr;
+      if (++issued > kMaxInstr) bad("instruction limit exceeded (runaway program?)");
+      if (op == OP_HALT) break;
+      if (op != OP_NOP) {
+        uint32_t copy_in[16];
+        std::memcpy(copy_in, in, sizeof copy_in);  // execute() may refetch the window (DRAM growth)
+        execute(copy_in);
+      }
+      if (ss != kNoSem) sem[ss]++;
+    }
+    int32_t st = 0;
+    hip_ok(hipMemcpyAsync(&st, status, 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
+    hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (st & 1) bad("invalid requantization table entry");
+  }
+};
+
+}  // namespace llhip
+
+using llhip::Device;
+
+template <class F>
+static int guarded(F&& f) {
+  try {
+    f();
+    return 0;
+  } catch (const std::exception& e) {
+    return llhip::fail(-EINVAL, "%s", e.what());
+  }
+}
+
+extern "C" {
+
+llhip_device* llhip_dev_create(uint64_t dram_bytes, int epilogue_fusion) {
+  Device* d = new Device();
+  if (guarded([&] { d->init(dram_bytes, epilogue_fusion != 0); })) {
+    delete d;
+    return nullptr;
+  }
+  return reinterpret_cast<llhip_device*>(d);
+}
+
+void llhip_dev_destroy(llhip_device* h) { delete reinterpret_cast<Device*>(h); }
+
+int llhip_dev_dram_write(llhip_device* h, uint64_t addr, const void* src, uint64_t n) {
+  if (!h || (n && !src)) return llhip::fail(-EINVAL, "dev_dram_write: null argument");
+  return guarded([&] { reinterpret_cast<Device*>(h)->write(addr, src, n); });
+}
+
+int llhip_dev_dram_read(llhip_device* h, uint64_t addr, void* dst, uint64_t n) {
+  if (!h || (n && !dst)) return llhip::fail(-EINVAL, "dev_dram_read: null argument");
+  return guarded([&] { reinterpret_cast<Device*>(h)->read(addr, dst, n); });
+}
+
+uint64_t llhip_dev_dram_size(const llhip_device* h) { return h ? reinterpret_cast<const Device*>(h)->size : 0; }
+
+int llhip_dev_run(llhip_device* h, uint32_t pc, uint32_t pos, uint64_t* perf) {
+  if (!h) return llhip::fail(-EINVAL, "dev_run: null device");
+  Device* d = reinterpret_cast<Device*>(h);
+  const int rc = guarded([&] { d->run(pc, pos); });
+  if (rc) (void)hipStreamSynchronize(d->stream);
+  if (!rc && perf) std::memcpy(perf, d->perf, sizeof d->perf);
+  return rc;
+}
+
+int llhip_dev_sram_snapshot(llhip_device* h, void* dst) {
+  if (!h || !dst) return llhip::fail(-EINVAL, "dev_sram_snapshot: null argument");
+  Device* d = reinterpret_cast<Device*>(h);
+  return guarded([&] {
+    llhip::hip_ok(hipMemcpyAsync(dst, d->sram, llhip::kSram, hipMemcpyDeviceToHost, d->stream), "hipMemcpyAsync");
+    llhip::hip_ok(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
+  });
+}
+
+uint32_t llhip_dev_max_attention_head_dim(void) { return 256; }
+
+void* llhip_dev_dram_ptr(llhip_device* h) { return h ? reinterpret_cast<Device*>(h)->dram : nullptr; }
+
+}  // extern "C"

@@ -43,10 +43,11 @@ def test_header_declarations_cite_the_reference():
             continue
         # the comment block directly above each compute entry point cites the reference function it
         # replaces: golden.py:<lines> (the datapath), verify.py:<lines> (record verification) or
-        # refquant.py:<lines> (the qgraph producer)
+        # refquant.py:<lines> (the qgraph producer), device.h:<lines> / funcsim.cpp:<lines> (the
+        # instruction-set device)
         idx = text.index(name + "(")
         before = text[:idx].rsplit(");", 1)[-1]
-        assert re.search(r"(golden|verify|refquant)\.py:\d+", before), name
+        assert re.search(r"((golden|verify|refquant)\.py|device\.h|funcsim\.cpp):\d+", before), name
 
 
 def test_hip_luts_are_current_and_equal_reference(golden_dir):

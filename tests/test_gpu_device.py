@@ -1,0 +1,77 @@
+"""The GPU instruction-set device (llaccel_amd.device.GpuDevice -> csrc/device.hip) against the
+CPU oracle of the reference's functional simulator (oracle/isa_np.py, itself pinned to the
+reference simulator in test_isa_oracle.py): after every seeded program the same SRAM, DRAM (size
+included) and 27 performance counters, bit for bit; the same errors; state kept across launches."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from llaccel_amd.device import GpuDevice
+from oracle.isa_np import FuncSimNp
+from tests import isa_cases as C
+
+pytestmark = pytest.mark.gpu
+CASES = C.cases()
+
+
+def _run(dev, img, pos):
+    dev.dram_write(0, img)
+    perf = dev.run(0, pos)
+    return perf, dev.sram_snapshot(), dev.dram_read(0, dev.dram_size())
+
+
+@pytest.mark.parametrize("cid,img,pos,fusion", CASES, ids=[c[0] for c in CASES])
+def test_device_equals_oracle(cid, img, pos, fusion):
+    print("case", cid, flush=True)
+    g = GpuDevice(0, fusion)
+    p1, s1, d1 = _run(g, img, pos)
+    p2, s2, d2 = _run(FuncSimNp(0, fusion), img, pos)
+    assert p1 == p2, [(i, a, b) for i, (a, b) in enumerate(zip(p1, p2)) if a != b]
+    assert s1 == s2, np.flatnonzero(np.frombuffer(s1, np.uint8) != np.frombuffer(s2, np.uint8))[:10]
+    assert len(d1) == len(d2) and d1 == d2
+
+
+@pytest.mark.parametrize("cid,img,pos,fusion,msg", C.error_cases(), ids=[c[0] for c in C.error_cases()])
+def test_device_errors_equal_oracle(cid, img, pos, fusion, msg):
+    g = GpuDevice(0, fusion)
+    g.dram_write(0, img)
+    with pytest.raises(RuntimeError, match=msg.replace("[", r"\[").replace("]", r"\]")):
+        g.run(0, pos)
+    # the device stays usable after an error (its SRAM keeps what the failed program wrote, so the
+    # next program's stored result and counters are compared)
+    ok = C.vec_case(np.random.default_rng(3), "ADD", 64)
+    p1, _, d1 = _run(g, ok, 0)
+    p2, _, d2 = _run(FuncSimNp(0, fusion), ok, 0)
+    assert p1 == p2 and d1[:len(ok)] == d2[:len(ok)]
+
+
+def test_state_persists_across_launches():
+    """One device, three launches of one KV_WRITE + ATTN program at positions 9, 10, 11 (the DRAM
+    K/V cache keeps every earlier launch's rows), against the oracle doing the same."""
+    img, _ = C.attn_case(np.random.default_rng(11), 1, 4, 2, 64, 9, True, max_seq=64)
+    g, o = GpuDevice(0, False), FuncSimNp(0, False)
+    g.dram_write(0, img)
+    o.dram_write(0, img)
+    for pos in (9, 10, 11):
+        assert g.run(0, pos) == o.run(0, pos)
+        assert g.sram_snapshot() == o.sram_snapshot()
+    assert g.dram_read(0, g.dram_size()) == o.dram_read(0, o.dram_size())
+
+
+def test_device_rejects_what_it_cannot_run_like_the_simulator():
+    """Operand layouts whose simulator result depends on its element order (an output partly
+    overlapping an input) or that the device does not map (a K/V head stride that is not a whole
+    number of rows) raise instead of computing something else."""
+    b = C.Builder()
+    b.emit("SILU", 0x0, 0x20, 64, 1 << 30, 30, 16)
+    g = GpuDevice(0, False)
+    g.dram_write(0, b.image())
+    with pytest.raises(RuntimeError, match="overlapping operands in VEC_SILU"):
+        g.run(0, 0)
+    b = C.Builder()
+    b.emit("ATTN", 0x0, 0x1000, C.DATA, C.DATA + 4096, 1, 1, 1, 64, 1040, 1, 0, 1, 0)
+    g.dram_write(0, b.image() + bytes(8192))
+    with pytest.raises(RuntimeError, match="kv_stride not a multiple of D"):
+        g.run(0, 0)
+    assert g.name() == "mi355x" and g.max_attention_head_dim() == 256

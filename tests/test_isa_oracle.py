@@ -1,0 +1,164 @@
+"""The instruction-set oracle (oracle/isa_np.py) against the reference's own functional simulator
+(runtime/src/funcsim.cpp compiled from the reference sources into oracle/_ref): the same DRAM,
+SRAM and 27 performance counters after every seeded program, the same error messages; and the
+`.llbin` container reader (llaccel_amd.device.Llbin, llbin.cpp) on containers built here."""
+from __future__ import annotations
+
+import ctypes
+import json
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle.isa_np import FuncSimNp
+from tests import isa_cases as C
+
+REF = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "libfuncsim_ref.so"
+
+
+class RefSim:
+    """ctypes front of oracle/funcsim_shim.cpp."""
+
+    def __init__(self, fusion: bool):
+        self.L = L = ctypes.CDLL(str(REF))
+        p, u64, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32
+        L.fs_create.restype = p
+        L.fs_create.argtypes = [u64, ctypes.c_int]
+        for n, a in dict(fs_destroy=[p], fs_write=[p, u64, p, u64], fs_read=[p, u64, p, u64], fs_size=[p],
+                         fs_run=[p, u32, u32, p], fs_sram=[p, p]).items():
+            getattr(L, n).argtypes = a
+        L.fs_size.restype = u64
+        L.fs_error.restype = ctypes.c_char_p
+        self.h = L.fs_create(0, int(fusion))
+
+    def _ok(self, rc):
+        if rc:
+            raise RuntimeError(self.L.fs_error().decode())
+
+    def dram_write(self, addr, b):
+        self._ok(self.L.fs_write(self.h, addr, ctypes.create_string_buffer(bytes(b), len(b)), len(b)))
+
+    def dram_read(self, addr, n):
+        buf = ctypes.create_string_buffer(n)
+        self._ok(self.L.fs_read(self.h, addr, buf, n))
+        return buf.raw
+
+    def dram_size(self):
+        return self.L.fs_size(self.h)
+
+    def run(self, pc, pos):
+        perf = (ctypes.c_uint64 * 27)()
+        self._ok(self.L.fs_run(self.h, pc, pos, perf))
+        return list(perf)
+
+    def sram_snapshot(self):
+        buf = ctypes.create_string_buffer(1 << 20)
+        self._ok(self.L.fs_sram(self.h, buf))
+        return buf.raw
+
+    def __del__(self):
+        self.L.fs_destroy(self.h)
+
+
+needs_ref = pytest.mark.skipif(not REF.exists(), reason="oracle/_ref/libfuncsim_ref.so not built (reference absent)")
+CASES = C.cases()
+
+
+def _run(dev, img, pos):
+    dev.dram_write(0, img)
+    perf = dev.run(0, pos)
+    return perf, dev.sram_snapshot(), dev.dram_read(0, dev.dram_size())
+
+
+@needs_ref
+@pytest.mark.parametrize("cid,img,pos,fusion", CASES, ids=[c[0] for c in CASES])
+def test_oracle_equals_reference_simulator(cid, img, pos, fusion):
+    ref = RefSim(fusion)
+    o = FuncSimNp(0, fusion)
+    p1, s1, d1 = _run(ref, img, pos)
+    p2, s2, d2 = _run(o, img, pos)
+    assert p1 == p2, [(i, a, b) for i, (a, b) in enumerate(zip(p1, p2)) if a != b]
+    assert s1 == s2
+    assert len(d1) == len(d2) and d1 == d2
+
+
+@needs_ref
+@pytest.mark.parametrize("cid,img,pos,fusion,msg", C.error_cases(), ids=[c[0] for c in C.error_cases()])
+def test_oracle_errors_equal_reference_simulator(cid, img, pos, fusion, msg):
+    for dev in (RefSim(fusion), FuncSimNp(0, fusion)):
+        dev.dram_write(0, img)
+        with pytest.raises(RuntimeError, match=msg.replace("[", r"\[").replace("]", r"\]")):
+            dev.run(0, pos)
+
+
+def test_oracle_plants_are_caught():
+    """A mistake planted in the oracle's GEMM (weights untiled transposed) changes its result on a
+    non-square case -- the parity test above would see it."""
+    img = C.gemm_case(np.random.default_rng(1), 2, 32, 64, 0)
+    good = _run(FuncSimNp(0, True), img, 0)[1]
+    import oracle.isa_np as I
+    orig = I.FuncSimNp._gemm
+
+    def planted(self, w):
+        w = list(w)
+        w[3] = w[3]  # same operands; transpose the tile bytes in SRAM first
+        wa, N, K = w[3], w[9], w[10]
+        t = np.frombuffer(bytes(self.sram[wa:wa + N * K]), np.int8).reshape(-1, 16, 16).transpose(0, 2, 1)
+        self.sram[wa:wa + N * K] = t.tobytes()
+        return orig(self, w)
+    I.FuncSimNp._gemm = planted
+    try:
+        bad = _run(FuncSimNp(0, True), img, 0)[1]
+    finally:
+        I.FuncSimNp._gemm = orig
+    assert bad != good
+
+
+# ---- .llbin container (llbin.cpp) ----
+def _container(sections):
+    hdr = struct.pack("<III", 0x4E424C4C, 2, len(sections))
+    off = 12 + 24 * len(sections)
+    table, body = b"", b""
+    for kind, flags, data in sections:
+        table += struct.pack("<IIQQ", kind, flags, off + len(body), len(data))
+        body += data
+    return hdr + table + body
+
+
+def _image():
+    prog = C.ins("NOP") + C.ins("HALT")
+    dram = prog + bytes(4096)
+    meta = {"programs": [{"M": 1, "pc": 0}], "model": {"head_dim": 64, "n_heads": 14, "n_kv_heads": 2,
+                                                       "max_seq": 512, "dim": 896},
+            "dram": {"kv_cache": [{"addr": 1024, "bytes": 2048}], "kv_cache_bytes": 2048}}
+    return dram, prog, meta
+
+
+def test_llbin_reader_accepts_a_valid_container():
+    from llaccel_amd.device import Llbin
+    dram, prog, meta = _image()
+    lb = Llbin.parse(_container([(1, 0, dram), (2, 1, prog), (3, 0, json.dumps(meta).encode())]))
+    p = lb.program_for_m(1)
+    assert p.pc == 0 and len(p.instrs) == 2 and lb.dram_image == dram and lb.meta["model"]["dim"] == 896
+    with pytest.raises(RuntimeError, match="no program compiled for M=4"):
+        lb.program_for_m(4)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda s: [(1, 0, s[0][2][:0])] + s[1:], "llbin has no DRAM image"),
+    (lambda s: s + [(2, 1, s[1][2])], "invalid or duplicate program shape"),
+    (lambda s: [s[0], (2, 1, s[1][2][:60]), s[2]], "program size not a multiple of 64"),
+    (lambda s: [s[0], s[1], (3, 0, json.dumps({"programs": []}).encode())], "program metadata count mismatch"),
+    (lambda s: [(1, 0, bytes(64) + s[0][2][64:]), s[1], s[2]], "program section differs from executable DRAM image"),
+    (lambda s: s + [(9, 0, b"")], "unknown section kind 9"),
+])
+def test_llbin_reader_rejects_like_the_reference(mutate, msg):
+    from llaccel_amd.device import Llbin
+    dram, prog, meta = _image()
+    secs = [(1, 0, dram), (2, 1, prog), (3, 0, json.dumps(meta).encode())]
+    with pytest.raises(RuntimeError, match=msg):
+        Llbin.parse(_container(mutate(secs)))
+    with pytest.raises(RuntimeError, match="bad llbin magic"):
+        Llbin.parse(b"XXXX" + _container(secs)[4:])
