@@ -279,3 +279,46 @@ def error_cases():
             ("bad-rq", bad_rq, 0, False, "invalid requantization table entry"),
             ("cp-opcode", bad_cp, 0, False, "invalid command processor opcode"),
             ("deadlock", sem_case(False), 0, False, "deadlock at pc=0x")]
+
+
+def toy_llbin(seed=5) -> bytes:
+    """A .llbin of a one-head toy model (vocab 48, dim 64, max_seq 32) with programs for M = 4 and
+    M = 1: input rows -> quant -> K/V cache write -> attention over the cache -> lm_head GEMM ->
+    logits rows, with the META entries the host loop reads (host.cpp:47-100)."""
+    rng = np.random.default_rng(seed)
+    V, Dm, S = 48, 64, 32
+    emb, inp, lg, wa, rqa, kc, vc = 0x4000, 0x6000, 0x7000, 0x8000, 0x9000, 0xA000, 0xA800
+    kvs = S * Dm
+
+    def program(M):
+        c = [ins("DMA_LOAD", 0x0, inp, M, 128, 128, 128),
+             ins("DMA_LOAD", 0x10000, wa, 1, V * Dm, V * Dm, V * Dm),
+             ins("DMA_LOAD", 0x20000, rqa, 1, V * 8, V * 8, V * 8),
+             ins("QUANT", 0x0, 0x1000, M * Dm, 1 << 28, 22),
+             ins("KV_WRITE", 0x1000, kc, M, 1, Dm, kvs),
+             ins("KV_WRITE", 0x1000, vc, M, 1, Dm, kvs),
+             ins("ATTN", 0x1000, 0x2000, kc, vc, M, 1, 1, Dm, kvs, 1 << 29, 30, 1 << 29, 36, flags=2),
+             ins("GEMM", 0x2000, 0x10000, 0x3000, 0x20000, 0, 0, M, V, Dm, 0, 0, 0),
+             ins("DMA_STORE", 0x3000, lg, M, V * 2, V * 2, 128),
+             ins("HALT")]
+        return b"".join(c)
+    p4, p1 = program(4), program(1)
+    dram = bytearray(0xB000)
+    dram[0:len(p4)] = p4
+    dram[0x1000:0x1000 + len(p1)] = p1
+    dram[emb:emb + V * 128] = _i16(rng.integers(-3000, 3000, (V, 64)))
+    dram[wa:wa + V * Dm] = tile_w(rng.integers(-128, 128, (V, Dm)))
+    dram[rqa:rqa + V * 8] = _i32(np.stack([rng.integers(1 << 24, 1 << 28, V), rng.integers(18, 26, V)], 1))
+    meta = {"programs": [{"M": 4, "pc": 0}, {"M": 1, "pc": 0x1000}],
+            "model": {"vocab": V, "dim": Dm, "max_seq": S, "head_dim": Dm, "n_heads": 1, "n_kv_heads": 1},
+            "dram": {"embedding": {"addr": emb, "row_bytes": 128}, "input": {"addr": inp, "row_bytes": 128},
+                     "logits": {"addr": lg, "row_bytes": 128},
+                     "kv_cache": [{"addr": kc, "bytes": kvs}, {"addr": vc, "bytes": kvs}], "kv_cache_bytes": 2 * kvs}}
+    import json
+    secs = [(1, 0, bytes(dram)), (2, 4, p4), (2, 1, p1), (3, 0, json.dumps(meta).encode())]
+    off = 12 + 24 * len(secs)
+    table, body = b"", b""
+    for kind, flags, data in secs:
+        table += struct.pack("<IIQQ", kind, flags, off + len(body), len(data))
+        body += data
+    return struct.pack("<III", 0x4E424C4C, 2, len(secs)) + table + body

@@ -75,3 +75,27 @@ def test_device_rejects_what_it_cannot_run_like_the_simulator():
     with pytest.raises(RuntimeError, match="kv_stride not a multiple of D"):
         g.run(0, 0)
     assert g.name() == "mi355x" and g.max_attention_head_dim() == 256
+
+
+def test_host_loop_on_gpu_equals_oracle(tmp_path):
+    """The reference's host loop (llaccel_amd.host.Host, host.cpp) on the GPU device: a toy .llbin
+    read from disk, two M = 4 prefill chunks and greedy M = 1 decode launches, twice (the KV cache
+    is cleared per generation) -- the same record as on the oracle, which verifies as MATCH."""
+    from llaccel_amd.device import Llbin
+    from llaccel_amd.host import Host, verify_against_golden
+    import json
+    path = tmp_path / "toy.llbin"
+    path.write_bytes(C.toy_llbin())
+    lb = Llbin.load(path)
+    prompt = [3, 17, 40, 9, 22, 5]
+    o = FuncSimNp(0, False)
+    o.name = lambda: "sim"
+    o.max_attention_head_dim = lambda: 256
+    want = Host(lb, o).generate_tokens(prompt, 9).to_json()
+    h = Host(lb, GpuDevice(0, False))
+    for _ in range(2):
+        r = h.generate_tokens(prompt, 9)
+        assert r.to_json() == want
+    g = tmp_path / "golden.json"
+    g.write_text(json.dumps(want))
+    assert verify_against_golden(r, g, out=lambda s: None)

@@ -162,3 +162,36 @@ def test_llbin_reader_rejects_like_the_reference(mutate, msg):
         Llbin.parse(_container(mutate(secs)))
     with pytest.raises(RuntimeError, match="bad llbin magic"):
         Llbin.parse(b"XXXX" + _container(secs)[4:])
+
+
+# ---- the host loop (host.cpp) over the oracle and the reference simulator ----
+def test_host_loop_on_oracle_equals_reference_simulator(tmp_path):
+    """llaccel_amd.host.Host (host.cpp) runs a toy .llbin -- two prefill chunks of M = 4, then greedy
+    M = 1 decode launches -- on the numpy oracle and on the reference simulator: identical records
+    (argmax, logits rows, per-launch counters); a second generation clears the KV cache first."""
+    if not REF.exists():
+        pytest.skip("oracle/_ref/libfuncsim_ref.so not built (reference absent)")
+    from llaccel_amd.device import Llbin
+    from llaccel_amd.host import Host, verify_against_golden
+    lb = Llbin.parse(C.toy_llbin())
+    prompt = [3, 17, 40, 9, 22, 5]
+    recs = []
+    for dev in (RefSim(False), FuncSimNp(0, False)):
+        dev.name = lambda: "sim"
+        dev.max_attention_head_dim = lambda: 256
+        h = Host(lb, dev)
+        r1 = h.generate_tokens(prompt, 7).to_json()
+        r2 = h.generate_tokens(prompt, 7).to_json()
+        assert r1 == r2
+        recs.append(r1)
+    assert recs[0] == recs[1]
+    assert [s["M"] for s in recs[0]["steps"]] == [4, 4] + [1] * 7 and len(recs[0]["generated"]) == 7
+    g = tmp_path / "golden.json"
+    g.write_text(json.dumps(recs[0]))
+    lines = []
+    r = h.generate_tokens(prompt, 7)
+    assert verify_against_golden(r, g, verbose=True, out=lines.append) and lines[-1].startswith("VERIFY: MATCH")
+    r.steps[3].logits[5] += 1
+    lines.clear()
+    assert not verify_against_golden(r, g, out=lines.append)
+    assert lines[0].startswith("VERIFY: step 3 logits differ at index 5") and "MISMATCH" in lines[-1]
