@@ -268,6 +268,69 @@ def quantizer_bench(cpu_rows: int = 2048) -> dict:
     return out
 
 
+def isa_device_bench() -> dict:
+    """The instruction-set device (llaccel_amd.device.GpuDevice) on a compiled-style M = 1 decode
+    step of the Qwen2.5-0.5B shape (llaccel_amd.isa_synth.decoder_program: 24 layers, weights
+    streamed into the 1 MiB SRAM in N-chunks, chunked lm_head; ~3200 instructions): wall time per
+    run() after one warm-up run.  CPU baseline: the reference's own functional simulator
+    (runtime/src/funcsim.cpp compiled into oracle/_ref) on the same program, one run, checked equal
+    to the GPU's logits and counters; without it, oracle/isa_np.py on a one-layer program."""
+    import ctypes
+
+    from llaccel_amd import isa_synth
+    from llaccel_amd.device import GpuDevice
+
+    img, pc, pos, meta = isa_synth.decoder_program(seed=3)
+    dev = GpuDevice(0, True)
+    dev.dram_write(0, img)
+    perf = dev.run(pc, pos)
+    t = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        dev.run(pc, pos)
+        t.append(time.perf_counter() - t0)
+    gpu_s = min(t)
+    logits = dev.dram_read(meta["logits"], meta["vocab"] * 2)
+    out = {"program": "compiled-style decode step, Qwen2.5-0.5B shape (synthetic weights)",
+           "instructions": meta["instructions"], "dram_bytes": len(img), "gpu_ms_per_run": round(gpu_s * 1e3, 2),
+           "gpu_instr_per_s": round(meta["instructions"] / gpu_s, 1),
+           "gemm_macs_per_run": perf[6] * 256}
+    del dev
+    ref = Path(__file__).resolve().parent / "oracle" / "_ref" / "libfuncsim_ref.so"
+    if ref.exists():
+        L = ctypes.CDLL(str(ref))
+        L.fs_create.restype = ctypes.c_void_p
+        L.fs_create.argtypes = [ctypes.c_uint64, ctypes.c_int]
+        L.fs_write.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_char_p, ctypes.c_uint64]
+        L.fs_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64]
+        L.fs_run.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+        L.fs_destroy.argtypes = [ctypes.c_void_p]
+        h = L.fs_create(0, 1)
+        L.fs_write(h, 0, img, len(img))
+        cperf = (ctypes.c_uint64 * 27)()
+        t0 = time.perf_counter()
+        rc = L.fs_run(h, pc, pos, cperf)
+        cdt = time.perf_counter() - t0
+        buf = ctypes.create_string_buffer(meta["vocab"] * 2)
+        L.fs_read(h, meta["logits"], buf, meta["vocab"] * 2)
+        L.fs_destroy(h)
+        same = rc == 0 and buf.raw == logits and list(cperf) == perf
+        out["cpu_baseline"] = {"ms_per_run": round(cdt * 1e3, 1), "cores": 1, "kind": "reference",
+                               "sample": f"the same program, one run on the reference functional simulator; logits "
+                                         f"and counters equal to the GPU's: {same}"}
+    else:
+        from oracle.isa_np import FuncSimNp
+        img1, pc1, pos1, meta1 = isa_synth.decoder_program(layers=1, seed=3)
+        o = FuncSimNp(0, True)
+        o.dram_write(0, img1)
+        t0 = time.perf_counter()
+        o.run(pc1, pos1)
+        out["cpu_baseline"] = {"ms_per_run": round((time.perf_counter() - t0) * 1e3, 1), "cores": 1, "kind": "port",
+                               "sample": f"one-layer program ({meta1['instructions']} instructions), numpy restatement"}
+    out["speedup_vs_cpu"] = round(out["cpu_baseline"]["ms_per_run"] / out["gpu_ms_per_run"], 1)
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -280,6 +343,7 @@ def main() -> None:
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-config5", action="store_true", help="skip the Qwen3 T=4096 decode timing")
     ap.add_argument("--no-quant", action="store_true", help="skip the weight-quantization kernel timing")
+    ap.add_argument("--no-isa", action="store_true", help="skip the instruction-set device timing")
     ap.add_argument("--batch", type=int, default=16, help="also time config 4's batch decode (1 = skip)")
     ap.add_argument("--profile", choices=("decode", "copy", "prefill", "gemm", "quant"),
                     help="workload-only runs for rocprofv3")
@@ -458,6 +522,8 @@ def main() -> None:
         extra["gemm_sweep"] = gemm_sweep()
     if not args.no_quant:
         extra["quantize_rows_i8"] = quantizer_bench()
+    if not args.no_isa:
+        extra["isa_device"] = isa_device_bench()
         log("quantize", extra["quantize_rows_i8"])
 
     line = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,

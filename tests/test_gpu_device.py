@@ -99,3 +99,16 @@ def test_host_loop_on_gpu_equals_oracle(tmp_path):
     g = tmp_path / "golden.json"
     g.write_text(json.dumps(want))
     assert verify_against_golden(r, g, out=lambda s: None)
+
+
+@pytest.mark.parametrize("shape", [dict(dim=64, heads=4, kv_heads=2, head_dim=16, ffn=192, vocab=1008, layers=2,
+                                        max_seq=64, pos=20),
+                                   dict(dim=256, heads=4, kv_heads=1, head_dim=64, ffn=1024, vocab=4096, layers=1,
+                                        max_seq=256, pos=200)])
+def test_synthetic_decoder_program_equals_oracle(shape):
+    """A compiled-style decode step (llaccel_amd.isa_synth: chunked weight streaming, every op of a
+    decoder layer, chunked lm_head) on the GPU device and on the oracle: same counters, SRAM, DRAM."""
+    from llaccel_amd import isa_synth
+    img, pc, pos, meta = isa_synth.decoder_program(**shape, seed=2)
+    print("program", shape, meta["instructions"], flush=True)
+    assert _run(GpuDevice(0, True), img, pos) == _run(FuncSimNp(0, True), img, pos)

@@ -195,3 +195,15 @@ def test_host_loop_on_oracle_equals_reference_simulator(tmp_path):
     lines.clear()
     assert not verify_against_golden(r, g, out=lines.append)
     assert lines[0].startswith("VERIFY: step 3 logits differ at index 5") and "MISMATCH" in lines[-1]
+
+
+def test_synthetic_decoder_program_oracle_equals_reference_simulator():
+    """llaccel_amd.isa_synth's compiled-style decode step (two layers of small shape): the oracle
+    and the reference simulator agree on counters, SRAM and DRAM."""
+    if not REF.exists():
+        pytest.skip("oracle/_ref/libfuncsim_ref.so not built (reference absent)")
+    from llaccel_amd import isa_synth
+    img, pc, pos, meta = isa_synth.decoder_program(dim=64, heads=4, kv_heads=2, head_dim=16, ffn=192, vocab=1008,
+                                                   layers=2, max_seq=64, pos=20, seed=1)
+    r, o = RefSim(True), FuncSimNp(0, True)
+    assert _run(r, img, pos) == _run(o, img, pos)
