@@ -8,7 +8,7 @@
 // signalled enough -- checks each instruction as the simulator does (same conditions, same
 // messages), accumulates the same performance counters (functions of the operands and POS only) and
 // enqueues the instruction's kernels on one stream: DMA and KV_WRITE as strided copies, GEMM as the
-// tiled-weight relayout + llhip_linear, the VEC ops and ATTN through the datapath's own kernels.
+// tiled-weight relayout (with the requant-table check) + llhip_linear, the VEC ops and ATTN through the datapath's own kernels.
 // Data-dependent faults (an invalid requant table entry) are flagged on the device and reported once
 // the program has drained.
 #include <cstring>
@@ -99,19 +99,18 @@ __global__ void copy_rows_ordered(uint8_t* dst, const uint8_t* src, uint32_t row
   }
 }
 // GEMM weights: tile (nt, kt) of 16x16 bytes at w + (nt*KT + kt)*256, byte n*16 + k = W[nt*16+n][kt*16+k]
-// (docs/ISA.md "GEMM details") -> row-major W [N][K]
-__global__ void untile_w(const uint8_t* __restrict__ w, int8_t* __restrict__ out, uint32_t N, uint32_t K) {
+// (docs/ISA.md "GEMM details") -> row-major W [N][K]; the first N threads also check the requant
+// table entries {M_n, S_n}: M_n >= 0 and S_n in [0, 63] (funcsim.cpp:214), else status flag 1
+__global__ void untile_w(const uint8_t* __restrict__ w, int8_t* __restrict__ out, uint32_t N, uint32_t K,
+                         const int32_t* __restrict__ rq, int32_t* status) {
   const uint64_t n_all = (uint64_t)N * K;
   const uint32_t KT = K / 16;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_all; i += (uint64_t)gridDim.x * blockDim.x) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < N && (rq[2 * t] < 0 || rq[2 * t + 1] < 0 || rq[2 * t + 1] > 63)) atomicOr(status, 1);
+  for (uint64_t i = t; i < n_all; i += (uint64_t)gridDim.x * blockDim.x) {
     const uint32_t n = (uint32_t)(i / K), k = (uint32_t)(i % K);
     out[i] = (int8_t)w[((uint64_t)(n / 16) * KT + k / 16) * 256 + (n % 16) * 16 + k % 16];
   }
-}
-// requant table entries {M_n, S_n}: M_n >= 0 and S_n in [0, 63] (funcsim.cpp:214), else flag 1
-__global__ void check_rq(const int32_t* __restrict__ rq, uint32_t N, int32_t* status) {
-  const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n < N && (rq[2 * n] < 0 || rq[2 * n + 1] < 0 || rq[2 * n + 1] > 63)) atomicOr(status, 1);
 }
 // RoPE rows p = pos + m of the SRAM table [cos D/2][sin D/2] (row stride `stride` bytes) gathered
 // into cos/sin [M][D/2]
@@ -321,9 +320,9 @@ struct Device {
     perf[P_GEMM_EPI] += uint64_t(NT) * M;
     perf[P_GEMM_BUSY] += uint64_t(NT) * KT * (1 + M) + uint64_t(NT) * M;
 
-    hipLaunchKernelGGL(check_rq, dim3(ceil_div(N, 256)), dim3(256), 0, stream,
-                       reinterpret_cast<const int32_t*>(sram + rq), N, status);
-    hipLaunchKernelGGL(untile_w, dim3(grid_for(uint64_t(N) * K)), dim3(256), 0, stream, sram + w, wrm, N, K);
+    // grid_for(N*K) >= ceil(N/256) blocks (K >= 16), so every table entry has a thread
+    hipLaunchKernelGGL(untile_w, dim3(grid_for(uint64_t(N) * K)), dim3(256), 0, stream, sram + w, wrm, N, K,
+                       reinterpret_cast<const int32_t*>(sram + rq), status);
     hip_ok(hipGetLastError(), "kernel launch");
     uint8_t* dst = inplace ? scratch : sram + out;
     rc_ok(llhip_linear(reinterpret_cast<const int8_t*>(sram + a), M, K, K, wrm, N,
