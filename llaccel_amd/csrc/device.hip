@@ -90,6 +90,26 @@ __global__ void copy_rows8(uint8_t* __restrict__ dst, const uint8_t* __restrict_
     dst[r * ds + b] = src[r * ss + b];
   }
 }
+// up to kBatch independent aligned copies in one launch (blockIdx.y = copy): consecutive DMA
+// instructions that neither read nor write what another one of the batch writes
+constexpr int kBatch = 8;
+struct CopyBatch {
+  uint8_t* dst[kBatch];
+  const uint8_t* src[kBatch];
+  uint32_t rows[kBatch], units[kBatch];
+  uint64_t ss[kBatch], ds[kBatch];
+};
+__global__ void copy_batch16(CopyBatch b) {
+  const int c = blockIdx.y;
+  const uint32_t units = b.units[c];
+  const uint64_t n = (uint64_t)b.rows[c] * units;
+  uint8_t* dst = b.dst[c];
+  const uint8_t* src = b.src[c];
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t r = i / units, u = i % units;
+    *reinterpret_cast<uint4*>(dst + r * b.ds[c] + 16 * u) = *reinterpret_cast<const uint4*>(src + r * b.ss[c] + 16 * u);
+  }
+}
 // destination rows that overlap each other: rows in order, one workgroup (later rows win)
 __global__ void copy_rows_ordered(uint8_t* dst, const uint8_t* src, uint32_t rows, uint32_t bytes, uint64_t ss,
                                   uint64_t ds) {
@@ -184,6 +204,7 @@ struct Device {
   void grow(uint64_t n) {
     if (n <= size) return;
     if (n > cap) {
+      flush();
       const uint64_t ncap = std::max<uint64_t>((n + (1u << 20) - 1) & ~uint64_t((1u << 20) - 1), 2 * cap);
       uint8_t* nd = nullptr;
       hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
@@ -232,6 +253,67 @@ struct Device {
     return true;
   }
 
+  // queued DMA copies: offsets (the DRAM may move when it grows) and the byte ranges they touch
+  struct Pending {
+    bool load;
+    uint64_t sram_off, dram_off, rows, bytes, ss, ds;
+    uint64_t span(uint64_t stride) const { return (rows - 1) * stride + bytes; }
+  };
+  std::vector<Pending> pend;
+
+  void flush() {
+    if (pend.empty()) return;
+    CopyBatch b{};
+    uint64_t most = 0;
+    for (size_t i = 0; i < pend.size(); ++i) {
+      const Pending& q = pend[i];
+      b.dst[i] = q.load ? sram + q.sram_off : dram + q.dram_off;
+      b.src[i] = q.load ? dram + q.dram_off : sram + q.sram_off;
+      b.rows[i] = (uint32_t)q.rows;
+      b.units[i] = (uint32_t)(q.bytes / 16);
+      b.ss[i] = q.ss;
+      b.ds[i] = q.ds;
+      most = std::max<uint64_t>(most, q.rows * q.bytes / 16);
+    }
+    const int n = (int)pend.size();
+    pend.clear();
+    hipLaunchKernelGGL(copy_batch16, dim3(grid_for(most), n), dim3(256), 0, stream, b);
+    hip_ok(hipGetLastError(), "kernel launch");
+  }
+
+  // a DMA joins the batch when it is aligned, its rows do not overlap, and it neither writes what a
+  // queued copy reads or writes nor reads what a queued copy writes
+  void queue_dma(bool load, uint64_t sramA, uint64_t dramA, uint64_t rows, uint64_t bytes, uint64_t ss, uint64_t ds) {
+    if (!rows || !bytes) return;
+    Pending q{load, sramA, dramA, rows, bytes, ss, ds};
+    const bool ok = (rows == 1 || ds >= bytes) && ((uintptr_t)dram | sramA | dramA | ss | ds | bytes) % 16 == 0;
+    if (!ok) {
+      flush();
+      if (load)
+        copy(sram + sramA, dram + dramA, (uint32_t)rows, (uint32_t)bytes, ss, ds);
+      else
+        copy(dram + dramA, sram + sramA, (uint32_t)rows, (uint32_t)bytes, ss, ds);
+      return;
+    }
+    // ranges: [lo, lo + span) in SRAM (sram side) or DRAM (dram side)
+    const uint64_t q_dst_lo = load ? sramA : dramA, q_src_lo = load ? dramA : sramA;
+    const uint64_t q_dst_n = q.span(ds), q_src_n = q.span(ss);
+    for (const Pending& o : pend) {
+      const uint64_t o_dst_lo = o.load ? o.sram_off : o.dram_off, o_src_lo = o.load ? o.dram_off : o.sram_off;
+      const uint64_t o_dst_n = o.span(o.ds), o_src_n = o.span(o.ss);
+      // same memory when both destinations are SRAM (both loads) or both DRAM (both stores), etc.
+      const bool dd = (o.load == load) && overlap(q_dst_lo, q_dst_n, o_dst_lo, o_dst_n);
+      const bool ds_ = (o.load != load) && overlap(q_dst_lo, q_dst_n, o_src_lo, o_src_n);
+      const bool sd = (o.load != load) && overlap(q_src_lo, q_src_n, o_dst_lo, o_dst_n);
+      if (dd || ds_ || sd) {
+        flush();
+        break;
+      }
+    }
+    pend.push_back(q);
+    if ((int)pend.size() == kBatch) flush();
+  }
+
   void copy(uint8_t* dst, const uint8_t* src, uint32_t rows, uint32_t bytes, uint64_t ss, uint64_t ds) {
     if (!rows || !bytes) return;
     if (rows > 1 && ds < bytes) {
@@ -277,10 +359,7 @@ struct Device {
     perf[load ? P_SRAM_WR : P_SRAM_RD] += load ? bytes : sramReadBytes;
     perf[load ? P_DRAM_RD : P_DRAM_WR] += beats * 64;
     perf[P_DMA_BUSY] += beats;
-    if (load)
-      copy(sram + sramA, dram + dramA, rows, rowBytes, srcStride, dstStride);
-    else
-      copy(dram + dramA, sram + sramA, rows, rowBytes, srcStride, dstStride);
+    queue_dma(load, sramA, dramA, rows, rowBytes, srcStride, dstStride);
   }
 
   void gemm(const uint32_t* in) {
@@ -529,6 +608,7 @@ struct Device {
       case OP_ATTN: shift(in[12]); shift(in[14]); break;
       default: break;
     }
+    if (op != OP_DMA_LOAD && op != OP_DMA_STORE) flush();
     switch (op) {
       case OP_DMA_LOAD: return dma(in, true);
       case OP_DMA_STORE: return dma(in, false);
@@ -547,6 +627,19 @@ struct Device {
 
   // Fetches, checks and executes instructions from `pc` until HALT (funcsim.cpp:41-107, sequential).
   void run(uint32_t pc, uint32_t p) {
+    pend.clear();
+    try {
+      run_program(pc, p);
+    } catch (...) {
+      try {
+        flush();  // the DMAs before a failing instruction have happened, as in the simulator
+      } catch (...) {
+      }
+      throw;
+    }
+  }
+
+  void run_program(uint32_t pc, uint32_t p) {
     std::memset(perf, 0, sizeof perf);
     std::memset(sem, 0, sizeof sem);
     pos = p;
@@ -556,6 +649,7 @@ struct Device {
     for (;;) {
       if (fetchPc + kInstr > size) bad("instruction fetch out of DRAM range");
       if (window.empty() || fetchPc < wbase || fetchPc + kInstr > wbase + window.size() * 4) {
+        flush();
         const uint64_t n = std::min<uint64_t>(1024 * kInstr, (size - fetchPc) / kInstr * kInstr);
         window.assign(n / 4, 0);
         wbase = fetchPc;
@@ -583,6 +677,7 @@ struct Device {
       }
       if (ss != kNoSem) sem[ss]++;
     }
+    flush();
     int32_t st = 0;
     hip_ok(hipMemcpyAsync(&st, status, 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
     hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");

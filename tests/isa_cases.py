@@ -182,6 +182,25 @@ def dma_case(rng):
     return b.image()
 
 
+def dma_chain_case(rng):
+    """Consecutive aligned DMAs that depend on each other (the GPU device batches independent
+    ones): store of what a load just wrote, load of what a store just wrote, two loads into
+    overlapping SRAM (the later wins), and more than eight independent loads in a row."""
+    b = Builder()
+    a = b.blob(rng.integers(0, 256, 2048).astype(np.uint8).tobytes())
+    c = b.blob(rng.integers(0, 256, 2048).astype(np.uint8).tobytes())
+    scratch = b.blob(bytes(4096))
+    b.emit("DMA_LOAD", 0x0, a, 4, 256, 256, 256)
+    b.emit("DMA_STORE", 0x0, scratch, 2, 512, 512, 512)
+    b.emit("DMA_LOAD", 0x2000, scratch + 256, 1, 512, 512, 512)
+    b.emit("DMA_LOAD", 0x3000, a, 1, 1024, 1024, 1024)
+    b.emit("DMA_LOAD", 0x3200, c, 1, 1024, 1024, 1024)
+    for i in range(10):
+        b.emit("DMA_LOAD", 0x8000 + 0x400 * i, c + 128 * i, 2, 64, 64, 128)
+    b.emit("DMA_STORE", 0x3000, scratch + 1024, 1, 1536, 1536, 1536)
+    return b.image()
+
+
 def sem_case(ok=True):
     """NOPs and ops that signal and wait on semaphores; ok=False waits for a count never reached."""
     b = Builder()
@@ -242,6 +261,7 @@ def cases():
     img, p = attn_case(rng, 2, 2, 2, 64, 9, True, inplace=True)
     out.append(("attn-inplace", img, p, False))
     out.append(("dma", dma_case(rng), 0, False))
+    out.append(("dma-chain", dma_chain_case(rng), 0, False))
     out.append(("semaphores", sem_case(True), 0, False))
     out.append(("chain", chain_case(rng), 0, True))
     return out
