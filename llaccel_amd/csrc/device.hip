@@ -7,8 +7,8 @@
 // before the next one issues, so a semaphore wait is satisfied exactly when earlier instructions
 // signalled enough -- checks each instruction as the simulator does (same conditions, same
 // messages), accumulates the same performance counters (functions of the operands and POS only) and
-// enqueues the instruction's kernels on one stream: DMA and KV_WRITE as strided copies, GEMM as the
-// tiled-weight relayout (with the requant-table check) + llhip_linear, the VEC ops and ATTN through the datapath's own kernels.
+// enqueues the instruction's kernels on one stream: DMA and KV_WRITE as strided copies, GEMM as one
+// kernel over the SRAM weight tiles, the VEC ops and ATTN through the datapath's own kernels.
 // Data-dependent faults (an invalid requant table entry) are flagged on the device and reported once
 // the program has drained.
 #include <cstring>
@@ -118,19 +118,75 @@ __global__ void copy_rows_ordered(uint8_t* dst, const uint8_t* src, uint32_t row
     __syncthreads();
   }
 }
-// GEMM weights: tile (nt, kt) of 16x16 bytes at w + (nt*KT + kt)*256, byte n*16 + k = W[nt*16+n][kt*16+k]
-// (docs/ISA.md "GEMM details") -> row-major W [N][K]; the first N threads also check the requant
-// table entries {M_n, S_n}: M_n >= 0 and S_n in [0, 63] (funcsim.cpp:214), else status flag 1
-__global__ void untile_w(const uint8_t* __restrict__ w, int8_t* __restrict__ out, uint32_t N, uint32_t K,
-                         const int32_t* __restrict__ rq, int32_t* status) {
-  const uint64_t n_all = (uint64_t)N * K;
-  const uint32_t KT = K / 16;
-  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < N && (rq[2 * t] < 0 || rq[2 * t + 1] < 0 || rq[2 * t + 1] > 63)) atomicOr(status, 1);
-  for (uint64_t i = t; i < n_all; i += (uint64_t)gridDim.x * blockDim.x) {
-    const uint32_t n = (uint32_t)(i / K), k = (uint32_t)(i % K);
-    out[i] = (int8_t)w[((uint64_t)(n / 16) * KT + k / 16) * 256 + (n % 16) * 16 + k % 16];
+// GEMM straight from the SRAM weight tiles, M <= 16 (funcsim.cpp:192-241): one workgroup per
+// 16-column tile nt.  Tile (nt, kt) holds rows nt*16..+16 x columns kt*16..+16 of W as 16 rows of
+// 16 bytes; thread t takes row n = t % 16 of tiles kt = t/16, t/16 + 16, ... (16-byte loads) and
+// dot products them with the A rows' matching 16 bytes; the 16 partial sums of each (row, column)
+// are added through LDS, and thread t = m*16 + n applies the bias, requant and epilogue of output
+// (m, nt*16 + n).  A requant entry outside M_n >= 0, S_n in [0, 63] sets status flag 1 and leaves
+// the column unwritten.
+struct IsaGemm {
+  const int8_t* A;
+  const uint8_t* W;
+  const int32_t* rq;
+  const int32_t* bias;  // or null
+  const int16_t* aux;   // resadd / mul, or null
+  void* out;
+  int32_t* status;
+  uint32_t M, N, K, Mi;
+  int mode, out_i8, aux_shift, Si, sh;
+};
+__global__ __launch_bounds__(256) void isa_gemm(IsaGemm g) {
+  __shared__ int32_t part[16][16][17];  // [k group][row][column]
+  const uint32_t nt = blockIdx.x, t = threadIdx.x, n = t & 15, q = t >> 4;
+  const uint32_t KT = g.K / 16;
+  int32_t acc[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) acc[m] = 0;
+#pragma unroll 2
+  for (uint32_t kt = q; kt < KT; kt += 16) {
+    const int4 w = *reinterpret_cast<const int4*>(g.W + ((uint64_t)nt * KT + kt) * 256 + n * 16);
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      if (m < (int)g.M) {
+        const int4 a = *reinterpret_cast<const int4*>(g.A + (uint64_t)m * g.K + kt * 16);
+        int32_t s = acc[m];
+        s = __builtin_amdgcn_sdot4(a.x, w.x, s, false);
+        s = __builtin_amdgcn_sdot4(a.y, w.y, s, false);
+        s = __builtin_amdgcn_sdot4(a.z, w.z, s, false);
+        acc[m] = __builtin_amdgcn_sdot4(a.w, w.w, s, false);
+      }
+    }
   }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) part[q][m][n] = acc[m];
+  __syncthreads();
+  const uint32_t m = t >> 4;
+  if (m >= g.M) return;
+  int32_t sum = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sum += part[k][m][n];
+  const uint32_t ch = nt * 16 + n;
+  const int32_t Mn = g.rq[2 * ch], Sn = g.rq[2 * ch + 1];
+  if (Mn < 0 || Sn < 0 || Sn > 63) {
+    atomicOr(g.status, 1);
+    return;
+  }
+  const int64_t v = (int64_t)sum + (g.bias ? g.bias[ch] : 0);
+  const uint64_t o = (uint64_t)m * g.N + ch;
+  if (g.out_i8) {
+    static_cast<int8_t*>(g.out)[o] = (int8_t)sat8(mulshift(v, Mn, Sn));
+    return;
+  }
+  const int64_t tq = sat16(mulshift(v, Mn, Sn));
+  int64_t y = tq;
+  if (g.mode == 1)
+    y = sat16(tq + g.aux[o]);
+  else if (g.mode == 2)
+    y = silu16(tq, g.Mi, g.Si, g.sh);
+  else if (g.mode == 3)
+    y = sat16(rshr(tq * g.aux[o], g.aux_shift));
+  static_cast<int16_t*>(g.out)[o] = (int16_t)y;
 }
 // RoPE rows p = pos + m of the SRAM table [cos D/2][sin D/2] (row stride `stride` bytes) gathered
 // into cos/sin [M][D/2]
@@ -168,7 +224,6 @@ struct Device {
   uint64_t cap = 0, size = 0;  // allocation (without the pad) and the simulator's DRAM size
   uint8_t* sram = nullptr;
   uint8_t* scratch = nullptr;  // results of ops whose output aliases an input, copied back after
-  int8_t* wrm = nullptr;       // row-major GEMM weights
   int16_t* rope_tab = nullptr;
   void* ws = nullptr;
   int32_t* status = nullptr;
@@ -180,7 +235,7 @@ struct Device {
 
   ~Device() {
     if (stream) (void)hipStreamSynchronize(stream);
-    for (void* p : {(void*)dram, (void*)sram, (void*)scratch, (void*)wrm, (void*)rope_tab, ws, (void*)status})
+    for (void* p : {(void*)dram, (void*)sram, (void*)scratch, (void*)rope_tab, ws, (void*)status})
       if (p) (void)hipFree(p);
     if (stream) (void)hipStreamDestroy(stream);
   }
@@ -190,7 +245,6 @@ struct Device {
     hip_ok(hipStreamCreate(&stream), "hipStreamCreate");
     hip_ok(hipMalloc(&sram, kSram), "hipMalloc");
     hip_ok(hipMalloc(&scratch, kSram), "hipMalloc");
-    hip_ok(hipMalloc(&wrm, kSram), "hipMalloc");
     hip_ok(hipMalloc(&rope_tab, 2 * kTM * 128 * sizeof(int16_t)), "hipMalloc");
     hip_ok(hipMalloc(&ws, (size_t)llhip_workspace_bytes()), "hipMalloc");
     hip_ok(hipMalloc(&status, 4), "hipMalloc");
@@ -399,16 +453,13 @@ struct Device {
     perf[P_GEMM_EPI] += uint64_t(NT) * M;
     perf[P_GEMM_BUSY] += uint64_t(NT) * KT * (1 + M) + uint64_t(NT) * M;
 
-    // grid_for(N*K) >= ceil(N/256) blocks (K >= 16), so every table entry has a thread
-    hipLaunchKernelGGL(untile_w, dim3(grid_for(uint64_t(N) * K)), dim3(256), 0, stream, sram + w, wrm, N, K,
-                       reinterpret_cast<const int32_t*>(sram + rq), status);
-    hip_ok(hipGetLastError(), "kernel launch");
     uint8_t* dst = inplace ? scratch : sram + out;
-    rc_ok(llhip_linear(reinterpret_cast<const int8_t*>(sram + a), M, K, K, wrm, N,
-                       reinterpret_cast<const int32_t*>(sram + rq),
-                       hasBias ? reinterpret_cast<const int32_t*>(sram + bias) : nullptr, (int)mode,
-                       useAux ? reinterpret_cast<const int16_t*>(sram + aux) : nullptr, N, auxShift, siluMi, siluSi,
-                       siluSh, outI8 ? 1 : 0, dst, N, ws, stream));
+    IsaGemm g{reinterpret_cast<const int8_t*>(sram + a), sram + w, reinterpret_cast<const int32_t*>(sram + rq),
+              hasBias ? reinterpret_cast<const int32_t*>(sram + bias) : nullptr,
+              useAux ? reinterpret_cast<const int16_t*>(sram + aux) : nullptr, dst, status, M, N, K, siluMi,
+              (int)mode, outI8 ? 1 : 0, (int)auxShift, (int)siluSi, (int)siluSh};
+    hipLaunchKernelGGL(isa_gemm, dim3(NT), dim3(256), 0, stream, g);
+    hip_ok(hipGetLastError(), "kernel launch");
     if (inplace) copy(sram + out, scratch, 1, (uint32_t)on, 0, 0);
   }
 
