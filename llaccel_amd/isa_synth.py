@@ -6,12 +6,11 @@ the down projection with the residual add; then the final RMSNorm and the lm_hea
 in DRAM in the ISA's 16x16-tile layout and stream into SRAM with DMA_LOAD in N-chunks that fit the
 1 MiB SRAM beside the activations, one GEMM per chunk, as a compiler for this SRAM must.  Values
 are seeded random integers (requant tables and normalisation constants in the ranges the quantizer
-produces), so the programs measure the device and are checked device-against-oracle; they are not
+produces), so the programs measure the device and check it against the CPU restatement; they are not
 a trained model.
 """
 from __future__ import annotations
 
-import json
 import struct
 
 import numpy as np
@@ -52,8 +51,9 @@ class _Image:
 
 def decoder_program(dim=896, heads=14, kv_heads=2, head_dim=64, ffn=4864, vocab=151936, layers=24, max_seq=1024,
                     pos=512, seed=0):
-    """(DRAM image, entry pc, POS) of one M = 1 decode step.  The K/V caches hold seeded keys and
-    values for positions 0..pos-1."""
+    """(DRAM image, entry pc, POS, meta) of one M = 1 decode step; meta gives the instruction count
+    and the logits buffer's DRAM address and length.  The K/V caches hold seeded keys and values for
+    every position."""
     rng = np.random.default_rng(seed)
     D, Hq, Hkv = head_dim, heads, kv_heads
     code: list[bytes] = []
@@ -135,7 +135,3 @@ def decoder_program(dim=896, heads=14, kv_heads=2, head_dim=64, ffn=4864, vocab=
     assert len(prog) <= img.base, "program exceeds its region"
     meta = {"instructions": len(code), "logits": logits, "vocab": vocab}
     return prog + bytes(img.base - len(prog)) + bytes(img.data), 0, pos, meta
-
-
-def describe(meta) -> str:
-    return json.dumps(meta)
