@@ -22,11 +22,13 @@ The JSON line also carries
                  per-family decode timings, config 4 at batch 16, config 5 (Qwen3 shape, T = 4096)
                  decode launch time, config-2 GEMM TOPS and GB/s (weights rotated through copies
                  larger than the memory-side cache), the qgraph producer's weight conversion
-                 (llhip_quant_rows_i8, lm_head-shaped f32) against HBM and its numpy baseline.
+                 (llhip_quant_rows_i8, lm_head-shaped f32) against HBM and its numpy baseline,
+                 and the instruction-set device running a compiled-style Qwen2.5-0.5B-shaped
+                 decode step beside the reference's functional simulator on one host core.
 
     python bench.py [--gpus 1] [--steps 64] [--warmup 8]
     python bench.py --profile decode   # prefill + decode launches only (for rocprofv3)
-    python bench.py --profile prefill  # prefill() once, then three one-launch 512-row prefills
+    python bench.py --profile prefill  # prefill() once, eager, captured and replayed 512-row prefills
     python bench.py --profile gemm     # config 2's M=2048 x K=896 x N=151936 GEMM, 7 launches
     python bench.py --profile copy     # 256 MiB device copies (counter calibration)
     python bench.py --profile quant    # llhip_quant_rows_i8 on a 151936 x 896 f32 matrix, 7 launches
