@@ -265,7 +265,7 @@ int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream);
  * A device holding the ISA's DRAM and 1 MiB SRAM in GPU memory that runs .llbin programs (docs/ISA.md,
  * binary version 2) with the functional simulator's semantics and performance counters.  Errors
  * (the simulator's runtime_error conditions, with its messages) return a negative errno with the
- * message in llhip_last_error(). */
+ * message in llhip_last_error().  Calls on one device must not overlap (one host thread at a time). */
 typedef struct llhip_device llhip_device;
 #define LLHIP_DEV_NUM_PERF 27
 

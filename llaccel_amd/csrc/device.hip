@@ -314,6 +314,13 @@ struct Device {
     uint64_t span(uint64_t stride) const { return (rows - 1) * stride + bytes; }
   };
   std::vector<Pending> pend;
+  // the DRAM range of the fetched instruction window: a DRAM write into it refetches the window,
+  // so a program that stores over its own later instructions runs what it stored, as in the simulator
+  uint64_t win_lo = 0, win_hi = 0;
+  bool win_stale = false;
+  void dram_written(uint64_t lo, uint64_t n) {
+    if (overlap(lo, n, win_lo, win_hi - win_lo)) win_stale = true;
+  }
 
   void flush() {
     if (pend.empty()) return;
@@ -407,6 +414,7 @@ struct Device {
         const uint64_t s = uint64_t(sramA) + uint64_t(r) * srcStride, d = uint64_t(dramA) + uint64_t(r) * dstStride;
         chk(s, rowBytes, "DMA_STORE");
         grow(d + rowBytes);
+        dram_written(d, rowBytes);
       }
     }
     const uint64_t bytes = uint64_t(rows) * rowBytes;
@@ -635,6 +643,7 @@ struct Device {
       for (uint32_t kvh = 0; kvh < Hkv; ++kvh) {
         const uint64_t d = uint64_t(base) + uint64_t(kvh) * kvStride + uint64_t(pos + m) * D;
         chk_dram(d, D, "KV_WRITE dst");
+        dram_written(d, D);
         const uint64_t wr = ((d % kBeat + D > kBeat) ? D / 16 : 1) * kBeat;
         perf[P_DRAM_WR] += wr;
         perf[P_ATTN_DRAM_WR] += wr;
@@ -697,13 +706,18 @@ struct Device {
     hip_ok(hipMemsetAsync(status, 0, 4, stream), "hipMemsetAsync");
     std::vector<uint32_t> window;  // instructions fetched from DRAM, 1024 at a time
     uint64_t wbase = 0, fetchPc = pc, issued = 0;
+    win_lo = win_hi = 0;
+    win_stale = false;
     for (;;) {
       if (fetchPc + kInstr > size) bad("instruction fetch out of DRAM range");
-      if (window.empty() || fetchPc < wbase || fetchPc + kInstr > wbase + window.size() * 4) {
+      if (win_stale || window.empty() || fetchPc < wbase || fetchPc + kInstr > wbase + window.size() * 4) {
         flush();
         const uint64_t n = std::min<uint64_t>(1024 * kInstr, (size - fetchPc) / kInstr * kInstr);
         window.assign(n / 4, 0);
         wbase = fetchPc;
+        win_lo = wbase;
+        win_hi = wbase + n;
+        win_stale = false;
         // ordered after every instruction enqueued so far: a program that stores over its own
         // later instructions sees them as the simulator does
         hip_ok(hipMemcpyAsync(window.data(), dram + fetchPc, n, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");

@@ -201,6 +201,20 @@ def dma_chain_case(rng):
     return b.image()
 
 
+def self_modifying_case():
+    """A program that stores over one of its own later instructions (a NOP becomes a VEC_ADD) before
+    reaching it: the stored instruction runs."""
+    b = Builder()
+    b.load(0x0, _i16(np.arange(64) - 32))
+    b.load(0x4000, ins("ADD", 0x0, 0x0, 0x200, 64, 1))
+    b.code.append(None)  # the DMA_STORE below, whose target is the NOP after it
+    b.emit("NOP")
+    b.store(0x200, 128)
+    i = b.code.index(None)
+    b.code[i] = ins("DMA_STORE", 0x4000, 64 * (i + 1), 1, 64, 64, 64)
+    return b.image()
+
+
 def sem_case(ok=True):
     """NOPs and ops that signal and wait on semaphores; ok=False waits for a count never reached."""
     b = Builder()
@@ -262,6 +276,7 @@ def cases():
     out.append(("attn-inplace", img, p, False))
     out.append(("dma", dma_case(rng), 0, False))
     out.append(("dma-chain", dma_chain_case(rng), 0, False))
+    out.append(("self-modifying", self_modifying_case(), 0, False))
     out.append(("semaphores", sem_case(True), 0, False))
     out.append(("chain", chain_case(rng), 0, True))
     return out
