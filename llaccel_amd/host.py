@@ -69,12 +69,6 @@ class GenerationResult:
                 "perf_total": dict(zip(PERF_NAMES, self.total))}
 
 
-def _u(v, what):
-    if not isinstance(v, int) or isinstance(v, bool) or v < 0:
-        raise RuntimeError(what)
-    return v
-
-
 class Host:
     """host.cpp:44-101 (construction and checks), 102-205 (launches and generation)."""
 
@@ -258,3 +252,119 @@ def verify_against_golden(r: GenerationResult, golden_path, verbose: bool = Fals
     if verbose or not ok:
         out(f"VERIFY: {'MATCH' if ok else 'MISMATCH'} ({n} launches, {ng} generated tokens compared)")
     return ok
+
+
+def print_perf(p, launches: int, out=print) -> None:
+    """host.cpp:288-299."""
+    out(f"Performance ({launches} launches)\n-------------------------")
+    for name, v in zip(PERF_NAMES, p):
+        out(f"  {name:<22} {v:>14}")
+    if p[0]:
+        pct = lambda v: 100.0 * v / p[0]  # noqa: E731
+        out(f"  GEMM utilization       {pct(p[6]):6.2f} %")
+        out(f"  ATTN MAC utilization   {pct(p[13]):6.2f} %")
+        out(f"  CP wait stalls         {pct(p[2]):6.2f} %")
+        out(f"  DMA busy               {pct(p[14]):6.2f} %")
+
+
+USAGE = """usage: python -m llaccel_amd.host <model.llbin> [options]
+  --backend gpu             (the MI355X instruction-set device; the only backend)
+  --prompt TEXT             (default "ROMEO:")
+  --prompt-ids PATH         JSON token-ID array; skips character tokenizer
+  --tokens N                greedy tokens to generate (default 32)
+  --tokenizer PATH          (default: <llbin dir>/tokenizer.json)
+  --verify golden.json      compare tokens+logits with python -m llaccel.golden output
+  --out result.json         write tokens, logits and per-launch perf counters
+  --quiet                   less output
+"""
+
+
+def main(argv=None) -> int:
+    """The reference runtime's command line (runtime/src/main.cpp) on the GPU device: load a .llbin,
+    generate, print the output and counters, --verify against a golden trace (exit 1 on MISMATCH),
+    --out the record."""
+    import sys
+    from pathlib import Path
+
+    from .device import GpuDevice
+    argv = list(sys.argv[1:] if argv is None else argv)
+    if not argv or argv[0] in ("--help", "-h"):
+        print(USAGE, end="")
+        return 2 if not argv else 0
+    a = dict(bin=argv[0], backend="gpu", prompt="ROMEO:", tokenizer="", verify="", out="", prompt_ids="", tokens=32,
+             quiet=False, explicit=False)
+    try:
+        i = 1
+        while i < len(argv):
+            f = argv[i]
+            if f in ("--backend", "--prompt", "--prompt-ids", "--tokens", "--tokenizer", "--verify", "--out"):
+                if i + 1 >= len(argv):
+                    print(f"{f} needs a value", file=sys.stderr)
+                    return 2
+                v = argv[i + 1]
+                i += 2
+                if f == "--tokens":
+                    if not v.isdigit() or int(v) > 0xFFFFFFFF:
+                        raise RuntimeError("--tokens requires an unsigned 32-bit integer")
+                    a["tokens"] = int(v)
+                else:
+                    a[f[2:].replace("-", "_")] = v
+                    if f == "--prompt":
+                        a["explicit"] = True
+            elif f == "--quiet":
+                a["quiet"] = True
+                i += 1
+            elif f in ("--help", "-h"):
+                print(USAGE, end="")
+                return 0
+            else:
+                print(f"unknown option {f}\n{USAGE}", file=sys.stderr, end="")
+                return 2
+        if a["prompt_ids"] and (a["explicit"] or a["tokenizer"]):
+            raise RuntimeError("--prompt-ids cannot be combined with --prompt or --tokenizer")
+        if a["backend"] != "gpu":
+            raise RuntimeError("backend must be gpu")
+        lb = Llbin.load(a["bin"])
+        tok = None
+        if not a["prompt_ids"]:
+            tok = Tokenizer.load(a["tokenizer"] or str(Path(a["bin"]).parent / "tokenizer.json"))
+            ids = None
+        else:
+            ids = load_prompt_ids(a["prompt_ids"])
+        fusion = bool(lb.meta.get("fusion", False)) or lb.meta.get("target", "") == "llaccel-v2"
+        dev = GpuDevice(len(lb.dram_image) + (1 << 20), fusion)
+        quiet = a["quiet"]
+        if not quiet:
+            print("Loading program...")
+            for p in lb.programs:
+                print(f"  program M={p.M:<2}  instructions: {len(p.instrs)}")
+            print(f"  target: {lb.meta.get('target', '?')}  fusion: {'on' if lb.meta.get('fusion') else 'off'}  "
+                  f"schedule: {lb.meta.get('schedule', '?')}")
+            print(f"\nExecuting on {dev.name()}...")
+        host = Host(lb, dev, tok)
+        r = host.generate(a["prompt"], a["tokens"]) if tok else host.generate_tokens(ids, a["tokens"])
+        if tok:
+            print(f"\nprompt:  {a['prompt']}\noutput:  {tok.decode(r.generated)}")
+        else:
+            print(f"\nprompt IDs: {json.dumps(r.prompt_tokens)}\noutput IDs: {json.dumps(r.generated)}")
+        if not quiet:
+            print("")
+            print_perf(r.total, len(r.steps))
+        rc = 0
+        if a["verify"]:
+            ok = verify_against_golden(r, a["verify"], True)
+            print(f"PyTorch/golden reference:  {'MATCH' if ok else 'MISMATCH'}")
+            rc = 0 if ok else 1
+        if a["out"]:
+            try:
+                Path(a["out"]).write_text(json.dumps(r.to_json(), indent=1) + "\n")
+            except OSError:
+                raise RuntimeError(f"cannot write result {a['out']}") from None
+        return rc
+    except (RuntimeError, ValueError, OSError, KeyError) as e:
+        print(f"error: {e}", file=sys.stderr)
+        return 1
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -112,3 +112,29 @@ def test_synthetic_decoder_program_equals_oracle(shape):
     img, pc, pos, meta = isa_synth.decoder_program(**shape, seed=2)
     print("program", shape, meta["instructions"], flush=True)
     assert _run(GpuDevice(0, True), img, pos) == _run(FuncSimNp(0, True), img, pos)
+
+
+def test_runtime_cli_runs_and_verifies_on_gpu(tmp_path, capsys):
+    """`python -m llaccel_amd.host model.llbin --prompt-ids ... --tokens N --verify golden.json --out
+    r.json` (the reference runtime's command line, runtime/src/main.cpp): MATCH against the oracle's
+    record with exit 0, the record written; a perturbed golden gives MISMATCH and exit 1."""
+    import json
+    from llaccel_amd import host as Hm
+    from llaccel_amd.device import Llbin
+    (tmp_path / "toy.llbin").write_bytes(C.toy_llbin())
+    (tmp_path / "ids.json").write_text(json.dumps([3, 17, 40, 9, 22, 5]))
+    o = FuncSimNp(0, False)
+    o.name = lambda: "sim"
+    o.max_attention_head_dim = lambda: 256
+    want = Hm.Host(Llbin.load(tmp_path / "toy.llbin"), o).generate_tokens([3, 17, 40, 9, 22, 5], 5).to_json()
+    (tmp_path / "golden.json").write_text(json.dumps(want))
+    args = [str(tmp_path / "toy.llbin"), "--prompt-ids", str(tmp_path / "ids.json"), "--tokens", "5", "--verify",
+            str(tmp_path / "golden.json"), "--out", str(tmp_path / "r.json")]
+    assert Hm.main(args) == 0
+    assert "PyTorch/golden reference:  MATCH" in capsys.readouterr().out
+    assert json.loads((tmp_path / "r.json").read_text()) == want
+    want["argmax_per_step"][2] += 1
+    (tmp_path / "golden.json").write_text(json.dumps(want))
+    assert Hm.main(args + ["--quiet"]) == 1
+    assert "MISMATCH" in capsys.readouterr().out
+    assert Hm.main([str(tmp_path / "toy.llbin"), "--bogus"]) == 2
