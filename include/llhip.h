@@ -286,6 +286,10 @@ uint64_t llhip_dev_dram_size(const llhip_device* dev);
 int llhip_dev_run(llhip_device* dev, uint32_t pc, uint32_t pos, uint64_t* perf);
 /* device.h:28 sramSnapshot: the 1 MiB SRAM into dst */
 int llhip_dev_sram_snapshot(llhip_device* dev, void* dst);
+/* device.h:36 DeviceOptions::interleaveSeed (funcsim.cpp:47-90): 0 runs the sequential policy;
+ * another seed executes the engine queues in the simulator's random legal order for that seed
+ * (std::mt19937 + uniform_int_distribution), which exposes missing semaphore dependencies. */
+int llhip_dev_set_interleave(llhip_device* dev, uint32_t seed);
 /* device.h:19 maxAttentionHeadDim (funcsim.cpp:24) */
 uint32_t llhip_dev_max_attention_head_dim(void);
 /* device.h:22 (device side): the DRAM's device address, valid until the DRAM next grows */

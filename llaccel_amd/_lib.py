@@ -66,6 +66,7 @@ _SIGS = {
     "llhip_dev_run": [_p, ctypes.c_uint32, ctypes.c_uint32, _p],
     "llhip_dev_sram_snapshot": [_p, _p],
     "llhip_dev_max_attention_head_dim": [],
+    "llhip_dev_set_interleave": [_p, ctypes.c_uint32],
     "llhip_dev_dram_ptr": [_p],
 }
 _RESTYPES = {"llhip_last_error": ctypes.c_char_p, "llhip_workspace_bytes": _i64, "llhip_dev_create": _p,

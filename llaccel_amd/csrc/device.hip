@@ -2,16 +2,19 @@
 // GPU: the llaccel::Device contract of runtime/include/llaccel/device.h:15-29 with the semantics of
 // the functional simulator runtime/src/funcsim.cpp.
 //
-// DRAM and the 1 MiB SRAM are device buffers.  run() decodes the instruction stream on the host in
-// program order -- the simulator's sequential policy, funcsim.cpp:84-87: every instruction executes
-// before the next one issues, so a semaphore wait is satisfied exactly when earlier instructions
-// signalled enough -- checks each instruction as the simulator does (same conditions, same
+// DRAM and the 1 MiB SRAM are device buffers.  run() walks the simulator's issue model on the host
+// (funcsim.cpp:41-107: in-order issue into four engine queues, semaphores; the sequential policy
+// executes every instruction right after it issues, an interleave seed picks random legal orders with
+// the simulator's own generator), checks each instruction as the simulator does (same conditions, same
 // messages), accumulates the same performance counters (functions of the operands and POS only) and
 // enqueues the instruction's kernels on one stream: DMA and KV_WRITE as strided copies, GEMM as one
 // kernel over the SRAM weight tiles, the VEC ops and ATTN through the datapath's own kernels.
 // Data-dependent faults (an invalid requant table entry) are flagged on the device and reported once
 // the program has drained.
+#include <array>
 #include <cstring>
+#include <deque>
+#include <random>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -22,7 +25,7 @@
 namespace llhip {
 namespace {
 
-constexpr uint32_t kSram = 1u << 20, kInstr = 64, kNumSem = 32, kTM = 16, kTMax = 4096, kBeat = 64;
+constexpr uint32_t kSram = 1u << 20, kInstr = 64, kNumSem = 32, kTM = 16, kTMax = 4096, kBeat = 64, kQueueDepth = 8;
 constexpr uint8_t kNoSem = 0xFF;
 constexpr uint64_t kMaxInstr = 50000000;
 constexpr uint64_t kDramPad = 64 << 10;  // zero bytes past the logical DRAM size (whole-tile reads)
@@ -229,6 +232,7 @@ struct Device {
   int32_t* status = nullptr;
   hipStream_t stream = nullptr;
   bool fusion = false;
+  uint32_t seed = 0;  // 0: sequential policy; else the simulator's random legal interleaving
   uint32_t pos = 0;
   uint64_t perf[P_NUM] = {};
   uint32_t sem[kNumSem] = {};
@@ -685,7 +689,7 @@ struct Device {
     }
   }
 
-  // Fetches, checks and executes instructions from `pc` until HALT (funcsim.cpp:41-107, sequential).
+  // Fetches, checks and executes instructions from `pc` until HALT (funcsim.cpp:41-107).
   void run(uint32_t pc, uint32_t p) {
     pend.clear();
     try {
@@ -708,39 +712,71 @@ struct Device {
     uint64_t wbase = 0, fetchPc = pc, issued = 0;
     win_lo = win_hi = 0;
     win_stale = false;
+    // the engine queues (dma, gemm, vec, attn) of the simulator's issue model, funcsim.cpp:46-105:
+    // each round the candidates are the non-empty queues' heads and, while not halted, issuing the
+    // next instruction (its semaphore wait met and its queue not full); the sequential policy takes
+    // the first queue head (so every instruction runs right after it issues), an interleave seed a
+    // uniformly random candidate from the same generator and distribution as the simulator
+    std::deque<std::array<uint32_t, 16>> queues[5];
+    std::mt19937 rng(seed);
+    bool halted = false;
+    std::vector<int> cands;
     for (;;) {
-      if (fetchPc + kInstr > size) bad("instruction fetch out of DRAM range");
-      if (win_stale || window.empty() || fetchPc < wbase || fetchPc + kInstr > wbase + window.size() * 4) {
-        flush();
-        const uint64_t n = std::min<uint64_t>(1024 * kInstr, (size - fetchPc) / kInstr * kInstr);
-        window.assign(n / 4, 0);
-        wbase = fetchPc;
-        win_lo = wbase;
-        win_hi = wbase + n;
-        win_stale = false;
-        // ordered after every instruction enqueued so far: a program that stores over its own
-        // later instructions sees them as the simulator does
-        hip_ok(hipMemcpyAsync(window.data(), dram + fetchPc, n, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
-        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      cands.clear();
+      for (int e = 1; e <= 4; ++e)
+        if (!queues[e].empty()) cands.push_back(e);
+      std::array<uint32_t, 16> next{};
+      if (!halted) {
+        if (fetchPc + kInstr > size) bad("instruction fetch out of DRAM range");
+        if (win_stale || window.empty() || fetchPc < wbase || fetchPc + kInstr > wbase + window.size() * 4) {
+          flush();
+          const uint64_t n = std::min<uint64_t>(1024 * kInstr, (size - fetchPc) / kInstr * kInstr);
+          window.assign(n / 4, 0);
+          wbase = fetchPc;
+          win_lo = wbase;
+          win_hi = wbase + n;
+          win_stale = false;
+          // ordered after every instruction enqueued so far: a program that stores over its own
+          // later instructions sees them as the simulator does
+          hip_ok(hipMemcpyAsync(window.data(), dram + fetchPc, n, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
+          hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        }
+        std::memcpy(next.data(), window.data() + (fetchPc - wbase) / 4, sizeof next);
+        const uint8_t op = next[0] & 0xFF, ws_ = (next[0] >> 16) & 0xFF, ss = (next[0] >> 24) & 0xFF;
+        if ((ws_ != kNoSem && ws_ >= kNumSem) || (ss != kNoSem && ss >= kNumSem)) bad("invalid semaphore index");
+        if (engine_of(op) == 0 && op != OP_NOP && op != OP_HALT) bad("invalid command processor opcode");
+        const bool waitOk = ws_ == kNoSem || sem[ws_] >= next[1];
+        const int eng = engine_of(op);
+        if (waitOk && (eng == 0 || queues[eng].size() < kQueueDepth)) cands.push_back(0);
       }
-      const uint32_t* in = window.data() + (fetchPc - wbase) / 4;
-      const uint8_t op = in[0] & 0xFF, ws_ = (in[0] >> 16) & 0xFF, ss = (in[0] >> 24) & 0xFF;
-      if ((ws_ != kNoSem && ws_ >= kNumSem) || (ss != kNoSem && ss >= kNumSem)) bad("invalid semaphore index");
-      if (engine_of(op) == 0 && op != OP_NOP && op != OP_HALT) bad("invalid command processor opcode");
-      if (ws_ != kNoSem && sem[ws_] < in[1])
-        bad("deadlock at pc=0x" + hex(fetchPc) + " (" + op_name(op) + " waits sem " + std::to_string(ws_) +
-            " >= " + std::to_string(in[1]) + ", current " + std::to_string(sem[ws_]) + ")");
-      fetchPc += kInstr;
-      perf[P_INSTR_ISSUED]++;
-      perf[P_DRAM_RD] += kInstr;
-      if (++issued > kMaxInstr) bad("instruction limit exceeded (runaway program?)");
-      if (op == OP_HALT) break;
-      if (op != OP_NOP) {
-        uint32_t copy_in[16];
-        std::memcpy(copy_in, in, sizeof copy_in);  // execute() may refetch the window (DRAM growth)
-        execute(copy_in);
+      if (cands.empty()) {
+        if (halted) break;  // every queue drained after HALT
+        const uint8_t op = next[0] & 0xFF, ws_ = (next[0] >> 16) & 0xFF;
+        bad("deadlock at pc=0x" + hex(fetchPc) + " (" + op_name(op) + " waits sem " + std::to_string(ws_) + " >= " +
+            std::to_string(next[1]) + ", current " + std::to_string(ws_ == kNoSem ? 0 : sem[ws_]) + ")");
       }
-      if (ss != kNoSem) sem[ss]++;
+      const int choice = seed == 0 ? cands[0]
+                                   : cands[std::uniform_int_distribution<size_t>(0, cands.size() - 1)(rng)];
+      if (choice == 0) {
+        fetchPc += kInstr;
+        perf[P_INSTR_ISSUED]++;
+        perf[P_DRAM_RD] += kInstr;
+        if (++issued > kMaxInstr) bad("instruction limit exceeded (runaway program?)");
+        const uint8_t op = next[0] & 0xFF, ss = (next[0] >> 24) & 0xFF;
+        if (op == OP_HALT) {
+          halted = true;
+        } else if (op == OP_NOP) {
+          if (ss != kNoSem) sem[ss]++;
+        } else {
+          queues[engine_of(op)].push_back(next);
+        }
+      } else {
+        const std::array<uint32_t, 16> in = queues[choice].front();
+        queues[choice].pop_front();
+        execute(in.data());
+        const uint8_t ss = (in[0] >> 24) & 0xFF;
+        if (ss != kNoSem) sem[ss]++;
+      }
     }
     flush();
     int32_t st = 0;
@@ -808,6 +844,12 @@ int llhip_dev_sram_snapshot(llhip_device* h, void* dst) {
 }
 
 uint32_t llhip_dev_max_attention_head_dim(void) { return 256; }
+
+int llhip_dev_set_interleave(llhip_device* h, uint32_t seed) {
+  if (!h) return llhip::fail(-EINVAL, "dev_set_interleave: null device");
+  reinterpret_cast<Device*>(h)->seed = seed;
+  return 0;
+}
 
 void* llhip_dev_dram_ptr(llhip_device* h) { return h ? reinterpret_cast<Device*>(h)->dram : nullptr; }
 

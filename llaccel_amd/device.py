@@ -3,7 +3,8 @@
 `GpuDevice` mirrors `llaccel::Device` (runtime/include/llaccel/device.h:15-29) -- `name`,
 `max_attention_head_dim`, `dram_write`, `dram_read`, `dram_size`, `run(pc, pos)` returning the 27
 performance counters, `sram_snapshot` -- with the semantics of the reference's functional simulator
-(runtime/src/funcsim.cpp, sequential policy): the ISA's DRAM and 1 MiB SRAM live in GPU memory and
+(runtime/src/funcsim.cpp: its sequential policy, or its random legal interleaving of the engine
+queues for a seed): the ISA's DRAM and 1 MiB SRAM live in GPU memory and
 every instruction runs as GPU kernels (`llaccel_amd/csrc/device.hip`, C ABI `llhip_dev_*`).  Errors
 are `RuntimeError`s carrying the simulator's messages, as its `std::runtime_error`s.
 
@@ -45,18 +46,22 @@ class GpuDevice:
     """`llaccel::Device` on the GPU (device.h:15-29; funcsim.cpp semantics and counters).
 
     `dram_bytes` = 0 sizes the DRAM to 1 MiB (it grows with writes, as the simulator's);
-    `epilogue_fusion` selects the v2 target whose GEMM runs epilogues (DeviceOptions,
+    `epilogue_fusion` selects the v2 target whose GEMM runs epilogues; `interleave_seed` != 0 runs
+    the engine queues in the simulator's random legal order for that seed (DeviceOptions,
     device.h:31-39)."""
 
-    def __init__(self, dram_bytes: int = 0, epilogue_fusion: bool = False):
+    def __init__(self, dram_bytes: int = 0, epilogue_fusion: bool = False, interleave_seed: int = 0):
         L = _lib.lib()
         self._h = L.llhip_dev_create(int(dram_bytes), int(bool(epilogue_fusion)))
         if not self._h:
             raise RuntimeError(_err())
         self.epilogue_fusion = bool(epilogue_fusion)
+        self.interleave_seed = int(interleave_seed)
+        if self.interleave_seed and L.llhip_dev_set_interleave(self._h, self.interleave_seed):
+            raise RuntimeError(_err())
 
     def name(self) -> str:
-        return "mi355x"
+        return "mi355x (interleaved)" if self.interleave_seed else "mi355x"
 
     def max_attention_head_dim(self) -> int:
         return int(_lib.lib().llhip_dev_max_attention_head_dim())

@@ -275,6 +275,7 @@ USAGE = """usage: python -m llaccel_amd.host <model.llbin> [options]
   --tokenizer PATH          (default: <llbin dir>/tokenizer.json)
   --verify golden.json      compare tokens+logits with python -m llaccel.golden output
   --out result.json         write tokens, logits and per-launch perf counters
+  --interleave SEED         random legal engine interleaving (hazard check)
   --quiet                   less output
 """
 
@@ -292,21 +293,22 @@ def main(argv=None) -> int:
         print(USAGE, end="")
         return 2 if not argv else 0
     a = dict(bin=argv[0], backend="gpu", prompt="ROMEO:", tokenizer="", verify="", out="", prompt_ids="", tokens=32,
-             quiet=False, explicit=False)
+             quiet=False, explicit=False, interleave=0)
     try:
         i = 1
         while i < len(argv):
             f = argv[i]
-            if f in ("--backend", "--prompt", "--prompt-ids", "--tokens", "--tokenizer", "--verify", "--out"):
+            if f in ("--backend", "--prompt", "--prompt-ids", "--tokens", "--tokenizer", "--verify", "--out",
+                     "--interleave"):
                 if i + 1 >= len(argv):
                     print(f"{f} needs a value", file=sys.stderr)
                     return 2
                 v = argv[i + 1]
                 i += 2
-                if f == "--tokens":
+                if f in ("--tokens", "--interleave"):
                     if not v.isdigit() or int(v) > 0xFFFFFFFF:
-                        raise RuntimeError("--tokens requires an unsigned 32-bit integer")
-                    a["tokens"] = int(v)
+                        raise RuntimeError(f"{f} requires an unsigned 32-bit integer")
+                    a[f[2:]] = int(v)
                 else:
                     a[f[2:].replace("-", "_")] = v
                     if f == "--prompt":
@@ -332,7 +334,7 @@ def main(argv=None) -> int:
         else:
             ids = load_prompt_ids(a["prompt_ids"])
         fusion = bool(lb.meta.get("fusion", False)) or lb.meta.get("target", "") == "llaccel-v2"
-        dev = GpuDevice(len(lb.dram_image) + (1 << 20), fusion)
+        dev = GpuDevice(len(lb.dram_image) + (1 << 20), fusion, a["interleave"])
         quiet = a["quiet"]
         if not quiet:
             print("Loading program...")

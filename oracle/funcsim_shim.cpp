@@ -29,6 +29,13 @@ void* fs_create(uint64_t dram_bytes, int fusion) {
   o.epilogueFusion = fusion != 0;
   return llaccel::makeFuncSim(o).release();
 }
+void* fs_create_interleaved(uint64_t dram_bytes, int fusion, uint32_t seed) {
+  llaccel::DeviceOptions o;
+  o.dramBytes = dram_bytes;
+  o.epilogueFusion = fusion != 0;
+  o.interleaveSeed = seed;
+  return llaccel::makeFuncSim(o).release();
+}
 void fs_destroy(void* d) { delete static_cast<Device*>(d); }
 int fs_write(void* d, uint64_t a, const void* s, uint64_t n) {
   return guarded([&] { static_cast<Device*>(d)->dramWrite(a, s, n); });

@@ -21,17 +21,19 @@ REF = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "libfuncsim_ref.
 class RefSim:
     """ctypes front of oracle/funcsim_shim.cpp."""
 
-    def __init__(self, fusion: bool):
+    def __init__(self, fusion: bool, seed: int = 0):
         self.L = L = ctypes.CDLL(str(REF))
         p, u64, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32
         L.fs_create.restype = p
         L.fs_create.argtypes = [u64, ctypes.c_int]
+        L.fs_create_interleaved.restype = p
+        L.fs_create_interleaved.argtypes = [u64, ctypes.c_int, u32]
         for n, a in dict(fs_destroy=[p], fs_write=[p, u64, p, u64], fs_read=[p, u64, p, u64], fs_size=[p],
                          fs_run=[p, u32, u32, p], fs_sram=[p, p]).items():
             getattr(L, n).argtypes = a
         L.fs_size.restype = u64
         L.fs_error.restype = ctypes.c_char_p
-        self.h = L.fs_create(0, int(fusion))
+        self.h = L.fs_create_interleaved(0, int(fusion), seed) if seed else L.fs_create(0, int(fusion))
 
     def _ok(self, rc):
         if rc:
@@ -207,3 +209,14 @@ def test_synthetic_decoder_program_oracle_equals_reference_simulator():
                                                    layers=2, max_seq=64, pos=20, seed=1)
     r, o = RefSim(True), FuncSimNp(0, True)
     assert _run(r, img, pos) == _run(o, img, pos)
+
+
+@needs_ref
+def test_interleaving_changes_results_of_programs_without_waits():
+    """The programs the GPU interleave test uses have no semaphore waits between dependent
+    instructions, so the reference simulator's random legal orders change their results: the GPU's
+    equality with it under a seed is a check of the order, not of a moot one."""
+    rng = np.random.default_rng(1)
+    img = C.chain_case(rng)
+    base = _run(RefSim(True), img, 0)[1]
+    assert any(_run(RefSim(True, s), img, 0)[1] != base for s in (1, 7, 1234))
