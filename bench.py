@@ -8,7 +8,7 @@ batch 1, after a 512-token prefill.  One step = one M=1 decode launch of the who
 graph, with weights, KV cache and activations resident in HBM.
 
 The JSON line also carries
-  roofline     : the decode kernel family with the most time per step: algorithmic bytes per
+  roofline     : the decode kernel family that moves the most bytes per step: algorithmic bytes per
                  launch / average launch duration (HIP events around a graph of that family's
                  launches), against 8 TB/s; `traffic` is the HBM bytes per launch measured with
                  rocprofv3 counters (profiles/decode_traffic.json, copy-kernel calibrated);
@@ -482,7 +482,9 @@ def main() -> None:
         log(f"  {kind:12s} {n:3d} launches {t * 1e6:8.1f} us/step {t / n * 1e6:7.2f} us/launch "
             f"{nbytes / 1e6:8.2f} MB -> {nbytes / t / 1e9:7.1f} GB/s")
         del graph
-    dom = max(fam, key=lambda k: fam[k]["us_per_step"] if fam[k]["bytes_per_launch"] > 0 else -1)
+    # the family that moves the most HBM bytes per step (the share of the step the HBM roofline
+    # bounds); time per step would tie between families of ~equal launch time and flip run to run
+    dom = max(fam, key=lambda k: fam[k]["bytes_per_launch"] * fam[k]["launches"])
     d = fam[dom]
     achieved = d["bytes_per_launch"] / (d["us_per_launch"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": f"{dom} (decode, M=1; {d['launches']} launches per step)",
