@@ -507,7 +507,14 @@ class GoldenModel:
     @property
     def kv(self) -> dict[int, tuple[np.ndarray, np.ndarray]]:
         """Host snapshots {layer: (K, V)} of the device caches, int8 (Hkv, max_seq, D)."""
-        return {L: (_down(k[self._slot]), _down(v[self._slot])) for L, (k, v) in self._kv.items()}
+        return self.kv_of(self._slot)
+
+    def kv_of(self, slot: int) -> dict[int, tuple[np.ndarray, np.ndarray]]:
+        """Host snapshots of the caches of KV slot `slot` (sequence `slot` of a batch run)."""
+        n = next(iter(self._kv.values()))[0].shape[0] if self._kv else 0
+        if not 0 <= slot < n:
+            raise ValueError(f"KV slot {slot} outside the {n} allocated")
+        return {L: (_down(k[slot]), _down(v[slot])) for L, (k, v) in self._kv.items()}
 
     def set_kv(self, layer: int, k: np.ndarray, v: np.ndarray) -> None:
         """Upload a (Hkv, max_seq, D) int8 K/V state for `layer` (preinitialised-state runs)."""
