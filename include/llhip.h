@@ -147,6 +147,22 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
                     const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
                     int64_t prob_bits, int8_t* out, int64_t ldo, void* ws, void* stream);
 
+/* No counterpart in the reference: llhip_attention for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, results and errors as llhip_attention without `ws`: the split-context partials of
+ * long contexts live in a static device array of LLHIP_ATTENTION_NOALLOC_SCRATCH bytes per GPU,
+ * held until the process ends.  A launch plan whose partials would not fit takes fewer key splits
+ * (or none), so every input llhip_attention accepts is accepted; the plan's size is checked before
+ * any launch.  The call allocates nothing (no hipMalloc/hipFree).  Every call on one GPU shares
+ * that GPU's array, and the partials are written in full before they are read within a call, so
+ * nothing carries over between calls -- but calls that overlap on one GPU (other streams, other
+ * threads) race on it. */
+#define LLHIP_ATTENTION_NOALLOC_SCRATCH (4 << 20)
+int llhip_attention_noalloc(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
+                            const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
+                            const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
+                            int64_t prob_bits, int8_t* out, int64_t ldo, void* stream);
+
 /* ---- host-loop helpers ---- */
 /* golden.py:369-373  rows[m] = embed[tokens[m]] for m < n_tokens, zero for n_tokens <= m < M.
  * tokens are int32 row indices already resolved by the caller to [0, vocab_rows). */

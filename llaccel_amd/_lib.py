@@ -45,6 +45,8 @@ _SIGS = {
     "llhip_kv_write": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p],
     "llhip_attention": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64,
                         _i64, _p, _i64, _p, _p],
+    "llhip_attention_noalloc": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64,
+                                _i64, _i64, _p, _i64, _p],
     "llhip_embed_rows": [_p, _i64, _i64, _p, _i64, _i64, _p, _p],
     "llhip_argmax_i16": [_p, _i64, _i64, _i64, _p, _p],
     "llhip_greedy_step": [_p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],

@@ -14,6 +14,7 @@
 // and the keys across thread groups (four keys in flight per thread); partial
 // sums are folded across lanes with shuffles, then across waves in LDS.
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/llhip.h"
 #include "common.h"
@@ -825,11 +826,18 @@ int llhip_kv_write(const int8_t* k, const int8_t* v, int64_t M, int64_t Hkv, int
   return 0;
 }
 
-int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
-                    const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
-                    const int8_t* vc, int64_t max_seq, int64_t Ms,
-                    int64_t Ss, int64_t Mo, int64_t So, int64_t prob_bits, int8_t* out, int64_t ldo, void* ws,
-                    void* stream) {
+}  // extern "C"
+
+namespace llhip {
+
+// llhip_attention with the split-context partials in `split_ws` (split_bytes long; NULL disables
+// the split): the launch plan is the same for both entry points, except that a plan whose
+// partials would not fit takes fewer key splits, or none.
+static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
+                          const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
+                          const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
+                          int64_t prob_bits, int8_t* out, int64_t ldo, void* split_ws, int64_t split_bytes,
+                          void* stream) {
   if (prob_bits != 8 && prob_bits != 15) return fail(-EINVAL, "attention prob_bits must be 8 or 15");
   if (M < 0 || H <= 0 || Hkv <= 0 || H % Hkv) return fail(-EINVAL, "attention: H must be a multiple of Hkv");
   if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256)
@@ -873,14 +881,18 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   // Long contexts with few (row block, head) pairs: split the key tiles over S workgroups per pair
   // (three reduction launches + a finishing one) so every CU streams a share of K and V.
   const int64_t rblocks = ceil_div(M, AT_ROWS), pairs = H * rblocks, ktiles = ceil_div(tmax, 64);
-  if (!row_pos && ws && tmax <= AT_MAX_T && ktiles >= AT_SPLIT_MIN_TILES && pairs * 4 <= cus) {
+  // bytes of the partials of S splits: per-split row maxima and sums, and value partials
+  auto split_need = [&](int64_t S) { return pairs * S * AT_ROWS * (2 + D) * 4; };
+  if (!row_pos && split_ws && tmax <= AT_MAX_T && ktiles >= AT_SPLIT_MIN_TILES && pairs * 4 <= cus &&
+      split_need(2) <= split_bytes) {
     int S = (int)std::min<int64_t>(std::min<int64_t>(ceil_div(cus, pairs), ceil_div(ktiles, 4)), AT_SPLIT_MAXS);
-    while (S > 1 && pairs * S * AT_ROWS * (2 + D) * 4 > WS_SCRATCH_BYTES) --S;
+    while (S > 2 && split_need(S) > split_bytes) --S;
     const int tps = (int)ceil_div(ktiles, S);
-    S = (int)ceil_div(ktiles, tps);
+    S = (int)ceil_div(ktiles, tps);  // never more than before: the plan still fits
+    if (split_need(S) > split_bytes) return fail(-EINVAL, "attention: split partials exceed the scratch");
     const int maxw = D <= 128 ? AttnTileCfg<128>::MAXW : AttnTileCfg<256>::MAXW;
     const int nw = std::min(maxw, tps);
-    int32_t* sw = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH);
+    int32_t* sw = static_cast<int32_t*>(split_ws);
     dim3 grid((unsigned)H, (unsigned)rblocks, (unsigned)S), block(64 * nw);
     dim3 fgrid((unsigned)H, (unsigned)rblocks, (unsigned)ceil_div(std::min<int64_t>(M, AT_ROWS) * D, 256));
 #define LLHIP_SPLIT(DD)                                                                      \
@@ -933,6 +945,61 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   }
   LLHIP_LAUNCH_CHECK();
   return 0;
+}
+
+// ---------------------------------------------------------------------------------------
+// scratch of the allocation-free entry point
+// ---------------------------------------------------------------------------------------
+// The split-context partials of llhip_attention_noalloc live in this file-scope array: every GPU
+// the library runs on holds its own copy until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol): the device address
+// comes from hipGetSymbolAddress, once per device with that device current, and is kept below.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = (int64_t)LLHIP_ATTENTION_NOALLOC_SCRATCH;
+static __device__ __align__(256) int32_t scratch[NOALLOC_SCRATCH_BYTES / 4];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES];
+
+// device address of `scratch` on the current device (looked up on the first call per device)
+static int noalloc_scratch(void** out) {
+  int dev = 0;
+  LLHIP_CHECK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(-EINVAL, "attention_noalloc: device %d above %d", dev, MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(-EIO, "attention_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace llhip
+
+extern "C" {
+
+int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
+                    const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
+                    const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
+                    int64_t prob_bits, int8_t* out, int64_t ldo, void* ws, void* stream) {
+  return attention_impl(q, M, H, Hkv, D, ldq, pos, pos_dev, row_pos, slot_stride, kc, vc, max_seq, Ms, Ss, Mo, So,
+                        prob_bits, out, ldo, ws ? static_cast<char*>(ws) + WS_SCRATCH : nullptr, WS_SCRATCH_BYTES,
+                        stream);
+}
+
+int llhip_attention_noalloc(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
+                            const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
+                            const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
+                            int64_t prob_bits, int8_t* out, int64_t ldo, void* stream) {
+  void* sw = nullptr;
+  const int rc = noalloc_scratch(&sw);
+  if (rc) return rc;
+  return attention_impl(q, M, H, Hkv, D, ldq, pos, pos_dev, row_pos, slot_stride, kc, vc, max_seq, Ms, Ss, Mo, So,
+                        prob_bits, out, ldo, sw, NOALLOC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"
