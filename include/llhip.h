@@ -277,6 +277,77 @@ typedef struct llhip_norm_linear_desc {
 /* golden.py:286-296 + 316-342 -- rmsnorm, quant, one linear with any epilogue. */
 int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream);
 
+/* ---- decode chain: one decode row of a fused graph in three launches per layer ----
+ * A decode launch (M = 1) of the reference's fused qgraph (golden.py:275-314) runs each layer as
+ *   llhip_dec_attn_in   : [finish the previous layer's down projection] rmsnorm, quant, q/k/v, rope,
+ *                         quant, kv_write, as the attn_in run above;
+ *   llhip_dec_attention : attention, then the output projection's partial sums per head;
+ *   llhip_dec_mlp       : finish the output projection, rmsnorm, quant, gate/up, quant, then the down
+ *                         projection's partial sums per 16 FFN columns;
+ * and the final norm + lm_head + greedy step as llhip_dec_finish + llhip_dec_head + llhip_dec_greedy.  The output (wo)
+ * and down (wd) projections -- linear with the resadd epilogue, golden.py:316-342 -- are computed as
+ * exact int32 partial sums of disjoint K ranges added into accumulator rows with atomics; the next
+ * launch finishes them (bias, requant16, resadd) in its prologue.  Integer addition is associative,
+ * so every activation equals the separate linear's.  Every activation the ops name is written. */
+typedef struct llhip_resid_desc {
+  const void* acc;  /* int32 [R][N] partial sums of the projection; NULL: the row is pre.x itself */
+  int64_t R;        /* accumulator rows (1..8) whose sum is the projection */
+  const void* rq;   /* int32 [N][2] the projection's requant pairs */
+  const void* bias; /* int32 [N] or NULL */
+  const void* aux;  /* i16 [N] the residual of the resadd epilogue */
+  void* x_out;      /* i16 [N] the finished row (the projection's output activation) */
+} llhip_resid_desc;
+
+/* golden.py:286-300 + 316-342 -- llhip_attn_in for one row whose input row is the resadd output of
+ * the previous projection when r->acc is non-NULL (written to r->x_out), else pre.x; it also clears
+ * zero[0..zero_n) (int32, 16-byte aligned) for the attention's output projection. */
+int llhip_dec_attn_in(const llhip_attn_in_desc* d, const llhip_resid_desc* r, void* zero, int64_t zero_n,
+                      void* stream);
+
+typedef struct llhip_dec_attn_desc {
+  const void* q;        /* i8 [H*D] */
+  const void* kc;       /* int8 caches [Hkv][max_seq][D] */
+  const void* vc;
+  void* out;            /* i8 [H*D] the attention activation */
+  const void* pos_dev;  /* int32 device position, or NULL: pos */
+  int64_t pos, H, Hkv, D, max_seq, Ms, Ss, Mo, So, prob_bits;
+  const void* wo_panel; /* i8 [H][N][D]: the output projection W[n][h*D + d] at [h][n][d] */
+  int64_t N;            /* the output projection's width */
+  void* acc;            /* int32 [N], zero on entry: receives the H per-head partial sums */
+  void* zero;           /* int32 [zero_n] cleared for the down projection (16-byte aligned) */
+  int64_t zero_n;
+} llhip_dec_attn_desc;
+
+/* golden.py:353-366 + 316-342 -- causal GQA attention of one row, then each head's partial sums of
+ * the output projection (K range h*D..h*D+D-1) added into acc.  ws as for llhip_attention. */
+int llhip_dec_attention(const llhip_dec_attn_desc* d, void* ws, void* stream);
+
+/* golden.py:286-309 + 316-342 -- llhip_mlp_in for one row whose input is the resadd output of the
+ * output projection (r), then the down projection's partial sums of each workgroup's 16 FFN columns
+ * added into wd_acc [R][N_out] (zero on entry; workgroup b adds into row b % R).  wd_panel is i8
+ * [ceil(N/16)][N_out][16]: W_down[n][16b + j] at [b][n][j], zero bytes for 16b + j >= N. */
+int llhip_dec_mlp(const llhip_mlp_in_desc* d, const llhip_resid_desc* r, const void* wd_panel, void* wd_acc,
+                  int64_t R, int64_t N_out, void* stream);
+
+/* golden.py:316-342 + 124-137 + 119-120 -- one row of the last down projection finished from its
+ * partial sums (r, written to r->x_out), then rmsnorm and quant of it (h_out, hq_out), by one
+ * workgroup: the input of llhip_dec_head with pre.prequant set. */
+int llhip_dec_finish(const llhip_norm_quant_desc* d, const llhip_resid_desc* r, void* stream);
+/* golden.py:286-296 + 316-342 + 376-377 -- llhip_norm_linear for one row.  With keys non-NULL
+ * (llhip_dec_head_keys(N) uint64 words), also the first half of the greedy step: keys[t] = the best
+ * (value, lowest index) of tile t's 16 columns below vocab, and the row's first vocab values
+ * recorded at ring[*step] when *step < ring_cap. */
+int llhip_dec_head(const llhip_norm_linear_desc* d, int64_t vocab, void* keys, const int32_t* step, int16_t* ring,
+                   int64_t ring_ld, int64_t ring_cap, void* stream);
+/* golden.py:376-377 -- the number of greedy keys llhip_dec_head writes for an output of N columns */
+int64_t llhip_dec_head_keys(int64_t N);
+/* golden.py:376-377 + 411-414 + 369-373 -- the greedy step's second half: *token = the first argmax
+ * (the best of nkeys keys), ring_tokens[*step] = token when *step < ring_cap, *pos += 1, *step += 1,
+ * and row[0..dim) = embed[token] (the next decode launch's input row). */
+int llhip_dec_greedy(const void* keys, int64_t nkeys, int32_t* token, int32_t* pos, int32_t* step,
+                     int32_t* ring_tokens, int64_t ring_cap, const int16_t* embed, int64_t dim, int16_t* row,
+                     void* stream);
+
 /* ---- the reference accelerator's instruction set on the GPU ----
  * A device holding the ISA's DRAM and 1 MiB SRAM in GPU memory that runs .llbin programs (docs/ISA.md,
  * binary version 2) with the functional simulator's semantics and performance counters.  Errors

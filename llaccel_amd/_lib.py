@@ -166,3 +166,26 @@ _SIGS.update({
     "llhip_mlp_in": [ctypes.POINTER(MlpInDesc), _p],
     "llhip_norm_linear": [ctypes.POINTER(NormLinearDesc), _p],
 })
+
+
+# ---- decode chain (include/llhip.h: llhip_dec_*) ------------------------------------------
+class ResidDesc(ctypes.Structure):
+    _fields_ = [("acc", _p), ("R", _i64), ("rq", _p), ("bias", _p), ("aux", _p), ("x_out", _p)]
+
+
+class DecAttnDesc(ctypes.Structure):
+    _fields_ = [("q", _p), ("kc", _p), ("vc", _p), ("out", _p), ("pos_dev", _p), ("pos", _i64), ("H", _i64),
+                ("Hkv", _i64), ("D", _i64), ("max_seq", _i64), ("Ms", _i64), ("Ss", _i64), ("Mo", _i64), ("So", _i64),
+                ("prob_bits", _i64), ("wo_panel", _p), ("N", _i64), ("acc", _p), ("zero", _p), ("zero_n", _i64)]
+
+
+_SIGS.update({
+    "llhip_dec_attn_in": [ctypes.POINTER(AttnInDesc), ctypes.POINTER(ResidDesc), _p, _i64, _p],
+    "llhip_dec_attention": [ctypes.POINTER(DecAttnDesc), _p, _p],
+    "llhip_dec_mlp": [ctypes.POINTER(MlpInDesc), ctypes.POINTER(ResidDesc), _p, _p, _i64, _i64, _p],
+    "llhip_dec_finish": [ctypes.POINTER(NormQuantDesc), ctypes.POINTER(ResidDesc), _p],
+    "llhip_dec_head": [ctypes.POINTER(NormLinearDesc), _i64, _p, _p, _p, _i64, _i64, _p],
+    "llhip_dec_head_keys": [_i64],
+    "llhip_dec_greedy": [_p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],
+})
+_RESTYPES["llhip_dec_head_keys"] = _i64

@@ -1,0 +1,223 @@
+"""Decode chain: a one-row launch of a fused qgraph as three kernel launches per layer.
+
+The fused plan (llaccel_amd.fusion) runs a layer of the reference's fused graph (the op order of
+refquant.py:426-467 with --fusion) as five launches: attn_in, attention, linear wo (resadd),
+mlp_in, linear wd (resadd).  For one row (a decode launch, golden.py:392-397) the two resadd
+projections move into their producers: each attention head adds its exact int32 partial sums of
+wo (the head's K range) into an accumulator row, each mlp_in workgroup adds the partial sums of wd
+over its 16 FFN columns into one of R accumulator rows, and the next launch finishes the
+projection -- bias, requant16 and the residual add of golden.py:316-342 -- in its prologue
+(include/llhip.h, llhip_dec_*).  Integer sums do not depend on their order, so every activation
+is the one the separate launches write.
+
+    layer l:  llhip_dec_attn_in  [finish wd(l-1)] rmsnorm quant q k v [q/k norm] rope quant kv_write
+              llhip_dec_attention attention + wo partial sums          (clears the wd accumulators)
+              llhip_dec_mlp      finish wo, rmsnorm quant gate/up quant + wd partial sums
+    final:    llhip_dec_finish   finish wd(L-1), rmsnorm, quant (one workgroup)
+              llhip_dec_head     lm_head [greedy keys + record row]
+              llhip_dec_greedy   (decode loop) argmax, record, position, next input row
+
+The chain exists only for graphs whose every layer has that shape; other graphs keep the fused
+plan.  The kernels read the output projections in panel layouts made once on the device:
+wo as [H][dim][D] (a head's K range contiguous) and wd as [FFN/16][dim][16].
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import _lib
+from . import fusion
+
+WD_ROWS = 8  # accumulator rows of the down projection (workgroup b adds into row b % 8)
+
+
+def _vp(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _resadd_linear(op, src, aux, N, K):
+    """op is `linear src -> out` with the resadd epilogue on `aux`, i16 output, N x K weights."""
+    return (op.get("op") == "linear" and op["in"] == src and (op.get("epilogue") or "none") == "resadd"
+            and op.get("aux") == aux and op.get("out_dtype", "i16") == "i16" and int(op["N"]) == N
+            and int(op["K"]) == K)
+
+
+class _Layer:
+    def __init__(self, attn_in, att_op, wo, mlp, wd, resid_in):
+        self.attn_in, self.att, self.wo, self.mlp, self.wd = attn_in, att_op, wo, mlp, wd
+        self.resid_in = resid_in
+
+
+class Chain:
+    """The decode-chain steps of a model (build with `build`); `run(pos, pd)` launches one row,
+    `run(pos, pd, greedy=...)` the decode loop's launch with the greedy step."""
+
+    def __init__(self, model, layers, head, head_ops):
+        torch = _torch()
+        self.model, self.layers, self.head, self.head_ops = model, layers, head, head_ops
+        dev = model.device
+        self.dim = model.dim
+        self.acc_wo = torch.zeros(self.dim, dtype=torch.int32, device=dev)
+        self.acc_wd = torch.zeros((WD_ROWS, self.dim), dtype=torch.int32, device=dev)
+        vp = int(head.desc_N)
+        self.keys = torch.zeros(int(_lib.lib().llhip_dec_head_keys(vp)), dtype=torch.int64, device=dev)
+        self.wo_panel, self.wd_panel = [], []
+        for ly in layers:
+            H, D = int(ly.att["H"]), int(ly.att["D"])
+            w = model._dt[ly.wo["w"]]  # [dim][H*D]
+            self.wo_panel.append(w.view(self.dim, H, D).permute(1, 0, 2).contiguous())
+            wd = model._dt[ly.wd["w"]]  # [dim][F]
+            F = wd.shape[1]
+            Fp = -(-F // 16) * 16
+            pad = torch.zeros((self.dim, Fp), dtype=torch.int8, device=dev)
+            pad[:, :F] = wd
+            self.wd_panel.append(pad.view(self.dim, Fp // 16, 16).permute(1, 0, 2).contiguous())
+        self._resid = _lib.ResidDesc()
+        self._att = _lib.DecAttnDesc()
+
+    # ---- descriptors ------------------------------------------------------------------------
+    def _fill_resid(self, op, acc, R):
+        """Finishing `op` (linear, resadd) from `acc` [R][dim]."""
+        m, r = self.model, self._resid
+        r.acc, r.R = _vp(acc), R
+        r.rq = _vp(m._dt[op["rq"]])
+        r.bias = _vp(m._dt[op["bias"]]) if op.get("bias") else None
+        r.aux = _vp(m._buf(op["aux"]))
+        r.x_out = _vp(m._buf(op["out"]))
+        return ctypes.byref(r)
+
+    def _launch_layer(self, i, ly, pos, pd):
+        m = self.model
+        s = m._stream_handle()
+        fs = ly.attn_in
+        fs.fill(fs.desc, 1, pos, pd)
+        fs.desc.pre.prequant = 0
+        resid = self._fill_resid(self.layers[i - 1].wd, self.acc_wd, WD_ROWS) if i else None
+        _lib.call("llhip_dec_attn_in", ctypes.byref(fs.desc), resid, _vp(self.acc_wo), self.dim, s)
+        a, d = ly.att, self._att
+        kcp, vcp, pdev, _, _ = m._kv_args(int(a["layer"]), pd)
+        d.q, d.kc, d.vc, d.out = _vp(m._buf(a["q"])), kcp, vcp, _vp(m._buf(a["out"]))
+        d.pos_dev, d.pos = pdev, pos
+        d.H, d.Hkv, d.D, d.max_seq = int(a["H"]), int(a["Hkv"]), int(a["D"]), m.max_seq
+        d.Ms, d.Ss, d.Mo, d.So = int(a["Ms"]), int(a["Ss"]), int(a["Mo"]), int(a["So"])
+        d.prob_bits = int(a.get("prob_bits", 8))
+        d.wo_panel, d.N, d.acc = _vp(self.wo_panel[i]), self.dim, _vp(self.acc_wo)
+        d.zero, d.zero_n = _vp(self.acc_wd), WD_ROWS * self.dim
+        _lib.call("llhip_dec_attention", ctypes.byref(d), _vp(m._ws), s)
+        fm = ly.mlp
+        fm.fill(fm.desc, 1, pos, pd)
+        fm.desc.pre.prequant = 0
+        _lib.call("llhip_dec_mlp", ctypes.byref(fm.desc), self._fill_resid(ly.wo, self.acc_wo, 1),
+                  _vp(self.wd_panel[i]), _vp(self.acc_wd), WD_ROWS, self.dim, s)
+
+    def run(self, pos, pd=None, greedy=None):
+        """One row at position pos (or *pd).  greedy = (token, pos, step) device int32 pointers plus
+        (ring_rows, ring_ld, ring_tokens, ring_cap): the decode loop's greedy step and record."""
+        m = self.model
+        for i, ly in enumerate(self.layers):
+            self._launch_layer(i, ly, pos, pd)
+        fh = self.head
+        fh.fill(fh.desc, 1, pos, pd)
+        s = m._stream_handle()
+        # the last down projection finished, normalised and quantised once; the lm_head workgroups
+        # read the quantised row
+        fh.desc.pre.prequant = 0
+        _lib.call("llhip_dec_finish", ctypes.byref(fh.desc.pre),
+                  self._fill_resid(self.layers[-1].wd, self.acc_wd, WD_ROWS), s)
+        fh.desc.pre.prequant = 1
+        if greedy is None:
+            _lib.call("llhip_dec_head", ctypes.byref(fh.desc), m.vocab, None, None, None, 0, 0, s)
+            return
+        tok, posp, step, ring_rows, ring_ld, ring_tok, ring_cap = greedy
+        _lib.call("llhip_dec_head", ctypes.byref(fh.desc), m.vocab, _vp(self.keys), step, ring_rows, ring_ld,
+                  ring_cap, s)
+        _lib.call("llhip_dec_greedy", _vp(self.keys), self.keys.numel(), tok, posp, step, ring_tok, ring_cap,
+                  _vp(m._dt["embed"]), self.dim, _vp(m._act[m.q.input_name]), s)
+
+    # ---- measurement ------------------------------------------------------------------------
+    def step_bytes(self, T: int):
+        """Algorithmic HBM bytes of one row's launch at context T, per chain kernel family: the bytes
+        of the ops each family computes (the linear(M,N,K) and attention formulas of the measurement
+        plan), so the families add up to the fused plan's step."""
+        fam = {"dec_attn_in": 0, "dec_attention": 0, "dec_mlp": 0, "dec_head": 0}  # dec_finish: in dec_head
+        for ly in self.layers:
+            fam["dec_attn_in"] += ly.attn_in.bytes_fn(1)
+            fam["dec_attention"] += ly.att_bytes(1, T) + ly.wo_bytes(1)
+            fam["dec_mlp"] += ly.mlp.bytes_fn(1) + ly.wd_bytes(1)
+        fam["dec_head"] = self.head.bytes_fn(1)
+        return fam
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def build(model):
+    """The decode chain of `model`'s op list, or None when a layer does not have the chain's shape."""
+    ops, steps = model.q.ops, model._plan_unfused
+    if any(getattr(s, "kind", "") == "error" for s in steps) or len(steps) != len(ops):
+        return None
+    spec = model._act_spec
+    resid = model.q.input_name
+    dim = model.dim
+    i, layers = 0, []
+    while i < len(ops):
+        got = fusion.match_attn_in(model, ops, i, steps)
+        if got is None:
+            break
+        n, fa = got
+        rn = fa.ops[0]
+        if rn["in"] != resid or fa.K != dim:
+            return None
+        j = i + n
+        if j + 1 >= len(ops):
+            return None
+        att, wo = ops[j], ops[j + 1]
+        qq = fa.ops[-3]  # quant q (rope q, rope k, quant q, quant k, kv_write end the run)
+        kvw = fa.ops[-1]
+        if att.get("op") != "attention" or att["q"] != qq["out"] or int(att["layer"]) != int(kvw["layer"]):
+            return None
+        H, D = int(att["H"]), int(att["D"])
+        if not _resadd_linear(wo, att["out"], resid, dim, H * D) or D % 16 or D > 256:
+            return None
+        j += 2
+        got = fusion.match_mlp_in(model, ops, j, steps)
+        if got is None:
+            return None
+        n, fm = got
+        if fm.ops[0]["in"] != wo["out"] or fm.K != dim:
+            return None
+        fq = fm.ops[-1]
+        j += n
+        if j >= len(ops):
+            return None
+        wd = ops[j]
+        F = spec[fq["out"]][1]
+        if not _resadd_linear(wd, fq["out"], wo["out"], dim, F):
+            return None
+        ly = _Layer(fa, att, wo, fm, wd, resid)
+        a_at = i + len(fa.ops)  # op index of the attention; wo follows it
+        ly.att_bytes, ly.wo_bytes, ly.wd_bytes = steps[a_at].bytes_fn, steps[a_at + 1].bytes_fn, steps[j].bytes_fn
+        layers.append(ly)
+        resid = wd["out"]
+        i = j + 1
+    if not layers:
+        return None
+    got = fusion.match_norm_linear(model, ops, i, steps)
+    if got is None:
+        return None
+    n, fh = got
+    lo = fh.ops[-1]
+    if (fh.ops[0]["in"] != resid or i + n != len(ops) or lo["out"] != model.q.output_name or fh.K != dim
+            or lo.get("out_dtype", "i16") != "i16" or int(lo["N"]) < model.vocab):
+        return None
+    fh.desc_N = int(lo["N"])
+    for ly in layers:  # the finished projections' operands must be 16-byte addressable
+        for op in (ly.wo, ly.wd):
+            if op.get("bias") and model._dt[op["bias"]].data_ptr() % 16:
+                return None
+            if model._dt[op["rq"]].data_ptr() % 16:
+                return None
+    return Chain(model, layers, fh, fh.ops)

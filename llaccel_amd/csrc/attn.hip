@@ -38,7 +38,80 @@ struct AttnArgs {
   int H, Hkv, pos, pb;
   int lds_T;  // score slots in LDS
   int M;
+  // decode chain (WO kernels, one row): the output projection's partial sums of each head,
+  // wo_acc[n] += sum_d out[h D + d] * Wo[n][h D + d] with the panel wop[h][n][d] = Wo[n][h D + d],
+  // and the accumulator rows of the next projection cleared by head 0
+  const int8_t* wop;
+  int32_t* wo_acc;
+  int32_t* zero;
+  int wo_N, zero_n;
 };
+
+// clear n int32 values from one workgroup (16-byte aligned)
+__device__ __forceinline__ void zero_words(int32_t* p, int n) {
+  if (!p) return;
+  for (int i = 4 * (int)threadIdx.x; i < n; i += 4 * (int)blockDim.x) {
+    if (i + 4 <= n) *reinterpret_cast<v4i*>(p + i) = v4i{0, 0, 0, 0};
+    else
+      for (int j = i; j < n; ++j) p[j] = 0;
+  }
+}
+
+// sum over aligned groups of DC consecutive lanes (DC in 1..16), every lane ending with its
+// group's total (DPP butterfly within a 16-lane row)
+template <int DC>
+__device__ __forceinline__ int32_t chunk_sum(int32_t v) {
+  if constexpr (DC >= 2) v += dpp_mov<DPP_QUAD_XOR1>(v);
+  if constexpr (DC >= 4) v += dpp_mov<DPP_QUAD_XOR2>(v);
+  if constexpr (DC >= 8) v += dpp_mov<DPP_HALF_MIRROR>(v);
+  if constexpr (DC >= 16) v += dpp_mov<DPP_ROW_MIRROR>(v);
+  return v;
+}
+
+__device__ __forceinline__ int32_t dot16(const v4i& a, const v4i& b) {
+  int32_t s = __builtin_amdgcn_sdot4(a.x, b.x, 0, false);
+  s = __builtin_amdgcn_sdot4(a.y, b.y, s, false);
+  s = __builtin_amdgcn_sdot4(a.z, b.z, s, false);
+  return __builtin_amdgcn_sdot4(a.w, b.w, s, false);
+}
+
+// The output projection's partial sums of head h from its D output bytes in LDS (one row).  Lane l
+// takes 16-byte chunk l % DC of panel column n (64 / DC consecutive columns per wave load, so the
+// loads are contiguous); the DC lanes of a column add their products and the first one adds the
+// column's sum into the accumulators.  wpre holds this thread's first NPF chunks.
+template <int D, int NPF>
+__device__ __forceinline__ void wo_partial(const AttnArgs& p, int h, const int8_t* ah, const v4i* wpre) {
+  constexpr int DC = D / 16;
+  const int lane = threadIdx.x & 63, kc = lane % DC;
+  const int cpb = (int)(blockDim.x / DC);  // columns per block-wide load
+  const int c0 = (int)(threadIdx.x / DC);
+  const v4i a = *reinterpret_cast<const v4i*>(ah + 16 * kc);
+#pragma unroll
+  for (int i = 0; i < NPF; ++i) {
+    const int n = c0 + i * cpb;
+    const int32_t s = chunk_sum<DC>(dot16(a, wpre[i]));
+    if (kc == 0 && n < p.wo_N && s != 0) atomic_add_dev(p.wo_acc + n, s);
+  }
+  const Rsrc wr = rsrc(p.wop + (int64_t)h * p.wo_N * D, (int64_t)p.wo_N * D);
+  for (int n0 = NPF * cpb; n0 < p.wo_N; n0 += cpb) {
+    const int n = c0 + n0;
+    const int32_t s = chunk_sum<DC>(dot16(a, ld16(wr, n < p.wo_N ? (uint32_t)(n * D + 16 * kc) : LD_OOB)));
+    if (kc == 0 && n < p.wo_N && s != 0) atomic_add_dev(p.wo_acc + n, s);
+  }
+}
+
+// this thread's first NPF chunks of head h's output-projection panel (the layout of wo_partial)
+template <int D, int NPF>
+__device__ __forceinline__ void wo_prefetch(const AttnArgs& p, int h, v4i* wpre) {
+  constexpr int DC = D / 16;
+  const int kc = (threadIdx.x & 63) % DC, cpb = (int)(blockDim.x / DC), c0 = (int)(threadIdx.x / DC);
+  const Rsrc wr = rsrc(p.wop + (int64_t)h * p.wo_N * D, (int64_t)p.wo_N * D);
+#pragma unroll
+  for (int i = 0; i < NPF; ++i) {
+    const int n = c0 + i * cpb;
+    wpre[i] = ld16(wr, n < p.wo_N ? (uint32_t)(n * D + 16 * kc) : LD_OOB);
+  }
+}
 
 constexpr int ATTN_THREADS = 512;
 constexpr int ATTN_WAVES = ATTN_THREADS / 64;
@@ -81,13 +154,16 @@ __device__ __forceinline__ uint32_t lut_prob_lds(int64_t z, const uint16_t* ei, 
 // Loads at entry, in order of use: q and the keys of the first score pass, the LUT dwords (wave
 // 0), then the value rows of this thread's first VPF keys, so each phase waits only for its own
 // group and the value latency hides behind the score and softmax phases.  Keys >= T read zeros.
-template <int D>
+template <int D, bool WO>
 __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   kernarg_warm<sizeof(AttnArgs)>();
   extern __shared__ int32_t sc[];  // [lds_T] scores, then probabilities
   __shared__ int32_t redmax[ATTN_WAVES], redsum[ATTN_WAVES];
   __shared__ uint32_t lut32[LUT_DW];
   __shared__ int32_t wpart[4 * ATTN_WAVES][D];
+  __shared__ __attribute__((aligned(16))) int8_t ah[WO ? D : 16];
+  // output-projection panel chunks per thread loaded ahead (covering 1024 columns x D bytes)
+  constexpr int WPF = WO ? (D <= 128 ? (1024 * (D / 16)) / ATTN_THREADS : 16) : 0;
   constexpr int DC = D / 16;  // 16-byte chunks per key row
   constexpr int TG = ATTN_THREADS / DC;
   constexpr int VPF = 8;
@@ -104,25 +180,24 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   const int h = g * G + xk % G;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   // Loads in order of use: q and the keys of the first score pass, the LUT dwords (wave 0), the
-  // value rows of this thread's first VPF keys.  Key rows at or past T read zeros.
-  // row m's context: T = position + 1 (row m of a launch at pos sits at pos + m; with per-row
-  // positions, row m is its own sequence in cache slot m), never past the cache
-  const int T = min((p.row_pos ? *(const __attribute__((address_space(4))) int32_t*)(p.row_pos + m)
-                               : load_pos(p.pos_dev, p.pos) + m) + 1,
-                    (int)p.max_seq);
+  // value rows of this thread's first VPF keys.  The cache rows are addressed over the whole cache,
+  // so these loads do not wait for the device position; rows at or past T are masked out below
+  // (their scores are never kept, their probabilities are zero).
   const int64_t slot = p.row_pos ? m * p.slot_stride : 0;
   const int8_t* kbase = p.kc + slot + (int64_t)g * p.max_seq * D;
   const int8_t* vbase = p.vc + slot + (int64_t)g * p.max_seq * D;
   const Rsrc qr = rsrc(p.q + (int64_t)m * p.ldq + (int64_t)h * D, D);
-  const Rsrc kr = rsrc(kbase, (int64_t)T * D), vr = rsrc(vbase, (int64_t)T * D);
-  v4i qv[DC], k0[DC], k1[DC];
-  const int t0 = tid, t1 = tid + ATTN_THREADS;
+  const Rsrc kr = rsrc(kbase, (int64_t)p.max_seq * D), vr = rsrc(vbase, (int64_t)p.max_seq * D);
+  // Score pass layout: lane l takes 16-byte chunk kc = l % DC of key kw + i * KPB, so one wave load
+  // covers 64 / DC consecutive keys (1 KiB contiguous) and the DC lanes of a key add their partial
+  // dot products with DPP.  The first KPF loads per lane are issued here.
+  constexpr int KPB = (64 / DC) * ATTN_WAVES;              // keys per block-wide load
+  constexpr int KPF = (D <= 128 ? 1024 : 512) / KPB;      // loads per lane issued at entry
+  const int kc = lane % DC, kw = wave * (64 / DC) + lane / DC;
+  const v4i qc = ld16(qr, 16 * kc);
+  v4i kpf[KPF];
 #pragma unroll
-  for (int c = 0; c < DC; ++c) {
-    qv[c] = ld16(qr, 16 * c);
-    k0[c] = ld16(kr, (uint32_t)(t0 * D + 16 * c));
-    k1[c] = ld16(kr, (uint32_t)(t1 * D + 16 * c));
-  }
+  for (int i = 0; i < KPF; ++i) kpf[i] = ld16(kr, (uint32_t)((i * KPB + kw) * D + 16 * kc));
   issue_fence();
   uint32_t lw[3];
   {
@@ -142,35 +217,43 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
 #pragma unroll
   for (int u = 0; u < VPF; ++u) vpre[u] = ld16(vr, (uint32_t)((tg + u * TG) * D + 16 * dc));
   issue_fence();
+  // row m's context T = position + 1 (row m of a launch at pos sits at pos + m; with per-row
+  // positions, row m is its own sequence in cache slot m), never past the cache.  A scalar load
+  // issued after the vector loads: a wait for it waits for every earlier scalar load.
+  const int T = min((p.row_pos ? *(const __attribute__((address_space(4))) int32_t*)(p.row_pos + m)
+                               : load_pos(p.pos_dev, p.pos) + m) + 1,
+                    (int)p.max_seq);
+  if (WO && h == 0 && m == 0) zero_words(p.zero, p.zero_n);
 
   // scores s[t] = q . k[t] (int32, |s| <= D * 2^14)
   int32_t lmax = INT32_MIN;
-  {
-    const int32_t s0 = dot_row<D>(qv, k0), s1 = dot_row<D>(qv, k1);
-    if (t0 < T) {
-      sc[t0] = s0;
-      lmax = s0;
-    }
-    if (t1 < T) {
-      sc[t1] = s1;
-      lmax = max(lmax, s1);
-    }
-  }
-  for (int ta = tid + 2 * ATTN_THREADS; ta < T; ta += 2 * ATTN_THREADS) {
-    const int tb = ta + ATTN_THREADS;
 #pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      k0[c] = ld16(kr, (uint32_t)(ta * D + 16 * c));
-      k1[c] = ld16(kr, (uint32_t)(tb * D + 16 * c));
-    }
-    const int32_t s0 = dot_row<D>(qv, k0), s1 = dot_row<D>(qv, k1);
-    sc[ta] = s0;
-    lmax = max(lmax, s0);
-    if (tb < T) {
-      sc[tb] = s1;
-      lmax = max(lmax, s1);
+  for (int i = 0; i < KPF; ++i) {
+    const int t = i * KPB + kw;
+    const int32_t sv = chunk_sum<DC>(dot16(qc, kpf[i]));
+    if (kc == 0 && t < T) {
+      sc[t] = sv;
+      lmax = max(lmax, sv);
     }
   }
+  for (int t0 = KPF * KPB; t0 < T; t0 += 4 * KPB) {
+    v4i kv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) kv[u] = ld16(kr, (uint32_t)((t0 + u * KPB + kw) * D + 16 * kc));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u * KPB + kw;
+      const int32_t sv = chunk_sum<DC>(dot16(qc, kv[u]));
+      if (kc == 0 && t < T) {
+        sc[t] = sv;
+        lmax = max(lmax, sv);
+      }
+    }
+  }
+  // the output-projection panel columns of this thread, requested once the score loads are
+  // consumed: they are needed last and their loads overlap the softmax and the value pass
+  v4i wpre[WPF > 0 ? WPF : 1];
+  if constexpr (WPF > 0) wo_prefetch<D, WPF>(p, h, wpre);
   if (wave == 0) {
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -257,7 +340,13 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
 #pragma unroll
     for (int w = 0; w < 4 * ATTN_WAVES; ++w) o += wpart[w][d];
     if (p.pb == 15) o = rshr32(o, 7);
-    p.out[(int64_t)m * p.ldo + (int64_t)h * D + d] = (int8_t)sat8(mulshift(o, p.Mo, p.So));
+    const int8_t y = (int8_t)sat8(mulshift(o, p.Mo, p.So));
+    p.out[(int64_t)m * p.ldo + (int64_t)h * D + d] = y;
+    if constexpr (WO) ah[d] = y;
+  }
+  if constexpr (WO) {
+    __syncthreads();
+    wo_partial<D, WPF>(p, h, ah, wpre);
   }
 }
 
@@ -786,6 +875,27 @@ __global__ __launch_bounds__(256) void attention_split_finish(AttnArgs p, int S,
   p.out[(int64_t)(rb * AT_ROWS + row) * p.ldo + (int64_t)h * D + d] = (int8_t)sat8(mulshift(o, p.Mo, p.So));
 }
 
+// split-context finish of one row with the output projection: workgroup h sums the S value
+// partials of head h, requantises the head's D outputs, then adds its output-projection partial sums
+template <int D>
+__global__ __launch_bounds__(256) void attention_split_finish_wo(AttnArgs p, int S, const int32_t* ws) {
+  __shared__ __attribute__((aligned(16))) int8_t ah[D];
+  const int h = blockIdx.x;
+  const int64_t pairs = p.H;
+  const int32_t* outv = ws + 2 * pairs * S * AT_ROWS + (int64_t)h * S * AT_ROWS * D;
+  if (h == 0) zero_words(p.zero, p.zero_n);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    int32_t o = 0;
+    for (int q = 0; q < S; ++q) o += outv[(int64_t)q * AT_ROWS * D + d];
+    if (p.pb == 15) o = rshr32(o, 7);
+    const int8_t y = (int8_t)sat8(mulshift(o, p.Mo, p.So));
+    p.out[(int64_t)h * D + d] = y;
+    ah[d] = y;
+  }
+  __syncthreads();
+  wo_partial<D, 0>(p, h, ah, nullptr);
+}
+
 __global__ void kv_write_kernel(const int8_t* __restrict__ k, const int8_t* __restrict__ v, int64_t M, int Hkv, int D,
                                 int64_t ldk, int64_t ldv, int pos, const int32_t* __restrict__ pos_dev,
                                 const int32_t* __restrict__ row_pos, int64_t slot_stride, int8_t* __restrict__ kc,
@@ -833,11 +943,19 @@ namespace llhip {
 // llhip_attention with the split-context partials in `split_ws` (split_bytes long; NULL disables
 // the split): the launch plan is the same for both entry points, except that a plan whose
 // partials would not fit takes fewer key splits, or none.
+// The output projection folded into a one-row launch (decode chain): panel, accumulators, rows to clear.
+struct WoFold {
+  const int8_t* wop;
+  int32_t* acc;
+  int32_t* zero;
+  int64_t N, zero_n;
+};
+
 static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
                           const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
                           const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
                           int64_t prob_bits, int8_t* out, int64_t ldo, void* split_ws, int64_t split_bytes,
-                          void* stream) {
+                          void* stream, const WoFold* fold = nullptr) {
   if (prob_bits != 8 && prob_bits != 15) return fail(-EINVAL, "attention prob_bits must be 8 or 15");
   if (M < 0 || H <= 0 || Hkv <= 0 || H % Hkv) return fail(-EINVAL, "attention: H must be a multiple of Hkv");
   if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256)
@@ -876,6 +994,18 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   p.pb = (int)prob_bits;
   p.lds_T = (int)((tmax + 3) / 4 * 4);
   p.M = (int)M;
+  if (fold) {
+    if (M != 1 || row_pos) return fail(-EINVAL, "dec_attention: one row, one sequence");
+    if (!fold->wop || !fold->acc || fold->N < 1 || fold->N > INT32_MAX / D || (uintptr_t)fold->wop % 16 ||
+        fold->zero_n < 0 || fold->zero_n > INT32_MAX || (fold->zero_n && !fold->zero) || (uintptr_t)fold->zero % 16)
+      return fail(-EINVAL, "dec_attention: bad output-projection panel or accumulators");
+    if (H * fold->N * D >= (1ll << 31)) return fail(-EINVAL, "dec_attention: panel above 2 GiB");
+    p.wop = fold->wop;
+    p.wo_acc = fold->acc;
+    p.wo_N = (int)fold->N;
+    p.zero = fold->zero;
+    p.zero_n = (int)fold->zero_n;
+  }
   hipStream_t s = (hipStream_t)stream;
   const int cus = current_cu_count();
   // Long contexts with few (row block, head) pairs: split the key tiles over S workgroups per pair
@@ -899,7 +1029,10 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   hipLaunchKernelGGL((attention_split<DD, 1>), grid, block, 0, s, p, S, tps, sw);           \
   hipLaunchKernelGGL((attention_split<DD, 2>), grid, block, 0, s, p, S, tps, sw);           \
   hipLaunchKernelGGL((attention_split<DD, 3>), grid, block, 0, s, p, S, tps, sw);           \
-  hipLaunchKernelGGL((attention_split_finish<DD>), fgrid, dim3(256), 0, s, p, S, sw);
+  if (fold)                                                                                 \
+    hipLaunchKernelGGL((attention_split_finish_wo<DD>), dim3((unsigned)H), dim3(256), 0, s, p, S, sw); \
+  else                                                                                      \
+    hipLaunchKernelGGL((attention_split_finish<DD>), fgrid, dim3(256), 0, s, p, S, sw);
     switch (D) {
       case 16: LLHIP_SPLIT(16) break;
       case 32: LLHIP_SPLIT(32) break;
@@ -936,13 +1069,19 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   if (M * Hkv > (int64_t)INT32_MAX / 8 / (H / Hkv)) return fail(-EINVAL, "attention: too many rows");
   dim3 grid((unsigned)(8 * ceil_div(M * Hkv, 8) * (H / Hkv)));
   dim3 block(ATTN_THREADS);
+#define LLHIP_ROWHEAD(DD)                                                            \
+  if (fold)                                                                         \
+    hipLaunchKernelGGL((attention_rowhead<DD, true>), grid, block, lds, s, p);      \
+  else                                                                              \
+    hipLaunchKernelGGL((attention_rowhead<DD, false>), grid, block, lds, s, p);
   switch (D) {
-    case 16: hipLaunchKernelGGL(attention_rowhead<16>, grid, block, lds, s, p); break;
-    case 32: hipLaunchKernelGGL(attention_rowhead<32>, grid, block, lds, s, p); break;
-    case 64: hipLaunchKernelGGL(attention_rowhead<64>, grid, block, lds, s, p); break;
-    case 128: hipLaunchKernelGGL(attention_rowhead<128>, grid, block, lds, s, p); break;
-    default: hipLaunchKernelGGL(attention_rowhead<256>, grid, block, lds, s, p); break;
+    case 16: LLHIP_ROWHEAD(16) break;
+    case 32: LLHIP_ROWHEAD(32) break;
+    case 64: LLHIP_ROWHEAD(64) break;
+    case 128: LLHIP_ROWHEAD(128) break;
+    default: LLHIP_ROWHEAD(256) break;
   }
+#undef LLHIP_ROWHEAD
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
@@ -989,6 +1128,17 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   return attention_impl(q, M, H, Hkv, D, ldq, pos, pos_dev, row_pos, slot_stride, kc, vc, max_seq, Ms, Ss, Mo, So,
                         prob_bits, out, ldo, ws ? static_cast<char*>(ws) + WS_SCRATCH : nullptr, WS_SCRATCH_BYTES,
                         stream);
+}
+
+int llhip_dec_attention(const llhip_dec_attn_desc* d, void* ws, void* stream) {
+  if (!d) return fail(-EINVAL, "dec_attention: null descriptor");
+  WoFold f{static_cast<const int8_t*>(d->wo_panel), static_cast<int32_t*>(d->acc), static_cast<int32_t*>(d->zero),
+           d->N, d->zero_n};
+  return attention_impl(static_cast<const int8_t*>(d->q), 1, d->H, d->Hkv, d->D, d->H * d->D, d->pos,
+                        static_cast<const int32_t*>(d->pos_dev), nullptr, 0, static_cast<const int8_t*>(d->kc),
+                        static_cast<const int8_t*>(d->vc), d->max_seq, d->Ms, d->Ss, d->Mo, d->So, d->prob_bits,
+                        static_cast<int8_t*>(d->out), d->H * d->D, ws ? static_cast<char*>(ws) + WS_SCRATCH : nullptr,
+                        WS_SCRATCH_BYTES, stream, &f);
 }
 
 int llhip_attention_noalloc(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,

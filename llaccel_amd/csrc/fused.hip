@@ -22,6 +22,8 @@
 // zeros), and waits for each group only where it is used: the RMSNorm prologue runs while the
 // weights are in flight.  No workgroup depends on another inside a launch (no device-scope
 // synchronisation).
+#include <algorithm>
+
 #include "../../include/llhip.h"
 #include "common.h"
 
@@ -260,6 +262,122 @@ __device__ __forceinline__ void sig_store(const SigRegs& r, uint32_t* sig32) {
 }
 
 // ---------------------------------------------------------------------------------------
+// decode-chain prologue (one row): the row x finishes the previous projection, then RMSNorm and
+// quant of x (golden.py:316-342 resadd epilogue, then 124-137 and 119-120)
+// ---------------------------------------------------------------------------------------
+// The previous launch left that projection (linear W, epilogue resadd with residual aux) as exact
+// int32 partial sums in R accumulator rows; x[n] = sat16(sat16(mulshift(sum_r acc[r][n] + bias[n],
+// M_n, S_n)) + aux[n]).  Without partial sums x is read from memory (the first layer).  Thread t
+// owns the 4-element unit t of the row; every operand is loaded at kernel entry (null operands
+// read zeros), and the sum of squares is one block reduction.
+struct ResidArgs {
+  const int32_t* acc;  // [R][K] int32 partial sums, or null (x is read from pre.x)
+  const int32_t* rq;   // [K][2] requant pairs of the projection
+  const int32_t* bias; // [K] or null
+  const int16_t* aux;  // [K] residual
+  int16_t* x_out;      // [K] the finished row, written by workgroup 0
+  int R;
+};
+constexpr int RESID_MAXR = 8;
+
+struct ResidRegs {
+  v4i acc[RESID_MAXR];
+  v4i rq[2];
+  v4i bias;
+  v2i x, g;
+};
+
+__device__ __forceinline__ void resid_prefetch(const NormQuant& pr, const ResidArgs& ra, ResidRegs& r) {
+  const int u = threadIdx.x, K = pr.K;
+  const bool in = u < (K >> 2);
+  const bool fin = ra.acc != nullptr;
+#pragma unroll
+  for (int i = 0; i < RESID_MAXR; ++i) r.acc[i] = v4i{0, 0, 0, 0};
+  r.rq[0] = r.rq[1] = r.bias = v4i{0, 0, 0, 0};
+  r.x = r.g = v2i{0, 0};
+  // waves past the row's units issue nothing (a load instruction costs address-unit cycles for
+  // all 64 lanes, in range or not)
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 256 >= K) return;
+  const Rsrc ar = rsrc(ra.acc, (int64_t)ra.R * K * 4);
+#pragma unroll
+  for (int i = 0; i < RESID_MAXR; ++i)
+    if (i < ra.R) r.acc[i] = ld16(ar, in ? (uint32_t)((i * K + 4 * u) * 4) : LD_OOB);
+  const Rsrc qr = rsrc(fin ? ra.rq : nullptr, (int64_t)K * 8);
+  r.rq[0] = ld16(qr, in ? 32u * u : LD_OOB);
+  r.rq[1] = ld16(qr, in ? 32u * u + 16u : LD_OOB);
+  r.bias = ld16(rsrc(fin ? ra.bias : nullptr, (int64_t)K * 4), in ? 16u * u : LD_OOB);
+  // x: the residual when finishing, else the row itself
+  r.x = ld8(rsrc(fin ? (const void*)ra.aux : (const void*)pr.x, (int64_t)K * 2), in ? 8u * u : LD_OOB);
+  r.g = ld8(rsrc(pr.gamma, (int64_t)K * 2), in ? 8u * u : LD_OOB);
+}
+
+// x, RMSNorm, quant of the row into a_lds (i8); workgroup 0 writes x (when finishing), h_out and
+// hq_out.  red64 is LDS for one u64 per wave.  Ends with a barrier.
+__device__ __forceinline__ void resid_norm_quant(const NormQuant& pr, const ResidArgs& ra, const ResidRegs& r,
+                                                 int8_t* a_lds, bool write_global, uint64_t* red64) {
+  const int u = threadIdx.x, lane = u & 63, wave = u >> 6, nw = blockDim.x >> 6;
+  const bool in = u < (pr.K >> 2);
+  int32_t xv[4] = {lo16(r.x.x), hi16(r.x.x), lo16(r.x.y), hi16(r.x.y)};
+  if (ra.acc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int32_t s = 0;
+#pragma unroll
+      for (int i = 0; i < RESID_MAXR; ++i) s += r.acc[i][j];  // |sum| < 2^31: an exact K-split of one dot product
+      const int32_t M = r.rq[j >> 1][2 * (j & 1)], S = r.rq[j >> 1][2 * (j & 1) + 1];
+      const int64_t t = sat16(mulshift((int64_t)s + r.bias[j], (int64_t)M, S));
+      xv[j] = (int32_t)sat16(t + xv[j]);
+    }
+  }
+  uint64_t ss = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ss += (uint64_t)(uint32_t)(xv[j] * xv[j]);
+  ss = wave_sum_u64(ss);
+  if (lane == 0) red64[wave] = ss;
+  __syncthreads();
+  uint64_t tot = 0;
+  for (int w = 0; w < nw; ++w) tot += red64[w];
+  const uint32_t inv = rms_inv(tot, pr.eps_t, pr.C);
+  if (in) {
+    const int32_t g[4] = {lo16(r.g.x), hi16(r.g.x), lo16(r.g.y), hi16(r.g.y)};
+    int16_t y[4];
+    uint32_t q = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      y[j] = rms_apply(xv[j], g[j], inv, pr.sh_post);
+      q |= (uint32_t)(uint8_t)sat8(mulshift(y[j], pr.Mq, pr.Sq)) << (8 * j);
+    }
+    *reinterpret_cast<uint32_t*>(a_lds + 4 * u) = q;
+    if (write_global) {
+      if (ra.acc && ra.x_out) {
+        v2i xo;
+        xo.x = pack16(xv[0], xv[1]);
+        xo.y = pack16(xv[2], xv[3]);
+        *reinterpret_cast<v2i*>(ra.x_out + 4 * u) = xo;
+      }
+      if (pr.h_out) {
+        v2i yo;
+        yo.x = pack16(y[0], y[1]);
+        yo.y = pack16(y[2], y[3]);
+        *reinterpret_cast<v2i*>(pr.h_out + 4 * u) = yo;
+      }
+      if (pr.hq_out) *reinterpret_cast<uint32_t*>(pr.hq_out + 4 * u) = q;
+    }
+  }
+  __syncthreads();
+}
+
+// zero n int32 accumulators (the next projection's) from one workgroup
+__device__ __forceinline__ void zero_rows(int32_t* p, int n) {
+  if (!p) return;
+  for (int i = 4 * threadIdx.x; i < n; i += 4 * blockDim.x) {
+    if (i + 4 <= n) *reinterpret_cast<v4i*>(p + i) = v4i{0, 0, 0, 0};
+    else
+      for (int j = i; j < n; ++j) p[j] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // weight slices: W [N][K] i8, 16 columns x one wave's K steps
 // ---------------------------------------------------------------------------------------
 // The first PF 64-deep K steps of a wave's slice are loaded at kernel entry; longer slices stream
@@ -347,6 +465,11 @@ struct AttnInArgs {
   int8_t* vc;
   int64_t max_seq;
   int M, H, Hkv, D, K, pos, KS, has_norm;
+  // decode chain (RESID kernels, M = 1): the row from the previous projection's partial sums, and
+  // the accumulators this launch clears for the attention's output projection
+  ResidArgs res;
+  int32_t* zero;
+  int zero_n;
 };
 
 // per-role kernel arguments chosen by scalar selects of the three values (an indexed read of the
@@ -357,12 +480,13 @@ __device__ __forceinline__ T pick3(int role, const T (&v)[3]) {
   return role == 0 ? a : (role == 1 ? b : c);
 }
 
-template <int MAXW>
+template <int MAXW, bool RESID>
 __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   kernarg_warm<sizeof(AttnInArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   __shared__ v4i red[MAXW][64];
   __shared__ int32_t rowpos[16];
+  __shared__ uint64_t red64[MAXW];
   const int lda = p.K + 16;
   int8_t* a_lds = dyn;                                                         // [M][lda] i8
   int32_t* hres = reinterpret_cast<int32_t*>(dyn + ((p.M * lda + 15) & ~15));  // [M][D] i32
@@ -390,7 +514,10 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   const NormMap nm = norm_map(M);
   NormRegs nr;
   PreRows pq;
-  if (p.pre.prequant)
+  ResidRegs rr;
+  if constexpr (RESID)
+    resid_prefetch(p.pre, p.res, rr);
+  else if (p.pre.prequant)
     prerows_load(p.pre, M, pq);
   else
     norm_prefetch(p.pre, M, nm, nr);
@@ -417,10 +544,14 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   }
   issue_fence();
 
-  if (p.pre.prequant)
+  if constexpr (RESID) {
+    if (b == 0) zero_rows(p.zero, p.zero_n);
+    resid_norm_quant(p.pre, p.res, rr, a_lds, b == 0, red64);
+  } else if (p.pre.prequant) {
     prerows_store(p.pre, M, pq, a_lds, lda);
-  else
+  } else {
     norm_quant_rows(p.pre, nr, M, nm, a_lds, lda, b == 0);
+  }
   const int pos0 = p.pos_dev ? __builtin_amdgcn_readfirstlane(posv) : p.pos;
   const bool rows = p.row_pos != nullptr;
   if (tid < M) rowpos[tid] = rows ? rp_own : pos0 + tid;
@@ -532,14 +663,25 @@ struct MlpInArgs {
   int64_t silu_Mi, fq_M;
   int silu_Si, silu_sh, mul_sh, fq_S;
   int M, N, K, KS;
+  // decode chain (RESID kernels, M = 1): the row from the output projection's partial sums, and the
+  // down projection's partial sums of this workgroup's 16 FFN columns: wd_acc[r][n] +=
+  // sum_j fq[16 b + j] * Wd[n][16 b + j] with the panel wdp[b][n][j] = Wd[n][16 b + j]
+  ResidArgs res;
+  const int8_t* wdp;
+  int32_t* wd_acc;
+  int wd_R, wd_N;
 };
 
-template <int MAXW>
+constexpr int WD_PF = 4;  // down-projection panel columns per thread loaded at kernel entry
+
+template <int MAXW, bool RESID>
 __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   kernarg_warm<sizeof(MlpInArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   __shared__ v4i red[MAXW][64];
   __shared__ uint32_t sig32[129];
+  __shared__ uint64_t red64[MAXW];
+  __shared__ __attribute__((aligned(16))) int8_t fq16[16];
   const int lda = p.K + 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int col = lane & 15, kg = lane >> 4;
@@ -548,7 +690,10 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   const NormMap nm = norm_map(p.M);
   NormRegs nr;
   PreRows pq;
-  if (p.pre.prequant)
+  ResidRegs rr;
+  if constexpr (RESID)
+    resid_prefetch(p.pre, p.res, rr);
+  else if (p.pre.prequant)
     prerows_load(p.pre, p.M, pq);
   else
     norm_prefetch(p.pre, p.M, nm, nr);
@@ -571,8 +716,20 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   const int32_t bgv = ld4(rsrc(p.bg, (int64_t)p.N * 4), o4);
   const int32_t buv = ld4(rsrc(p.bu, (int64_t)p.N * 4), o4);
   issue_fence();
+  v4i wdv[WD_PF];  // this thread's first down-projection panel columns
+  if constexpr (RESID) {
+    const Rsrc dr = rsrc(p.wdp + (int64_t)blockIdx.x * p.wd_N * 16, (int64_t)p.wd_N * 16);
+#pragma unroll
+    for (int i = 0; i < WD_PF; ++i) {
+      const int c = tid + i * (int)blockDim.x;
+      wdv[i] = ld16(dr, c < p.wd_N ? 16u * c : LD_OOB);
+    }
+    issue_fence();
+  }
 
-  if (p.pre.prequant)
+  if constexpr (RESID)
+    resid_norm_quant(p.pre, p.res, rr, dyn, blockIdx.x == 0, red64);
+  else if (p.pre.prequant)
     prerows_store(p.pre, p.M, pq, dyn, lda);
   else
     norm_quant_rows(p.pre, nr, p.M, nm, dyn, lda, blockIdx.x == 0);
@@ -580,27 +737,55 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   __syncthreads();
   red[wave][lane] = wslice_mfma(ws, wr, dyn, lda, p.M, p.K);
   __syncthreads();
-  if (wave != 0 || n >= p.N) return;
-  v4i ag = red[0][lane], au = red[p.KS][lane];
-  for (int ks = 1; ks < p.KS; ++ks) {
-    v4_add(ag, red[ks][lane]);
-    v4_add(au, red[p.KS + ks][lane]);
-  }
-  const uint16_t* sig = reinterpret_cast<const uint16_t*>(sig32);
+  if (wave == 0) {
+    v4i ag = red[0][lane], au = red[p.KS][lane];
+    for (int ks = 1; ks < p.KS; ++ks) {
+      v4_add(ag, red[ks][lane]);
+      v4_add(au, red[p.KS + ks][lane]);
+    }
+    const uint16_t* sig = reinterpret_cast<const uint16_t*>(sig32);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * kg + r;
-    if (m >= p.M) continue;
-    const int64_t o = (int64_t)m * p.N + n;
-    const int64_t tg = sat16(mulshift((int64_t)ag[r] + bgv, rg.x, rg.y));
-    const int64_t tu = sat16(mulshift((int64_t)au[r] + buv, ru.x, ru.y));
-    if (p.g_out) p.g_out[o] = (int16_t)tg;
-    if (p.u_out) p.u_out[o] = (int16_t)tu;
-    const int64_t sg = silu16_lds(tg, p.silu_Mi, p.silu_Si, p.silu_sh, sig);
-    const int64_t f = sat16(rshr(tu * sg, p.mul_sh));
-    p.sg_out[o] = (int16_t)sg;
-    p.f_out[o] = (int16_t)f;
-    p.fq_out[o] = (int8_t)sat8(mulshift(f, p.fq_M, p.fq_S));
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * kg + r;
+      if (m >= p.M) continue;
+      int8_t fq = 0;
+      if (n < p.N) {
+        const int64_t o = (int64_t)m * p.N + n;
+        const int64_t tg = sat16(mulshift((int64_t)ag[r] + bgv, rg.x, rg.y));
+        const int64_t tu = sat16(mulshift((int64_t)au[r] + buv, ru.x, ru.y));
+        if (p.g_out) p.g_out[o] = (int16_t)tg;
+        if (p.u_out) p.u_out[o] = (int16_t)tu;
+        const int64_t sg = silu16_lds(tg, p.silu_Mi, p.silu_Si, p.silu_sh, sig);
+        const int64_t f = sat16(rshr(tu * sg, p.mul_sh));
+        p.sg_out[o] = (int16_t)sg;
+        p.f_out[o] = (int16_t)f;
+        fq = (int8_t)sat8(mulshift(f, p.fq_M, p.fq_S));
+        p.fq_out[o] = fq;
+      }
+      if (RESID && m == 0) fq16[col] = fq;  // columns past N contribute nothing (zero panel bytes)
+    }
+  }
+  if constexpr (!RESID) return;
+  // down projection: the 16 quantised FFN values of this workgroup against every output column
+  __syncthreads();
+  const v4i f4 = *reinterpret_cast<const v4i*>(fq16);
+  int32_t* acc = p.wd_acc + (int64_t)(blockIdx.x % p.wd_R) * p.wd_N;
+  auto dot16 = [&](const v4i& w) {
+    int32_t d = __builtin_amdgcn_sdot4(f4.x, w.x, 0, false);
+    d = __builtin_amdgcn_sdot4(f4.y, w.y, d, false);
+    d = __builtin_amdgcn_sdot4(f4.z, w.z, d, false);
+    return __builtin_amdgcn_sdot4(f4.w, w.w, d, false);
+  };
+#pragma unroll
+  for (int i = 0; i < WD_PF; ++i) {
+    const int c = tid + i * (int)blockDim.x;
+    const int32_t d = dot16(wdv[i]);
+    if (c < p.wd_N && d != 0) atomic_add_dev(acc + c, d);
+  }
+  const int8_t* panel = p.wdp + (int64_t)blockIdx.x * p.wd_N * 16;
+  for (int c = tid + WD_PF * (int)blockDim.x; c < p.wd_N; c += blockDim.x) {
+    const int32_t d = dot16(*reinterpret_cast<const v4i*>(panel + 16 * (int64_t)c));
+    if (d != 0) atomic_add_dev(acc + c, d);
   }
 }
 
@@ -618,6 +803,14 @@ struct NormGemvArgs {
   int64_t Mi;
   int aux_shift, Si, sh, epilogue, out_i8;
   int M, N, K, KS, TPW;
+  // decode chain (one row): with keys, the greedy step's first half -- keys[tile] = the best
+  // (value, lowest index) key of the tile's columns below vocab, and the row recorded at
+  // ring[*step] when *step < ring_cap
+  uint64_t* keys;
+  const int32_t* step;
+  int16_t* ring;
+  int64_t ring_ld;
+  int ring_cap, vocab;
 };
 
 template <int MAXW>
@@ -632,6 +825,8 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
   const int t = wave % p.TPW, ks = wave / p.TPW;
   const int n = (blockIdx.x * p.TPW + t) * 16 + col;
 
+  // the record slot of this decode launch (an earlier launch wrote it)
+  const int32_t stepv = ld4(rsrc(p.keys ? p.step : nullptr, 4), 0);
   const NormMap nm = norm_map(p.M);
   NormRegs nr;
   PreRows pq;
@@ -678,12 +873,12 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
     if (ks != 0) return;
     for (int j = 1; j < p.KS; ++j) v4_add(acc, red[t + j * p.TPW][lane]);
   }
-  if (n >= p.N) return;
   const uint16_t* sig = reinterpret_cast<const uint16_t*>(sig32);
+  uint64_t key = 0;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * kg + r;
-    if (m >= p.M) continue;
+    if (m >= p.M || n >= p.N) continue;
     const int64_t o = (int64_t)m * p.N + n;
     const int64_t v = mulshift((int64_t)acc[r] + bias, rq.x, rq.y);
     if (p.out_i8) {
@@ -695,6 +890,21 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
     else if (p.epilogue == 2) y = silu16_lds(y, p.Mi, p.Si, p.sh, sig);
     else if (p.epilogue == 3) y = sat16(rshr(y * aux[r], p.aux_shift));
     static_cast<int16_t*>(p.out)[o] = (int16_t)y;
+    if (p.keys && m == 0 && n < p.vocab) {
+      key = amax_key((int)y, n);
+      if (stepv < p.ring_cap) p.ring[(int64_t)stepv * p.ring_ld + n] = (int16_t)y;
+    }
+  }
+  if (p.keys) {
+    // the tile's best key: lanes 0..15 hold its 16 columns (row 0)
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+      const uint32_t lo = __shfl_xor((uint32_t)key, off), hi = __shfl_xor((uint32_t)(key >> 32), off);
+      const uint64_t o = ((uint64_t)hi << 32) | lo;
+      key = o > key ? o : key;
+    }
+    const int tile = blockIdx.x * p.TPW + t;
+    if (lane == 0 && tile * 16 < p.N) p.keys[tile] = key;
   }
 }
 
@@ -759,9 +969,8 @@ extern "C" int llhip_rmsnorm_quant(const llhip_norm_quant_desc* d, int64_t M, vo
   return 0;
 }
 
-extern "C" int llhip_attn_in(const llhip_attn_in_desc* d, void* stream) {
+static int attn_in_args(const llhip_attn_in_desc* d, AttnInArgs& p, int& waves, size_t& lds, int min_threads) {
   if (!d) return fail(-EINVAL, "attn_in: null descriptor");
-  AttnInArgs p{};
   int rc = fill_pre(p.pre, d->pre);
   if (rc) return rc;
   const int64_t M = d->M, H = d->H, Hkv = d->Hkv, D = d->D, K = d->pre.K;
@@ -812,22 +1021,77 @@ extern "C" int llhip_attn_in(const llhip_attn_in_desc* d, void* stream) {
   const int steps = (int)ceil_div(K, 64);
   if (!w_ok(H * D, K) || d->max_seq * D >= (1ll << 31)) return fail(-EINVAL, "attn_in: operand above 2 GiB");
   p.KS = pick_ks(H + 2 * Hkv, tiles, steps, tiles > FUSED_WAVES ? 16 : FUSED_WAVES);
-  const size_t lds = (size_t)((M * (K + 16) + 15) & ~15) + sizeof(int32_t) * (size_t)(M * D);
+  while (64 * tiles * p.KS < min_threads && p.KS < steps) ++p.KS;  // one row unit per thread
+  lds = (size_t)((M * (K + 16) + 15) & ~15) + sizeof(int32_t) * (size_t)(M * D);
   if (lds > 48 * 1024) return fail(-EINVAL, "attn_in: M*K too large for the LDS staging");
-  const int waves = tiles * p.KS;
+  waves = tiles * p.KS;
+  if (waves > 16 || 64 * waves < min_threads) return fail(-EINVAL, "attn_in: no workgroup shape fits");
+  return 0;
+}
+
+template <bool RESID>
+static int attn_in_launch(const AttnInArgs& p, int waves, size_t lds, void* stream) {
+  const dim3 grid((unsigned)(p.H + 2 * p.Hkv)), block(64 * waves);
   if (waves <= FUSED_WAVES)
-    hipLaunchKernelGGL(attn_in_kernel<FUSED_WAVES>, dim3((unsigned)(H + 2 * Hkv)), dim3(64 * waves), lds,
-                       (hipStream_t)stream, p);
+    hipLaunchKernelGGL((attn_in_kernel<FUSED_WAVES, RESID>), grid, block, lds, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL(attn_in_kernel<16>, dim3((unsigned)(H + 2 * Hkv)), dim3(64 * waves), lds, (hipStream_t)stream,
-                       p);
+    hipLaunchKernelGGL((attn_in_kernel<16, RESID>), grid, block, lds, (hipStream_t)stream, p);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
 
-extern "C" int llhip_mlp_in(const llhip_mlp_in_desc* d, void* stream) {
+static int fill_resid(ResidArgs& ra, const llhip_resid_desc* r, const NormQuant& pre) {
+  ra = ResidArgs{};
+  ra.R = 1;
+  if (!r || !r->acc) return 0;
+  if (r->R < 1 || r->R > RESID_MAXR) return fail(-EINVAL, "decode chain: %lld accumulator rows (1..%d)",
+                                                  (long long)r->R, RESID_MAXR);
+  if (!r->rq || !r->aux) return fail(-EINVAL, "decode chain: the finished projection needs rq and the residual");
+  if ((uintptr_t)r->acc % 16 || (uintptr_t)r->rq % 16 || (r->bias && (uintptr_t)r->bias % 16) ||
+      (uintptr_t)r->aux % 8 || (r->x_out && (uintptr_t)r->x_out % 8))
+    return fail(-EINVAL, "decode chain: misaligned operands");
+  if (pre.K % 4) return fail(-EINVAL, "decode chain: row width must be a multiple of 4");
+  ra.acc = static_cast<const int32_t*>(r->acc);
+  ra.rq = static_cast<const int32_t*>(r->rq);
+  ra.bias = static_cast<const int32_t*>(r->bias);
+  ra.aux = static_cast<const int16_t*>(r->aux);
+  ra.x_out = static_cast<int16_t*>(r->x_out);
+  ra.R = (int)r->R;
+  return 0;
+}
+
+static int check_zero(const void* zero, int64_t zero_n) {
+  if (zero_n < 0 || zero_n > INT32_MAX || (zero_n && !zero) || (uintptr_t)zero % 16)
+    return fail(-EINVAL, "decode chain: bad accumulator rows to clear");
+  return 0;
+}
+
+extern "C" int llhip_attn_in(const llhip_attn_in_desc* d, void* stream) {
+  AttnInArgs p{};
+  int waves = 0;
+  size_t lds = 0;
+  const int rc = attn_in_args(d, p, waves, lds, 0);
+  return rc ? rc : attn_in_launch<false>(p, waves, lds, stream);
+}
+
+extern "C" int llhip_dec_attn_in(const llhip_attn_in_desc* d, const llhip_resid_desc* r, void* zero, int64_t zero_n,
+                                 void* stream) {
+  if (!d) return fail(-EINVAL, "dec_attn_in: null descriptor");
+  if (d->M != 1 || d->row_pos || d->pre.prequant) return fail(-EINVAL, "dec_attn_in: one row, one sequence");
+  AttnInArgs p{};
+  int waves = 0;
+  size_t lds = 0;
+  int rc = attn_in_args(d, p, waves, lds, (int)(d->pre.K / 4));
+  if (!rc) rc = fill_resid(p.res, r, p.pre);
+  if (!rc) rc = check_zero(zero, zero_n);
+  if (rc) return rc;
+  p.zero = static_cast<int32_t*>(zero);
+  p.zero_n = (int)zero_n;
+  return attn_in_launch<true>(p, waves, lds, stream);
+}
+
+static int mlp_in_args(const llhip_mlp_in_desc* d, MlpInArgs& p, int min_threads) {
   if (!d) return fail(-EINVAL, "mlp_in: null descriptor");
-  MlpInArgs p{};
   int rc = fill_pre(p.pre, d->pre);
   if (rc) return rc;
   const int64_t M = d->M, N = d->N, K = d->pre.K;
@@ -859,17 +1123,47 @@ extern "C" int llhip_mlp_in(const llhip_mlp_in_desc* d, void* stream) {
   const int tiles = (int)ceil_div(N, 16);
   if (!w_ok(N, K)) return fail(-EINVAL, "mlp_in: weights above 2 GiB");
   p.KS = pick_ks(tiles, 2, (int)ceil_div(K, 64), FUSED_WAVES);
+  while (128 * p.KS < min_threads && 2 * p.KS < FUSED_WAVES) ++p.KS;  // one row unit per thread
+  if (128 * p.KS < min_threads) return fail(-EINVAL, "mlp_in: no workgroup shape fits");
   const size_t lds = (size_t)(M * (K + 16));
   if (lds > 48 * 1024) return fail(-EINVAL, "mlp_in: M*K too large for the LDS staging");
-  hipLaunchKernelGGL(mlp_in_kernel<FUSED_WAVES>, dim3((unsigned)tiles), dim3(64 * 2 * p.KS), lds, (hipStream_t)stream,
-                     p);
+  return 0;
+}
+
+extern "C" int llhip_mlp_in(const llhip_mlp_in_desc* d, void* stream) {
+  MlpInArgs p{};
+  const int rc = mlp_in_args(d, p, 0);
+  if (rc) return rc;
+  hipLaunchKernelGGL((mlp_in_kernel<FUSED_WAVES, false>), dim3((unsigned)ceil_div(p.N, 16)), dim3(128 * p.KS),
+                     (size_t)(p.M * (p.K + 16)), (hipStream_t)stream, p);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
 
-extern "C" int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream) {
+extern "C" int llhip_dec_mlp(const llhip_mlp_in_desc* d, const llhip_resid_desc* r, const void* wd_panel, void* wd_acc,
+                             int64_t R, int64_t N_out, void* stream) {
+  if (!d) return fail(-EINVAL, "dec_mlp: null descriptor");
+  if (d->M != 1 || d->pre.prequant) return fail(-EINVAL, "dec_mlp: one row");
+  MlpInArgs p{};
+  int rc = mlp_in_args(d, p, (int)(d->pre.K / 4));
+  if (!rc) rc = fill_resid(p.res, r, p.pre);
+  if (rc) return rc;
+  if (R < 1 || R > RESID_MAXR || N_out < 1 || N_out > INT32_MAX / 16 || !wd_panel || !wd_acc ||
+      (uintptr_t)wd_panel % 16 || (uintptr_t)wd_acc % 16)
+    return fail(-EINVAL, "dec_mlp: bad down-projection panel or accumulators");
+  if (!w_ok(ceil_div(p.N, 16) * 16, N_out)) return fail(-EINVAL, "dec_mlp: down-projection panel above 2 GiB");
+  p.wdp = static_cast<const int8_t*>(wd_panel);
+  p.wd_acc = static_cast<int32_t*>(wd_acc);
+  p.wd_R = (int)R;
+  p.wd_N = (int)N_out;
+  hipLaunchKernelGGL((mlp_in_kernel<FUSED_WAVES, true>), dim3((unsigned)ceil_div(p.N, 16)), dim3(128 * p.KS),
+                     (size_t)(p.M * (p.K + 16)), (hipStream_t)stream, p);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+static int norm_linear_args(const llhip_norm_linear_desc* d, NormGemvArgs& p, int min_threads) {
   if (!d) return fail(-EINVAL, "norm_linear: null descriptor");
-  NormGemvArgs p{};
   int rc = fill_pre(p.pre, d->pre);
   if (rc) return rc;
   const int64_t M = d->M, N = d->N, K = d->pre.K;
@@ -901,11 +1195,128 @@ extern "C" int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream) 
   // a wave's slice is loaded at entry; narrow ones split K further
   p.TPW = tiles >= 4096 ? 4 : 1;
   p.KS = p.TPW == 1 ? pick_ks(tiles, 1, steps, FUSED_WAVES) : (steps > PF ? 2 : 1);
-  const int blocks = (int)ceil_div(tiles, p.TPW);
+  while (64 * p.TPW * p.KS < min_threads && p.TPW * p.KS < FUSED_WAVES && p.KS < steps) ++p.KS;
+  if (64 * p.TPW * p.KS < min_threads) return fail(-EINVAL, "norm_linear: no workgroup shape fits");
   const size_t lds = (size_t)(M * (K + 16));
   if (lds > 48 * 1024) return fail(-EINVAL, "norm_linear: M*K too large for the LDS staging");
-  hipLaunchKernelGGL(norm_gemv_kernel<FUSED_WAVES>, dim3((unsigned)blocks), dim3(64 * p.TPW * p.KS), lds,
-                     (hipStream_t)stream, p);
+  return 0;
+}
+
+static int norm_linear_launch(const NormGemvArgs& p, void* stream) {
+  const int blocks = (int)ceil_div(ceil_div(p.N, 16), p.TPW);
+  hipLaunchKernelGGL((norm_gemv_kernel<FUSED_WAVES>), dim3((unsigned)blocks), dim3(64 * p.TPW * p.KS),
+                     (size_t)(p.M * (p.K + 16)), (hipStream_t)stream, p);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
+
+extern "C" int llhip_norm_linear(const llhip_norm_linear_desc* d, void* stream) {
+  NormGemvArgs p{};
+  const int rc = norm_linear_args(d, p, 0);
+  return rc ? rc : norm_linear_launch(p, stream);
+}
+
+// one row finished from partial sums, normalised and quantised by one workgroup (dec_finish)
+__global__ __launch_bounds__(256) void dec_finish_kernel(NormQuant pre, ResidArgs res) {
+  extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
+  __shared__ uint64_t red64[4];
+  ResidRegs rr;
+  resid_prefetch(pre, res, rr);
+  resid_norm_quant(pre, res, rr, dyn, true, red64);
+}
+
+extern "C" int llhip_dec_finish(const llhip_norm_quant_desc* d, const llhip_resid_desc* r, void* stream) {
+  if (!d) return fail(-EINVAL, "dec_finish: null descriptor");
+  NormQuant pre{};
+  int rc = fill_pre(pre, *d);
+  if (rc) return rc;
+  if (d->prequant || pre.K > 4 * 256) return fail(-EINVAL, "dec_finish: one row of at most 1024 values");
+  ResidArgs res{};
+  rc = fill_resid(res, r, pre);
+  if (rc) return rc;
+  hipLaunchKernelGGL(dec_finish_kernel, dim3(1), dim3(256), (size_t)(pre.K + 16), (hipStream_t)stream, pre, res);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int llhip_dec_head(const llhip_norm_linear_desc* d, int64_t vocab, void* keys, const int32_t* step,
+                              int16_t* ring, int64_t ring_ld, int64_t ring_cap, void* stream) {
+  if (!d) return fail(-EINVAL, "dec_head: null descriptor");
+  if (d->M != 1) return fail(-EINVAL, "dec_head: one row");
+  NormGemvArgs p{};
+  const int rc = norm_linear_args(d, p, 0);
+  if (rc) return rc;
+  if (keys) {
+    if (d->out_i8 || vocab < 1 || vocab > d->N || !step || (uintptr_t)keys % 8 || ring_cap < 0 ||
+        (ring_cap && (!ring || ring_ld < vocab)))
+      return fail(-EINVAL, "dec_head: bad greedy-step operands");
+    p.keys = static_cast<uint64_t*>(keys);
+    p.step = step;
+    p.ring = ring;
+    p.ring_ld = ring_ld;
+    p.ring_cap = (int)std::min<int64_t>(ring_cap, INT32_MAX);
+    p.vocab = (int)vocab;
+  }
+  return norm_linear_launch(p, stream);
+}
+
+// The greedy step of a decode chain (golden.py:376-377 and the record of golden.py:411-414): the
+// best of the tiles' keys is the first argmax; then token, record, position and step updates, and
+// the next launch's input row = embed[token] (golden.py:369-373).
+__global__ __launch_bounds__(1024) void dec_greedy_kernel(const uint64_t* __restrict__ keys, int nkeys, int32_t* token,
+                                                          int32_t* pos, int32_t* step, int32_t* ring_tok, int ring_cap,
+                                                          const int16_t* __restrict__ embed, int dim, int16_t* row) {
+  __shared__ uint64_t best[16];
+  __shared__ int32_t win;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t k = 0;
+  constexpr int BATCH = 16;  // keys in flight per thread
+  for (int base = tid; base < nkeys; base += BATCH * (int)blockDim.x) {
+    uint64_t v[BATCH];
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      const int i = base + j * (int)blockDim.x;
+      v[j] = i < nkeys ? keys[i] : 0ull;
+    }
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) k = v[j] > k ? v[j] : k;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)k, off), hi = __shfl_xor((uint32_t)(k >> 32), off);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    k = o > k ? o : k;
+  }
+  if (lane == 0) best[wave] = k;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t b = best[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) b = best[w] > b ? best[w] : b;
+    // every tile with a column below vocab wrote a nonzero key; a zero maximum cannot occur
+    const int32_t idx = b ? (int32_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull)) : 0;
+    win = idx;
+    *token = idx;
+    const int32_t s = *step;
+    if (s < ring_cap) ring_tok[s] = idx;
+    *pos = *pos + 1;
+    *step = s + 1;
+  }
+  __syncthreads();
+  const int16_t* src = embed + (int64_t)win * dim;
+  for (int i = tid; i < dim; i += blockDim.x) row[i] = src[i];
+}
+
+extern "C" int llhip_dec_greedy(const void* keys, int64_t nkeys, int32_t* token, int32_t* pos, int32_t* step,
+                                int32_t* ring_tokens, int64_t ring_cap, const int16_t* embed, int64_t dim, int16_t* row,
+                                void* stream) {
+  if (!keys || nkeys < 1 || nkeys > INT32_MAX || !token || !pos || !step || ring_cap < 0 ||
+      (ring_cap && !ring_tokens) || !embed || dim < 1 || dim > INT32_MAX || !row)
+    return fail(-EINVAL, "dec_greedy: bad arguments");
+  hipLaunchKernelGGL(dec_greedy_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream,
+                     static_cast<const uint64_t*>(keys), (int)nkeys, token, pos, step, ring_tokens,
+                     (int)std::min<int64_t>(ring_cap, INT32_MAX), embed, (int)dim, row);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+extern "C" int64_t llhip_dec_head_keys(int64_t N) { return ceil_div(N, 16); }

@@ -219,11 +219,6 @@ __global__ void embed_kernel(const int16_t* __restrict__ embed, int64_t dim, con
   rows[idx] = m < n_tokens ? embed[(int64_t)tokens[m] * dim + d] : (int16_t)0;
 }
 
-// key orders by value, then by lower index: larger key = better
-__device__ __forceinline__ uint64_t amax_key(int v, int64_t i) {
-  return ((uint64_t)(uint32_t)(v + 32768) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
-}
-
 __global__ __launch_bounds__(256) void argmax_kernel(const int16_t* __restrict__ logits, int64_t ld, int64_t vocab,
                                                      int32_t* __restrict__ idx) {
   __shared__ uint64_t best[4];

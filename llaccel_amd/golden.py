@@ -438,6 +438,13 @@ class GoldenModel:
         self._pf_graphs: dict = {}  # whole-prompt prefill graphs by (rows, prompt length, KV slot)
         self._pf_seen: dict = {}
         self._plan = self._compile()
+        # one-row launches of a fused graph: three launches per layer (llaccel_amd.chain)
+        self._chain = None
+        if self.fuse:
+            from . import chain
+
+            self._chain = chain.build(self)
+        self.use_chain = self._chain is not None
         self._ensure_capacity(self.prefill_m)
         self._graph = None
         self._ring_cap = 0
@@ -758,7 +765,13 @@ class GoldenModel:
         return run
 
     # ---- one device launch --------------------------------------------------------------
+    def _chained(self, M: int, pd=None) -> bool:
+        return M == 1 and self.use_chain and self._chain is not None and not isinstance(pd, _RowPos)
+
     def _execute(self, M: int, pos: int, pd=None) -> None:
+        if self._chained(M, pd):
+            self._chain.run(pos, pd)
+            return
         for step in self._plan:
             step(M, pos, pd)
 
@@ -942,9 +955,16 @@ class GoldenModel:
             self._st = torch.zeros(3, dtype=torch.int32, device=self.device)  # token, pos, step
 
     def _decode_launch(self) -> None:
-        """Embedding gather of the device token, the op list at the device position, greedy step."""
+        """One greedy decode launch at the device position.  Fused plan: embedding gather of the
+        device token, the op list, greedy step.  Decode chain: the layers, the head and the greedy
+        step, which also gathers the next launch's input row (the first one is gathered by
+        decode_loop)."""
         st = self._st
         tok, pos, step = (ctypes.c_void_p(st.data_ptr() + 4 * i) for i in range(3))
+        if self._chained(1):
+            self._chain.run(0, pos, greedy=(tok, pos, step, _ptr(self._ring_rows), self.vocab, _ptr(self._ring_tok),
+                                            self._ring_cap))
+            return
         _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, tok, 1, 1,
                   _ptr(self._act[self.q.input_name]), _stream())
         self._execute(1, 0, pos)
@@ -957,6 +977,7 @@ class GoldenModel:
         with capture_graph(g):
             self._decode_launch()
         self._graph = g
+        self._graph_chained = self._chained(1)
 
     def decode_loop(self, token: int, pos: int, n: int, *, sync: bool = True):
         """Run `n` greedy M=1 decode launches from (token, pos) entirely on the device.
@@ -973,7 +994,10 @@ class GoldenModel:
         torch = _t()
         self._decode_state(n if sync else min(n, max(self._ring_cap, 64)))
         self._st.copy_(torch.tensor([int(self._token_rows([token])[0]), pos, 0], dtype=torch.int32))
-        if self.use_graph and self._graph is None:
+        if self._chained(1):  # the chain's launches gather their next input row themselves
+            _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim,
+                      ctypes.c_void_p(self._st.data_ptr()), 1, 1, _ptr(self._act[self.q.input_name]), _stream())
+        if self.use_graph and (self._graph is None or self._graph_chained != self._chained(1)):
             self._capture()
         for _ in range(n):
             if self.use_graph:
