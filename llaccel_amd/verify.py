@@ -31,26 +31,41 @@ from . import _lib
 _KEYS = ("argmax_per_step", "generated", "logits_last_rows")
 
 
+def _format_problem(record: dict) -> str | None:
+    """The first way `record` departs from the record format (verify.py:86-95), or None: the three
+    arrays present, one logits row per recorded argmax, integer tokens, nonempty integer rows."""
+    missing = [k for k in _KEYS if not isinstance(record.get(k), list)]
+    if missing:
+        return f"lacks an array {missing[0]!r}"
+    tokens, rows = record["argmax_per_step"] + record["generated"], record["logits_last_rows"]
+    if len(rows) != len(record["argmax_per_step"]):
+        return "logits/launch counts differ"
+    if not all(type(t) is int for t in tokens):
+        return "token IDs must be integers"
+    if not all(isinstance(r, list) and r and all(type(v) is int for v in r) for r in rows):
+        return "logits must be nonempty integer rows"
+    return None
+
+
+def _first_difference(a: list, b: list):
+    """(index, a[i], b[i]) of the first unequal element of two equally long lists, or None."""
+    return next(((i, x, y) for i, (x, y) in enumerate(zip(a, b)) if x != y), None)
+
+
 def compare_records(sim: dict, gold: dict) -> tuple[bool, str]:
-    """verify.py:80-104 on two loaded records."""
+    """The record check of verify.py:80-104 on two loaded records: both well formed, then the three
+    arrays equal element by element (the first difference is reported)."""
     for owner, record in (("sim", sim), ("golden", gold)):
-        for key in _KEYS:
-            if not isinstance(record.get(key), list):
-                return False, f"MISMATCH: {owner}.json lacks an array {key!r}"
-        if len(record["logits_last_rows"]) != len(record["argmax_per_step"]):
-            return False, f"MISMATCH: {owner}.json logits/launch counts differ"
-        if any(type(x) is not int for key in ("argmax_per_step", "generated") for x in record[key]):
-            return False, f"MISMATCH: {owner}.json token IDs must be integers"
-        if any(not isinstance(row, list) or not row or any(type(x) is not int for x in row)
-               for row in record["logits_last_rows"]):
-            return False, f"MISMATCH: {owner}.json logits must be nonempty integer rows"
+        problem = _format_problem(record)
+        if problem is not None:
+            return False, f"MISMATCH: {owner}.json {problem}"
     for key in _KEYS:
-        a, b = sim[key], gold[key]
-        if len(a) != len(b):
-            return False, f"MISMATCH: {key} length sim={len(a)} golden={len(b)}"
-        for i, (left, right) in enumerate(zip(a, b)):
-            if left != right:
-                return False, f"MISMATCH in {key} at step {i}: sim={left} golden={right}"
+        if len(sim[key]) != len(gold[key]):
+            return False, f"MISMATCH: {key} length sim={len(sim[key])} golden={len(gold[key])}"
+        diff = _first_difference(sim[key], gold[key])
+        if diff is not None:
+            step, left, right = diff
+            return False, f"MISMATCH in {key} at step {step}: sim={left} golden={right}"
     return True, f"MATCH: {len(gold['generated'])} tokens, {len(gold['argmax_per_step'])} steps identical"
 
 

@@ -238,14 +238,14 @@ def test_late_residual_outlier_known_answers(produced):
     calib["l1.d"] = calib["l1.x2"] = 1024.0
     weights = dict(weights)
     weights["embed"] = np.full_like(weights["embed"], 0.01)
-    qs = [Q.Quantizer(cfg, weights, calib, fusion) for fusion in (False, True)]
-    graphs = [q.run() for q in qs]
-    assert qs[0].blob.bytes() == qs[1].blob.bytes()
+    qs = [Q.Graph(cfg, weights, calib, fusion) for fusion in (False, True)]
+    graphs = [q.build() for q in qs]
+    assert qs[0].pack.bytes() == qs[1].pack.bytes()
     for q, gph in zip(qs, graphs):
         assert gph["model"]["E_RES"] == gph["exps"]["input"] == -15
         assert gph["exps"]["l0.x1"] == gph["exps"]["l0.x2"] == -15 and gph["exps"]["l1.x2"] == -4
         off = gph["tensors"]["embed"]["offset"]
-        assert np.all(np.frombuffer(q.blob.bytes(), "<i2", count=weights["embed"].size, offset=off) == 328)
+        assert np.all(np.frombuffer(q.pack.bytes(), "<i2", count=weights["embed"].size, offset=off) == 328)
         late = next(op for op in gph["ops"] if op["op"] == "add" and op["out"] == "l1.x2")
         assert (late["a"], late["b"], late["sh_b"]) == ("l1.d", "l1.x1", 11)
         assert not any(op.get("epilogue") == "resadd" and op["out"] == "l1.x2" for op in gph["ops"])
@@ -259,4 +259,15 @@ def test_head_dim_128_with_qk_norm(tmp_path):
     prompt = list(range(5, 25))
     assert g.generate(prompt, 4) == o.generate(prompt, 4)
     with pytest.raises(ValueError, match="head_dim"):
-        Q.Quantizer({**Q.load_export(ex)[0], "head_dim": 8}, {}, {}, False).run()
+        Q.Graph({**Q.load_export(ex)[0], "head_dim": 8}, {}, {}, False).build()
+
+
+@pytest.mark.parametrize("name,model,fusion", [("llama_v2", "llama", True), ("qwen_v1", "qwen", False),
+                                               ("qwen_v2", "qwen", True)])
+def test_gpu_producer_equals_reference_quantizer(golden_dir, tmp_path, name, model, fusion):
+    """The producer with its GPU conversions writes the graph and the byte-identical qweights.bin
+    that the reference's refquant.quantize_export wrote (tests/golden/refquant/)."""
+    ref = golden_dir / "refquant"
+    got = Q.quantize_export(ref / f"export_{model}", tmp_path / "q", fusion=fusion)
+    assert json.loads(json.dumps(got)) == json.loads((ref / f"q_{name}" / "qgraph.json").read_text())
+    assert (tmp_path / "q" / "qweights.bin").read_bytes() == (ref / f"q_{name}" / "qweights.bin").read_bytes()

@@ -8,6 +8,7 @@ The device conversions are checked against the oracle in tests/test_gpu_quantize
 from __future__ import annotations
 
 import dataclasses
+import json
 import math
 from fractions import Fraction
 
@@ -198,14 +199,63 @@ def test_export_directory_round_trip(tmp_path):
 
 
 def test_blob_layout():
-    b = Q.Blob()
-    b.add("a", np.arange(3, dtype=np.int64), "i8")
-    b.add("r", np.array([[1, 2], [3, 4]], dtype=np.int64), "rq", None)
-    b.add("g", np.ones(5, dtype=np.int64), "i16", -3)
+    b = Q.Pack(OracleDevice())
+    b.put("a", np.arange(3, dtype=np.int64), "i8")
+    b.put("r", np.array([[1, 2], [3, 4]], dtype=np.int64), "rq", None)
+    b.put("g", np.ones(5, dtype=np.int64), "i16", -3)
     assert b.tensors == {"a": {"dtype": "i8", "shape": [3], "offset": 0},
                          "r": {"dtype": "rq", "shape": [2], "offset": 64},
                          "g": {"dtype": "i16", "shape": [5], "offset": 128, "exp": -3}}
     data = b.bytes()
     assert len(data) == 192 and data[:3] == b"\x00\x01\x02" and data[64:80] == np.array([1, 2, 3, 4], "<i4").tobytes()
     with pytest.raises(ValueError, match="duplicate"):
-        b.add("a", np.zeros(1), "i8")
+        b.put("a", np.zeros(1), "i8")
+
+
+# ---- the whole producer against graphs written by the reference quantizer --------------------
+class OracleDevice:
+    """The producer's device conversions restated on the CPU by oracle/quant_np.py (refquant.py:119-141),
+    so the host side of the producer -- formats, parameters, op list, blob layout -- is checked
+    without a GPU.  The GPU conversions themselves are compared with the same fixtures in
+    tests/test_gpu_quantize.py."""
+
+    def rows_i8(self, w, n_rows=None):
+        w = np.asarray(w, np.float32)
+        full = np.zeros((w.shape[0] if n_rows is None else int(n_rows), w.shape[1]), np.float32)
+        full[: w.shape[0]] = w
+        return QN.quant_rows_i8(full)
+
+    def i16(self, x, e):
+        return QN.quant_i16(np.asarray(x, np.float32), e)
+
+
+REFQUANT = {"llama_v2": ("llama", True), "qwen_v1": ("qwen", False), "qwen_v2": ("qwen", True)}
+
+
+@pytest.mark.parametrize("name", sorted(REFQUANT))
+def test_producer_equals_reference_quantizer(golden_dir, tmp_path, name):
+    """tests/golden/refquant/q_*: qgraph.json + qweights.bin written by the reference's
+    refquant.quantize_export (refquant.py:493-506) on the committed export directories; the producer
+    writes the same graph and byte-identical weights."""
+    model, fusion = REFQUANT[name]
+    ref = golden_dir / "refquant"
+    got = Q.quantize_export(ref / f"export_{model}", tmp_path / "q", fusion=fusion, device=OracleDevice())
+    want = json.loads((ref / f"q_{name}" / "qgraph.json").read_text())
+    assert json.loads(json.dumps(got)) == want
+    assert (tmp_path / "q" / "qweights.bin").read_bytes() == (ref / f"q_{name}" / "qweights.bin").read_bytes()
+    assert json.loads((tmp_path / "q" / "qgraph.json").read_text()) == want
+
+
+def test_producer_fixture_catches_a_planted_formula_change(golden_dir, tmp_path, monkeypatch):
+    """A one-step change of the RMSNorm R rule (the largest feasible shift minus one) changes the
+    written graph: the fixture comparison is sensitive to the formulas it pins."""
+    real = Q._rms_shift
+
+    def off_by_one(K, r_typ):
+        R, _ = real(K, r_typ)
+        return R - 1, Q.llround(math.ldexp(math.sqrt(float(K)), R - 1))
+
+    monkeypatch.setattr(Q, "_rms_shift", off_by_one)
+    ref = golden_dir / "refquant"
+    got = Q.quantize_export(ref / "export_llama", tmp_path / "q", fusion=True, device=OracleDevice())
+    assert json.loads(json.dumps(got)) != json.loads((ref / "q_llama_v2" / "qgraph.json").read_text())
