@@ -86,14 +86,25 @@ class Chain:
         r.x_out = _vp(m._buf(op["out"]))
         return ctypes.byref(r)
 
-    def _launch_layer(self, i, ly, pos, pd):
-        m = self.model
-        s = m._stream_handle()
+    def _launch_layer(self, i, ly, pos, pd, only=None):
+        """Layer i's three launches (or, with `only`, the launch of that family alone)."""
+        s = self.model._stream_handle()
+        if only is None or only == "dec_attn_in":
+            self._attn_in(i, ly, pos, pd, s)
+        if only is None or only == "dec_attention":
+            self._attention(i, ly, pos, pd, s)
+        if only is None or only == "dec_mlp":
+            self._mlp(i, ly, pos, pd, s)
+
+    def _attn_in(self, i, ly, pos, pd, s):
         fs = ly.attn_in
         fs.fill(fs.desc, 1, pos, pd)
         fs.desc.pre.prequant = 0
         resid = self._fill_resid(self.layers[i - 1].wd, self.acc_wd, WD_ROWS) if i else None
         _lib.call("llhip_dec_attn_in", ctypes.byref(fs.desc), resid, _vp(self.acc_wo), self.dim, s)
+
+    def _attention(self, i, ly, pos, pd, s):
+        m = self.model
         a, d = ly.att, self._att
         kcp, vcp, pdev, _, _ = m._kv_args(int(a["layer"]), pd)
         d.q, d.kc, d.vc, d.out = _vp(m._buf(a["q"])), kcp, vcp, _vp(m._buf(a["out"]))
@@ -104,18 +115,24 @@ class Chain:
         d.wo_panel, d.N, d.acc = _vp(self.wo_panel[i]), self.dim, _vp(self.acc_wo)
         d.zero, d.zero_n = _vp(self.acc_wd), WD_ROWS * self.dim
         _lib.call("llhip_dec_attention", ctypes.byref(d), _vp(m._ws), s)
+
+    def _mlp(self, i, ly, pos, pd, s):
         fm = ly.mlp
         fm.fill(fm.desc, 1, pos, pd)
         fm.desc.pre.prequant = 0
         _lib.call("llhip_dec_mlp", ctypes.byref(fm.desc), self._fill_resid(ly.wo, self.acc_wo, 1),
                   _vp(self.wd_panel[i]), _vp(self.acc_wd), WD_ROWS, self.dim, s)
 
-    def run(self, pos, pd=None, greedy=None):
+    def run(self, pos, pd=None, greedy=None, only=None):
         """One row at position pos (or *pd).  greedy = (token, pos, step) device int32 pointers plus
-        (ring_rows, ring_ld, ring_tokens, ring_cap): the decode loop's greedy step and record."""
+        (ring_rows, ring_ld, ring_tokens, ring_cap): the decode loop's greedy step and record.
+        `only` names one family (dec_attn_in, dec_attention, dec_mlp, dec_head) whose launches alone
+        run -- a measurement aid: the values they compute are then meaningless."""
         m = self.model
         for i, ly in enumerate(self.layers):
-            self._launch_layer(i, ly, pos, pd)
+            self._launch_layer(i, ly, pos, pd, only)
+        if only not in (None, "dec_head"):
+            return
         fh = self.head
         fh.fill(fh.desc, 1, pos, pd)
         s = m._stream_handle()
@@ -135,6 +152,27 @@ class Chain:
                   _vp(m._dt["embed"]), self.dim, _vp(m._act[m.q.input_name]), s)
 
     # ---- measurement ------------------------------------------------------------------------
+    FAMILIES = ("dec_attn_in", "dec_attention", "dec_mlp", "dec_head")
+
+    def launches(self, family: str) -> int:
+        return 2 if family == "dec_head" else len(self.layers)  # dec_head: the finish and the lm_head
+
+    def capture_family(self, family: str | None, pos: int):
+        """A HIP graph of one decode step's launches of `family` at the device position `pos` (for
+        timing them in isolation: the values are then meaningless), or with family None the whole
+        step's layers and head (without the greedy step), which can be replayed at one position."""
+        m = self.model
+        torch = _torch()
+        m._decode_state(1)
+        m._st.copy_(torch.tensor([0, pos, 0], dtype=torch.int32))
+        pd = ctypes.c_void_p(m._st.data_ptr() + 4)
+        from .golden import capture_graph
+
+        g = torch.cuda.CUDAGraph()
+        with capture_graph(g):
+            self.run(0, pd, only=family)
+        return g
+
     def step_bytes(self, T: int):
         """Algorithmic HBM bytes of one row's launch at context T, per chain kernel family: the bytes
         of the ops each family computes (the linear(M,N,K) and attention formulas of the measurement

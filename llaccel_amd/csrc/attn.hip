@@ -79,37 +79,53 @@ __device__ __forceinline__ int32_t dot16(const v4i& a, const v4i& b) {
 // takes 16-byte chunk l % DC of panel column n (64 / DC consecutive columns per wave load, so the
 // loads are contiguous); the DC lanes of a column add their products and the first one adds the
 // column's sum into the accumulators.  wpre holds this thread's first NPF chunks.
+// Columns [n_lo, n_hi) of the output projection's partial sums of head h from its D output bytes
+// in LDS (one row).  Lane l takes 16-byte chunk l % DC of a panel column (64 / DC consecutive
+// columns per wave load, so the loads are contiguous); the DC lanes of a column add their products
+// and the first one adds the column's sum into the accumulators.  wpre holds this thread's first
+// NPF chunks (wo_prefetch).
 template <int D, int NPF>
-__device__ __forceinline__ void wo_partial(const AttnArgs& p, int h, const int8_t* ah, const v4i* wpre) {
+__device__ __forceinline__ void wo_partial(const AttnArgs& p, int h, const int8_t* ah, const v4i* wpre, int n_lo,
+                                           int n_hi) {
   constexpr int DC = D / 16;
   const int lane = threadIdx.x & 63, kc = lane % DC;
   const int cpb = (int)(blockDim.x / DC);  // columns per block-wide load
-  const int c0 = (int)(threadIdx.x / DC);
+  const int c0 = n_lo + (int)(threadIdx.x / DC);
   const v4i a = *reinterpret_cast<const v4i*>(ah + 16 * kc);
 #pragma unroll
   for (int i = 0; i < NPF; ++i) {
     const int n = c0 + i * cpb;
     const int32_t s = chunk_sum<DC>(dot16(a, wpre[i]));
-    if (kc == 0 && n < p.wo_N && s != 0) atomic_add_dev(p.wo_acc + n, s);
+    if (kc == 0 && n < n_hi && s != 0) atomic_add_dev(p.wo_acc + n, s);
   }
+  // the rest four loads at a time (all in flight before the first is used)
   const Rsrc wr = rsrc(p.wop + (int64_t)h * p.wo_N * D, (int64_t)p.wo_N * D);
-  for (int n0 = NPF * cpb; n0 < p.wo_N; n0 += cpb) {
-    const int n = c0 + n0;
-    const int32_t s = chunk_sum<DC>(dot16(a, ld16(wr, n < p.wo_N ? (uint32_t)(n * D + 16 * kc) : LD_OOB)));
-    if (kc == 0 && n < p.wo_N && s != 0) atomic_add_dev(p.wo_acc + n, s);
+  for (int n0 = NPF * cpb; c0 - (int)(threadIdx.x / DC) + n0 < n_hi; n0 += 4 * cpb) {
+    v4i w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int n = c0 + n0 + u * cpb;
+      w[u] = ld16(wr, n < n_hi ? (uint32_t)(n * D + 16 * kc) : LD_OOB);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int n = c0 + n0 + u * cpb;
+      const int32_t s = chunk_sum<DC>(dot16(a, w[u]));
+      if (kc == 0 && n < n_hi && s != 0) atomic_add_dev(p.wo_acc + n, s);
+    }
   }
 }
 
-// this thread's first NPF chunks of head h's output-projection panel (the layout of wo_partial)
+// this thread's first NPF chunks of head h's output-projection panel for columns from n_lo
 template <int D, int NPF>
-__device__ __forceinline__ void wo_prefetch(const AttnArgs& p, int h, v4i* wpre) {
+__device__ __forceinline__ void wo_prefetch(const AttnArgs& p, int h, v4i* wpre, int n_lo, int n_hi) {
   constexpr int DC = D / 16;
-  const int kc = (threadIdx.x & 63) % DC, cpb = (int)(blockDim.x / DC), c0 = (int)(threadIdx.x / DC);
+  const int kc = (threadIdx.x & 63) % DC, cpb = (int)(blockDim.x / DC), c0 = n_lo + (int)(threadIdx.x / DC);
   const Rsrc wr = rsrc(p.wop + (int64_t)h * p.wo_N * D, (int64_t)p.wo_N * D);
 #pragma unroll
   for (int i = 0; i < NPF; ++i) {
     const int n = c0 + i * cpb;
-    wpre[i] = ld16(wr, n < p.wo_N ? (uint32_t)(n * D + 16 * kc) : LD_OOB);
+    wpre[i] = ld16(wr, n < n_hi ? (uint32_t)(n * D + 16 * kc) : LD_OOB);
   }
 }
 
@@ -253,7 +269,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   // the output-projection panel columns of this thread, requested once the score loads are
   // consumed: they are needed last and their loads overlap the softmax and the value pass
   v4i wpre[WPF > 0 ? WPF : 1];
-  if constexpr (WPF > 0) wo_prefetch<D, WPF>(p, h, wpre);
+  if constexpr (WPF > 0) wo_prefetch<D, WPF>(p, h, wpre, 0, p.wo_N);
   if (wave == 0) {
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -346,7 +362,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   }
   if constexpr (WO) {
     __syncthreads();
-    wo_partial<D, WPF>(p, h, ah, wpre);
+    wo_partial<D, WPF>(p, h, ah, wpre, 0, p.wo_N);
   }
 }
 
@@ -877,23 +893,32 @@ __global__ __launch_bounds__(256) void attention_split_finish(AttnArgs p, int S,
 
 // split-context finish of one row with the output projection: workgroup h sums the S value
 // partials of head h, requantises the head's D outputs, then adds its output-projection partial sums
+// The output projection's columns are split over gridDim.y workgroups per head (WO_SLICE columns each):
+// every workgroup of head h sums the partials and requantises (one of them stores the outputs), then
+// adds the partial sums of its columns.
+constexpr int WO_SLICE = 128;
+
 template <int D>
 __global__ __launch_bounds__(256) void attention_split_finish_wo(AttnArgs p, int S, const int32_t* ws) {
   __shared__ __attribute__((aligned(16))) int8_t ah[D];
-  const int h = blockIdx.x;
+  // the output-projection panel chunks of this thread, requested first: they overlap the partial sums
+  constexpr int WPF = (WO_SLICE * (D / 16)) / 256 > 0 ? (WO_SLICE * (D / 16)) / 256 : 1;
+  const int h = blockIdx.x, n_lo = (int)blockIdx.y * WO_SLICE, n_hi = min(n_lo + WO_SLICE, p.wo_N);
+  v4i wpre[WPF];
+  wo_prefetch<D, WPF>(p, h, wpre, n_lo, n_hi);
   const int64_t pairs = p.H;
   const int32_t* outv = ws + 2 * pairs * S * AT_ROWS + (int64_t)h * S * AT_ROWS * D;
-  if (h == 0) zero_words(p.zero, p.zero_n);
+  if (h == 0 && blockIdx.y == 0) zero_words(p.zero, p.zero_n);
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     int32_t o = 0;
     for (int q = 0; q < S; ++q) o += outv[(int64_t)q * AT_ROWS * D + d];
     if (p.pb == 15) o = rshr32(o, 7);
     const int8_t y = (int8_t)sat8(mulshift(o, p.Mo, p.So));
-    p.out[(int64_t)h * D + d] = y;
+    if (blockIdx.y == 0) p.out[(int64_t)h * D + d] = y;
     ah[d] = y;
   }
   __syncthreads();
-  wo_partial<D, 0>(p, h, ah, nullptr);
+  wo_partial<D, WPF>(p, h, ah, wpre, n_lo, n_hi);
 }
 
 __global__ void kv_write_kernel(const int8_t* __restrict__ k, const int8_t* __restrict__ v, int64_t M, int Hkv, int D,
@@ -1030,7 +1055,8 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   hipLaunchKernelGGL((attention_split<DD, 2>), grid, block, 0, s, p, S, tps, sw);           \
   hipLaunchKernelGGL((attention_split<DD, 3>), grid, block, 0, s, p, S, tps, sw);           \
   if (fold)                                                                                 \
-    hipLaunchKernelGGL((attention_split_finish_wo<DD>), dim3((unsigned)H), dim3(256), 0, s, p, S, sw); \
+    hipLaunchKernelGGL((attention_split_finish_wo<DD>), dim3((unsigned)H, (unsigned)ceil_div(p.wo_N, WO_SLICE)),    \
+                       dim3(256), 0, s, p, S, sw);                                                  \
   else                                                                                      \
     hipLaunchKernelGGL((attention_split_finish<DD>), fgrid, dim3(256), 0, s, p, S, sw);
     switch (D) {

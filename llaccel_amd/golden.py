@@ -24,6 +24,7 @@ import ctypes
 import gc
 import json
 import math
+from collections.abc import Sequence
 from pathlib import Path
 
 import numpy as np
@@ -1102,17 +1103,8 @@ class GoldenModel:
         if L + n_tokens > self.max_seq:
             raise ValueError(f"prompt + tokens = {L + n_tokens} exceeds max_seq={self.max_seq}")
         B = len(prompts)
-        recs, nxt = [], []
-        for b, (p, rows) in enumerate(zip(prompts, self.prefill_batch(prompts))):
-            steps, argm, lrows = [], [], []
-            for c in range(math.ceil(L / self.prefill_m)):
-                last = min(L, (c + 1) * self.prefill_m) - 1
-                steps.append({"kind": "prefill", "pos": c * self.prefill_m, "rows": self.prefill_m,
-                              "valid_rows": last + 1 - c * self.prefill_m})
-                argm.append(self.argmax(rows[last], self.vocab))
-                lrows.append([int(v) for v in rows[last][:self.vocab]])
-            recs.append((steps, argm, lrows))
-            nxt.append(argm[-1])
+        recs = [self._chunk_records(rows, L) for rows in self.prefill_batch(prompts)]
+        nxt = [argm[-1] for _, argm, _ in recs]
         n_dec = min(n_tokens, self.max_seq - L - 1)
         toks = rows_dev = None
         if n_dec > 0:
@@ -1161,21 +1153,41 @@ class GoldenModel:
     def count_steps(self, kind: str) -> int:
         return sum(1 for st in self._plan if st.kind == kind)
 
-    def prefill(self, tokens, acts: list | None = None) -> list[np.ndarray]:
+    def _chunk_records(self, rows, L: int) -> tuple[list, list, list]:
+        """The prefill part of the launch record (golden.py:411-431): one entry per prompt chunk, its
+        argmax and logits row taken from row (L - 1) mod prefill_m of the last chunk and row
+        prefill_m - 1 of the others.  Rows still on the device are gathered there, their argmax
+        computed there and only those rows downloaded."""
+        P = self.prefill_m
+        lasts = [min(L, (c + 1) * P) - 1 for c in range(math.ceil(L / P))]
+        steps = [{"kind": "prefill", "pos": c * P, "rows": P, "valid_rows": last + 1 - c * P}
+                 for c, last in enumerate(lasts)]
+        if isinstance(rows, DeviceRows):
+            torch = _t()
+            sel = rows._rows[torch.tensor(lasts, device=self.device)]
+            idx = torch.empty(len(lasts), dtype=torch.int32, device=self.device)
+            _lib.call("llhip_argmax_i16", _ptr(sel), len(lasts), sel.shape[1], self.vocab, _ptr(idx), _stream())
+            return steps, [int(v) for v in idx.cpu()], sel[:, :self.vocab].cpu().numpy().tolist()
+        return (steps, [self.argmax(rows[i], self.vocab) for i in lasts],
+                [[int(v) for v in rows[i][:self.vocab]] for i in lasts])
+
+    def prefill(self, tokens, acts: list | None = None) -> Sequence:
         """Prefill with the launch structure of golden.py:379-390 (chunks of prefill_m rows).
 
         Without `acts` (and with `whole_prompt_prefill`) the chunks run as ONE launch of all
         ceil(L/prefill_m)*prefill_m rows at positions 0..: every row depends only on itself and
         on keys at earlier positions, and the zero pad rows of the last chunk sit at the same
         positions as in the chunked run, so logits and the KV state are identical (a GPU test
-        checks it) while the GEMMs run at M = padded prompt length on the MFMA tiled kernel."""
+        checks it) while the GEMMs run at M = padded prompt length on the MFMA tiled kernel.  That
+        path returns the rows as a DeviceRows sequence (each row an int64 array when read), the
+        chunked one as a list."""
         tokens = [int(t) for t in tokens]
         L = len(tokens)
         padded = -(-L // self.prefill_m) * self.prefill_m
         if acts is None and self.whole_prompt_prefill and L > self.prefill_m and padded <= self.max_seq:
             self._prefill_launch(tokens, padded)
-            # int16 rows downloaded, widened to int64 by torch's multithreaded CPU copy
-            return list(self._act[self.q.output_name][:L].cpu().to(_t().int64).numpy())
+            # a device copy of the L rows; each row crosses to the host when it is read
+            return DeviceRows(self._act[self.q.output_name][:L].clone())
         rows_out = []
         for start in range(0, len(tokens), self.prefill_m):
             chunk = tokens[start:start + self.prefill_m]
@@ -1204,7 +1216,6 @@ class GoldenModel:
         if len(prompt_tokens) + n_tokens > self.max_seq:
             raise ValueError(f"prompt + tokens = {len(prompt_tokens) + n_tokens} exceeds max_seq={self.max_seq}")
         self.reset()
-        steps, argmax_per_step, logits_rows = [], [], []
 
         def record(kind: str, pos: int, valid: int, row: np.ndarray) -> int:
             steps.append({"kind": kind, "pos": pos, "rows": self.prefill_m if kind == "prefill" else 1,
@@ -1213,13 +1224,9 @@ class GoldenModel:
             logits_rows.append([int(v) for v in row[:self.vocab]])
             return argmax_per_step[-1]
 
-        rows = self.prefill(prompt_tokens, acts)
         L = len(prompt_tokens)
-        n_chunks = math.ceil(L / self.prefill_m)
-        nxt = -1
-        for c in range(n_chunks):
-            last = min(L, (c + 1) * self.prefill_m) - 1
-            nxt = record("prefill", c * self.prefill_m, last + 1 - c * self.prefill_m, rows[last])
+        steps, argmax_per_step, logits_rows = self._chunk_records(self.prefill(prompt_tokens, acts), L)
+        nxt = argmax_per_step[-1]
         generated: list[int] = []
         n_dec = min(n_tokens, self.max_seq - L - 1)
         if acts is None and self.use_graph and n_dec > 0:
@@ -1243,6 +1250,32 @@ class GoldenModel:
                 "logits_last_rows": logits_rows, "steps": steps,
                 "model": {"vocab": self.vocab, "vocab_padded": self.vocab_padded, "E_LOGIT": self.E_LOGIT,
                           "E_RES": self.E_RES, "max_seq": self.max_seq}}
+
+
+class DeviceRows(Sequence):
+    """The logits rows of a whole-prompt prefill, kept on the device: row i is an int64 numpy array
+    (the values golden.py:379-390 returns), downloaded when it is read.  Callers that read a few
+    rows -- generate() reads one per prompt chunk -- move a few rows instead of L x vocab_padded
+    values; `numpy()` downloads them all at once."""
+
+    def __init__(self, rows) -> None:
+        self._rows = rows  # int16 [L][vocab_padded] device tensor owned by this object
+
+    def __len__(self) -> int:
+        return int(self._rows.shape[0])
+
+    def __getitem__(self, i):
+        if isinstance(i, slice):
+            return list(self.numpy()[i])
+        n = len(self)
+        i = int(i)
+        if not -n <= i < n:
+            raise IndexError("prefill row index out of range")
+        return self._rows[i].cpu().numpy().astype(I64)
+
+    def numpy(self) -> np.ndarray:
+        """All rows as one int64 [L][vocab_padded] array."""
+        return self._rows.cpu().numpy().astype(I64)
 
 
 def dump_acts(acts: list, out_dir: Path) -> int:

@@ -347,10 +347,34 @@ class OracleQGraph:
 # --------------------------------------------------------------------------------------
 # the model (golden.py:246-440)
 # --------------------------------------------------------------------------------------
+def exact_blas_matmul(a: np.ndarray, w: np.ndarray, chunk_rows: int = 1024) -> np.ndarray:
+    """Integer A @ W.T through FP64 BLAS, exact because every product and partial sum stays below
+    2^53 (golden.py:217-240): the same checks and errors, W converted chunk_rows rows at a time."""
+    if a.ndim != 2 or w.ndim != 2 or a.shape[1] != w.shape[1]:
+        raise ValueError("invalid matrix dimensions")
+    if a.dtype.kind not in "iu" or w.dtype.kind not in "iu" or chunk_rows < 1:
+        raise ValueError("exact BLAS requires integer inputs and positive chunks")
+    amax = max(abs(int(a.min(initial=0))), abs(int(a.max(initial=0))))
+    info = np.iinfo(w.dtype)
+    if a.shape[1] * amax * max(abs(int(info.min)), abs(int(info.max))) > (1 << 53):
+        raise ValueError("integer dot product exceeds exact FP64 accumulation bound")
+    af = a.astype(np.float64)
+    out = np.empty((a.shape[0], w.shape[0]), dtype=I64)
+    for lo in range(0, w.shape[0], chunk_rows):
+        hi = min(lo + chunk_rows, w.shape[0])
+        out[:, lo:hi] = (af @ w[lo:hi].astype(np.float64).T).astype(I64)
+    return out
+
+
 class OracleModel:
-    """CPU restatement of GoldenModel.  `backend` is "np" (reference structure) or "c"."""
+    """CPU restatement of GoldenModel.  `backend` is "np" (reference structure: int64 a @ w.T and a
+    Python loop per (row, head) for attention), "blas" (the reference's fast_matmul path: the
+    GEMMs through exact_blas_matmul, golden.py:217-240, with all BLAS threads) or "c"
+    (oracle/numerics.c, OpenMP)."""
 
     def __init__(self, qdir, backend: str = "np") -> None:
+        if backend not in ("np", "blas", "c"):
+            raise ValueError(f"unknown oracle backend {backend!r}")
         if backend == "c" and c_oracle() is None:
             raise RuntimeError("oracle/liboracle.so is not built (make -C oracle)")
         self.backend = backend
@@ -437,7 +461,7 @@ class OracleModel:
         aux = env[op["aux"]] if ep in ("resadd", "mul") else None
         if self.backend == "c":
             return linear_c(a, w, rq, bias, out_i8, ep, aux, int(op.get("aux_shift", 0)), op.get("silu"))
-        acc = a @ w.astype(I64).T
+        acc = exact_blas_matmul(a, w) if self.backend == "blas" else a @ w.astype(I64).T
         if bias is not None:
             acc = acc + bias.astype(I64)[None, :]
         Mn = rq[:, 0].astype(I64)[None, :]

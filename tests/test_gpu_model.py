@@ -212,3 +212,44 @@ def test_generate_batch_errors(golden_dir):
         g.generate_batch([[1, 2], [3]], 2)
     with pytest.raises(ValueError, match="max_seq"):
         g.generate_batch([[1, 2]], 63)
+
+
+def test_golden_cli_and_dump_acts(golden_dir, tmp_path):
+    """The golden CLI and dump_acts (golden.py:443-477), as the reference's
+    tests/python/test_golden_e2e.py:165-189 checks them: the record of a 5-token run from a char
+    prompt, one int32 .npy per activation per launch named step{i:03d}_{kind}_pos{P}_{name}.npy with
+    the launch's shapes, the recorded logits rows equal to the dumped logits activation's rows, and
+    the record verifying against itself (MATCH) but not against a perturbed copy ("step 2")."""
+    import json as _json
+
+    from llaccel_amd import verify
+
+    qdir = golden_dir / "ref_tiny_v1" / "qgraph"
+    graph = _json.loads((qdir / "qgraph.json").read_text())
+    m = graph["model"]
+    itos = [chr(ord("a") + i) for i in range(26)] + [chr(0x4E00 + i) for i in range(m["vocab"] - 26)]
+    (tmp_path / "tok.json").write_text(_json.dumps({"itos": itos}))
+    out, acts = tmp_path / "golden.json", tmp_path / "acts"
+    G.main(["--qgraph", str(qdir), "--prompt", "abcde", "--tokenizer", str(tmp_path / "tok.json"), "--tokens", "5",
+            "-o", str(out), "--dump-acts", str(acts)])
+    rec = _json.loads(out.read_text())
+    assert rec["prompt_tokens"] == [0, 1, 2, 3, 4] and len(rec["generated"]) == 5 and len(rec["argmax_per_step"]) == 6
+    assert rec["argmax_per_step"][:5] == rec["generated"]  # the last decode launch's argmax is not generated
+    per_launch = 1 + sum(1 for op in graph["ops"] if "out" in op)  # the input rows and every op output
+    files = sorted(acts.glob("*.npy"))
+    assert len(files) == 6 * per_launch
+    assert all(np.load(f).dtype == np.int32 for f in files)
+    H, Hkv, D = m["n_heads"], m["n_kv_heads"], m["head_dim"]
+    assert np.load(acts / "step000_prefill_pos0_logits.npy").shape == (16, m["vocab_padded"])
+    assert np.load(acts / "step001_decode_pos5_l0.a.npy").shape == (1, H * D)
+    assert np.load(acts / "step005_decode_pos9_l0.kr.q.npy").shape == (1, Hkv * D)
+    # the golden.json logits row is the recorded row of the dumped logits activation
+    assert np.load(acts / "step000_prefill_pos0_logits.npy")[4, :m["vocab"]].tolist() == rec["logits_last_rows"][0]
+    assert np.load(acts / "step003_decode_pos7_logits.npy")[0, :m["vocab"]].tolist() == rec["logits_last_rows"][3]
+    ok, msg = verify.compare_sim(out, out)
+    assert ok and msg.startswith("MATCH")
+    bad = dict(rec, generated=list(rec["generated"]))
+    bad["generated"][2] = (bad["generated"][2] + 1) % m["vocab"]
+    (tmp_path / "sim.json").write_text(_json.dumps(bad))
+    ok, msg = verify.compare_sim(tmp_path / "sim.json", out)
+    assert not ok and "step 2" in msg

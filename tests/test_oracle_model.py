@@ -95,3 +95,32 @@ def test_planted_composition_mistake_is_caught(golden_dir):
     bad_first = [int(v) for v in rows[16][:256]]
     assert bad_first != rec["logits_last_rows"][1]
     assert [int(v) for v in rows[19][:256]] == rec["logits_last_rows"][1]
+
+
+# ---- the oracle's FP64-BLAS backend (the reference's fast_matmul path) --------------------------
+@pytest.mark.parametrize("m,n,k", [(1, 17, 16), (4, 33, 4096), (16, 257, 512), (3, 1025, 32)])
+def test_exact_blas_matmul_against_integer(m, n, k):
+    """test_exact_blas.py:5-11: exact against int64 matmul at the extreme operands."""
+    rng = np.random.default_rng(m + n + k)
+    a = rng.integers(-32768, 32768, (m, k), dtype=np.int64)
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    a[0, :] = -32768
+    w[0, :] = -128
+    assert np.array_equal(O.exact_blas_matmul(a, w, 17), a @ w.astype(np.int64).T)
+
+
+def test_exact_blas_matmul_errors():
+    """test_exact_blas.py:13-19: the 2^53 bound and integer-only inputs."""
+    with pytest.raises(ValueError, match="bound"):
+        O.exact_blas_matmul(np.array([[2**53]], dtype=np.int64), np.array([[127]], dtype=np.int8))
+    with pytest.raises(ValueError, match="integer"):
+        O.exact_blas_matmul(np.ones((1, 1)), np.ones((1, 1), dtype=np.int8))
+
+
+def test_blas_backend_equals_the_reference_fixture(golden_dir):
+    """The fast_matmul oracle reproduces the reference golden.py's own record and KV."""
+    qdir, meta, rec, kv, _ = _load(golden_dir, "ref_tiny_v2")
+    o = O.OracleModel(qdir, "blas")
+    assert o.generate(meta["prompt"], meta["n_tokens"]) == rec
+    for layer, (k, v) in o.kv.items():
+        assert np.array_equal(k, kv[f"k{layer}"]) and np.array_equal(v, kv[f"v{layer}"])
