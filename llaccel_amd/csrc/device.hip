@@ -9,8 +9,13 @@
 // messages), accumulates the same performance counters (functions of the operands and POS only) and
 // enqueues the instruction's kernels on one stream: DMA and KV_WRITE as strided copies, GEMM as one
 // kernel over the SRAM weight tiles, the VEC ops and ATTN through the datapath's own kernels.
-// Data-dependent faults (an invalid requant table entry) are flagged on the device and reported once
-// the program has drained.
+// Data-dependent faults (an invalid requant table entry) are flagged on the device; the flag is read
+// before the next instruction that writes DRAM (DMA_STORE, KV_WRITE), when the program drains, and when
+// a later instruction fails, so the program stops with the simulator's message before any later DRAM
+// write.  A DMA or KV_WRITE that fails at a row first writes the rows before it, as the simulator does.
+// After a failed run DRAM is the simulator's; SRAM written by the failed instruction (a GEMM's valid
+// columns, ROPE/ATTN rows before a failing row, which the device does not write) and by the VEC/GEMM
+// instructions after an invalid requant entry may differ from it.
 #include <array>
 #include <cstring>
 #include <deque>
@@ -232,6 +237,7 @@ struct Device {
   int32_t* status = nullptr;
   hipStream_t stream = nullptr;
   bool fusion = false;
+  bool rq_unchecked = false;  // a GEMM was enqueued since the status flag was last read
   uint32_t seed = 0;  // 0: sequential policy; else the simulator's random legal interleaving
   uint32_t pos = 0;
   uint64_t perf[P_NUM] = {};
@@ -393,12 +399,46 @@ struct Device {
     hip_ok(hipGetLastError(), "kernel launch");
   }
 
+  // the range checks of DMA row r (funcsim.cpp:171-184)
+  void row_check(uint32_t r, bool load, uint32_t sramA, uint32_t dramA, uint32_t rowBytes, uint32_t srcStride,
+                 uint32_t dstStride) const {
+    if (load) {
+      const uint64_t s = uint64_t(dramA) + uint64_t(r) * srcStride, d = uint64_t(sramA) + uint64_t(r) * dstStride;
+      if (s + rowBytes > size) bad("DMA_LOAD source out of DRAM range");
+      chk(d, rowBytes, "DMA_LOAD");
+    } else {
+      chk(uint64_t(sramA) + uint64_t(r) * srcStride, rowBytes, "DMA_STORE");
+    }
+  }
+
+  // Reads the requant status flag once the GEMMs enqueued so far have run; raises the simulator's
+  // error if one of them met an invalid table entry (funcsim.cpp:239).
+  void requant_check() {
+    if (!rq_unchecked) return;
+    rq_unchecked = false;
+    flush();
+    int32_t st = 0;
+    hip_ok(hipMemcpyAsync(&st, status, 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
+    hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (st & 1) bad("invalid requantization table entry");
+  }
+
   // ---- instructions ----
   void dma(const uint32_t* in, bool load) {
     const uint32_t sramA = in[2], dramA = in[3], rows = in[4], rowBytes = in[5], srcStride = in[6], dstStride = in[7];
     if (rowBytes % 16 || sramA % 16) bad("DMA row/addr not 16-B aligned");
+    if (!load) requant_check();
     uint64_t beats = 0, sramReadBytes = 0;
-    for (uint32_t r = 0; r < rows; ++r) {  // funcsim.cpp:162-186
+    uint32_t r = 0;
+    // a row that fails its check: the rows before it are copied first (funcsim.cpp:162-186 copies
+    // row by row)
+    try {
+      for (; r < rows; ++r) row_check(r, load, sramA, dramA, rowBytes, srcStride, dstStride);
+    } catch (...) {
+      if (r) queue_dma(load, sramA, dramA, r, rowBytes, srcStride, dstStride);
+      throw;
+    }
+    for (r = 0; r < rows; ++r) {  // funcsim.cpp:162-186
       const uint64_t dramRow = uint64_t(dramA) + uint64_t(r) * (load ? srcStride : dstStride);
       beats += rowBytes ? ((dramRow % 64) + rowBytes + 63) / 64 : 0;
       if (!load) {
@@ -410,13 +450,8 @@ struct Device {
           copied += useful;
         }
       }
-      if (load) {
-        const uint64_t s = uint64_t(dramA) + uint64_t(r) * srcStride, d = uint64_t(sramA) + uint64_t(r) * dstStride;
-        if (s + rowBytes > size) bad("DMA_LOAD source out of DRAM range");
-        chk(d, rowBytes, "DMA_LOAD");
-      } else {
-        const uint64_t s = uint64_t(sramA) + uint64_t(r) * srcStride, d = uint64_t(dramA) + uint64_t(r) * dstStride;
-        chk(s, rowBytes, "DMA_STORE");
+      if (!load) {
+        const uint64_t d = uint64_t(dramA) + uint64_t(r) * dstStride;
         grow(d + rowBytes);
         dram_written(d, rowBytes);
       }
@@ -472,6 +507,7 @@ struct Device {
               (int)mode, outI8 ? 1 : 0, (int)auxShift, (int)siluSi, (int)siluSh};
     hipLaunchKernelGGL(isa_gemm, dim3(NT), dim3(256), 0, stream, g);
     hip_ok(hipGetLastError(), "kernel launch");
+    rq_unchecked = true;
     if (inplace) copy(sram + out, scratch, 1, (uint32_t)on, 0, 0);
   }
 
@@ -643,10 +679,17 @@ struct Device {
       bad("KV_WRITE invalid dimensions/DRAM cache stride");
     const uint32_t row = Hkv * D;
     chk(src, uint64_t(M) * row, "KV_WRITE src");
+    requant_check();
     for (uint32_t m = 0; m < M; ++m)
       for (uint32_t kvh = 0; kvh < Hkv; ++kvh) {
         const uint64_t d = uint64_t(base) + uint64_t(kvh) * kvStride + uint64_t(pos + m) * D;
-        chk_dram(d, D, "KV_WRITE dst");
+        try {
+          chk_dram(d, D, "KV_WRITE dst");
+        } catch (...) {  // the (row, head) pairs before this one are written first (funcsim.cpp:388-398)
+          if (m) kv_launch(src, base, m, Hkv, D, kvStride, pos);
+          if (kvh) kv_launch(src + m * row, base, 1, kvh, D, kvStride, pos + m);
+          throw;
+        }
         dram_written(d, D);
         const uint64_t wr = ((d % kBeat + D > kBeat) ? D / 16 : 1) * kBeat;
         perf[P_DRAM_WR] += wr;
@@ -654,8 +697,13 @@ struct Device {
       }
     perf[P_SRAM_RD] += uint64_t(M) * row;
     perf[P_ATTN_BUSY] += uint64_t(M) * Hkv;
-    hipLaunchKernelGGL(kv_rows, dim3(grid_for(uint64_t(M) * row)), dim3(256), 0, stream, dram, sram + src, uint64_t(base),
-                       M, Hkv, D, uint64_t(kvStride), pos);
+    kv_launch(src, base, M, Hkv, D, kvStride, pos);
+  }
+
+  // heads 0..Hkv-1 of M rows of `src` (row stride Hkv * D) into the cache rows p .. p+M-1
+  void kv_launch(uint32_t src, uint32_t base, uint32_t M, uint32_t Hkv, uint32_t D, uint32_t kvStride, uint32_t p) {
+    hipLaunchKernelGGL(kv_rows, dim3(grid_for(uint64_t(M) * Hkv * D)), dim3(256), 0, stream, dram, sram + src,
+                       uint64_t(base), M, Hkv, D, uint64_t(kvStride), p);
     hip_ok(hipGetLastError(), "kernel launch");
   }
 
@@ -699,6 +747,8 @@ struct Device {
         flush();  // the DMAs before a failing instruction have happened, as in the simulator
       } catch (...) {
       }
+      // an invalid requant entry met by an earlier GEMM is the error the simulator stopped at
+      requant_check();
       throw;
     }
   }
@@ -708,6 +758,7 @@ struct Device {
     std::memset(sem, 0, sizeof sem);
     pos = p;
     hip_ok(hipMemsetAsync(status, 0, 4, stream), "hipMemsetAsync");
+    rq_unchecked = false;
     std::vector<uint32_t> window;  // instructions fetched from DRAM, 1024 at a time
     uint64_t wbase = 0, fetchPc = pc, issued = 0;
     win_lo = win_hi = 0;
@@ -779,10 +830,8 @@ struct Device {
       }
     }
     flush();
-    int32_t st = 0;
-    hip_ok(hipMemcpyAsync(&st, status, 4, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
-    hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
-    if (st & 1) bad("invalid requantization table entry");
+    rq_unchecked = true;
+    requant_check();
   }
 };
 

@@ -316,6 +316,41 @@ def error_cases():
             ("deadlock", sem_case(False), 0, False, "deadlock at pc=0x")]
 
 
+def partial_error_cases():
+    """(id, dram image, pos, fusion, message, sram_exact) of failing programs whose DRAM (and, where
+    sram_exact, SRAM) after the error the device must leave as the simulator does: a DMA or KV_WRITE
+    that fails at a later row writes the rows before it; an invalid requant entry stops the program
+    before a later DMA_STORE, and a later failing instruction does not replace its message."""
+    rng = np.random.default_rng(21)
+    out = []
+    b = Builder()
+    b.load(0x100, _i8(rng.integers(-128, 128, 64)))
+    b.load(0x2000, _i32(np.array([[1 << 20, 64]] * 16)))
+    b.emit("GEMM", 0, 0, 0x1000, 0x2000, 0, 0, 1, 16, 16, 0, 0, 0)
+    b.store(0x100, 64)
+    b.emit("QUANT", 0xFFFF0, 0, 32, 1, 1)
+    out.append(("rq-then-store", b.image(), 0, False, "invalid requantization table entry", False))
+    # DMA_STORE rows at SRAM 0xFFF00 + r * 0x80: row 2 starts past the SRAM
+    b = Builder()
+    b.load(0xFFF00, _i8(rng.integers(-128, 128, 256)))
+    dst = b.blob(bytes(4 * 64))
+    b.emit("DMA_STORE", 0xFFF00, dst, 4, 64, 0x80, 64)
+    out.append(("dma-store-rows", b.image(), 0, False, "SRAM access out of range in DMA_STORE", True))
+    # DMA_LOAD rows from the last 192 bytes of a 1 MiB DRAM, stride 64: row 3 ends past it
+    b = Builder()
+    b.emit("DMA_LOAD", 0x400, (1 << 20) - 192, 4, 64, 64, 64)
+    img = b.image()
+    img = img + bytes((1 << 20) - 192 - len(img)) + _i8(rng.integers(-128, 128, 192))
+    out.append(("dma-load-rows", img, 0, False, "DMA_LOAD source out of DRAM range", True))
+    # KV_WRITE of 2 rows x 2 heads (D = 16, head stride 64) ending at the 1 MiB DRAM's end: the pair
+    # (row 1, head 1) is out of range, row 0 and (row 1, head 0) are written
+    b = Builder()
+    b.load(0x0, _i8(rng.integers(-128, 128, 64)))
+    b.emit("KV_WRITE", 0x0, (1 << 20) - 80, 2, 2, 16, 64)
+    out.append(("kv-write-rows", b.image(), 0, False, "DRAM access out of range in KV_WRITE dst", True))
+    return out
+
+
 def toy_llbin(seed=5) -> bytes:
     """A .llbin of a one-head toy model (vocab 48, dim 64, max_seq 32) with programs for M = 4 and
     M = 1: input rows -> quant -> K/V cache write -> attention over the cache -> lm_head GEMM ->

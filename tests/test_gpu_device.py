@@ -38,12 +38,29 @@ def test_device_errors_equal_oracle(cid, img, pos, fusion, msg):
     g.dram_write(0, img)
     with pytest.raises(RuntimeError, match=msg.replace("[", r"\[").replace("]", r"\]")):
         g.run(0, pos)
-    # the device stays usable after an error (its SRAM keeps what the failed program wrote, so the
-    # next program's stored result and counters are compared)
+    # the device stays usable after an error (the next program's stored result and counters are
+    # compared; its DRAM after the error is the simulator's, test_device_state_after_error)
     ok = C.vec_case(np.random.default_rng(3), "ADD", 64)
     p1, _, d1 = _run(g, ok, 0)
     p2, _, d2 = _run(FuncSimNp(0, fusion), ok, 0)
     assert p1 == p2 and d1[:len(ok)] == d2[:len(ok)]
+
+
+@pytest.mark.parametrize("cid,img,pos,fusion,msg,sram_exact", C.partial_error_cases(),
+                         ids=[c[0] for c in C.partial_error_cases()])
+def test_device_state_after_error(cid, img, pos, fusion, msg, sram_exact):
+    """A program that fails part-way leaves DRAM (and, for a DMA or KV_WRITE that fails at a later
+    row, SRAM) as the simulator leaves it, with the simulator's message."""
+    print("case", cid, flush=True)
+    g, o = GpuDevice(0, fusion), FuncSimNp(0, fusion)
+    for d in (g, o):
+        d.dram_write(0, img)
+        with pytest.raises(RuntimeError, match=msg):
+            d.run(0, pos)
+    assert g.dram_size() == o.dram_size() == 1 << 20
+    assert g.dram_read(0, g.dram_size()) == o.dram_read(0, o.dram_size())
+    if sram_exact:
+        assert g.sram_snapshot() == o.sram_snapshot()
 
 
 def test_state_persists_across_launches():

@@ -95,6 +95,22 @@ def test_oracle_errors_equal_reference_simulator(cid, img, pos, fusion, msg):
             dev.run(0, pos)
 
 
+@pytest.mark.parametrize("cid,img,pos,fusion,msg,sram_exact", C.partial_error_cases(),
+                         ids=[c[0] for c in C.partial_error_cases()])
+def test_oracle_state_after_error_equals_reference_simulator(cid, img, pos, fusion, msg, sram_exact):
+    """The rows a failing DMA or KV_WRITE writes before its failing row, and the DRAM an invalid
+    requant entry leaves, are the reference simulator's (the GPU device is held to the same state)."""
+    devs = (RefSim(fusion), FuncSimNp(0, fusion))
+    for dev in devs:
+        dev.dram_write(0, img)
+        with pytest.raises(RuntimeError, match=msg):
+            dev.run(0, pos)
+    assert devs[0].dram_size() == devs[1].dram_size()
+    assert devs[0].dram_read(0, devs[0].dram_size()) == devs[1].dram_read(0, devs[1].dram_size())
+    if sram_exact:
+        assert devs[0].sram_snapshot() == devs[1].sram_snapshot()
+
+
 def test_oracle_plants_are_caught():
     """A mistake planted in the oracle's GEMM (weights untiled transposed) changes its result on a
     non-square case -- the parity test above would see it."""
