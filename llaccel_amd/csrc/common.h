@@ -59,6 +59,36 @@ __device__ __forceinline__ int32_t rshr32(int32_t v, int s) {
   return s == 0 ? v : (v >> s) + ((v >> (s - 1)) & 1);
 }
 
+// rshr of an int32 by any shift in [0, 63]: for s >= 32, |v| <= 2^31 gives v / 2^s in [-1/2, 1/2)
+// and the rounded result 0
+__device__ __forceinline__ int32_t rshr32_any(int32_t v, int s) {
+  return s == 0 ? v : (s >= 32 ? 0 : (v >> s) + ((v >> (s - 1)) & 1));
+}
+
+// mulshift(x, M, S) = floor(x * M / 2^S + 1/2) (golden.py:35-45, 64-65) for |x| <= 2^20, M < 2^32 and
+// S in [0, 63], in double precision with `scale` = M * 2^-S (exact: M has 32 significant bits): x *
+// scale + 1/2 is a multiple of 2^-(S+1) below 2^52 in magnitude, exact in the 53-bit significand for
+// S <= 52, so the fused multiply-add rounds nothing; for S > 52 |x * scale| < 2^-1 and the rounded sum
+// stays inside (0, 1), whose floor 0 is the exact one.  Four full-rate instructions instead of 64-bit
+// multiplies.
+__device__ __forceinline__ double mulshift_scale(int64_t M, int S) { return __builtin_ldexp((double)M, -S); }
+__device__ __forceinline__ int32_t mulshift_small_sat(int32_t x, double scale, double lo, double hi) {
+  const double v = __builtin_floor(__builtin_fma((double)x, scale, 0.5));
+  return (int32_t)__builtin_fmin(__builtin_fmax(v, lo), hi);
+}
+
+// silu16 (golden.py:101-107) of an i16-range x with the SIG table in LDS, exactly, in 32-bit and
+// double arithmetic: u = sat16(mulshift(x, Mi, Si)) by mulshift_small_sat; SIG values are below
+// 2^16, so x * sg lies in [-2^31, 2^31) and its rounding shift is rshr32_any.
+__device__ __forceinline__ int32_t silu16_fast(int32_t x, double smul, int sh, const uint16_t* sig) {
+  const int32_t u = mulshift_small_sat(x, smul, -32768.0, 32767.0);
+  const int j = (u >> 8) + 128;
+  const int32_t f = u & 255;
+  const int32_t lo = sig[j], hi = sig[j + 1];
+  const int32_t sg = lo + (((hi - lo) * f) >> 8);
+  return min(max(rshr32_any(x * sg, sh), -32768), 32767);
+}
+
 // floor(sqrt(t)) for t < 2^48 (golden.py:68-81 computes it by the restoring method, two bits
 // per step).  t converts to double exactly and its square root is within a few ulp (< 2^-26
 // here) of sqrt(t), so the truncated root r is floor(sqrt(t)) or, when t = n^2 and the rounded

@@ -450,15 +450,17 @@ __device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) { 
 // this one run (one barrier per tile, in the middle of the tile's MFMA stream).  Rows past M/N
 // read a clamped valid row (their outputs are discarded); K is a multiple of 64, so no K chunk is
 // partial.
+// Ring depth NS = GSTAGES.  Deeper rings (up to 12 stages in 144 KB, one workgroup per CU) measured
+// slower on the prompt-sized GEMMs: their K loop is not bound by the number of tiles in flight.
 constexpr int GSTAGES = 4;
 
 __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-template <int GM, int GN, int NW>
+template <int GM, int GN, int NW, int NS = GSTAGES>
 struct MfmaTile {
   static constexpr int NT = 64 * NW;
   static constexpr int STAGE_BYTES = (GM + GN) * 64;  // A + W of one K tile
-  static constexpr int LDS_BYTES = GSTAGES * STAGE_BYTES;
+  static constexpr int LDS_BYTES = NS * STAGE_BYTES;
   static constexpr int WROWS = GM / 2;                // wave tile: 2 x NW/2 waves
   static constexpr int WCOLS = 2 * GN / NW;
   static constexpr int WM = WROWS / 32, WN = WCOLS / 32;  // 32x32 MFMA tiles per wave
@@ -466,31 +468,29 @@ struct MfmaTile {
   static constexpr int LW = GN / (16 * NW);           // 1 KiB W loads per wave per stage
   static constexpr int LOADS = LA + LW;
   static_assert(WM >= 1 && WN >= 1 && LA >= 1 && LW >= 1 && LA * 16 * NW == GM && LW * 16 * NW == GN, "tile shape");
-  static_assert(2 * LOADS <= 15, "vmcnt waits are encoded in the low 4 bits");
+  static_assert(NS >= 3 && LOADS * (NS - 2) <= 63, "vmcnt counts at most 63 loads");
   static_assert(LA <= 4 && LW <= 4, "load source arrays");
 };
 
-// s_waitcnt vmcnt(N), expcnt and lgkmcnt not waited for.  Each builtin call takes a literal: a
-// template-dependent argument keeps the host pass from emitting the kernels' launch stubs.
+// s_waitcnt vmcnt(N) (bits 3:0 and 15:14 of the immediate), expcnt and lgkmcnt not waited for
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N == 0 || N == 2 || N == 3 || N == 4 || N == 5 || N == 6 || N == 8 || N == 10, "vmcnt values");
-  if constexpr (N == 0)
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-  else if constexpr (N == 2)
-    __builtin_amdgcn_s_waitcnt(0x0F72);
-  else if constexpr (N == 3)
-    __builtin_amdgcn_s_waitcnt(0x0F73);
-  else if constexpr (N == 4)
-    __builtin_amdgcn_s_waitcnt(0x0F74);
-  else if constexpr (N == 5)
-    __builtin_amdgcn_s_waitcnt(0x0F75);
-  else if constexpr (N == 6)
-    __builtin_amdgcn_s_waitcnt(0x0F76);
-  else if constexpr (N == 8)
-    __builtin_amdgcn_s_waitcnt(0x0F78);
-  else
-    __builtin_amdgcn_s_waitcnt(0x0F7A);
+  static_assert(N >= 0 && N <= 63, "vmcnt values");
+  constexpr int imm = (N & 15) | ((N >> 4) << 14) | 0x0F70;
+  __builtin_amdgcn_s_waitcnt(imm);
+}
+
+// wait until at most n tiles of L loads each are outstanding (n wave-uniform, n <= MAXN)
+template <int L, int MAXN>
+__device__ __forceinline__ void wait_tiles(int n) {
+  if constexpr (MAXN <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (n >= MAXN)
+      wait_vmcnt<L * MAXN>();
+    else
+      wait_tiles<L, MAXN - 1>(n);
+  }
 }
 
 __device__ __forceinline__ void lds_barrier() {
@@ -632,10 +632,10 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
 // Split-K (part != NULL): workgroup (tile, z = blockIdx.y) accumulates K tiles [z*kps, z*kps + kps)
 // and stores its int32 partial tile into plane z of part [splits][M][N]; linear_splitk_finish
 // sums the planes (integer addition: any split gives the same sum) and applies the epilogue.
-template <int EPI, bool OUT8, int GM, int GN, int NW>
+template <int EPI, bool OUT8, int GM, int GN, int NW, int NS>
 __device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, int kps, int32_t* part) {
-  using T = MfmaTile<GM, GN, NW>;
-  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [GSTAGES][A GMx64 | W GNx64]
+  using T = MfmaTile<GM, GN, NW, NS>;
+  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [NS][A GMx64 | W GNx64]
   const int m0 = mb * GM, n0 = nbk * GN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -658,7 +658,7 @@ __device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, 
     wsrc[i] = p.W + (int64_t)gn * p.K + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
   }
   auto issue = [&](int kt) {
-    int8_t* st = ring + (kt % GSTAGES) * T::STAGE_BYTES;
+    int8_t* st = ring + (kt % NS) * T::STAGE_BYTES;
     const int k0 = kt * 64;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -710,13 +710,10 @@ __device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, 
     for (int j = 0; j < T::WN; ++j) acc[i][j] = v16i{};
 
   const int ktiles = min(kps, p.K / 64 - (int)blockIdx.y * kps);
-  for (int s0 = 0; s0 < GSTAGES - 1; ++s0)
+  for (int s0 = 0; s0 < NS - 1; ++s0)
     if (s0 < ktiles) issue(s0);
-  // tile 0 landed: at most the next two tiles' loads are outstanding
-  if (ktiles > 2)
-    wait_vmcnt<2 * T::LOADS>();
-  else
-    wait_vmcnt<0>();
+  // tile 0 landed: the loads of the tiles issued after it may be outstanding
+  wait_tiles<T::LOADS, NS - 2>(min(ktiles, NS - 1) - 1);
   lds_barrier();
   v4i fa0[T::WM], fb0[T::WN], fa1[T::WM], fb1[T::WN];
 #pragma unroll
@@ -724,7 +721,7 @@ __device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, 
 #pragma unroll
   for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(ring + woff[j][0]);
   for (int kt = 0; kt < ktiles; ++kt) {
-    const int8_t* st = ring + (kt % GSTAGES) * T::STAGE_BYTES;
+    const int8_t* st = ring + (kt % NS) * T::STAGE_BYTES;
     // first K step of tile kt (fragments already in registers) while the second one's are read
 #pragma unroll
     for (int i = 0; i < T::WM; ++i) fa1[i] = *reinterpret_cast<const v4i*>(st + aoff[i][1]);
@@ -735,19 +732,16 @@ __device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, 
 #pragma unroll
       for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
     mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
-    // Tile kt+1 landed once at most tile kt+2's loads are outstanding; after the barrier every
-    // wave's copies of it are visible and every wave has finished reading stage (kt-1) % 4, which
-    // issue(kt + 3) overwrites.  A bare s_barrier: __syncthreads() would also drain the later
-    // tiles still in flight.
-    if (kt + 2 < ktiles)
-      wait_vmcnt<T::LOADS>();
-    else
-      wait_vmcnt<0>();
+    // Tile kt+1 landed once at most the loads of the tiles issued after it (kt+2 .. kt+NS-2) are
+    // outstanding; after the barrier every wave's copies of it are visible and every wave has
+    // finished reading stage (kt-1) % NS, which issue(kt + NS - 1) overwrites.  A bare s_barrier:
+    // __syncthreads() would also drain the later tiles still in flight.
+    wait_tiles<T::LOADS, NS - 2>(min(ktiles, kt + NS - 1) - kt - 2);
     lds_barrier();
-    if (kt + GSTAGES - 1 < ktiles) issue(kt + GSTAGES - 1);
+    if (kt + NS - 1 < ktiles) issue(kt + NS - 1);
     // second K step of tile kt while the next tile's first-step fragments are read (after the
     // last tile they come from a stale stage and are never used)
-    const int8_t* sn = ring + ((kt + 1) % GSTAGES) * T::STAGE_BYTES;
+    const int8_t* sn = ring + ((kt + 1) % NS) * T::STAGE_BYTES;
 #pragma unroll
     for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(sn + aoff[i][0]);
 #pragma unroll
@@ -804,12 +798,12 @@ __device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, 
 
 // The grid is padded to a multiple of 8 and workgroup b runs on XCD b % 8, which takes a
 // contiguous range of tiles (M fastest): the M-blocks that share a W panel share that XCD's L2.
-template <int EPI, bool OUT8, int GM, int GN, int NW>
+template <int EPI, bool OUT8, int GM, int GN, int NW, int NS>
 __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part) {
   const int b = blockIdx.x;
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
   if (logical >= mblocks * nblocks) return;
-  mfma_tile<EPI, OUT8, GM, GN, NW>(p, logical % mblocks, logical / mblocks, kps, part);
+  mfma_tile<EPI, OUT8, GM, GN, NW, NS>(p, logical % mblocks, logical / mblocks, kps, part);
 }
 
 // Several linears of one input in one launch (the q, k, v projections of a prompt chunk): the
@@ -827,7 +821,7 @@ struct LinearGroup {
   int out8[GROUP_MAX];
 };
 
-template <int GM, int GN, int NW>
+template <int GM, int GN, int NW, int NS>
 __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, LinearGroup g, int mblocks) {
   const int b = blockIdx.x;
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
@@ -844,9 +838,9 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, Linea
   pp.N = g.N[q];
   nbk -= g.nb0[q];
   if (g.out8[q])
-    mfma_tile<EPI_NONE, true, GM, GN, NW>(pp, mb, nbk, p.K / 64, nullptr);
+    mfma_tile<EPI_NONE, true, GM, GN, NW, NS>(pp, mb, nbk, p.K / 64, nullptr);
   else
-    mfma_tile<EPI_NONE, false, GM, GN, NW>(pp, mb, nbk, p.K / 64, nullptr);
+    mfma_tile<EPI_NONE, false, GM, GN, NW, NS>(pp, mb, nbk, p.K / 64, nullptr);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -872,12 +866,13 @@ struct DualArgs {
 // outputs from the same LDS stages (each wave the MFMA work of a 4-wave single GEMM tile, two waves
 // per SIMD); the up waves pass their requantised values to the gate waves through LDS for the
 // epilogue.  Stage loads: gate waves 1 A + 2 Wg instructions, up waves 2 Wu instructions.
+template <int NS>
 __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d, int mblocks, int nblocks) {
   constexpr int GM = 64, GN = 128, LW = 2;
   constexpr int STAGE = (GM + 2 * GN) * 64;
   constexpr int WN = 2;  // 32x32 tiles per wave along N (one along M)
-  // [GSTAGES][A | Wg | Wu]; after the k loop it holds the requantised up tile and the SiLU table
-  // (80 KB in all, so two workgroups share a CU)
+  // [NS][A | Wg | Wu]; after the k loop it holds the requantised gate and up tiles and the SiLU table
+  // (NS = 4: 80 KB, so two workgroups share a CU)
   extern __shared__ __attribute__((aligned(1024))) int8_t ring[];
   const int b = blockIdx.x;
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
@@ -903,7 +898,7 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
   }
   const int wbase = (upw ? GM + GN : GM) * 64;  // this wave group's W panel in a stage
   auto issue = [&](int kt) {
-    int8_t* st = ring + (kt % GSTAGES) * STAGE;
+    int8_t* st = ring + (kt % NS) * STAGE;
     const int k0 = kt * 64;
     if (!upw) {
       const int8_t* src = asrc + k0;
@@ -918,17 +913,11 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
     }
   };
   // vmcnt waits by wave group: gate waves issue 3 loads per stage, up waves 2
-  auto wait_two = [&]() {
+  auto wait_n = [&](int n) {
     if (upw)
-      wait_vmcnt<4>();
+      wait_tiles<2, NS - 2>(n);
     else
-      wait_vmcnt<6>();
-  };
-  auto wait_one = [&]() {
-    if (upw)
-      wait_vmcnt<2>();
-    else
-      wait_vmcnt<3>();
+      wait_tiles<3, NS - 2>(n);
   };
   int aoff[2], woff[WN][2];
 #pragma unroll
@@ -955,32 +944,26 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
   for (int j = 0; j < WN; ++j) acc[j] = v16i{};
 
   const int ktiles = p.K / 64;
-  for (int s0 = 0; s0 < GSTAGES - 1; ++s0)
+  for (int s0 = 0; s0 < NS - 1; ++s0)
     if (s0 < ktiles) issue(s0);
-  if (ktiles > 2)
-    wait_two();
-  else
-    wait_vmcnt<0>();
+  wait_n(min(ktiles, NS - 1) - 1);
   lds_barrier();
   v4i fa0, fa1, fb0[WN], fb1[WN];
   fa0 = *reinterpret_cast<const v4i*>(ring + aoff[0]);
 #pragma unroll
   for (int j = 0; j < WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(ring + woff[j][0]);
   for (int kt = 0; kt < ktiles; ++kt) {
-    const int8_t* st = ring + (kt % GSTAGES) * STAGE;
+    const int8_t* st = ring + (kt % NS) * STAGE;
     fa1 = *reinterpret_cast<const v4i*>(st + aoff[1]);
 #pragma unroll
     for (int j = 0; j < WN; ++j) fb1[j] = *reinterpret_cast<const v4i*>(st + woff[j][1]);
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb0[j], acc[j], 0, 0, 0);
     mfma_ds_interleave<WN, 1 + WN>();
-    if (kt + 2 < ktiles)
-      wait_one();
-    else
-      wait_vmcnt<0>();
+    wait_n(min(ktiles, kt + NS - 1) - kt - 2);
     lds_barrier();
-    if (kt + GSTAGES - 1 < ktiles) issue(kt + GSTAGES - 1);
-    const int8_t* sn = ring + ((kt + 1) % GSTAGES) * STAGE;
+    if (kt + NS - 1 < ktiles) issue(kt + NS - 1);
+    const int8_t* sn = ring + ((kt + 1) % NS) * STAGE;
     fa0 = *reinterpret_cast<const v4i*>(sn + aoff[0]);
 #pragma unroll
     for (int j = 0; j < WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(sn + woff[j][0]);
@@ -989,39 +972,67 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
     mfma_ds_interleave<WN, 1 + WN>();
   }
   __syncthreads();  // every wave's fragment reads have returned; no stage load is outstanding
-  int16_t* ubuf = reinterpret_cast<int16_t*>(ring);  // [GM][GN]
-  uint32_t* sig32 = reinterpret_cast<uint32_t*>(ring + GM * GN * 2);
+  // Epilogue over all eight waves: each wave stores its requantised accumulators (gate or up, i16)
+  // into the ring, then every thread finishes four adjacent columns of one row at a time from the
+  // two tiles -- SiLU of the gate, the product with the up value, the quant -- and stores them as
+  // 8-, 8- and 4-byte words.
+  int16_t* gbuf = reinterpret_cast<int16_t*>(ring);  // [GM][GN] requantised gate
+  int16_t* ubuf = gbuf + GM * GN;                      // [GM][GN] requantised up
+  uint32_t* sig32 = reinterpret_cast<uint32_t*>(ubuf + GM * GN);
   if (tid < 129) sig32[tid] = reinterpret_cast<const uint32_t*>(kSig)[tid];
   const uint16_t* sig16 = reinterpret_cast<const uint16_t*>(sig32);
-
-  // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, column l%32
-  if (upw) {
+  {
+    bool col_fast = true;
 #pragma unroll
-    for (int j = 0; j < WN; ++j)
+    for (int j = 0; j < WN; ++j) col_fast = col_fast && colrq_fast(cq[j]);
+    int16_t* mine = upw ? ubuf : gbuf;
+    // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, column l%32
+    auto put = [&](auto fast) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ml = wm + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), nl = wn + 32 * j + (lane & 31);
-        ubuf[ml * GN + nl] = (int16_t)clamp32(requant_col<false>(acc[j][r], cq[j]), -32768, 32767);
-      }
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int ml = wm + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), nl = wn + 32 * j + (lane & 31);
+          mine[ml * GN + nl] = (int16_t)clamp32(requant_col<decltype(fast)::value>(acc[j][r], cq[j]), -32768, 32767);
+        }
+    };
+    if (__all(col_fast))
+      put(std::true_type{});
+    else
+      put(std::false_type{});
   }
   __syncthreads();
-  if (upw) return;
+  const double smul = mulshift_scale(p.Mi, p.Si), fqs = mulshift_scale(d.fqM, d.fqS);
+  const bool vec = d.ld % 4 == 0 && (uintptr_t)d.sg % 8 == 0 && (uintptr_t)d.f % 8 == 0 && (uintptr_t)d.fq % 4 == 0;
+  constexpr int QPR = GN / 4;  // column quads per row
+  for (int q = tid; q < GM * QPR; q += 512) {
+    const int ml = q / QPR, nl = (q % QPR) * 4, m = m0 + ml, n = n0 + nl;
+    if (m >= p.M) break;  // rows ascend with q
+    const v2i gq = *reinterpret_cast<const v2i*>(gbuf + ml * GN + nl);
+    const v2i uq = *reinterpret_cast<const v2i*>(ubuf + ml * GN + nl);
+    const int32_t g4[4] = {lo16(gq.x), hi16(gq.x), lo16(gq.y), hi16(gq.y)};
+    const int32_t u4[4] = {lo16(uq.x), hi16(uq.x), lo16(uq.y), hi16(uq.y)};
+    int32_t sg[4], f[4], fq[4];
 #pragma unroll
-  for (int j = 0; j < WN; ++j) {
-    const int nl = wn + 32 * j + (lane & 31), n = n0 + nl;
-    if (n >= p.N) continue;
+    for (int e = 0; e < 4; ++e) {
+      sg[e] = silu16_fast(g4[e], smul, p.sh, sig16);
+      f[e] = min(max(rshr32_any(u4[e] * sg[e], d.mul_sh), -32768), 32767);  // |u * sg| <= 2^30
+      fq[e] = mulshift_small_sat(f[e], fqs, -128.0, 127.0);
+    }
+    const int64_t o = (int64_t)m * d.ld + n;
+    if (vec && n + 4 <= p.N) {
+      *reinterpret_cast<v2i*>(d.sg + o) = v2i{pack16(sg[0], sg[1]), pack16(sg[2], sg[3])};
+      *reinterpret_cast<v2i*>(d.f + o) = v2i{pack16(f[0], f[1]), pack16(f[2], f[3])};
+      *reinterpret_cast<uint32_t*>(d.fq + o) = (uint32_t)(fq[0] & 255) | (uint32_t)(fq[1] & 255) << 8 |
+                                               (uint32_t)(fq[2] & 255) << 16 | (uint32_t)(fq[3] & 255) << 24;
+    } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int ml = wm + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), m = m0 + ml;
-      if (m >= p.M) continue;
-      const int32_t g = clamp32(requant_col<false>(acc[j][r], cq[j]), -32768, 32767);
-      const int32_t sg = silu16_i16(g, (uint32_t)p.Mi, p.Si, p.sh, sig16);
-      const int32_t u = ubuf[ml * GN + nl];
-      const int32_t f = (int32_t)sat16(rshr((int64_t)(u * sg), d.mul_sh));
-      const int64_t o = (int64_t)m * d.ld + n;
-      d.sg[o] = (int16_t)sg;
-      d.f[o] = (int16_t)f;
-      d.fq[o] = (int8_t)sat8(mulshift(f, d.fqM, d.fqS));
+      for (int e = 0; e < 4; ++e)
+        if (n + e < p.N) {
+          d.sg[o + e] = (int16_t)sg[e];
+          d.f[o + e] = (int16_t)f[e];
+          d.fq[o + e] = (int8_t)fq[e];
+        }
     }
   }
 }
@@ -1081,7 +1092,7 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
   const int kps = (int)ceil_div(ktiles, splits);
   splits = (int)ceil_div(ktiles, kps);
   int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
-  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW>), dim3(ceil_div(mblocks * nblocks, 8) * 8, splits),
+  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW, GSTAGES>), dim3(ceil_div(mblocks * nblocks, 8) * 8, splits),
                      dim3(T::NT), T::LDS_BYTES, stream, p, mblocks, nblocks, kps, part);
   LLHIP_LAUNCH_CHECK();
   if (part) {
@@ -1196,7 +1207,7 @@ static int launch_linear_group(const LinearArgs& base, const llhip_linear_proble
     g.nb0[q + 1] = g.nb0[q] + (int)ceil_div(pr[q].N, 128);
   }
   const int mblocks = (int)ceil_div(base.M, 64);
-  hipLaunchKernelGGL((linear_mfma_group<64, 128, 4>), dim3(ceil_div((int64_t)mblocks * g.nb0[count], 8) * 8),
+  hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, GSTAGES>), dim3(ceil_div((int64_t)mblocks * g.nb0[count], 8) * 8),
                      dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
   LLHIP_LAUNCH_CHECK();
   return 0;
@@ -1325,7 +1336,7 @@ extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {
   a.fqS = (int)d->fq_S;
   a.mul_sh = (int)d->mul_sh;
   const int mblocks = (int)ceil_div(M, 64), nblocks = (int)ceil_div(N, 128);
-  hipLaunchKernelGGL(linear_mfma_dual, dim3(ceil_div((int64_t)mblocks * nblocks, 8) * 8), dim3(512),
+  hipLaunchKernelGGL(linear_mfma_dual<GSTAGES>, dim3(ceil_div((int64_t)mblocks * nblocks, 8) * 8), dim3(512),
                      GSTAGES * (64 + 2 * 128) * 64, s, p, a, mblocks, nblocks);
   LLHIP_LAUNCH_CHECK();
   return 0;

@@ -184,11 +184,12 @@ def test_linear_group_equals_separate_launches(M, K):
         _lib.call("llhip_linear_group", ptr(ad), M, K, K, 5, probs, ptr(workspace()), stream())
 
 
-@pytest.mark.parametrize("M,K,N", [(512, 896, 4864), (300, 128, 200), (40, 100, 64)])
-def test_gate_up_equals_the_three_ops(M, K, N):
+@pytest.mark.parametrize("M,K,N,pad", [(512, 896, 4864, 0), (512, 896, 4864, 5), (300, 128, 200, 4), (40, 100, 64, 5)])
+def test_gate_up_equals_the_three_ops(M, K, N, pad):
     """llhip_gate_up (gate linear with the silu epilogue, up linear with the mul epilogue on the
-    gate's output, quant of the product, in one launch) equals the three ops run one by one; K = 100
-    runs the op-by-op fallback inside the entry point."""
+    gate's output, quant of the product, in one launch) equals the three ops run one by one; output
+    rows of N + pad elements (pad 0 and 4: the word stores, 5: element stores); K = 100 runs the
+    op-by-op fallback inside the entry point."""
     from llaccel_amd import _lib
     from oracle import golden_np as OO
     from tests.gpu_helpers import ptr, stream, torch, up
@@ -206,7 +207,7 @@ def test_gate_up_equals_the_three_ops(M, K, N):
     fq = OO.vquant(f, fqM, fqS)
     d = _lib.GateUpDesc()
     keep = [up(a, np.int8), up(wg, np.int8), up(rqg, np.int32), up(bg, np.int32), up(wu, np.int8), up(rqu, np.int32)]
-    ld = N + 5
+    ld = N + pad
     outs = [t.zeros((M, ld), dtype=t.int16, device="cuda"), t.zeros((M, ld), dtype=t.int16, device="cuda"),
             t.zeros((M, ld), dtype=t.int8, device="cuda")]
     d.A, d.M, d.K, d.lda = ptr(keep[0]), M, K, K
