@@ -382,6 +382,26 @@ uint32_t llhip_dev_max_attention_head_dim(void);
 /* device.h:22 (device side): the DRAM's device address, valid until the DRAM next grows */
 void* llhip_dev_dram_ptr(llhip_device* dev);
 
+/* ---- float side: activation calibration and SmoothQuant over fp32 tensors on the GPU ---- */
+/* calibrate.py:56-66 (AbsMaxRecorder.run_node), smoothquant.py:95-99 (recorder): running maxima of
+ * |x| over the rows of x [rows][ld] -- per column into col_max [cols] and over the tensor into
+ * amax [1] (either may be NULL; both start at the caller's values, 0 for a fresh record).  Exact in
+ * any order.  Non-finite values are not folded in but counted into nonfinite [1]. */
+int llhip_f32_absmax(const float* x, int64_t rows, int64_t cols, int64_t ld, float* col_max, float* amax,
+                     int32_t* nonfinite, void* stream);
+/* calibrate.py:67-72: out_min [1] = min(out_min, min over the rows of x [rows][width] of
+ * sqrt(mean(x^2))), in double */
+int llhip_f32_rms_min(const float* x, int64_t rows, int64_t width, double* out_min, void* stream);
+/* smoothquant.py:250-261: x [rows][ld] in place: x * col_mul[c], then / col_div[c], then / row_div[r],
+ * each an fp32 operation (NULL skips one) */
+int llhip_f32_rescale(float* x, int64_t rows, int64_t cols, int64_t ld, const float* col_mul, const float* col_div,
+                      const float* row_div, void* stream);
+/* smoothquant.py:152-163 (quantization_objective, weight terms): out [2] += the sums over W [rows][cols]
+ * (rows of cols floats) of w^2 * act_err[c] and (q - w)^2 * act_energy[c], w = W * scales[c], q = w
+ * rounded to the row's int8 grid max|w| / 127 (half to even, clamped to [-128, 127]) */
+int llhip_f32_smooth_objective(const float* W, int64_t rows, int64_t cols, const float* scales, const float* act_err,
+                               const float* act_energy, double* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

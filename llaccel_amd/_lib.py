@@ -58,6 +58,10 @@ _SIGS = {
     "llhip_rope_quant": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _p,
                          _i64, _i64, _p],
     "llhip_quant_rows_i8": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
+    "llhip_f32_absmax": [_p, _i64, _i64, _i64, _p, _p, _p, _p],
+    "llhip_f32_rms_min": [_p, _i64, _i64, _p, _p],
+    "llhip_f32_rescale": [_p, _i64, _i64, _i64, _p, _p, _p, _p],
+    "llhip_f32_smooth_objective": [_p, _i64, _i64, _p, _p, _p, _p, _p],
     "llhip_quant_i16": [_p, _i64, _i64, _p, _p, _p],
     "llhip_rmsnorm_quant": [_p, _i64, _p],
     "llhip_dev_create": [ctypes.c_uint64, _i32],

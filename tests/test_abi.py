@@ -42,13 +42,13 @@ def test_header_declarations_cite_the_reference():
         if name in ("llhip_abi_version", "llhip_last_error", "llhip_workspace_bytes"):
             continue
         # the comment block directly above each compute entry point cites the reference function it
-        # replaces: golden.py:<lines> (the datapath), verify.py:<lines> (record verification) or
+        # replaces: golden.py:<lines> (the datapath), verify.py:<lines> (record verification),
         # refquant.py:<lines> (the qgraph producer), device.h:<lines> / funcsim.cpp:<lines> (the
-        # instruction-set device); an entry point with no reference counterpart says so and names
-        # the callers it is for
+        # instruction-set device), calibrate.py / smoothquant.py:<lines> (the float side); an entry
+        # point with no reference counterpart says so and names the callers it is for
         idx = text.index(name + "(")
         before = text[:idx].rsplit(");", 1)[-1]
-        assert (re.search(r"((golden|verify|refquant)\.py|device\.h|funcsim\.cpp):\d+", before)
+        assert (re.search(r"((golden|verify|refquant|calibrate|smoothquant)\.py|device\.h|funcsim\.cpp):\d+", before)
                 or re.search(r"No counterpart in the reference: .* for callers", before, re.S)), name
 
 

@@ -184,12 +184,19 @@ def test_linear_group_equals_separate_launches(M, K):
         _lib.call("llhip_linear_group", ptr(ad), M, K, K, 5, probs, ptr(workspace()), stream())
 
 
-@pytest.mark.parametrize("M,K,N,pad", [(512, 896, 4864, 0), (512, 896, 4864, 5), (300, 128, 200, 4), (40, 100, 64, 5)])
-def test_gate_up_equals_the_three_ops(M, K, N, pad):
+# (silu Mi, Si, sh_out, mul_sh, fq_M, fq_S): the model's kind of parameters, then the extremes of the
+# shifts the exact double-precision and 32-bit epilogue arithmetic must hold for (0, 31, 32, 52, 53, 63)
+PARAMS = [(1 << 30, 30, 16, 11, 1518500250, 38), ((1 << 32) - 1, 0, 31, 31, (1 << 32) - 1, 52),
+          ((1 << 32) - 1, 53, 0, 32, 3, 0), (12345, 63, 63, 0, (1 << 31) + 7, 63), (987654321, 52, 32, 30, 1, 53)]
+
+
+@pytest.mark.parametrize("M,K,N,pad,par", [(512, 896, 4864, 0, 0), (512, 896, 4864, 5, 0), (300, 128, 200, 4, 0),
+                                           (40, 100, 64, 5, 0)] + [(70, 128, 256, 0, i) for i in range(1, 5)])
+def test_gate_up_equals_the_three_ops(M, K, N, pad, par):
     """llhip_gate_up (gate linear with the silu epilogue, up linear with the mul epilogue on the
     gate's output, quant of the product, in one launch) equals the three ops run one by one; output
     rows of N + pad elements (pad 0 and 4: the word stores, 5: element stores); K = 100 runs the
-    op-by-op fallback inside the entry point."""
+    op-by-op fallback inside the entry point; PARAMS[1:] put every shift at its extremes."""
     from llaccel_amd import _lib
     from oracle import golden_np as OO
     from tests.gpu_helpers import ptr, stream, torch, up
@@ -200,10 +207,11 @@ def test_gate_up_equals_the_three_ops(M, K, N, pad):
     wg, wu = (rng.integers(-127, 128, (N, K)).astype(np.int8) for _ in range(2))
     rqg, rqu = random_rq(rng, N, K, False), random_rq(rng, N, K, False)
     bg, bu = rng.integers(-(2**20), 2**20, N), None
-    silu = {"Mi": 1 << 30, "Si": 30, "sh_out": 16}
-    mul_sh, fqM, fqS = 11, 1518500250, 38
-    sg = gpu_linear(a, wg, rqg, bias=bg, epilogue="silu", silu=silu)
-    f = gpu_linear(a, wu, rqu, epilogue="mul", aux=sg, aux_shift=mul_sh)
+    Mi, Si, sh_out, mul_sh, fqM, fqS = PARAMS[par]
+    silu = {"Mi": Mi, "Si": Si, "sh_out": sh_out}
+    # the three ops in the oracle
+    sg = O.linear_c(a, wg, rqg, bg, False, "silu", None, 0, silu)
+    f = O.linear_c(a, wu, rqu, None, False, "mul", sg, mul_sh, None)
     fq = OO.vquant(f, fqM, fqS)
     d = _lib.GateUpDesc()
     keep = [up(a, np.int8), up(wg, np.int8), up(rqg, np.int32), up(bg, np.int32), up(wu, np.int8), up(rqu, np.int32)]
@@ -219,4 +227,5 @@ def test_gate_up_equals_the_three_ops(M, K, N, pad):
     got = [o.cpu().numpy() for o in outs]
     for g_, w_ in zip(got, (sg, f, fq)):
         assert np.array_equal(g_[:, :N], w_) and not g_[:, N:].any()
-    assert np.count_nonzero(f) > f.size // 2  # the products are not degenerate
+    if par == 0:
+        assert np.count_nonzero(f) > f.size // 2  # the products are not degenerate
