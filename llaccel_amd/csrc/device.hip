@@ -9,13 +9,14 @@
 // messages), accumulates the same performance counters (functions of the operands and POS only) and
 // enqueues the instruction's kernels on one stream: DMA and KV_WRITE as strided copies, GEMM as one
 // kernel over the SRAM weight tiles, the VEC ops and ATTN through the datapath's own kernels.
-// Data-dependent faults (an invalid requant table entry) are flagged on the device; the flag is read
-// before the next instruction that writes DRAM (DMA_STORE, KV_WRITE), when the program drains, and when
-// a later instruction fails, so the program stops with the simulator's message before any later DRAM
-// write.  A DMA or KV_WRITE that fails at a row first writes the rows before it, as the simulator does.
-// After a failed run DRAM is the simulator's; SRAM written by the failed instruction (a GEMM's valid
-// columns, ROPE/ATTN rows before a failing row, which the device does not write) and by the VEC/GEMM
-// instructions after an invalid requant entry may differ from it.
+// Data-dependent faults (an invalid requant table entry) set a device status flag.  The copies of the
+// DMA and KV_WRITE instructions read it and write nothing once it is set, so no DMA or KV_WRITE after
+// the failing GEMM changes memory, as in the simulator, which stops at that GEMM (funcsim.cpp:239);
+// the host reads the flag when the program drains and when a later instruction fails, and then
+// reports the simulator's message.  A DMA or KV_WRITE that fails at a row first writes the rows
+// before it, as the simulator does.  After a failed run DRAM is the simulator's; SRAM written by the
+// failed instruction (a GEMM's valid columns, ROPE/ATTN rows before a failing row, which the device
+// does not write) and by VEC/GEMM/ATTN instructions after an invalid requant entry may differ.
 #include <array>
 #include <cstring>
 #include <deque>
@@ -82,8 +83,10 @@ void rc_ok(int rc) {
 
 // ---- kernels ----------------------------------------------------------------------------
 // rows x bytes strided copy; 16-byte units when every address and stride allows it
+// gate: a status flag; once it is set the copy writes nothing (NULL: always copy)
 __global__ void copy_rows16(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, uint32_t rows, uint32_t units,
-                            uint64_t ss, uint64_t ds) {
+                            uint64_t ss, uint64_t ds, const int32_t* gate) {
+  if (gate && *gate) return;
   const uint64_t n = (uint64_t)rows * units;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
     const uint64_t r = i / units, u = i % units;
@@ -91,7 +94,8 @@ __global__ void copy_rows16(uint8_t* __restrict__ dst, const uint8_t* __restrict
   }
 }
 __global__ void copy_rows8(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, uint32_t rows, uint32_t bytes,
-                           uint64_t ss, uint64_t ds) {
+                           uint64_t ss, uint64_t ds, const int32_t* gate) {
+  if (gate && *gate) return;
   const uint64_t n = (uint64_t)rows * bytes;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
     const uint64_t r = i / bytes, b = i % bytes;
@@ -106,8 +110,10 @@ struct CopyBatch {
   const uint8_t* src[kBatch];
   uint32_t rows[kBatch], units[kBatch];
   uint64_t ss[kBatch], ds[kBatch];
+  const int32_t* gate;
 };
 __global__ void copy_batch16(CopyBatch b) {
+  if (b.gate && *b.gate) return;
   const int c = blockIdx.y;
   const uint32_t units = b.units[c];
   const uint64_t n = (uint64_t)b.rows[c] * units;
@@ -120,7 +126,8 @@ __global__ void copy_batch16(CopyBatch b) {
 }
 // destination rows that overlap each other: rows in order, one workgroup (later rows win)
 __global__ void copy_rows_ordered(uint8_t* dst, const uint8_t* src, uint32_t rows, uint32_t bytes, uint64_t ss,
-                                  uint64_t ds) {
+                                  uint64_t ds, const int32_t* gate) {
+  if (gate && *gate) return;
   for (uint32_t r = 0; r < rows; ++r) {
     for (uint32_t b = threadIdx.x; b < bytes; b += blockDim.x) dst[r * ds + b] = src[r * ss + b];
     __syncthreads();
@@ -213,7 +220,8 @@ __global__ void gather_rope(const uint8_t* __restrict__ sram, uint32_t table, ui
 }
 // KV_WRITE: src [M][Hkv*D] -> base + kvh*stride + (pos+m)*D (funcsim.cpp:390-398)
 __global__ void kv_rows(uint8_t* __restrict__ dram, const uint8_t* __restrict__ src, uint64_t base, uint32_t M,
-                        uint32_t Hkv, uint32_t D, uint64_t stride, uint32_t pos) {
+                        uint32_t Hkv, uint32_t D, uint64_t stride, uint32_t pos, const int32_t* gate) {
+  if (*gate) return;
   const uint64_t n = (uint64_t)M * Hkv * D;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
     const uint64_t d = i % D, r = i / D, kvh = r % Hkv, m = r / Hkv;
@@ -348,6 +356,7 @@ struct Device {
     }
     const int n = (int)pend.size();
     pend.clear();
+    b.gate = status;
     hipLaunchKernelGGL(copy_batch16, dim3(grid_for(most), n), dim3(256), 0, stream, b);
     hip_ok(hipGetLastError(), "kernel launch");
   }
@@ -361,9 +370,9 @@ struct Device {
     if (!ok) {
       flush();
       if (load)
-        copy(sram + sramA, dram + dramA, (uint32_t)rows, (uint32_t)bytes, ss, ds);
+        copy(sram + sramA, dram + dramA, (uint32_t)rows, (uint32_t)bytes, ss, ds, status);
       else
-        copy(dram + dramA, sram + sramA, (uint32_t)rows, (uint32_t)bytes, ss, ds);
+        copy(dram + dramA, sram + sramA, (uint32_t)rows, (uint32_t)bytes, ss, ds, status);
       return;
     }
     // ranges: [lo, lo + span) in SRAM (sram side) or DRAM (dram side)
@@ -385,16 +394,19 @@ struct Device {
     if ((int)pend.size() == kBatch) flush();
   }
 
-  void copy(uint8_t* dst, const uint8_t* src, uint32_t rows, uint32_t bytes, uint64_t ss, uint64_t ds) {
+  // gate: the status flag for the copies of DMA instructions, NULL for the copy-back of an op's
+  // in-place result
+  void copy(uint8_t* dst, const uint8_t* src, uint32_t rows, uint32_t bytes, uint64_t ss, uint64_t ds,
+            const int32_t* gate = nullptr) {
     if (!rows || !bytes) return;
     if (rows > 1 && ds < bytes) {
-      hipLaunchKernelGGL(copy_rows_ordered, dim3(1), dim3(256), 0, stream, dst, src, rows, bytes, ss, ds);
+      hipLaunchKernelGGL(copy_rows_ordered, dim3(1), dim3(256), 0, stream, dst, src, rows, bytes, ss, ds, gate);
     } else if (((uintptr_t)dst | (uintptr_t)src | ss | ds | bytes) % 16 == 0) {
       hipLaunchKernelGGL(copy_rows16, dim3(grid_for((uint64_t)rows * bytes / 16)), dim3(256), 0, stream, dst, src, rows,
-                         bytes / 16, ss, ds);
+                         bytes / 16, ss, ds, gate);
     } else {
       hipLaunchKernelGGL(copy_rows8, dim3(grid_for((uint64_t)rows * bytes)), dim3(256), 0, stream, dst, src, rows, bytes,
-                         ss, ds);
+                         ss, ds, gate);
     }
     hip_ok(hipGetLastError(), "kernel launch");
   }
@@ -411,8 +423,9 @@ struct Device {
     }
   }
 
-  // Reads the requant status flag once the GEMMs enqueued so far have run; raises the simulator's
-  // error if one of them met an invalid table entry (funcsim.cpp:239).
+  // Reads the requant status flag once the work enqueued so far has run (when the program drains or
+  // an instruction fails); raises the simulator's error if a GEMM met an invalid table entry
+  // (funcsim.cpp:239).
   void requant_check() {
     if (!rq_unchecked) return;
     rq_unchecked = false;
@@ -427,7 +440,6 @@ struct Device {
   void dma(const uint32_t* in, bool load) {
     const uint32_t sramA = in[2], dramA = in[3], rows = in[4], rowBytes = in[5], srcStride = in[6], dstStride = in[7];
     if (rowBytes % 16 || sramA % 16) bad("DMA row/addr not 16-B aligned");
-    if (!load) requant_check();
     uint64_t beats = 0, sramReadBytes = 0;
     uint32_t r = 0;
     // a row that fails its check: the rows before it are copied first (funcsim.cpp:162-186 copies
@@ -679,7 +691,6 @@ struct Device {
       bad("KV_WRITE invalid dimensions/DRAM cache stride");
     const uint32_t row = Hkv * D;
     chk(src, uint64_t(M) * row, "KV_WRITE src");
-    requant_check();
     for (uint32_t m = 0; m < M; ++m)
       for (uint32_t kvh = 0; kvh < Hkv; ++kvh) {
         const uint64_t d = uint64_t(base) + uint64_t(kvh) * kvStride + uint64_t(pos + m) * D;
@@ -703,7 +714,7 @@ struct Device {
   // heads 0..Hkv-1 of M rows of `src` (row stride Hkv * D) into the cache rows p .. p+M-1
   void kv_launch(uint32_t src, uint32_t base, uint32_t M, uint32_t Hkv, uint32_t D, uint32_t kvStride, uint32_t p) {
     hipLaunchKernelGGL(kv_rows, dim3(grid_for(uint64_t(M) * Hkv * D)), dim3(256), 0, stream, dram, sram + src,
-                       uint64_t(base), M, Hkv, D, uint64_t(kvStride), p);
+                       uint64_t(base), M, Hkv, D, uint64_t(kvStride), p, status);
     hip_ok(hipGetLastError(), "kernel launch");
   }
 
