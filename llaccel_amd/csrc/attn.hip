@@ -661,11 +661,15 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
 // partials and requantises.  Every partial is an exact integer max or sum, so the split changes
 // no result.  The per-tile arithmetic is that of attention_tiled (16 query rows per workgroup,
 // S^T = K . Q^T, V^T by selection MFMAs, base-128 probability digits).
+// ONE (a single query row, the decode launch): phase 1 also stores the row's scores (4 bytes per
+// key), and phase 3 sums the LUT exponentials of all of them itself -- every workgroup of a head
+// reads the head's T scores -- so phase 2 and its launch are not needed.
 // ---------------------------------------------------------------------------------------
 struct SplitWs {
   int32_t* maxv;  // [pairs][S][16]
   int32_t* sumv;  // [pairs][S][16]
   int32_t* outv;  // [pairs][S][16][D]
+  int32_t* sc;    // ONE: [pairs][ntiles * 64] scores of row 0
 };
 
 template <int D>
@@ -674,10 +678,11 @@ __device__ __forceinline__ SplitWs split_ws(int32_t* ws, int64_t pairs, int S) {
   w.maxv = ws;
   w.sumv = ws + pairs * S * AT_ROWS;
   w.outv = ws + 2 * pairs * S * AT_ROWS;
+  w.sc = w.outv + pairs * S * AT_ROWS * D;
   return w;
 }
 
-template <int D, int PHASE>
+template <int D, int PHASE, bool ONE>
 __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_split(AttnArgs p, int S, int tps, int32_t* ws) {
   using C = AttnTileCfg<D>;
   constexpr int DK = C::DK, DB = C::DB;
@@ -720,6 +725,18 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_split(Att
     for (int c = 0; c < DK; ++c)
       qf[c] = ld16(qr, (m < p.M && 64 * c + 16 * lg < D) ? (uint32_t)(lr * p.ldq + 64 * c + 16 * lg) : LD_OOB);
   }
+  // ONE, phase 3: row 0's scores of the first SPF * blockDim keys, loaded before anything waits
+  constexpr int SPF = (ONE && PHASE == 3) ? 16 : 1;
+  const int t0 = min(pos + 1, (int)p.max_seq);
+  const Rsrc scr = rsrc(w.sc + pair * ((int64_t)ntiles * 64), (int64_t)t0 * 4);
+  int32_t sv[SPF];
+  if constexpr (ONE && PHASE == 3) {
+#pragma unroll
+    for (int u = 0; u < SPF; ++u) {
+      const int k = tid + u * (int)blockDim.x;
+      sv[u] = ld4(scr, k < t0 ? (uint32_t)(4 * k) : LD_OOB);
+    }
+  }
   if (PHASE >= 2) {
     const Rsrc ir = rsrc(kExpI, sizeof(kExpI)), fr = rsrc(kExpF, sizeof(kExpF));
     for (int idx = tid; idx < LUT_DW; idx += blockDim.x)
@@ -747,6 +764,7 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_split(Att
 
   if (PHASE == 1) {
     int32_t vmax = INT32_MIN;
+    int32_t* scrow = w.sc + pair * ((int64_t)ntiles * 64);
     for (int kt = kt0 + wave; kt < kt1; kt += nw) {
       v4i st[4];
       scores(kt, st);
@@ -754,7 +772,10 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_split(Att
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (key(kt, j, r) < tlim) vmax = max(vmax, st[j][r]);
+          if (key(kt, j, r) < tlim) {
+            vmax = max(vmax, st[j][r]);
+            if (ONE && lr == 0) scrow[key(kt, j, r)] = st[j][r];
+          }
     }
     vmax = max(vmax, __shfl_xor(vmax, 16));
     vmax = max(vmax, __shfl_xor(vmax, 32));
@@ -804,11 +825,37 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_split(Att
   }
 
   // PHASE 3: the row's total over all splits -> inv, then this split's P . V
-  __syncthreads();  // every lane has its maximum
-  for (int idx = tid; idx < S * AT_ROWS; idx += blockDim.x) (&spart[0][0])[idx] = w.sumv[pair * S * AT_ROWS + idx];
-  __syncthreads();
   uint32_t total = 0;
-  for (int q = 0; q < S; ++q) total += (uint32_t)spart[q][lr];
+  if constexpr (ONE) {
+    // row 0's total from its stored scores, every thread a share of the keys (the first SPF of
+    // them already in registers)
+    int32_t mx0 = INT32_MIN;
+    for (int q = 0; q < S; ++q) mx0 = max(mx0, spart[q][0]);
+    uint32_t vs = 0;
+    const int bd = (int)blockDim.x;
+#pragma unroll
+    for (int u = 0; u < SPF; ++u)
+      if (tid + u * bd < t0) vs += prob_lds(mx0 - sv[u], pq, ei, ef);
+    for (int k0 = tid + SPF * bd; k0 < t0; k0 += 8 * bd) {
+      int32_t sb[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sb[u] = ld4(scr, k0 + u * bd < t0 ? (uint32_t)(4 * (k0 + u * bd)) : LD_OOB);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u * bd < t0) vs += prob_lds(mx0 - sb[u], pq, ei, ef);
+    }
+    for (int o = 32; o > 0; o >>= 1) vs += (uint32_t)__shfl_xor((int)vs, o);
+    __syncthreads();  // every lane has read spart (the maxima)
+    if (lane == 0) red[wave][0] = (int32_t)vs;
+    __syncthreads();
+    for (int q = 0; q < nw; ++q) total += (uint32_t)red[q][0];
+    if (lr != 0) total = 0;  // rows past M have no keys
+  } else {
+    __syncthreads();  // every lane has its maximum
+    for (int idx = tid; idx < S * AT_ROWS; idx += blockDim.x) (&spart[0][0])[idx] = w.sumv[pair * S * AT_ROWS + idx];
+    __syncthreads();
+    for (int q = 0; q < S; ++q) total += (uint32_t)spart[q][lr];
+  }
   const uint32_t inv = 0x80000000u / (total > 1u ? total : 1u);  // 2^31 / total (golden.py:174)
   const uint32_t cap = (1u << p.pb) - 1u;
   const int shp = 31 - p.pb;
@@ -1036,8 +1083,10 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   // Long contexts with few (row block, head) pairs: split the key tiles over S workgroups per pair
   // (three reduction launches + a finishing one) so every CU streams a share of K and V.
   const int64_t rblocks = ceil_div(M, AT_ROWS), pairs = H * rblocks, ktiles = ceil_div(tmax, 64);
-  // bytes of the partials of S splits: per-split row maxima and sums, and value partials
-  auto split_need = [&](int64_t S) { return pairs * S * AT_ROWS * (2 + D) * 4; };
+  // bytes of the partials of S splits: per-split row maxima and sums, and value partials (+ one
+  // row's scores for a single-row launch)
+  const bool one = M == 1;
+  auto split_need = [&](int64_t S) { return pairs * S * AT_ROWS * (2 + D) * 4 + (one ? pairs * ktiles * 64 * 4 : 0); };
   if (!row_pos && split_ws && tmax <= AT_MAX_T && ktiles >= AT_SPLIT_MIN_TILES && pairs * 4 <= cus &&
       split_need(2) <= split_bytes) {
     int S = (int)std::min<int64_t>(std::min<int64_t>(ceil_div(cus, pairs), ceil_div(ktiles, 4)), AT_SPLIT_MAXS);
@@ -1051,9 +1100,14 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
     dim3 grid((unsigned)H, (unsigned)rblocks, (unsigned)S), block(64 * nw);
     dim3 fgrid((unsigned)H, (unsigned)rblocks, (unsigned)ceil_div(std::min<int64_t>(M, AT_ROWS) * D, 256));
 #define LLHIP_SPLIT(DD)                                                                      \
-  hipLaunchKernelGGL((attention_split<DD, 1>), grid, block, 0, s, p, S, tps, sw);           \
-  hipLaunchKernelGGL((attention_split<DD, 2>), grid, block, 0, s, p, S, tps, sw);           \
-  hipLaunchKernelGGL((attention_split<DD, 3>), grid, block, 0, s, p, S, tps, sw);           \
+  if (one) {                                                                                \
+    hipLaunchKernelGGL((attention_split<DD, 1, true>), grid, block, 0, s, p, S, tps, sw);   \
+    hipLaunchKernelGGL((attention_split<DD, 3, true>), grid, block, 0, s, p, S, tps, sw);   \
+  } else {                                                                                  \
+    hipLaunchKernelGGL((attention_split<DD, 1, false>), grid, block, 0, s, p, S, tps, sw);  \
+    hipLaunchKernelGGL((attention_split<DD, 2, false>), grid, block, 0, s, p, S, tps, sw);  \
+    hipLaunchKernelGGL((attention_split<DD, 3, false>), grid, block, 0, s, p, S, tps, sw);  \
+  }                                                                                         \
   if (fold)                                                                                 \
     hipLaunchKernelGGL((attention_split_finish_wo<DD>), dim3((unsigned)H, (unsigned)ceil_div(p.wo_N, WO_SLICE)),    \
                        dim3(256), 0, s, p, S, sw);                                                  \
