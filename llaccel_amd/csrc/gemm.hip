@@ -629,14 +629,22 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
   }
 }
 
-// Split-K (part != NULL): workgroup (tile, z = blockIdx.y) accumulates K tiles [z*kps, z*kps + kps)
-// and stores its int32 partial tile into plane z of part [splits][M][N]; linear_splitk_finish
-// sums the planes (integer addition: any split gives the same sum) and applies the epilogue.
+// Output tiles l = l0, l0 + lstep, ... < lend (logical index: M-block l % mblocks, N-block
+// l / mblocks), one after another.  The first stages of the next tile are issued as soon as the
+// K loop of this one has finished reading the ring, so their memory latency passes during this
+// tile's epilogue (which works from registers only).  The K-loop waits stay correct with the
+// epilogue's stores in flight: vector loads complete in order, so at most n tiles' loads
+// outstanding still means every earlier stage has landed.
+// Split-K (part != NULL, one tile per workgroup): workgroup (tile, z = blockIdx.y) accumulates K
+// tiles [z*kps, z*kps + kps) and stores its int32 partial tile into plane z of part
+// [splits][M][N]; linear_splitk_finish sums the planes (integer addition: any split gives the same
+// sum) and applies the epilogue.
 template <int EPI, bool OUT8, int GM, int GN, int NW, int NS>
-__device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, int kps, int32_t* part) {
+__device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int l0, int lstep, int lend, int kps,
+                                           int32_t* part) {
   using T = MfmaTile<GM, GN, NW, NS>;
   extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [NS][A GMx64 | W GNx64]
-  const int m0 = mb * GM, n0 = nbk * GN;
+  if (l0 >= lend) return;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave & 1) * T::WROWS, wn = (wave >> 1) * T::WCOLS;
@@ -645,18 +653,21 @@ __device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, 
   const int8_t* asrc[4];  // fixed sizes (see wait_vmcnt)
   const int8_t* wsrc[4];
   const int kbase = (int)blockIdx.y * kps * 64;  // first K byte of this split
+  auto sources = [&](int l) {
+    const int m0 = (l % mblocks) * GM, n0 = (l / mblocks) * GN;
 #pragma unroll
-  for (int i = 0; i < T::LA; ++i) {
-    const int r = (wave * T::LA + i) * 16 + (lane >> 2);
-    const int gm = min(m0 + r, p.M - 1);
-    asrc[i] = p.A + (int64_t)gm * p.lda + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
-  }
+    for (int i = 0; i < T::LA; ++i) {
+      const int r = (wave * T::LA + i) * 16 + (lane >> 2);
+      const int gm = min(m0 + r, p.M - 1);
+      asrc[i] = p.A + (int64_t)gm * p.lda + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
+    }
 #pragma unroll
-  for (int i = 0; i < T::LW; ++i) {
-    const int r = (wave * T::LW + i) * 16 + (lane >> 2);
-    const int gn = min(n0 + r, p.N - 1);
-    wsrc[i] = p.W + (int64_t)gn * p.K + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
-  }
+    for (int i = 0; i < T::LW; ++i) {
+      const int r = (wave * T::LW + i) * 16 + (lane >> 2);
+      const int gn = min(n0 + r, p.N - 1);
+      wsrc[i] = p.W + (int64_t)gn * p.K + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
+    }
+  };
   auto issue = [&](int kt) {
     int8_t* st = ring + (kt % NS) * T::STAGE_BYTES;
     const int k0 = kt * 64;
@@ -695,115 +706,140 @@ __device__ __forceinline__ void mfma_tile(const LinearArgs& p, int mb, int nbk, 
   __shared__ uint32_t sig32[EPI == EPI_SILU ? 129 : 1];
   if (EPI == EPI_SILU && tid < 129) sig32[tid] = reinterpret_cast<const uint32_t*>(kSig)[tid];
   const uint16_t* sig16 = reinterpret_cast<const uint16_t*>(sig32);
-  // epilogue column parameters, loaded while the first tiles stream in
-  ColRq cq[T::WN];
-#pragma unroll
-  for (int j = 0; j < T::WN; ++j) {
-    const int n = min(n0 + wn + 32 * j + (lane & 31), p.N - 1);
-    cq[j] = make_colrq(p.rq[2 * n], p.rq[2 * n + 1], p.bias ? p.bias[n] : 0);  // (acc+bias)*M = acc*M + bias*M
-  }
-
-  v16i acc[T::WM][T::WN];
-#pragma unroll
-  for (int i = 0; i < T::WM; ++i)
-#pragma unroll
-    for (int j = 0; j < T::WN; ++j) acc[i][j] = v16i{};
-
   const int ktiles = min(kps, p.K / 64 - (int)blockIdx.y * kps);
+  sources(l0);
   for (int s0 = 0; s0 < NS - 1; ++s0)
     if (s0 < ktiles) issue(s0);
-  // tile 0 landed: the loads of the tiles issued after it may be outstanding
-  wait_tiles<T::LOADS, NS - 2>(min(ktiles, NS - 1) - 1);
-  lds_barrier();
-  v4i fa0[T::WM], fb0[T::WN], fa1[T::WM], fb1[T::WN];
-#pragma unroll
-  for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(ring + aoff[i][0]);
-#pragma unroll
-  for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(ring + woff[j][0]);
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int8_t* st = ring + (kt % NS) * T::STAGE_BYTES;
-    // first K step of tile kt (fragments already in registers) while the second one's are read
-#pragma unroll
-    for (int i = 0; i < T::WM; ++i) fa1[i] = *reinterpret_cast<const v4i*>(st + aoff[i][1]);
-#pragma unroll
-    for (int j = 0; j < T::WN; ++j) fb1[j] = *reinterpret_cast<const v4i*>(st + woff[j][1]);
-#pragma unroll
-    for (int i = 0; i < T::WM; ++i)
-#pragma unroll
-      for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
-    mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
-    // Tile kt+1 landed once at most the loads of the tiles issued after it (kt+2 .. kt+NS-2) are
-    // outstanding; after the barrier every wave's copies of it are visible and every wave has
-    // finished reading stage (kt-1) % NS, which issue(kt + NS - 1) overwrites.  A bare s_barrier:
-    // __syncthreads() would also drain the later tiles still in flight.
-    wait_tiles<T::LOADS, NS - 2>(min(ktiles, kt + NS - 1) - kt - 2);
-    lds_barrier();
-    if (kt + NS - 1 < ktiles) issue(kt + NS - 1);
-    // second K step of tile kt while the next tile's first-step fragments are read (after the
-    // last tile they come from a stale stage and are never used)
-    const int8_t* sn = ring + ((kt + 1) % NS) * T::STAGE_BYTES;
-#pragma unroll
-    for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(sn + aoff[i][0]);
-#pragma unroll
-    for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(sn + woff[j][0]);
-#pragma unroll
-    for (int i = 0; i < T::WM; ++i)
-#pragma unroll
-      for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
-    mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
-  }
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stale fragment reads have returned
-
-  if (part) {
-    // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32; each
-    // element store of the wave writes 2 rows x 128 contiguous bytes
-    int32_t* plane = part + (int64_t)blockIdx.y * p.M * p.N;
+  for (int l = l0;;) {
+    const int m0 = (l % mblocks) * GM, n0 = (l / mblocks) * GN;
+    // epilogue column parameters, loaded while the first K tiles stream in
+    ColRq cq[T::WN];
 #pragma unroll
     for (int j = 0; j < T::WN; ++j) {
-      const int n = n0 + wn + 32 * j + (lane & 31);
+      const int n = min(n0 + wn + 32 * j + (lane & 31), p.N - 1);
+      cq[j] = make_colrq(p.rq[2 * n], p.rq[2 * n + 1], p.bias ? p.bias[n] : 0);  // (acc+bias)*M = acc*M + bias*M
+    }
+
+    v16i acc[T::WM][T::WN];
+#pragma unroll
+    for (int i = 0; i < T::WM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::WN; ++j) acc[i][j] = v16i{};
+
+    // K tile 0 landed: the loads of the tiles issued after it may be outstanding
+    wait_tiles<T::LOADS, NS - 2>(min(ktiles, NS - 1) - 1);
+    lds_barrier();
+    v4i fa0[T::WM], fb0[T::WN], fa1[T::WM], fb1[T::WN];
+#pragma unroll
+    for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(ring + aoff[i][0]);
+#pragma unroll
+    for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(ring + woff[j][0]);
+    for (int kt = 0; kt < ktiles; ++kt) {
+      const int8_t* st = ring + (kt % NS) * T::STAGE_BYTES;
+      // first K step of tile kt (fragments already in registers) while the second one's are read
+#pragma unroll
+      for (int i = 0; i < T::WM; ++i) fa1[i] = *reinterpret_cast<const v4i*>(st + aoff[i][1]);
+#pragma unroll
+      for (int j = 0; j < T::WN; ++j) fb1[j] = *reinterpret_cast<const v4i*>(st + woff[j][1]);
 #pragma unroll
       for (int i = 0; i < T::WM; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-          if (m < p.M && n < p.N) plane[(int64_t)m * p.N + n] = acc[i][j][r];
-        }
-    }
-    return;
-  }
-
-  // one wave-uniform choice of the requant form
-  bool col_fast = true;
+        for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
+      mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
+      // Tile kt+1 landed once at most the loads of the tiles issued after it (kt+2 .. kt+NS-2) are
+      // outstanding; after the barrier every wave's copies of it are visible and every wave has
+      // finished reading stage (kt-1) % NS, which issue(kt + NS - 1) overwrites.  A bare s_barrier:
+      // __syncthreads() would also drain the later tiles still in flight.
+      wait_tiles<T::LOADS, NS - 2>(min(ktiles, kt + NS - 1) - kt - 2);
+      lds_barrier();
+      if (kt + NS - 1 < ktiles) issue(kt + NS - 1);
+      // second K step of tile kt while the next tile's first-step fragments are read (after the
+      // last tile they come from a stale stage and are never used)
+      const int8_t* sn = ring + ((kt + 1) % NS) * T::STAGE_BYTES;
 #pragma unroll
-  for (int j = 0; j < T::WN; ++j) col_fast = col_fast && colrq_fast(cq[j]);
-  const bool fast = __all(col_fast);
+      for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(sn + aoff[i][0]);
+#pragma unroll
+      for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(sn + woff[j][0]);
+#pragma unroll
+      for (int i = 0; i < T::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
+      mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stale fragment reads have returned
+    // the next tile's first stages, once every wave is done with the ring
+    const int ln = l + lstep;
+    if (ln < lend) {
+      lds_barrier();
+      sources(ln);
+      for (int s0 = 0; s0 < NS - 1; ++s0)
+        if (s0 < ktiles) issue(s0);
+    }
 
-  if constexpr (OUT8) {
-    const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 4 == 0;
-    if (fast)
-      store_i8_tile<true>(p, acc, cq, m0 + wm, n0 + wn, full);
-    else
-      store_i8_tile<false>(p, acc, cq, m0 + wm, n0 + wn, full);
-    return;
+    if (part) {
+      // C layout of a 32x32 tile: lane l, element r -> row (r/4)*8 + (l/32)*4 + r%4, col l%32; each
+      // element store of the wave writes 2 rows x 128 contiguous bytes
+      int32_t* plane = part + (int64_t)blockIdx.y * p.M * p.N;
+#pragma unroll
+      for (int j = 0; j < T::WN; ++j) {
+        const int n = n0 + wn + 32 * j + (lane & 31);
+#pragma unroll
+        for (int i = 0; i < T::WM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = m0 + wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            if (m < p.M && n < p.N) plane[(int64_t)m * p.N + n] = acc[i][j][r];
+          }
+      }
+      if (ln >= lend) return;
+      l = ln;
+      continue;
+    }
+
+    // one wave-uniform choice of the requant form
+    bool col_fast = true;
+#pragma unroll
+    for (int j = 0; j < T::WN; ++j) col_fast = col_fast && colrq_fast(cq[j]);
+    const bool fast = __all(col_fast);
+
+    if constexpr (OUT8) {
+      const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 4 == 0;
+      if (fast)
+        store_i8_tile<true>(p, acc, cq, m0 + wm, n0 + wn, full);
+      else
+        store_i8_tile<false>(p, acc, cq, m0 + wm, n0 + wn, full);
+    } else {
+      // i16 output (with the aux-reading epilogues) from registers as well
+      const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 8 == 0 &&
+                        ((EPI != EPI_RESADD && EPI != EPI_MUL) || (p.ldaux % 4 == 0 && (uintptr_t)p.aux % 8 == 0));
+      if (fast)
+        store_i16_tile<EPI, true>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
+      else
+        store_i16_tile<EPI, false>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
+    }
+    if (ln >= lend) return;
+    l = ln;
   }
-
-  // i16 output (with the aux-reading epilogues) from registers as well
-  const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 8 == 0 &&
-                    ((EPI != EPI_RESADD && EPI != EPI_MUL) || (p.ldaux % 4 == 0 && (uintptr_t)p.aux % 8 == 0));
-  if (fast)
-    store_i16_tile<EPI, true>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
-  else
-    store_i16_tile<EPI, false>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
 }
 
 // The grid is padded to a multiple of 8 and workgroup b runs on XCD b % 8, which takes a
 // contiguous range of tiles (M fastest): the M-blocks that share a W panel share that XCD's L2.
+// Persistent form (persist != 0, no split): the grid is a multiple of 8 workgroups, at most one
+// per CU; XCD x takes the contiguous tile range [x * per, (x + 1) * per), per = ceil(tiles / 8),
+// and its gridDim.x / 8 workgroups step through it together, so the ones running at any time still
+// share W panels in that XCD's L2.
 template <int EPI, bool OUT8, int GM, int GN, int NW, int NS>
-__global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part) {
+__global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part,
+                                                       int persist) {
   const int b = blockIdx.x;
+  const int tiles = mblocks * nblocks;
+  if (persist) {
+    const int per = (tiles + 7) / 8, x = b % 8, lo = x * per;
+    mfma_tiles<EPI, OUT8, GM, GN, NW, NS>(p, mblocks, lo + b / 8, (int)gridDim.x / 8, min(lo + per, tiles), kps, part);
+    return;
+  }
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
-  if (logical >= mblocks * nblocks) return;
-  mfma_tile<EPI, OUT8, GM, GN, NW, NS>(p, logical % mblocks, logical / mblocks, kps, part);
+  mfma_tiles<EPI, OUT8, GM, GN, NW, NS>(p, mblocks, logical, 1, min(logical + 1, tiles), kps, part);
 }
 
 // Several linears of one input in one launch (the q, k, v projections of a prompt chunk): the
@@ -837,10 +873,11 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, Linea
   pp.ldo = g.ldo[q];
   pp.N = g.N[q];
   nbk -= g.nb0[q];
+  const int l = nbk * mblocks + mb;
   if (g.out8[q])
-    mfma_tile<EPI_NONE, true, GM, GN, NW, NS>(pp, mb, nbk, p.K / 64, nullptr);
+    mfma_tiles<EPI_NONE, true, GM, GN, NW, NS>(pp, mblocks, l, 1, l + 1, p.K / 64, nullptr);
   else
-    mfma_tile<EPI_NONE, false, GM, GN, NW, NS>(pp, mb, nbk, p.K / 64, nullptr);
+    mfma_tiles<EPI_NONE, false, GM, GN, NW, NS>(pp, mblocks, l, 1, l + 1, p.K / 64, nullptr);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1092,8 +1129,13 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
   const int kps = (int)ceil_div(ktiles, splits);
   splits = (int)ceil_div(ktiles, kps);
   int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
-  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW, GSTAGES>), dim3(ceil_div(mblocks * nblocks, 8) * 8, splits),
-                     dim3(T::NT), T::LDS_BYTES, stream, p, mblocks, nblocks, kps, part);
+  // more tiles than one round of workgroups: persistent workgroups, one per CU (the 4-stage ring of
+  // the large tiles fills a CU's LDS), each stepping through its XCD's tiles
+  const int per_cu = std::max(1, (160 * 1024) / T::LDS_BYTES);
+  const bool persist = !part && tiles > (int64_t)cus * per_cu;
+  const unsigned gx = persist ? (unsigned)(cus / 8 * 8 * per_cu) : (unsigned)(ceil_div(mblocks * nblocks, 8) * 8);
+  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW, GSTAGES>), dim3(gx, splits), dim3(T::NT), T::LDS_BYTES, stream,
+                     p, mblocks, nblocks, kps, part, persist ? 1 : 0);
   LLHIP_LAUNCH_CHECK();
   if (part) {
     const int64_t quads = (int64_t)p.M * p.N / 4;
