@@ -30,8 +30,10 @@ The JSON line also carries
                  decode launch time, config-2 GEMM TOPS and GB/s (weights rotated through copies
                  larger than the memory-side cache), the qgraph producer's weight conversion
                  (llhip_quant_rows_i8, lm_head-shaped f32) against HBM and its numpy baseline,
-                 and the instruction-set device running a compiled-style Qwen2.5-0.5B-shaped
-                 decode step beside the reference's functional simulator on one host core.
+                 the instruction-set device running a compiled-style Qwen2.5-0.5B-shaped
+                 decode step beside the reference's functional simulator on one host core, and
+                 the float side's calibration and SmoothQuant of a Qwen2.5-0.5B-shaped fp32 model
+                 beside its float64 restatement.
 
     python bench.py [--gpus 1] [--steps 64] [--warmup 8]
     python bench.py --profile decode   # prefill + decode launches only (for rocprofv3)
@@ -345,6 +347,58 @@ def quantizer_bench(cpu_rows: int = 2048) -> dict:
     return out
 
 
+def floatside_bench(cpu_tokens: int = 16) -> dict:
+    """The float side on the GPU (llaccel_amd.floatside) over a Qwen2.5-0.5B-shaped fp32 model
+    (seeded N(0, 0.02) weights, unit norms, small QKV biases; 494M parameters): calibrate_tokens over
+    4 seeded sequences of 256 tokens and smooth_model (alpha 0.5) over the same sequences, wall clock
+    around each call (the records are downloaded once, at the end of a call).  CPU baseline: the
+    float64 numpy restatement (oracle/float_np.py) calibrating the first `cpu_tokens` tokens of the
+    first sequence, whose records the GPU's equal to rtol 1e-4."""
+    import torch
+
+    from llaccel_amd.floatside import FloatConfig, FloatModel, _expected_shapes, calibrate_tokens, smooth_model
+    from oracle import float_np as FO
+
+    cfg = FloatConfig(dim=896, n_layers=24, n_heads=14, n_kv_heads=2, head_dim=64, ffn=4864, vocab=151936,
+                      max_seq=1024, qkv_bias=True, rope_base=1e6, rms_eps=1e-6)
+    g = torch.Generator(device="cuda").manual_seed(23)
+    params = {}
+    for name, shape in _expected_shapes(cfg).items():
+        role = name.split("_", 1)[-1]
+        if "norm" in role:
+            params[name] = torch.ones(shape, dtype=torch.float32, device="cuda")
+        elif role in ("bq", "bk", "bv"):
+            params[name] = (torch.rand(shape, generator=g, device="cuda") - 0.5) * 0.06
+        else:
+            params[name] = torch.randn(shape, generator=g, device="cuda") * 0.02
+    model = FloatModel(cfg, params)
+    rng = np.random.default_rng(5)
+    seqs = [rng.integers(0, cfg.vocab, 256).tolist() for _ in range(4)]
+    sample = [seqs[0][:cpu_tokens]]
+    gpu_sample = calibrate_tokens(model, sample)  # also the warm-up (library heuristics, first launches)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    calibrate_tokens(model, seqs)
+    t_cal = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    meta = smooth_model(model, seqs, 0.5)
+    t_sm = time.perf_counter() - t0
+    del model
+    p64 = {k: v.double().cpu().numpy() for k, v in params.items()}
+    del params
+    t0 = time.perf_counter()
+    want = FO.calibrate_tokens(cfg, p64, sample)
+    t_cpu = time.perf_counter() - t0
+    worst = max(abs(gpu_sample[k] - v) / max(abs(v), 1e-30) for k, v in want.items())
+    ntok = sum(map(len, seqs))
+    return {"model": "Qwen2.5-0.5B shape, fp32, seeded weights", "calibration_tokens": ntok,
+            "calibrate_ms": round(t_cal * 1e3, 2), "calibrate_tok_s": round(ntok / t_cal, 1),
+            "smooth_ms": round(t_sm * 1e3, 2), "smooth_groups": len(meta["groups"]),
+            "cpu_baseline": {"tok_s": round(cpu_tokens / t_cpu, 2), "cores": "BLAS threads", "kind": "port",
+                             "sample": f"calibration of the first {cpu_tokens} tokens, float64 numpy restatement; "
+                                       f"GPU records equal to rtol 1e-4: {worst < 1e-4} (worst {worst:.1e})"}}
+
+
 def isa_device_bench() -> dict:
     """The instruction-set device (llaccel_amd.device.GpuDevice) on a compiled-style M = 1 decode
     step of the Qwen2.5-0.5B shape (llaccel_amd.isa_synth.decoder_program: 24 layers, weights
@@ -421,6 +475,7 @@ def main() -> None:
     ap.add_argument("--no-config5", action="store_true", help="skip the Qwen3 T=4096 decode timing")
     ap.add_argument("--no-quant", action="store_true", help="skip the weight-quantization kernel timing")
     ap.add_argument("--no-isa", action="store_true", help="skip the instruction-set device timing")
+    ap.add_argument("--no-float", action="store_true", help="skip the float-side calibration timing")
     ap.add_argument("--batch", type=int, default=16, help="also time config 4's batch decode (1 = skip)")
     ap.add_argument("--profile", choices=("decode", "copy", "prefill", "gemm", "quant", "config5", "batch"),
                     help="workload-only runs for rocprofv3")
@@ -613,9 +668,13 @@ def main() -> None:
         extra["gemm_sweep"] = gemm_sweep()
     if not args.no_quant:
         extra["quantize_rows_i8"] = quantizer_bench()
+        log("quantize", extra["quantize_rows_i8"])
     if not args.no_isa:
         extra["isa_device"] = isa_device_bench()
-        log("quantize", extra["quantize_rows_i8"])
+        log("isa device", extra["isa_device"])
+    if not args.no_float:
+        extra["float_side"] = floatside_bench()
+        log("float side", extra["float_side"])
 
     line = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True,

@@ -1129,10 +1129,12 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
   const int kps = (int)ceil_div(ktiles, splits);
   splits = (int)ceil_div(ktiles, kps);
   int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
-  // more tiles than one round of workgroups: persistent workgroups, one per CU (the 4-stage ring of
-  // the large tiles fills a CU's LDS), each stepping through its XCD's tiles
+  // many rounds of workgroups (8 or more): persistent workgroups, as many as fit at once (one per
+  // CU for the 256x256 tiles, whose ring fills the LDS), each stepping through its XCD's tiles.
+  // Measured: 2048 x 896 x 151936 (18.6 rounds) 457 -> 447 us; 512 x 896 x 151936 (4.6 rounds)
+  // 136 -> 147 us, so fewer rounds keep one workgroup per tile.
   const int per_cu = std::max(1, (160 * 1024) / T::LDS_BYTES);
-  const bool persist = !part && tiles > (int64_t)cus * per_cu;
+  const bool persist = !part && tiles >= 8ll * cus * per_cu;
   const unsigned gx = persist ? (unsigned)(cus / 8 * 8 * per_cu) : (unsigned)(ceil_div(mblocks * nblocks, 8) * 8);
   hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW, GSTAGES>), dim3(gx, splits), dim3(T::NT), T::LDS_BYTES, stream,
                      p, mblocks, nblocks, kps, part, persist ? 1 : 0);
