@@ -352,7 +352,6 @@ class _Records:
         self.device = device
         self.names: list[str] = []
         self.slot: dict[str, int] = {}
-        self.amax = self.torch.zeros(0)
         self.cols: dict[str, object] = {}
         self.rms: dict[str, object] = {}
         self._amax_parts = []

@@ -219,7 +219,7 @@ class _Device:
     def rows_i8(self, w: np.ndarray, n_rows: int | None = None) -> tuple[np.ndarray, np.ndarray]:
         """int8 rows and scales of w [N][K]; rows w.shape[0] .. n_rows - 1 are zero padding."""
         t = self.torch
-        w = np.ascontiguousarray(w, dtype=np.float32)
+        w = np.require(w, dtype=np.float32, requirements=["C", "W"])  # a read-only view is copied
         N, K = (w.shape[0] if n_rows is None else int(n_rows)), w.shape[1]
         src = t.zeros((N, K), dtype=t.float32, device="cuda")
         src[: w.shape[0]].copy_(t.from_numpy(w))
