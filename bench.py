@@ -347,6 +347,16 @@ def quantizer_bench(cpu_rows: int = 2048) -> dict:
     return out
 
 
+def blas_threads() -> int:
+    """Threads of the host BLAS numpy uses (threadpoolctl), else the host's CPU count."""
+    try:
+        from threadpoolctl import threadpool_info
+
+        return int(max(i["num_threads"] for i in threadpool_info() if i.get("user_api") == "blas"))
+    except (ImportError, ValueError, KeyError):
+        return os.cpu_count() or 1
+
+
 def floatside_bench(cpu_tokens: int = 16) -> dict:
     """The float side on the GPU (llaccel_amd.floatside) over a Qwen2.5-0.5B-shaped fp32 model
     (seeded N(0, 0.02) weights, unit norms, small QKV biases; 494M parameters): calibrate_tokens over
@@ -394,7 +404,7 @@ def floatside_bench(cpu_tokens: int = 16) -> dict:
     return {"model": "Qwen2.5-0.5B shape, fp32, seeded weights", "calibration_tokens": ntok,
             "calibrate_ms": round(t_cal * 1e3, 2), "calibrate_tok_s": round(ntok / t_cal, 1),
             "smooth_ms": round(t_sm * 1e3, 2), "smooth_groups": len(meta["groups"]),
-            "cpu_baseline": {"tok_s": round(cpu_tokens / t_cpu, 2), "cores": "BLAS threads", "kind": "port",
+            "cpu_baseline": {"tok_s": round(cpu_tokens / t_cpu, 2), "cores": blas_threads(), "kind": "port",
                              "sample": f"calibration of the first {cpu_tokens} tokens, float64 numpy restatement; "
                                        f"GPU records equal to rtol 1e-4: {worst < 1e-4} (worst {worst:.1e})"}}
 
