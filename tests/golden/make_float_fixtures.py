@@ -9,7 +9,8 @@ them (taken with forward hooks at the modules whose outputs the exported graph n
 apply_rotary for the RoPE outputs; case.json), the clipping bounds calibration_bounds.py selects from
 those activations with a 64-value budget, the logits of every sequence (`logits.<i>`), and for
 each smoothing option set the smoothed state dict (`sm<k>.<name>`) and the metadata record
-smooth_model returns (case.json).  The reference is read from /root/reference, which exists only in
+smooth_model returns (case.json); and rope.npz / rope.json, the cos/sin tables of every RoPE scaling
+kind.  The reference is read from /root/reference, which exists only in
 the build container; the fixtures travel with the repository.
 """
 from __future__ import annotations
@@ -152,6 +153,36 @@ def bounds(acts, amax, n_seqs, budget):
     return out
 
 
+# RoPE scalings of rope.py:64-99, each with a head_dim and context where they differ from the default
+ROPE = {
+    "default": dict(head_dim=32, max_seq=64, rope_base=10000.0, rope_scaling=None),
+    "linear": dict(head_dim=64, max_seq=96, rope_base=1e6, rope_scaling={"rope_type": "linear", "rope_theta": 1e6,
+                                                                          "factor": 4.0}),
+    "llama3": dict(head_dim=64, max_seq=96, rope_base=5e5,
+                   rope_scaling={"rope_type": "llama3", "rope_theta": 5e5, "factor": 8.0, "low_freq_factor": 1.0,
+                                 "high_freq_factor": 4.0, "original_max_position_embeddings": 16}),
+    "yarn": dict(head_dim=64, max_seq=96, rope_base=1e4,
+                 rope_scaling={"rope_type": "yarn", "rope_theta": 1e4, "factor": 4.0, "original_max_position_embeddings": 32,
+                               "attention_factor": 1.1386, "beta_fast": 32.0, "beta_slow": 1.0, "truncate": True}),
+}
+
+
+def rope_fixture(out) -> None:
+    """cos/sin tables the reference's build_rope_tables (rope.py:64-99) writes for every scaling kind"""
+    from llaccel.model import ModelConfig
+    from llaccel.rope import build_rope_tables
+
+    arrays, cfgs = {}, {}
+    for name, kw in ROPE.items():
+        cfg = ModelConfig(dim=kw["head_dim"] * 2, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=kw["head_dim"], ffn=64,
+                          vocab=16, max_seq=kw["max_seq"], rope_base=kw["rope_base"], rope_scaling=kw["rope_scaling"])
+        cos, sin = build_rope_tables(cfg)
+        arrays[f"{name}.cos"], arrays[f"{name}.sin"] = cos.numpy(), sin.numpy()
+        cfgs[name] = cfg.to_dict()
+    np.savez_compressed(out / "rope.npz", **arrays)
+    (out / "rope.json").write_text(json.dumps(cfgs))
+
+
 def main() -> None:
     sys.path.insert(0, str(REF / "python"))
     import torch
@@ -160,6 +191,7 @@ def main() -> None:
 
     out = HERE / "float"
     out.mkdir(exist_ok=True)
+    rope_fixture(out)
     for name, case in CASES.items():
         model = build(torch, TinyLlama, ModelConfig, case)
         cfg = model.cfg

@@ -150,6 +150,66 @@ def test_rope_tables_are_the_reference_float32_tables():
         assert np.abs(c - oc)[:8].max() < 3e-7  # early positions: the fp32 rounding of cos only
 
 
+def _rope_fixture():
+    meta = json.loads((GOLD / "rope.json").read_text())
+    z = np.load(GOLD / "rope.npz")
+    return {k: (FloatConfig.from_dict(c), z[f"{k}.cos"], z[f"{k}.sin"]) for k, c in meta.items()}
+
+
+def _ratios(cfg, cos, sin):
+    """default inv_freq / the table's inv_freq per frequency, read off position 1's angle"""
+    d = cfg.head_dim
+    theta = (cfg.rope_scaling or {}).get("rope_theta", cfg.rope_base)
+    ang = np.arctan2(sin[1, :d // 2].astype(np.float64), cos[1, :d // 2].astype(np.float64))
+    return theta ** (-np.arange(0, d, 2) / d) / ang
+
+
+def test_reference_rope_fixture_follows_each_scaling_rule():
+    """The reference's tables (tests/golden/float/rope.npz, from rope.py:64-99) against what each scaling
+    fixes: cos^2 + sin^2 = amplitude^2 (attention_factor for yarn, 1 otherwise); default keeps the
+    frequencies, linear divides all by `factor`; llama3 divides those with wavelength above
+    original_max/low_freq_factor by `factor` and blends the band below it monotonically; yarn keeps the
+    dimensions below the floor of the beta_fast correction, divides those from the ceiling of the
+    beta_slow correction on by `factor`, and ramps 1/ratio linearly in between (here dims 0..6)."""
+    tabs = _rope_fixture()
+    for kind, (cfg, cos, sin) in tabs.items():
+        amp = (cfg.rope_scaling or {}).get("attention_factor", 1.0)
+        np.testing.assert_allclose(np.hypot(cos, sin), amp, rtol=3e-7, err_msg=kind)
+        np.testing.assert_array_equal(cos[0], np.float32(amp))
+        np.testing.assert_array_equal(cos[:, :cfg.head_dim // 2], cos[:, cfg.head_dim // 2:])
+    np.testing.assert_allclose(_ratios(*tabs["default"]), 1.0, rtol=1e-5)
+    np.testing.assert_allclose(_ratios(*tabs["linear"]), 4.0, rtol=1e-5)
+    cfg, cos, sin = tabs["llama3"]
+    r = _ratios(cfg, cos, sin)
+    p = cfg.rope_scaling
+    wave = 2 * np.pi * (p["rope_theta"] ** (np.arange(0, cfg.head_dim, 2) / cfg.head_dim))
+    far = wave > p["original_max_position_embeddings"] / p["low_freq_factor"]
+    assert far.sum() == 29 and (~far).sum() == 3  # the fixture covers both regions
+    np.testing.assert_allclose(r[far], p["factor"], rtol=1e-5)
+    assert np.all(np.diff(r[~far]) > 0) and np.all((r[~far] > 1) & (r[~far] < p["factor"]))
+    cfg, cos, sin = tabs["yarn"]
+    r = _ratios(cfg, cos, sin)
+    np.testing.assert_allclose(r[0], 1.0, rtol=1e-5)
+    np.testing.assert_allclose(r[6:], 4.0, rtol=1e-5)
+    ramp = (1 - 1 / r[:7]) / (1 - 1 / 4.0)
+    np.testing.assert_allclose(ramp, np.arange(7) / 6, atol=1e-5)
+
+
+def test_rope_tables_equal_the_reference_tables_for_every_scaling():
+    """llaccel_amd.floatside.rope_tables against the reference's own default, linear, llama3 and yarn tables
+    (the same float32 operations in the same order: equal up to the platform's float32 cos/sin)"""
+    from llaccel_amd.floatside import rope_tables
+
+    for kind, (cfg, cos, sin) in _rope_fixture().items():
+        c, s = (t.numpy() for t in rope_tables(cfg))
+        np.testing.assert_allclose(c, cos, rtol=0, atol=2.4e-7, err_msg=kind)
+        np.testing.assert_allclose(s, sin, rtol=0, atol=2.4e-7, err_msg=kind)
+        if kind in ("default", "linear"):
+            oc, os_ = FO.rope_tables(cfg)
+            np.testing.assert_allclose(oc, cos, rtol=0, atol=1e-5, err_msg=kind)
+            np.testing.assert_allclose(os_, sin, rtol=0, atol=1e-5, err_msg=kind)
+
+
 def test_float_model_needs_the_library_and_a_gpu():
     """The product path refuses to run without the HIP library and a GPU (no CPU fallback)."""
     import torch
