@@ -439,38 +439,77 @@ __device__ __forceinline__ int32_t requant_col(int32_t acc, const ColRq& c) {
 __device__ __forceinline__ int32_t clamp32(int32_t v, int32_t lo, int32_t hi) { return min(max(v, lo), hi); }
 
 // ---------------------------------------------------------------------------------------
-// Large GEMM (M >= 128, K % 64 == 0): GM x GN x 64 block tile (256 x 256 with 8 waves, 128 x 128
-// or 64 x 128 with 4), 4-stage LDS ring fed by direct global->LDS loads (global_load_lds_dwordx4)
+// Large GEMM (M >= 128, K % 64 == 0): GM x GN block tile (256 x 256 with 8 waves, 128 x 128 or
+// 64 x 128 with 4) over K tiles of KT bytes (128 where K allows it, else 64) in an NS-stage LDS ring
+// fed by direct global->LDS loads (global_load_lds_dwordx4)
 // ---------------------------------------------------------------------------------------
-// Each wave instruction moves 64 x 16 B into 1 KiB of LDS (16 rows of 64 B).  Lane L of it
-// writes slot L of that KiB (row L/4, slot L%4) and fetches K chunk (L%4) ^ swz(row), so a row's
-// four 16-byte chunks are stored XOR-permuted: fragment reads of 8 (or 16) consecutive rows at one
-// K chunk then fall into distinct LDS banks without padding.  Tiles k+1..k+3 are in flight while
-// tile k feeds the MFMAs, and the fragments of the next 32-byte K step are read while the MFMAs of
-// this one run (one barrier per tile, in the middle of the tile's MFMA stream).  Rows past M/N
-// read a clamped valid row (their outputs are discarded); K is a multiple of 64, so no K chunk is
-// partial.
-// Ring depth NS = GSTAGES.  Deeper rings (up to 12 stages in 144 KB, one workgroup per CU) measured
-// slower on the prompt-sized GEMMs: their K loop is not bound by the number of tiles in flight.
+// Each wave instruction moves 64 x 16 B into 1 KiB of LDS: RPL = 1024 / KT rows of KT bytes.  Lane L
+// writes slot L of that KiB (row L / (KT/16), slot L % (KT/16)) and fetches K chunk slot ^ swz(row),
+// so a row's 16-byte chunks are stored XOR-permuted and the fragment reads of 16 consecutive rows at
+// one K chunk fall into distinct LDS banks without padding.  With 128-byte K tiles every row's part
+// of a load is a whole 128-byte line (8 rows per instruction): 16 rows x 64 B per instruction moved
+// 16 TB/s from L2 to LDS, 8 rows x 128 B 21-30 TB/s (the contiguous-KiB rate), and the 2048 x 896 x
+// 151936 GEMM went 441 -> 406 us.  The ring holds NS = 4 tiles of 64 bytes or 2 of 128.  The K loop
+// reads the fragments of the next 32-byte K step while the MFMAs of this one run; once all of tile
+// kt's fragments are in registers one barrier frees its stage for tile kt + NS and publishes tile
+// kt + 1 (landed when at most the loads of tiles kt+2 .. kt+NS-1 are outstanding).  Rows past M/N
+// read a clamped valid row (their outputs are discarded); K is a multiple of KT, so no chunk is
+// partial.  Deeper rings (up to 12 stages in 144 KB, one workgroup per CU) measured slower on the
+// prompt-sized GEMMs: their K loop is not bound by the number of tiles in flight.
 constexpr int GSTAGES = 4;
 
+// 16-byte K chunk c of row r sits in slot c ^ swz(r) (64-byte rows: lds_swz; 128-byte: stage_swz<128>).
+// Both are periodic in r with period 32, so fragment blocks 32 rows apart share their slot pattern.
 __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+template <int KT>
+__device__ __forceinline__ int stage_swz(int r) {
+  if constexpr (KT == 64)
+    return lds_swz(r);
+  else
+    return ((r >> 1) ^ (r << 2)) & 7;
+}
+template <int KT>
+constexpr int ring_stages() {
+  return KT == 64 ? GSTAGES : 2;
+}
 
-template <int GM, int GN, int NW, int NS = GSTAGES>
+template <int GM, int GN, int NW, int KT = 64>
 struct MfmaTile {
   static constexpr int NT = 64 * NW;
-  static constexpr int STAGE_BYTES = (GM + GN) * 64;  // A + W of one K tile
+  static constexpr int NS = ring_stages<KT>();
+  static constexpr int STAGE_BYTES = (GM + GN) * KT;  // A + W of one K tile
   static constexpr int LDS_BYTES = NS * STAGE_BYTES;
   static constexpr int WROWS = GM / 2;                // wave tile: 2 x NW/2 waves
   static constexpr int WCOLS = 2 * GN / NW;
   static constexpr int WM = WROWS / 32, WN = WCOLS / 32;  // 32x32 MFMA tiles per wave
-  static constexpr int LA = GM / (16 * NW);           // 1 KiB A loads per wave per stage
-  static constexpr int LW = GN / (16 * NW);           // 1 KiB W loads per wave per stage
+  static constexpr int RPL = 1024 / KT;                   // rows per 1 KiB load instruction
+  static constexpr int CPR = KT / 16;                     // 16-byte chunks per row
+  static constexpr int KSTEPS = KT / 32;                  // 32-byte MFMA K steps per K tile
+  static constexpr int LA = GM / (RPL * NW);              // 1 KiB A loads per wave per stage
+  static constexpr int LW = GN / (RPL * NW);              // 1 KiB W loads per wave per stage
   static constexpr int LOADS = LA + LW;
-  static_assert(WM >= 1 && WN >= 1 && LA >= 1 && LW >= 1 && LA * 16 * NW == GM && LW * 16 * NW == GN, "tile shape");
-  static_assert(NS >= 3 && LOADS * (NS - 2) <= 63, "vmcnt counts at most 63 loads");
+  // accumulators read from their AGPRs at the point of use (off: the compiler keeps the
+  // accumulators of every tile shape here in VGPRs, two waves per SIMD fit 256 of them)
+  static constexpr bool AREG = false;
+  static_assert(KT == 64 || KT == 128, "K tile bytes");
+  static_assert(WM >= 1 && WN >= 1 && LA >= 1 && LW >= 1 && LA * RPL * NW == GM && LW * RPL * NW == GN, "tile shape");
+  static_assert(NS >= 2 && LOADS * (NS - 1) <= 63, "vmcnt counts at most 63 loads");
   static_assert(LA <= 4 && LW <= 4, "load source arrays");
 };
+
+// An accumulator element read from its AGPR where it is used.  Without it the compiler copies all
+// accumulators of a large tile into VGPRs after the K loop (and spills); with AREG false the value
+// is used as it is.
+template <bool AREG>
+__device__ __forceinline__ int32_t acc_at(int32_t a) {
+  if constexpr (AREG) {
+    int32_t v;
+    __asm__ volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+    return v;
+  } else {
+    return a;
+  }
+}
 
 // s_waitcnt vmcnt(N) (bits 3:0 and 15:14 of the immediate), expcnt and lgkmcnt not waited for
 template <int N>
@@ -514,7 +553,7 @@ __device__ __forceinline__ void mfma_ds_interleave() {
 // each lane quad (the 32x32 C layout gives lane l rows (r/4)*8 + (l/32)*4 + r%4 of column l%32;
 // afterwards lane 4q+t of a half-wave holds row (r/4)*8 + (l/32)*4 + t, columns 4q..4q+3) and one
 // dword store per four outputs.
-template <bool FAST, int WM, int WN>
+template <bool FAST, bool AREG, int WM, int WN>
 __device__ __forceinline__ void store_i8_tile(const LinearArgs& p, const v16i (&acc)[WM][WN], const ColRq (&cq)[WN],
                                               int mrow0, int ncol0, bool full) {
   const int lane = threadIdx.x & 63;
@@ -531,7 +570,7 @@ __device__ __forceinline__ void store_i8_tile(const LinearArgs& p, const v16i (&
       for (int g = 0; g < 4; ++g) {
         int32_t v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = clamp32(requant_col<FAST>(acc[i][j][4 * g + q], cq[j]), -128, 127);
+        for (int q = 0; q < 4; ++q) v[q] = clamp32(requant_col<FAST>(acc_at<AREG>(acc[i][j][4 * g + q]), cq[j]), -128, 127);
         const uint32_t d = __builtin_amdgcn_perm((uint32_t)v[1], (uint32_t)v[0], 0x0c0c0400u) |
                            __builtin_amdgcn_perm((uint32_t)v[3], (uint32_t)v[2], 0x04000c0cu);
         const uint32_t d1 = __builtin_amdgcn_perm((uint32_t)dpp_mov<DPP_QUAD_XOR1>((int)d), d, sel1);
@@ -545,6 +584,9 @@ __device__ __forceinline__ void store_i8_tile(const LinearArgs& p, const v16i (&
           for (int b = 0; b < 4; ++b)
             if (nq + b < p.N) dst[b] = (int8_t)(e >> (8 * b));
         }
+        // the exact 64-bit form one output group at a time (its temporaries would otherwise be
+        // interleaved across groups and raise the kernel's register peak)
+        if constexpr (!FAST) __builtin_amdgcn_sched_barrier(0);
       }
   }
 }
@@ -553,7 +595,7 @@ __device__ __forceinline__ void store_i8_tile(const LinearArgs& p, const v16i (&
 // transpose of 16-bit values across each lane quad (an exchange of dwords with lane ^ 2, then of
 // halves with lane ^ 1), after which lane 4q+t of a half-wave holds row (r/4)*8 + (l/32)*4 + t,
 // columns 4q..4q+3: the aux operand is read and the result written 8 bytes at a time.
-template <int EPI, bool FAST, int WM, int WN>
+template <int EPI, bool FAST, bool AREG, int WM, int WN>
 __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (&acc)[WM][WN], const ColRq (&cq)[WN],
                                                int mrow0, int ncol0, bool full, const uint16_t* sig) {
   const int lane = threadIdx.x & 63;
@@ -587,7 +629,8 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
       for (int g = 0; g < 4; ++g) {
         int32_t v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = clamp32(requant_col<FAST>(acc[i][j][4 * g + q], cq[j]), -32768, 32767);
+        for (int q = 0; q < 4; ++q)
+          v[q] = clamp32(requant_col<FAST>(acc_at<AREG>(acc[i][j][4 * g + q]), cq[j]), -32768, 32767);
         // E[lane][row]: d0 = rows 0,1, d1 = rows 2,3 of this lane's column
         const uint32_t d0 = __builtin_amdgcn_perm((uint32_t)v[1], (uint32_t)v[0], 0x05040100u);
         const uint32_t d1 = __builtin_amdgcn_perm((uint32_t)v[3], (uint32_t)v[2], 0x05040100u);
@@ -639,11 +682,12 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
 // tiles [z*kps, z*kps + kps) and stores its int32 partial tile into plane z of part
 // [splits][M][N]; linear_splitk_finish sums the planes (integer addition: any split gives the same
 // sum) and applies the epilogue.
-template <int EPI, bool OUT8, int GM, int GN, int NW, int NS>
+template <int EPI, bool OUT8, int GM, int GN, int NW, int KT>
 __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int l0, int lstep, int lend, int kps,
                                            int32_t* part) {
-  using T = MfmaTile<GM, GN, NW, NS>;
-  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [NS][A GMx64 | W GNx64]
+  using T = MfmaTile<GM, GN, NW, KT>;
+  constexpr int NS = T::NS;
+  extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [NS][A GM x KT | W GN x KT]
   if (l0 >= lend) return;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -652,25 +696,26 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
   // this lane's source rows for the LA A and LW W load instructions of a stage
   const int8_t* asrc[4];  // fixed sizes (see wait_vmcnt)
   const int8_t* wsrc[4];
-  const int kbase = (int)blockIdx.y * kps * 64;  // first K byte of this split
+  const int kbase = (int)blockIdx.y * kps * KT;  // first K byte of this split
   auto sources = [&](int l) {
     const int m0 = (l % mblocks) * GM, n0 = (l / mblocks) * GN;
+    const int rl = lane / T::CPR, slot = lane % T::CPR;
 #pragma unroll
     for (int i = 0; i < T::LA; ++i) {
-      const int r = (wave * T::LA + i) * 16 + (lane >> 2);
+      const int r = (wave * T::LA + i) * T::RPL + rl;
       const int gm = min(m0 + r, p.M - 1);
-      asrc[i] = p.A + (int64_t)gm * p.lda + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
+      asrc[i] = p.A + (int64_t)gm * p.lda + kbase + ((slot ^ stage_swz<KT>(r)) * 16);
     }
 #pragma unroll
     for (int i = 0; i < T::LW; ++i) {
-      const int r = (wave * T::LW + i) * 16 + (lane >> 2);
+      const int r = (wave * T::LW + i) * T::RPL + rl;
       const int gn = min(n0 + r, p.N - 1);
-      wsrc[i] = p.W + (int64_t)gn * p.K + kbase + (((lane & 3) ^ lds_swz(r)) * 16);
+      wsrc[i] = p.W + (int64_t)gn * p.K + kbase + ((slot ^ stage_swz<KT>(r)) * 16);
     }
   };
   auto issue = [&](int kt) {
     int8_t* st = ring + (kt % NS) * T::STAGE_BYTES;
-    const int k0 = kt * 64;
+    const int k0 = kt * KT;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // explicitly typed operands (see wait_vmcnt)
@@ -681,34 +726,28 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
       }
       if (i < T::LW) {
         const int8_t* src = wsrc[i] + k0;
-        int8_t* dst = st + GM * 64 + (wave * T::LW + i) * 1024;
+        int8_t* dst = st + GM * KT + (wave * T::LW + i) * 1024;
         __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
       }
     }
   };
-  // LDS offsets of this lane's fragments for the two 32-byte K steps of a tile
-  int aoff[T::WM][2], woff[T::WN][2];
+  // LDS offsets of this lane's fragments of block 0 for each 32-byte K step of a tile (block i / j
+  // adds 32 * KT * i / j: the slot pattern repeats every 32 rows)
+  int aoff[T::KSTEPS], woff[T::KSTEPS];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int ks = 0; ks < T::KSTEPS; ++ks) {
     const int c = ks * 2 + (lane >> 5);  // 16-byte K chunk of this lane's fragment
-#pragma unroll
-    for (int i = 0; i < T::WM; ++i) {
-      const int r = wm + 32 * i + (lane & 31);
-      aoff[i][ks] = r * 64 + ((c ^ lds_swz(r)) << 4);
-    }
-#pragma unroll
-    for (int j = 0; j < T::WN; ++j) {
-      const int r = wn + 32 * j + (lane & 31);
-      woff[j][ks] = GM * 64 + r * 64 + ((c ^ lds_swz(r)) << 4);
-    }
+    const int ra = wm + (lane & 31), rw = wn + (lane & 31);
+    aoff[ks] = ra * KT + ((c ^ stage_swz<KT>(ra)) << 4);
+    woff[ks] = GM * KT + rw * KT + ((c ^ stage_swz<KT>(rw)) << 4);
   }
   // SiLU table for the silu epilogue, staged in LDS (visible after the main loop's barriers)
   __shared__ uint32_t sig32[EPI == EPI_SILU ? 129 : 1];
   if (EPI == EPI_SILU && tid < 129) sig32[tid] = reinterpret_cast<const uint32_t*>(kSig)[tid];
   const uint16_t* sig16 = reinterpret_cast<const uint16_t*>(sig32);
-  const int ktiles = min(kps, p.K / 64 - (int)blockIdx.y * kps);
+  const int ktiles = min(kps, p.K / KT - (int)blockIdx.y * kps);
   sources(l0);
-  for (int s0 = 0; s0 < NS - 1; ++s0)
+  for (int s0 = 0; s0 < NS; ++s0)
     if (s0 < ktiles) issue(s0);
   for (int l = l0;;) {
     const int m0 = (l % mblocks) * GM, n0 = (l / mblocks) * GN;
@@ -721,58 +760,53 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
     }
 
     v16i acc[T::WM][T::WN];
-#pragma unroll
-    for (int i = 0; i < T::WM; ++i)
-#pragma unroll
-      for (int j = 0; j < T::WN; ++j) acc[i][j] = v16i{};
-
     // K tile 0 landed: the loads of the tiles issued after it may be outstanding
-    wait_tiles<T::LOADS, NS - 2>(min(ktiles, NS - 1) - 1);
+    wait_tiles<T::LOADS, NS - 1>(min(ktiles, NS) - 1);
     lds_barrier();
-    v4i fa0[T::WM], fb0[T::WN], fa1[T::WM], fb1[T::WN];
+    v4i fa[2][T::WM], fb[2][T::WN];
+    auto frags = [&](const int8_t* st, int ks, int buf) {
 #pragma unroll
-    for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(ring + aoff[i][0]);
+      for (int i = 0; i < T::WM; ++i) fa[buf][i] = *reinterpret_cast<const v4i*>(st + aoff[ks] + 32 * KT * i);
 #pragma unroll
-    for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(ring + woff[j][0]);
-    for (int kt = 0; kt < ktiles; ++kt) {
+      for (int j = 0; j < T::WN; ++j) fb[buf][j] = *reinterpret_cast<const v4i*>(st + woff[ks] + 32 * KT * j);
+    };
+    // the MFMAs of one K step (the first of a tile's first K tile starts the accumulators at zero)
+    auto mfmas = [&](int buf, bool zero) {
+#pragma unroll
+      for (int i = 0; i < T::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[buf][i], fb[buf][j], zero ? v16i{} : acc[i][j], 0, 0, 0);
+      mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
+    };
+    frags(ring, 0, 0);
+    // K tile kt: step s runs on fragment buffer s & 1 while step s+1's are read; after its last
+    // reads (lgkmcnt(0)) and the barrier, stage kt % NS takes tile kt + NS and tile kt+1's first
+    // fragments are read during the last step (after the last tile they come from a stale stage
+    // and are never used)
+    auto ktile = [&](int kt, auto first) {
       const int8_t* st = ring + (kt % NS) * T::STAGE_BYTES;
-      // first K step of tile kt (fragments already in registers) while the second one's are read
 #pragma unroll
-      for (int i = 0; i < T::WM; ++i) fa1[i] = *reinterpret_cast<const v4i*>(st + aoff[i][1]);
-#pragma unroll
-      for (int j = 0; j < T::WN; ++j) fb1[j] = *reinterpret_cast<const v4i*>(st + woff[j][1]);
-#pragma unroll
-      for (int i = 0; i < T::WM; ++i)
-#pragma unroll
-        for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[i], fb0[j], acc[i][j], 0, 0, 0);
-      mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
-      // Tile kt+1 landed once at most the loads of the tiles issued after it (kt+2 .. kt+NS-2) are
-      // outstanding; after the barrier every wave's copies of it are visible and every wave has
-      // finished reading stage (kt-1) % NS, which issue(kt + NS - 1) overwrites.  A bare s_barrier:
-      // __syncthreads() would also drain the later tiles still in flight.
-      wait_tiles<T::LOADS, NS - 2>(min(ktiles, kt + NS - 1) - kt - 2);
+      for (int s = 0; s + 1 < T::KSTEPS; ++s) {
+        frags(st, s + 1, (s + 1) & 1);
+        mfmas(s & 1, decltype(first)::value && s == 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      wait_tiles<T::LOADS, NS - 1>(min(ktiles, kt + NS) - kt - 2);
       lds_barrier();
-      if (kt + NS - 1 < ktiles) issue(kt + NS - 1);
-      // second K step of tile kt while the next tile's first-step fragments are read (after the
-      // last tile they come from a stale stage and are never used)
-      const int8_t* sn = ring + ((kt + 1) % NS) * T::STAGE_BYTES;
-#pragma unroll
-      for (int i = 0; i < T::WM; ++i) fa0[i] = *reinterpret_cast<const v4i*>(sn + aoff[i][0]);
-#pragma unroll
-      for (int j = 0; j < T::WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(sn + woff[j][0]);
-#pragma unroll
-      for (int i = 0; i < T::WM; ++i)
-#pragma unroll
-        for (int j = 0; j < T::WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[i], fb1[j], acc[i][j], 0, 0, 0);
-      mfma_ds_interleave<T::WM * T::WN, T::WM + T::WN>();
-    }
+      if (kt + NS < ktiles) issue(kt + NS);
+      frags(ring + ((kt + 1) % NS) * T::STAGE_BYTES, 0, T::KSTEPS & 1);
+      mfmas((T::KSTEPS - 1) & 1, false);
+    };
+    ktile(0, std::true_type{});
+    for (int kt = 1; kt < ktiles; ++kt) ktile(kt, std::false_type{});
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the stale fragment reads have returned
     // the next tile's first stages, once every wave is done with the ring
     const int ln = l + lstep;
     if (ln < lend) {
       lds_barrier();
       sources(ln);
-      for (int s0 = 0; s0 < NS - 1; ++s0)
+      for (int s0 = 0; s0 < NS; ++s0)
         if (s0 < ktiles) issue(s0);
     }
 
@@ -788,7 +822,7 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int m = m0 + wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-            if (m < p.M && n < p.N) plane[(int64_t)m * p.N + n] = acc[i][j][r];
+            if (m < p.M && n < p.N) plane[(int64_t)m * p.N + n] = acc_at<T::AREG>(acc[i][j][r]);
           }
       }
       if (ln >= lend) return;
@@ -805,17 +839,17 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
     if constexpr (OUT8) {
       const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 4 == 0;
       if (fast)
-        store_i8_tile<true>(p, acc, cq, m0 + wm, n0 + wn, full);
+        store_i8_tile<true, T::AREG>(p, acc, cq, m0 + wm, n0 + wn, full);
       else
-        store_i8_tile<false>(p, acc, cq, m0 + wm, n0 + wn, full);
+        store_i8_tile<false, T::AREG>(p, acc, cq, m0 + wm, n0 + wn, full);
     } else {
       // i16 output (with the aux-reading epilogues) from registers as well
       const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 8 == 0 &&
                         ((EPI != EPI_RESADD && EPI != EPI_MUL) || (p.ldaux % 4 == 0 && (uintptr_t)p.aux % 8 == 0));
       if (fast)
-        store_i16_tile<EPI, true>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
+        store_i16_tile<EPI, true, T::AREG>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
       else
-        store_i16_tile<EPI, false>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
+        store_i16_tile<EPI, false, T::AREG>(p, acc, cq, m0 + wm, n0 + wn, full, sig16);
     }
     if (ln >= lend) return;
     l = ln;
@@ -828,18 +862,18 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
 // per CU; XCD x takes the contiguous tile range [x * per, (x + 1) * per), per = ceil(tiles / 8),
 // and its gridDim.x / 8 workgroups step through it together, so the ones running at any time still
 // share W panels in that XCD's L2.
-template <int EPI, bool OUT8, int GM, int GN, int NW, int NS>
+template <int EPI, bool OUT8, int GM, int GN, int NW, int KT>
 __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part,
                                                        int persist) {
   const int b = blockIdx.x;
   const int tiles = mblocks * nblocks;
   if (persist) {
     const int per = (tiles + 7) / 8, x = b % 8, lo = x * per;
-    mfma_tiles<EPI, OUT8, GM, GN, NW, NS>(p, mblocks, lo + b / 8, (int)gridDim.x / 8, min(lo + per, tiles), kps, part);
+    mfma_tiles<EPI, OUT8, GM, GN, NW, KT>(p, mblocks, lo + b / 8, (int)gridDim.x / 8, min(lo + per, tiles), kps, part);
     return;
   }
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
-  mfma_tiles<EPI, OUT8, GM, GN, NW, NS>(p, mblocks, logical, 1, min(logical + 1, tiles), kps, part);
+  mfma_tiles<EPI, OUT8, GM, GN, NW, KT>(p, mblocks, logical, 1, min(logical + 1, tiles), kps, part);
 }
 
 // Several linears of one input in one launch (the q, k, v projections of a prompt chunk): the
@@ -857,7 +891,7 @@ struct LinearGroup {
   int out8[GROUP_MAX];
 };
 
-template <int GM, int GN, int NW, int NS>
+template <int GM, int GN, int NW, int KT>
 __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, LinearGroup g, int mblocks) {
   const int b = blockIdx.x;
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
@@ -875,9 +909,9 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, Linea
   nbk -= g.nb0[q];
   const int l = nbk * mblocks + mb;
   if (g.out8[q])
-    mfma_tiles<EPI_NONE, true, GM, GN, NW, NS>(pp, mblocks, l, 1, l + 1, p.K / 64, nullptr);
+    mfma_tiles<EPI_NONE, true, GM, GN, NW, KT>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr);
   else
-    mfma_tiles<EPI_NONE, false, GM, GN, NW, NS>(pp, mblocks, l, 1, l + 1, p.K / 64, nullptr);
+    mfma_tiles<EPI_NONE, false, GM, GN, NW, KT>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1100,33 +1134,34 @@ __global__ __launch_bounds__(256) void linear_splitk_finish(LinearArgs p, const 
 // ---------------------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------------------
-// One MFMA GEMM launch with GM x GN tiles.  Too few output tiles for the CUs (narrow projections of
-// a prompt): split K into ranges of at least 4 K tiles whose int32 partial tiles fit the workspace,
-// then sum them.  The split count maximises (K-loop time saved) - (partial-plane traffic + the
-// finishing launch), with measured costs: ~0.5 us (128x128) or ~0.4 us (64x128) per K tile of a
-// workgroup, ~5 us for the finishing launch and ~4 TB/s for the planes.
-template <int EPI, bool OUT8, int GM, int GN, int NW>
+// One MFMA GEMM launch with GM x GN tiles of KT-byte K tiles.  Too few output tiles for the CUs
+// (narrow projections of a prompt): split K into ranges of at least 256 bytes whose int32 partial
+// tiles fit the workspace, then sum them.  The split count maximises (K-loop time saved) -
+// (partial-plane traffic + the finishing launch), with measured costs: ~0.5 us (128x128) or ~0.4 us
+// (64x128) per 64 bytes of K of a workgroup, ~5 us for the finishing launch and ~4 TB/s for the
+// planes.
+template <int EPI, bool OUT8, int GM, int GN, int NW, int KT>
 static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
-  using T = MfmaTile<GM, GN, NW>;
+  using T = MfmaTile<GM, GN, NW, KT>;
   const int mblocks = (int)ceil_div(p.M, GM), nblocks = (int)ceil_div(p.N, GN);
   const int64_t tiles = (int64_t)mblocks * nblocks;
-  const int ktiles = (int)(p.K / 64);
+  const int k64 = (int)(p.K / 64), ktiles = (int)(p.K / KT);
   const int cus = current_cu_count();
   int splits = 1;
   if (ws && p.N % 4 == 0 && tiles < cus) {
-    const int smax = (int)std::min<int64_t>(std::min<int64_t>(8, ceil_div(2 * cus, tiles)), ktiles / 4);
+    const int smax = (int)std::min<int64_t>(std::min<int64_t>(8, ceil_div(2 * cus, tiles)), k64 / 4);
     double best = 0.0;
     for (int sp = 2; sp <= smax; ++sp) {
       const double plane_bytes = (double)sp * p.M * p.N * 4;
       if (plane_bytes > (double)WS_SCRATCH_BYTES) break;
-      const double gain = (GM * GN >= 128 * 128 ? 0.5 : 0.4) * ktiles * (sp - 1) / sp - (5.0 + plane_bytes / 4e6);
+      const double gain = (GM * GN >= 128 * 128 ? 0.5 : 0.4) * k64 * (sp - 1) / sp - (5.0 + plane_bytes / 4e6);
       if (gain > best) {
         best = gain;
         splits = sp;
       }
     }
   }
-  const int kps = (int)ceil_div(ktiles, splits);
+  const int kps = (int)ceil_div(ktiles, splits);  // K tiles per split
   splits = (int)ceil_div(ktiles, kps);
   int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
   // many rounds of workgroups (8 or more): persistent workgroups, as many as fit at once (one per
@@ -1136,7 +1171,7 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
   const int per_cu = std::max(1, (160 * 1024) / T::LDS_BYTES);
   const bool persist = !part && tiles >= 8ll * cus * per_cu;
   const unsigned gx = persist ? (unsigned)(cus / 8 * 8 * per_cu) : (unsigned)(ceil_div(mblocks * nblocks, 8) * 8);
-  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW, GSTAGES>), dim3(gx, splits), dim3(T::NT), T::LDS_BYTES, stream,
+  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW, KT>), dim3(gx, splits), dim3(T::NT), T::LDS_BYTES, stream,
                      p, mblocks, nblocks, kps, part, persist ? 1 : 0);
   LLHIP_LAUNCH_CHECK();
   if (part) {
@@ -1148,21 +1183,28 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
   return 0;
 }
 
+// The MFMA tile shape for a prompt-sized linear, over K tiles of KT bytes
+template <int EPI, bool OUT8, int KT>
+static int launch_mfma_shape(LinearArgs& p, void* ws, hipStream_t stream) {
+  // 256x256 tiles when M fills them and they fill every CU.  The 256x256 kernel keeps 128
+  // accumulators per lane at two waves per SIMD; the aux-reading epilogues would spill there.
+  if constexpr (EPI == EPI_NONE) {
+    if (p.M >= 256 && (int64_t)ceil_div(p.M, 256) * ceil_div(p.N, 256) >= current_cu_count())
+      return launch_mfma<EPI, OUT8, 256, 256, 8, KT>(p, ws, stream);
+  }
+  // 128x128 tiles while they fill the CUs, else 64x128 tiles (twice as many workgroups, three per
+  // CU), split along K when even those are too few
+  if ((int64_t)ceil_div(p.M, 128) * ceil_div(p.N, 128) >= current_cu_count())
+    return launch_mfma<EPI, OUT8, 128, 128, 4, KT>(p, ws, stream);
+  return launch_mfma<EPI, OUT8, 64, 128, 4, KT>(p, ws, stream);
+}
+
 template <int EPI, bool OUT8>
 static int launch_linear(LinearArgs& p, void* ws, hipStream_t stream) {
   const bool aligned = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.W % 16 == 0);
   if (p.M >= 128 && p.K % 64 == 0 && aligned) {
-    // 256x256 tiles when M fills them and they fill every CU.  The 256x256 kernel keeps 128
-    // accumulators per lane at two waves per SIMD; the aux-reading epilogues would spill there.
-    if constexpr (EPI == EPI_NONE) {
-      if (p.M >= 256 && (int64_t)ceil_div(p.M, 256) * ceil_div(p.N, 256) >= current_cu_count())
-        return launch_mfma<EPI, OUT8, 256, 256, 8>(p, ws, stream);
-    }
-    // 128x128 tiles while they fill the CUs, else 64x128 tiles (twice as many workgroups, three per
-    // CU), split along K when even those are too few
-    if ((int64_t)ceil_div(p.M, 128) * ceil_div(p.N, 128) >= current_cu_count())
-      return launch_mfma<EPI, OUT8, 128, 128, 4>(p, ws, stream);
-    return launch_mfma<EPI, OUT8, 64, 128, 4>(p, ws, stream);
+    if (p.K % 128 == 0) return launch_mfma_shape<EPI, OUT8, 128>(p, ws, stream);
+    return launch_mfma_shape<EPI, OUT8, 64>(p, ws, stream);
   }
   if (p.M > 16 && aligned) {
     // 128x256 block tiles when they still fill the chip, else 128x128
@@ -1236,7 +1278,6 @@ static int launch_linear_group(const LinearArgs& base, const llhip_linear_proble
     }
     return 0;
   }
-  using T = MfmaTile<64, 128, 4>;
   LinearGroup g{};
   g.count = count;
   g.nb0[0] = 0;
@@ -1251,8 +1292,14 @@ static int launch_linear_group(const LinearArgs& base, const llhip_linear_proble
     g.nb0[q + 1] = g.nb0[q] + (int)ceil_div(pr[q].N, 128);
   }
   const int mblocks = (int)ceil_div(base.M, 64);
-  hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, GSTAGES>), dim3(ceil_div((int64_t)mblocks * g.nb0[count], 8) * 8),
-                     dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
+  const dim3 grid((unsigned)(ceil_div((int64_t)mblocks * g.nb0[count], 8) * 8));
+  if (base.K % 128 == 0) {
+    using T = MfmaTile<64, 128, 4, 128>;
+    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 128>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
+  } else {
+    using T = MfmaTile<64, 128, 4, 64>;
+    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 64>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
+  }
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
