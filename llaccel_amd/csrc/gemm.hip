@@ -468,15 +468,22 @@ __device__ __forceinline__ int stage_swz(int r) {
   else
     return ((r >> 1) ^ (r << 2)) & 7;
 }
+// ring depth: 4 tiles of 64 bytes; 2 tiles of 128 bytes (two workgroups per CU for the smaller
+// tile shapes), or 3 for a launch of fewer workgroups than CUs, where each one is alone on its CU
+// and the deeper ring keeps more of its loads in flight (512 x 896 x 896: 8.7 -> 7.5 us)
 template <int KT>
 constexpr int ring_stages() {
   return KT == 64 ? GSTAGES : 2;
 }
+template <int GM, int GN, int KT>
+constexpr bool deep_ring_fits() {
+  return KT == 128 && (GM + GN) * KT * 3 <= 160 * 1024;
+}
 
-template <int GM, int GN, int NW, int KT = 64>
+template <int GM, int GN, int NW, int KT = 64, int NSTAGES = ring_stages<KT>()>
 struct MfmaTile {
   static constexpr int NT = 64 * NW;
-  static constexpr int NS = ring_stages<KT>();
+  static constexpr int NS = NSTAGES;
   static constexpr int STAGE_BYTES = (GM + GN) * KT;  // A + W of one K tile
   static constexpr int LDS_BYTES = NS * STAGE_BYTES;
   static constexpr int WROWS = GM / 2;                // wave tile: 2 x NW/2 waves
@@ -682,10 +689,10 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
 // tiles [z*kps, z*kps + kps) and stores its int32 partial tile into plane z of part
 // [splits][M][N]; linear_splitk_finish sums the planes (integer addition: any split gives the same
 // sum) and applies the epilogue.
-template <int EPI, bool OUT8, int GM, int GN, int NW, int KT>
+template <int EPI, bool OUT8, int GM, int GN, int NW, int KT, int NS_>
 __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int l0, int lstep, int lend, int kps,
                                            int32_t* part) {
-  using T = MfmaTile<GM, GN, NW, KT>;
+  using T = MfmaTile<GM, GN, NW, KT, NS_>;
   constexpr int NS = T::NS;
   extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [NS][A GM x KT | W GN x KT]
   if (l0 >= lend) return;
@@ -862,18 +869,18 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
 // per CU; XCD x takes the contiguous tile range [x * per, (x + 1) * per), per = ceil(tiles / 8),
 // and its gridDim.x / 8 workgroups step through it together, so the ones running at any time still
 // share W panels in that XCD's L2.
-template <int EPI, bool OUT8, int GM, int GN, int NW, int KT>
+template <int EPI, bool OUT8, int GM, int GN, int NW, int KT, int NS>
 __global__ __launch_bounds__(64 * NW) void linear_mfma(LinearArgs p, int mblocks, int nblocks, int kps, int32_t* part,
                                                        int persist) {
   const int b = blockIdx.x;
   const int tiles = mblocks * nblocks;
   if (persist) {
     const int per = (tiles + 7) / 8, x = b % 8, lo = x * per;
-    mfma_tiles<EPI, OUT8, GM, GN, NW, KT>(p, mblocks, lo + b / 8, (int)gridDim.x / 8, min(lo + per, tiles), kps, part);
+    mfma_tiles<EPI, OUT8, GM, GN, NW, KT, NS>(p, mblocks, lo + b / 8, (int)gridDim.x / 8, min(lo + per, tiles), kps, part);
     return;
   }
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
-  mfma_tiles<EPI, OUT8, GM, GN, NW, KT>(p, mblocks, logical, 1, min(logical + 1, tiles), kps, part);
+  mfma_tiles<EPI, OUT8, GM, GN, NW, KT, NS>(p, mblocks, logical, 1, min(logical + 1, tiles), kps, part);
 }
 
 // Several linears of one input in one launch (the q, k, v projections of a prompt chunk): the
@@ -891,7 +898,7 @@ struct LinearGroup {
   int out8[GROUP_MAX];
 };
 
-template <int GM, int GN, int NW, int KT>
+template <int GM, int GN, int NW, int KT, int NS>
 __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, LinearGroup g, int mblocks) {
   const int b = blockIdx.x;
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
@@ -909,9 +916,9 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, Linea
   nbk -= g.nb0[q];
   const int l = nbk * mblocks + mb;
   if (g.out8[q])
-    mfma_tiles<EPI_NONE, true, GM, GN, NW, KT>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr);
+    mfma_tiles<EPI_NONE, true, GM, GN, NW, KT, NS>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr);
   else
-    mfma_tiles<EPI_NONE, false, GM, GN, NW, KT>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr);
+    mfma_tiles<EPI_NONE, false, GM, GN, NW, KT, NS>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1140,9 +1147,25 @@ __global__ __launch_bounds__(256) void linear_splitk_finish(LinearArgs p, const 
 // (partial-plane traffic + the finishing launch), with measured costs: ~0.5 us (128x128) or ~0.4 us
 // (64x128) per 64 bytes of K of a workgroup, ~5 us for the finishing launch and ~4 TB/s for the
 // planes.
+template <int EPI, bool OUT8, int GM, int GN, int NW, int KT, int NS>
+static void launch_mfma_kernel(LinearArgs& p, int mblocks, int nblocks, int splits, int kps, int32_t* part,
+                               hipStream_t stream) {
+  using T = MfmaTile<GM, GN, NW, KT, NS>;
+  const int cus = current_cu_count();
+  const int64_t tiles = (int64_t)mblocks * nblocks;
+  // many rounds of workgroups (8 or more): persistent workgroups, as many as fit at once (one per
+  // CU for the 256x256 tiles, whose ring fills the LDS), each stepping through its XCD's tiles.
+  // Measured: 2048 x 896 x 151936 (18.6 rounds) 457 -> 447 us; 512 x 896 x 151936 (4.6 rounds)
+  // 136 -> 147 us, so fewer rounds keep one workgroup per tile.
+  const int per_cu = std::max(1, (160 * 1024) / T::LDS_BYTES);
+  const bool persist = !part && tiles >= 8ll * cus * per_cu;
+  const unsigned gx = persist ? (unsigned)(cus / 8 * 8 * per_cu) : (unsigned)(ceil_div(mblocks * nblocks, 8) * 8);
+  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW, KT, NS>), dim3(gx, splits), dim3(T::NT), T::LDS_BYTES, stream,
+                     p, mblocks, nblocks, kps, part, persist ? 1 : 0);
+}
+
 template <int EPI, bool OUT8, int GM, int GN, int NW, int KT>
 static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
-  using T = MfmaTile<GM, GN, NW, KT>;
   const int mblocks = (int)ceil_div(p.M, GM), nblocks = (int)ceil_div(p.N, GN);
   const int64_t tiles = (int64_t)mblocks * nblocks;
   const int k64 = (int)(p.K / 64), ktiles = (int)(p.K / KT);
@@ -1164,15 +1187,14 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
   const int kps = (int)ceil_div(ktiles, splits);  // K tiles per split
   splits = (int)ceil_div(ktiles, kps);
   int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
-  // many rounds of workgroups (8 or more): persistent workgroups, as many as fit at once (one per
-  // CU for the 256x256 tiles, whose ring fills the LDS), each stepping through its XCD's tiles.
-  // Measured: 2048 x 896 x 151936 (18.6 rounds) 457 -> 447 us; 512 x 896 x 151936 (4.6 rounds)
-  // 136 -> 147 us, so fewer rounds keep one workgroup per tile.
-  const int per_cu = std::max(1, (160 * 1024) / T::LDS_BYTES);
-  const bool persist = !part && tiles >= 8ll * cus * per_cu;
-  const unsigned gx = persist ? (unsigned)(cus / 8 * 8 * per_cu) : (unsigned)(ceil_div(mblocks * nblocks, 8) * 8);
-  hipLaunchKernelGGL((linear_mfma<EPI, OUT8, GM, GN, NW, KT>), dim3(gx, splits), dim3(T::NT), T::LDS_BYTES, stream,
-                     p, mblocks, nblocks, kps, part, persist ? 1 : 0);
+  if constexpr (deep_ring_fits<GM, GN, KT>()) {
+    if (tiles * splits < cus)
+      launch_mfma_kernel<EPI, OUT8, GM, GN, NW, KT, 3>(p, mblocks, nblocks, splits, kps, part, stream);
+    else
+      launch_mfma_kernel<EPI, OUT8, GM, GN, NW, KT, ring_stages<KT>()>(p, mblocks, nblocks, splits, kps, part, stream);
+  } else {
+    launch_mfma_kernel<EPI, OUT8, GM, GN, NW, KT, ring_stages<KT>()>(p, mblocks, nblocks, splits, kps, part, stream);
+  }
   LLHIP_LAUNCH_CHECK();
   if (part) {
     const int64_t quads = (int64_t)p.M * p.N / 4;
@@ -1293,12 +1315,15 @@ static int launch_linear_group(const LinearArgs& base, const llhip_linear_proble
   }
   const int mblocks = (int)ceil_div(base.M, 64);
   const dim3 grid((unsigned)(ceil_div((int64_t)mblocks * g.nb0[count], 8) * 8));
-  if (base.K % 128 == 0) {
+  if (base.K % 128 == 0 && grid.x < (unsigned)current_cu_count()) {
+    using T = MfmaTile<64, 128, 4, 128, 3>;
+    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 128, 3>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
+  } else if (base.K % 128 == 0) {
     using T = MfmaTile<64, 128, 4, 128>;
-    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 128>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
+    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 128, T::NS>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
   } else {
     using T = MfmaTile<64, 128, 4, 64>;
-    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 64>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
+    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 64, T::NS>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
   }
   LLHIP_LAUNCH_CHECK();
   return 0;
