@@ -944,13 +944,16 @@ struct DualArgs {
 // outputs from the same LDS stages (each wave the MFMA work of a 4-wave single GEMM tile, two waves
 // per SIMD); the up waves pass their requantised values to the gate waves through LDS for the
 // epilogue.  Stage loads: gate waves 1 A + 2 Wg instructions, up waves 2 Wu instructions.
-template <int NS>
+template <int KT, int NS>
 __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d, int mblocks, int nblocks) {
-  constexpr int GM = 64, GN = 128, LW = 2;
-  constexpr int STAGE = (GM + 2 * GN) * 64;
+  constexpr int GM = 64, GN = 128;
+  constexpr int RPL = 1024 / KT, CPR = KT / 16, KSTEPS = KT / 32;
+  constexpr int LA = GM / (RPL * 4), LW = GN / (RPL * 4);  // 1 KiB loads per wave of one group
+  constexpr int STAGE = (GM + 2 * GN) * KT;
   constexpr int WN = 2;  // 32x32 tiles per wave along N (one along M)
+  static_assert(LA >= 1 && LW >= 1 && (LA + LW) * (NS - 1) <= 63 && LA <= 4 && LW <= 4, "dual tile loads");
   // [NS][A | Wg | Wu]; after the k loop it holds the requantised gate and up tiles and the SiLU table
-  // (NS = 4: 80 KB, so two workgroups share a CU)
+  // (80 KB: 4 stages of 64-byte or 2 of 128-byte K tiles, so two workgroups share a CU)
   extern __shared__ __attribute__((aligned(1024))) int8_t ring[];
   const int b = blockIdx.x;
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
@@ -958,30 +961,37 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
   const int mb = logical % mblocks, nbk = logical / mblocks;
   const int m0 = mb * GM, n0 = nbk * GN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool upw = wave >= 4;  // wave-uniform role
+  const bool upw = wave >= 4;  // wave-uniform role: waves 0-3 gate (and the A loads), 4-7 up
   const int wq = wave & 3;
   const int wm = (wq & 1) * 32, wn = (wq >> 1) * 64;
   const int8_t* Wsrc = upw ? d.Wu : p.W;
 
-  const int8_t* asrc;
+  const int8_t* asrc[LA];
   const int8_t* wsrc[LW];
   {
-    const int r = wq * 16 + (lane >> 2);
-    asrc = p.A + (int64_t)min(m0 + r, p.M - 1) * p.lda + (((lane & 3) ^ lds_swz(r)) * 16);
-  }
+    const int rl = lane / CPR, slot = lane % CPR;
 #pragma unroll
-  for (int i = 0; i < LW; ++i) {
-    const int r = (wq * LW + i) * 16 + (lane >> 2);
-    wsrc[i] = Wsrc + (int64_t)min(n0 + r, p.N - 1) * p.K + (((lane & 3) ^ lds_swz(r)) * 16);
+    for (int i = 0; i < LA; ++i) {
+      const int r = (wq * LA + i) * RPL + rl;
+      asrc[i] = p.A + (int64_t)min(m0 + r, p.M - 1) * p.lda + ((slot ^ stage_swz<KT>(r)) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < LW; ++i) {
+      const int r = (wq * LW + i) * RPL + rl;
+      wsrc[i] = Wsrc + (int64_t)min(n0 + r, p.N - 1) * p.K + ((slot ^ stage_swz<KT>(r)) * 16);
+    }
   }
-  const int wbase = (upw ? GM + GN : GM) * 64;  // this wave group's W panel in a stage
+  const int wbase = (upw ? GM + GN : GM) * KT;  // this wave group's W panel in a stage
   auto issue = [&](int kt) {
     int8_t* st = ring + (kt % NS) * STAGE;
-    const int k0 = kt * 64;
+    const int k0 = kt * KT;
     if (!upw) {
-      const int8_t* src = asrc + k0;
-      int8_t* dst = st + wq * 1024;
-      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+#pragma unroll
+      for (int i = 0; i < LA; ++i) {
+        const int8_t* src = asrc[i] + k0;
+        int8_t* dst = st + (wq * LA + i) * 1024;
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      }
     }
 #pragma unroll
     for (int i = 0; i < LW; ++i) {
@@ -990,24 +1000,21 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
       __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
     }
   };
-  // vmcnt waits by wave group: gate waves issue 3 loads per stage, up waves 2
+  // vmcnt waits by wave group: gate waves issue LA + LW loads per stage, up waves LW
   auto wait_n = [&](int n) {
     if (upw)
-      wait_tiles<2, NS - 2>(n);
+      wait_tiles<LW, NS - 1>(n);
     else
-      wait_tiles<3, NS - 2>(n);
+      wait_tiles<LA + LW, NS - 1>(n);
   };
-  int aoff[2], woff[WN][2];
+  // fragment offsets of block 0 per 32-byte K step (block j adds 32 * KT * j)
+  int aoff[KSTEPS], woff[KSTEPS];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int ks = 0; ks < KSTEPS; ++ks) {
     const int c = ks * 2 + (lane >> 5);
-    const int ra = wm + (lane & 31);
-    aoff[ks] = ra * 64 + ((c ^ lds_swz(ra)) << 4);
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int r = wn + 32 * j + (lane & 31);
-      woff[j][ks] = wbase + r * 64 + ((c ^ lds_swz(r)) << 4);
-    }
+    const int ra = wm + (lane & 31), rw = wn + (lane & 31);
+    aoff[ks] = ra * KT + ((c ^ stage_swz<KT>(ra)) << 4);
+    woff[ks] = wbase + rw * KT + ((c ^ stage_swz<KT>(rw)) << 4);
   }
   const int32_t* rqp = upw ? d.rqu : p.rq;
   const int32_t* bp = upw ? d.bu : p.bias;
@@ -1018,37 +1025,43 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
     cq[j] = make_colrq(rqp[2 * n], rqp[2 * n + 1], bp ? bp[n] : 0);
   }
   v16i acc[WN];
-#pragma unroll
-  for (int j = 0; j < WN; ++j) acc[j] = v16i{};
 
-  const int ktiles = p.K / 64;
-  for (int s0 = 0; s0 < NS - 1; ++s0)
+  // the K loop of mfma_tiles: tile kt's last fragments read, then one barrier frees its stage for
+  // tile kt + NS and publishes tile kt + 1
+  const int ktiles = p.K / KT;
+  for (int s0 = 0; s0 < NS; ++s0)
     if (s0 < ktiles) issue(s0);
-  wait_n(min(ktiles, NS - 1) - 1);
+  wait_n(min(ktiles, NS) - 1);
   lds_barrier();
-  v4i fa0, fa1, fb0[WN], fb1[WN];
-  fa0 = *reinterpret_cast<const v4i*>(ring + aoff[0]);
+  v4i fa[2], fb[2][WN];
+  auto frags = [&](const int8_t* st, int ks, int buf) {
+    fa[buf] = *reinterpret_cast<const v4i*>(st + aoff[ks]);
 #pragma unroll
-  for (int j = 0; j < WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(ring + woff[j][0]);
-  for (int kt = 0; kt < ktiles; ++kt) {
+    for (int j = 0; j < WN; ++j) fb[buf][j] = *reinterpret_cast<const v4i*>(st + woff[ks] + 32 * KT * j);
+  };
+  auto mfmas = [&](int buf, bool zero) {
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+      acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[buf], fb[buf][j], zero ? v16i{} : acc[j], 0, 0, 0);
+    mfma_ds_interleave<WN, 1 + WN>();
+  };
+  frags(ring, 0, 0);
+  auto ktile = [&](int kt, auto first) {
     const int8_t* st = ring + (kt % NS) * STAGE;
-    fa1 = *reinterpret_cast<const v4i*>(st + aoff[1]);
 #pragma unroll
-    for (int j = 0; j < WN; ++j) fb1[j] = *reinterpret_cast<const v4i*>(st + woff[j][1]);
-#pragma unroll
-    for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb0[j], acc[j], 0, 0, 0);
-    mfma_ds_interleave<WN, 1 + WN>();
-    wait_n(min(ktiles, kt + NS - 1) - kt - 2);
+    for (int s = 0; s + 1 < KSTEPS; ++s) {
+      frags(st, s + 1, (s + 1) & 1);
+      mfmas(s & 1, decltype(first)::value && s == 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    wait_n(min(ktiles, kt + NS) - kt - 2);
     lds_barrier();
-    if (kt + NS - 1 < ktiles) issue(kt + NS - 1);
-    const int8_t* sn = ring + ((kt + 1) % NS) * STAGE;
-    fa0 = *reinterpret_cast<const v4i*>(sn + aoff[0]);
-#pragma unroll
-    for (int j = 0; j < WN; ++j) fb0[j] = *reinterpret_cast<const v4i*>(sn + woff[j][0]);
-#pragma unroll
-    for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb1[j], acc[j], 0, 0, 0);
-    mfma_ds_interleave<WN, 1 + WN>();
-  }
+    if (kt + NS < ktiles) issue(kt + NS);
+    frags(ring + ((kt + 1) % NS) * STAGE, 0, KSTEPS & 1);
+    mfmas((KSTEPS - 1) & 1, false);
+  };
+  ktile(0, std::true_type{});
+  for (int kt = 1; kt < ktiles; ++kt) ktile(kt, std::false_type{});
   __syncthreads();  // every wave's fragment reads have returned; no stage load is outstanding
   // Epilogue over all eight waves: each wave stores its requantised accumulators (gate or up, i16)
   // into the ring, then every thread finishes four adjacent columns of one row at a time from the
@@ -1452,8 +1465,12 @@ extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {
   a.fqS = (int)d->fq_S;
   a.mul_sh = (int)d->mul_sh;
   const int mblocks = (int)ceil_div(M, 64), nblocks = (int)ceil_div(N, 128);
-  hipLaunchKernelGGL(linear_mfma_dual<GSTAGES>, dim3(ceil_div((int64_t)mblocks * nblocks, 8) * 8), dim3(512),
-                     GSTAGES * (64 + 2 * 128) * 64, s, p, a, mblocks, nblocks);
+  const dim3 grid((unsigned)(ceil_div((int64_t)mblocks * nblocks, 8) * 8));
+  if (p.K % 128 == 0)
+    hipLaunchKernelGGL((linear_mfma_dual<128, 2>), grid, dim3(512), 2 * (64 + 2 * 128) * 128, s, p, a, mblocks, nblocks);
+  else
+    hipLaunchKernelGGL((linear_mfma_dual<64, GSTAGES>), grid, dim3(512), GSTAGES * (64 + 2 * 128) * 64, s, p, a, mblocks,
+                       nblocks);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }

@@ -1,7 +1,8 @@
 """GPU parity of the gemm engine (llhip_linear) against the CPU oracle, bit-exact.
 
 Covers BASELINE config 2 (M in {1,16,128,2048} x (K,N) in {(896,896),(896,4864),(4864,896),
-(896,151936)}) plus every epilogue, bias, i8/i16 output, ragged K/N/M, split-K on and off.
+(896,151936)}) plus every epilogue, bias, i8/i16 output, ragged K/N/M, split-K on and off, and both
+K-tile sizes of the MFMA kernels (128 bytes when K % 128 == 0, else 64: K = 192, 576).
 At M=2048 x N=151936 the oracle checks 8 sampled rows over all columns and 96 sampled
 columns over all rows (an output element depends only on its A row and W row)."""
 from __future__ import annotations
@@ -61,7 +62,8 @@ def test_epilogues_and_bias(M, epilogue):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 64, 64), (16, 64, 172), (16, 172, 64), (5, 16, 3), (1, 4864, 896),
-                                   (17, 172, 33), (33, 96, 130), (2, 1, 5), (16, 65, 17), (300, 64, 1000)])
+                                   (17, 172, 33), (33, 96, 130), (2, 1, 5), (16, 65, 17), (300, 64, 1000),
+                                   (300, 576, 1000)])
 def test_ragged_shapes(M, K, N):
     rng = np.random.default_rng(M * 131 + K * 7 + N)
     a, w, rq = _operands(rng, M, K, N, out_i8=False)
@@ -149,7 +151,7 @@ def test_split_k_gemm(M, K, N, epilogue, out_i8):
     assert np.array_equal(got[rows], want)
 
 
-@pytest.mark.parametrize("M,K", [(512, 896), (300, 896), (37, 128), (64, 100)])
+@pytest.mark.parametrize("M,K", [(512, 896), (300, 896), (300, 576), (37, 128), (64, 100)])
 def test_linear_group_equals_separate_launches(M, K):
     """llhip_linear_group (q, k, v of a prompt chunk in one launch: i16, i16 and i8 outputs, bias
     on two of them) equals one llhip_linear launch per problem; K = 100 runs the per-problem
@@ -191,6 +193,7 @@ PARAMS = [(1 << 30, 30, 16, 11, 1518500250, 38), ((1 << 32) - 1, 0, 31, 31, (1 <
 
 
 @pytest.mark.parametrize("M,K,N,pad,par", [(512, 896, 4864, 0, 0), (512, 896, 4864, 5, 0), (300, 128, 200, 4, 0),
+                                           (200, 192, 256, 0, 0),
                                            (40, 100, 64, 5, 0)] + [(70, 128, 256, 0, i) for i in range(1, 5)])
 def test_gate_up_equals_the_three_ops(M, K, N, pad, par):
     """llhip_gate_up (gate linear with the silu epilogue, up linear with the mul epilogue on the
