@@ -410,29 +410,32 @@ __global__ __launch_bounds__(256) void linear_tiled(LinearArgs p, int mblocks, i
 struct ColRq {
   int32_t M;
   int S;
-  int64_t bM;  // bias * M
-  int64_t bR;  // bias * M + 2^(S-1)
+  int64_t bR;  // bias * M + 2^(S-1) (bias * M when S = 0)
 };
 
 __device__ __forceinline__ ColRq make_colrq(int32_t M, int S, int32_t bias) {
   ColRq c;
   c.M = M;
   c.S = S;
-  c.bM = (int64_t)bias * M;
-  c.bR = c.bM + (S > 0 ? (int64_t)1 << (S - 1) : 0);
-  // opaque to the optimiser (emits nothing): otherwise acc * M + bias * M is refactored into
-  // (acc + bias) * M, a 64 x 32-bit product, instead of one v_mad_i64_i32 per element
-  __asm__ volatile("" : "+v"(c.bM));
+  c.bR = (int64_t)bias * M + (S > 0 ? (int64_t)1 << (S - 1) : 0);
+  // opaque to the optimiser (emits nothing): otherwise acc * M + bR is refactored into a
+  // 64 x 32-bit product instead of one v_mad_i64_i32 per element
   __asm__ volatile("" : "+v"(c.bR));
   return c;
 }
 
 __device__ __forceinline__ bool colrq_fast(const ColRq& c) { return c.S >= 32 && c.S <= 62; }
 
+// requant of one accumulator: rshr((acc + bias) * M, S) (golden.py:323-337).  FAST (S in [32, 62]):
+// for K <= 2^16, |(acc + bias) * M| < 1.5 * 2^62, so adding the rounding bit before the shift cannot
+// overflow and the high word shifted by S - 32 is the result.  Otherwise the reference's
+// overflow-free rounding shift of the 64-bit product (bias * M recovered from bR, not kept per
+// column).
 template <bool FAST>
 __device__ __forceinline__ int32_t requant_col(int32_t acc, const ColRq& c) {
   if (FAST) return (int32_t)(((int64_t)acc * (int64_t)c.M + c.bR) >> 32) >> (c.S - 32);
-  const int64_t v = (int64_t)acc * (int64_t)c.M + c.bM;
+  const int64_t bM = c.bR - (c.S > 0 ? (int64_t)1 << (c.S - 1) : 0);
+  const int64_t v = (int64_t)acc * (int64_t)c.M + bM;
   return (int32_t)clamp64(rshr(v, c.S), INT32_MIN, INT32_MAX);
 }
 
