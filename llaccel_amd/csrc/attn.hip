@@ -131,6 +131,37 @@ __device__ __forceinline__ void wo_prefetch(const AttnArgs& p, int h, v4i* wpre,
 
 constexpr int ATTN_THREADS = 512;
 constexpr int ATTN_WAVES = ATTN_THREADS / 64;
+constexpr int SLICE_WPF = 2;  // output-projection columns per thread loaded at entry by a slice workgroup
+
+// Output-projection partial sums of the 16 head dimensions [16 ds, 16 ds + 16) of head h (their
+// requantised outputs in ah): each thread takes whole panel columns n = tid, tid + 512, ... (one
+// 16-byte chunk each; the first SLICE_WPF of them loaded at entry into wpre).
+template <int D>
+__device__ __forceinline__ void wo_slice(const AttnArgs& p, int h, int ds, const int8_t* ah, const v4i* wpre) {
+  const v4i a = *reinterpret_cast<const v4i*>(ah);
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < SLICE_WPF; ++i) {
+    const int n = tid + i * ATTN_THREADS;
+    const int32_t s = dot16(a, wpre[i]);
+    if (n < p.wo_N && s != 0) atomic_add_dev(p.wo_acc + n, s);
+  }
+  const Rsrc wr = rsrc(p.wop + (int64_t)h * p.wo_N * D, (int64_t)p.wo_N * D);
+  for (int n0 = SLICE_WPF * ATTN_THREADS + tid; n0 < p.wo_N; n0 += 4 * ATTN_THREADS) {
+    v4i w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int n = n0 + u * ATTN_THREADS;
+      w[u] = ld16(wr, n < p.wo_N ? (uint32_t)(n * D + 16 * ds) : LD_OOB);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int n = n0 + u * ATTN_THREADS;
+      const int32_t s = dot16(a, w[u]);
+      if (n < p.wo_N && s != 0) atomic_add_dev(p.wo_acc + n, s);
+    }
+  }
+}
 
 __device__ __forceinline__ int32_t sbyte(int w, int i) { return (int32_t)(int8_t)((uint32_t)w >> (8 * i)); }
 
@@ -170,8 +201,13 @@ __device__ __forceinline__ uint32_t lut_prob_lds(int64_t z, const uint16_t* ei, 
 // Loads at entry, in order of use: q and the keys of the first score pass, the LUT dwords (wave
 // 0), then the value rows of this thread's first VPF keys, so each phase waits only for its own
 // group and the value latency hides behind the score and softmax phases.  Keys >= T read zeros.
-template <int D, bool WO>
+// SLICE (output-projection fold, one row): D / 16 workgroups per head, workgroup ds computing the
+// head's full softmax but only the 16 output dimensions [16 ds, 16 ds + 16) and their share of the
+// output projection -- each workgroup streams all keys but a sixteenth-byte slice of every value row
+// and of the panel, so a head's value and panel bytes are spread over D / 16 CUs.
+template <int D, bool WO, bool SLICE = false>
 __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
+  static_assert(!SLICE || WO, "dimension slices fold the output projection");
   kernarg_warm<sizeof(AttnArgs)>();
   extern __shared__ int32_t sc[];  // [lds_T] scores, then probabilities
   __shared__ int32_t redmax[ATTN_WAVES], redsum[ATTN_WAVES];
@@ -179,21 +215,24 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   __shared__ int32_t wpart[4 * ATTN_WAVES][D];
   __shared__ __attribute__((aligned(16))) int8_t ah[WO ? D : 16];
   // output-projection panel chunks per thread loaded ahead (covering 1024 columns x D bytes)
-  constexpr int WPF = WO ? (D <= 128 ? (1024 * (D / 16)) / ATTN_THREADS : 16) : 0;
+  constexpr int WPF = SLICE ? SLICE_WPF : WO ? (D <= 128 ? (1024 * (D / 16)) / ATTN_THREADS : 16) : 0;
   constexpr int DC = D / 16;  // 16-byte chunks per key row
-  constexpr int TG = ATTN_THREADS / DC;
-  constexpr int VPF = 8;
+  constexpr int DS = SLICE ? DC : 1;        // workgroups per head
+  constexpr int VDC = SLICE ? 1 : DC;       // value chunks per key across the threads
+  constexpr int TG = ATTN_THREADS / VDC;    // keys per block-wide value load
+  constexpr int VPF = SLICE ? 2 : 8;
 
   // The G = H/Hkv query heads that read one (row, GQA group)'s K/V run on one XCD and share its
   // L2 (workgroup b is dispatched to XCD b % 8): pair u = m * Hkv + g goes to XCD u % 8, as
   // workgroups b = u % 8 + 8 * ((u / 8) * G + j) for its heads j.  The grid is
   // 8 * ceil(M * Hkv / 8) * G; workgroups past the last pair exit.
+  // (With slices the grid has DS workgroups per head: j = (xk % (G * DS)) / DS, ds = xk % DS.)
   const int G = p.H / p.Hkv;
   const int xk = (int)(blockIdx.x / 8);
-  const int u = (int)(blockIdx.x % 8) + 8 * (xk / G);
+  const int u = (int)(blockIdx.x % 8) + 8 * (xk / (G * DS));
   if (u >= p.M * p.Hkv) return;
   const int m = u / p.Hkv, g = u % p.Hkv;
-  const int h = g * G + xk % G;
+  const int h = g * G + (xk % (G * DS)) / DS, ds = xk % DS;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   // Loads in order of use: q and the keys of the first score pass, the LUT dwords (wave 0), the
   // value rows of this thread's first VPF keys.  The cache rows are addressed over the whole cache,
@@ -228,7 +267,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
     }
   }
   issue_fence();
-  const int dc = tid % DC, tg = tid / DC;
+  const int dc = SLICE ? ds : tid % DC, tg = tid / VDC;
   v4i vpre[VPF];
 #pragma unroll
   for (int u = 0; u < VPF; ++u) vpre[u] = ld16(vr, (uint32_t)((tg + u * TG) * D + 16 * dc));
@@ -239,7 +278,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   const int T = min((p.row_pos ? *(const __attribute__((address_space(4))) int32_t*)(p.row_pos + m)
                                : load_pos(p.pos_dev, p.pos) + m) + 1,
                     (int)p.max_seq);
-  if (WO && h == 0 && m == 0) zero_words(p.zero, p.zero_n);
+  if (WO && h == 0 && m == 0 && ds == 0) zero_words(p.zero, p.zero_n);
 
   // scores s[t] = q . k[t] (int32, |s| <= D * 2^14)
   int32_t lmax = INT32_MIN;
@@ -269,7 +308,16 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   // the output-projection panel columns of this thread, requested once the score loads are
   // consumed: they are needed last and their loads overlap the softmax and the value pass
   v4i wpre[WPF > 0 ? WPF : 1];
-  if constexpr (WPF > 0) wo_prefetch<D, WPF>(p, h, wpre, 0, p.wo_N);
+  if constexpr (SLICE) {
+    const Rsrc wr = rsrc(p.wop + (int64_t)h * p.wo_N * D, (int64_t)p.wo_N * D);
+#pragma unroll
+    for (int i = 0; i < WPF; ++i) {
+      const int n = tid + i * ATTN_THREADS;
+      wpre[i] = ld16(wr, n < p.wo_N ? (uint32_t)(n * D + 16 * ds) : LD_OOB);
+    }
+  } else if constexpr (WPF > 0) {
+    wo_prefetch<D, WPF>(p, h, wpre, 0, p.wo_N);
+  }
   if (wave == 0) {
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -342,25 +390,28 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
         acc[12 + i] += pn[u] * sbyte(vv[u].w, i);
       }
   }
-  // the lanes of a 16-lane row with equal lane % DC hold the same 16 columns: fold them with
+  // the lanes of a 16-lane row with equal lane % VDC hold the same 16 columns: fold them with
   // row rotations, then the 4 rows x ATTN_WAVES partials in LDS
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = row_fold<DC>(acc[i]);
-  if ((lane & 15) < DC) {
+  for (int i = 0; i < 16; ++i) acc[i] = row_fold<VDC>(acc[i]);
+  if ((lane & 15) < VDC) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) wpart[wave * 4 + (lane >> 4)][16 * (lane & 15) + i] = acc[i];
   }
   __syncthreads();
-  for (int d = tid; d < D; d += ATTN_THREADS) {
+  for (int d = tid; d < (SLICE ? 16 : D); d += ATTN_THREADS) {
     int32_t o = 0;
 #pragma unroll
     for (int w = 0; w < 4 * ATTN_WAVES; ++w) o += wpart[w][d];
     if (p.pb == 15) o = rshr32(o, 7);
     const int8_t y = (int8_t)sat8(mulshift(o, p.Mo, p.So));
-    p.out[(int64_t)m * p.ldo + (int64_t)h * D + d] = y;
+    p.out[(int64_t)m * p.ldo + (int64_t)h * D + 16 * ds + d] = y;
     if constexpr (WO) ah[d] = y;
   }
-  if constexpr (WO) {
+  if constexpr (SLICE) {
+    __syncthreads();
+    wo_slice<D>(p, h, ds, ah, wpre);
+  } else if constexpr (WO) {
     __syncthreads();
     wo_partial<D, WPF>(p, h, ah, wpre, 0, p.wo_N);
   }
@@ -1146,11 +1197,17 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
     return 0;
   }
   const size_t lds = sizeof(int32_t) * (size_t)p.lds_T;
-  if (M * Hkv > (int64_t)INT32_MAX / 8 / (H / Hkv)) return fail(-EINVAL, "attention: too many rows");
-  dim3 grid((unsigned)(8 * ceil_div(M * Hkv, 8) * (H / Hkv)));
+  // the output-projection fold of one row runs D / 16 workgroups per head (dimension slices),
+  // heads of D = 256 one workgroup each
+  const bool slice = fold && M == 1 && D <= 128;
+  const int64_t per_head = slice ? D / 16 : 1;
+  if (M * Hkv > (int64_t)INT32_MAX / 8 / (H / Hkv) / per_head) return fail(-EINVAL, "attention: too many rows");
+  dim3 grid((unsigned)(8 * ceil_div(M * Hkv, 8) * (H / Hkv) * per_head));
   dim3 block(ATTN_THREADS);
 #define LLHIP_ROWHEAD(DD)                                                            \
-  if (fold)                                                                         \
+  if (slice)                                                                        \
+    hipLaunchKernelGGL((attention_rowhead<DD, true, DD <= 128>), grid, block, lds, s, p); \
+  else if (fold)                                                                    \
     hipLaunchKernelGGL((attention_rowhead<DD, true>), grid, block, lds, s, p);      \
   else                                                                              \
     hipLaunchKernelGGL((attention_rowhead<DD, false>), grid, block, lds, s, p);
