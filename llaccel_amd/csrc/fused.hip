@@ -480,7 +480,10 @@ __device__ __forceinline__ T pick3(int role, const T (&v)[3]) {
   return role == 0 ? a : (role == 1 ? b : c);
 }
 
-template <int MAXW, bool RESID>
+// SPL > 1 (decode chain, no head norm): SPL workgroups per head block, workgroup s taking the
+// 16-column tiles t with t % SPL == s -- a tile and its RoPE partner t + D/32 fall in the same
+// workgroup when (D / 32) % SPL == 0 -- so each streams 1/SPL of the head's weights.
+template <int MAXW, bool RESID, int SPL = 1>
 __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   kernarg_warm<sizeof(AttnInArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
@@ -492,13 +495,17 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   int32_t* hres = reinterpret_cast<int32_t*>(dyn + ((p.M * lda + 15) & ~15));  // [M][D] i32
 
   const int b = blockIdx.x;
-  const int role = b < p.H ? 0 : (b < p.H + p.Hkv ? 1 : 2);
-  const int hh = role == 0 ? b : (role == 1 ? b - p.H : b - p.H - p.Hkv);
+  const int bh = b / SPL, sp = b % SPL;  // head block, its tile share
+  const int role = bh < p.H ? 0 : (bh < p.H + p.Hkv ? 1 : 2);
+  const int hh = role == 0 ? bh : (role == 1 ? bh - p.H : bh - p.H - p.Hkv);
   const int D = p.D, M = p.M;
   const int Nrole = (role == 0 ? p.H : p.Hkv) * D;
   const int base = hh * D;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int tiles = D >> 4;
+  const int tiles = (D >> 4) / SPL;  // 16-column tiles of this workgroup
+  const int DW = D / SPL;            // its columns
+  // head column of this workgroup's column lc: tile (lc / 16) * SPL + sp
+  auto gcol = [&](int lc) { return 16 * ((lc >> 4) * SPL + sp) + (lc & 15); };
 
   // kernel entry, in order of use: the device position, RMSNorm operands, weight slice, epilogue
   // operands of this thread's column, head-norm gamma.  The position is a vector load issued
@@ -507,7 +514,7 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   const int32_t posv = ld4(rsrc(p.pos_dev, 4), 0);
   // per-row positions: the row of this thread's RoPE pair and row tid (staged in LDS for the tail)
   const int half = D >> 1;
-  const int jrope = tid % half, mrope = tid / half;
+  const int jrope = gcol(tid % (half / SPL)), mrope = tid / (half / SPL);
   const Rsrc rpr = rsrc(p.row_pos, 4 * M);
   const int32_t rp_rope = ld4(rpr, mrope < M ? 4 * mrope : LD_OOB), rp_own = ld4(rpr, tid < M ? 4 * tid : LD_OOB);
   issue_fence();
@@ -528,14 +535,14 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     const int t = wave % tiles, ks = wave / tiles;
     int s0, s1;
     split_range((p.K + 63) >> 6, p.KS, ks, s0, s1);
-    wslice_prefetch(ws, wr, base + t * 16 + (lane & 15), p.K, lane >> 4, s0, s1);
+    wslice_prefetch(ws, wr, base + (t * SPL + sp) * 16 + (lane & 15), p.K, lane >> 4, s0, s1);
   }
   issue_fence();
-  const int dcol = tid % D;  // blockDim is a multiple of D: each thread owns one column in the tail
+  const int dcol = gcol(tid % DW);  // blockDim is a multiple of DW: each thread owns one column in the tail
   const int ncol = base + dcol;
   const v2i rq = ld8(rsrc(pick3(role, p.rq), (int64_t)Nrole * 8), 8 * ncol);
   const int32_t bias = ld4(rsrc(pick3(role, p.bias), (int64_t)Nrole * 4), 4 * ncol);
-  const bool hn = p.has_norm && role < 2;
+  const bool hn = SPL == 1 && p.has_norm && role < 2;  // split heads are never normed (host)
   int32_t hg[4];  // head-norm gamma of dims lane + 64 i (the per-row norm runs wave-wide)
   {
     const Rsrc gr = rsrc(hn ? (role == 0 ? p.nrm_gamma[0] : p.nrm_gamma[1]) : nullptr, (int64_t)D * 2);
@@ -575,14 +582,14 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 4 * kg + r;
-      if (m < M) hres[m * D + wave * 16 + col] = acc[r];
+      if (m < M) hres[m * D + (wave * SPL + sp) * 16 + col] = acc[r];
     }
   }
   __syncthreads();
 
-  const int rstep = blockDim.x / D;
+  const int rstep = blockDim.x / DW;
   if (role == 2) {  // v: requant8 -> v activation and V cache
-    for (int m = tid / D; m < M; m += rstep) {
+    for (int m = tid / DW; m < M; m += rstep) {
       const int8_t y = (int8_t)sat8(mulshift((int64_t)hres[m * D + dcol] + bias, rq.x, rq.y));
       static_cast<int8_t*>(p.lin_out[2])[(int64_t)m * Nrole + ncol] = y;
       const int pm = rowpos[m];
@@ -592,7 +599,7 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     return;
   }
   // q / k: requant16 -> activation; head values kept in hres as int32
-  for (int m = tid / D; m < M; m += rstep) {
+  for (int m = tid / DW; m < M; m += rstep) {
     const int16_t y = (int16_t)sat16(mulshift((int64_t)hres[m * D + dcol] + bias, rq.x, rq.y));
     static_cast<int16_t*>(p.lin_out[role])[(int64_t)m * Nrole + ncol] = y;
     hres[m * D + dcol] = y;
@@ -617,7 +624,7 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     __syncthreads();
   }
   // RoPE (golden.py:141-158) -> quant (golden.py:119-120) -> K cache for keys
-  for (int m = mrope; m < M; m += blockDim.x / half) {
+  for (int m = mrope; m < M; m += blockDim.x / (half / SPL)) {
     int64_t c = c0, s = s0r;
     const int pm = rowpos[m];
     if (pm < 0 || pm >= p.max_seq) continue;
@@ -1040,6 +1047,24 @@ static int attn_in_launch(const AttnInArgs& p, int waves, size_t lds, void* stre
   return 0;
 }
 
+// The decode chain's attn_in with each head block over two workgroups (half of its 16-column
+// tiles each, eight waves: more K splits per tile), when the head has no Q/K norm and its RoPE
+// pairs stay within a half (D / 32 even).  Returns false when the shape does not allow it.
+static bool attn_in_split_launch(AttnInArgs p, void* stream, int& rc) {
+  constexpr int SPL = 2;
+  const int tiles = p.D / 16 / SPL;
+  if (p.has_norm || p.M != 1 || (p.D / 32) % SPL || tiles < 1 || FUSED_WAVES % tiles) return false;
+  const int steps = (int)ceil_div(p.K, 64);
+  const int ks = std::min(FUSED_WAVES / tiles, steps);
+  if (64 * tiles * ks < p.K / 4 || (64 * tiles * ks) % (p.D / SPL)) return false;  // one row unit per thread
+  p.KS = ks;
+  const size_t lds = (size_t)((p.K + 16 + 15) & ~15) + sizeof(int32_t) * (size_t)p.D;
+  hipLaunchKernelGGL((attn_in_kernel<FUSED_WAVES, true, SPL>), dim3((unsigned)((p.H + 2 * p.Hkv) * SPL)),
+                     dim3(64 * tiles * ks), lds, (hipStream_t)stream, p);
+  rc = hipGetLastError() == hipSuccess ? 0 : fail(-EIO, "dec_attn_in: launch failed");
+  return true;
+}
+
 static int fill_resid(ResidArgs& ra, const llhip_resid_desc* r, const NormQuant& pre) {
   ra = ResidArgs{};
   ra.R = 1;
@@ -1087,6 +1112,7 @@ extern "C" int llhip_dec_attn_in(const llhip_attn_in_desc* d, const llhip_resid_
   if (rc) return rc;
   p.zero = static_cast<int32_t*>(zero);
   p.zero_n = (int)zero_n;
+  if (attn_in_split_launch(p, stream, rc)) return rc;
   return attn_in_launch<true>(p, waves, lds, stream);
 }
 
