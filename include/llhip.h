@@ -87,6 +87,28 @@ int llhip_rope_quant(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t 
                      const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev,
                      const int32_t* row_pos, int16_t* y, int8_t* yq, int64_t qM, int64_t qS, int8_t* kc,
                      const int8_t* v, int64_t ldv, int8_t* vc, int64_t max_seq, int64_t slot_stride, void* stream);
+/* the arguments of one llhip_rope_quant call */
+typedef struct llhip_rope_quant_desc {
+  const void* x;        /* i16 [M][ldx] */
+  int64_t M, H, D, ldx;
+  const void* cos_tab;  /* i16 [table_rows][D/2] */
+  const void* sin_tab;
+  int64_t table_rows, pos;
+  const void* pos_dev;  /* int32, or NULL: pos */
+  const void* row_pos;  /* int32 [M] per-row positions, or NULL */
+  void* y;              /* i16 [M][H*D] */
+  void* yq;             /* i8 [M][H*D] */
+  int64_t qM, qS;
+  void* kc;             /* K cache or NULL */
+  const void* v;        /* v rows [M][ldv] (with vc) */
+  int64_t ldv;
+  void* vc;             /* V cache or NULL */
+  int64_t max_seq, slot_stride;
+} llhip_rope_quant_desc;
+/* golden.py:141-158 + 119-120 [+ 344-351]  two llhip_rope_quant calls in one launch (a prompt
+ * chunk's query rows, then its key rows with the layer's kv_write): the same checks and results as
+ * the two calls in order. */
+int llhip_rope_quant2(const llhip_rope_quant_desc* a, const llhip_rope_quant_desc* b, void* stream);
 
 /* ---- gemm engine ---- */
 /* golden.py:316-342  out[M][N] = epilogue(requant(A[M][K] . W[N][K]^T + bias)).

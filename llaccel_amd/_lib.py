@@ -57,6 +57,7 @@ _SIGS = {
     "llhip_gate_up": [_p, _p],
     "llhip_rope_quant": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64, _p,
                          _i64, _i64, _p],
+    "llhip_rope_quant2": [_p, _p, _p],
     "llhip_quant_rows_i8": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p],
     "llhip_f32_absmax": [_p, _i64, _i64, _i64, _p, _p, _p, _p],
     "llhip_f32_rms_min": [_p, _i64, _i64, _p, _p],
@@ -137,6 +138,14 @@ class GateUpDesc(ctypes.Structure):
                 ("rqu", _p), ("bu", _p), ("N", _i64), ("ld", _i64), ("silu_Mi", _i64), ("silu_Si", _i64),
                 ("silu_sh", _i64), ("mul_sh", _i64), ("fq_M", _i64), ("fq_S", _i64), ("sg_out", _p), ("f_out", _p),
                 ("fq_out", _p)]
+
+
+class RopeQuantDesc(ctypes.Structure):
+    """llhip_rope_quant_desc: the arguments of one llhip_rope_quant call."""
+    _fields_ = [("x", _p), ("M", _i64), ("H", _i64), ("D", _i64), ("ldx", _i64), ("cos_tab", _p), ("sin_tab", _p),
+                ("table_rows", _i64), ("pos", _i64), ("pos_dev", _p), ("row_pos", _p), ("y", _p), ("yq", _p),
+                ("qM", _i64), ("qS", _i64), ("kc", _p), ("v", _p), ("ldv", _i64), ("vc", _p), ("max_seq", _i64),
+                ("slot_stride", _i64)]
 
 
 class LinearProblem(ctypes.Structure):

@@ -168,44 +168,59 @@ __global__ void rope_kernel(const int16_t* __restrict__ x, int64_t M, int H, int
   y[m * ldy + h * D + half + i] = (int16_t)sat16(rshr(b * c + a * s, 14));
 }
 
-// RoPE then quant of the rotated rows in one pass (golden.py:141-158, 119-120); for key rows also
-// the layer's kv_write (golden.py:344-351): the quantised keys and the v rows into the caches at
-// their positions.  Thread per (row, head, i < D/2), as rope_kernel.
-__global__ void rope_quant_kernel(const int16_t* __restrict__ x, int64_t M, int H, int D, int64_t ldx,
-                                  const int16_t* __restrict__ cos_tab, const int16_t* __restrict__ sin_tab,
-                                  int64_t table_rows, int pos, const int32_t* __restrict__ pos_dev,
-                                  const int32_t* __restrict__ row_pos, int16_t* __restrict__ y, int8_t* __restrict__ yq,
-                                  int64_t qM, int qS, int8_t* __restrict__ kc, const int8_t* __restrict__ v,
-                                  int64_t ldv, int8_t* __restrict__ vc, int64_t max_seq, int64_t slot_stride) {
-  const int half = D / 2;
-  const int64_t total = M * H * half;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int64_t m = idx / ((int64_t)H * half);
-  const int rem = (int)(idx % ((int64_t)H * half));
+struct RopeJob {
+  const int16_t* x;
+  int64_t M, ldx, table_rows, qM, ldv, max_seq, slot_stride, total;
+  int H, D, pos, qS;
+  const int16_t* cos_tab;
+  const int16_t* sin_tab;
+  const int32_t* pos_dev;
+  const int32_t* row_pos;
+  int16_t* y;
+  int8_t* yq;
+  int8_t* kc;
+  const int8_t* v;
+  int8_t* vc;
+};
+
+__device__ __forceinline__ void rope_quant_one(const RopeJob& j, int64_t idx) {
+  const int half = j.D / 2;
+  const int64_t m = idx / ((int64_t)j.H * half);
+  const int rem = (int)(idx % ((int64_t)j.H * half));
   const int h = rem / half, i = rem % half;
-  const int64_t pm = row_pos ? (int64_t)row_pos[m] : (int64_t)(pos_dev ? *pos_dev : pos) + m;
-  if (pm < 0 || pm >= table_rows) return;  // device positions are checked by the caller; never read past the table
+  const int64_t pm = j.row_pos ? (int64_t)j.row_pos[m] : (int64_t)(j.pos_dev ? *j.pos_dev : j.pos) + m;
+  if (pm < 0 || pm >= j.table_rows) return;  // device positions are checked by the caller; never read past the table
   const int64_t trow = pm * half;
-  const int64_t c = cos_tab[trow + i], s = sin_tab[trow + i];
-  const int64_t o = m * (int64_t)H * D + (int64_t)h * D;
-  const int64_t a = x[m * ldx + h * D + i], b = x[m * ldx + h * D + half + i];
+  const int64_t c = j.cos_tab[trow + i], s = j.sin_tab[trow + i];
+  const int64_t o = m * (int64_t)j.H * j.D + (int64_t)h * j.D;
+  const int64_t a = j.x[m * j.ldx + h * j.D + i], b = j.x[m * j.ldx + h * j.D + half + i];
   const int16_t y1 = (int16_t)sat16(rshr(a * c - b * s, 14));
   const int16_t y2 = (int16_t)sat16(rshr(b * c + a * s, 14));
-  y[o + i] = y1;
-  y[o + half + i] = y2;
-  const int8_t q1 = (int8_t)sat8(mulshift(y1, qM, qS)), q2 = (int8_t)sat8(mulshift(y2, qM, qS));
-  yq[o + i] = q1;
-  yq[o + half + i] = q2;
-  if (kc && pm < max_seq) {  // never write past a cache
-    const int64_t dst = (row_pos ? m * slot_stride : 0) + ((int64_t)h * max_seq + pm) * D;
-    kc[dst + i] = q1;
-    kc[dst + half + i] = q2;
-    if (vc) {
-      vc[dst + i] = v[m * ldv + (int64_t)h * D + i];
-      vc[dst + half + i] = v[m * ldv + (int64_t)h * D + half + i];
+  j.y[o + i] = y1;
+  j.y[o + half + i] = y2;
+  const int8_t q1 = (int8_t)sat8(mulshift(y1, j.qM, j.qS)), q2 = (int8_t)sat8(mulshift(y2, j.qM, j.qS));
+  j.yq[o + i] = q1;
+  j.yq[o + half + i] = q2;
+  if (j.kc && pm < j.max_seq) {  // never write past a cache
+    const int64_t dst = (j.row_pos ? m * j.slot_stride : 0) + ((int64_t)h * j.max_seq + pm) * j.D;
+    j.kc[dst + i] = q1;
+    j.kc[dst + half + i] = q2;
+    if (j.vc) {
+      j.vc[dst + i] = j.v[m * j.ldv + (int64_t)h * j.D + i];
+      j.vc[dst + half + i] = j.v[m * j.ldv + (int64_t)h * j.D + half + i];
     }
   }
+}
+
+// RoPE then quant of the rotated rows in one pass (golden.py:141-158, 119-120); for key rows also
+// the layer's kv_write (golden.py:344-351): the quantised keys and the v rows into the caches at
+// their positions.  Thread per (row, head, i < D/2) of job a, then of job b (b.total = 0: none).
+__global__ void rope_quant_kernel(RopeJob a, RopeJob b) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx < a.total)
+    rope_quant_one(a, idx);
+  else if (idx < a.total + b.total)
+    rope_quant_one(b, idx - a.total);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -471,28 +486,78 @@ int llhip_rope(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, c
   return 0;
 }
 
+}  // extern "C"
+
+namespace llhip {
+// the checks of llhip_rope_quant, and its launch arguments
+static int rope_job(const llhip_rope_quant_desc& d, RopeJob& j) {
+  const int64_t M = d.M, H = d.H, D = d.D;
+  if (M < 0 || H < 0 || D < 0 || D % 2) return fail(-EINVAL, "rope_quant: bad geometry (D must be even)");
+  if (d.ldx < H * D) return fail(-EINVAL, "rope_quant: leading dimension too small");
+  if (!u32_ok(d.qM) || !shift_ok(d.qS)) return fail(-EINVAL, "rope_quant: quant multiplier must be u32, shift in [0,63]");
+  if (!d.pos_dev && !d.row_pos && (d.pos < 0 || d.pos + M > d.table_rows))
+    return fail(-ERANGE, "rope: positions exceed the table");
+  if (d.vc && (!d.kc || !d.v || d.ldv < H * D)) return fail(-EINVAL, "rope_quant: the V cache write needs kc and v rows");
+  if (d.kc) {
+    if (!d.pos_dev && !d.row_pos && d.pos + M > d.max_seq)
+      return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)d.pos, (long long)(d.pos + M - 1),
+                  (long long)d.max_seq);
+    if (d.row_pos && d.slot_stride < H * d.max_seq * D) return fail(-EINVAL, "rope_quant: cache slots overlap");
+  }
+  j = RopeJob{};
+  j.x = static_cast<const int16_t*>(d.x);
+  j.M = M;
+  j.ldx = d.ldx;
+  j.table_rows = d.table_rows;
+  j.qM = d.qM;
+  j.ldv = d.ldv;
+  j.max_seq = d.max_seq;
+  j.slot_stride = d.slot_stride;
+  j.total = M * H * (D / 2);
+  j.H = (int)H;
+  j.D = (int)D;
+  j.pos = (int)d.pos;
+  j.qS = (int)d.qS;
+  j.cos_tab = static_cast<const int16_t*>(d.cos_tab);
+  j.sin_tab = static_cast<const int16_t*>(d.sin_tab);
+  j.pos_dev = static_cast<const int32_t*>(d.pos_dev);
+  j.row_pos = static_cast<const int32_t*>(d.row_pos);
+  j.y = static_cast<int16_t*>(d.y);
+  j.yq = static_cast<int8_t*>(d.yq);
+  j.kc = static_cast<int8_t*>(d.kc);
+  j.v = static_cast<const int8_t*>(d.v);
+  j.vc = static_cast<int8_t*>(d.vc);
+  return 0;
+}
+
+static int rope_launch(const RopeJob& a, const RopeJob& b, void* stream) {
+  const int64_t total = a.total + b.total;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(rope_quant_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, a, b);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+}  // namespace llhip
+
+extern "C" {
+
 int llhip_rope_quant(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t ldx, const int16_t* cos_tab,
                      const int16_t* sin_tab, int64_t table_rows, int64_t pos, const int32_t* pos_dev,
                      const int32_t* row_pos, int16_t* y, int8_t* yq, int64_t qM, int64_t qS, int8_t* kc,
                      const int8_t* v, int64_t ldv, int8_t* vc, int64_t max_seq, int64_t slot_stride, void* stream) {
-  if (M < 0 || H < 0 || D < 0 || D % 2) return fail(-EINVAL, "rope_quant: bad geometry (D must be even)");
-  if (ldx < H * D) return fail(-EINVAL, "rope_quant: leading dimension too small");
-  if (!u32_ok(qM) || !shift_ok(qS)) return fail(-EINVAL, "rope_quant: quant multiplier must be u32, shift in [0,63]");
-  if (!pos_dev && !row_pos && (pos < 0 || pos + M > table_rows)) return fail(-ERANGE, "rope: positions exceed the table");
-  if (vc && (!kc || !v || ldv < H * D)) return fail(-EINVAL, "rope_quant: the V cache write needs kc and v rows");
-  if (kc) {
-    if (!pos_dev && !row_pos && pos + M > max_seq)
-      return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)pos, (long long)(pos + M - 1),
-                  (long long)max_seq);
-    if (row_pos && slot_stride < H * max_seq * D) return fail(-EINVAL, "rope_quant: cache slots overlap");
-  }
-  const int64_t total = M * H * (D / 2);
-  if (total == 0) return 0;
-  hipLaunchKernelGGL(rope_quant_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, x, M,
-                     (int)H, (int)D, ldx, cos_tab, sin_tab, table_rows, (int)pos, pos_dev, row_pos, y, yq, qM, (int)qS,
-                     kc, v, ldv, vc, max_seq, slot_stride);
-  LLHIP_LAUNCH_CHECK();
-  return 0;
+  const llhip_rope_quant_desc d{x, M, H, D, ldx, cos_tab, sin_tab, table_rows, pos, pos_dev, row_pos, y, yq, qM, qS,
+                                kc, v, ldv, vc, max_seq, slot_stride};
+  RopeJob a, none{};
+  const int rc = rope_job(d, a);
+  return rc ? rc : rope_launch(a, none, stream);
+}
+
+int llhip_rope_quant2(const llhip_rope_quant_desc* a, const llhip_rope_quant_desc* b, void* stream) {
+  if (!a || !b) return fail(-EINVAL, "rope_quant2: null descriptor");
+  RopeJob ja, jb;
+  int rc = rope_job(*a, ja);
+  if (!rc) rc = rope_job(*b, jb);
+  return rc ? rc : rope_launch(ja, jb, stream);
 }
 
 int llhip_embed_rows(const int16_t* embed, int64_t vocab_rows, int64_t dim, const int32_t* tokens, int64_t n_tokens,

@@ -68,14 +68,15 @@ class _NormQuantStep:
 
 
 class _RopeQuantStep:
-    """rope -> quant of the rotated rows in one llhip_rope_quant launch; for the key rows also the
-    layer's kv_write (quantised keys and the v rows into the caches)."""
+    """rope -> quant of the query rows, and rope -> quant of the key rows with the layer's kv_write
+    (quantised keys and the v rows into the caches), in one llhip_rope_quant2 launch."""
 
-    def __init__(self, model, rope, quant, kvw=None):
-        self.model, self.rope, self.quant, self.kvw = model, rope, quant, kvw
+    def __init__(self, model, rope_q, quant_q, rope_k, quant_k, kvw):
+        self.model, self.parts = model, ((rope_q, quant_q, None), (rope_k, quant_k, kvw))
+        self.desc = (_lib.RopeQuantDesc(), _lib.RopeQuantDesc())
 
-    def __call__(self, M, pos, pd=None):
-        m, ro, qu, kvw = self.model, self.rope, self.quant, self.kvw
+    def _fill(self, d, ro, qu, kvw, M, pos, pd):
+        m = self.model
         H, D = int(ro["H"]), int(ro["D"])
         cos_t, sin_t = m._dt["rope_cos"], m._dt["rope_sin"]
         if kvw is None:
@@ -88,9 +89,17 @@ class _RopeQuantStep:
             kc, vc, pdev, rpos, stride = m._kv_args(int(kvw["layer"]), pd)
             vbuf = m._buf(kvw["v"])
             v, ldv = _vp(vbuf), vbuf.shape[1]
-        _lib.call("llhip_rope_quant", _vp(m._buf(ro["in"])), M, H, D, H * D, _vp(cos_t), _vp(sin_t),
-                  int(cos_t.shape[0]), pos, pdev, rpos, _vp(m._buf(ro["out"])), _vp(m._buf(qu["out"])),
-                  int(qu["M"]), int(qu["S"]), kc, v, ldv, vc, m.max_seq, stride, m._stream_handle())
+        d.x, d.M, d.H, d.D, d.ldx = _vp(m._buf(ro["in"])), M, H, D, H * D
+        d.cos_tab, d.sin_tab, d.table_rows, d.pos = _vp(cos_t), _vp(sin_t), int(cos_t.shape[0]), pos
+        d.pos_dev, d.row_pos = pdev, rpos
+        d.y, d.yq, d.qM, d.qS = _vp(m._buf(ro["out"])), _vp(m._buf(qu["out"])), int(qu["M"]), int(qu["S"])
+        d.kc, d.v, d.ldv, d.vc, d.max_seq, d.slot_stride = kc, v, ldv, vc, m.max_seq, stride
+
+    def __call__(self, M, pos, pd=None):
+        for d, (ro, qu, kvw) in zip(self.desc, self.parts):
+            self._fill(d, ro, qu, kvw, M, pos, pd)
+        _lib.call("llhip_rope_quant2", ctypes.byref(self.desc[0]), ctypes.byref(self.desc[1]),
+                  self.model._stream_handle())
 
 
 class _GroupLinearStep:
@@ -156,7 +165,7 @@ def wide_steps(model, ops, steps):
     """Launches of a fused run for more rows than its fused kernel takes (prompt chunks): the run's
     per-op steps, with each rmsnorm + quant of its output as one launch, three linears of one input
     (q, k, v) as one grouped launch, the gate and up linears and the quant of their product as
-    one launch, and attn_in's group rope q, rope k, quant q, quant k, kv_write as two.  The
+    one launch, and attn_in's group rope q, rope k, quant q, quant k, kv_write as one.  The
     arithmetic of every op is unchanged."""
     out, i = [], 0
     while i < len(ops):
@@ -186,8 +195,7 @@ def wide_steps(model, ops, steps):
                     and _is(kvw, "kv_write") and qq_["in"] == rq_["out"] and kq_["in"] == rk_["out"]
                     and kvw["k"] == kq_["out"] and int(kvw["Hkv"]) == int(rk_["H"]) and int(kvw["D"]) == int(rk_["D"])
                     and model._act_spec[kvw["v"]][1] >= int(rk_["H"]) * int(rk_["D"])):
-                out.append(_RopeQuantStep(model, rq_, qq_))
-                out.append(_RopeQuantStep(model, rk_, kq_, kvw))
+                out.append(_RopeQuantStep(model, rq_, qq_, rk_, kq_, kvw))
                 i += 5
                 continue
         out.append(steps[i])

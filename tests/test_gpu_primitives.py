@@ -2,6 +2,7 @@
 (bit-exact).  Calls go through llaccel_amd.golden, i.e. through the libllhip C ABI."""
 from __future__ import annotations
 
+import ctypes
 import math
 
 import numpy as np
@@ -204,3 +205,52 @@ def test_rope_quant_with_cache_writes(H, D, rows):
     with pytest.raises(ValueError):
         _lib.call("llhip_rope_quant", ptr(xd), M, H, D, H * D, ptr(cd), ptr(sd), max_seq, 60, None, None, ptr(yd),
                   ptr(yqd), qM, qS, ptr(kcd), ptr(vd), H * D, ptr(vcd), max_seq, 0, stream())
+
+
+def test_rope_quant2_equals_two_calls():
+    """llhip_rope_quant2 (the query rows, then the key rows with the layer's kv_write, in one launch)
+    equals the oracle's rope, vquant and cache write of each part, and refuses a bad part as the
+    single call would."""
+    from llaccel_amd import _lib
+    from tests.gpu_helpers import ptr, stream, torch, up
+
+    t = torch()
+    M, H, Hkv, D, max_seq, pos = 37, 14, 2, 64, 96, 41
+    qq, qk = (1234567891, 40), (987654321, 39)
+    inv = 1e6 ** (-np.arange(0, D, 2) / D)
+    ang = np.outer(np.arange(max_seq), inv)
+    c = np.round(np.cos(ang) * 16384).astype(np.int64)
+    s = np.round(np.sin(ang) * 16384).astype(np.int64)
+    xq = RNG.integers(-32768, 32768, (M, H * D))
+    xk = RNG.integers(-32768, 32768, (M, Hkv * D))
+    v = RNG.integers(-128, 128, (M, Hkv * D))
+    kc0 = RNG.integers(-128, 128, (Hkv, max_seq, D))
+    vc0 = RNG.integers(-128, 128, (Hkv, max_seq, D))
+    xqd, xkd, cd, sd, vd = up(xq, np.int16), up(xk, np.int16), up(c, np.int16), up(s, np.int16), up(v, np.int8)
+    kcd, vcd = up(kc0, np.int8), up(vc0, np.int8)
+    outs = [t.zeros((M, n * D), dtype=dt, device="cuda") for n in (H, Hkv) for dt in (t.int16, t.int8)]
+
+    def desc(x, n, y, yq, q, kc=None, vv=None, vc=None, p=pos):
+        d = _lib.RopeQuantDesc()
+        d.x, d.M, d.H, d.D, d.ldx = ptr(x), M, n, D, n * D
+        d.cos_tab, d.sin_tab, d.table_rows, d.pos = ptr(cd), ptr(sd), max_seq, p
+        d.y, d.yq, d.qM, d.qS = ptr(y), ptr(yq), q[0], q[1]
+        d.kc, d.v, d.ldv, d.vc, d.max_seq = ptr(kc), ptr(vv), n * D if vv is not None else 0, ptr(vc), max_seq
+        return d
+
+    a = desc(xqd, H, outs[0], outs[1], qq)
+    b = desc(xkd, Hkv, outs[2], outs[3], qk, kcd, vd, vcd)
+    _lib.call("llhip_rope_quant2", ctypes.byref(a), ctypes.byref(b), stream())
+    yq_want, yk_want = O.rope(xq, H, D, c, s, pos), O.rope(xk, Hkv, D, c, s, pos)
+    kq_want = O.vquant(yk_want, *qk)
+    assert np.array_equal(outs[0].cpu().numpy(), yq_want)
+    assert np.array_equal(outs[1].cpu().numpy(), O.vquant(yq_want, *qq))
+    assert np.array_equal(outs[2].cpu().numpy(), yk_want) and np.array_equal(outs[3].cpu().numpy(), kq_want)
+    kc, vc = kc0.copy(), vc0.copy()
+    for m in range(M):
+        kc[:, pos + m] = kq_want[m].reshape(Hkv, D)
+        vc[:, pos + m] = v[m].reshape(Hkv, D)
+    assert np.array_equal(kcd.cpu().numpy(), kc) and np.array_equal(vcd.cpu().numpy(), vc)
+    with pytest.raises(ValueError):  # the key part's positions run past the cache
+        _lib.call("llhip_rope_quant2", ctypes.byref(a), ctypes.byref(desc(xkd, Hkv, outs[2], outs[3], qk, kcd, vd, vcd,
+                                                                          p=max_seq - 10)), stream())
