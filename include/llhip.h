@@ -247,6 +247,13 @@ typedef struct llhip_norm_quant_desc {
 /* golden.py:124-137 + 119-120  rmsnorm then quant of M rows in one launch (one workgroup per row):
  * h_out = rmsnorm(x), hq_out = quant(h_out).  Multi-row fused launches run it first (prequant). */
 int llhip_rmsnorm_quant(const llhip_norm_quant_desc* d, int64_t M, void* stream);
+/* golden.py:316-342 (resadd epilogue) + 124-137 + 119-120  llhip_linear with the resadd epilogue
+ * (out i16 [M][ldo]) followed by llhip_rmsnorm_quant(norm, M) of its output rows (norm->x == out,
+ * norm->ldx == ldo, norm->K == N): the same results; a launch split along K finishes its partial
+ * sums and normalises the rows in one kernel. */
+int llhip_linear_norm(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_t* W, int64_t N, const int32_t* rq,
+                      const int32_t* bias, const int16_t* aux, int64_t ldaux, int16_t* out, int64_t ldo,
+                      const llhip_norm_quant_desc* norm, void* ws, void* stream);
 
 typedef struct llhip_attn_in_desc {
   llhip_norm_quant_desc pre;

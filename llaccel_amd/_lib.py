@@ -41,6 +41,7 @@ _SIGS = {
     "llhip_rope": [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _p, _i64, _p],
     "llhip_linear": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p,
                      _i64, _p, _p],
+    "llhip_linear_norm": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _p, _i64, _p, _p, _p],
     "llhip_exact_matmul": [_p, _i64, _i64, _p, _i64, _p, _p],
     "llhip_kv_write": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p],
     "llhip_attention": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64,

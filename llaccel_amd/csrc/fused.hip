@@ -32,19 +32,6 @@ namespace llhip {
 // ---------------------------------------------------------------------------------------
 // RMSNorm + quant prologue (golden.py:124-137, 119-120)
 // ---------------------------------------------------------------------------------------
-struct NormQuant {
-  const int16_t* x;
-  const int16_t* gamma;
-  int16_t* h_out;   // normalised rows (i16), written by workgroup 0
-  int8_t* hq_out;   // quantised rows (i8), written by workgroup 0
-  int64_t ldx;      // row stride of x and of the outputs (elements)
-  int64_t Mq;       // quant multiplier
-  uint32_t eps_t, C;
-  int sh_post, Sq, K;
-  int prequant;     // rows already normalised + quantised into h_out/hq_out
-};
-
-constexpr int NORM_MAX_K = 1024;  // a row's sum of squares takes chunks lane and lane + 64
 
 // Rows and 4-element output units of this wave.  With M < nw several waves share a row: each
 // computes the row's sum of squares (the row is 2 KiB at most) and applies the scale to its own
@@ -918,31 +905,6 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
 // ---------------------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------------------
-static int fill_pre(NormQuant& pr, const llhip_norm_quant_desc& d) {
-  if (d.K <= 0 || d.K % 16 || d.ldx < d.K || d.ldx % 8)
-    return fail(-EINVAL, "fused rmsnorm: K must be a multiple of 16 and ldx of 8");
-  if (d.K > NORM_MAX_K) return fail(-EINVAL, "fused rmsnorm: K=%lld above %d", (long long)d.K, NORM_MAX_K);
-  if (!u32_ok(d.eps_t) || !u32_ok(d.C) || !shift_ok(d.sh_post) || !u32_ok(d.Mq) || !shift_ok(d.Sq))
-    return fail(-EINVAL, "fused rmsnorm/quant parameter out of range");
-  if (d.K >= (int64_t)((1ull << 48) - (1ull << 32)) >> 30) return fail(-ERANGE, "isqrt48 input out of range");
-  if ((uintptr_t)d.x % 16 || (uintptr_t)d.gamma % 16 || (d.h_out && (uintptr_t)d.h_out % 16) ||
-      (d.hq_out && (uintptr_t)d.hq_out % 8))
-    return fail(-EINVAL, "fused rmsnorm: misaligned operands");
-  pr.x = static_cast<const int16_t*>(d.x);
-  pr.gamma = static_cast<const int16_t*>(d.gamma);
-  pr.h_out = static_cast<int16_t*>(d.h_out);
-  pr.hq_out = static_cast<int8_t*>(d.hq_out);
-  pr.ldx = d.ldx;
-  pr.Mq = d.Mq;
-  pr.eps_t = (uint32_t)d.eps_t;
-  pr.C = (uint32_t)d.C;
-  pr.sh_post = (int)d.sh_post;
-  pr.Sq = (int)d.Sq;
-  pr.K = (int)d.K;
-  pr.prequant = d.prequant ? 1 : 0;
-  if (pr.prequant && !d.hq_out) return fail(-EINVAL, "fused rmsnorm: prequant needs the quantised rows (hq_out)");
-  return 0;
-}
 
 // Waves per workgroup are capped at 8 (512 threads, 256 VGPRs per lane) unless one split
 // alone needs more (attn_in with D = 256): 16-wave workgroups leave 128 VGPRs per lane.

@@ -1154,6 +1154,80 @@ __global__ __launch_bounds__(256) void linear_splitk_finish(LinearArgs p, const 
   }
 }
 
+// The split-K sum of a resadd linear and the RMSNorm + quant of its output rows in one launch
+// (golden.py:316-342, then 124-137 + 119-120, as linear_splitk_finish followed by
+// rmsnorm_quant_kernel): one 256-thread workgroup per row, thread t finishing columns 8t..8t+7 --
+// planes summed, bias, requant, sat16, + aux, sat16 -- and writing them to the linear's output, then
+// normalising and quantising them from registers once the row's sum of squares is reduced.
+// N % 8 == 0, N <= NORM_MAX_K.
+__device__ __forceinline__ void v4_acc(v4i& a, const v4i& b) {
+  a.x += b.x;
+  a.y += b.y;
+  a.z += b.z;
+  a.w += b.w;
+}
+
+__global__ __launch_bounds__(256) void splitk_finish_norm_kernel(LinearArgs p, const int32_t* part, int splits,
+                                                                 NormQuant pr) {
+  constexpr int NCH = NORM_MAX_K / 8 / 256 + 1;
+  __shared__ uint64_t red[4];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nch = p.N >> 3;
+  const int64_t plane = (int64_t)p.M * p.N;
+  const Rsrc gr = rsrc(pr.gamma, (int64_t)p.N * 2);
+  v4i x[NCH], g[NCH];
+  uint64_t ss = 0;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = tid + 256 * i;
+    g[i] = ld16(gr, c < nch ? 16 * c : LD_OOB);
+    x[i] = v4i{0, 0, 0, 0};
+    if (c >= nch) continue;
+    const int64_t e = (int64_t)m * p.N + 8 * c;
+    v4i a0 = *reinterpret_cast<const v4i*>(part + e), a1 = *reinterpret_cast<const v4i*>(part + e + 4);
+    for (int z = 1; z < splits; ++z) {
+      const v4i b0 = *reinterpret_cast<const v4i*>(part + z * plane + e);
+      const v4i b1 = *reinterpret_cast<const v4i*>(part + z * plane + e + 4);
+      v4_acc(a0, b0);
+      v4_acc(a1, b1);
+    }
+    const int32_t acc[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    int32_t t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int n = 8 * c + j;
+      int64_t v = acc[j];
+      if (p.bias) v += p.bias[n];
+      const int64_t r = sat16(mulshift(v, (int64_t)p.rq[2 * n], p.rq[2 * n + 1]));
+      t[j] = (int32_t)sat16(r + p.aux[(int64_t)m * p.ldaux + n]);
+      ss += (uint32_t)(t[j] * t[j]);
+    }
+    x[i] = v4i{pack16(t[0], t[1]), pack16(t[2], t[3]), pack16(t[4], t[5]), pack16(t[6], t[7])};
+    *reinterpret_cast<v4i*>(static_cast<int16_t*>(p.out) + (int64_t)m * p.ldo + 8 * c) = x[i];
+  }
+  ss = wave_sum_u64(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  const uint32_t inv = rms_inv(red[0] + red[1] + red[2] + red[3], pr.eps_t, pr.C);
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = tid + 256 * i;
+    if (c >= nch) break;
+    v4i y;
+    uint32_t qw[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int16_t y0 = rms_apply(lo16(x[i][j]), lo16(g[i][j]), inv, pr.sh_post);
+      const int16_t y1 = rms_apply(hi16(x[i][j]), hi16(g[i][j]), inv, pr.sh_post);
+      y[j] = pack16(y0, y1);
+      const uint32_t q0 = (uint8_t)sat8(mulshift(y0, pr.Mq, pr.Sq));
+      const uint32_t q1 = (uint8_t)sat8(mulshift(y1, pr.Mq, pr.Sq));
+      qw[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
+    }
+    if (pr.h_out) *reinterpret_cast<v4i*>(pr.h_out + (int64_t)m * pr.ldx + 8 * c) = y;
+    if (pr.hq_out) *reinterpret_cast<v2i*>(pr.hq_out + (int64_t)m * pr.K + 8 * c) = v2i{(int)qw[0], (int)qw[1]};
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------------------
@@ -1180,8 +1254,11 @@ static void launch_mfma_kernel(LinearArgs& p, int mblocks, int nblocks, int spli
                      p, mblocks, nblocks, kps, part, persist ? 1 : 0);
 }
 
+// With norm (a resadd linear whose output rows are normalised and quantised next): a split-K
+// launch finishes its planes with splitk_finish_norm_kernel and sets *norm_done.
 template <int EPI, bool OUT8, int GM, int GN, int NW, int KT>
-static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
+static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream, const NormQuant* norm = nullptr,
+                       bool* norm_done = nullptr) {
   const int mblocks = (int)ceil_div(p.M, GM), nblocks = (int)ceil_div(p.N, GN);
   const int64_t tiles = (int64_t)mblocks * nblocks;
   const int k64 = (int)(p.K / 64), ktiles = (int)(p.K / KT);
@@ -1213,6 +1290,14 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
   }
   LLHIP_LAUNCH_CHECK();
   if (part) {
+    if constexpr (EPI == EPI_RESADD && !OUT8) {
+      if (norm && p.N % 8 == 0 && p.N <= NORM_MAX_K) {
+        hipLaunchKernelGGL(splitk_finish_norm_kernel, dim3((unsigned)p.M), dim3(256), 0, stream, p, part, splits, *norm);
+        LLHIP_LAUNCH_CHECK();
+        *norm_done = true;
+        return 0;
+      }
+    }
     const int64_t quads = (int64_t)p.M * p.N / 4;
     hipLaunchKernelGGL((linear_splitk_finish<EPI, OUT8>), dim3((unsigned)std::min<int64_t>(ceil_div(quads, 256), 8 * cus)),
                        dim3(256), 0, stream, p, part, splits);
@@ -1223,7 +1308,7 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream) {
 
 // The MFMA tile shape for a prompt-sized linear, over K tiles of KT bytes
 template <int EPI, bool OUT8, int KT>
-static int launch_mfma_shape(LinearArgs& p, void* ws, hipStream_t stream) {
+static int launch_mfma_shape(LinearArgs& p, void* ws, hipStream_t stream, const NormQuant* norm, bool* norm_done) {
   // 256x256 tiles when M fills them and they fill every CU.  The 256x256 kernel keeps 128
   // accumulators per lane at two waves per SIMD; the aux-reading epilogues would spill there.
   if constexpr (EPI == EPI_NONE) {
@@ -1233,16 +1318,17 @@ static int launch_mfma_shape(LinearArgs& p, void* ws, hipStream_t stream) {
   // 128x128 tiles while they fill the CUs, else 64x128 tiles (twice as many workgroups, three per
   // CU), split along K when even those are too few
   if ((int64_t)ceil_div(p.M, 128) * ceil_div(p.N, 128) >= current_cu_count())
-    return launch_mfma<EPI, OUT8, 128, 128, 4, KT>(p, ws, stream);
-  return launch_mfma<EPI, OUT8, 64, 128, 4, KT>(p, ws, stream);
+    return launch_mfma<EPI, OUT8, 128, 128, 4, KT>(p, ws, stream, norm, norm_done);
+  return launch_mfma<EPI, OUT8, 64, 128, 4, KT>(p, ws, stream, norm, norm_done);
 }
 
 template <int EPI, bool OUT8>
-static int launch_linear(LinearArgs& p, void* ws, hipStream_t stream) {
+static int launch_linear(LinearArgs& p, void* ws, hipStream_t stream, const NormQuant* norm = nullptr,
+                         bool* norm_done = nullptr) {
   const bool aligned = (p.K % 16 == 0) && (p.lda % 16 == 0) && ((uintptr_t)p.A % 16 == 0) && ((uintptr_t)p.W % 16 == 0);
   if (p.M >= 128 && p.K % 64 == 0 && aligned) {
-    if (p.K % 128 == 0) return launch_mfma_shape<EPI, OUT8, 128>(p, ws, stream);
-    return launch_mfma_shape<EPI, OUT8, 64>(p, ws, stream);
+    if (p.K % 128 == 0) return launch_mfma_shape<EPI, OUT8, 128>(p, ws, stream, norm, norm_done);
+    return launch_mfma_shape<EPI, OUT8, 64>(p, ws, stream, norm, norm_done);
   }
   if (p.M > 16 && aligned) {
     // 128x256 block tiles when they still fill the chip, else 128x128
@@ -1359,12 +1445,13 @@ __global__ void exact_matmul_kernel(const int64_t* A, int64_t M, int64_t K, cons
 
 using namespace llhip;
 
-extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_t* W, int64_t N,
-                            const int32_t* rq, const int32_t* bias, int epilogue, const int16_t* aux, int64_t ldaux,
-                            int64_t aux_shift, int64_t silu_Mi, int64_t silu_Si, int64_t silu_sh, int out_i8,
-                            void* out, int64_t ldo, void* ws, void* stream) {
+// llhip_linear's checks and kernel arguments (rc 1: nothing to compute)
+static int linear_args(LinearArgs& p, const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_t* W, int64_t N,
+                       const int32_t* rq, const int32_t* bias, int epilogue, const int16_t* aux, int64_t ldaux,
+                       int64_t aux_shift, int64_t silu_Mi, int64_t silu_Si, int64_t silu_sh, int out_i8, void* out,
+                       int64_t ldo) {
   if (M < 0 || N < 0 || K < 0) return fail(-EINVAL, "linear: negative shape");
-  if (M == 0 || N == 0) return 0;
+  if (M == 0 || N == 0) return 1;
   if (K > 65535) return fail(-EINVAL, "linear: K=%lld exceeds the int32 accumulator bound 65535", (long long)K);
   if (M > INT32_MAX || N > INT32_MAX) return fail(-EINVAL, "linear: shape too large");
   if (lda < K || ldo < N) return fail(-EINVAL, "linear: leading dimension too small");
@@ -1377,7 +1464,6 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
   if (epilogue == EPI_SILU && (!shift_ok(silu_Si) || !shift_ok(silu_sh)))
     return fail(-EINVAL, "linear: silu shift out of [0,63]");
   if (epilogue == EPI_SILU && !u32_ok(silu_Mi)) return fail(-EINVAL, "linear: silu Mi must be u32");
-  LinearArgs p{};
   p.A = A;
   p.W = W;
   p.rq = rq;
@@ -1396,6 +1482,17 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
   p.sh = (int)silu_sh;
   p.steps = (int)ceil_div(K, 64);
   if (p.steps == 0) p.steps = 1;
+  return 0;
+}
+
+extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_t* W, int64_t N,
+                            const int32_t* rq, const int32_t* bias, int epilogue, const int16_t* aux, int64_t ldaux,
+                            int64_t aux_shift, int64_t silu_Mi, int64_t silu_Si, int64_t silu_sh, int out_i8,
+                            void* out, int64_t ldo, void* ws, void* stream) {
+  LinearArgs p{};
+  const int rc = linear_args(p, A, M, K, lda, W, N, rq, bias, epilogue, aux, ldaux, aux_shift, silu_Mi, silu_Si, silu_sh,
+                             out_i8, out, ldo);
+  if (rc) return rc < 0 ? rc : 0;
   hipStream_t s = (hipStream_t)stream;
   if (out_i8) return launch_linear<EPI_NONE, true>(p, ws, s);
   switch (epilogue) {
@@ -1404,6 +1501,24 @@ extern "C" int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, 
     case EPI_MUL: return launch_linear<EPI_MUL, false>(p, ws, s);
     default: return launch_linear<EPI_NONE, false>(p, ws, s);
   }
+}
+
+extern "C" int llhip_linear_norm(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_t* W, int64_t N,
+                                 const int32_t* rq, const int32_t* bias, const int16_t* aux, int64_t ldaux, int16_t* out,
+                                 int64_t ldo, const llhip_norm_quant_desc* norm, void* ws, void* stream) {
+  if (!norm) return fail(-EINVAL, "linear_norm: null descriptor");
+  NormQuant pr{};
+  int rc = fill_pre(pr, *norm);
+  if (rc) return rc;
+  if (norm->prequant || norm->x != out || norm->ldx != ldo || norm->K != N || (!norm->h_out && !norm->hq_out))
+    return fail(-EINVAL, "linear_norm: the norm must read the linear's output rows [M][N] and write a result");
+  LinearArgs p{};
+  rc = linear_args(p, A, M, K, lda, W, N, rq, bias, EPI_RESADD, aux, ldaux, 0, 0, 0, 0, 0, out, ldo);
+  if (rc) return rc < 0 ? rc : 0;
+  bool done = false;
+  rc = launch_linear<EPI_RESADD, false>(p, ws, (hipStream_t)stream, &pr, &done);
+  if (rc || done) return rc;
+  return llhip_rmsnorm_quant(norm, M, stream);
 }
 
 extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {

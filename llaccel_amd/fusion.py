@@ -38,10 +38,20 @@ class FusedStep:
         self.entry, self.desc = entry, desc_cls()
         self.K, self.bytes_fn, self.name, self.ops = K, bytes_fn, name, ops
         self.wide = wide_steps(model, ops, fallback)
+        self.lead = None  # a _LinearNormStep for the preceding resadd linear (see _pair_linear_norm)
+
+    def takes_wide(self, M):
+        return M > 16 or M * (self.K + 16) > LDS_LIMIT or self.K > NORM_MAX_K
 
     def __call__(self, M, pos, pd=None):
-        if M > 16 or M * (self.K + 16) > LDS_LIMIT or self.K > NORM_MAX_K:
-            for st in self.wide:
+        if self.takes_wide(M):
+            if self.lead is not None:
+                # the preceding linear deferred itself: it runs here with this run's leading rmsnorm + quant
+                self.lead(M, pos, pd)
+                rest = self.wide[1:]
+            else:
+                rest = self.wide
+            for st in rest:
                 st(M, pos, pd)
             return
         self.fill(self.desc, M, pos, pd)
@@ -100,6 +110,39 @@ class _RopeQuantStep:
             self._fill(d, ro, qu, kvw, M, pos, pd)
         _lib.call("llhip_rope_quant2", ctypes.byref(self.desc[0]), ctypes.byref(self.desc[1]),
                   self.model._stream_handle())
+
+
+class _LinearNormStep:
+    """A resadd linear (i16 out) and the rmsnorm -> quant of its output rows in one
+    llhip_linear_norm call (one finishing launch for both when the linear is split along K)."""
+
+    def __init__(self, model, lin, rn, qu):
+        self.model, self.lin = model, lin
+        self.norm = _NormQuantStep(model, rn, qu)
+
+    def __call__(self, M, pos, pd=None):
+        m, o = self.model, self.lin
+        _pre(m, self.norm.desc, self.norm.rn, self.norm.qu)
+        self.norm.desc.prequant = 0
+        N, K = int(o["N"]), int(o["K"])
+        out, aux = m._buf(o["out"]), m._buf(o["aux"])
+        _lib.call("llhip_linear_norm", _vp(m._buf(o["in"])), M, K, K, _vp(m._dt[o["w"]]), N, _vp(m._dt[o["rq"]]),
+                  _vp(m._dt[o["bias"]]) if o.get("bias") else None, _vp(aux), aux.shape[1], _vp(out), out.shape[1],
+                  ctypes.byref(self.norm.desc), _vp(m._ws), m._stream_handle())
+
+
+class _DeferredLinear:
+    """The plan's step for a resadd linear whose output the next fused run normalises first: for the
+    rows that run takes on its wide path, the run makes the linear's call itself (its `lead`,
+    one llhip_linear_norm call), so this step does nothing; otherwise it is the linear's own step."""
+
+    def __init__(self, step, fused):
+        self.step, self.fused = step, fused
+        self.kind, self.bytes_fn, self.name = step.kind, step.bytes_fn, step.name
+
+    def __call__(self, M, pos, pd=None):
+        if not self.fused.takes_wide(M):
+            self.step(M, pos, pd)
 
 
 class _GroupLinearStep:
@@ -163,7 +206,7 @@ def _gate_up(model, ops, i):
 
 def wide_steps(model, ops, steps):
     """Launches of a fused run for more rows than its fused kernel takes (prompt chunks): the run's
-    per-op steps, with each rmsnorm + quant of its output as one launch, three linears of one input
+    per-op steps, with each rmsnorm + quant as one launch, three linears of one input
     (q, k, v) as one grouped launch, the gate and up linears and the quant of their product as
     one launch, and attn_in's group rope q, rope k, quant q, quant k, kv_write as one.  The
     arithmetic of every op is unchanged."""
@@ -437,7 +480,7 @@ MATCHERS = (match_attn_in, match_mlp_in, match_norm_linear)
 
 def fuse(model, ops, steps):
     """New plan: matched runs of `ops` (steps[i] is op i's per-op step) become FusedSteps."""
-    out = []
+    out, src = [], []  # src[j]: the op index of a per-op step, None for a fused run
     i = 0
     while i < len(ops):
         if i >= len(steps):
@@ -453,10 +496,35 @@ def fuse(model, ops, steps):
                 break
         if got is None:
             out.append(steps[i])
+            src.append(i)
             i += 1
         else:
             n, st = got
             out.append(st)
+            src.append(None)
             i += n
+    _pair_linear_norm(model, ops, out, src)
     out.extend(steps[len(ops):])
     return out
+
+
+def _pair_linear_norm(model, ops, out, src):
+    """A resadd linear (i16 out) followed by a fused run that starts with rmsnorm -> quant of the
+    linear's output (o_proj before the MLP run, down before the next layer's attention run or the
+    head): on the run's wide path the two become one llhip_linear_norm call, which finishes a
+    split-K linear and normalises its rows in one launch."""
+    for j in range(len(out) - 1):
+        f = out[j + 1]
+        if src[j] is None or getattr(out[j], "kind", "") != "linear" or not isinstance(f, FusedStep):
+            continue
+        if not f.wide or not isinstance(f.wide[0], _NormQuantStep):
+            continue
+        a, nq = ops[src[j]], f.wide[0]
+        if not (_is(a, "linear") and (a.get("epilogue") or "none") == "resadd" and a.get("out_dtype", "i16") == "i16"
+                and nq.rn is f.ops[0] and nq.rn["in"] == a["out"] and int(a["K"]) % 16 == 0):
+            continue
+        K = int(model._dt[nq.rn["gamma"]].shape[0])
+        if K != int(a["N"]) or K % 16 or K > NORM_MAX_K:
+            continue
+        f.lead = _LinearNormStep(model, a, nq.rn, nq.qu)
+        out[j] = _DeferredLinear(out[j], f)

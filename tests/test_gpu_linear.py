@@ -232,3 +232,41 @@ def test_gate_up_equals_the_three_ops(M, K, N, pad, par):
         assert np.array_equal(g_[:, :N], w_) and not g_[:, N:].any()
     if par == 0:
         assert np.count_nonzero(f) > f.size // 2  # the products are not degenerate
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 4864, 896), (300, 2048, 576), (300, 896, 896), (40, 896, 896)])
+def test_linear_norm_equals_linear_then_rmsnorm_quant(M, K, N):
+    """llhip_linear_norm (a resadd linear, then rmsnorm + quant of its output rows) equals the resadd
+    linear checked against the oracle followed by the oracle's rmsnorm and quant: with the split-K
+    finishing kernel (512 x 4864 x 896, 300 x 2048 x 576) and with the separate launches (unsplit
+    300 x 896 x 896, the 40-row GEMV path)."""
+    import math
+
+    from llaccel_amd import _lib
+    from tests.gpu_helpers import down, ptr, stream, torch, up, workspace
+
+    t = torch()
+    rng = np.random.default_rng(M + K + N)
+    a, w, rq = _operands(rng, M, K, N, out_i8=False)
+    bias = rng.integers(-(1 << 20), 1 << 20, N)
+    aux = rng.integers(-20000, 20000, (M, N))
+    g = rng.integers(-32768, 32768, N)
+    eps_t, C, sh, qM, qS = 12345, int(2**24 * math.sqrt(N)), 24, 1234567891, 38
+    ad, wd, rqd, bd, auxd, gd = up(a, np.int8), up(w, np.int8), up(rq, np.int32), up(bias, np.int32), up(aux, np.int16), \
+        up(g, np.int16)
+    xd = t.zeros((M, N), dtype=t.int16, device="cuda")
+    hd = t.zeros((M, N), dtype=t.int16, device="cuda")
+    hqd = t.zeros((M, N), dtype=t.int8, device="cuda")
+    d = _lib.NormQuantDesc()
+    d.x, d.gamma, d.h_out, d.hq_out, d.ldx, d.K = ptr(xd), ptr(gd), ptr(hd), ptr(hqd), N, N
+    d.eps_t, d.C, d.sh_post, d.Mq, d.Sq, d.prequant = eps_t, C, sh, qM, qS, 0
+    _lib.call("llhip_linear_norm", ptr(ad), M, K, K, ptr(wd), N, ptr(rqd), ptr(bd), ptr(auxd), N, ptr(xd), N,
+              ctypes.byref(d), ptr(workspace()), stream())
+    x_want = O.linear_c(a, w, rq, bias, False, "resadd", aux, 0, None)
+    assert np.array_equal(down(xd), x_want)
+    h_want = O.rmsnorm(x_want, g, eps_t, C, sh)
+    assert np.array_equal(down(hd), h_want) and np.array_equal(down(hqd), O.vquant(h_want, qM, qS))
+    d.x = ptr(hd)  # the norm must read the linear's output
+    with pytest.raises(ValueError):
+        _lib.call("llhip_linear_norm", ptr(ad), M, K, K, ptr(wd), N, ptr(rqd), ptr(bd), ptr(auxd), N, ptr(xd), N,
+                  ctypes.byref(d), ptr(workspace()), stream())

@@ -107,6 +107,12 @@ def test_smol_shape_prefill_decode(tmp_path, fusion):
     prompt = synth.seeded_prompt("smol", 20, 1)
     g = G.GoldenModel(qdir)
     o = O.OracleModel(qdir, backend="c")
+    # resadd o_proj and down (the fused graph's; the unfused graph adds separately) each pair with
+    # the rmsnorm + quant that opens the next fused run, which the prompt launch takes on its wide
+    # path (one llhip_linear_norm call per pair)
+    from llaccel_amd import fusion as F
+
+    assert sum(isinstance(s, F._DeferredLinear) for s in g._plan) == (2 * 30 if fusion else 0)
     assert g.generate(prompt, 4) == o.generate(prompt, 4)
     for layer in (0, 17, 29):
         assert np.array_equal(g.kv[layer][0], o.kv[layer][0]) and np.array_equal(g.kv[layer][1], o.kv[layer][1])
