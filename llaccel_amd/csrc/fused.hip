@@ -223,28 +223,38 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(NormQuant pr) {
   }
 }
 
-// SIG table (258 u16 = 129 dwords) staged into LDS by wave 0: three dword loads per lane at
-// kernel entry, stored once the prologue waits anyway
+// SIG table (258 u16 = 129 dwords) staged into LDS by one wave (threads first..first+63, wave 0
+// by default): three dword loads per lane at kernel entry, stored once the prologue waits anyway
 struct SigRegs {
   uint32_t w[3];
 };
 
-__device__ __forceinline__ void sig_prefetch(SigRegs& r) {
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void sig_prefetch(SigRegs& r, int first = 0) {
+  const int t = (int)threadIdx.x - first;
   const Rsrc sr = rsrc(kSig, sizeof(kSig));
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    const int idx = tid + 64 * i;
-    r.w[i] = (uint32_t)ld4(sr, (tid < 64 && idx < 129) ? 4 * idx : LD_OOB);
+    const int idx = t + 64 * i;
+    r.w[i] = (uint32_t)ld4(sr, (t >= 0 && t < 64 && idx < 129) ? 4 * idx : LD_OOB);
   }
 }
 
-__device__ __forceinline__ void sig_store(const SigRegs& r, uint32_t* sig32) {
-  const int tid = threadIdx.x;
-  if (tid < 64) {
+// sig_store into a 192-dword array: every lane stores its three dwords (zeros past the table), so
+// no load is used under a condition (the compiler would move it there, behind a wait)
+__device__ __forceinline__ void sig_store192(const SigRegs& r, uint32_t* sig32, int first) {
+  const int t = (int)threadIdx.x - first;
+  if (t >= 0 && t < 64) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) sig32[t + 64 * i] = r.w[i];
+  }
+}
+
+__device__ __forceinline__ void sig_store(const SigRegs& r, uint32_t* sig32, int first = 0) {
+  const int t = (int)threadIdx.x - first;
+  if (t >= 0 && t < 64) {
 #pragma unroll
     for (int i = 0; i < 3; ++i)
-      if (tid + 64 * i < 129) sig32[tid + 64 * i] = r.w[i];
+      if (t + 64 * i < 129) sig32[t + 64 * i] = r.w[i];
   }
 }
 
@@ -298,13 +308,13 @@ __device__ __forceinline__ void resid_prefetch(const NormQuant& pr, const ResidA
   r.g = ld8(rsrc(pr.gamma, (int64_t)K * 2), in ? 8u * u : LD_OOB);
 }
 
-// x, RMSNorm, quant of the row into a_lds (i8); workgroup 0 writes x (when finishing), h_out and
-// hq_out.  red64 is LDS for one u64 per wave.  Ends with a barrier.
-__device__ __forceinline__ void resid_norm_quant(const NormQuant& pr, const ResidArgs& ra, const ResidRegs& r,
-                                                 int8_t* a_lds, bool write_global, uint64_t* red64) {
-  const int u = threadIdx.x, lane = u & 63, wave = u >> 6, nw = blockDim.x >> 6;
-  const bool in = u < (pr.K >> 2);
-  int32_t xv[4] = {lo16(r.x.x), hi16(r.x.x), lo16(r.x.y), hi16(r.x.y)};
+// thread u's four values of the row x (finished from the partial sums, or as read) and their sum of
+// squares
+__device__ __forceinline__ uint64_t resid_row(const ResidArgs& ra, const ResidRegs& r, int32_t xv[4]) {
+  xv[0] = lo16(r.x.x);
+  xv[1] = hi16(r.x.x);
+  xv[2] = lo16(r.x.y);
+  xv[3] = hi16(r.x.y);
   if (ra.acc) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -319,38 +329,53 @@ __device__ __forceinline__ void resid_norm_quant(const NormQuant& pr, const Resi
   uint64_t ss = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) ss += (uint64_t)(uint32_t)(xv[j] * xv[j]);
-  ss = wave_sum_u64(ss);
+  return ss;
+}
+
+// RMSNorm (reciprocal inv) and quant of thread u's four values into a_lds (i8); workgroup 0 writes
+// x (when finishing), h_out and hq_out
+__device__ __forceinline__ void resid_apply(const NormQuant& pr, const ResidArgs& ra, const ResidRegs& r,
+                                            const int32_t xv[4], uint32_t inv, int8_t* a_lds, bool write_global) {
+  const int u = threadIdx.x;
+  if (u >= (pr.K >> 2)) return;
+  const int32_t g[4] = {lo16(r.g.x), hi16(r.g.x), lo16(r.g.y), hi16(r.g.y)};
+  int16_t y[4];
+  uint32_t q = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    y[j] = rms_apply(xv[j], g[j], inv, pr.sh_post);
+    q |= (uint32_t)(uint8_t)sat8(mulshift(y[j], pr.Mq, pr.Sq)) << (8 * j);
+  }
+  *reinterpret_cast<uint32_t*>(a_lds + 4 * u) = q;
+  if (write_global) {
+    if (ra.acc && ra.x_out) {
+      v2i xo;
+      xo.x = pack16(xv[0], xv[1]);
+      xo.y = pack16(xv[2], xv[3]);
+      *reinterpret_cast<v2i*>(ra.x_out + 4 * u) = xo;
+    }
+    if (pr.h_out) {
+      v2i yo;
+      yo.x = pack16(y[0], y[1]);
+      yo.y = pack16(y[2], y[3]);
+      *reinterpret_cast<v2i*>(pr.h_out + 4 * u) = yo;
+    }
+    if (pr.hq_out) *reinterpret_cast<uint32_t*>(pr.hq_out + 4 * u) = q;
+  }
+}
+
+// x, RMSNorm, quant of the row into a_lds (i8); workgroup 0 writes x (when finishing), h_out and
+// hq_out.  red64 is LDS for one u64 per wave.  Ends with a barrier.
+__device__ __forceinline__ void resid_norm_quant(const NormQuant& pr, const ResidArgs& ra, const ResidRegs& r,
+                                                 int8_t* a_lds, bool write_global, uint64_t* red64) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int32_t xv[4];
+  uint64_t ss = wave_sum_u64(resid_row(ra, r, xv));
   if (lane == 0) red64[wave] = ss;
   __syncthreads();
   uint64_t tot = 0;
   for (int w = 0; w < nw; ++w) tot += red64[w];
-  const uint32_t inv = rms_inv(tot, pr.eps_t, pr.C);
-  if (in) {
-    const int32_t g[4] = {lo16(r.g.x), hi16(r.g.x), lo16(r.g.y), hi16(r.g.y)};
-    int16_t y[4];
-    uint32_t q = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      y[j] = rms_apply(xv[j], g[j], inv, pr.sh_post);
-      q |= (uint32_t)(uint8_t)sat8(mulshift(y[j], pr.Mq, pr.Sq)) << (8 * j);
-    }
-    *reinterpret_cast<uint32_t*>(a_lds + 4 * u) = q;
-    if (write_global) {
-      if (ra.acc && ra.x_out) {
-        v2i xo;
-        xo.x = pack16(xv[0], xv[1]);
-        xo.y = pack16(xv[2], xv[3]);
-        *reinterpret_cast<v2i*>(ra.x_out + 4 * u) = xo;
-      }
-      if (pr.h_out) {
-        v2i yo;
-        yo.x = pack16(y[0], y[1]);
-        yo.y = pack16(y[2], y[3]);
-        *reinterpret_cast<v2i*>(pr.h_out + 4 * u) = yo;
-      }
-      if (pr.hq_out) *reinterpret_cast<uint32_t*>(pr.hq_out + 4 * u) = q;
-    }
-  }
+  resid_apply(pr, ra, r, xv, rms_inv(tot, pr.eps_t, pr.C), a_lds, write_global);
   __syncthreads();
 }
 
@@ -664,6 +689,9 @@ struct MlpInArgs {
   const int8_t* wdp;
   int32_t* wd_acc;
   int wd_R, wd_N;
+  // dec_mlp_kernel's column assignment: workgroup b < W owns FFN tile b (columns 16b..16b+15) and
+  // at most one tail group of tail_gw columns of the tiles W.. (see dec_tail_group)
+  int tail_tiles, tail_gw;
 };
 
 constexpr int WD_PF = 4;  // down-projection panel columns per thread loaded at kernel entry
@@ -779,6 +807,185 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   const int8_t* panel = p.wdp + (int64_t)blockIdx.x * p.wd_N * 16;
   for (int c = tid + WD_PF * (int)blockDim.x; c < p.wd_N; c += blockDim.x) {
     const int32_t d = dot16(*reinterpret_cast<const v4i*>(panel + 16 * (int64_t)c));
+    if (d != 0) atomic_add_dev(acc + c, d);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// dec_mlp (decode chain, one row): mlp_in over the FFN columns, then the down projection's partial
+// sums of those columns.  The work of a workgroup is split over two sets of waves.  Waves 0-3 (the
+// norm waves) finish the output projection's row from its partial sums, normalise and quantise it
+// into LDS; waves 4-7 (the weight waves) stream the gate (waves 4, 5: the two K halves) and up
+// (6, 7) weights and the down-projection panel.  A wave that issues a long run of loads cannot
+// pass a workgroup barrier before the last one is issued, so the norm waves meet through an LDS
+// counter instead.  Then the weight waves' MFMAs, wave 0's requant / SiLU / mul / quant epilogue,
+// and the weight waves' down-projection partial sums (the accumulator layout of the mlp_in decode
+// form: workgroup b adds into row b % R).
+// Columns: with more 16-column tiles than CUs, one tile per workgroup would put two workgroups on
+// some CUs and the launch would last twice as long there.  So the grid is W = #CUs workgroups,
+// workgroup b owns tile b, and the tiles past W are cut into groups of gw = 4, 8 or 16 columns
+// (bytes 4i.. of a panel row) handed to one workgroup each.  The groups of one tile go to
+// workgroups of one XCD (workgroup b runs on XCD b % 8), which then read each panel line once
+// through their shared L2.
+// ---------------------------------------------------------------------------------------
+constexpr int DM_THREADS = 512;  // 4 norm waves + 4 weight waves
+
+// waves [0, n) meet without the others: each adds one to *cnt (zeroed before the workgroup's first
+// barrier, and only these waves add to it) and waits until all n have.  Only LDS is ordered (the
+// LDS performs one wave's operations in issue order): a release/acquire pair would also wait for
+// every global load in flight, which is what the meeting must not do.
+__device__ __forceinline__ void wave_group_meet(int* cnt, int n) {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes before the add
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < n) __builtin_amdgcn_s_sleep(1);
+  __asm__ volatile("" ::: "memory");  // LDS reads of the others' values stay after the wait
+}
+
+// the tail group of workgroup b: its first column (or -1: none).  Tile u of the tail (u < tiles)
+// has 16 / gw groups i, held by workgroup (u % 8) + 8 * ((u / 8) * (16 / gw) + i).
+__host__ __device__ __forceinline__ int dec_tail_group(int b, int W, int tiles, int gw) {
+  if (tiles <= 0) return -1;
+  const int per = 16 / gw, x = b % 8, slot = b / 8;
+  const int u = (slot / per) * 8 + x, i = slot % per;
+  return u < tiles ? 16 * (W + u) + gw * i : -1;
+}
+
+template <int GW>
+__global__ __launch_bounds__(DM_THREADS) void dec_mlp_kernel(MlpInArgs p) {
+  kernarg_warm<sizeof(MlpInArgs)>();
+  extern __shared__ __attribute__((aligned(16))) int8_t dyn[];  // the quantised row
+  __shared__ v4i red[2][4][64];  // [main, tail][weight wave] MFMA tiles
+  __shared__ uint32_t sig32[192];
+  __shared__ uint64_t red64[4];
+  __shared__ int meet;
+  __shared__ __attribute__((aligned(16))) int8_t fq16[2][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int col = lane & 15, kg = lane >> 4;
+  const int W = (int)gridDim.x, gw = GW;
+  const int t0 = dec_tail_group((int)blockIdx.x, W, p.tail_tiles, GW);  // first tail column, or -1
+  if (tid == 0) meet = 0;
+  __syncthreads();  // no load has been issued yet: every wave is here at once
+
+  WSlice ws[2];
+  Rsrc wr;
+  v4i wdv[WD_PF];     // weight waves: their first panel rows of the main tile
+  v4i wdt[WD_PF];     // ... and the tail group's bytes of the tail tile's rows
+  v2i rq{0, 0};       // wave 0: the epilogue's requant pair and bias for gate (g) and up (u)
+  v2i rqu{0, 0};
+  int32_t bgv = 0, buv = 0;
+  // wave 0's epilogue lanes: kg 0 = the main tile's column col, kg 1 = the tail group's column col
+  const int en = kg == 0 ? (int)blockIdx.x * 16 + col : (kg == 1 && t0 >= 0 && col < gw ? t0 + col : p.N);
+  // Load order matters: a wave's loads complete in issue order, so whatever a wave issues before
+  // (or, through a branch the wait counts cannot see past, beside) the loads it needs first is
+  // waited for too.  The norm waves issue their row operands, then wave 0's epilogue operands
+  // (the other norm waves issue the same loads out of range, so every norm wave has the same
+  // count in flight); the SIG table is the last load of wave 4.
+  if (wave < 4) {
+    ResidRegs rr;
+    resid_prefetch(p.pre, p.res, rr);
+    issue_fence();
+    {
+      const bool mine = wave == 0 && en < p.N;
+      const uint32_t o8 = mine ? 8 * en : LD_OOB, o4 = mine ? 4 * en : LD_OOB;
+      rq = ld8(rsrc(p.rqg, (int64_t)p.N * 8), o8);
+      rqu = ld8(rsrc(p.rqu, (int64_t)p.N * 8), o8);
+      bgv = ld4(rsrc(p.bg, (int64_t)p.N * 4), o4);
+      buv = ld4(rsrc(p.bu, (int64_t)p.N * 4), o4);
+    }
+    issue_fence();
+    int32_t xv[4];
+    const uint64_t ss = wave_sum_u64(resid_row(p.res, rr, xv));
+    if (lane == 0) red64[wave] = ss;
+    wave_group_meet(&meet, 4);
+    const uint32_t inv = rms_inv(red64[0] + red64[1] + red64[2] + red64[3], p.pre.eps_t, p.pre.C);
+    resid_apply(p.pre, p.res, rr, xv, inv, dyn, blockIdx.x == 0);
+  } else {
+    const int wi = wave - 4;
+    wr = rsrc(wi >= 2 ? p.Wu : p.Wg, (int64_t)p.N * p.K);
+    int s0, s1;
+    split_range((p.K + 63) >> 6, 2, wi & 1, s0, s1);
+    wslice_prefetch(ws[0], wr, (int)blockIdx.x * 16 + col, p.K, kg, s0, s1);
+    // tail lanes past the group read zeros (row N is past the weights)
+    wslice_prefetch(ws[1], wr, t0 >= 0 && col < gw ? t0 + col : p.N, p.K, kg, t0 >= 0 ? s0 : s1, s1);
+    issue_fence();
+    const int64_t rows = (int64_t)((p.N + 15) / 16) * p.wd_N * 16;
+    const Rsrc dr = rsrc(p.wdp, rows);
+    const int64_t tbase = t0 >= 0 ? (int64_t)(t0 >> 4) * p.wd_N * 16 + (t0 & 15) : 0;
+#pragma unroll
+    for (int i = 0; i < WD_PF; ++i) {
+      const int c = tid - 256 + 256 * i;
+      const bool in = c < p.wd_N;
+      wdv[i] = ld16(dr, in ? (uint32_t)(((int64_t)blockIdx.x * p.wd_N + c) * 16) : LD_OOB);
+      const uint32_t to = (in && t0 >= 0) ? (uint32_t)(tbase + 16 * (int64_t)c) : LD_OOB;
+      if constexpr (GW == 16) {
+        wdt[i] = ld16(dr, to);
+      } else if constexpr (GW == 8) {
+        const v2i w2 = ld8(dr, to);
+        wdt[i] = v4i{w2.x, w2.y, 0, 0};
+      } else {
+        wdt[i] = v4i{ld4(dr, to), 0, 0, 0};
+      }
+    }
+    issue_fence();
+    SigRegs sr;
+    sig_prefetch(sr, 256);
+    issue_fence();
+    sig_store192(sr, sig32, 256);
+  }
+  __syncthreads();
+  if (wave >= 4) {
+    red[0][wave - 4][lane] = wslice_mfma(ws[0], wr, dyn, p.K + 16, 1, p.K);
+    if (t0 >= 0) red[1][wave - 4][lane] = wslice_mfma(ws[1], wr, dyn, p.K + 16, 1, p.K);
+  }
+  __syncthreads();
+  if (wave == 0 && kg < 2) {
+    // the requant operands are used from here on: the compiler may not widen them (and wait for
+    // their loads, which queue behind the weights) while the norm waves still need wave 0
+    asm volatile("" : "+v"(rq), "+v"(rqu), "+v"(bgv), "+v"(buv));
+    const int tl = kg;  // 0: main, 1: tail
+    const v4i a0 = red[tl][0][col], a1 = red[tl][1][col], u0 = red[tl][2][col], u1 = red[tl][3][col];
+    int8_t fq = 0;
+    if (en < p.N) {
+      const uint16_t* sig = reinterpret_cast<const uint16_t*>(sig32);
+      const int64_t tg = sat16(mulshift((int64_t)(a0.x + a1.x) + bgv, rq.x, rq.y));
+      const int64_t tu = sat16(mulshift((int64_t)(u0.x + u1.x) + buv, rqu.x, rqu.y));
+      if (p.g_out) p.g_out[en] = (int16_t)tg;
+      if (p.u_out) p.u_out[en] = (int16_t)tu;
+      const int64_t sg = silu16_lds(tg, p.silu_Mi, p.silu_Si, p.silu_sh, sig);
+      const int64_t f = sat16(rshr(tu * sg, p.mul_sh));
+      p.sg_out[en] = (int16_t)sg;
+      p.f_out[en] = (int16_t)f;
+      fq = (int8_t)sat8(mulshift(f, p.fq_M, p.fq_S));
+      p.fq_out[en] = fq;
+    }
+    fq16[tl][col] = fq;  // columns past N or past the group contribute nothing
+  }
+  __syncthreads();
+  if (wave < 4) return;
+  // down projection: the quantised FFN values of this workgroup's columns against every output column
+  const v4i f4 = *reinterpret_cast<const v4i*>(fq16[0]);
+  const v4i ft = *reinterpret_cast<const v4i*>(fq16[1]);
+  int32_t* acc = p.wd_acc + (int64_t)(blockIdx.x % p.wd_R) * p.wd_N;
+  auto dot16 = [](const v4i& f, const v4i& w, int32_t d) {
+    d = __builtin_amdgcn_sdot4(f.x, w.x, d, false);
+    d = __builtin_amdgcn_sdot4(f.y, w.y, d, false);
+    d = __builtin_amdgcn_sdot4(f.z, w.z, d, false);
+    return __builtin_amdgcn_sdot4(f.w, w.w, d, false);
+  };
+#pragma unroll
+  for (int i = 0; i < WD_PF; ++i) {
+    const int c = tid - 256 + 256 * i;
+    const int32_t d = dot16(ft, wdt[i], dot16(f4, wdv[i], 0));
+    if (c < p.wd_N && d != 0) atomic_add_dev(acc + c, d);
+  }
+  for (int c = tid - 256 + 256 * WD_PF; c < p.wd_N; c += 256) {
+    int32_t d = dot16(f4, *reinterpret_cast<const v4i*>(p.wdp + ((int64_t)blockIdx.x * p.wd_N + c) * 16), 0);
+    if (t0 >= 0) {
+      const int8_t* tr = p.wdp + ((int64_t)(t0 >> 4) * p.wd_N + c) * 16 + (t0 & 15);
+#pragma unroll
+      for (int j = 0; j < GW; j += 4) d = __builtin_amdgcn_sdot4(reinterpret_cast<const int*>(fq16[1])[j >> 2],
+                                                                 *reinterpret_cast<const int*>(tr + j), d, false);
+    }
     if (d != 0) atomic_add_dev(acc + c, d);
   }
 }
@@ -1144,8 +1351,31 @@ extern "C" int llhip_dec_mlp(const llhip_mlp_in_desc* d, const llhip_resid_desc*
   p.wd_acc = static_cast<int32_t*>(wd_acc);
   p.wd_R = (int)R;
   p.wd_N = (int)N_out;
-  hipLaunchKernelGGL((mlp_in_kernel<FUSED_WAVES, true>), dim3((unsigned)ceil_div(p.N, 16)), dim3(128 * p.KS),
-                     (size_t)(p.M * (p.K + 16)), (hipStream_t)stream, p);
+  if (p.K > 4 * DM_THREADS / 2) return fail(-EINVAL, "dec_mlp: row width above %d", 4 * DM_THREADS / 2);
+  // one workgroup per CU when the tiles past the CU count fit as one tail group per workgroup
+  const int tiles = (int)ceil_div(p.N, 16), cus = current_cu_count();
+  int W = tiles;
+  p.tail_tiles = 0;
+  p.tail_gw = 16;
+  if (tiles > cus) {
+    for (int gw = 4; gw <= 16; gw *= 2) {
+      const int tt = tiles - cus;  // every group (u, i) lands on a workgroup below 8 * ceil(tt / 8) * (16 / gw)
+      if (8 * ceil_div(tt, 8) * (16 / gw) <= cus) {
+        W = cus;
+        p.tail_tiles = tt;
+        p.tail_gw = gw;
+        break;
+      }
+    }
+  }
+  const dim3 grid((unsigned)W), block(DM_THREADS);
+  const size_t lds = (size_t)(p.K + 16);
+  if (p.tail_gw == 4)
+    hipLaunchKernelGGL(dec_mlp_kernel<4>, grid, block, lds, (hipStream_t)stream, p);
+  else if (p.tail_gw == 8)
+    hipLaunchKernelGGL(dec_mlp_kernel<8>, grid, block, lds, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(dec_mlp_kernel<16>, grid, block, lds, (hipStream_t)stream, p);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }

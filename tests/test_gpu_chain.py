@@ -69,3 +69,28 @@ def test_chain_decode_loop_graph_equals_eager(tmp_path_factory):
             assert np.array_equal(a, b)
         for kv_a, kv_b in zip(base[4:], other[4:]):
             assert np.array_equal(kv_a[0], kv_b[0]) and np.array_equal(kv_a[1], kv_b[1])
+
+
+@pytest.mark.parametrize("ffn", [4112, 6000, 7008])
+def test_chain_ffn_tail_groups(tmp_path, ffn):
+    """FFN widths whose 16-column tiles outnumber the CUs (on a 256-CU device): the MLP launch runs one
+    workgroup per CU, each with one tile and at most one group of columns of the tiles past the CU
+    count -- 4112: one such tile in groups of 4; 6000: 119 tiles in groups of 8; 7008: 182 tiles in
+    groups of 16.  Chain == fused plan == oracle on a 2-layer Qwen2.5-shaped model."""
+    import dataclasses
+
+    cfg = dataclasses.replace(synth.CONFIGS["qwen25"], n_layers=2, vocab=4096, ffn=ffn, max_seq=64,
+                              name=f"q25f{ffn}")
+    qdir = synth.build_qgraph(tmp_path / cfg.name, cfg, seed=4)
+    g = G.GoldenModel(qdir)
+    assert g._chain is not None and g.use_chain
+    f = G.GoldenModel(qdir)
+    f.use_chain = False
+    prompt = synth.seeded_prompt(cfg, 13, 5)
+    rc, ac = _decode_acts(g, prompt, 4)
+    rf, af = _decode_acts(f, prompt, 4)
+    assert rc == rf
+    for sc, sf in zip(ac, af):
+        for name in sf["acts"]:
+            assert np.array_equal(sc["acts"][name], sf["acts"][name]), (sc["pos"], name)
+    assert g.generate(prompt, 6) == O.OracleModel(qdir, backend="c").generate(prompt, 6)
