@@ -682,9 +682,9 @@ struct MlpInArgs {
   int64_t silu_Mi, fq_M;
   int silu_Si, silu_sh, mul_sh, fq_S;
   int M, N, K, KS;
-  // decode chain (RESID kernels, M = 1): the row from the output projection's partial sums, and the
-  // down projection's partial sums of this workgroup's 16 FFN columns: wd_acc[r][n] +=
-  // sum_j fq[16 b + j] * Wd[n][16 b + j] with the panel wdp[b][n][j] = Wd[n][16 b + j]
+  // decode chain (dec_mlp_kernel, M = 1): the row from the output projection's partial sums, and
+  // the down projection's partial sums of the workgroup's FFN columns j: wd_acc[r][n] +=
+  // sum_j fq[j] * Wd[n][j], read from the panel wdp[b][n][i] = Wd[n][16 b + i]
   ResidArgs res;
   const int8_t* wdp;
   int32_t* wd_acc;
@@ -696,26 +696,21 @@ struct MlpInArgs {
 
 constexpr int WD_PF = 4;  // down-projection panel columns per thread loaded at kernel entry
 
-template <int MAXW, bool RESID>
+template <int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   kernarg_warm<sizeof(MlpInArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   __shared__ v4i red[MAXW][64];
   __shared__ uint32_t sig32[129];
-  __shared__ uint64_t red64[MAXW];
-  __shared__ __attribute__((aligned(16))) int8_t fq16[16];
   const int lda = p.K + 16;
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int col = lane & 15, kg = lane >> 4;
   const int n = blockIdx.x * 16 + col;
 
   const NormMap nm = norm_map(p.M);
   NormRegs nr;
   PreRows pq;
-  ResidRegs rr;
-  if constexpr (RESID)
-    resid_prefetch(p.pre, p.res, rr);
-  else if (p.pre.prequant)
+  if (p.pre.prequant)
     prerows_load(p.pre, p.M, pq);
   else
     norm_prefetch(p.pre, p.M, nm, nr);
@@ -733,25 +728,13 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   }
   issue_fence();
   const uint32_t o8 = n < p.N ? 8 * n : LD_OOB, o4 = n < p.N ? 4 * n : LD_OOB;
-  const v2i rg = ld8(rsrc(p.rqg, (int64_t)p.N * 8), o8);
-  const v2i ru = ld8(rsrc(p.rqu, (int64_t)p.N * 8), o8);
-  const int32_t bgv = ld4(rsrc(p.bg, (int64_t)p.N * 4), o4);
-  const int32_t buv = ld4(rsrc(p.bu, (int64_t)p.N * 4), o4);
+  v2i rg = ld8(rsrc(p.rqg, (int64_t)p.N * 8), o8);
+  v2i ru = ld8(rsrc(p.rqu, (int64_t)p.N * 8), o8);
+  int32_t bgv = ld4(rsrc(p.bg, (int64_t)p.N * 4), o4);
+  int32_t buv = ld4(rsrc(p.bu, (int64_t)p.N * 4), o4);
   issue_fence();
-  v4i wdv[WD_PF];  // this thread's first down-projection panel columns
-  if constexpr (RESID) {
-    const Rsrc dr = rsrc(p.wdp + (int64_t)blockIdx.x * p.wd_N * 16, (int64_t)p.wd_N * 16);
-#pragma unroll
-    for (int i = 0; i < WD_PF; ++i) {
-      const int c = tid + i * (int)blockDim.x;
-      wdv[i] = ld16(dr, c < p.wd_N ? 16u * c : LD_OOB);
-    }
-    issue_fence();
-  }
 
-  if constexpr (RESID)
-    resid_norm_quant(p.pre, p.res, rr, dyn, blockIdx.x == 0, red64);
-  else if (p.pre.prequant)
+  if (p.pre.prequant)
     prerows_store(p.pre, p.M, pq, dyn, lda);
   else
     norm_quant_rows(p.pre, nr, p.M, nm, dyn, lda, blockIdx.x == 0);
@@ -760,6 +743,9 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   red[wave][lane] = wslice_mfma(ws, wr, dyn, lda, p.M, p.K);
   __syncthreads();
   if (wave == 0) {
+    // the requant operands are used from here on (the compiler may not widen them earlier, which
+    // would wait for every load before the prologue)
+    asm volatile("" : "+v"(rg), "+v"(ru), "+v"(bgv), "+v"(buv));
     v4i ag = red[0][lane], au = red[p.KS][lane];
     for (int ks = 1; ks < p.KS; ++ks) {
       v4_add(ag, red[ks][lane]);
@@ -769,45 +755,18 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 4 * kg + r;
-      if (m >= p.M) continue;
-      int8_t fq = 0;
-      if (n < p.N) {
-        const int64_t o = (int64_t)m * p.N + n;
-        const int64_t tg = sat16(mulshift((int64_t)ag[r] + bgv, rg.x, rg.y));
-        const int64_t tu = sat16(mulshift((int64_t)au[r] + buv, ru.x, ru.y));
-        if (p.g_out) p.g_out[o] = (int16_t)tg;
-        if (p.u_out) p.u_out[o] = (int16_t)tu;
-        const int64_t sg = silu16_lds(tg, p.silu_Mi, p.silu_Si, p.silu_sh, sig);
-        const int64_t f = sat16(rshr(tu * sg, p.mul_sh));
-        p.sg_out[o] = (int16_t)sg;
-        p.f_out[o] = (int16_t)f;
-        fq = (int8_t)sat8(mulshift(f, p.fq_M, p.fq_S));
-        p.fq_out[o] = fq;
-      }
-      if (RESID && m == 0) fq16[col] = fq;  // columns past N contribute nothing (zero panel bytes)
+      if (m >= p.M || n >= p.N) continue;
+      const int64_t o = (int64_t)m * p.N + n;
+      const int64_t tg = sat16(mulshift((int64_t)ag[r] + bgv, rg.x, rg.y));
+      const int64_t tu = sat16(mulshift((int64_t)au[r] + buv, ru.x, ru.y));
+      if (p.g_out) p.g_out[o] = (int16_t)tg;
+      if (p.u_out) p.u_out[o] = (int16_t)tu;
+      const int64_t sg = silu16_lds(tg, p.silu_Mi, p.silu_Si, p.silu_sh, sig);
+      const int64_t f = sat16(rshr(tu * sg, p.mul_sh));
+      p.sg_out[o] = (int16_t)sg;
+      p.f_out[o] = (int16_t)f;
+      p.fq_out[o] = (int8_t)sat8(mulshift(f, p.fq_M, p.fq_S));
     }
-  }
-  if constexpr (!RESID) return;
-  // down projection: the 16 quantised FFN values of this workgroup against every output column
-  __syncthreads();
-  const v4i f4 = *reinterpret_cast<const v4i*>(fq16);
-  int32_t* acc = p.wd_acc + (int64_t)(blockIdx.x % p.wd_R) * p.wd_N;
-  auto dot16 = [&](const v4i& w) {
-    int32_t d = __builtin_amdgcn_sdot4(f4.x, w.x, 0, false);
-    d = __builtin_amdgcn_sdot4(f4.y, w.y, d, false);
-    d = __builtin_amdgcn_sdot4(f4.z, w.z, d, false);
-    return __builtin_amdgcn_sdot4(f4.w, w.w, d, false);
-  };
-#pragma unroll
-  for (int i = 0; i < WD_PF; ++i) {
-    const int c = tid + i * (int)blockDim.x;
-    const int32_t d = dot16(wdv[i]);
-    if (c < p.wd_N && d != 0) atomic_add_dev(acc + c, d);
-  }
-  const int8_t* panel = p.wdp + (int64_t)blockIdx.x * p.wd_N * 16;
-  for (int c = tid + WD_PF * (int)blockDim.x; c < p.wd_N; c += blockDim.x) {
-    const int32_t d = dot16(*reinterpret_cast<const v4i*>(panel + 16 * (int64_t)c));
-    if (d != 0) atomic_add_dev(acc + c, d);
   }
 }
 
@@ -1027,7 +986,7 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
   const int n = (blockIdx.x * p.TPW + t) * 16 + col;
 
   // the record slot of this decode launch (an earlier launch wrote it)
-  const int32_t stepv = ld4(rsrc(p.keys ? p.step : nullptr, 4), 0);
+  int32_t stepv = ld4(rsrc(p.keys ? p.step : nullptr, 4), 0);
   const NormMap nm = norm_map(p.M);
   NormRegs nr;
   PreRows pq;
@@ -1093,6 +1052,9 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
     static_cast<int16_t*>(p.out)[o] = (int16_t)y;
     if (p.keys && m == 0 && n < p.vocab) {
       key = amax_key((int)y, n);
+      // the slot is needed from here on: the compiler may not make it uniform (and wait for its
+      // load, before any other load is issued) at the kernel's start
+      asm volatile("" : "+v"(stepv));
       if (stepv < p.ring_cap) p.ring[(int64_t)stepv * p.ring_ld + n] = (int16_t)y;
     }
   }
@@ -1329,7 +1291,7 @@ extern "C" int llhip_mlp_in(const llhip_mlp_in_desc* d, void* stream) {
   MlpInArgs p{};
   const int rc = mlp_in_args(d, p, 0);
   if (rc) return rc;
-  hipLaunchKernelGGL((mlp_in_kernel<FUSED_WAVES, false>), dim3((unsigned)ceil_div(p.N, 16)), dim3(128 * p.KS),
+  hipLaunchKernelGGL((mlp_in_kernel<FUSED_WAVES>), dim3((unsigned)ceil_div(p.N, 16)), dim3(128 * p.KS),
                      (size_t)(p.M * (p.K + 16)), (hipStream_t)stream, p);
   LLHIP_LAUNCH_CHECK();
   return 0;
