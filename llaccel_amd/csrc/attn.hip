@@ -45,6 +45,7 @@ struct AttnArgs {
   int32_t* wo_acc;
   int32_t* zero;
   int wo_N, zero_n;
+  int span;  // dimension-slice launches of one row: XCDs per GQA group (0: one, the grid below)
 };
 
 // clear n int32 values from one workgroup (16-byte aligned)
@@ -227,12 +228,27 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
   // workgroups b = u % 8 + 8 * ((u / 8) * G + j) for its heads j.  The grid is
   // 8 * ceil(M * Hkv / 8) * G; workgroups past the last pair exit.
   // (With slices the grid has DS workgroups per head: j = (xk % (G * DS)) / DS, ds = xk % DS.)
+  // A slice launch with span P > 1 (one row, Hkv * P = 8) spreads group g over the P XCDs
+  // g * P .. g * P + P - 1 instead: its G * DS workgroups w sit at b = g * P + w % P + 8 * (w / P),
+  // so all eight XCDs (their L2 and their CUs) serve the row and the grid has no idle workgroups.
   const int G = p.H / p.Hkv;
-  const int xk = (int)(blockIdx.x / 8);
-  const int u = (int)(blockIdx.x % 8) + 8 * (xk / (G * DS));
-  if (u >= p.M * p.Hkv) return;
-  const int m = u / p.Hkv, g = u % p.Hkv;
-  const int h = g * G + (xk % (G * DS)) / DS, ds = xk % DS;
+  int m, g, h, ds;
+  if (SLICE && p.span > 1) {
+    const int x = (int)(blockIdx.x % 8), w = x % p.span + p.span * (int)(blockIdx.x / 8);
+    g = x / p.span;
+    if (g >= p.Hkv || w >= G * DS) return;
+    m = 0;
+    h = g * G + w / DS;
+    ds = w % DS;
+  } else {
+    const int xk = (int)(blockIdx.x / 8);
+    const int u = (int)(blockIdx.x % 8) + 8 * (xk / (G * DS));
+    if (u >= p.M * p.Hkv) return;
+    m = u / p.Hkv;
+    g = u % p.Hkv;
+    h = g * G + (xk % (G * DS)) / DS;
+    ds = xk % DS;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   // Loads in order of use: q and the keys of the first score pass, the LUT dwords (wave 0), the
   // value rows of this thread's first VPF keys.  The cache rows are addressed over the whole cache,
@@ -1203,6 +1219,11 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   const int64_t per_head = slice ? D / 16 : 1;
   if (M * Hkv > (int64_t)INT32_MAX / 8 / (H / Hkv) / per_head) return fail(-EINVAL, "attention: too many rows");
   dim3 grid((unsigned)(8 * ceil_div(M * Hkv, 8) * (H / Hkv) * per_head));
+  p.span = 0;
+  if (slice && Hkv < 8 && 8 % Hkv == 0) {
+    p.span = (int)(8 / Hkv);
+    grid = dim3((unsigned)(8 * ceil_div((H / Hkv) * per_head, p.span)));
+  }
   dim3 block(ATTN_THREADS);
 #define LLHIP_ROWHEAD(DD)                                                            \
   if (slice)                                                                        \
