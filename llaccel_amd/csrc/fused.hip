@@ -396,19 +396,23 @@ __device__ __forceinline__ void zero_rows(int32_t* p, int n) {
 // the rest four steps at a time.  Lane (col, kg) holds K bytes [s*64 + kg*16, +16) of column col.
 constexpr int PF = 8;
 
+// NP: the K steps loaded at entry (the launch sizes it to the steps of a wave's K range, so no load
+// instruction is spent on steps past the range)
+template <int NP = PF>
 struct WSlice {
-  v4i w[PF];
+  v4i w[NP];
   uint32_t rowoff;
   int s0, s1, kg;
 };
 
-__device__ __forceinline__ void wslice_prefetch(WSlice& ws, Rsrc wr, int n, int K, int kg, int s0, int s1) {
+template <int NP>
+__device__ __forceinline__ void wslice_prefetch(WSlice<NP>& ws, Rsrc wr, int n, int K, int kg, int s0, int s1) {
   ws.rowoff = (uint32_t)n * (uint32_t)K;  // rows n >= N fall past the range and read zeros
   ws.s0 = s0;
   ws.s1 = s1;
   ws.kg = kg;
 #pragma unroll
-  for (int u = 0; u < PF; ++u) {
+  for (int u = 0; u < NP; ++u) {
     const int k = (s0 + u) * 64 + kg * 16;
     ws.w[u] = ld16(wr, (s0 + u < s1 && k < K) ? ws.rowoff + k : LD_OOB);
   }
@@ -417,16 +421,17 @@ __device__ __forceinline__ void wslice_prefetch(WSlice& ws, Rsrc wr, int n, int 
 // 16x16 partial tile of the slice; A rows from LDS.  A rows >= M are read from row M - 1: output
 // row m depends only on A row m, so those rows only produce discarded outputs.  Steps past the
 // slice have zero weights, so their A reads only need to stay inside the LDS rows.
-__device__ __forceinline__ v4i wslice_mfma(const WSlice& ws, Rsrc wr, const int8_t* a_lds, int lda, int M, int K) {
+template <int NP>
+__device__ __forceinline__ v4i wslice_mfma(const WSlice<NP>& ws, Rsrc wr, const int8_t* a_lds, int lda, int M, int K) {
   const int lane = threadIdx.x & 63;
   const int8_t* arow = a_lds + min(lane & 15, M - 1) * lda;
   v4i acc = {0, 0, 0, 0};
 #pragma unroll
-  for (int u = 0; u < PF; ++u) {
+  for (int u = 0; u < NP; ++u) {
     const int k = min((ws.s0 + u) * 64 + ws.kg * 16, K - 16);
     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const v4i*>(arow + k), ws.w[u], acc, 0, 0, 0);
   }
-  for (int s = ws.s0 + PF; s < ws.s1; s += 4) {
+  for (int s = ws.s0 + NP; s < ws.s1; s += 4) {
     v4i b[4], a[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -495,7 +500,7 @@ __device__ __forceinline__ T pick3(int role, const T (&v)[3]) {
 // SPL > 1 (decode chain, no head norm): SPL workgroups per head block, workgroup s taking the
 // 16-column tiles t with t % SPL == s -- a tile and its RoPE partner t + D/32 fall in the same
 // workgroup when (D / 32) % SPL == 0 -- so each streams 1/SPL of the head's weights.
-template <int MAXW, bool RESID, int SPL = 1>
+template <int MAXW, bool RESID, int SPL = 1, int PFN = PF>
 __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   kernarg_warm<sizeof(AttnInArgs)>();
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
@@ -527,8 +532,12 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   // per-row positions: the row of this thread's RoPE pair and row tid (staged in LDS for the tail)
   const int half = D >> 1;
   const int jrope = gcol(tid % (half / SPL)), mrope = tid / (half / SPL);
-  const Rsrc rpr = rsrc(p.row_pos, 4 * M);
-  const int32_t rp_rope = ld4(rpr, mrope < M ? 4 * mrope : LD_OOB), rp_own = ld4(rpr, tid < M ? 4 * tid : LD_OOB);
+  int32_t rp_rope = 0, rp_own = 0;
+  if (p.row_pos) {  // (a load instruction costs address-unit cycles even when it reads nothing)
+    const Rsrc rpr = rsrc(p.row_pos, 4 * M);
+    rp_rope = ld4(rpr, mrope < M ? 4 * mrope : LD_OOB);
+    rp_own = ld4(rpr, tid < M ? 4 * tid : LD_OOB);
+  }
   issue_fence();
   const NormMap nm = norm_map(M);
   NormRegs nr;
@@ -542,7 +551,7 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     norm_prefetch(p.pre, M, nm, nr);
   issue_fence();
   const Rsrc wr = rsrc(pick3(role, p.W), (int64_t)Nrole * p.K);
-  WSlice ws;
+  WSlice<PFN> ws;
   {
     const int t = wave % tiles, ks = wave / tiles;
     int s0, s1;
@@ -555,9 +564,9 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
   const v2i rq = ld8(rsrc(pick3(role, p.rq), (int64_t)Nrole * 8), 8 * ncol);
   const int32_t bias = ld4(rsrc(pick3(role, p.bias), (int64_t)Nrole * 4), 4 * ncol);
   const bool hn = SPL == 1 && p.has_norm && role < 2;  // split heads are never normed (host)
-  int32_t hg[4];  // head-norm gamma of dims lane + 64 i (the per-row norm runs wave-wide)
-  {
-    const Rsrc gr = rsrc(hn ? (role == 0 ? p.nrm_gamma[0] : p.nrm_gamma[1]) : nullptr, (int64_t)D * 2);
+  int32_t hg[4] = {0, 0, 0, 0};  // head-norm gamma of dims lane + 64 i (the per-row norm runs wave-wide)
+  if (hn) {
+    const Rsrc gr = rsrc(role == 0 ? p.nrm_gamma[0] : p.nrm_gamma[1], (int64_t)D * 2);
 #pragma unroll
     for (int i = 0; i < 4; ++i) hg[i] = ld2s(gr, lane + 64 * i < D ? 2 * (lane + 64 * i) : LD_OOB);
   }
@@ -720,7 +729,7 @@ __global__ __launch_bounds__(64 * MAXW) void mlp_in_kernel(MlpInArgs p) {
   issue_fence();
   const int up = wave >= p.KS;  // waves [0, KS): gate, [KS, 2KS): up
   const Rsrc wr = rsrc(up ? p.Wu : p.Wg, (int64_t)p.N * p.K);
-  WSlice ws;
+  WSlice<> ws;
   {
     int s0, s1;
     split_range((p.K + 63) >> 6, p.KS, up ? wave - p.KS : wave, s0, s1);
@@ -825,7 +834,7 @@ __global__ __launch_bounds__(DM_THREADS) void dec_mlp_kernel(MlpInArgs p) {
   if (tid == 0) meet = 0;
   __syncthreads();  // no load has been issued yet: every wave is here at once
 
-  WSlice ws[2];
+  WSlice<> ws[2];
   Rsrc wr;
   v4i wdv[WD_PF];     // weight waves: their first panel rows of the main tile
   v4i wdt[WD_PF];     // ... and the tail group's bytes of the tail tile's rows
@@ -999,7 +1008,7 @@ __global__ __launch_bounds__(64 * MAXW) void norm_gemv_kernel(NormGemvArgs p) {
   sig_prefetch(sr);
   issue_fence();
   const Rsrc wr = rsrc(p.W, (int64_t)p.N * p.K);
-  WSlice ws;
+  WSlice<> ws;
   {
     int s0, s1;
     split_range((p.K + 63) >> 6, p.KS, ks, s0, s1);
@@ -1190,8 +1199,12 @@ static bool attn_in_split_launch(AttnInArgs p, void* stream, int& rc) {
   if (64 * tiles * ks < p.K / 4 || (64 * tiles * ks) % (p.D / SPL)) return false;  // one row unit per thread
   p.KS = ks;
   const size_t lds = (size_t)((p.K + 16 + 15) & ~15) + sizeof(int32_t) * (size_t)p.D;
-  hipLaunchKernelGGL((attn_in_kernel<FUSED_WAVES, true, SPL>), dim3((unsigned)((p.H + 2 * p.Hkv) * SPL)),
-                     dim3(64 * tiles * ks), lds, (hipStream_t)stream, p);
+  if (ceil_div(steps, ks) <= 4)
+    hipLaunchKernelGGL((attn_in_kernel<FUSED_WAVES, true, SPL, 4>), dim3((unsigned)((p.H + 2 * p.Hkv) * SPL)),
+                       dim3(64 * tiles * ks), lds, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL((attn_in_kernel<FUSED_WAVES, true, SPL>), dim3((unsigned)((p.H + 2 * p.Hkv) * SPL)),
+                       dim3(64 * tiles * ks), lds, (hipStream_t)stream, p);
   rc = hipGetLastError() == hipSuccess ? 0 : fail(-EIO, "dec_attn_in: launch failed");
   return true;
 }
