@@ -270,13 +270,13 @@ __global__ __launch_bounds__(ATTN_THREADS) void attention_rowhead(AttnArgs p) {
 #pragma unroll
   for (int i = 0; i < KPF; ++i) kpf[i] = ld16(kr, (uint32_t)((i * KPB + kw) * D + 16 * kc));
   issue_fence();
-  uint32_t lw[3];
-  {
+  uint32_t lw[3] = {0u, 0u, 0u};
+  if (wave == 0) {  // (a load instruction costs address-unit cycles even when it reads nothing)
     const Rsrc ir = rsrc(kExpI, sizeof(kExpI)), fr = rsrc(kExpF, sizeof(kExpF));
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       const int idx = lane + 64 * i;
-      const bool mine = wave == 0 && idx < LUT_DW;
+      const bool mine = idx < LUT_DW;
       // one of the two reads is out of range (zero)
       lw[i] = (uint32_t)ld4(ir, mine && idx < 8 ? 4 * idx : LD_OOB) |
               (uint32_t)ld4(fr, mine && idx >= 8 ? 4 * (idx - 8) : LD_OOB);
