@@ -1167,42 +1167,63 @@ __device__ __forceinline__ void v4_acc(v4i& a, const v4i& b) {
   a.w += b.w;
 }
 
+constexpr int FINISH_MAX_SPLITS = 8;  // launch_mfma splits K at most 8 ways
+
+// One row per workgroup, 8 columns per thread.  Every operand is requested at entry (all planes'
+// partial sums, requant pairs, bias, residual, gamma: 21 loads per thread, none waiting for another),
+// then the sums, requant + resadd, the row's sum of squares, RMSNorm and quant.
 __global__ __launch_bounds__(256) void splitk_finish_norm_kernel(LinearArgs p, const int32_t* part, int splits,
                                                                  NormQuant pr) {
   constexpr int NCH = NORM_MAX_K / 8 / 256 + 1;
+  static_assert(NCH == 1, "one 8-column chunk per thread");
   __shared__ uint64_t red[4];
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nch = p.N >> 3;
   const int64_t plane = (int64_t)p.M * p.N;
-  const Rsrc gr = rsrc(pr.gamma, (int64_t)p.N * 2);
-  v4i x[NCH], g[NCH];
-  uint64_t ss = 0;
+  const int c = tid;
+  const bool in = c < nch;
+  const int64_t e = (int64_t)m * p.N + 8 * c;
+  const Rsrc prs = rsrc(part, (int64_t)splits * plane * 4);
+  v4i a[2 * FINISH_MAX_SPLITS];
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    const int c = tid + 256 * i;
-    g[i] = ld16(gr, c < nch ? 16 * c : LD_OOB);
-    x[i] = v4i{0, 0, 0, 0};
-    if (c >= nch) continue;
-    const int64_t e = (int64_t)m * p.N + 8 * c;
-    v4i a0 = *reinterpret_cast<const v4i*>(part + e), a1 = *reinterpret_cast<const v4i*>(part + e + 4);
-    for (int z = 1; z < splits; ++z) {
-      const v4i b0 = *reinterpret_cast<const v4i*>(part + z * plane + e);
-      const v4i b1 = *reinterpret_cast<const v4i*>(part + z * plane + e + 4);
-      v4_acc(a0, b0);
-      v4_acc(a1, b1);
+  for (int z = 0; z < FINISH_MAX_SPLITS; ++z) {
+    const uint32_t off = (in && z < splits) ? (uint32_t)((z * plane + e) * 4) : LD_OOB;
+    a[2 * z] = ld16(prs, off);
+    a[2 * z + 1] = ld16(prs, off == LD_OOB ? LD_OOB : off + 16);
+  }
+  const Rsrc qr = rsrc(p.rq, (int64_t)p.N * 8), br = rsrc(p.bias, (int64_t)p.N * 4);
+  v4i rq[4], bi[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) rq[j] = ld16(qr, in ? (uint32_t)(64 * c + 16 * j) : LD_OOB);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) bi[j] = ld16(br, in ? (uint32_t)(32 * c + 16 * j) : LD_OOB);
+  const v4i ax = ld16(rsrc(p.aux + (int64_t)m * p.ldaux, (int64_t)p.N * 2), in ? (uint32_t)(16 * c) : LD_OOB);
+  v4i g[NCH];
+  g[0] = ld16(rsrc(pr.gamma, (int64_t)p.N * 2), in ? (uint32_t)(16 * c) : LD_OOB);
+  v4i x[NCH];
+  x[0] = v4i{0, 0, 0, 0};
+  uint64_t ss = 0;
+  if (in) {
+    v4i a0 = a[0], a1 = a[1];
+#pragma unroll
+    for (int z = 1; z < FINISH_MAX_SPLITS; ++z) {  // planes past splits read zeros
+      v4_acc(a0, a[2 * z]);
+      v4_acc(a1, a[2 * z + 1]);
     }
     const int32_t acc[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const int32_t bias[8] = {bi[0].x, bi[0].y, bi[0].z, bi[0].w, bi[1].x, bi[1].y, bi[1].z, bi[1].w};
+    const int32_t rqv[16] = {rq[0].x, rq[0].y, rq[0].z, rq[0].w, rq[1].x, rq[1].y, rq[1].z, rq[1].w,
+                             rq[2].x, rq[2].y, rq[2].z, rq[2].w, rq[3].x, rq[3].y, rq[3].z, rq[3].w};
+    const int32_t aux[8] = {lo16(ax.x), hi16(ax.x), lo16(ax.y), hi16(ax.y), lo16(ax.z), hi16(ax.z), lo16(ax.w), hi16(ax.w)};
     int32_t t[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int n = 8 * c + j;
-      int64_t v = acc[j];
-      if (p.bias) v += p.bias[n];
-      const int64_t r = sat16(mulshift(v, (int64_t)p.rq[2 * n], p.rq[2 * n + 1]));
-      t[j] = (int32_t)sat16(r + p.aux[(int64_t)m * p.ldaux + n]);
+      const int64_t v = (int64_t)acc[j] + bias[j];  // bias reads zeros when absent
+      const int64_t r = sat16(mulshift(v, (int64_t)rqv[2 * j], rqv[2 * j + 1]));
+      t[j] = (int32_t)sat16(r + aux[j]);
       ss += (uint32_t)(t[j] * t[j]);
     }
-    x[i] = v4i{pack16(t[0], t[1]), pack16(t[2], t[3]), pack16(t[4], t[5]), pack16(t[6], t[7])};
-    *reinterpret_cast<v4i*>(static_cast<int16_t*>(p.out) + (int64_t)m * p.ldo + 8 * c) = x[i];
+    x[0] = v4i{pack16(t[0], t[1]), pack16(t[2], t[3]), pack16(t[4], t[5]), pack16(t[6], t[7])};
+    *reinterpret_cast<v4i*>(static_cast<int16_t*>(p.out) + (int64_t)m * p.ldo + 8 * c) = x[0];
   }
   ss = wave_sum_u64(ss);
   if (lane == 0) red[wave] = ss;
