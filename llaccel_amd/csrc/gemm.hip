@@ -1132,25 +1132,64 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
 }
 
 // sum of the split-K planes + bias, requant and epilogue; four columns per thread
+// (every operand of a quad -- all planes, the requant pairs, bias, aux -- is requested before any is
+// used: the stores of one quad may not be followed by its next loads in a dependent chain)
 template <int EPI, bool OUT8>
 __global__ __launch_bounds__(256) void linear_splitk_finish(LinearArgs p, const int32_t* part, int splits) {
+  constexpr int MAXS = 8;  // launch_mfma splits K at most 8 ways
   const int64_t plane = (int64_t)p.M * p.N;
   const int64_t quads = plane / 4;
+  const Rsrc prs = rsrc(part, (int64_t)splits * plane * 4);
+  const Rsrc qr = rsrc(p.rq, (int64_t)p.N * 8), br = rsrc(p.bias, (int64_t)p.N * 4);
+  constexpr bool AUX = EPI == EPI_RESADD || EPI == EPI_MUL;
   for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += (int64_t)gridDim.x * blockDim.x) {
-    v4i a = *reinterpret_cast<const v4i*>(part + 4 * q);
-    for (int z = 1; z < splits; ++z) {
-      const v4i b = *reinterpret_cast<const v4i*>(part + z * plane + 4 * q);
-      a.x += b.x;
-      a.y += b.y;
-      a.z += b.z;
-      a.w += b.w;
-    }
     const int64_t e = 4 * q;
     const int m = (int)(e / p.N), n = (int)(e % p.N);  // N % 4 == 0: the quad stays in one row
-    finish<EPI, OUT8>(p, m, n, a.x);
-    finish<EPI, OUT8>(p, m, n + 1, a.y);
-    finish<EPI, OUT8>(p, m, n + 2, a.z);
-    finish<EPI, OUT8>(p, m, n + 3, a.w);
+    v4i pl[MAXS];
+#pragma unroll
+    for (int z = 0; z < MAXS; ++z) pl[z] = ld16(prs, z < splits ? (uint32_t)((z * plane + e) * 4) : LD_OOB);
+    const v4i rq0 = ld16(qr, (uint32_t)(8 * n)), rq1 = ld16(qr, (uint32_t)(8 * n + 16));
+    const v4i bi = ld16(br, (uint32_t)(4 * n));
+    v2i ax = v2i{0, 0};
+    if constexpr (AUX && !OUT8)
+      ax = ld8(rsrc(p.aux + (int64_t)m * p.ldaux, (int64_t)p.N * 2), (uint32_t)(2 * n));
+    v4i a = pl[0];
+#pragma unroll
+    for (int z = 1; z < MAXS; ++z) {  // planes past splits read zeros
+      a.x += pl[z].x;
+      a.y += pl[z].y;
+      a.z += pl[z].z;
+      a.w += pl[z].w;
+    }
+    const int32_t acc[4] = {a.x, a.y, a.z, a.w}, bias[4] = {bi.x, bi.y, bi.z, bi.w};
+    const int32_t Mv[4] = {rq0.x, rq0.z, rq1.x, rq1.z}, Sv[4] = {rq0.y, rq0.w, rq1.y, rq1.w};
+    const int32_t aux[4] = {lo16(ax.x), hi16(ax.x), lo16(ax.y), hi16(ax.y)};
+    int32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t r = mulshift((int64_t)acc[j] + bias[j], (int64_t)Mv[j], Sv[j]);  // bias reads zeros when absent
+      if (OUT8) {
+        o[j] = (int32_t)sat8(r);
+        continue;
+      }
+      int64_t t = sat16(r);
+      if (EPI == EPI_RESADD) {
+        t = sat16(t + aux[j]);
+      } else if (EPI == EPI_SILU) {
+        t = silu16(t, p.Mi, p.Si, p.sh);
+      } else if (EPI == EPI_MUL) {
+        t = sat16(rshr(wmul(t, aux[j]), p.aux_shift));
+      }
+      o[j] = (int32_t)t;
+    }
+    if (OUT8) {
+      const uint32_t w = (uint32_t)(uint8_t)o[0] | ((uint32_t)(uint8_t)o[1] << 8) | ((uint32_t)(uint8_t)o[2] << 16) |
+                         ((uint32_t)(uint8_t)o[3] << 24);
+      *reinterpret_cast<uint32_t*>(static_cast<int8_t*>(p.out) + (int64_t)m * p.ldo + n) = w;
+    } else {
+      *reinterpret_cast<v2i*>(static_cast<int16_t*>(p.out) + (int64_t)m * p.ldo + n) =
+          v2i{pack16(o[0], o[1]), pack16(o[2], o[3])};
+    }
   }
 }
 
@@ -1285,7 +1324,9 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream, const NormQu
   const int k64 = (int)(p.K / 64), ktiles = (int)(p.K / KT);
   const int cus = current_cu_count();
   int splits = 1;
-  if (ws && p.N % 4 == 0 && tiles < cus) {
+  // the finishing kernels store 4 (8) adjacent columns at once and read aux rows in 8-byte words
+  const bool fin_ok = p.ldo % 4 == 0 && (uintptr_t)p.out % 8 == 0 && (!p.aux || (p.ldaux % 4 == 0 && (uintptr_t)p.aux % 8 == 0));
+  if (ws && p.N % 4 == 0 && tiles < cus && fin_ok) {
     const int smax = (int)std::min<int64_t>(std::min<int64_t>(8, ceil_div(2 * cus, tiles)), k64 / 4);
     double best = 0.0;
     for (int sp = 2; sp <= smax; ++sp) {
