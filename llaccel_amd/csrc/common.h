@@ -290,6 +290,14 @@ __device__ __forceinline__ uint32_t rms_inv(uint64_t ss, uint32_t eps_t, uint32_
 __device__ __forceinline__ int16_t rms_apply(int32_t x, int32_t g, uint32_t inv, int sh) {
   return (int16_t)sat16(rshr((int64_t)(x * g) * (int64_t)inv, sh));
 }
+// rms_apply with the row's scale = inv * 2^-sh in double: x * g (i16 x i16, |x g| <= 2^30) times
+// inv (< 2^16) is below 2^46, so x g * scale + 1/2 is exact (a multiple of 2^-(sh+1) below 2^52, or
+// for sh > 52 a value in (0, 1) whose floor 0 is exact) and its floor is rshr(x g inv, sh)
+__device__ __forceinline__ double rms_scale(uint32_t inv, int sh) { return __builtin_ldexp((double)inv, -sh); }
+__device__ __forceinline__ int32_t rms_apply_d(int32_t x, int32_t g, double scale) {
+  const double v = __builtin_floor(__builtin_fma((double)(x * g), scale, 0.5));
+  return (int32_t)__builtin_fmin(__builtin_fmax(v, -32768.0), 32767.0);
+}
 
 // argmax key: orders by value, then by lower index (larger key = better; golden.py:376-377 keeps
 // the first maximum)

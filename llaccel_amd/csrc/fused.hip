@@ -339,12 +339,14 @@ __device__ __forceinline__ void resid_apply(const NormQuant& pr, const ResidArgs
   const int u = threadIdx.x;
   if (u >= (pr.K >> 2)) return;
   const int32_t g[4] = {lo16(r.g.x), hi16(r.g.x), lo16(r.g.y), hi16(r.g.y)};
+  // double-precision forms of rms_apply and of the quant's mulshift (exact for these ranges)
+  const double sy = rms_scale(inv, pr.sh_post), sq = mulshift_scale(pr.Mq, pr.Sq);
   int16_t y[4];
   uint32_t q = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    y[j] = rms_apply(xv[j], g[j], inv, pr.sh_post);
-    q |= (uint32_t)(uint8_t)sat8(mulshift(y[j], pr.Mq, pr.Sq)) << (8 * j);
+    y[j] = (int16_t)rms_apply_d(xv[j], g[j], sy);
+    q |= (uint32_t)(uint8_t)mulshift_small_sat(y[j], sq, -128.0, 127.0) << (8 * j);
   }
   *reinterpret_cast<uint32_t*>(a_lds + 4 * u) = q;
   if (write_global) {
