@@ -90,14 +90,15 @@ __device__ __forceinline__ uint32_t norm_row_inv(const NormQuant& pr, const v4i&
 __device__ __forceinline__ void norm_apply_unit(const NormQuant& pr, int m, int u, uint32_t inv, const v2i& xu,
                                                 const v2i& gu, int8_t* a_lds, int lda, bool write_global) {
   if (u >= (pr.K >> 2)) return;
-  const int16_t y0 = rms_apply(lo16(xu.x), lo16(gu.x), inv, pr.sh_post);
-  const int16_t y1 = rms_apply(hi16(xu.x), hi16(gu.x), inv, pr.sh_post);
-  const int16_t y2 = rms_apply(lo16(xu.y), lo16(gu.y), inv, pr.sh_post);
-  const int16_t y3 = rms_apply(hi16(xu.y), hi16(gu.y), inv, pr.sh_post);
-  const uint32_t q = (uint32_t)(uint8_t)sat8(mulshift(y0, pr.Mq, pr.Sq)) |
-                     ((uint32_t)(uint8_t)sat8(mulshift(y1, pr.Mq, pr.Sq)) << 8) |
-                     ((uint32_t)(uint8_t)sat8(mulshift(y2, pr.Mq, pr.Sq)) << 16) |
-                     ((uint32_t)(uint8_t)sat8(mulshift(y3, pr.Mq, pr.Sq)) << 24);
+  const double sy = rms_scale(inv, pr.sh_post), sq = mulshift_scale(pr.Mq, pr.Sq);  // exact forms
+  const int16_t y0 = (int16_t)rms_apply_d(lo16(xu.x), lo16(gu.x), sy);
+  const int16_t y1 = (int16_t)rms_apply_d(hi16(xu.x), hi16(gu.x), sy);
+  const int16_t y2 = (int16_t)rms_apply_d(lo16(xu.y), lo16(gu.y), sy);
+  const int16_t y3 = (int16_t)rms_apply_d(hi16(xu.y), hi16(gu.y), sy);
+  const uint32_t q = (uint32_t)(uint8_t)mulshift_small_sat(y0, sq, -128.0, 127.0) |
+                     ((uint32_t)(uint8_t)mulshift_small_sat(y1, sq, -128.0, 127.0) << 8) |
+                     ((uint32_t)(uint8_t)mulshift_small_sat(y2, sq, -128.0, 127.0) << 16) |
+                     ((uint32_t)(uint8_t)mulshift_small_sat(y3, sq, -128.0, 127.0) << 24);
   *reinterpret_cast<uint32_t*>(a_lds + m * lda + 4 * u) = q;
   if (write_global) {
     if (pr.h_out) {
@@ -198,6 +199,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(NormQuant pr) {
   if (lane == 0) part[wave] = ss;
   __syncthreads();
   const uint32_t inv = rms_inv(part[0] + part[1] + part[2] + part[3], pr.eps_t, pr.C);
+  const double sy = rms_scale(inv, pr.sh_post), sq = mulshift_scale(pr.Mq, pr.Sq);  // exact forms
 #pragma unroll
   for (int i = 0; i < NORM_MAX_K / 8 / 256 + 1; ++i) {
     const int c = tid + 256 * i;
@@ -206,11 +208,11 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(NormQuant pr) {
     uint32_t qw[2] = {0u, 0u};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int16_t y0 = rms_apply(lo16(x[i][j]), lo16(g[i][j]), inv, pr.sh_post);
-      const int16_t y1 = rms_apply(hi16(x[i][j]), hi16(g[i][j]), inv, pr.sh_post);
+      const int16_t y0 = (int16_t)rms_apply_d(lo16(x[i][j]), lo16(g[i][j]), sy);
+      const int16_t y1 = (int16_t)rms_apply_d(hi16(x[i][j]), hi16(g[i][j]), sy);
       y[j] = pack16(y0, y1);
-      const uint32_t q0 = (uint8_t)sat8(mulshift(y0, pr.Mq, pr.Sq));
-      const uint32_t q1 = (uint8_t)sat8(mulshift(y1, pr.Mq, pr.Sq));
+      const uint32_t q0 = (uint8_t)mulshift_small_sat(y0, sq, -128.0, 127.0);
+      const uint32_t q1 = (uint8_t)mulshift_small_sat(y1, sq, -128.0, 127.0);
       qw[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
     }
     if (pr.h_out) *reinterpret_cast<v4i*>(pr.h_out + (int64_t)m * pr.ldx + 8 * c) = y;

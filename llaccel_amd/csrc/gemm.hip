@@ -1268,6 +1268,7 @@ __global__ __launch_bounds__(256) void splitk_finish_norm_kernel(LinearArgs p, c
   if (lane == 0) red[wave] = ss;
   __syncthreads();
   const uint32_t inv = rms_inv(red[0] + red[1] + red[2] + red[3], pr.eps_t, pr.C);
+  const double sy = rms_scale(inv, pr.sh_post), sq = mulshift_scale(pr.Mq, pr.Sq);  // exact forms
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int c = tid + 256 * i;
@@ -1276,11 +1277,11 @@ __global__ __launch_bounds__(256) void splitk_finish_norm_kernel(LinearArgs p, c
     uint32_t qw[2] = {0u, 0u};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int16_t y0 = rms_apply(lo16(x[i][j]), lo16(g[i][j]), inv, pr.sh_post);
-      const int16_t y1 = rms_apply(hi16(x[i][j]), hi16(g[i][j]), inv, pr.sh_post);
+      const int16_t y0 = (int16_t)rms_apply_d(lo16(x[i][j]), lo16(g[i][j]), sy);
+      const int16_t y1 = (int16_t)rms_apply_d(hi16(x[i][j]), hi16(g[i][j]), sy);
       y[j] = pack16(y0, y1);
-      const uint32_t q0 = (uint8_t)sat8(mulshift(y0, pr.Mq, pr.Sq));
-      const uint32_t q1 = (uint8_t)sat8(mulshift(y1, pr.Mq, pr.Sq));
+      const uint32_t q0 = (uint8_t)mulshift_small_sat(y0, sq, -128.0, 127.0);
+      const uint32_t q1 = (uint8_t)mulshift_small_sat(y1, sq, -128.0, 127.0);
       qw[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
     }
     if (pr.h_out) *reinterpret_cast<v4i*>(pr.h_out + (int64_t)m * pr.ldx + 8 * c) = y;
