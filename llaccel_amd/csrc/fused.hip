@@ -923,11 +923,13 @@ __global__ __launch_bounds__(DM_THREADS) void dec_mlp_kernel(MlpInArgs p) {
       const int64_t tu = sat16(mulshift((int64_t)(u0.x + u1.x) + buv, rqu.x, rqu.y));
       if (p.g_out) p.g_out[en] = (int16_t)tg;
       if (p.u_out) p.u_out[en] = (int16_t)tu;
-      const int64_t sg = silu16_lds(tg, p.silu_Mi, p.silu_Si, p.silu_sh, sig);
-      const int64_t f = sat16(rshr(tu * sg, p.mul_sh));
+      // SiLU, the product's rounding shift and the quant in their exact 32-bit / double forms
+      // (|tg|, |tu| < 2^15: silu16_fast's domain; |tu * sg| < 2^31)
+      const int32_t sg = silu16_fast((int32_t)tg, mulshift_scale(p.silu_Mi, p.silu_Si), p.silu_sh, sig);
+      const int32_t f = min(max(rshr32_any((int32_t)tu * sg, p.mul_sh), -32768), 32767);
       p.sg_out[en] = (int16_t)sg;
       p.f_out[en] = (int16_t)f;
-      fq = (int8_t)sat8(mulshift(f, p.fq_M, p.fq_S));
+      fq = (int8_t)mulshift_small_sat(f, mulshift_scale(p.fq_M, p.fq_S), -128.0, 127.0);
       p.fq_out[en] = fq;
     }
     fq16[tl][col] = fq;  // columns past N or past the group contribute nothing
