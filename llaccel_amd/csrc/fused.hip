@@ -648,9 +648,12 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     }
     __syncthreads();
   }
-  // RoPE (golden.py:141-158) -> quant (golden.py:119-120) -> K cache for keys
+  // RoPE (golden.py:141-158) -> quant (golden.py:119-120) -> K cache for keys, in 32-bit and
+  // double arithmetic: x and the table entries are i16, so |x1 c| + |x2 s| < 2^31, and the quant's
+  // mulshift of an i16 is exact in double (mulshift_small_sat)
+  const double sq = mulshift_scale(p.quant_M[role], (int)p.quant_S[role]);
   for (int m = mrope; m < M; m += blockDim.x / (half / SPL)) {
-    int64_t c = c0, s = s0r;
+    int32_t c = c0, s = s0r;
     const int pm = rowpos[m];
     if (pm < 0 || pm >= p.max_seq) continue;
     if (m != mrope) {
@@ -658,14 +661,14 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
       s = p.sin_tab[(int64_t)pm * half + jrope];
     }
     const int j = jrope;
-    const int64_t x1 = hres[m * D + j], x2 = hres[m * D + half + j];
-    const int16_t y1 = (int16_t)sat16(rshr(x1 * c - x2 * s, 14));
-    const int16_t y2 = (int16_t)sat16(rshr(x2 * c + x1 * s, 14));
+    const int32_t x1 = hres[m * D + j], x2 = hres[m * D + half + j];
+    const int16_t y1 = (int16_t)min(max(rshr32(x1 * c - x2 * s, 14), -32768), 32767);
+    const int16_t y2 = (int16_t)min(max(rshr32(x2 * c + x1 * s, 14), -32768), 32767);
     const int64_t o = (int64_t)m * Nrole + base;
     p.rope_out[role][o + j] = y1;
     p.rope_out[role][o + half + j] = y2;
-    const int8_t q1 = (int8_t)sat8(mulshift(y1, p.quant_M[role], (int)p.quant_S[role]));
-    const int8_t q2 = (int8_t)sat8(mulshift(y2, p.quant_M[role], (int)p.quant_S[role]));
+    const int8_t q1 = (int8_t)mulshift_small_sat(y1, sq, -128.0, 127.0);
+    const int8_t q2 = (int8_t)mulshift_small_sat(y2, sq, -128.0, 127.0);
     p.quant_out[role][o + j] = q1;
     p.quant_out[role][o + half + j] = q2;
     if (role == 1) {
