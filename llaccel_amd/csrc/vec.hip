@@ -183,22 +183,28 @@ struct RopeJob {
   int8_t* vc;
 };
 
-__device__ __forceinline__ void rope_quant_one(const RopeJob& j, int64_t idx) {
+// IDX: the index type of the launch (32-bit division where the total allows it)
+template <class IDX>
+__device__ __forceinline__ void rope_quant_one(const RopeJob& j, IDX idx) {
   const int half = j.D / 2;
-  const int64_t m = idx / ((int64_t)j.H * half);
-  const int rem = (int)(idx % ((int64_t)j.H * half));
+  const IDX hh = (IDX)j.H * (IDX)half;
+  const int64_t m = (int64_t)(idx / hh);
+  const int rem = (int)(idx % hh);
   const int h = rem / half, i = rem % half;
   const int64_t pm = j.row_pos ? (int64_t)j.row_pos[m] : (int64_t)(j.pos_dev ? *j.pos_dev : j.pos) + m;
   if (pm < 0 || pm >= j.table_rows) return;  // device positions are checked by the caller; never read past the table
   const int64_t trow = pm * half;
-  const int64_t c = j.cos_tab[trow + i], s = j.sin_tab[trow + i];
+  // i16 operands: |a c| + |b s| < 2^31 (32-bit), and the quant of an i16 is exact in double
+  const int32_t c = j.cos_tab[trow + i], s = j.sin_tab[trow + i];
   const int64_t o = m * (int64_t)j.H * j.D + (int64_t)h * j.D;
-  const int64_t a = j.x[m * j.ldx + h * j.D + i], b = j.x[m * j.ldx + h * j.D + half + i];
-  const int16_t y1 = (int16_t)sat16(rshr(a * c - b * s, 14));
-  const int16_t y2 = (int16_t)sat16(rshr(b * c + a * s, 14));
+  const int32_t a = j.x[m * j.ldx + h * j.D + i], b = j.x[m * j.ldx + h * j.D + half + i];
+  const int16_t y1 = (int16_t)min(max(rshr32(a * c - b * s, 14), -32768), 32767);
+  const int16_t y2 = (int16_t)min(max(rshr32(b * c + a * s, 14), -32768), 32767);
   j.y[o + i] = y1;
   j.y[o + half + i] = y2;
-  const int8_t q1 = (int8_t)sat8(mulshift(y1, j.qM, j.qS)), q2 = (int8_t)sat8(mulshift(y2, j.qM, j.qS));
+  const double sq = mulshift_scale(j.qM, j.qS);
+  const int8_t q1 = (int8_t)mulshift_small_sat(y1, sq, -128.0, 127.0);
+  const int8_t q2 = (int8_t)mulshift_small_sat(y2, sq, -128.0, 127.0);
   j.yq[o + i] = q1;
   j.yq[o + half + i] = q2;
   if (j.kc && pm < j.max_seq) {  // never write past a cache
@@ -215,12 +221,13 @@ __device__ __forceinline__ void rope_quant_one(const RopeJob& j, int64_t idx) {
 // RoPE then quant of the rotated rows in one pass (golden.py:141-158, 119-120); for key rows also
 // the layer's kv_write (golden.py:344-351): the quantised keys and the v rows into the caches at
 // their positions.  Thread per (row, head, i < D/2) of job a, then of job b (b.total = 0: none).
+template <class IDX>
 __global__ void rope_quant_kernel(RopeJob a, RopeJob b) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx < a.total)
-    rope_quant_one(a, idx);
-  else if (idx < a.total + b.total)
-    rope_quant_one(b, idx - a.total);
+  const IDX idx = (IDX)blockIdx.x * (IDX)blockDim.x + (IDX)threadIdx.x;
+  if (idx < (IDX)a.total)
+    rope_quant_one<IDX>(a, idx);
+  else if (idx < (IDX)(a.total + b.total))
+    rope_quant_one<IDX>(b, idx - (IDX)a.total);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -533,7 +540,10 @@ static int rope_job(const llhip_rope_quant_desc& d, RopeJob& j) {
 static int rope_launch(const RopeJob& a, const RopeJob& b, void* stream) {
   const int64_t total = a.total + b.total;
   if (total == 0) return 0;
-  hipLaunchKernelGGL(rope_quant_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, a, b);
+  if (total + 256 < (int64_t)UINT32_MAX)
+    hipLaunchKernelGGL(rope_quant_kernel<uint32_t>, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, a, b);
+  else
+    hipLaunchKernelGGL(rope_quant_kernel<int64_t>, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, a, b);
   LLHIP_LAUNCH_CHECK();
   return 0;
 }
