@@ -637,11 +637,12 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
       for (int d = lane; d < D; d += 64) ss += (uint64_t)(uint32_t)(hres[m * D + d] * hres[m * D + d]);
       ss = wave_sum_u64(ss);
       const uint32_t inv = rms_inv(ss, (uint32_t)p.nrm_eps[role], (uint32_t)p.nrm_C[role]);
+      const double sy = rms_scale(inv, (int)p.nrm_sh[role]);  // exact double form of rms_apply
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = lane + 64 * i;
         if (d >= D) break;
-        const int16_t y = rms_apply(hres[m * D + d], hg[i], inv, (int)p.nrm_sh[role]);
+        const int16_t y = (int16_t)rms_apply_d(hres[m * D + d], hg[i], sy);
         p.nrm_out[role][(int64_t)m * Nrole + base + d] = y;
         hres[m * D + d] = y;
       }
