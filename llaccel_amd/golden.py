@@ -349,12 +349,21 @@ def exact_blas_matmul(a: np.ndarray, w: np.ndarray, chunk_rows: int = 1024) -> n
     wmax = max(abs(int(wi.min)), abs(int(wi.max)))
     if a.shape[1] * amax * wmax > (1 << 53):
         raise ValueError("integer dot product exceeds exact FP64 accumulation bound")
-    if w.dtype != np.int8:
-        raise ValueError("exact_blas_matmul: weights must be int8 (NUMERICS.md i8pc)")
     M, K = a.shape
     N = w.shape[0]
-    out = _t().empty((M, N), dtype=_t().int64, device=_dev())
-    ad, wd = _up(a), _up(w, np.int8)
+    torch = _t()
+    if w.dtype != np.int8 and (int(w.min(initial=0)) < -128 or int(w.max(initial=0)) > 127):
+        # weights beyond int8 (any integer dtype, as the reference accepts): FP64 products and sums of
+        # integers whose partial sums stay below 2^53 -- the bound checked above -- are exact, which is
+        # the reference's own method (golden.py:226-240); here on the GPU through the library's FP64 GEMM
+        af = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float64)).to(_dev())
+        wf = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float64)).to(_dev())
+        out = torch.empty((M, N), dtype=torch.int64, device=_dev())
+        for r0 in range(0, M, chunk_rows):
+            out[r0:r0 + chunk_rows] = torch.matmul(af[r0:r0 + chunk_rows], wf.T.contiguous()).round().to(torch.int64)
+        return _down(out)
+    out = torch.empty((M, N), dtype=torch.int64, device=_dev())
+    ad, wd = _up(a), _up(w, np.int8)  # int8-valued weights of a wider dtype convert exactly
     _lib.call("llhip_exact_matmul", _ptr(ad), M, K, _ptr(wd), N, _ptr(out), _stream())
     return _down(out)
 

@@ -143,6 +143,13 @@ def test_exact_blas_matmul():
         a[0, :] = -32768
         w[0, :] = -128
         assert np.array_equal(G.exact_blas_matmul(a, w, 17), a @ w.astype(np.int64).T)
+    # any integer weight dtype, as the reference accepts (golden.py:226): int8-valued int32 weights, and
+    # int16 weights beyond int8 (the FP64 path, exact under the 2^53 bound)
+    a = RNG.integers(-1000, 1000, (5, 300), dtype=np.int64)
+    for w in (RNG.integers(-128, 128, (70, 300)).astype(np.int32),
+              RNG.integers(-32768, 32768, (70, 300)).astype(np.int16)):
+        w[0, 0] = np.iinfo(w.dtype).min if w.dtype == np.int16 else -128
+        assert np.array_equal(G.exact_blas_matmul(a, w, 3), a @ w.astype(np.int64).T), w.dtype
     with pytest.raises(ValueError, match="bound"):
         G.exact_blas_matmul(np.array([[2**53]], np.int64), np.array([[127]], np.int8))
     with pytest.raises(ValueError, match="integer"):
