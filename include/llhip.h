@@ -124,7 +124,9 @@ int llhip_linear(const int8_t* A, int64_t M, int64_t K, int64_t lda, const int8_
 /* golden.py:316-342 (silu and mul epilogues) + 119-120  the gate and up projections of an MLP over
  * M rows in one launch: sg = silu16(requant16(A . Wg^T + bg)), f = sat16(rshr(requant16(A . Wu^T +
  * bu) * sg, mul_sh)), fq = quant(f), outputs [M][ld] (i16, i16, i8) -- the values of the gate
- * linear, the up linear and the quant run one by one. */
+ * linear, the up linear and the quant run one by one.  sg_out and f_out may be NULL (those rows
+ * are then not written) when K % 64 == 0, lda % 16 == 0 and A, Wg, Wu are 16-byte aligned (the
+ * one-launch path), and are an error otherwise.  fq_out is always required. */
 typedef struct llhip_gate_up_desc {
   const void* A;  /* i8 [M][lda] */
   int64_t M, K, lda;

@@ -1098,6 +1098,7 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
   __syncthreads();
   const double smul = mulshift_scale(p.Mi, p.Si), fqs = mulshift_scale(d.fqM, d.fqS);
   const bool vec = d.ld % 4 == 0 && (uintptr_t)d.sg % 8 == 0 && (uintptr_t)d.f % 8 == 0 && (uintptr_t)d.fq % 4 == 0;
+  const bool keep_sg = d.sg != nullptr, keep_f = d.f != nullptr;  // NULL: that intermediate is not written
   constexpr int QPR = GN / 4;  // column quads per row
   for (int q = tid; q < GM * QPR; q += 512) {
     const int ml = q / QPR, nl = (q % QPR) * 4, m = m0 + ml, n = n0 + nl;
@@ -1115,16 +1116,16 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
     }
     const int64_t o = (int64_t)m * d.ld + n;
     if (vec && n + 4 <= p.N) {
-      *reinterpret_cast<v2i*>(d.sg + o) = v2i{pack16(sg[0], sg[1]), pack16(sg[2], sg[3])};
-      *reinterpret_cast<v2i*>(d.f + o) = v2i{pack16(f[0], f[1]), pack16(f[2], f[3])};
+      if (keep_sg) *reinterpret_cast<v2i*>(d.sg + o) = v2i{pack16(sg[0], sg[1]), pack16(sg[2], sg[3])};
+      if (keep_f) *reinterpret_cast<v2i*>(d.f + o) = v2i{pack16(f[0], f[1]), pack16(f[2], f[3])};
       *reinterpret_cast<uint32_t*>(d.fq + o) = (uint32_t)(fq[0] & 255) | (uint32_t)(fq[1] & 255) << 8 |
                                                (uint32_t)(fq[2] & 255) << 16 | (uint32_t)(fq[3] & 255) << 24;
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (n + e < p.N) {
-          d.sg[o + e] = (int16_t)sg[e];
-          d.f[o + e] = (int16_t)f[e];
+          if (keep_sg) d.sg[o + e] = (int16_t)sg[e];
+          if (keep_f) d.f[o + e] = (int16_t)f[e];
           d.fq[o + e] = (int8_t)fq[e];
         }
     }
@@ -1590,8 +1591,7 @@ extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {
   if (M < 0 || K < 0 || N < 0 || M > INT32_MAX || N > INT32_MAX || d->lda < K || d->ld < N)
     return fail(-EINVAL, "gate_up: bad shape");
   if (K > 65535) return fail(-EINVAL, "linear: K=%lld exceeds the int32 accumulator bound 65535", (long long)K);
-  if (!d->A || !d->Wg || !d->Wu || !d->rqg || !d->rqu || !d->sg_out || !d->f_out || !d->fq_out)
-    return fail(-EINVAL, "gate_up: null operand");
+  if (!d->A || !d->Wg || !d->Wu || !d->rqg || !d->rqu || !d->fq_out) return fail(-EINVAL, "gate_up: null operand");
   if (!u32_ok(d->silu_Mi) || !shift_ok(d->silu_Si) || !shift_ok(d->silu_sh) || !shift_ok(d->mul_sh) ||
       !u32_ok(d->fq_M) || !shift_ok(d->fq_S))
     return fail(-EINVAL, "gate_up: parameter out of range");
@@ -1610,6 +1610,9 @@ extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {
   const bool fits = K % 64 == 0 && K > 0 && d->lda % 16 == 0 && (uintptr_t)d->A % 16 == 0 && (uintptr_t)d->Wg % 16 == 0 &&
                     (uintptr_t)d->Wu % 16 == 0;
   if (!fits) {  // the three ops one by one
+    if (!d->sg_out || !d->f_out)
+      return fail(-EINVAL, "gate_up: sg_out and f_out may be NULL only when K %% 64 == 0 and A, lda, Wg, Wu are "
+                           "16-byte aligned");
     p.W = static_cast<const int8_t*>(d->Wg);
     p.rq = static_cast<const int32_t*>(d->rqg);
     p.bias = static_cast<const int32_t*>(d->bg);

@@ -172,6 +172,11 @@ class _GateUpStep:
     def __init__(self, model, g, u, q):
         self.model, self.g, self.u, self.q = model, g, u, q
         self.desc = _lib.GateUpDesc()
+        # the gate output is read only by the up linear (its aux) and the up output only by the
+        # quant: in a launch that collects no activations (model._lean) neither is written
+        # (llhip_gate_up takes NULL for them on its one-launch path, K % 64 == 0)
+        self.lean_ok = (int(g["K"]) % 64 == 0 and _reads(model, g["out"]) == 1 and _reads(model, u["out"]) == 1
+                        and model.q.output_name not in (g["out"], u["out"]))
 
     def __call__(self, M, pos, pd=None):
         m, g, u, q, d = self.model, self.g, self.u, self.q, self.desc
@@ -186,7 +191,14 @@ class _GateUpStep:
         d.silu_Mi, d.silu_Si, d.silu_sh = int(s["Mi"]), int(s["Si"]), int(s["sh_out"])
         d.mul_sh, d.fq_M, d.fq_S = int(u["aux_shift"]), int(q["M"]), int(q["S"])
         d.sg_out, d.f_out, d.fq_out = _vp(sg), _vp(m._buf(u["out"])), _vp(m._buf(q["out"]))
+        if self.lean_ok and getattr(m, "_lean", False):
+            d.sg_out = d.f_out = None
         _lib.call("llhip_gate_up", ctypes.byref(d), m._stream_handle())
+
+
+def _reads(model, name: str) -> int:
+    """How many ops of the model's op list read activation `name`."""
+    return sum(1 for o in model.q.ops for k, v in o.items() if k not in ("op", "out") and isinstance(v, str) and v == name)
 
 
 def _gate_up(model, ops, i):

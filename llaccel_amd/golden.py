@@ -444,6 +444,7 @@ class GoldenModel:
         self._ws = torch.zeros(int(_lib.lib().llhip_workspace_bytes()), dtype=torch.uint8, device=self.device)
         self._act: dict[str, object] = {}
         self._cap = 0
+        self._lean = False  # set while a launch collects no activations (llaccel_amd.fusion)
         self._act_spec: dict[str, tuple[str, int]] = {}
         self._pf_graphs: dict = {}  # whole-prompt prefill graphs by (rows, prompt length, KV slot)
         self._pf_seen: dict = {}
@@ -925,6 +926,13 @@ class GoldenModel:
         ~300 kernel launches are enqueued by the host in about as long as the GPU runs them, so
         the second prefill of a (rows, prompt length, KV slot) shape captures them in a HIP graph
         and every later one replays it, after copying the token ids into the graph's buffer."""
+        self._lean = True  # no activation is collected here: dead intermediates go unwritten
+        try:
+            self._prefill_launch_rows(tokens, M)
+        finally:
+            self._lean = False
+
+    def _prefill_launch_rows(self, tokens, M: int) -> None:
         key = (M, len(tokens), self._slot)
         if not self.use_graph:
             self._launch_tokens(tokens, 0, M)

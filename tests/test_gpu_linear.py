@@ -232,6 +232,16 @@ def test_gate_up_equals_the_three_ops(M, K, N, pad, par):
         assert np.array_equal(g_[:, :N], w_) and not g_[:, N:].any()
     if par == 0:
         assert np.count_nonzero(f) > f.size // 2  # the products are not degenerate
+    # NULL gate and up outputs: only the quantised product is written, the same one; the
+    # op-by-op fallback (K % 64 != 0) needs them and refuses NULL
+    fq2 = t.zeros((M, ld), dtype=t.int8, device="cuda")
+    d.sg_out, d.f_out, d.fq_out = None, None, ptr(fq2)
+    if K % 64:
+        with pytest.raises(ValueError, match="may be NULL only"):
+            _lib.call("llhip_gate_up", ctypes.byref(d), stream())
+    else:
+        _lib.call("llhip_gate_up", ctypes.byref(d), stream())
+        assert np.array_equal(fq2.cpu().numpy(), got[2])
 
 
 @pytest.mark.parametrize("M,K,N", [(512, 4864, 896), (300, 2048, 576), (300, 896, 896), (40, 896, 896)])
