@@ -1471,6 +1471,13 @@ static int launch_linear_group(const LinearArgs& base, const llhip_linear_proble
     }
     return 0;
   }
+  // 64x64 tiles while they take one round of workgroups (each workgroup streams half the W rows per
+  // K tile), else 64x128
+  const int mblocks = (int)ceil_div(base.M, 64), cus = current_cu_count();
+  int64_t n64 = 0;
+  for (int q = 0; q < count; ++q) n64 += ceil_div(pr[q].N, 64);
+  const bool narrow = base.K % 128 == 0 && mblocks * n64 <= cus;
+  const int gn = narrow ? 64 : 128;
   LinearGroup g{};
   g.count = count;
   g.nb0[0] = 0;
@@ -1482,11 +1489,13 @@ static int launch_linear_group(const LinearArgs& base, const llhip_linear_proble
     g.ldo[q] = pr[q].ldo;
     g.N[q] = (int)pr[q].N;
     g.out8[q] = pr[q].out_i8 ? 1 : 0;
-    g.nb0[q + 1] = g.nb0[q] + (int)ceil_div(pr[q].N, 128);
+    g.nb0[q + 1] = g.nb0[q] + (int)ceil_div(pr[q].N, gn);
   }
-  const int mblocks = (int)ceil_div(base.M, 64);
   const dim3 grid((unsigned)(ceil_div((int64_t)mblocks * g.nb0[count], 8) * 8));
-  if (base.K % 128 == 0 && grid.x < (unsigned)current_cu_count()) {
+  if (narrow) {
+    using T = MfmaTile<64, 64, 4, 128, 3>;
+    hipLaunchKernelGGL((linear_mfma_group<64, 64, 4, 128, 3>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
+  } else if (base.K % 128 == 0 && grid.x < (unsigned)cus) {
     using T = MfmaTile<64, 128, 4, 128, 3>;
     hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 128, 3>), grid, dim3(T::NT), T::LDS_BYTES, s, base, g, mblocks);
   } else if (base.K % 128 == 0) {
