@@ -1380,13 +1380,14 @@ static int launch_mfma_shape(LinearArgs& p, void* ws, hipStream_t stream, const 
       return launch_mfma<EPI, OUT8, 256, 256, 8, KT>(p, ws, stream);
   }
   // 128x128 tiles while they fill the CUs, else 64x128 tiles (twice as many workgroups, three per
-  // CU), or 64x64 tiles while those still take one round of workgroups (each workgroup streams
+  // CU), or 64x64 tiles while those take at most two rounds of workgroups (each workgroup streams
   // half the W rows per K tile: 512 x 896 x 896 7.9 -> 6.0 us, 512 x 4864 x 896 split along K
-  // 15.6 -> 14.0 us); split along K when even those are too few
+  // 15.6 -> 14.0 us, 2048 x 896 x 896 7.7 -> 6.9 us, 2048 x 4864 x 896 27.6 -> 25.3 us); split
+  // along K when even those are too few
   const int cus = current_cu_count();
   if ((int64_t)ceil_div(p.M, 128) * ceil_div(p.N, 128) >= cus)
     return launch_mfma<EPI, OUT8, 128, 128, 4, KT>(p, ws, stream, norm, norm_done);
-  if ((int64_t)ceil_div(p.M, 64) * ceil_div(p.N, 64) <= cus)
+  if ((int64_t)ceil_div(p.M, 64) * ceil_div(p.N, 64) <= 2ll * cus)
     return launch_mfma<EPI, OUT8, 64, 64, 4, KT>(p, ws, stream, norm, norm_done);
   return launch_mfma<EPI, OUT8, 64, 128, 4, KT>(p, ws, stream, norm, norm_done);
 }

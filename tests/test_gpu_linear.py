@@ -132,11 +132,12 @@ def test_large_gemm_path_ragged_with_epilogues(epilogue, out_i8):
 @pytest.mark.parametrize("epilogue,out_i8", [("none", True), ("none", False), ("resadd", False), ("silu", False),
                                              ("mul", False)])
 @pytest.mark.parametrize("M,K,N", [(512, 4864, 896), (300, 2048, 900), (2048, 4864, 896), (130, 4864, 130),
-                                   (512, 896, 896), (33, 256, 130)])
+                                   (512, 896, 896), (33, 256, 130), (2048, 256, 1152)])
 def test_split_k_gemm(M, K, N, epilogue, out_i8):
     """Prompt-sized GEMMs with too few output tiles for the GPU take the split-K path (int32
     partial planes in the workspace, summed by a second kernel): equal to the oracle and to the
-    unsplit kernel (no workspace), with a full-range bias and every epilogue; ragged M and N."""
+    unsplit kernel (no workspace), with a full-range bias and every epilogue; ragged M and N.  The
+    2048-row shapes have tiles enough and run unsplit: 64x64 tiles (N = 896), 64x128 (N = 1152)."""
     rng = np.random.default_rng(M + K + N + len(epilogue) + out_i8)
     a, w, rq = _operands(rng, M, K, N, out_i8=out_i8)
     bias = rng.integers(-(2**31), 2**31 - 1, N)
