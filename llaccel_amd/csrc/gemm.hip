@@ -1380,14 +1380,16 @@ static int launch_mfma_shape(LinearArgs& p, void* ws, hipStream_t stream, const 
       return launch_mfma<EPI, OUT8, 256, 256, 8, KT>(p, ws, stream);
   }
   // 128x128 tiles while they fill the CUs, else 64x128 tiles (twice as many workgroups, three per
-  // CU), or 64x64 tiles while those take at most two rounds of workgroups (each workgroup streams
-  // half the W rows per K tile: 512 x 896 x 896 7.9 -> 6.0 us, 512 x 4864 x 896 split along K
-  // 15.6 -> 14.0 us, 2048 x 896 x 896 7.7 -> 6.9 us, 2048 x 4864 x 896 27.6 -> 25.3 us); split
+  // CU), or 64x64 tiles (each workgroup streams half the W rows per K tile) while those take one
+  // round of workgroups (512 x 896 x 896 7.9 -> 6.0 us, 512 x 4864 x 896 split along K 15.6 ->
+  // 14.0 us), or two for a short K, where 64x128 tiles would run unsplit (2048 x 896 x 896 7.3 ->
+  // 6.6 us; at K = 4864 two rounds of them lose to 64x128 split along K, 29.6 vs 25.9 us); split
   // along K when even those are too few
   const int cus = current_cu_count();
   if ((int64_t)ceil_div(p.M, 128) * ceil_div(p.N, 128) >= cus)
     return launch_mfma<EPI, OUT8, 128, 128, 4, KT>(p, ws, stream, norm, norm_done);
-  if ((int64_t)ceil_div(p.M, 64) * ceil_div(p.N, 64) <= 2ll * cus)
+  const int64_t t64 = (int64_t)ceil_div(p.M, 64) * ceil_div(p.N, 64);
+  if (t64 <= cus || (t64 <= 2ll * cus && p.K <= 1024))
     return launch_mfma<EPI, OUT8, 64, 64, 4, KT>(p, ws, stream, norm, norm_done);
   return launch_mfma<EPI, OUT8, 64, 128, 4, KT>(p, ws, stream, norm, norm_done);
 }

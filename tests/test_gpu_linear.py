@@ -137,7 +137,7 @@ def test_split_k_gemm(M, K, N, epilogue, out_i8):
     """Prompt-sized GEMMs with too few output tiles for the GPU take the split-K path (int32
     partial planes in the workspace, summed by a second kernel): equal to the oracle and to the
     unsplit kernel (no workspace), with a full-range bias and every epilogue; ragged M and N.  The
-    2048-row shapes have tiles enough and run unsplit: 64x64 tiles (N = 896), 64x128 (N = 1152)."""
+    2048-row shapes: K = 4864 on 64x128 tiles split along K, K = 256 on 64x128 tiles unsplit."""
     rng = np.random.default_rng(M + K + N + len(epilogue) + out_i8)
     a, w, rq = _operands(rng, M, K, N, out_i8=out_i8)
     bias = rng.integers(-(2**31), 2**31 - 1, N)
