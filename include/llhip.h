@@ -379,6 +379,60 @@ int llhip_dec_greedy(const void* keys, int64_t nkeys, int32_t* token, int32_t* p
                      int32_t* ring_tokens, int64_t ring_cap, const int16_t* embed, int64_t dim, int16_t* row,
                      void* stream);
 
+/* ---- decode step: every layer of one decode row in one launch ----
+ * golden.py:392-397 (decode) running golden.py:275-314 over the layers of a fused graph whose every
+ * layer is  rmsnorm, quant, linear q/k/v (+bias), rope q/k, quant q/k, kv_write, attention,
+ * linear o (resadd), rmsnorm, quant, linear gate (silu), linear up (mul), quant, linear down
+ * (resadd)  -- the layers of the decode chain above, without Q/K norm, head_dim 64 or 128.
+ * One persistent workgroup per CU computes its fixed share of each stage (q/k/v columns, an
+ * attention head slice with its output-projection partial sums, FFN columns with their
+ * down-projection partial sums) and hands results to the next stage's workgroups through
+ * device-scope flags; each workgroup's weights for a stage are requested before it waits for
+ * the stage's input.  Every wait is bounded: a timed-out wait records an error (read with
+ * llhip_dec_step_status) and the launch ends.  The KV caches receive the row's keys and values;
+ * the last layer's down projection is left as int32 partial sums (llhip_dec_step_outputs) for
+ * llhip_dec_finish, with the residual row it adds to.  No other activation is written. */
+typedef struct llhip_step_layer {
+  const void* g1; int64_t eps1, C1, sh1, Mq1, Sq1; /* attention rmsnorm + quant */
+  const void* W[3]; const void* rq[3]; const void* bias[3]; /* q, k, v (bias NULL when absent) */
+  int64_t quant_M[2], quant_S[2]; /* quant of rope(q), rope(k) */
+  void* kc; void* vc;             /* int8 caches [Hkv][max_seq][D] */
+  int64_t Ms, Ss, Mo, So, prob_bits;
+  const void* wo_panel;           /* i8 [H][dim][D]: W_o[n][h*D + d] at [h][n][d] */
+  const void* rq_o; const void* bias_o;
+  const void* g2; int64_t eps2, C2, sh2, Mq2, Sq2; /* mlp rmsnorm + quant */
+  const void* Wg; const void* Wu; const void* rqg; const void* rqu; const void* bg; const void* bu;
+  int64_t silu_Mi, silu_Si, silu_sh, mul_sh, fq_M, fq_S;
+  const void* wd_panel;           /* i8 [F/16][dim][16]: W_d[n][16b + j] at [b][n][j] */
+  const void* rq_d; const void* bias_d;
+} llhip_step_layer;
+
+typedef struct llhip_dec_step_desc {
+  const llhip_step_layer* layers; /* host array of L layers (copied by create) */
+  int64_t L, dim, H, Hkv, D, F, max_seq;
+  const void* x_in;               /* i16 [dim] the launch's input row */
+  const void* cos_tab; const void* sin_tab; /* i16 [max_seq][D/2] */
+  const void* pos_dev;            /* int32 device position of the row */
+} llhip_dec_step_desc;
+
+typedef struct llhip_dec_step llhip_dec_step;
+/* golden.py:246-273 (GoldenModel over the qgraph's layers) -- validate the graph shape and allocate
+ * the step's device state (zero-filled).  Returns NULL with llhip_last_error() set when the shape is
+ * not supported. */
+llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d);
+/* golden.py:392-397 + 275-314 -- one decode row through every layer (stream-ordered; capturable in a
+ * graph).  The row's input is x_in at position *pos_dev. */
+int llhip_dec_step_run(llhip_dec_step* s, void* stream);
+/* golden.py:316-342 (the last layer's resadd down projection, finished by llhip_dec_finish) -- device
+ * pointers valid for the step's lifetime: *acc = int32 [8][dim], its partial sums after a run;
+ * *resid = i16 [dim], the residual row it adds to. */
+int llhip_dec_step_outputs(llhip_dec_step* s, void** acc, void** resid);
+/* golden.py:392-397 -- synchronous: *launches = completed launches, *err = nonzero when a launch hit
+ * a bounded-wait timeout (sticky: later launches end at once). */
+int llhip_dec_step_status(llhip_dec_step* s, int64_t* launches, int64_t* err);
+/* golden.py:246-273 -- release what llhip_dec_step_create allocated. */
+void llhip_dec_step_destroy(llhip_dec_step* s);
+
 /* ---- the reference accelerator's instruction set on the GPU ----
  * A device holding the ISA's DRAM and 1 MiB SRAM in GPU memory that runs .llbin programs (docs/ISA.md,
  * binary version 2) with the functional simulator's semantics and performance counters.  Errors

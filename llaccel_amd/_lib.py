@@ -203,3 +203,31 @@ _SIGS.update({
     "llhip_dec_greedy": [_p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],
 })
 _RESTYPES["llhip_dec_head_keys"] = _i64
+
+
+# ---- decode step (include/llhip.h: llhip_dec_step_*) -------------------------------------
+class StepLayer(ctypes.Structure):
+    _fields_ = [("g1", _p), ("eps1", _i64), ("C1", _i64), ("sh1", _i64), ("Mq1", _i64), ("Sq1", _i64),
+                ("W", _p * 3), ("rq", _p * 3), ("bias", _p * 3), ("quant_M", _i64 * 2), ("quant_S", _i64 * 2),
+                ("kc", _p), ("vc", _p), ("Ms", _i64), ("Ss", _i64), ("Mo", _i64), ("So", _i64), ("prob_bits", _i64),
+                ("wo_panel", _p), ("rq_o", _p), ("bias_o", _p), ("g2", _p), ("eps2", _i64), ("C2", _i64),
+                ("sh2", _i64), ("Mq2", _i64), ("Sq2", _i64), ("Wg", _p), ("Wu", _p), ("rqg", _p), ("rqu", _p),
+                ("bg", _p), ("bu", _p), ("silu_Mi", _i64), ("silu_Si", _i64), ("silu_sh", _i64), ("mul_sh", _i64),
+                ("fq_M", _i64), ("fq_S", _i64), ("wd_panel", _p), ("rq_d", _p), ("bias_d", _p)]
+
+
+class DecStepDesc(ctypes.Structure):
+    _fields_ = [("layers", ctypes.POINTER(StepLayer)), ("L", _i64), ("dim", _i64), ("H", _i64), ("Hkv", _i64),
+                ("D", _i64), ("F", _i64), ("max_seq", _i64), ("x_in", _p), ("cos_tab", _p), ("sin_tab", _p),
+                ("pos_dev", _p)]
+
+
+_SIGS.update({
+    "llhip_dec_step_create": [ctypes.POINTER(DecStepDesc)],
+    "llhip_dec_step_run": [_p, _p],
+    "llhip_dec_step_outputs": [_p, ctypes.POINTER(_p), ctypes.POINTER(_p)],
+    "llhip_dec_step_status": [_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
+    "llhip_dec_step_destroy": [_p],
+})
+_RESTYPES["llhip_dec_step_create"] = _p
+_RESTYPES["llhip_dec_step_destroy"] = None

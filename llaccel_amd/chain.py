@@ -20,6 +20,12 @@ is the one the separate launches write.
 The chain exists only for graphs whose every layer has that shape; other graphs keep the fused
 plan.  The kernels read the output projections in panel layouts made once on the device:
 wo as [H][dim][D] (a head's K range contiguous) and wd as [FFN/16][dim][16].
+
+Decode step: for a launch at a device position (the decode loop) whose layers have no Q/K norm and
+head_dim 64 or 128, all layers run as one persistent launch instead (llhip_dec_step: the same three
+stages per layer, handed between workgroups inside the launch), followed by the same finish, head
+and greedy launches.  It writes the KV caches and the last layer's residual row and partial sums,
+not the other activations, so launches that collect activations keep the three launches per layer.
 """
 from __future__ import annotations
 
@@ -74,15 +80,111 @@ class Chain:
             self.wd_panel.append(pad.view(self.dim, Fp // 16, 16).permute(1, 0, 2).contiguous())
         self._resid = _lib.ResidDesc()
         self._att = _lib.DecAttnDesc()
+        self.use_step = True  # one-launch decode step where the graph allows it (llhip_dec_step)
+        self._step = None
+        self._step_key = None
+        self.step_unsupported = None  # the reason llhip_dec_step_create gave, once it refused
+
+    def __del__(self):
+        st = getattr(self, "_step", None)
+        if st:
+            try:
+                _lib.lib().llhip_dec_step_destroy(st)
+            except Exception:
+                pass
+
+    # ---- the one-launch decode step ---------------------------------------------------------
+    def _step_layer(self, i, ly, pd):
+        m = self.model
+        dt = m._dt
+        t = _lib.StepLayer()
+        fa, fm = ly.attn_in, ly.mlp
+        fa.fill(fa.desc, 1, 0, pd)
+        fm.fill(fm.desc, 1, 0, pd)
+        if fa.desc.has_norm:
+            return None
+        a, f = fa.desc, fm.desc
+        t.g1, t.eps1, t.C1, t.sh1, t.Mq1, t.Sq1 = a.pre.gamma, a.pre.eps_t, a.pre.C, a.pre.sh_post, a.pre.Mq, a.pre.Sq
+        for r in range(3):
+            t.W[r], t.rq[r], t.bias[r] = a.W[r], a.rq[r], a.bias[r]
+        for r in range(2):
+            t.quant_M[r], t.quant_S[r] = a.quant_M[r], a.quant_S[r]
+        t.kc, t.vc = a.kc, a.vc
+        att = ly.att
+        t.Ms, t.Ss, t.Mo, t.So = int(att["Ms"]), int(att["Ss"]), int(att["Mo"]), int(att["So"])
+        t.prob_bits = int(att.get("prob_bits", 8))
+        t.wo_panel = _vp(self.wo_panel[i])
+        t.rq_o = _vp(dt[ly.wo["rq"]])
+        t.bias_o = _vp(dt[ly.wo["bias"]]) if ly.wo.get("bias") else None
+        t.g2, t.eps2, t.C2, t.sh2, t.Mq2, t.Sq2 = f.pre.gamma, f.pre.eps_t, f.pre.C, f.pre.sh_post, f.pre.Mq, f.pre.Sq
+        t.Wg, t.Wu, t.rqg, t.rqu, t.bg, t.bu = f.Wg, f.Wu, f.rqg, f.rqu, f.bg, f.bu
+        t.silu_Mi, t.silu_Si, t.silu_sh, t.mul_sh, t.fq_M, t.fq_S = (f.silu_Mi, f.silu_Si, f.silu_sh, f.mul_sh,
+                                                                     f.fq_M, f.fq_S)
+        t.wd_panel = _vp(self.wd_panel[i])
+        t.rq_d = _vp(dt[ly.wd["rq"]])
+        t.bias_d = _vp(dt[ly.wd["bias"]]) if ly.wd.get("bias") else None
+        return t
+
+    def step(self, pd):
+        """The llhip_dec_step handle for launches at the device position pd (created on first use),
+        or None when the graph's shape is outside it (the reason is kept in step_unsupported)."""
+        if not self.use_step or not isinstance(pd, ctypes.c_void_p) or not pd.value or self.step_unsupported:
+            return None
+        m = self.model
+        # the handle holds the cache, input-row and position addresses of its creation
+        key = (pd.value, getattr(m, "_kv_gen", 0), m._slot, m._act[m.q.input_name].data_ptr())
+        if self._step is not None and self._step_key == key:
+            return self._step
+        if _torch().cuda.is_current_stream_capturing():
+            return None  # creating one allocates: never inside a graph capture
+        L = len(self.layers)
+        arr = (_lib.StepLayer * L)()
+        for i, ly in enumerate(self.layers):
+            t = self._step_layer(i, ly, pd)
+            if t is None:
+                self.step_unsupported = "Q/K norm"
+                return None
+            arr[i] = t
+        a0, f0 = self.layers[0].att, self.layers[0].mlp.desc
+        d = _lib.DecStepDesc()
+        d.layers, d.L, d.dim = arr, L, self.dim
+        d.H, d.Hkv, d.D, d.F, d.max_seq = int(a0["H"]), int(a0["Hkv"]), int(a0["D"]), int(f0.N), m.max_seq
+        d.x_in = _vp(m._act[m.q.input_name])
+        d.cos_tab, d.sin_tab, d.pos_dev = _vp(m._dt["rope_cos"]), _vp(m._dt["rope_sin"]), pd
+        lib = _lib.lib()
+        h = lib.llhip_dec_step_create(ctypes.byref(d))
+        if not h:
+            self.step_unsupported = (lib.llhip_last_error() or b"").decode() or "unsupported"
+            return None
+        if self._step:
+            lib.llhip_dec_step_destroy(self._step)
+        self._step, self._step_key = h, key
+        acc, res = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.call("llhip_dec_step_outputs", h, ctypes.byref(acc), ctypes.byref(res))
+        self._step_acc, self._step_res = acc, res
+        return h
+
+    def check_step(self):
+        """Raise if a decode-step launch hit its bounded-wait timeout (synchronises the device)."""
+        if not self._step:
+            return
+        n, err = ctypes.c_int64(), ctypes.c_int64()
+        _lib.call("llhip_dec_step_status", self._step, ctypes.byref(n), ctypes.byref(err))
+        if err.value:
+            self.use_step = False
+            self.model._graph = None  # a captured decode graph holds the step's launch
+            raise RuntimeError(f"decode step: a hand-off wait timed out (error word {err.value}); "
+                               "the step is disabled for this model")
 
     # ---- descriptors ------------------------------------------------------------------------
-    def _fill_resid(self, op, acc, R):
-        """Finishing `op` (linear, resadd) from `acc` [R][dim]."""
+    def _fill_resid(self, op, acc, R, aux=None):
+        """Finishing `op` (linear, resadd) from `acc` [R][dim] (a tensor or a device pointer), adding
+        the residual `aux` (default: the op's aux activation)."""
         m, r = self.model, self._resid
-        r.acc, r.R = _vp(acc), R
+        r.acc, r.R = (acc if isinstance(acc, ctypes.c_void_p) else _vp(acc)), R
         r.rq = _vp(m._dt[op["rq"]])
         r.bias = _vp(m._dt[op["bias"]]) if op.get("bias") else None
-        r.aux = _vp(m._buf(op["aux"]))
+        r.aux = aux if aux is not None else _vp(m._buf(op["aux"]))
         r.x_out = _vp(m._buf(op["out"]))
         return ctypes.byref(r)
 
@@ -129,8 +231,17 @@ class Chain:
         `only` names one family (dec_attn_in, dec_attention, dec_mlp, dec_head) whose launches alone
         run -- a measurement aid: the values they compute are then meaningless."""
         m = self.model
-        for i, ly in enumerate(self.layers):
-            self._launch_layer(i, ly, pos, pd, only)
+        st = self.step(pd) if only in (None, "dec_step", "dec_head") else None
+        if only == "dec_step":
+            if st is None:
+                raise ValueError(f"no decode step for this graph: {self.step_unsupported}")
+            _lib.call("llhip_dec_step_run", st, m._stream_handle())
+            return
+        if st is not None and only is None:
+            _lib.call("llhip_dec_step_run", st, m._stream_handle())
+        elif st is None or only != "dec_head":
+            for i, ly in enumerate(self.layers):
+                self._launch_layer(i, ly, pos, pd, only)
         if only not in (None, "dec_head"):
             return
         fh = self.head
@@ -139,8 +250,11 @@ class Chain:
         # the last down projection finished, normalised and quantised once; the lm_head workgroups
         # read the quantised row
         fh.desc.pre.prequant = 0
-        _lib.call("llhip_dec_finish", ctypes.byref(fh.desc.pre),
-                  self._fill_resid(self.layers[-1].wd, self.acc_wd, WD_ROWS), s)
+        if st is not None:
+            resid = self._fill_resid(self.layers[-1].wd, self._step_acc, WD_ROWS, aux=self._step_res)
+        else:
+            resid = self._fill_resid(self.layers[-1].wd, self.acc_wd, WD_ROWS)
+        _lib.call("llhip_dec_finish", ctypes.byref(fh.desc.pre), resid, s)
         fh.desc.pre.prequant = 1
         if greedy is None:
             _lib.call("llhip_dec_head", ctypes.byref(fh.desc), m.vocab, None, None, None, 0, 0, s)

@@ -514,6 +514,7 @@ class GoldenModel:
         self._graph_b = None
         getattr(self, "_pf_graphs", {}).clear()
         self._slot = 0
+        self._kv_gen = getattr(self, "_kv_gen", 0) + 1  # new cache addresses (llaccel_amd.chain keys on it)
         self._kv: dict[int, tuple] = {}
         for op in self.q.ops:
             if op["op"] == "kv_write":
@@ -995,7 +996,12 @@ class GoldenModel:
         with capture_graph(g):
             self._decode_launch()
         self._graph = g
-        self._graph_chained = self._chained(1)
+        self._graph_chained = self._graph_key()
+
+    def _graph_key(self):
+        """What a captured decode graph depends on: the chain, and the decode step it launched."""
+        ch = self._chain if self._chained(1) else None
+        return (ch is not None, ch._step if ch is not None and ch.use_step else None)
 
     def decode_loop(self, token: int, pos: int, n: int, *, sync: bool = True):
         """Run `n` greedy M=1 decode launches from (token, pos) entirely on the device.
@@ -1015,7 +1021,9 @@ class GoldenModel:
         if self._chained(1):  # the chain's launches gather their next input row themselves
             _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim,
                       ctypes.c_void_p(self._st.data_ptr()), 1, 1, _ptr(self._act[self.q.input_name]), _stream())
-        if self.use_graph and (self._graph is None or self._graph_chained != self._chained(1)):
+        if self._chained(1):  # the decode step's handle is made outside any capture
+            self._chain.step(ctypes.c_void_p(self._st.data_ptr() + 4))
+        if self.use_graph and (self._graph is None or self._graph_chained != self._graph_key()):
             self._capture()
         for _ in range(n):
             if self.use_graph:
@@ -1024,6 +1032,8 @@ class GoldenModel:
                 self._decode_launch()
         if not sync:
             return None
+        if self._chained(1):
+            self._chain.check_step()
         return _down(self._ring_tok[:n]).astype(np.int64), self._ring_rows[:n].cpu().numpy()
 
     def decode_ring(self, n: int):
