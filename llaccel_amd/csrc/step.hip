@@ -42,8 +42,7 @@ constexpr int NTH = 512;    // 4 row waves + 4 weight waves
 constexpr int R = 8;        // accumulator replicas: producer j adds into row j % R
 constexpr int D = 64;       // head_dim of the decode step
 constexpr int DC = D / 16;  // 16-byte chunks per key row
-constexpr int KR = 6;       // key chunks per thread held in registers (512 threads: 768 keys)
-constexpr int VR = 2;       // value chunks per thread held in registers (1024 keys)
+constexpr int KR = 6;       // keys per thread held in registers (512 threads, 4 per key: 768 keys)
 constexpr int PNL = 4;      // output-projection / down-projection panel chunks per row thread
 constexpr int MAX_DIM = 1024;
 constexpr int MAX_G = 256;
@@ -315,7 +314,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
   const bool roww = wave < 4;
   const int rt = tid;   // row thread index (row waves)
   const int w4 = wave - 4;
-  const int dim = a.dim, kst = dim >> 6;
+  const int dim = a.dim;  // 64 KST
   const int u2 = b < a.nu2 ? b : -1;                                // S12 unit
   const int u3 = (b >= a.nu2 && b - a.nu2 < a.nu3) ? b - a.nu2 : -1;  // S3 unit
   const int rep = b % NREP;  // flag replica this workgroup polls
@@ -357,6 +356,10 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
     sn = ld2s(snr, off);
   }
   for (int i = dim + tid; i < KST * 64 + 16; i += NTH) xq[i] = 0;  // K steps past the row multiply zeros
+  if (!roww) {  // blocks that are never loaded (steps past the row, an absent FFN tile) read as zeros
+    int8_t* bw = dyn + (wave - 4) * NB * 1024;
+    for (int i = 16 * lane; i < NB * 1024; i += 1024) *reinterpret_cast<v4i*>(bw + i) = v4i{0, 0, 0, 0};
+  }
   if (tid == 0) sy = Sync{0u, 0u, 0u, 0u, 0u};
   __syncthreads();  // the only workgroup barrier: tables and counters in place
 
@@ -422,30 +425,29 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
 #pragma unroll
       for (int s = 0; s < KST; ++s) {
         const uint32_t k = (uint32_t)(s * 64 + kg * 16);
-        dma16(qr, blk + s * 1024, s < kst ? (uint32_t)(nq * dim) + k : LD_OOB);
-        dma16(kr, blk + (KST + s) * 1024, s < kst ? (uint32_t)(nk * dim) + k : LD_OOB);
+        dma16(qr, blk + s * 1024, (uint32_t)(nq * dim) + k);
+        dma16(kr, blk + (KST + s) * 1024, (uint32_t)(nk * dim) + k);
       }
 #pragma unroll
       for (int i = 0; i < VS; ++i) {
         const int s = w4 * VS + i;
-        dma16(vr, blk + (2 * KST + i) * 1024, s < kst ? (uint32_t)(nv * dim + s * 64 + kg * 16) : LD_OOB);
+        if (s < KST) dma16(vr, blk + (2 * KST + i) * 1024, (uint32_t)(nv * dim + s * 64 + kg * 16));
       }
     };
-    // this thread's cached keys (key t = tid / DC + 128 i, chunk tid % DC) and value slices (key
-    // tid + 512 i) of a layer, positions below T - 1 (the cache rows of earlier launches)
-    v4i kreg[KR], vreg[VR];
-    auto kv_issue = [&](const CLayer& ly) {
+    // Attention layout: thread tid holds chunk kc = tid % 4 (16 key bytes, 4 value bytes of the
+    // slice) of keys t = tid / 4 + 128 i, i < KR: the four threads of a key meet by DPP within a
+    // quad, so scores, probabilities and products never leave the registers.
+    const int kc = tid & 3, k0 = tid >> 2;
+    v4i kreg[KR];
+    int32_t vreg[KR];
+    auto kv_issue = [&](const CLayer& ly) {  // the cache rows of earlier launches (positions < T - 1)
       const Rsrc krr = rsrc(ly.kc + (int64_t)g * a.max_seq * D, (int64_t)a.max_seq * D);
       const Rsrc vrr = rsrc(ly.vc + (int64_t)g * a.max_seq * D, (int64_t)a.max_seq * D);
 #pragma unroll
       for (int i = 0; i < KR; ++i) {
-        const int t = tid / DC + 128 * i;
-        kreg[i] = ld16(krr, t < T - 1 ? (uint32_t)(t * D + 16 * (tid % DC)) : LD_OOB);
-      }
-#pragma unroll
-      for (int i = 0; i < VR; ++i) {
-        const int t = tid + 512 * i;
-        vreg[i] = ld16(vrr, t < T - 1 ? (uint32_t)(t * D + 16 * ds) : LD_OOB);
+        const int t = k0 + 128 * i;
+        kreg[i] = ld16(krr, t < T - 1 ? (uint32_t)(t * D + 16 * kc) : LD_OOB);
+        vreg[i] = ld4(vrr, t < T - 1 ? (uint32_t)(t * D + 16 * ds + 4 * kc) : LD_OOB);
       }
     };
     if (alive) {
@@ -559,22 +561,34 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
           break;
         }
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this layer's blocks (and cached keys)
+        // q tile w and k tile w (all K steps), the v tile's steps w*VS.. (blocks past the row are zero)
         v4i aq = {0, 0, 0, 0}, ak = {0, 0, 0, 0}, av = {0, 0, 0, 0};
+        // four K steps' operands read at once, then their eight products (the LDS latency of a
+        // group is paid once)
 #pragma unroll
-        for (int s = 0; s < KST; ++s) {
-          if (s < kst) {  // (steps past the row hold no loaded block)
-            const v4i xa = *reinterpret_cast<const v4i*>(xq + s * 64 + kg * 16);
-            aq = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, lds16(blk + s * 1024), aq, 0, 0, 0);
-            ak = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, lds16(blk + (KST + s) * 1024), ak, 0, 0, 0);
+        for (int s0 = 0; s0 < KST; s0 += 4) {
+          v4i xa[4], bq[4], bk[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int s = min(s0 + u, KST - 1);
+            xa[u] = *reinterpret_cast<const v4i*>(xq + s * 64 + kg * 16);
+            bq[u] = lds16(blk + s * 1024);
+            bk[u] = lds16(blk + (KST + s) * 1024);
+          }
+          __builtin_amdgcn_sched_barrier(0);  // all twelve reads issued before the first product
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (s0 + u < KST) {
+              aq = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u], bq[u], aq, 0, 0, 0);
+              ak = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u], bk[u], ak, 0, 0, 0);
+            }
           }
         }
 #pragma unroll
         for (int i = 0; i < VS; ++i) {
-          const int s = w4 * VS + i;
-          if (s < kst) {  // (steps past the row hold no loaded block)
-            const v4i xa = *reinterpret_cast<const v4i*>(xq + s * 64 + kg * 16);
-            av = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, lds16(blk + (2 * KST + i) * 1024), av, 0, 0, 0);
-          }
+          const int s = min(w4 * VS + i, KST - 1);  // (a step past the row meets a zero block)
+          const v4i xa = *reinterpret_cast<const v4i*>(xq + s * 64 + kg * 16);
+          av = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, lds16(blk + (2 * KST + i) * 1024), av, 0, 0, 0);
         }
         if (lane < 16) {  // one input row: every output row equals row 0
           gq[16 * w4 + lane] = aq.x;
@@ -589,42 +603,35 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         alive = false;
         break;
       }
-      const v4i qv = *reinterpret_cast<const v4i*>(q8 + 16 * (tid % DC));
+      const v4i qv = *reinterpret_cast<const v4i*>(q8 + 16 * kc);
+      const v4i kn = *reinterpret_cast<const v4i*>(k8 + 16 * kc);
+      const int32_t vnw = *reinterpret_cast<const int32_t*>(vnew + 4 * kc);
+      int32_t sreg[KR];
       int32_t lmax = INT32_MIN;
 #pragma unroll
       for (int i = 0; i < KR; ++i) {
-        const int t = tid / DC + 128 * i;
-        const int32_t s = quad_sum(dot16(qv, kreg[i]));
-        if (tid % DC == 0 && t < T - 1) {
-          sc[t] = s;
-          lmax = max(lmax, s);
-        }
+        const int t = k0 + 128 * i;
+        sreg[i] = quad_sum(dot16(qv, t == T - 1 ? kn : kreg[i]));
+        if (t < T) lmax = max(lmax, sreg[i]);
       }
-      if (KR * 128 < T - 1) {  // keys past the registers (long contexts)
+      if (KR * 128 < T) {  // keys past the registers (long contexts): scores into sc[]
         const Rsrc krr = rsrc(ly.kc + (int64_t)g * a.max_seq * D, (int64_t)a.max_seq * D);
-        for (int tb0 = KR * 128; tb0 < T - 1; tb0 += 4 * 128) {
+        for (int tb0 = KR * 128; tb0 < T; tb0 += 4 * 128) {
           v4i kx[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const int t = tb0 + 128 * u + tid / DC;
-            kx[u] = ld16(krr, t < T - 1 ? (uint32_t)(t * D + 16 * (tid % DC)) : LD_OOB);
+            const int t = tb0 + 128 * u + k0;
+            kx[u] = ld16(krr, t < T - 1 ? (uint32_t)(t * D + 16 * kc) : LD_OOB);
           }
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const int t = tb0 + 128 * u + tid / DC;
-            const int32_t s = quad_sum(dot16(qv, kx[u]));
-            if (tid % DC == 0 && t < T - 1) {
-              sc[t] = s;
+            const int t = tb0 + 128 * u + k0;
+            const int32_t s = quad_sum(dot16(qv, t == T - 1 ? kn : kx[u]));
+            if (t < T) {
+              if (kc == 0) sc[t] = s;
               lmax = max(lmax, s);
             }
           }
-        }
-      }
-      if (tid < DC) {  // the new key at position T - 1
-        const int32_t s = quad_sum(dot16(qv, *reinterpret_cast<const v4i*>(k8 + 16 * tid)));
-        if (tid == 0) {
-          sc[T - 1] = s;
-          lmax = max(lmax, s);
         }
       }
       lmax = wave_max_i32(lmax);
@@ -636,19 +643,20 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       int32_t mx = redmax[0];
 #pragma unroll
       for (int w = 1; w < 8; ++w) mx = max(mx, redmax[w]);
-      // probabilities (golden.py:168-172) of the value layout's keys t = tid + 512 i
-      uint32_t pv[VR];
+      // probabilities (golden.py:168-172); each key's four threads compute it, its first adds it
+      uint32_t pv[KR];
       uint32_t lsum = 0;
 #pragma unroll
-      for (int i = 0; i < VR; ++i) {
-        const int t = tid + 512 * i;
-        pv[i] = t < T ? lut_p(mulshift((int64_t)mx - sc[t], ly.Ms, (int)ly.Ss), ei, ef) : 0u;
-        lsum += pv[i];
+      for (int i = 0; i < KR; ++i) {
+        const int t = k0 + 128 * i;
+        pv[i] = t < T ? lut_p(mulshift((int64_t)mx - sreg[i], ly.Ms, (int)ly.Ss), ei, ef) : 0u;
+        if (kc == 0) lsum += pv[i];
       }
-      for (int t = tid + 512 * VR; t < T; t += 512) {
-        const uint32_t p = lut_p(mulshift((int64_t)mx - sc[t], ly.Ms, (int)ly.Ss), ei, ef);
-        sc[t] = (int32_t)p;
-        lsum += p;
+      if (KR * 128 < T) {
+        for (int t = KR * 128 + k0; t < T; t += 128) {
+          const uint32_t p = lut_p(mulshift((int64_t)mx - sc[t], ly.Ms, (int)ly.Ss), ei, ef);
+          if (kc == 0) lsum += p;
+        }
       }
       lsum = (uint32_t)wave_sum_i32((int)lsum);  // T * 65535 < 2^31
       if (lane == 0) redsum[wave] = (int32_t)lsum;
@@ -662,37 +670,38 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       const uint32_t inv = 0x80000000u / (total > 1u ? total : 1u);  // udiv(2^31, total), golden.py:174
       const int pb = (int)ly.pb, shp = 31 - pb;
       const int32_t cap = (1 << pb) - 1;
-      int32_t o[16];
+      // o[j] = sum_t pn[t] * v[t][16 ds + 4 kc + j]
+      int32_t o[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int d = 0; d < 16; ++d) o[d] = 0;
-      const v4i vn = *reinterpret_cast<const v4i*>(vnew);
-      auto pv_add = [&](int32_t pn, const v4i& vv) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          o[j] += pn * sbyte(vv.x, j);
-          o[4 + j] += pn * sbyte(vv.y, j);
-          o[8 + j] += pn * sbyte(vv.z, j);
-          o[12 + j] += pn * sbyte(vv.w, j);
-        }
-      };
-#pragma unroll
-      for (int i = 0; i < VR; ++i) {
-        const int t = tid + 512 * i;
+      for (int i = 0; i < KR; ++i) {
+        const int t = k0 + 128 * i;
         const int64_t q = rshr((int64_t)pv[i] * inv, shp);
-        pv_add((int32_t)(q < cap ? q : cap), t == T - 1 ? vn : vreg[i]);
+        const int32_t pn = (int32_t)(q < cap ? q : cap);
+        const int32_t vw = t == T - 1 ? vnw : vreg[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] += pn * sbyte(vw, j);
       }
-      if (512 * VR < T) {  // keys past the registers
+      if (KR * 128 < T) {  // keys past the registers
         const Rsrc vrr = rsrc(ly.vc + (int64_t)g * a.max_seq * D, (int64_t)a.max_seq * D);
-        for (int t = tid + 512 * VR; t < T; t += 512) {
-          const int64_t q = rshr((int64_t)(uint32_t)sc[t] * inv, shp);
-          pv_add((int32_t)(q < cap ? q : cap), t == T - 1 ? vn : ld16(vrr, (uint32_t)(t * D + 16 * ds)));
+        for (int t = KR * 128 + k0; t < T; t += 128) {
+          const uint32_t p = lut_p(mulshift((int64_t)mx - sc[t], ly.Ms, (int)ly.Ss), ei, ef);
+          const int64_t q = rshr((int64_t)p * inv, shp);
+          const int32_t pn = (int32_t)(q < cap ? q : cap);
+          const int32_t vw = t == T - 1 ? vnw : ld4(vrr, (uint32_t)(t * D + 16 * ds + 4 * kc));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] += pn * sbyte(vw, j);
         }
       }
+      // the 16 lanes of a row with equal lane % 4 hold the same four dimensions: fold them, then the
+      // 4 rows x 8 waves partials in LDS
 #pragma unroll
-      for (int d = 0; d < 16; ++d) o[d] = row16_sum(o[d]);
-      if ((lane & 15) == 0) {
+      for (int j = 0; j < 4; ++j) {
+        o[j] += dpp_mov<DPP_ROW_ROR + 4>(o[j]);
+        o[j] += dpp_mov<DPP_ROW_ROR + 8>(o[j]);
+      }
+      if ((lane & 15) < 4) {
 #pragma unroll
-        for (int d = 0; d < 16; ++d) wpart[4 * wave + (lane >> 4)][d] = o[d];
+        for (int j = 0; j < 4; ++j) wpart[4 * wave + (lane >> 4)][4 * kc + j] = o[j];
       }
       if (!all_meet()) {
         alive = false;
@@ -754,8 +763,10 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       for (int u = 0; u < NS3; ++u) {
         const int s = s0 + u;
         const uint32_t k = (uint32_t)(s * 64 + kg * 16);
-        dma16(wr, blk + u * 1024, s < kst ? (uint32_t)(na * dim) + k : LD_OOB);
-        dma16(wr, blk + (NS3 + u) * 1024, (tb >= 0 && s < kst) ? (uint32_t)(nb * dim) + k : LD_OOB);
+        if (s < KST) {  // blocks past the row, and those of an absent tile, are never loaded: zero
+          dma16(wr, blk + u * 1024, (uint32_t)(na * dim) + k);
+          if (tb >= 0) dma16(wr, blk + (NS3 + u) * 1024, (uint32_t)(nb * dim) + k);
+        }
       }
     };
     if (alive && !roww) w_issue(lyr[0]);
@@ -861,11 +872,23 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         const int kh = w4 & 1, s0 = kh * NS3;
         v4i am = {0, 0, 0, 0}, at = {0, 0, 0, 0};
 #pragma unroll
-        for (int u = 0; u < NS3; ++u) {
-          if (s0 + u < kst) {  // (steps past the row hold no loaded block)
-            const v4i xa = *reinterpret_cast<const v4i*>(xq + (s0 + u) * 64 + kg * 16);
-            am = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, lds16(blk + u * 1024), am, 0, 0, 0);
-            at = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, lds16(blk + (NS3 + u) * 1024), at, 0, 0, 0);
+        for (int u0 = 0; u0 < NS3; u0 += 4) {  // four steps' operands read at once
+          v4i xa[4], ba[4], bb[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int uu = min(u0 + u, NS3 - 1);
+            const int s = min(s0 + uu, KST - 1);  // (a step past the row meets zero blocks)
+            xa[u] = *reinterpret_cast<const v4i*>(xq + s * 64 + kg * 16);
+            ba[u] = lds16(blk + uu * 1024);
+            bb[u] = lds16(blk + (NS3 + uu) * 1024);
+          }
+          __builtin_amdgcn_sched_barrier(0);  // all twelve reads issued before the first product
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (u0 + u < NS3) {
+              am = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u], ba[u], am, 0, 0, 0);
+              at = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u], bb[u], at, 0, 0, 0);
+            }
           }
         }
         if (lane < 16) {
@@ -1032,8 +1055,12 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
     t.mul_sh = s.mul_sh;
     t.fq_S = s.fq_S;
   }
-  const int kst = (int)(dim / 64);
-  const size_t lds = kst <= 9 ? step_lds<9>((int)S) : kst <= 14 ? step_lds<14>((int)S) : step_lds<16>((int)S);
+  const int kst = (int)(dim / 64);  // K steps of 64: the kernel is compiled for 9, 14 and 16
+  if (kst != 9 && kst != 14 && kst != 16) {
+    fail(-EINVAL, "dec_step: dim %lld is not one of 576, 896, 1024", (long long)dim);
+    return nullptr;
+  }
+  const size_t lds = kst == 9 ? step_lds<9>((int)S) : kst == 14 ? step_lds<14>((int)S) : step_lds<16>((int)S);
   if (lds > 150 * 1024) {  // 160 KiB per CU, of which the kernel's fixed arrays take a few
     fail(-EINVAL, "dec_step: %zu bytes of LDS (dim %lld, max_seq %lld) exceed the CU", lds, (long long)dim,
          (long long)S);
@@ -1089,8 +1116,8 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
 
 extern "C" int llhip_dec_step_run(llhip_dec_step* s, void* stream) {
   if (!s) return fail(-EINVAL, "dec_step: null step");
-  if (s->kst <= 9) return launch_step<9>(s, stream);
-  if (s->kst <= 14) return launch_step<14>(s, stream);
+  if (s->kst == 9) return launch_step<9>(s, stream);
+  if (s->kst == 14) return launch_step<14>(s, stream);
   return launch_step<16>(s, stream);
 }
 
