@@ -88,6 +88,7 @@ struct Args {
   uint32_t* fl2;   // S12 units done
   uint32_t* fl3;   // S3 units done
   uint32_t* ctl;   // [0] launches, [1] workgroups done, [2] error, [3] abort
+  const int32_t* role;  // [G] workgroup -> S12 unit u (u), S3 unit u (256 + u) or idle (-1)
   int L, dim, H, Hkv, max_seq, F;
   int nu2, nu3, tiles;  // S12 units (H * D / 16), S3 units with FFN tiles, 16-column FFN tiles
   uint32_t spin_max;
@@ -142,10 +143,21 @@ __device__ __forceinline__ int32_t row16_sum(int32_t v) {
   return v + dpp_mov<DPP_ROW_ROR + 8>(v);
 }
 
-__device__ __forceinline__ uint32_t lut_p(int64_t z, const uint16_t* ei, const uint16_t* ef) {
-  if (z >= 4096 || z < 0) return 0u;
+// Probability of a key whose score lies x below the maximum (golden.py:168-172): z = rshr(x Ms, Ss)
+// with x in [0, 2^21] (|score| <= 64 * 128 * 128) and Ms < 2^32 is (x Ms + 2^(Ss-1)) >> Ss, one
+// unsigned 32 x 32 + 64 multiply-add and a shift; z >= 4096 is past the exp table (probability 0).
+__device__ __forceinline__ uint32_t prob_gap(int32_t x, uint32_t Ms, uint64_t half, int Ss, const uint16_t* ei,
+                                             const uint16_t* ef) {
+  const uint64_t z = ((uint64_t)(uint32_t)x * Ms + half) >> Ss;
+  if (z >= 4096u) return 0u;
   const uint32_t zi = (uint32_t)z;
   return ((uint32_t)ei[zi >> 8] * (uint32_t)ef[zi & 255] + 32768u) >> 16;
+}
+// Normalised probability min(rshr(p inv, shp), cap) (golden.py:173-176) for p < 2^16, inv <= 2^31,
+// shp >= 1: p inv + 2^(shp-1) < 2^48, one multiply-add and a shift.
+__device__ __forceinline__ int32_t prob_norm(uint32_t p, uint32_t inv, uint64_t half, int shp, int32_t cap) {
+  const uint32_t q = (uint32_t)(((uint64_t)p * inv + half) >> shp);
+  return q < (uint32_t)cap ? (int32_t)q : cap;
 }
 
 // ---- flags ------------------------------------------------------------------------------------
@@ -167,11 +179,12 @@ __device__ bool poll(const uint32_t* f, int n, uint32_t want, uint32_t* ctl, uin
     for (int j = 0; j < 4; ++j) ok = ok && (w0 + j >= n || (int32_t)((uint32_t)v[j] - want) >= 0);
     return __builtin_amdgcn_ballot_w64(!ok) == 0;
   };
-  v4i nxt = ldc16(fr, 4u * w0);
+  const uint32_t off = w0 < n ? 4u * w0 : LD_OOB;  // lanes past the producers read nothing
+  v4i nxt = ldc16(fr, off);
   for (uint32_t it = 0;; ++it) {
     __asm__ volatile("" ::: "memory");  // a fresh load on every pass
     const v4i cur = nxt;
-    nxt = ldc16(fr, 4u * w0);
+    nxt = ldc16(fr, off);
     __asm__ volatile("s_waitcnt vmcnt(1)" ::: "memory");  // cur has arrived, nxt may still be in flight
     if (all_set(cur)) {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -203,7 +216,7 @@ __device__ __forceinline__ void publish(uint32_t* f, int idx, uint32_t v) {
 // until the count reaches its target.  The abort word ends every wait when the launch is being
 // abandoned.
 struct Sync {
-  uint32_t rowbar, allbar, xrdy, wrdy, abort;
+  uint32_t rowbar, allbar, xrdy, wrdy, aiss, abort;  // aiss: the row waves' atomics issued (4 a layer)
 };
 
 __device__ __forceinline__ void sig_add(uint32_t* c) {
@@ -315,8 +328,9 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
   const int rt = tid;   // row thread index (row waves)
   const int w4 = wave - 4;
   const int dim = a.dim;  // 64 KST
-  const int u2 = b < a.nu2 ? b : -1;                                // S12 unit
-  const int u3 = (b >= a.nu2 && b - a.nu2 < a.nu3) ? b - a.nu2 : -1;  // S3 unit
+  const int role = ((const __attribute__((address_space(4))) int32_t*)a.role)[b];
+  const int u2 = role >= 0 && role < 256 ? role : -1;  // S12 unit
+  const int u3 = role >= 256 ? role - 256 : -1;        // S3 unit
   const int rep = b % NREP;  // flag replica this workgroup polls
   const int col = lane & 15, kg = lane >> 4;
   const CLayer* lyr = (const CLayer*)a.layers;  // read-only for the launch: scalar loads
@@ -360,7 +374,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
     int8_t* bw = dyn + (wave - 4) * NB * 1024;
     for (int i = 16 * lane; i < NB * 1024; i += 1024) *reinterpret_cast<v4i*>(bw + i) = v4i{0, 0, 0, 0};
   }
-  if (tid == 0) sy = Sync{0u, 0u, 0u, 0u, 0u};
+  if (tid == 0) sy = Sync{0u, 0u, 0u, 0u, 0u, 0u};
   __syncthreads();  // the only workgroup barrier: tables and counters in place
 
   const uint16_t* ei = reinterpret_cast<const uint16_t*>(lut32);
@@ -646,15 +660,18 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       // probabilities (golden.py:168-172); each key's four threads compute it, its first adds it
       uint32_t pv[KR];
       uint32_t lsum = 0;
+      const uint32_t Ms = (uint32_t)ly.Ms;
+      const int Ss = (int)ly.Ss;
+      const uint64_t zhalf = Ss > 0 ? 1ull << (Ss - 1) : 0ull;
 #pragma unroll
       for (int i = 0; i < KR; ++i) {
         const int t = k0 + 128 * i;
-        pv[i] = t < T ? lut_p(mulshift((int64_t)mx - sreg[i], ly.Ms, (int)ly.Ss), ei, ef) : 0u;
+        pv[i] = t < T ? prob_gap(mx - sreg[i], Ms, zhalf, Ss, ei, ef) : 0u;
         if (kc == 0) lsum += pv[i];
       }
       if (KR * 128 < T) {
         for (int t = KR * 128 + k0; t < T; t += 128) {
-          const uint32_t p = lut_p(mulshift((int64_t)mx - sc[t], ly.Ms, (int)ly.Ss), ei, ef);
+          const uint32_t p = prob_gap(mx - sc[t], Ms, zhalf, Ss, ei, ef);
           if (kc == 0) lsum += p;
         }
       }
@@ -670,13 +687,13 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       const uint32_t inv = 0x80000000u / (total > 1u ? total : 1u);  // udiv(2^31, total), golden.py:174
       const int pb = (int)ly.pb, shp = 31 - pb;
       const int32_t cap = (1 << pb) - 1;
+      const uint64_t phalf = 1ull << (shp - 1);
       // o[j] = sum_t pn[t] * v[t][16 ds + 4 kc + j]
       int32_t o[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < KR; ++i) {
         const int t = k0 + 128 * i;
-        const int64_t q = rshr((int64_t)pv[i] * inv, shp);
-        const int32_t pn = (int32_t)(q < cap ? q : cap);
+        const int32_t pn = prob_norm(pv[i], inv, phalf, shp, cap);
         const int32_t vw = t == T - 1 ? vnw : vreg[i];
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] += pn * sbyte(vw, j);
@@ -684,9 +701,8 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       if (KR * 128 < T) {  // keys past the registers
         const Rsrc vrr = rsrc(ly.vc + (int64_t)g * a.max_seq * D, (int64_t)a.max_seq * D);
         for (int t = KR * 128 + k0; t < T; t += 128) {
-          const uint32_t p = lut_p(mulshift((int64_t)mx - sc[t], ly.Ms, (int)ly.Ss), ei, ef);
-          const int64_t q = rshr((int64_t)p * inv, shp);
-          const int32_t pn = (int32_t)(q < cap ? q : cap);
+          const uint32_t p = prob_gap(mx - sc[t], Ms, zhalf, Ss, ei, ef);
+          const int32_t pn = prob_norm(p, inv, phalf, shp, cap);
           const int32_t vw = t == T - 1 ? vnw : ld4(vrr, (uint32_t)(t * D + 16 * ds + 4 * kc));
 #pragma unroll
           for (int j = 0; j < 4; ++j) o[j] += pn * sbyte(vw, j);
@@ -708,10 +724,15 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         break;
       }
       if (!roww) {
-        // the next layer's blocks and cached keys/values (the row waves request theirs after the
-        // layer's atomics)
+        // the next layer's blocks and cached keys/values, requested once the row waves' atomics
+        // are on their way (ahead of these loads in the CU's memory queue; the row waves request
+        // their keys after the atomics)
         if (l + 1 < a.L) {
           __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (!sig_wait(&sy.aiss, 4u * (uint32_t)(l + 1), &sy.abort)) {
+            alive = false;
+            break;
+          }
           w_issue(lyr[l + 1]);
           kv_issue(lyr[l + 1]);
         }
@@ -744,6 +765,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         const int32_t s = dot16(avv, wop[i]);
         if (n < dim && s != 0) atomic_add_dev(acc + n, s);
       }
+      sig_add(&sy.aiss);
       drain();
       if (!row_meet()) {
         alive = false;
@@ -856,6 +878,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
           const int32_t d = dot16(fb, wdb[i], dot16(fa, wda[i]));
           if (n < dim && d != 0) atomic_add_dev(acc + n, d);
         }
+        sig_add(&sy.aiss);
         drain();
         if (!row_meet()) {
           alive = false;
@@ -897,8 +920,14 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         }
         sig_add(&sy.wrdy);
         nw += 4;
-        if (l + 1 < a.L) {  // the next layer's blocks, refilled once this wave's reads are done
+        // the next layer's blocks, requested once this wave's reads are done and the row waves'
+        // atomics are on their way (ahead of these loads in the CU's memory queue)
+        if (l + 1 < a.L) {
           __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (!sig_wait(&sy.aiss, 4u * (uint32_t)(l + 1), &sy.abort)) {
+            alive = false;
+            break;
+          }
           w_issue(lyr[l + 1]);
         }
       }
@@ -998,7 +1027,7 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
       }
     if (!norm_ok(s.eps1, s.C1, s.sh1, s.Mq1, s.Sq1) || !norm_ok(s.eps2, s.C2, s.sh2, s.Mq2, s.Sq2) ||
         !u32_ok(s.quant_M[0]) || !u32_ok(s.quant_M[1]) || !shift_ok(s.quant_S[0]) || !shift_ok(s.quant_S[1]) ||
-        !shift_ok(s.Ss) || !shift_ok(s.So) || !(s.prob_bits == 8 || s.prob_bits == 15) || !u32_ok(s.silu_Mi) ||
+        !shift_ok(s.Ss) || !shift_ok(s.So) || !u32_ok(s.Ms) || !(s.prob_bits == 8 || s.prob_bits == 15) || !u32_ok(s.silu_Mi) ||
         !shift_ok(s.silu_Si) || !shift_ok(s.silu_sh) || !shift_ok(s.mul_sh) || !u32_ok(s.fq_M) || !shift_ok(s.fq_S)) {
       fail(-EINVAL, "dec_step: layer %lld parameter out of range", (long long)l);
       return nullptr;
@@ -1066,11 +1095,27 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
          (long long)S);
     return nullptr;
   }
-  // one allocation: layer table | ctl (256 B) | flags 3 x NREP KiB | acc_o | acc_d | xres
+  // Workgroup roles.  Workgroup b runs on XCD b % 8 (dispatch is round-robin over the XCDs), so
+  // the DC slices of head h go to workgroups b = 8 (DC (h / 8) + ds) + h % 8: one XCD, whose L2
+  // then serves the head's q rows once for its slices.  The S3 units take the rest in order.
+  std::vector<int32_t> role((size_t)G, -1);
+  {
+    bool xcd = G % 8 == 0;
+    for (int64_t u = 0; u < nu2 && xcd; ++u) xcd = 8 * (DC * (u / DC / 8) + u % DC) + (u / DC) % 8 < G;
+    for (int64_t u = 0; u < nu2; ++u) {
+      const int64_t h = u / DC, b = xcd ? 8 * (DC * (h / 8) + u % DC) + h % 8 : u;
+      role[(size_t)b] = (int32_t)u;
+    }
+    int64_t u3 = 0;
+    for (int64_t b = 0; b < G && u3 < nu3; ++b)
+      if (role[(size_t)b] < 0) role[(size_t)b] = (int32_t)(256 + u3++);
+  }
+  // one allocation: layer table | ctl (256 B) | roles (1 KiB) | flags 3 x NREP KiB | acc_o | acc_d | xres
   const size_t tab_b = (sizeof(Layer) * (size_t)d->L + 255) & ~(size_t)255;
   const size_t acc_b = (size_t)2 * R * dim * 4;
-  const size_t off_ctl = tab_b, off_fl = off_ctl + 256, off_ao = off_fl + 3 * FLAG_WORDS * 4, off_ad = off_ao + acc_b,
-               off_x = off_ad + acc_b, total = off_x + ((size_t)(2 * dim * 2 + 255) & ~(size_t)255);
+  const size_t off_ctl = tab_b, off_role = off_ctl + 256, off_fl = off_role + 4 * MAX_G,
+               off_ao = off_fl + 3 * FLAG_WORDS * 4, off_ad = off_ao + acc_b, off_x = off_ad + acc_b,
+               total = off_x + ((size_t)(2 * dim * 2 + 255) & ~(size_t)255);
   llhip_dec_step* s = new llhip_dec_step();
   if (hipMalloc(&s->mem, total) != hipSuccess) {
     fail(-EIO, "dec_step: device allocation failed");
@@ -1079,7 +1124,8 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
   }
   char* m = static_cast<char*>(s->mem);
   if (hipMemset(m, 0, total) != hipSuccess ||
-      hipMemcpy(m, tab.data(), sizeof(Layer) * (size_t)d->L, hipMemcpyHostToDevice) != hipSuccess) {
+      hipMemcpy(m, tab.data(), sizeof(Layer) * (size_t)d->L, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(m + off_role, role.data(), 4 * (size_t)G, hipMemcpyHostToDevice) != hipSuccess) {
     fail(-EIO, "dec_step: upload failed");
     (void)hipFree(s->mem);
     delete s;
@@ -1092,6 +1138,7 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
   a.sin_tab = static_cast<const int16_t*>(d->sin_tab);
   a.pos_dev = static_cast<const int32_t*>(d->pos_dev);
   a.ctl = reinterpret_cast<uint32_t*>(m + off_ctl);
+  a.role = reinterpret_cast<const int32_t*>(m + off_role);
   a.fl0 = reinterpret_cast<uint32_t*>(m + off_fl);
   a.fl2 = reinterpret_cast<uint32_t*>(m + off_fl + FLAG_WORDS * 4);
   a.fl3 = reinterpret_cast<uint32_t*>(m + off_fl + 2 * FLAG_WORDS * 4);
