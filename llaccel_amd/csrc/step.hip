@@ -89,6 +89,7 @@ struct Args {
   uint32_t* fl3;   // S3 units done
   uint32_t* ctl;   // [0] launches, [1] workgroups done, [2] error, [3] abort
   const int32_t* role;  // [G] workgroup -> S12 unit u (u), S3 unit u (256 + u) or idle (-1)
+  uint32_t* kx;         // [H][D] a head's new key (tagged words), exchanged between its slices
   int L, dim, H, Hkv, max_seq, F;
   int nu2, nu3, tiles;  // S12 units (H * D / 16), S3 units with FFN tiles, 16-column FFN tiles
   uint32_t spin_max;
@@ -205,6 +206,45 @@ __device__ bool poll(const uint32_t* f, int n, uint32_t want, uint32_t* ctl, uin
   }
 }
 
+// Tagged words: (tag << 16) | (value & 0xFFFF) in one 32-bit store, so a reader that sees the tag of
+// the current layer sees the value with it (no separate flag: one trip through memory).  The wave
+// waits until word `lane` of p (D words) carries `tag` and returns its 16-bit value; `first` is a
+// load of that word issued earlier (its latency hidden behind other work).  False on timeout
+// (recorded) or abort.
+__device__ bool take_tagged(const uint32_t* p, uint32_t tag, uint32_t first, uint32_t* ctl, uint32_t spin_max,
+                            int32_t& val) {
+  const int lane = threadIdx.x & 63;
+  if (__builtin_amdgcn_ballot_w64((first >> 16) != tag) == 0) {
+    val = (int32_t)(int16_t)(first & 0xFFFFu);
+    return true;
+  }
+  const Rsrc pr = rsrc(p, 4 * D), cr = rsrc(ctl, 16);
+  uint32_t nxt = ldc4(pr, 4u * lane);
+  for (uint32_t it = 0;; ++it) {
+    __asm__ volatile("" ::: "memory");  // a fresh load on every pass
+    const uint32_t cur = nxt;
+    nxt = ldc4(pr, 4u * lane);
+    __asm__ volatile("s_waitcnt vmcnt(1)" ::: "memory");  // cur has arrived, nxt may still be in flight
+    if (__builtin_amdgcn_ballot_w64((cur >> 16) != tag) == 0) {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      val = (int32_t)(int16_t)(cur & 0xFFFFu);
+      return true;
+    }
+    if (it >= spin_max) {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (lane == 0) {
+        __hip_atomic_fetch_or(ctl + 2, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return false;
+    }
+    if ((it & 31) == 31 && ldc4(cr, 12) != 0) {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      return false;
+    }
+  }
+}
+
 // wave 0: store the flag word of producer idx into every replica (after the workgroup's drain)
 __device__ __forceinline__ void publish(uint32_t* f, int idx, uint32_t v) {
   const int lane = threadIdx.x & 63;
@@ -216,7 +256,7 @@ __device__ __forceinline__ void publish(uint32_t* f, int idx, uint32_t v) {
 // until the count reaches its target.  The abort word ends every wait when the launch is being
 // abandoned.
 struct Sync {
-  uint32_t rowbar, allbar, xrdy, wrdy, aiss, abort;  // aiss: the row waves' atomics issued (4 a layer)
+  uint32_t rowbar, allbar, xrdy, wrdy, krdy, aiss, abort;  // krdy: k partials in; aiss: flag published
 };
 
 __device__ __forceinline__ void sig_add(uint32_t* c) {
@@ -284,13 +324,13 @@ __device__ __forceinline__ void zero_slice(const Args& a, int par, int lo, int h
 
 // LDS of the two kinds of workgroup (dynamic part; the scores follow the blocks).  Each weight wave
 // owns 1 KiB blocks (lane l's 16 bytes at 16 l), filled by direct loads in the order it reads them.
-//   S12: per weight wave w, q tile w and k tile w over all K steps, then its share of the v tile's
-//        K steps (VS of them): 2 KST + VS blocks.
+//   S12: per weight wave w, q tile w of head h over all K steps, then K steps w VS .. w VS + VS - 1
+//        of the slice's k and v tiles: KST + 2 VS blocks.
 //   S3 : per weight wave (gate or up, K half), NS3 steps of each of the two FFN tiles: 2 NS3 blocks.
 template <int KST>
 struct StepCfg {
   static constexpr int VS = (KST + 3) / 4;
-  static constexpr int NB12 = 2 * KST + VS;
+  static constexpr int NB12 = KST + 2 * VS;
   static constexpr int NS3 = (KST + 1) / 2;
   static constexpr int NB3 = 2 * NS3;
   static constexpr int NB = NB12 > NB3 ? NB12 : NB3;
@@ -310,7 +350,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) int8_t ah[16];
   __shared__ __attribute__((aligned(16))) int8_t fq16[2][16];
   __shared__ uint64_t red64[4];
-  __shared__ int32_t gq[D], gk[D], gv[4][16];
+  __shared__ int32_t gq[D], gk[4][16], gv[4][16];  // q; k and v slice: per weight wave K-step partial sums
   __shared__ int32_t yq[D], yk[D];
   __shared__ int32_t redmax[8], redsum[8];
   __shared__ int32_t wpart[32][16];
@@ -351,7 +391,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
   const int ta = u3, tb = (u3 >= 0 && u3 + a.nu3 < a.tiles) ? u3 + a.nu3 : -1;
 
   // ---- constant tables into LDS, zero padding of the quantised row, RoPE factors ----
-  int32_t cs = 0, sn = 0;  // row waves 0 and 1, lane p < D/2: RoPE pair (p, p + D/2) factors
+  int32_t cs = 0, sn = 0;  // lane p < D/2: RoPE pair (p, p + D/2) factors (q: wave 0; new key: any wave)
   if (wave == 0) {
     const Rsrc ir = rsrc(kExpI, sizeof(kExpI)), fr = rsrc(kExpF, sizeof(kExpF)), sr = rsrc(kSig, sizeof(kSig));
 #pragma unroll
@@ -363,7 +403,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       sig32[idx] = (uint32_t)ld4(sr, idx < 129 ? 4 * idx : LD_OOB);
     }
   }
-  if (u2 >= 0 && wave < 2 && lane < D / 2) {
+  if (u2 >= 0 && lane < D / 2) {
     const Rsrc cr = rsrc(a.cos_tab, (int64_t)a.max_seq * D), snr = rsrc(a.sin_tab, (int64_t)a.max_seq * D);
     const uint32_t off = dead0 ? LD_OOB : (uint32_t)(((int64_t)pos * (D / 2) + lane) * 2);
     cs = ld2s(cr, off);
@@ -374,14 +414,14 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
     int8_t* bw = dyn + (wave - 4) * NB * 1024;
     for (int i = 16 * lane; i < NB * 1024; i += 1024) *reinterpret_cast<v4i*>(bw + i) = v4i{0, 0, 0, 0};
   }
-  if (tid == 0) sy = Sync{0u, 0u, 0u, 0u, 0u, 0u};
+  if (tid == 0) sy = Sync{0u, 0u, 0u, 0u, 0u, 0u, 0u};
   __syncthreads();  // the only workgroup barrier: tables and counters in place
 
   const uint16_t* ei = reinterpret_cast<const uint16_t*>(lut32);
   const uint16_t* ef = ei + 16;
   const uint16_t* sig = reinterpret_cast<const uint16_t*>(sig32);
   int8_t* blk = dyn + w4 * NB * 1024;  // this weight wave's blocks
-  uint32_t nrow = 0, nall = 0, nx = 0, nw = 0;
+  uint32_t nrow = 0, nall = 0, nx = 0, nw = 0, nk = 0;
   bool alive = !dead0 && (u2 >= 0 || u3 >= 0);
 
   auto row_meet = [&]() -> bool {  // the four row waves
@@ -431,22 +471,25 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
 
   if (u2 >= 0) {
     // =============================== S12 unit (h, ds) ===============================
-    // weight wave w: blocks [0, KST) q tile w, [KST, 2 KST) k tile w, [2 KST, 2 KST + VS) v steps w*VS..
+    // Weight wave w: blocks [0, KST) q tile w of head h (all K steps); [KST, KST + VS) and
+    // [KST + VS, KST + 2 VS) K steps w VS .. w VS + VS - 1 of the slice's k and v columns
+    // 16 ds .. 16 ds + 15 of group g (steps past the row are never loaded: zero).  The head's four
+    // slices trade their k columns (the new key is needed last, after the cached keys' scores).
     auto w_issue = [&](const CLayer& ly) {
       const Rsrc qr = rsrc(ly.W[0], (int64_t)a.H * D * dim), kr = rsrc(ly.W[1], (int64_t)a.Hkv * D * dim);
       const Rsrc vr = rsrc(ly.W[2], (int64_t)a.Hkv * D * dim);
-      const int nq = h * D + 16 * w4 + col, nk = g * D + 16 * w4 + col, nv = g * D + 16 * ds + col;
-#pragma unroll
-      for (int s = 0; s < KST; ++s) {
-        const uint32_t k = (uint32_t)(s * 64 + kg * 16);
-        dma16(qr, blk + s * 1024, (uint32_t)(nq * dim) + k);
-        dma16(kr, blk + (KST + s) * 1024, (uint32_t)(nk * dim) + k);
-      }
+      const int nq = h * D + 16 * w4 + col, nk = g * D + 16 * ds + col;
 #pragma unroll
       for (int i = 0; i < VS; ++i) {
         const int s = w4 * VS + i;
-        if (s < KST) dma16(vr, blk + (2 * KST + i) * 1024, (uint32_t)(nv * dim + s * 64 + kg * 16));
+        if (s < KST) {
+          const uint32_t k = (uint32_t)(s * 64 + kg * 16);
+          dma16(kr, blk + (KST + i) * 1024, (uint32_t)(nk * dim) + k);
+          dma16(vr, blk + (KST + VS + i) * 1024, (uint32_t)(nk * dim) + k);
+        }
       }
+#pragma unroll
+      for (int s = 0; s < KST; ++s) dma16(qr, blk + s * 1024, (uint32_t)(nq * dim + s * 64 + kg * 16));
     };
     // Attention layout: thread tid holds chunk kc = tid % 4 (16 key bytes, 4 value bytes of the
     // slice) of keys t = tid / 4 + 128 i, i < KR: the four threads of a key meet by DPP within a
@@ -478,11 +521,11 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         v2i rqc{0, 0};
         int32_t bc = 0;
         rowops_load(fo, l > 0 ? lyr[l - 1].rq_d : nullptr, l > 0 ? lyr[l - 1].bias_d : nullptr, ly.g1, dim, rt);
-        if (wave < 3) {  // epilogue columns: wave 0 q (h D + lane), wave 1 k (g D + lane), wave 2 v slice
+        if (wave < 3) {  // epilogue columns: wave 0 q (h D + lane), wave 1 k and wave 2 v (g D + 16 ds + lane)
           const int rl = wave;
-          const int n = wave == 0 ? h * D + lane : (wave == 1 ? g * D + lane : g * D + 16 * ds + lane);
+          const int n = wave == 0 ? h * D + lane : g * D + 16 * ds + lane;
           const int nr = (rl == 0 ? a.H : a.Hkv) * D;
-          const bool in = wave < 2 || lane < 16;
+          const bool in = wave == 0 || lane < 16;
           rqc = ld8(rsrc(ly.rq[rl], (int64_t)nr * 8), in ? 8u * n : LD_OOB);
           bc = ld4(rsrc(ly.bias[rl], (int64_t)nr * 4), in ? 4u * n : LD_OOB);
         }
@@ -525,39 +568,43 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
           break;
         }
         sig_add(&sy.xrdy);
-        if (wave < 3) {
-          // q (wave 0), k (wave 1): requant16 + bias, RoPE in 64-bit sums, quant (golden.py:316-342,
-          // 141-158, 119-120); v slice (wave 2): requant8 + bias
+        if (wave == 1) {
+          // the slice's k columns: requant16 + bias (golden.py:316-342) out as tagged words for the
+          // head's four slices (RoPE and quant follow on the whole key, after the cached scores)
+          nk += 4;
+          if (!sig_wait(&sy.krdy, nk, &sy.abort)) {
+            alive = false;
+            break;
+          }
+          if (lane < 16) {
+            const int32_t s = gk[0][lane] + gk[1][lane] + gk[2][lane] + gk[3][lane];
+            const int32_t y = (int32_t)sat16(mulshift((int64_t)s + bc, (int64_t)rqc.x, rqc.y));
+            stc4(rsrc(a.kx + (int64_t)h * D, 4 * D), 4u * (16 * ds + lane), ((ep & 0xFFFFu) << 16) | (uint32_t)(uint16_t)y);
+          }
+        } else if (wave != 3) {
+          // q (wave 0): requant16 + bias, RoPE in 64-bit sums, quant (golden.py:316-342, 141-158,
+          // 119-120); v slice (wave 2): requant8 + bias
           nw += 4;
           if (!sig_wait(&sy.wrdy, nw, &sy.abort)) {
             alive = false;
             break;
           }
-          const int64_t krow = ((int64_t)g * a.max_seq + pos) * D;
-          if (wave < 2) {
-            const int32_t s = wave == 0 ? gq[lane] : gk[lane];
-            const int32_t y = (int32_t)sat16(mulshift((int64_t)s + bc, (int64_t)rqc.x, rqc.y));
-            int32_t* yy = wave == 0 ? yq : yk;
-            yy[lane] = y;
+          if (wave == 0) {
+            const int32_t y = (int32_t)sat16(mulshift((int64_t)gq[lane] + bc, (int64_t)rqc.x, rqc.y));
+            yq[lane] = y;
             if (lane < D / 2) {
-              const int32_t x1 = yy[lane], x2 = yy[lane + D / 2];
+              const int32_t x1 = yq[lane], x2 = yq[lane + D / 2];
               const int64_t r1 = (int64_t)x1 * cs - (int64_t)x2 * sn, r2 = (int64_t)x2 * cs + (int64_t)x1 * sn;
               const int32_t y1 = (int32_t)sat16(rshr(r1, 14)), y2 = (int32_t)sat16(rshr(r2, 14));
-              const double sq = mulshift_scale(ly.quant_M[wave], (int)ly.quant_S[wave]);
-              const int q1 = mulshift_small_sat(y1, sq, -128.0, 127.0), q2 = mulshift_small_sat(y2, sq, -128.0, 127.0);
-              int8_t* dst = wave == 0 ? q8 : k8;
-              dst[lane] = (int8_t)q1;
-              dst[lane + D / 2] = (int8_t)q2;
-              if (wave == 1 && kv_writer && ds == 0) {  // the new key row (golden.py:344-351)
-                ly.kc[krow + lane] = (int8_t)q1;
-                ly.kc[krow + lane + D / 2] = (int8_t)q2;
-              }
+              const double sq = mulshift_scale(ly.quant_M[0], (int)ly.quant_S[0]);
+              q8[lane] = (int8_t)mulshift_small_sat(y1, sq, -128.0, 127.0);
+              q8[lane + D / 2] = (int8_t)mulshift_small_sat(y2, sq, -128.0, 127.0);
             }
           } else if (lane < 16) {
             const int32_t s = gv[0][lane] + gv[1][lane] + gv[2][lane] + gv[3][lane];
             const int8_t y = (int8_t)sat8(mulshift((int64_t)s + bc, (int64_t)rqc.x, rqc.y));
             vnew[lane] = y;
-            if (kv_writer) ly.vc[krow + 16 * ds + lane] = y;  // the new value slice
+            if (kv_writer) ly.vc[((int64_t)g * a.max_seq + pos) * D + 16 * ds + lane] = y;  // the new value slice
           }
         }
         if (l == 0) {  // every unit's clearing stores done before any unit adds
@@ -575,58 +622,76 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
           break;
         }
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this layer's blocks (and cached keys)
-        // q tile w and k tile w (all K steps), the v tile's steps w*VS.. (blocks past the row are zero)
-        v4i aq = {0, 0, 0, 0}, ak = {0, 0, 0, 0}, av = {0, 0, 0, 0};
-        // four K steps' operands read at once, then their eight products (the LDS latency of a
-        // group is paid once)
+        // first the slice's k columns (their exchange between the head's slices overlaps the rest):
+        // K steps w VS .. w VS + VS - 1, every operand read at once (a step past the row meets a
+        // zero block)
+        {
+          v4i ak = {0, 0, 0, 0}, xa[VS], bk[VS];
+#pragma unroll
+          for (int i = 0; i < VS; ++i) {
+            xa[i] = *reinterpret_cast<const v4i*>(xq + min(w4 * VS + i, KST - 1) * 64 + kg * 16);
+            bk[i] = lds16(blk + (KST + i) * 1024);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < VS; ++i) ak = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i], bk[i], ak, 0, 0, 0);
+          if (lane < 16) gk[w4][lane] = ak.x;  // one input row: every output row equals row 0
+          sig_add(&sy.krdy);
+        }
+        // q tile w (all K steps) and the v columns' steps w VS ..: four K steps' operands read at
+        // once, then their products (the LDS latency of a group is paid once)
+        v4i aq = {0, 0, 0, 0}, av = {0, 0, 0, 0};
 #pragma unroll
         for (int s0 = 0; s0 < KST; s0 += 4) {
-          v4i xa[4], bq[4], bk[4];
+          v4i xa[4], bq[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int s = min(s0 + u, KST - 1);
             xa[u] = *reinterpret_cast<const v4i*>(xq + s * 64 + kg * 16);
             bq[u] = lds16(blk + s * 1024);
-            bk[u] = lds16(blk + (KST + s) * 1024);
           }
-          __builtin_amdgcn_sched_barrier(0);  // all twelve reads issued before the first product
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (s0 + u < KST) {
-              aq = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u], bq[u], aq, 0, 0, 0);
-              ak = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u], bk[u], ak, 0, 0, 0);
-            }
+          for (int u = 0; u < 4; ++u)
+            if (s0 + u < KST) aq = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u], bq[u], aq, 0, 0, 0);
+        }
+        {
+          v4i xa[VS], bv[VS];
+#pragma unroll
+          for (int i = 0; i < VS; ++i) {
+            xa[i] = *reinterpret_cast<const v4i*>(xq + min(w4 * VS + i, KST - 1) * 64 + kg * 16);
+            bv[i] = lds16(blk + (KST + VS + i) * 1024);
           }
-        }
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < VS; ++i) {
-          const int s = min(w4 * VS + i, KST - 1);  // (a step past the row meets a zero block)
-          const v4i xa = *reinterpret_cast<const v4i*>(xq + s * 64 + kg * 16);
-          av = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, lds16(blk + (2 * KST + i) * 1024), av, 0, 0, 0);
+          for (int i = 0; i < VS; ++i) av = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[i], bv[i], av, 0, 0, 0);
         }
-        if (lane < 16) {  // one input row: every output row equals row 0
+        if (lane < 16) {
           gq[16 * w4 + lane] = aq.x;
-          gk[16 * w4 + lane] = ak.x;
           gv[w4][lane] = av.x;
         }
         sig_add(&sy.wrdy);
         nw += 4;
       }
       // ---- attention over T keys on all eight waves (golden.py:162-180) ----
-      if (!all_meet()) {  // q8, k8, vnew in LDS
+      if (!all_meet()) {  // q8 and vnew in LDS
         alive = false;
         break;
       }
+      // the new key (position tn) belongs to the quad k0 = tn % 128, in wave kwave; that wave
+      // requests the head's k words now and takes them after its cached keys' scores
+      const int tn = T - 1;
+      const bool kwave = wave == ((tn & 127) >> 4);
+      const uint32_t kw0 = kwave ? ldc4(rsrc(a.kx + (int64_t)h * D, 4 * D), 4u * lane) : 0u;
       const v4i qv = *reinterpret_cast<const v4i*>(q8 + 16 * kc);
-      const v4i kn = *reinterpret_cast<const v4i*>(k8 + 16 * kc);
       const int32_t vnw = *reinterpret_cast<const int32_t*>(vnew + 4 * kc);
       int32_t sreg[KR];
       int32_t lmax = INT32_MIN;
 #pragma unroll
       for (int i = 0; i < KR; ++i) {
         const int t = k0 + 128 * i;
-        sreg[i] = quad_sum(dot16(qv, t == T - 1 ? kn : kreg[i]));
-        if (t < T) lmax = max(lmax, sreg[i]);
+        sreg[i] = quad_sum(dot16(qv, kreg[i]));
+        if (t < tn) lmax = max(lmax, sreg[i]);
       }
       if (KR * 128 < T) {  // keys past the registers (long contexts): scores into sc[]
         const Rsrc krr = rsrc(ly.kc + (int64_t)g * a.max_seq * D, (int64_t)a.max_seq * D);
@@ -640,11 +705,47 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int t = tb0 + 128 * u + k0;
-            const int32_t s = quad_sum(dot16(qv, t == T - 1 ? kn : kx[u]));
-            if (t < T) {
+            const int32_t s = quad_sum(dot16(qv, kx[u]));
+            if (t < tn) {
               if (kc == 0) sc[t] = s;
               lmax = max(lmax, s);
             }
+          }
+        }
+      }
+      if (kwave) {
+        // the new key: the head's k from its four slices, RoPE in 64-bit sums and quant
+        // (golden.py:141-158, 119-120), its cache row (golden.py:344-351), its score
+        int32_t y = 0;
+        if (!take_tagged(a.kx + (int64_t)h * D, ep & 0xFFFFu, kw0, a.ctl, a.spin_max, y)) {
+          alive = false;
+          break;
+        }
+        yk[lane] = y;
+        if (lane < D / 2) {
+          const int32_t x1 = yk[lane], x2 = yk[lane + D / 2];
+          const int64_t r1 = (int64_t)x1 * cs - (int64_t)x2 * sn, r2 = (int64_t)x2 * cs + (int64_t)x1 * sn;
+          const int32_t y1 = (int32_t)sat16(rshr(r1, 14)), y2 = (int32_t)sat16(rshr(r2, 14));
+          const double sq = mulshift_scale(ly.quant_M[1], (int)ly.quant_S[1]);
+          const int8_t q1 = (int8_t)mulshift_small_sat(y1, sq, -128.0, 127.0);
+          const int8_t q2 = (int8_t)mulshift_small_sat(y2, sq, -128.0, 127.0);
+          k8[lane] = q1;
+          k8[lane + D / 2] = q2;
+          if (kv_writer && ds == 0) {
+            const int64_t krow = ((int64_t)g * a.max_seq + pos) * D;
+            ly.kc[krow + lane] = q1;
+            ly.kc[krow + lane + D / 2] = q2;
+          }
+        }
+        if (k0 == (tn & 127)) {
+          const int32_t s = quad_sum(dot16(qv, *reinterpret_cast<const v4i*>(k8 + 16 * kc)));
+          lmax = max(lmax, s);
+          if (tn >= KR * 128) {
+            if (kc == 0) sc[tn] = s;
+          } else {
+#pragma unroll
+            for (int i = 0; i < KR; ++i)
+              if (i == (tn >> 7)) sreg[i] = s;
           }
         }
       }
@@ -725,8 +826,8 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       }
       if (!roww) {
         // the next layer's blocks and cached keys/values, requested once the row waves' atomics
-        // are on their way (ahead of these loads in the CU's memory queue; the row waves request
-        // their keys after the atomics)
+        // have landed and the flag is on its way (ahead of these loads in the CU's memory queue;
+        // the row waves request their keys after the flag)
         if (l + 1 < a.L) {
           __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           if (!sig_wait(&sy.aiss, 4u * (uint32_t)(l + 1), &sy.abort)) {
@@ -765,13 +866,13 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         const int32_t s = dot16(avv, wop[i]);
         if (n < dim && s != 0) atomic_add_dev(acc + n, s);
       }
-      sig_add(&sy.aiss);
       drain();
       if (!row_meet()) {
         alive = false;
         break;
       }
       if (wave == 0) publish(a.fl2, u2, ep);
+      sig_add(&sy.aiss);
       if (l + 1 < a.L) kv_issue(lyr[l + 1]);
     }
   } else if (u3 >= 0) {
@@ -878,13 +979,13 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
           const int32_t d = dot16(fb, wdb[i], dot16(fa, wda[i]));
           if (n < dim && d != 0) atomic_add_dev(acc + n, d);
         }
-        sig_add(&sy.aiss);
         drain();
         if (!row_meet()) {
           alive = false;
           break;
         }
         if (wave == 0) publish(a.fl3, u3, ep);
+        sig_add(&sy.aiss);
       } else {
         nx += 4;
         if (!sig_wait(&sy.xrdy, nx, &sy.abort)) {
@@ -921,7 +1022,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         sig_add(&sy.wrdy);
         nw += 4;
         // the next layer's blocks, requested once this wave's reads are done and the row waves'
-        // atomics are on their way (ahead of these loads in the CU's memory queue)
+        // atomics have landed and the flag is on its way (ahead of these loads in the CU's queue)
         if (l + 1 < a.L) {
           __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           if (!sig_wait(&sy.aiss, 4u * (uint32_t)(l + 1), &sy.abort)) {
@@ -1110,11 +1211,13 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
     for (int64_t b = 0; b < G && u3 < nu3; ++b)
       if (role[(size_t)b] < 0) role[(size_t)b] = (int32_t)(256 + u3++);
   }
-  // one allocation: layer table | ctl (256 B) | roles (1 KiB) | flags 3 x NREP KiB | acc_o | acc_d | xres
+  // one allocation: layer table | ctl (256 B) | roles (1 KiB) | flags 3 x NREP KiB | k exchange |
+  // acc_o | acc_d | xres
   const size_t tab_b = (sizeof(Layer) * (size_t)d->L + 255) & ~(size_t)255;
   const size_t acc_b = (size_t)2 * R * dim * 4;
   const size_t off_ctl = tab_b, off_role = off_ctl + 256, off_fl = off_role + 4 * MAX_G,
-               off_ao = off_fl + 3 * FLAG_WORDS * 4, off_ad = off_ao + acc_b, off_x = off_ad + acc_b,
+               off_kx = off_fl + 3 * FLAG_WORDS * 4, off_ao = off_kx + (((size_t)H * D * 4 + 255) & ~(size_t)255),
+               off_ad = off_ao + acc_b, off_x = off_ad + acc_b,
                total = off_x + ((size_t)(2 * dim * 2 + 255) & ~(size_t)255);
   llhip_dec_step* s = new llhip_dec_step();
   if (hipMalloc(&s->mem, total) != hipSuccess) {
@@ -1142,6 +1245,7 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
   a.fl0 = reinterpret_cast<uint32_t*>(m + off_fl);
   a.fl2 = reinterpret_cast<uint32_t*>(m + off_fl + FLAG_WORDS * 4);
   a.fl3 = reinterpret_cast<uint32_t*>(m + off_fl + 2 * FLAG_WORDS * 4);
+  a.kx = reinterpret_cast<uint32_t*>(m + off_kx);
   a.acc_o = reinterpret_cast<int32_t*>(m + off_ao);
   a.acc_d = reinterpret_cast<int32_t*>(m + off_ad);
   a.xres = reinterpret_cast<int16_t*>(m + off_x);
