@@ -3,15 +3,16 @@
 
 Headline (BASELINE.json metric): greedy INT8 decode tok/s at the Qwen2.5-0.5B shape
 (config 4: 24 layers, dim 896, 14/2 heads, head_dim 64, FFN 4864, vocab 151936, QKV bias),
-batch 1, after a 512-token prefill.  One step = one M=1 decode launch of the whole model
-(embedding gather, 24 layers, lm_head, argmax and record), each a replay of a captured HIP
-graph, with weights, KV cache and activations resident in HBM.
+batch 1, over the 256 positions after a 512-token prefill.  One step = one replay of the captured
+decode graph: the one-launch decode step (all 24 layers), the last layer's finish, the lm_head with
+the record row, and the greedy step (argmax, embedding gather of the next row), with weights, KV
+cache and activations resident in HBM.
 
 The JSON line also carries
-  roofline     : the decode kernel family that moves the most bytes per step (dec_mlp: the MLP
-                 with the down projection, 24 launches and 317 MB per step): algorithmic bytes per
-                 launch / average launch duration (HIP events around a graph of that family's
-                 launches, whose weights exceed the 256 MB memory-side cache), against 8 TB/s;
+  roofline     : the decode kernel family that moves the most bytes per step (dec_step: the
+                 one-launch decode step, every layer's weights and K/V rows, 363 MB): algorithmic
+                 bytes per launch / average launch duration (HIP events around a graph of that
+                 family's launch, whose weights exceed the 256 MB memory-side cache), against 8 TB/s;
                  `traffic` is the HBM bytes per launch measured with rocprofv3 counters
                  (profiles/decode_traffic.json, copy-kernel calibrated); extra.decode_hbm_frac_of_step
                  is the whole step's bytes over its time;
@@ -113,7 +114,8 @@ def config5_decode(args) -> dict:
     """Config 5: Qwen3-0.6B shape (28 layers, dim 1024, 16/8 heads, head_dim 128, Q/K norm, vocab
     151936), every layer's KV filled with seeded int8 at positions 0..4094, then the 28 layers +
     lm_head of one decode launch at position 4095 (T = 4096 keys per head) captured as one graph
-    and replayed (the embedding gather and greedy step, ~12 us, are not in it)."""
+    and replayed; then whole decode steps as decode_loop replays them (embedding gather, layers,
+    head and greedy step) at positions 4076 .. 4095 (T = 4077 .. 4096)."""
     import torch
 
     from llaccel_amd import golden as G
@@ -134,7 +136,14 @@ def config5_decode(args) -> dict:
     ga = g._chain.capture_family("dec_attention", T - 1)
     ta = time_graph(ga, 20) / g.n_layers
     att_bytes = g._chain.step_bytes(T)["dec_attention"] / g.n_layers
-    return {"T": T, "layers": g.n_layers, "ms_per_step": round(dt * 1e3, 4), "tok_s": round(1 / dt, 1),
+    g.decode_loop(1, T - 20, 2)  # captures the decode graph
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.decode_loop(1, T - 20, 20, sync=False)
+    torch.cuda.synchronize()
+    dl = (time.perf_counter() - t0) / 20
+    return {"T": T, "layers": g.n_layers, "ms_per_step": round(dl * 1e3, 4), "tok_s": round(1 / dl, 1),
+            "whole_step_positions": [T - 20, T - 1], "layers_head_ms_at_T4096": round(dt * 1e3, 4),
             "kv_bytes_read": kv_bytes, "step_bytes": step_bytes,
             "hbm_frac_of_step": round(step_bytes / dt / 1e9 / HBM_PEAK_GBS, 4),
             "attention_us_per_layer": round(ta * 1e6, 2), "attention_bytes_per_layer": round(att_bytes),
@@ -142,13 +151,6 @@ def config5_decode(args) -> dict:
             "note": "layers + lm_head of one M=1 decode launch at position 4095 (the decode chain's launches, "
                     "replayed at that position); attention: the layer's attention launches with the output "
                     "projection's partial sums"}
-
-
-# decode kernel of each plan-step family (rocprofv3 kernel names)
-# kernels of each decode family, as rocprofv3 names them (the decode chain; the fused per-block
-# plan's families for graphs without a chain)
-FAMILY_KERNELS = {"dec_attn_in": ("attn_in_kernel<8, true>",), "dec_attention": ("attention_rowhead<64, true>",),
-                  "dec_mlp": ("mlp_in_kernel<8, true>",), "dec_head": ("dec_finish_kernel", "norm_gemv_kernel")}
 
 
 def measured_traffic(family: str):
@@ -270,8 +272,8 @@ def gemm_sweep(min_reps: int = 8):
 
     ws = torch.zeros(int(_lib.lib().llhip_workspace_bytes()), dtype=torch.uint8, device="cuda")
     out = []
-    for M, K, N in ((2048, 896, 151936), (2048, 896, 4864), (2048, 4864, 896), (2048, 896, 896),
-                    (1, 896, 151936), (1, 896, 4864), (1, 4864, 896), (16, 896, 151936), (128, 896, 151936)):
+    shapes = [(M, K, N) for M in (2048, 128, 16, 1) for K, N in ((896, 151936), (896, 4864), (4864, 896), (896, 896))]
+    for M, K, N in shapes:  # config 2: the 16 shapes
         copies = max(4, -(-(512 << 20) // (N * K)))
         reps = max(min_reps, copies)
         g = torch.Generator(device="cuda").manual_seed(M + K + N)
@@ -475,7 +477,7 @@ def isa_device_bench() -> dict:
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode steps (config 4 decodes 256 positions)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--seed", type=int, default=0)
@@ -569,9 +571,9 @@ def main() -> None:
     prompt = synth.seeded_prompt(cfg, args.prompt, args.seed)
     L = len(prompt)
     g = G.GoldenModel(qdir)
-    need = L + args.warmup + args.steps + 1
+    need = L + max(args.warmup, args.steps) + 1
     if need > g.max_seq:
-        raise SystemExit(f"prompt + warmup + steps = {need} exceeds max_seq {g.max_seq}")
+        raise SystemExit(f"prompt + steps = {need} exceeds max_seq {g.max_seq}")
 
     # ---- prefill (one launch of the whole prompt) ----
     torch.cuda.synchronize()
@@ -608,27 +610,32 @@ def main() -> None:
     if args.profile == "prefill":
         return
 
-    # ---- decode: warmup (captures the graph), then the timed steps ----
+    # ---- decode: warmup steps at positions L.. (the first captures the graph), then the timed steps
+    # decode again from position L: config 4's positions L .. L + steps - 1.  Greedy decode is
+    # deterministic, so the timed run rewrites the warmup's KV rows with equal values. ----
     toks_w, rows_w = g.decode_loop(nxt, L, args.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    g.decode_loop(int(toks_w[-1]), L + args.warmup, args.steps, sync=False)
+    g.decode_loop(nxt, L, args.steps, sync=False)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    g._chain.check_step()
     tok_s = args.steps / dt
-    log(f"decode: {args.steps} steps in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
+    log(f"decode: {args.steps} steps (positions {L}..{L + args.steps - 1}) in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
     if args.profile == "decode":
         return
 
     # ---- per-kernel families of one decode step (graphs of the step's launches of one kind) ----
-    # Each family's launches of one step replayed alone, HIP events around 20 replays.  The dominant
-    # family by bytes (dec_mlp: the gate/up and down weights of all 24 layers, 317 MB) exceeds the
+    # Each family's launches of one step replayed alone at the last timed position, HIP events around
+    # 20 replays.  The dominant family by bytes (dec_step: every layer's weights, 363 MB) exceeds the
     # 256 MB memory-side cache, so its replays stream from HBM.
-    T = L + args.warmup + args.steps
+    import ctypes
+
+    T = L + args.steps
     fam = {}
     ch = g._chain
     fbytes = ch.step_bytes(T)
-    for kind in ch.FAMILIES:
+    for kind in ch.families(ctypes.c_void_p(g._st.data_ptr() + 4)):
         n = ch.launches(kind)
         graph = ch.capture_family(kind, T - 1)
         t = time_graph(graph, 20)
@@ -648,6 +655,22 @@ def main() -> None:
                 "bytes_per_launch": d["bytes_per_launch"], "avg_launch_us": d["us_per_launch"]}
     step_bytes = sum(fam[k]["bytes_per_launch"] * fam[k]["launches"] for k in fam)
 
+    # the three-launch chain (24 x 3 layer launches, then the head) on the first 64 of the same positions
+    chain = None
+    if ch._step is not None:
+        ch.use_step = False
+        g.decode_loop(nxt, L, 2)  # captures the chain's graph
+        n_ch = min(64, args.steps)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.decode_loop(nxt, L, n_ch, sync=False)
+        torch.cuda.synchronize()
+        t_ch = time.perf_counter() - t0
+        ch.use_step = True
+        chain = {"tok_s": round(n_ch / t_ch, 1), "ms_per_step": round(t_ch / n_ch * 1e3, 4), "steps": n_ch,
+                 "note": "the same decode as the headline through the three-launch-per-layer chain"}
+        log("decode chain", chain)
+
     # ---- CPU baselines (bounded samples of the same decode launches) ----
     cpu = cpus = None
     if not args.no_cpu:
@@ -666,7 +689,8 @@ def main() -> None:
              "prefill_api_ms": round(t_prefill_api * 1e3, 3), "prefill_first_call_ms": round(t_prefill * 1e3, 2),
              "decode_step_bytes": step_bytes, "decode_hbm_frac_of_step": round(step_bytes / (dt / args.steps) / 1e9
                                                                                 / HBM_PEAK_GBS, 4),
-             "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1), "decode_kernel_families": fam}
+             "decode_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1), "decode_kernel_families": fam,
+             "decode_chain": chain}
     if batch is not None:
         extra[f"decode_batch{args.batch}"] = batch
     if cpus is not None:
@@ -694,7 +718,7 @@ def main() -> None:
             "config": {"workload": "config 4: Qwen2.5-0.5B-shaped integer decoder (24L, dim 896, 14/2 heads, "
                                    "head_dim 64, FFN 4864, vocab 151936, QKV bias), greedy decode batch 1 after a "
                                    f"{L}-token prefill", "batch": 1, "prompt_tokens": L,
-                       "decode_positions": [L + args.warmup, L + args.warmup + args.steps - 1]},
+                       "decode_positions": [L, L + args.steps - 1]},
             "roofline": roofline, "cpu_baseline": cpu, "extra": extra}
     print(json.dumps(line), flush=True)
 

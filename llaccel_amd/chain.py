@@ -266,10 +266,18 @@ class Chain:
                   _vp(m._dt["embed"]), self.dim, _vp(m._act[m.q.input_name]), s)
 
     # ---- measurement ------------------------------------------------------------------------
-    FAMILIES = ("dec_attn_in", "dec_attention", "dec_mlp", "dec_head")
+    FAMILIES = ("dec_attn_in", "dec_attention", "dec_mlp", "dec_head")  # the three-launch chain
+    STEP_FAMILIES = ("dec_step", "dec_head")  # the one-launch step: every layer, then the head
+
+    def families(self, pd=None):
+        """The kernel families of a decode step as run(): the one-launch step's when it serves this
+        graph (pd: the device position pointer the step is created for), else the chain's."""
+        return self.STEP_FAMILIES if self.step(pd) is not None else self.FAMILIES
 
     def launches(self, family: str) -> int:
-        return 2 if family == "dec_head" else len(self.layers)  # dec_head: the finish and the lm_head
+        if family == "dec_head":
+            return 2  # the finish and the lm_head
+        return 1 if family == "dec_step" else len(self.layers)
 
     def capture_family(self, family: str | None, pos: int):
         """A HIP graph of one decode step's launches of `family` at the device position `pos` (for
@@ -297,6 +305,7 @@ class Chain:
             fam["dec_attention"] += ly.att_bytes(1, T) + ly.wo_bytes(1)
             fam["dec_mlp"] += ly.mlp.bytes_fn(1) + ly.wd_bytes(1)
         fam["dec_head"] = self.head.bytes_fn(1)
+        fam["dec_step"] = fam["dec_attn_in"] + fam["dec_attention"] + fam["dec_mlp"]  # the same ops, one launch
         return fam
 
 
