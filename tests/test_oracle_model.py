@@ -11,7 +11,8 @@ import pytest
 
 from oracle import golden_np as O
 
-CASES = ["ref_tiny_v2", "ref_tiny_v1", "ref_tiny_v2_pad", "ref_tiny_v2_m4"]
+CASES = ["ref_tiny_v2", "ref_tiny_v1", "ref_tiny_v2_pad", "ref_tiny_v2_m4",
+         "ref_qwen2_bias", "ref_qwen3_qknorm_d128", "ref_d256"]  # Qwen2 bias, Qwen3 Q/K norm at D = 128, D = 256
 
 
 def _load(golden_dir, name):
