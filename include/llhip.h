@@ -418,7 +418,8 @@ typedef struct llhip_dec_step_desc {
 typedef struct llhip_dec_step llhip_dec_step;
 /* golden.py:246-273 (GoldenModel over the qgraph's layers) -- validate the graph shape and allocate
  * the step's device state (zero-filled).  Returns NULL with llhip_last_error() set when the shape is
- * not supported. */
+ * not supported (head_dim other than 64, dim other than 576/896/1024, more units than CUs, weights,
+ * gammas, requant tables, biases or panels not 16-byte aligned). */
 llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d);
 /* golden.py:392-397 + 275-314 -- one decode row through every layer (stream-ordered; capturable in a
  * graph).  The row's input is x_in at position *pos_dev. */

@@ -649,9 +649,9 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     }
     __syncthreads();
   }
-  // RoPE (golden.py:141-158) -> quant (golden.py:119-120) -> K cache for keys, in 32-bit and
-  // double arithmetic: x and the table entries are i16, so |x1 c| + |x2 s| < 2^31, and the quant's
-  // mulshift of an i16 is exact in double (mulshift_small_sat)
+  // RoPE (golden.py:141-158) -> quant (golden.py:119-120) -> K cache for keys: the rotation's sums
+  // in 64-bit (x and the table entries are i16, so a sum reaches 2^31 when all four are -32768), and
+  // the quant's mulshift of an i16 is exact in double (mulshift_small_sat)
   const double sq = mulshift_scale(p.quant_M[role], (int)p.quant_S[role]);
   for (int m = mrope; m < M; m += blockDim.x / (half / SPL)) {
     int32_t c = c0, s = s0r;
@@ -663,8 +663,8 @@ __global__ __launch_bounds__(64 * MAXW) void attn_in_kernel(AttnInArgs p) {
     }
     const int j = jrope;
     const int32_t x1 = hres[m * D + j], x2 = hres[m * D + half + j];
-    const int16_t y1 = (int16_t)min(max(rshr32(x1 * c - x2 * s, 14), -32768), 32767);
-    const int16_t y2 = (int16_t)min(max(rshr32(x2 * c + x1 * s, 14), -32768), 32767);
+    const int16_t y1 = (int16_t)sat16(rshr((int64_t)x1 * c - (int64_t)x2 * s, 14));
+    const int16_t y2 = (int16_t)sat16(rshr((int64_t)x2 * c + (int64_t)x1 * s, 14));
     const int64_t o = (int64_t)m * Nrole + base;
     p.rope_out[role][o + j] = y1;
     p.rope_out[role][o + half + j] = y2;

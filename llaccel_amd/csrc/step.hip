@@ -1134,7 +1134,8 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
       return nullptr;
     }
     if (!al16(s.g1) || !al16(s.g2) || !al16(s.rq_o) || !al16(s.rq_d) || (s.bias_o && !al16(s.bias_o)) ||
-        (s.bias_d && !al16(s.bias_d)) || !al16(s.wo_panel) || !al16(s.wd_panel)) {
+        (s.bias_d && !al16(s.bias_d)) || !al16(s.wo_panel) || !al16(s.wd_panel) || !al16(s.W[0]) ||
+        !al16(s.W[1]) || !al16(s.W[2]) || !al16(s.Wg) || !al16(s.Wu)) {
       fail(-EINVAL, "dec_step: layer %lld operands must be 16-byte aligned", (long long)l);
       return nullptr;
     }

@@ -194,12 +194,13 @@ __device__ __forceinline__ void rope_quant_one(const RopeJob& j, IDX idx) {
   const int64_t pm = j.row_pos ? (int64_t)j.row_pos[m] : (int64_t)(j.pos_dev ? *j.pos_dev : j.pos) + m;
   if (pm < 0 || pm >= j.table_rows) return;  // device positions are checked by the caller; never read past the table
   const int64_t trow = pm * half;
-  // i16 operands: |a c| + |b s| < 2^31 (32-bit), and the quant of an i16 is exact in double
+  // i16 operands: the rotation's sums in 64-bit (b c + a s reaches 2^31 when all four are -32768),
+  // and the quant of an i16 is exact in double
   const int32_t c = j.cos_tab[trow + i], s = j.sin_tab[trow + i];
   const int64_t o = m * (int64_t)j.H * j.D + (int64_t)h * j.D;
   const int32_t a = j.x[m * j.ldx + h * j.D + i], b = j.x[m * j.ldx + h * j.D + half + i];
-  const int16_t y1 = (int16_t)min(max(rshr32(a * c - b * s, 14), -32768), 32767);
-  const int16_t y2 = (int16_t)min(max(rshr32(b * c + a * s, 14), -32768), 32767);
+  const int16_t y1 = (int16_t)sat16(rshr((int64_t)a * c - (int64_t)b * s, 14));
+  const int16_t y2 = (int16_t)sat16(rshr((int64_t)b * c + (int64_t)a * s, 14));
   j.y[o + i] = y1;
   j.y[o + half + i] = y2;
   const double sq = mulshift_scale(j.qM, j.qS);

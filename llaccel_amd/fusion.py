@@ -174,9 +174,11 @@ class _GateUpStep:
         self.desc = _lib.GateUpDesc()
         # the gate output is read only by the up linear (its aux) and the up output only by the
         # quant: in a launch that collects no activations (model._lean) neither is written
-        # (llhip_gate_up takes NULL for them on its one-launch path, K % 64 == 0)
+        # (llhip_gate_up takes NULL for them on its one-launch path: K % 64 == 0 and 16-byte aligned
+        # weights; weights are views into the qgraph's blob at its offsets, which need not be aligned)
         self.lean_ok = (int(g["K"]) % 64 == 0 and _reads(model, g["out"]) == 1 and _reads(model, u["out"]) == 1
-                        and model.q.output_name not in (g["out"], u["out"]))
+                        and model.q.output_name not in (g["out"], u["out"])
+                        and model._dt[g["w"]].data_ptr() % 16 == 0 and model._dt[u["w"]].data_ptr() % 16 == 0)
 
     def __call__(self, M, pos, pd=None):
         m, g, u, q, d = self.model, self.g, self.u, self.q, self.desc

@@ -214,6 +214,33 @@ def test_rope_quant_with_cache_writes(H, D, rows):
                   ptr(yqd), qM, qS, ptr(kcd), ptr(vd), H * D, ptr(vcd), max_seq, 0, stream())
 
 
+def test_rope_quant_extreme_table_entries():
+    """Table entries and inputs of -32768 (x2 c + x1 s = 2^31, past int32): llhip_rope and
+    llhip_rope_quant equal the oracle's int64 rotation (saturated to 32767)."""
+    from llaccel_amd import _lib
+    from tests.gpu_helpers import ptr, stream, torch, up
+
+    t = torch()
+    M, H, D, max_seq, qM, qS = 8, 2, 16, 4, 1234567891, 40
+    c = RNG.choice([-32768, 32767, 16384, -1], (max_seq, D // 2))
+    s = RNG.choice([-32768, 32767, -16384, 1], (max_seq, D // 2))
+    c[0], s[0] = -32768, -32768
+    x = RNG.choice([-32768, 32767, 5, -7], (M, H * D))
+    x[0] = -32768
+    want = O.rope(x, H, D, c, s, 0)
+    assert want[0, D // 2] == 32767
+    assert np.array_equal(G.rope(x[:1], H, D, c, s, 0), want[:1])
+    xd, cd, sd = up(x, np.int16), up(c, np.int16), up(s, np.int16)
+    yd = t.zeros((M, H * D), dtype=t.int16, device="cuda")
+    yqd = t.zeros((M, H * D), dtype=t.int8, device="cuda")
+    rp = up(np.arange(M) % max_seq, np.int32)
+    _lib.call("llhip_rope_quant", ptr(xd), M, H, D, H * D, ptr(cd), ptr(sd), max_seq, 0, None, ptr(rp), ptr(yd),
+              ptr(yqd), qM, qS, None, None, 0, None, max_seq, 0, stream())
+    want_y = np.stack([O.rope(x[m:m + 1], H, D, c, s, m % max_seq)[0] for m in range(M)])
+    assert np.array_equal(yd.cpu().numpy(), want_y)
+    assert np.array_equal(yqd.cpu().numpy(), O.vquant(want_y, qM, qS))
+
+
 def test_rope_quant2_equals_two_calls():
     """llhip_rope_quant2 (the query rows, then the key rows with the layer's kv_write, in one launch)
     equals the oracle's rope, vquant and cache write of each part, and refuses a bad part as the

@@ -272,6 +272,26 @@ def test_rope_matches_reference_and_float(ref_lib):
         assert np.abs(y - ref).max() < 3 + 1e-9
 
 
+def test_rope_extreme_table_entries(ref_lib):
+    """Table entries and inputs of -32768: x2 c + x1 s = 2^31, past int32 (golden.py:141-158 sums in
+    int64), so the rotated value saturates to 32767; the compiled numerics.h agrees."""
+    H, D = 1, 16
+    cos_t = np.full((2, D // 2), -32768, np.int64)
+    sin_t = np.full((2, D // 2), -32768, np.int64)
+    cos_t[1, ::2], sin_t[1, 1::2] = 32767, 32767
+    x = np.full((2, H * D), -32768, np.int64)
+    x[1, 3] = 32767
+    y = O.rope(x, H, D, cos_t, sin_t, 0)
+    assert y[0, D // 2] == 32767  # b c + a s = 2^31 -> rshr 2^17 -> sat16 32767
+    assert y[0, 0] == 0  # a c - b s = 0
+    for m in range(2):
+        out = np.zeros(H * D, np.int16)
+        xm = x[m].astype(np.int16)
+        c, s = cos_t[m].astype(np.int16), sin_t[m].astype(np.int16)
+        ref_lib.ref_rope(xm.ctypes.data, out.ctypes.data, H, D, c.ctypes.data, s.ctypes.data)
+        assert y[m].tolist() == out.tolist()
+
+
 # ---- attention -------------------------------------------------------------------------------
 def _ref_attn(ref_lib, q, k, v, Ms, Ss, Mo, So, wide):
     D, T = q.shape[0], k.shape[0]
