@@ -104,6 +104,9 @@ typedef struct llhip_rope_quant_desc {
   int64_t ldv;
   void* vc;             /* V cache or NULL */
   int64_t max_seq, slot_stride;
+  int64_t seq_rows;     /* > 0 (no pos_dev, no row_pos): M / seq_rows sequences of seq_rows rows; row m is
+                         * at position pos + m % seq_rows, its caches at kc/vc + (m / seq_rows) * slot_stride
+                         * (a batch of prompts prefilled in one launch); 0: off */
 } llhip_rope_quant_desc;
 /* golden.py:141-158 + 119-120 [+ 344-351]  two llhip_rope_quant calls in one launch (a prompt
  * chunk's query rows, then its key rows with the layer's kv_write): the same checks and results as
@@ -170,6 +173,16 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
                     const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
                     const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
                     int64_t prob_bits, int8_t* out, int64_t ldo, void* ws, void* stream);
+
+/* golden.py:353-366 for a batch of prompts prefilled in one launch (golden.py:379-390 per prompt):
+ * M / seq_rows sequences of seq_rows rows, seq_rows a multiple of 16.  Row m is row m % seq_rows of
+ * sequence m / seq_rows, at position pos + m % seq_rows, over the caches at kc/vc + (m / seq_rows) *
+ * slot_stride, slot_stride >= Hkv * max_seq * D.  A row sees the keys of its own sequence up to its
+ * position: the same results per sequence as llhip_attention on that sequence's rows alone. */
+int llhip_attention_seqs(const int8_t* q, int64_t M, int64_t seq_rows, int64_t H, int64_t Hkv, int64_t D,
+                         int64_t ldq, int64_t pos, const int8_t* kc, const int8_t* vc, int64_t slot_stride,
+                         int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So, int64_t prob_bits,
+                         int8_t* out, int64_t ldo, void* stream);
 
 /* No counterpart in the reference: llhip_attention for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same

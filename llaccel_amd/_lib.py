@@ -46,6 +46,8 @@ _SIGS = {
     "llhip_kv_write": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p],
     "llhip_attention": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64,
                         _i64, _p, _i64, _p, _p],
+    "llhip_attention_seqs": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                             _i64, _p, _i64, _p],
     "llhip_attention_noalloc": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64,
                                 _i64, _i64, _p, _i64, _p],
     "llhip_embed_rows": [_p, _i64, _i64, _p, _i64, _i64, _p, _p],
@@ -146,7 +148,7 @@ class RopeQuantDesc(ctypes.Structure):
     _fields_ = [("x", _p), ("M", _i64), ("H", _i64), ("D", _i64), ("ldx", _i64), ("cos_tab", _p), ("sin_tab", _p),
                 ("table_rows", _i64), ("pos", _i64), ("pos_dev", _p), ("row_pos", _p), ("y", _p), ("yq", _p),
                 ("qM", _i64), ("qS", _i64), ("kc", _p), ("v", _p), ("ldv", _i64), ("vc", _p), ("max_seq", _i64),
-                ("slot_stride", _i64)]
+                ("slot_stride", _i64), ("seq_rows", _i64)]
 
 
 class LinearProblem(ctypes.Structure):

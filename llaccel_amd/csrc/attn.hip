@@ -32,6 +32,7 @@ struct AttnArgs {
   const int32_t* pos_dev;
   const int32_t* row_pos;  // per-row positions (row m in cache slot m), or null
   int64_t slot_stride;
+  int seq_rows;  // > 0: rows of seq_rows each per sequence (row m at pos + m % seq_rows, slot m / seq_rows)
   int64_t ldq, ldo, max_seq;
   int64_t Ms, Mo;
   int Ss, So;
@@ -511,14 +512,20 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int nw = blockDim.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int pos = load_pos(p.pos_dev, p.pos);
+  int pos = load_pos(p.pos_dev, p.pos);
+  int64_t slot = 0;
+  if (p.seq_rows > 0) {  // a block of sequence b = m0 / seq_rows (seq_rows % 16 == 0): its own caches
+    const int b = m0 / p.seq_rows;
+    pos -= b * p.seq_rows;
+    slot = (int64_t)b * p.slot_stride;
+  }
   const int mlast = min(m0 + AT_ROWS, p.M) - 1;
   const int Tb = min(pos + mlast + 1, (int)p.max_seq);  // keys any row of the block sees
   const int ntiles = (Tb + 63) >> 6;
   const int m = m0 + lr;  // this lane's query row
   const int tlim = m < p.M ? min(pos + m + 1, (int)p.max_seq) : 0;
-  const int8_t* kbase = p.kc + (int64_t)g * p.max_seq * D;
-  const int8_t* vbase = p.vc + (int64_t)g * p.max_seq * D;
+  const int8_t* kbase = p.kc + slot + (int64_t)g * p.max_seq * D;
+  const int8_t* vbase = p.vc + slot + (int64_t)g * p.max_seq * D;
   const Rsrc kr = rsrc(kbase, (int64_t)Tb * D), vr = rsrc(vbase, (int64_t)Tb * D);
 
   v4i qf[DK];
@@ -1094,7 +1101,7 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
                           const int32_t* pos_dev, const int32_t* row_pos, int64_t slot_stride, const int8_t* kc,
                           const int8_t* vc, int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So,
                           int64_t prob_bits, int8_t* out, int64_t ldo, void* split_ws, int64_t split_bytes,
-                          void* stream, const WoFold* fold = nullptr) {
+                          void* stream, const WoFold* fold = nullptr, int64_t seq_rows = 0) {
   if (prob_bits != 8 && prob_bits != 15) return fail(-EINVAL, "attention prob_bits must be 8 or 15");
   if (M < 0 || H <= 0 || Hkv <= 0 || H % Hkv) return fail(-EINVAL, "attention: H must be a multiple of Hkv");
   if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256)
@@ -1103,12 +1110,22 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
     return fail(-EINVAL, "attention: multipliers must be u32, shifts in [0,63]");
   if (ldq < H * D || ldo < H * D) return fail(-EINVAL, "attention: leading dimension too small");
   if (row_pos && slot_stride < Hkv * max_seq * D) return fail(-EINVAL, "attention: cache slots overlap");
-  if (!pos_dev && !row_pos && (pos < 0 || pos + M > max_seq))
+  if (seq_rows > 0) {  // sequence-major rows: row m is row m % seq_rows of sequence m / seq_rows
+    if (row_pos || pos_dev || fold || seq_rows % AT_ROWS || M % seq_rows)
+      return fail(-EINVAL, "attention: sequences of seq_rows rows need M %% seq_rows == 0, seq_rows %% %d == 0",
+                  AT_ROWS);
+    if (pos < 0 || pos + seq_rows > max_seq)
+      return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)pos,
+                  (long long)(pos + seq_rows - 1), (long long)max_seq);
+    if (slot_stride < Hkv * max_seq * D) return fail(-EINVAL, "attention: cache slots overlap");
+    if (M / seq_rows * slot_stride >= (1ll << 40)) return fail(-EINVAL, "attention: caches too large");
+  } else if (!pos_dev && !row_pos && (pos < 0 || pos + M > max_seq)) {
     return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)pos, (long long)(pos + M - 1),
                 (long long)max_seq);
+  }
   if (M == 0) return 0;
-  const int64_t tmax = (pos_dev || row_pos) ? max_seq : pos + M;
-  const bool tiled = !row_pos && M >= AT_MIN_M;
+  const int64_t tmax = (pos_dev || row_pos) ? max_seq : pos + (seq_rows > 0 ? seq_rows : M);
+  const bool tiled = !row_pos && (M >= AT_MIN_M || seq_rows > 0);
   if (tmax > (tiled ? AT_MAX_T : ATTN_MAX_T))
     return fail(-EINVAL, "attention: context %lld exceeds %d", (long long)tmax, tiled ? AT_MAX_T : ATTN_MAX_T);
   if (max_seq * D * Hkv >= (1ll << 31)) return fail(-EINVAL, "attention: KV cache above 2 GiB");
@@ -1120,6 +1137,7 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   p.pos_dev = pos_dev;
   p.row_pos = row_pos;
   p.slot_stride = slot_stride;
+  p.seq_rows = (int)seq_rows;
   p.ldq = ldq;
   p.ldo = ldo;
   p.max_seq = max_seq;
@@ -1154,7 +1172,7 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   // row's scores for a single-row launch)
   const bool one = M == 1;
   auto split_need = [&](int64_t S) { return pairs * S * AT_ROWS * (2 + D) * 4 + (one ? pairs * ktiles * 64 * 4 : 0); };
-  if (!row_pos && split_ws && tmax <= AT_MAX_T && ktiles >= AT_SPLIT_MIN_TILES && pairs * 4 <= cus &&
+  if (!row_pos && seq_rows == 0 && split_ws && tmax <= AT_MAX_T && ktiles >= AT_SPLIT_MIN_TILES && pairs * 4 <= cus &&
       split_need(2) <= split_bytes) {
     int S = (int)std::min<int64_t>(std::min<int64_t>(ceil_div(cus, pairs), ceil_div(ktiles, 4)), AT_SPLIT_MAXS);
     while (S > 2 && split_need(S) > split_bytes) --S;
@@ -1286,6 +1304,15 @@ int llhip_attention(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t 
   return attention_impl(q, M, H, Hkv, D, ldq, pos, pos_dev, row_pos, slot_stride, kc, vc, max_seq, Ms, Ss, Mo, So,
                         prob_bits, out, ldo, ws ? static_cast<char*>(ws) + WS_SCRATCH : nullptr, WS_SCRATCH_BYTES,
                         stream);
+}
+
+int llhip_attention_seqs(const int8_t* q, int64_t M, int64_t seq_rows, int64_t H, int64_t Hkv, int64_t D,
+                         int64_t ldq, int64_t pos, const int8_t* kc, const int8_t* vc, int64_t slot_stride,
+                         int64_t max_seq, int64_t Ms, int64_t Ss, int64_t Mo, int64_t So, int64_t prob_bits,
+                         int8_t* out, int64_t ldo, void* stream) {
+  if (seq_rows <= 0) return fail(-EINVAL, "attention_seqs: seq_rows must be positive");
+  return attention_impl(q, M, H, Hkv, D, ldq, pos, nullptr, nullptr, slot_stride, kc, vc, max_seq, Ms, Ss, Mo, So,
+                        prob_bits, out, ldo, nullptr, 0, stream, nullptr, seq_rows);
 }
 
 int llhip_dec_attention(const llhip_dec_attn_desc* d, void* ws, void* stream) {

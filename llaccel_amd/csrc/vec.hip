@@ -171,6 +171,7 @@ __global__ void rope_kernel(const int16_t* __restrict__ x, int64_t M, int H, int
 struct RopeJob {
   const int16_t* x;
   int64_t M, ldx, table_rows, qM, ldv, max_seq, slot_stride, total;
+  int64_t seq_rows;  // > 0: row m at pos + m % seq_rows in cache slot m / seq_rows
   int H, D, pos, qS;
   const int16_t* cos_tab;
   const int16_t* sin_tab;
@@ -191,7 +192,9 @@ __device__ __forceinline__ void rope_quant_one(const RopeJob& j, IDX idx) {
   const int64_t m = (int64_t)(idx / hh);
   const int rem = (int)(idx % hh);
   const int h = rem / half, i = rem % half;
-  const int64_t pm = j.row_pos ? (int64_t)j.row_pos[m] : (int64_t)(j.pos_dev ? *j.pos_dev : j.pos) + m;
+  const int64_t pm = j.row_pos    ? (int64_t)j.row_pos[m]
+                     : j.seq_rows ? (int64_t)j.pos + m % j.seq_rows
+                                  : (int64_t)(j.pos_dev ? *j.pos_dev : j.pos) + m;
   if (pm < 0 || pm >= j.table_rows) return;  // device positions are checked by the caller; never read past the table
   const int64_t trow = pm * half;
   // i16 operands: the rotation's sums in 64-bit (b c + a s reaches 2^31 when all four are -32768),
@@ -209,7 +212,8 @@ __device__ __forceinline__ void rope_quant_one(const RopeJob& j, IDX idx) {
   j.yq[o + i] = q1;
   j.yq[o + half + i] = q2;
   if (j.kc && pm < j.max_seq) {  // never write past a cache
-    const int64_t dst = (j.row_pos ? m * j.slot_stride : 0) + ((int64_t)h * j.max_seq + pm) * j.D;
+    const int64_t slot = j.row_pos ? m * j.slot_stride : (j.seq_rows ? m / j.seq_rows * j.slot_stride : 0);
+    const int64_t dst = slot + ((int64_t)h * j.max_seq + pm) * j.D;
     j.kc[dst + i] = q1;
     j.kc[dst + half + i] = q2;
     if (j.vc) {
@@ -503,14 +507,18 @@ static int rope_job(const llhip_rope_quant_desc& d, RopeJob& j) {
   if (M < 0 || H < 0 || D < 0 || D % 2) return fail(-EINVAL, "rope_quant: bad geometry (D must be even)");
   if (d.ldx < H * D) return fail(-EINVAL, "rope_quant: leading dimension too small");
   if (!u32_ok(d.qM) || !shift_ok(d.qS)) return fail(-EINVAL, "rope_quant: quant multiplier must be u32, shift in [0,63]");
-  if (!d.pos_dev && !d.row_pos && (d.pos < 0 || d.pos + M > d.table_rows))
+  if (d.seq_rows < 0 || (d.seq_rows > 0 && (d.pos_dev || d.row_pos || M % d.seq_rows)))
+    return fail(-EINVAL, "rope_quant: sequences of seq_rows rows need M %% seq_rows == 0 and no row positions");
+  const int64_t span = d.seq_rows > 0 ? d.seq_rows : M;  // consecutive positions of one sequence
+  if (!d.pos_dev && !d.row_pos && (d.pos < 0 || d.pos + span > d.table_rows))
     return fail(-ERANGE, "rope: positions exceed the table");
   if (d.vc && (!d.kc || !d.v || d.ldv < H * D)) return fail(-EINVAL, "rope_quant: the V cache write needs kc and v rows");
   if (d.kc) {
-    if (!d.pos_dev && !d.row_pos && d.pos + M > d.max_seq)
-      return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)d.pos, (long long)(d.pos + M - 1),
+    if (!d.pos_dev && !d.row_pos && d.pos + span > d.max_seq)
+      return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)d.pos, (long long)(d.pos + span - 1),
                   (long long)d.max_seq);
-    if (d.row_pos && d.slot_stride < H * d.max_seq * D) return fail(-EINVAL, "rope_quant: cache slots overlap");
+    if ((d.row_pos || d.seq_rows > 0) && d.slot_stride < H * d.max_seq * D)
+      return fail(-EINVAL, "rope_quant: cache slots overlap");
   }
   j = RopeJob{};
   j.x = static_cast<const int16_t*>(d.x);
@@ -521,6 +529,7 @@ static int rope_job(const llhip_rope_quant_desc& d, RopeJob& j) {
   j.ldv = d.ldv;
   j.max_seq = d.max_seq;
   j.slot_stride = d.slot_stride;
+  j.seq_rows = d.seq_rows;
   j.total = M * H * (D / 2);
   j.H = (int)H;
   j.D = (int)D;
@@ -557,7 +566,7 @@ int llhip_rope_quant(const int16_t* x, int64_t M, int64_t H, int64_t D, int64_t 
                      const int32_t* row_pos, int16_t* y, int8_t* yq, int64_t qM, int64_t qS, int8_t* kc,
                      const int8_t* v, int64_t ldv, int8_t* vc, int64_t max_seq, int64_t slot_stride, void* stream) {
   const llhip_rope_quant_desc d{x, M, H, D, ldx, cos_tab, sin_tab, table_rows, pos, pos_dev, row_pos, y, yq, qM, qS,
-                                kc, v, ldv, vc, max_seq, slot_stride};
+                                kc, v, ldv, vc, max_seq, slot_stride, 0};
   RopeJob a, none{};
   const int rc = rope_job(d, a);
   return rc ? rc : rope_launch(a, none, stream);

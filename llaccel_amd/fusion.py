@@ -104,6 +104,9 @@ class _RopeQuantStep:
         d.pos_dev, d.row_pos = pdev, rpos
         d.y, d.yq, d.qM, d.qS = _vp(m._buf(ro["out"])), _vp(m._buf(qu["out"])), int(qu["M"]), int(qu["S"])
         d.kc, d.v, d.ldv, d.vc, d.max_seq, d.slot_stride = kc, v, ldv, vc, m.max_seq, stride
+        from .golden import _seq_rows
+
+        d.seq_rows = _seq_rows(pd)
 
     def __call__(self, M, pos, pd=None):
         for d, (ro, qu, kvw) in zip(self.desc, self.parts):

@@ -395,11 +395,27 @@ class _RowPos:
         self.ptr, self.stride = ptr, stride
 
 
+class _SeqRows:
+    """Position context of a batch prefill launch: the rows are M / rows sequences of `rows` rows
+    each; row m is row m % rows of sequence m / rows, at position pos + m % rows, with its K/V caches
+    in slot m / rows (`stride` elements after the slot before)."""
+
+    def __init__(self, rows: int, stride: int) -> None:
+        self.rows, self.stride = rows, stride
+
+
 def _pos_args(pd):
     """(pos_dev, row_pos, slot_stride) kernel arguments of a step's position context."""
     if isinstance(pd, _RowPos):
         return None, pd.ptr, pd.stride
+    if isinstance(pd, _SeqRows):
+        return None, None, pd.stride
     return pd, None, 0
+
+
+def _seq_rows(pd) -> int:
+    """The rows per sequence of a batch prefill context (0 otherwise)."""
+    return pd.rows if isinstance(pd, _SeqRows) else 0
 
 
 class _Step:
@@ -482,6 +498,8 @@ class GoldenModel:
         kc, vc = self._kv[layer]
         if isinstance(pd, _RowPos):
             return _ptr(kc), _ptr(vc), None, pd.ptr, pd.stride
+        if isinstance(pd, _SeqRows):
+            return _ptr(kc), _ptr(vc), None, None, pd.stride
         return _ptr(kc[self._slot]), _ptr(vc[self._slot]), pd, None, 0
 
     def _ensure_capacity(self, M: int) -> None:
@@ -706,6 +724,8 @@ class GoldenModel:
         rows = int(cos_t.shape[0])
 
         def run(M, pos, pd=None):
+            if isinstance(pd, _SeqRows):
+                raise ValueError("rope: no batch-prefill form (unfused graph)")
             pdev, rpos, _ = _pos_args(pd)
             _lib.call("llhip_rope", _ptr(self._buf(src)), M, H, D, H * D, _ptr(cos_t), _ptr(sin_t), rows, pos, pdev,
                       rpos, _ptr(self._buf(dst)), H * D, _stream())
@@ -721,6 +741,8 @@ class GoldenModel:
         ksrc, vsrc = op["k"], op["v"]
 
         def run(M, pos, pd=None):
+            if isinstance(pd, _SeqRows):
+                raise ValueError("kv_write: no batch-prefill form (unfused graph)")
             kcp, vcp, pdev, rpos, stride = self._kv_args(layer, pd)
             _lib.call("llhip_kv_write", _ptr(self._buf(ksrc)), _ptr(self._buf(vsrc)), M, Hkv, D, ck, cv, pos, pdev,
                       rpos, stride, kcp, vcp, self.max_seq, _stream())
@@ -749,6 +771,10 @@ class GoldenModel:
             if layer not in self._kv:
                 raise KeyError(layer)
             kcp, vcp, pdev, rpos, stride = self._kv_args(layer, pd)
+            if isinstance(pd, _SeqRows):
+                _lib.call("llhip_attention_seqs", _ptr(self._buf(src)), M, pd.rows, H, Hkv, D, H * D, pos, kcp, vcp,
+                          stride, self.max_seq, Ms, Ss, Mo, So, pb, _ptr(self._buf(dst)), H * D, _stream())
+                return
             _lib.call("llhip_attention", _ptr(self._buf(src)), M, H, Hkv, D, H * D, pos, pdev, rpos, stride, kcp, vcp,
                       self.max_seq, Ms, Ss, Mo, So, pb, _ptr(self._buf(dst)), H * D, _ptr(self._ws), _stream())
 
@@ -1103,16 +1129,54 @@ class GoldenModel:
             return None
         return (_down(self._b_ring_tok[:n]).astype(np.int64), self._b_ring_rows[:n].cpu().numpy())
 
-    def prefill_batch(self, prompts) -> list[list[np.ndarray]]:
+    def prefill_batch(self, prompts) -> list[Sequence]:
         """Reallocate the KV caches with B = len(prompts) slots and prefill prompt b into slot b
-        (the launches of prefill()); returns each prompt's prefill logits rows."""
+        (golden.py:379-390 per prompt); returns each prompt's prefill logits rows.
+
+        Prompts of one length run as ONE launch of B x padded rows: sequence b's rows (its prompt,
+        then the zero pad rows of its last chunk) at positions 0.. in slot b, each row seeing only
+        its own sequence's keys -- the whole-prompt prefill of every prompt at once, so the logits
+        and the KV state equal B separate prefill() calls (a GPU test checks it), with the GEMMs at
+        M = B x padded rows.  Otherwise (other lengths, a graph with unfused rope or kv_write ops)
+        one prefill() per prompt."""
+        prompts = [[int(t) for t in p] for p in prompts]
         self._alloc_kv(len(prompts))
+        B = len(prompts)
+        L = len(prompts[0]) if prompts else 0
+        Lp = -(-L // self.prefill_m) * self.prefill_m
+        if (B > 1 and L > self.prefill_m and all(len(p) == L for p in prompts) and self.whole_prompt_prefill
+                and Lp % 16 == 0 and Lp <= self.max_seq
+                and not any(st.kind in ("rope", "kv_write") for st in self._plan)):
+            rows = self._prefill_seqs(prompts, Lp)
+            return [DeviceRows(rows[b * Lp:b * Lp + L]) for b in range(B)]
         out = []
         for b, p in enumerate(prompts):
             self._slot = b
             out.append(self.prefill(p))
         self._slot = 0
         return out
+
+    def _prefill_seqs(self, prompts, Lp: int):
+        """The one-launch batch prefill: embedding gathers of every prompt into its Lp rows (pad rows
+        zero), then the op list over B x Lp rows in the sequence-major position context.  Returns a
+        device copy of the B x Lp logits rows."""
+        B = len(prompts)
+        M = B * Lp
+        self._ensure_capacity(M)
+        x = self._act[self.q.input_name]
+        toks = [_up(self._token_rows(p), np.int32) for p in prompts]  # alive until the launches ran
+        for b, td in enumerate(toks):
+            _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, _ptr(td),
+                      len(prompts[b]), Lp, _ptr(x[b * Lp]), _stream())
+        kc0 = next(iter(self._kv.values()))[0]
+        self._lean = True  # no activation is collected: dead intermediates go unwritten
+        try:
+            self._execute(M, 0, _SeqRows(Lp, kc0[0].numel()))
+        finally:
+            self._lean = False
+        # freed in stream order: the caching allocator reuses the token buffers only after the gathers
+        del toks
+        return self._act[self.q.output_name][:M].clone()
 
     def generate_batch(self, prompts, n_tokens: int) -> list[dict]:
         """Greedy generation of B = len(prompts) independent sequences of one prompt length: each

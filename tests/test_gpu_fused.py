@@ -135,3 +135,42 @@ def test_fused_and_unfused_graph_decode_agree(tmp_path_factory):
     prompt = synth.seeded_prompt("smol", 33, 9)
     g, u = G.GoldenModel(qdir), G.GoldenModel(qdir, fuse=False)
     assert g.generate(prompt, 24) == u.generate(prompt, 24)
+
+
+@pytest.mark.parametrize("cfg", ["smol", "qwen25", "qwen3"])
+def test_prefill_batch_one_launch_equals_separate_prefills(tmp_path_factory, cfg):
+    """prefill_batch of prompts of one length runs ONE launch of B x padded rows (sequence-major
+    positions, slot per sequence); its logits rows and every slot's KV equal separate prefill()
+    calls (each the whole-prompt launch into slot 0 of its own model)."""
+    qdir = _qgraph(tmp_path_factory, cfg, True)
+    B, L = 3, 61
+    prompts = [synth.seeded_prompt(cfg, L, 10 + b) for b in range(B)]
+    g = G.GoldenModel(qdir)
+    calls = []
+    one = g._prefill_seqs
+    g._prefill_seqs = lambda *a: calls.append(1) or one(*a)
+    rows = g.prefill_batch(prompts)
+    assert calls == [1] and len(rows) == B
+    for b, p in enumerate(prompts):
+        s = G.GoldenModel(qdir)
+        want = s.prefill(p)
+        assert len(rows[b]) == L == len(want)
+        assert np.array_equal(rows[b].numpy(), want.numpy()), b
+        got_kv, want_kv = g.kv_of(b), s.kv
+        for layer in want_kv:
+            assert np.array_equal(got_kv[layer][0], want_kv[layer][0]), (b, layer)
+            assert np.array_equal(got_kv[layer][1], want_kv[layer][1]), (b, layer)
+
+
+def test_prefill_batch_other_lengths_run_separately(tmp_path_factory):
+    """Prompts of different lengths (or one chunk long) take one prefill() per prompt."""
+    qdir = _qgraph(tmp_path_factory, "qwen25", True)
+    g = G.GoldenModel(qdir)
+    calls = []
+    one = g._prefill_seqs
+    g._prefill_seqs = lambda *a: calls.append(1) or one(*a)
+    prompts = [synth.seeded_prompt("qwen25", 40, 1), synth.seeded_prompt("qwen25", 33, 2)]
+    rows = g.prefill_batch(prompts)
+    assert calls == [] and [len(r) for r in rows] == [40, 33]
+    s = G.GoldenModel(qdir)
+    assert np.array_equal(np.asarray(rows[1][32]), np.asarray(s.prefill(prompts[1])[32]))

@@ -227,9 +227,9 @@ def test_rope_quant_extreme_table_entries():
     c[0], s[0] = -32768, -32768
     x = RNG.choice([-32768, 32767, 5, -7], (M, H * D))
     x[0] = -32768
-    want = O.rope(x, H, D, c, s, 0)
+    want = O.rope(x[:1], H, D, c, s, 0)
     assert want[0, D // 2] == 32767
-    assert np.array_equal(G.rope(x[:1], H, D, c, s, 0), want[:1])
+    assert np.array_equal(G.rope(x[:1], H, D, c, s, 0), want)
     xd, cd, sd = up(x, np.int16), up(c, np.int16), up(s, np.int16)
     yd = t.zeros((M, H * D), dtype=t.int16, device="cuda")
     yqd = t.zeros((M, H * D), dtype=t.int8, device="cuda")
