@@ -84,7 +84,7 @@ struct Args {
   int16_t* xres;   // [2][dim]: the layer input x, the attention residual x1
   int32_t* acc_o;  // [2][R][dim] output-projection partial sums (layer parity)
   int32_t* acc_d;  // [2][R][dim] down-projection partial sums
-  uint32_t* fl0;   // stage flags, [NREP][256] words each: S12 units' layer-0 clearing
+  uint32_t* fl0;   // stage flags, [NREP][32 lines][32] words each: S12 units' layer-0 clearing
   uint32_t* fl2;   // S12 units done
   uint32_t* fl3;   // S3 units done
   uint32_t* ctl;   // [0] launches, [1] workgroups done, [2] error, [3] abort
@@ -162,47 +162,45 @@ __device__ __forceinline__ int32_t prob_norm(uint32_t p, uint32_t inv, uint64_t 
 }
 
 // ---- flags ------------------------------------------------------------------------------------
-// Stage flags: each producer writes its word into NREP replicas (1 KiB apart, so on separate
-// lines); workgroup b polls replica b % NREP, so no line has more than G / NREP pollers.
+// Stage flags: each producer writes its word into NREP replicas; workgroup b polls replica b % NREP
+// (the replica of its XCD), so no line has more than G / NREP pollers.  Within a replica the n
+// producers' words are spread over nl = min(32, ceil(n / 4)) lines of 32 words (word of producer u:
+// line u % nl, slot u / nl), so a line takes at most 4 writes at once (8 for 200+ producers): the
+// memory side serialises the partial writes to one line, and 56 or 200 of them packed into two or
+// seven lines completed up to a microsecond apart from replica to replica (8 writers a line:
+// 364 us a step, 4: 361 us, 64 lines of 4: no better).
 constexpr int NREP = 8;
-constexpr int FLAG_WORDS = 256 * NREP;
+constexpr int REP_WORDS = 32 * 32;  // 32 lines of 32 words (4 KiB) per replica
+constexpr int FLAG_WORDS = REP_WORDS * NREP;
+__device__ __forceinline__ int flag_lines(int n) { return min(32, (n + 3) / 4); }
+__device__ __forceinline__ uint32_t flag_off(int u, int nl) { return 4u * (uint32_t)((u % nl) * 32 + u / nl); }
 
-// Wave 0: wait until words [0, n) of f (n <= 256) all reach `want` (signed 32-bit difference, so
-// epochs may wrap).  False on timeout (recorded) or abort.  Two loads are kept in flight, so a flag
-// set between them is seen half a round trip sooner.
+// Wave 0: wait until the words of producers [0, n) (n <= 256) in replica f all reach `want` (signed
+// 32-bit difference, so epochs may wrap).  False on timeout (recorded) or abort.  Lane i reads the
+// words of producers i, i + 64, i + 128, i + 192.
 __device__ bool poll(const uint32_t* f, int n, uint32_t want, uint32_t* ctl, uint32_t spin_max) {
-  const int lane = threadIdx.x & 63;
-  const Rsrc fr = rsrc(f, 1024), cr = rsrc(ctl, 16);
-  const int w0 = 4 * lane;
-  auto all_set = [&](const v4i& v) {
+  const int lane = threadIdx.x & 63, nl = flag_lines(n);
+  const Rsrc fr = rsrc(f, REP_WORDS * 4), cr = rsrc(ctl, 16);
+  uint32_t off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) off[j] = lane + 64 * j < n ? flag_off(lane + 64 * j, nl) : LD_OOB;
+  for (uint32_t it = 0;; ++it) {
+    __asm__ volatile("" ::: "memory");  // fresh loads on every pass
+    uint32_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = ldc4(fr, off[j]);
     bool ok = true;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ok = ok && (w0 + j >= n || (int32_t)((uint32_t)v[j] - want) >= 0);
-    return __builtin_amdgcn_ballot_w64(!ok) == 0;
-  };
-  const uint32_t off = w0 < n ? 4u * w0 : LD_OOB;  // lanes past the producers read nothing
-  v4i nxt = ldc16(fr, off);
-  for (uint32_t it = 0;; ++it) {
-    __asm__ volatile("" ::: "memory");  // a fresh load on every pass
-    const v4i cur = nxt;
-    nxt = ldc16(fr, off);
-    __asm__ volatile("s_waitcnt vmcnt(1)" ::: "memory");  // cur has arrived, nxt may still be in flight
-    if (all_set(cur)) {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      return true;
-    }
+    for (int j = 0; j < 4; ++j) ok = ok && (lane + 64 * j >= n || (int32_t)(v[j] - want) >= 0);
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
     if (it >= spin_max) {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       if (lane == 0) {
         __hip_atomic_fetch_or(ctl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(ctl + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       return false;
     }
-    if ((it & 31) == 31 && ldc4(cr, 12) != 0) {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      return false;
-    }
+    if ((it & 31) == 31 && ldc4(cr, 12) != 0) return false;  // another workgroup gave up
   }
 }
 
@@ -246,9 +244,9 @@ __device__ bool take_tagged(const uint32_t* p, uint32_t tag, uint32_t first, uin
 }
 
 // wave 0: store the flag word of producer idx into every replica (after the workgroup's drain)
-__device__ __forceinline__ void publish(uint32_t* f, int idx, uint32_t v) {
+__device__ __forceinline__ void publish(uint32_t* f, int idx, int n, uint32_t v) {
   const int lane = threadIdx.x & 63;
-  if (lane < NREP) stc4(rsrc(f, FLAG_WORDS * 4), 4u * (256 * lane + idx), v);
+  if (lane < NREP) stc4(rsrc(f, FLAG_WORDS * 4), 4u * REP_WORDS * lane + flag_off(idx, flag_lines(n)), v);
 }
 
 // ---- LDS hand-offs inside the workgroup ------------------------------------------------------
@@ -537,7 +535,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         }
         if (l > 0) {
           bool ok = true;
-          if (wave == 0) ok = poll(a.fl3 + 256 * rep, a.nu3, ep - 1u, a.ctl, a.spin_max);
+          if (wave == 0) ok = poll(a.fl3 + REP_WORDS * rep, a.nu3, ep - 1u, a.ctl, a.spin_max);
           if (!row_polled(ok)) {
             alive = false;
             break;
@@ -613,7 +611,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
             alive = false;
             break;
           }
-          if (wave == 0) publish(a.fl0, u2, ep);
+          if (wave == 0) publish(a.fl0, u2, a.nu2, ep);
         }
       } else {
         nx += 4;
@@ -848,7 +846,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
       }
       if (l == 0) {  // every unit's clearing done (the row waves' wait on fl0)
         bool ok = true;
-        if (wave == 0) ok = poll(a.fl0 + 256 * rep, a.nu2, ep, a.ctl, a.spin_max);
+        if (wave == 0) ok = poll(a.fl0 + REP_WORDS * rep, a.nu2, ep, a.ctl, a.spin_max);
         if (!row_polled(ok)) {
           alive = false;
           break;
@@ -871,7 +869,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
         alive = false;
         break;
       }
-      if (wave == 0) publish(a.fl2, u2, ep);
+      if (wave == 0) publish(a.fl2, u2, a.nu2, ep);
       sig_add(&sy.aiss);
       if (l + 1 < a.L) kv_issue(lyr[l + 1]);
     }
@@ -922,7 +920,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
           wdb[i] = ld16(dr, (in && tb >= 0) ? (uint32_t)(((int64_t)tb * dim + n) * 16) : LD_OOB);
         }
         bool ok = true;
-        if (wave == 0) ok = poll(a.fl2 + 256 * rep, a.nu2, ep, a.ctl, a.spin_max);
+        if (wave == 0) ok = poll(a.fl2 + REP_WORDS * rep, a.nu2, ep, a.ctl, a.spin_max);
         if (!row_polled(ok)) {
           alive = false;
           break;
@@ -984,7 +982,7 @@ __global__ __launch_bounds__(NTH) void dec_step_kernel(Args a) {
           alive = false;
           break;
         }
-        if (wave == 0) publish(a.fl3, u3, ep);
+        if (wave == 0) publish(a.fl3, u3, a.nu3, ep);
         sig_add(&sy.aiss);
       } else {
         nx += 4;
@@ -1212,7 +1210,7 @@ extern "C" llhip_dec_step* llhip_dec_step_create(const llhip_dec_step_desc* d) {
     for (int64_t b = 0; b < G && u3 < nu3; ++b)
       if (role[(size_t)b] < 0) role[(size_t)b] = (int32_t)(256 + u3++);
   }
-  // one allocation: layer table | ctl (256 B) | roles (1 KiB) | flags 3 x NREP KiB | k exchange |
+  // one allocation: layer table | ctl (256 B) | roles (1 KiB) | flags 3 x NREP x 4 KiB | k exchange |
   // acc_o | acc_d | xres
   const size_t tab_b = (sizeof(Layer) * (size_t)d->L + 255) & ~(size_t)255;
   const size_t acc_b = (size_t)2 * R * dim * 4;
