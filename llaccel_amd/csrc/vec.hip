@@ -252,9 +252,40 @@ __global__ __launch_bounds__(256) void argmax_kernel(const int16_t* __restrict__
   const int64_t row = blockIdx.x;
   const int16_t* lr = logits + row * ld;
   uint64_t key = 0;
-  for (int64_t i = threadIdx.x; i < vocab; i += 256) {
-    const uint64_t k = amax_key(lr[i], i);
-    key = k > key ? k : key;
+  if ((reinterpret_cast<uintptr_t>(lr) & 15) == 0 && vocab < (1ll << 31) / 2) {
+    // 16-byte chunks of 8 values, eight chunks per thread in flight per pass (a pass of one load
+    // at a time waits a memory round trip per value)
+    const int64_t chunks = vocab / 8;  // whole chunks; the vocab % 8 values after them one at a time
+    const Rsrc rr = rsrc(lr, chunks * 16);
+    for (int64_t c0 = threadIdx.x; c0 < chunks; c0 += 256 * 8) {
+      v4i w[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t c = c0 + 256 * u;
+        w[u] = ld16(rr, c < chunks ? (uint32_t)(16 * c) : LD_OOB);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t c = c0 + 256 * u;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t i = 8 * c + e;
+          const int16_t v = (int16_t)((uint32_t)w[u][e >> 1] >> (16 * (e & 1)));
+          const uint64_t k = c < chunks ? amax_key(v, i) : 0;
+          key = k > key ? k : key;
+        }
+      }
+    }
+    if (threadIdx.x < vocab - 8 * chunks) {
+      const int64_t i = 8 * chunks + threadIdx.x;
+      const uint64_t k = amax_key(lr[i], i);
+      key = k > key ? k : key;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < vocab; i += 256) {
+      const uint64_t k = amax_key(lr[i], i);
+      key = k > key ? k : key;
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {

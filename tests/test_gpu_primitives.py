@@ -156,6 +156,30 @@ def test_exact_blas_matmul():
         G.exact_blas_matmul(np.ones((1, 1)), np.ones((1, 1), np.int8))
 
 
+@pytest.mark.parametrize("vocab", [1, 7, 8, 9, 2047, 2048, 16385, 151936])
+def test_argmax_row_lengths_and_tails(vocab):
+    """llhip_argmax_i16 over rows of every tail length (16-byte chunks of 8 values, eight chunks
+    per thread in flight), maxima in the last partial chunk and ties across chunks and threads;
+    rows at a 16-byte-aligned and at an odd row stride (the one-value-at-a-time form)."""
+    from llaccel_amd import _lib
+    from tests.gpu_helpers import ptr, stream, torch, up
+
+    t = torch()
+    rows = RNG.integers(-32768, 32767, (4, vocab))
+    rows[1, -1] = 32767  # the last value
+    rows[2, :] = -5
+    rows[2, [vocab // 3, vocab - 1]] = 9  # a tie: the lower index wins
+    rows[3, :] = 32767  # all equal: index 0
+    for ld in (vocab + (-vocab) % 8, vocab + 1):
+        buf = np.zeros((4, ld), np.int64)
+        buf[:, :vocab] = rows
+        buf[:, vocab:] = 32767  # past vocab: never chosen
+        d = up(buf, np.int16)
+        idx = t.empty(4, dtype=t.int32, device="cuda")
+        _lib.call("llhip_argmax_i16", ptr(d), 4, ld, vocab, ptr(idx), stream())
+        assert idx.cpu().numpy().tolist() == [int(np.argmax(r)) for r in rows], ld
+
+
 def test_argmax_lowest_index_on_ties():
     row = np.zeros(151936, np.int64)
     row[[5, 100, 151935]] = 7
