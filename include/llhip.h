@@ -360,11 +360,25 @@ typedef struct llhip_dec_attn_desc {
   void* acc;            /* int32 [N], zero on entry: receives the H per-head partial sums */
   void* zero;           /* int32 [zero_n] cleared for the down projection (16-byte aligned) */
   int64_t zero_n;
+  void* state;          /* or NULL: zero-filled device memory owned by the caller, kept across launches,
+                         * of the size llhip_dec_attn_state_bytes gives; long contexts then run as ONE
+                         * launch whose H x S workgroups exchange their partials through it */
+  int64_t state_bytes;
 } llhip_dec_attn_desc;
 
 /* golden.py:353-366 + 316-342 -- causal GQA attention of one row, then each head's partial sums of
- * the output projection (K range h*D..h*D+D-1) added into acc.  ws as for llhip_attention. */
+ * the output projection (K range h*D..h*D+D-1) added into acc.  ws as for llhip_attention.  With
+ * `state`, a long context (>= 2048 keys, head_dim 64 or 128) is one launch of H x S workgroups (S
+ * <= 16 splits of the keys per head) that wait for each other with bounded waits; a timed-out wait
+ * sets the state's error word (read with llhip_dec_attn_status), and later launches with that state
+ * do nothing. */
 int llhip_dec_attention(const llhip_dec_attn_desc* d, void* ws, void* stream);
+/* golden.py:353-366 -- bytes of the state of llhip_dec_attention's one-launch form for H heads of
+ * head_dim D (at most 16 splits per head). */
+int64_t llhip_dec_attn_state_bytes(int64_t H, int64_t D);
+/* golden.py:353-366 -- synchronous: *launches = one-launch attentions completed with this state,
+ * *err = nonzero when one hit a bounded-wait timeout (sticky). */
+int llhip_dec_attn_status(const void* state, int64_t* launches, int64_t* err);
 
 /* golden.py:286-309 + 316-342 -- llhip_mlp_in for one row whose input is the resadd output of the
  * output projection (r), then the down projection's partial sums of each workgroup's 16 FFN columns

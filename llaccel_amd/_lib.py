@@ -192,12 +192,15 @@ class ResidDesc(ctypes.Structure):
 class DecAttnDesc(ctypes.Structure):
     _fields_ = [("q", _p), ("kc", _p), ("vc", _p), ("out", _p), ("pos_dev", _p), ("pos", _i64), ("H", _i64),
                 ("Hkv", _i64), ("D", _i64), ("max_seq", _i64), ("Ms", _i64), ("Ss", _i64), ("Mo", _i64), ("So", _i64),
-                ("prob_bits", _i64), ("wo_panel", _p), ("N", _i64), ("acc", _p), ("zero", _p), ("zero_n", _i64)]
+                ("prob_bits", _i64), ("wo_panel", _p), ("N", _i64), ("acc", _p), ("zero", _p), ("zero_n", _i64),
+                ("state", _p), ("state_bytes", _i64)]
 
 
 _SIGS.update({
     "llhip_dec_attn_in": [ctypes.POINTER(AttnInDesc), ctypes.POINTER(ResidDesc), _p, _i64, _p],
     "llhip_dec_attention": [ctypes.POINTER(DecAttnDesc), _p, _p],
+    "llhip_dec_attn_state_bytes": [_i64, _i64],
+    "llhip_dec_attn_status": [_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
     "llhip_dec_mlp": [ctypes.POINTER(MlpInDesc), ctypes.POINTER(ResidDesc), _p, _p, _i64, _i64, _p],
     "llhip_dec_finish": [ctypes.POINTER(NormQuantDesc), ctypes.POINTER(ResidDesc), _p],
     "llhip_dec_head": [ctypes.POINTER(NormLinearDesc), _i64, _p, _p, _p, _i64, _i64, _p],
@@ -205,6 +208,7 @@ _SIGS.update({
     "llhip_dec_greedy": [_p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],
 })
 _RESTYPES["llhip_dec_head_keys"] = _i64
+_RESTYPES["llhip_dec_attn_state_bytes"] = _i64
 
 
 # ---- decode step (include/llhip.h: llhip_dec_step_*) -------------------------------------

@@ -80,6 +80,10 @@ class Chain:
             self.wd_panel.append(pad.view(self.dim, Fp // 16, 16).permute(1, 0, 2).contiguous())
         self._resid = _lib.ResidDesc()
         self._att = _lib.DecAttnDesc()
+        # state of the one-launch long-context attention (zero-filled once, shared by the layers,
+        # which run one after another)
+        nb = max(int(_lib.lib().llhip_dec_attn_state_bytes(int(ly.att["H"]), int(ly.att["D"]))) for ly in layers)
+        self.att_state = torch.zeros(nb, dtype=torch.uint8, device=dev)
         self.use_step = True  # one-launch decode step where the graph allows it (llhip_dec_step)
         self._step = None
         self._step_key = None
@@ -165,7 +169,12 @@ class Chain:
         return h
 
     def check_step(self):
-        """Raise if a decode-step launch hit its bounded-wait timeout (synchronises the device)."""
+        """Raise if a decode-step launch or a one-launch attention hit its bounded-wait timeout
+        (synchronises the device)."""
+        n, err = ctypes.c_int64(), ctypes.c_int64()
+        _lib.call("llhip_dec_attn_status", _vp(self.att_state), ctypes.byref(n), ctypes.byref(err))
+        if err.value:
+            raise RuntimeError(f"decode attention: a hand-off wait timed out (error word {err.value})")
         if not self._step:
             return
         n, err = ctypes.c_int64(), ctypes.c_int64()
@@ -216,6 +225,7 @@ class Chain:
         d.prob_bits = int(a.get("prob_bits", 8))
         d.wo_panel, d.N, d.acc = _vp(self.wo_panel[i]), self.dim, _vp(self.acc_wo)
         d.zero, d.zero_n = _vp(self.acc_wd), WD_ROWS * self.dim
+        d.state, d.state_bytes = _vp(self.att_state), self.att_state.numel()
         _lib.call("llhip_dec_attention", ctypes.byref(d), _vp(m._ws), s)
 
     def _mlp(self, i, ly, pos, pd, s):

@@ -1042,6 +1042,278 @@ __global__ __launch_bounds__(256) void attention_split_finish_wo(AttnArgs p, int
   wo_partial<D, WPF>(p, h, ah, wpre, n_lo, n_hi);
 }
 
+// ---------------------------------------------------------------------------------------
+// attention_row_fused: one row's attention over a long context and the output projection's partial
+// sums in ONE launch (the decode chain, one query row).  Grid H x S: workgroup (h, z) takes keys
+// [z Tz, (z + 1) Tz) of head h.  The three global reductions of golden.py:167-177 (max, sum of the
+// LUT exponentials, probability-weighted value sums) are exchanged between the S workgroups of a
+// head through tagged 64-bit words in `st` (the launch's tag in the high half, the value in the
+// low half: a reader that sees the tag sees the value, one trip through memory), each wait
+// bounded.  Then every workgroup of the head sums the S partials of its D dimensions and
+// requantises them, and workgroup z adds the products with output-projection columns
+// [z N / S, (z + 1) N / S) into the accumulators: one add per column and head (with one per column
+// and workgroup, 256-way contention on each column's word cost microseconds).  Every partial is an
+// exact integer max or sum: the split changes no result.
+// The S workgroups of a head wait for each other, so the grid (H x S <= CUs) must be resident at
+// once; workgroup b = h + H z runs on XCD b % 8, so with H a multiple of 8 a head's workgroups
+// share one XCD.  `st`: [0] launches, [1] workgroups done, [2] error, [3] abort, then from word 64
+// the exchange words [H][S][2 + D] (uint64: max, sum, D value partials).
+// ---------------------------------------------------------------------------------------
+constexpr int ARF_THREADS = 256;
+constexpr uint32_t ARF_SPIN = 1u << 20;
+
+// the tagged word of `tag` at p (one 8-byte load a pass), or false on timeout / abort
+__device__ __forceinline__ bool arf_take(Rsrc r, uint32_t off, uint32_t tag, uint32_t* st, int32_t& v) {
+  const Rsrc cr = rsrc(st, 16);
+  for (uint32_t it = 0;; ++it) {
+    __asm__ volatile("" ::: "memory");  // a fresh load on every pass
+    const v2i w = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16));
+    if ((uint32_t)w.y == tag) {
+      v = w.x;
+      return true;
+    }
+    if (it >= ARF_SPIN) {
+      __hip_atomic_fetch_or(st + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(st + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    if ((it & 31) == 31 && __builtin_amdgcn_raw_buffer_load_b32(cr, 12, 0, 16) != 0) return false;
+  }
+}
+// the tagged words at offsets off[0..8) (LD_OOB: none), all eight loads in flight per pass, until
+// every one carries `tag`; false on timeout / abort
+__device__ __forceinline__ bool arf_take8(Rsrc r, const uint32_t* off, uint32_t tag, uint32_t* st, int32_t* v) {
+  const Rsrc cr = rsrc(st, 16);
+  for (uint32_t it = 0;; ++it) {
+    __asm__ volatile("" ::: "memory");  // fresh loads on every pass
+    v2i w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(r, off[k], 0, 16));
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      ok = ok && (off[k] == LD_OOB || (uint32_t)w[k].y == tag);
+      v[k] = w[k].x;
+    }
+    if (ok) return true;
+    if (it >= ARF_SPIN) {
+      __hip_atomic_fetch_or(st + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(st + 3, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    if ((it & 31) == 31 && __builtin_amdgcn_raw_buffer_load_b32(cr, 12, 0, 16) != 0) return false;
+  }
+}
+__device__ __forceinline__ void arf_put(Rsrc r, uint32_t off, uint32_t tag, int32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i, v2i{v, (int32_t)tag}), r, off, 0, 16);
+}
+
+template <int D, int NK>
+__global__ __launch_bounds__(ARF_THREADS) void attention_row_fused(AttnArgs p, int S, uint32_t* st) {
+  constexpr int CH = D / 16;              // threads per key (16-byte chunks)
+  constexpr int KP = ARF_THREADS / CH;    // keys per pass
+  __shared__ uint32_t lut32[LUT_DW];
+  __shared__ int32_t red[4];
+  __shared__ int32_t bc;
+  __shared__ int32_t part[KP][D + 1];
+  __shared__ __attribute__((aligned(16))) int8_t ah[D];
+  __shared__ int ok_s;
+  const int h = (int)blockIdx.x, z = (int)blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kc = tid % CH, k0 = tid / CH;
+  const int G = p.H / p.Hkv, g = h / G;
+  const int DS = D / S;
+  const Rsrc sr = rsrc(st, 16);
+  const uint32_t tag = __builtin_amdgcn_raw_buffer_load_b32(sr, 0, 0, 16) + 1u;  // this launch's tag
+  if (__builtin_amdgcn_raw_buffer_load_b32(sr, 12, 0, 16) != 0) return;  // an earlier launch gave up (sticky)
+  const Rsrc xr = rsrc(st + 64, (int64_t)p.H * S * (2 + D) * 8);
+  auto word = [&](int zz, int i) { return (uint32_t)(((h * S + zz) * (2 + D) + i) * 8); };
+  const int pos = load_pos(p.pos_dev, p.pos);
+  const int T = min(pos + 1, (int)p.max_seq);
+  const int Tz = (T + S - 1) / S, t0 = z * Tz, t1 = min(T, t0 + Tz);
+  const int8_t* kbase = p.kc + (int64_t)g * p.max_seq * D;
+  const int8_t* vbase = p.vc + (int64_t)g * p.max_seq * D;
+  const Rsrc kr = rsrc(kbase, (int64_t)T * D), vr = rsrc(vbase, (int64_t)T * D);
+
+  // loads in order of use: q chunk, this thread's key chunks, the LUT, its value chunks
+  const v4i qv = ld16(rsrc(p.q + (int64_t)h * D, D), 16u * kc);
+  v4i kreg[NK], vreg[NK];
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    const int t = t0 + k0 + KP * i;
+    kreg[i] = ld16(kr, t < t1 ? (uint32_t)(t * D + 16 * kc) : LD_OOB);
+  }
+  if (wave == 0) {
+    const Rsrc ir = rsrc(kExpI, sizeof(kExpI)), fr = rsrc(kExpF, sizeof(kExpF));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int idx = lane + 64 * i;
+      const uint32_t lw = (uint32_t)ld4(ir, idx < 8 ? 4 * idx : LD_OOB) |
+                          (uint32_t)ld4(fr, idx >= 8 && idx < LUT_DW ? 4 * (idx - 8) : LD_OOB);
+      if (idx < LUT_DW) lut32[idx] = lw;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    const int t = t0 + k0 + KP * i;
+    vreg[i] = ld16(vr, t < t1 ? (uint32_t)(t * D + 16 * kc) : LD_OOB);
+  }
+  // this workgroup's output-projection columns [z NS, z NS + NS), the first 2 KP of them requested
+  // now (they do not depend on the attention)
+  const int NS = (p.wo_N + S - 1) / S, n_lo = z * NS, n_hi = min(p.wo_N, n_lo + NS);
+  const Rsrc wr = rsrc(p.wop + (int64_t)h * p.wo_N * D, (int64_t)p.wo_N * D);
+  v4i wpre[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int n = n_lo + u * KP + k0;
+    wpre[u] = ld16(wr, n < n_hi ? (uint32_t)(n * D + 16 * kc) : LD_OOB);
+  }
+  if (h == 0 && z == 0) zero_words(p.zero, p.zero_n);
+
+  // scores and this split's maximum
+  int32_t sreg[NK];
+  int32_t lmax = INT32_MIN;
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    sreg[i] = chunk_sum<CH>(dot16(qv, kreg[i]));
+    if (t0 + k0 + KP * i < t1) lmax = max(lmax, sreg[i]);
+  }
+  lmax = wave_max_i32(lmax);
+  if (lane == 0) red[wave] = lmax;
+  __syncthreads();
+  if (tid == 0) arf_put(xr, word(z, 0), tag, max(max(red[0], red[1]), max(red[2], red[3])));
+  // the head's maximum over its S splits
+  if (wave == 0) {
+    int32_t v = INT32_MIN;
+    bool ok = true;
+    if (lane < S) ok = arf_take(xr, word(lane, 0), tag, st, v);
+    v = wave_max_i32(v);
+    const bool all = __builtin_amdgcn_ballot_w64(!ok) == 0;
+    if (lane == 0) {
+      bc = v;
+      ok_s = all;
+    }
+  }
+  __syncthreads();
+  if (!ok_s) return;
+  const int32_t mx = bc;
+  const uint16_t* ei = reinterpret_cast<const uint16_t*>(lut32);
+  const uint16_t* ef = ei + 16;
+  uint32_t pr[NK];
+  uint32_t lsum = 0;
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    pr[i] = t0 + k0 + KP * i < t1 ? lut_prob_lds(mulshift((int64_t)mx - sreg[i], p.Ms, p.Ss), ei, ef) : 0u;
+    if (kc == 0) lsum += pr[i];
+  }
+  lsum = (uint32_t)wave_sum_i32((int)lsum);  // T * 65535 < 2^31
+  __syncthreads();  // every lane read bc and red before they are reused
+  if (lane == 0) red[wave] = (int32_t)lsum;
+  __syncthreads();
+  if (tid == 0) arf_put(xr, word(z, 1), tag, red[0] + red[1] + red[2] + red[3]);
+  if (wave == 0) {
+    int32_t v = 0;
+    bool ok = true;
+    if (lane < S) ok = arf_take(xr, word(lane, 1), tag, st, v);
+    v = wave_sum_i32(v);
+    const bool all = __builtin_amdgcn_ballot_w64(!ok) == 0;
+    if (lane == 0) {
+      bc = v;
+      ok_s = all;
+    }
+  }
+  __syncthreads();
+  if (!ok_s) return;
+  const uint32_t total = (uint32_t)bc;
+  const uint32_t inv = 0x80000000u / (total > 1u ? total : 1u);  // 2^31 / total (golden.py:174)
+  const int32_t cap = (1 << p.pb) - 1;
+  const int shp = 31 - p.pb;
+  // this split's value sums: 16 dimensions (chunk kc) of this thread's keys, then over the key groups
+  int32_t o[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) o[j] = 0;
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    const int64_t q = rshr((int64_t)pr[i] * (int64_t)inv, shp);
+    const int32_t pn = (int32_t)(q < cap ? q : cap);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[j] += pn * (int32_t)(int8_t)((uint32_t)vreg[i][j >> 2] >> (8 * (j & 3)));
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) part[k0][16 * kc + j] = o[j];
+  __syncthreads();
+  if (tid < D) {
+    int32_t sum = 0;
+    for (int r = 0; r < KP; ++r) sum += part[r][tid];
+    arf_put(xr, word(z, 2 + tid), tag, sum);
+  }
+  // the head's D outputs: every workgroup sums the S partials of every dimension (S D tagged words,
+  // eight loads in flight per thread) and requantises them (golden.py:175-180)
+  __syncthreads();  // part is reused below
+  {
+    uint32_t off[8];
+    int32_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int f = tid + ARF_THREADS * k;  // word (f / D, f % D)
+      off[k] = f < S * D ? word(f / D, 2 + f % D) : LD_OOB;
+    }
+    const bool ok = arf_take8(xr, off, tag, st, v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int f = tid + ARF_THREADS * k;
+      if (f < S * D) part[f / D][f % D] = v[k];
+    }
+    if (!ok) ok_s = 0;
+  }
+  __syncthreads();
+  if (!ok_s) return;
+  if (tid < D) {
+    int32_t ov = 0;
+    for (int zz = 0; zz < S; ++zz) ov += part[zz][tid];
+    if (p.pb == 15) ov = rshr32(ov, 7);
+    const int8_t y = (int8_t)sat8(mulshift(ov, p.Mo, p.So));
+    ah[tid] = y;
+    if (tid / DS == z) p.out[(int64_t)h * D + tid] = y;  // each workgroup stores its DS of them
+  }
+  __syncthreads();
+  // the output projection's partial sums of head h for columns [z NS, z NS + NS): CH lanes per column
+  // (16-byte chunks of the panel row [h][n][:]), their products summed within the lanes' group, one
+  // device-scope add per column (each column gets one add per head, not one per workgroup)
+  {
+    const v4i a = *reinterpret_cast<const v4i*>(ah + 16 * kc);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int n = n_lo + u * KP + k0;
+      const int32_t sacc = chunk_sum<CH>(dot16(a, wpre[u]));
+      if (kc == 0 && n < n_hi && sacc != 0) atomic_add_dev(p.wo_acc + n, sacc);
+    }
+    for (int n0 = n_lo + 2 * KP; n0 < n_hi; n0 += 4 * KP) {
+      v4i w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int n = n0 + u * KP + k0;
+        w[u] = ld16(wr, n < n_hi ? (uint32_t)(n * D + 16 * kc) : LD_OOB);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int n = n0 + u * KP + k0;
+        const int32_t sacc = chunk_sum<CH>(dot16(a, w[u]));
+        if (kc == 0 && n < n_hi && sacc != 0) atomic_add_dev(p.wo_acc + n, sacc);
+      }
+    }
+  }
+  // launch count: the last workgroup to finish advances the tag of the next launch
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(st + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == (uint32_t)(gridDim.x * gridDim.y) - 1u) {
+      __hip_atomic_store(st + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(st + 0, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 __global__ void kv_write_kernel(const int8_t* __restrict__ k, const int8_t* __restrict__ v, int64_t M, int Hkv, int D,
                                 int64_t ldk, int64_t ldv, int pos, const int32_t* __restrict__ pos_dev,
                                 const int32_t* __restrict__ row_pos, int64_t slot_stride, int8_t* __restrict__ kc,
@@ -1095,6 +1367,8 @@ struct WoFold {
   int32_t* acc;
   int32_t* zero;
   int64_t N, zero_n;
+  uint32_t* st;       // attention_row_fused's state (zero-filled once), or null
+  int64_t st_bytes;
 };
 
 static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
@@ -1171,6 +1445,31 @@ static int attention_impl(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, in
   // bytes of the partials of S splits: per-split row maxima and sums, and value partials (+ one
   // row's scores for a single-row launch)
   const bool one = M == 1;
+  // one row folded into the output projection over a long context: the fused single launch when
+  // the caller gave it state and the grid fits the CUs (its workgroups wait for each other)
+  if (fold && fold->st && one && !row_pos && (D == 64 || D == 128) && tmax <= AT_MAX_T && ktiles >= AT_SPLIT_MIN_TILES) {
+    int S = 16;
+    while (S > D / 16 && H * S > cus) S /= 2;
+    const int64_t Tz = ceil_div(tmax, S), KP = ARF_THREADS / (D / 16);
+    const int64_t nk = ceil_div(Tz, KP);
+    const int64_t st_need = 256 + H * S * (2 + D) * 8;
+    if (H * S <= cus && nk <= 16 && fold->st_bytes >= st_need && (uintptr_t)fold->st % 16 == 0) {
+      dim3 grid((unsigned)H, (unsigned)S), block(ARF_THREADS);
+      uint32_t* st = fold->st;
+#define LLHIP_ARF(DD)                                                                                   \
+  if (nk <= 4) hipLaunchKernelGGL((attention_row_fused<DD, 4>), grid, block, 0, s, p, S, st);          \
+  else if (nk <= 8) hipLaunchKernelGGL((attention_row_fused<DD, 8>), grid, block, 0, s, p, S, st);     \
+  else hipLaunchKernelGGL((attention_row_fused<DD, 16>), grid, block, 0, s, p, S, st);
+      if (D == 64) {
+        LLHIP_ARF(64)
+      } else {
+        LLHIP_ARF(128)
+      }
+#undef LLHIP_ARF
+      LLHIP_LAUNCH_CHECK();
+      return 0;
+    }
+  }
   auto split_need = [&](int64_t S) { return pairs * S * AT_ROWS * (2 + D) * 4 + (one ? pairs * ktiles * 64 * 4 : 0); };
   if (!row_pos && seq_rows == 0 && split_ws && tmax <= AT_MAX_T && ktiles >= AT_SPLIT_MIN_TILES && pairs * 4 <= cus &&
       split_need(2) <= split_bytes) {
@@ -1318,12 +1617,27 @@ int llhip_attention_seqs(const int8_t* q, int64_t M, int64_t seq_rows, int64_t H
 int llhip_dec_attention(const llhip_dec_attn_desc* d, void* ws, void* stream) {
   if (!d) return fail(-EINVAL, "dec_attention: null descriptor");
   WoFold f{static_cast<const int8_t*>(d->wo_panel), static_cast<int32_t*>(d->acc), static_cast<int32_t*>(d->zero),
-           d->N, d->zero_n};
+           d->N, d->zero_n, static_cast<uint32_t*>(d->state), d->state_bytes};
   return attention_impl(static_cast<const int8_t*>(d->q), 1, d->H, d->Hkv, d->D, d->H * d->D, d->pos,
                         static_cast<const int32_t*>(d->pos_dev), nullptr, 0, static_cast<const int8_t*>(d->kc),
                         static_cast<const int8_t*>(d->vc), d->max_seq, d->Ms, d->Ss, d->Mo, d->So, d->prob_bits,
                         static_cast<int8_t*>(d->out), d->H * d->D, ws ? static_cast<char*>(ws) + WS_SCRATCH : nullptr,
                         WS_SCRATCH_BYTES, stream, &f);
+}
+
+int64_t llhip_dec_attn_state_bytes(int64_t H, int64_t D) {
+  if (H < 1 || D < 1 || H > 4096 || D > 256) return fail(-EINVAL, "dec_attn_state_bytes: bad shape");
+  return 256 + H * 16 * (2 + D) * 8;
+}
+
+int llhip_dec_attn_status(const void* state, int64_t* launches, int64_t* err) {
+  if (!state) return fail(-EINVAL, "dec_attn_status: null state");
+  uint32_t h[4];
+  LLHIP_CHECK_HIP(hipDeviceSynchronize());
+  LLHIP_CHECK_HIP(hipMemcpy(h, state, sizeof(h), hipMemcpyDeviceToHost));
+  if (launches) *launches = h[0];
+  if (err) *err = h[2];
+  return 0;
 }
 
 int llhip_attention_noalloc(const int8_t* q, int64_t M, int64_t H, int64_t Hkv, int64_t D, int64_t ldq, int64_t pos,
