@@ -405,6 +405,27 @@ int64_t llhip_dec_head_keys(int64_t N);
 int llhip_dec_greedy(const void* keys, int64_t nkeys, int32_t* token, int32_t* pos, int32_t* step,
                      int32_t* ring_tokens, int64_t ring_cap, const int16_t* embed, int64_t dim, int16_t* row,
                      void* stream);
+/* golden.py:316-342 + 286-296 + 376-377 + 411-414 + 369-373 -- llhip_dec_finish, llhip_dec_head and
+ * llhip_dec_greedy of one row as ONE launch of one workgroup per CU: each workgroup finishes the
+ * projection r, normalises and quantises the row (workgroup 0 writes the finished row, h_out and
+ * hq_out), computes its share of d's 16-column tiles (logits to d->out when non-NULL, the record
+ * row at ring[*step] when *step < ring_cap) and its best (value, lowest index) key; the last
+ * workgroup to finish takes the greedy step (token, ring_tokens, pos, step, row = embed[token]).
+ * d->pre.prequant = 0, d->M = 1, plain epilogue, K a multiple of 64 up to 1024.  keys: the
+ * launch's llhip_dec_logits_keys() uint64 words, zero-filled before the first launch -- the
+ * arrival counter returns to zero at the end of each launch.  Launches sharing keys run in order.
+ * panel: NULL, or d->W in tile order, which streams in whole 1 KiB pieces: for 16-column tile t, K
+ * step s and lane l = 16 kg + c, bytes [16 l, 16 l + 16) of piece t K/64 + s hold
+ * W[16 t + c][64 s + 16 kg, +16) -- ceil(N/16) tiles, columns past N zero. */
+int llhip_dec_logits(const llhip_norm_linear_desc* d, const void* panel, const llhip_resid_desc* r, int64_t vocab,
+                     void* keys, int32_t* token, int32_t* pos, int32_t* step, int16_t* ring, int64_t ring_ld,
+                     int32_t* ring_tokens, int64_t ring_cap, const int16_t* embed, int64_t dim, int16_t* row,
+                     void* stream);
+/* golden.py:316-342 -- W [N][K] i8 (K a multiple of 64) rewritten in llhip_dec_logits' tile order
+ * into panel (ceil(N/16) 16 K bytes) */
+int llhip_dec_logits_panel(const void* W, int64_t N, int64_t K, void* panel, void* stream);
+/* golden.py:376-377 -- the uint64 words of llhip_dec_logits' keys */
+int64_t llhip_dec_logits_keys(void);
 
 /* ---- decode step: every layer of one decode row in one launch ----
  * golden.py:392-397 (decode) running golden.py:275-314 over the layers of a fused graph whose every

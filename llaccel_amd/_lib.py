@@ -206,8 +206,12 @@ _SIGS.update({
     "llhip_dec_head": [ctypes.POINTER(NormLinearDesc), _i64, _p, _p, _p, _i64, _i64, _p],
     "llhip_dec_head_keys": [_i64],
     "llhip_dec_greedy": [_p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _p, _p],
+    "llhip_dec_logits": [ctypes.POINTER(NormLinearDesc), _p, ctypes.POINTER(ResidDesc), _i64, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _p, _p],
+    "llhip_dec_logits_keys": [],
+    "llhip_dec_logits_panel": [_p, _i64, _i64, _p, _p],
 })
 _RESTYPES["llhip_dec_head_keys"] = _i64
+_RESTYPES["llhip_dec_logits_keys"] = _i64
 _RESTYPES["llhip_dec_attn_state_bytes"] = _i64
 
 

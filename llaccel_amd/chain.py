@@ -67,6 +67,11 @@ class Chain:
         self.acc_wd = torch.zeros((WD_ROWS, self.dim), dtype=torch.int32, device=dev)
         vp = int(head.desc_N)
         self.keys = torch.zeros(int(_lib.lib().llhip_dec_head_keys(vp)), dtype=torch.int64, device=dev)
+        # the one-launch head's keys and arrival counter (zero-filled once; each launch leaves the
+        # counter at zero)
+        self.logit_keys = torch.zeros(int(_lib.lib().llhip_dec_logits_keys()), dtype=torch.int64, device=dev)
+        self.use_logits = True  # the greedy head as one launch (llhip_dec_logits) where it applies
+        self._panel = None  # the lm_head in llhip_dec_logits' tile order, made on first use
         self.wo_panel, self.wd_panel = [], []
         for ly in layers:
             H, D = int(ly.att["H"]), int(ly.att["D"])
@@ -257,13 +262,20 @@ class Chain:
         fh = self.head
         fh.fill(fh.desc, 1, pos, pd)
         s = m._stream_handle()
-        # the last down projection finished, normalised and quantised once; the lm_head workgroups
-        # read the quantised row
         fh.desc.pre.prequant = 0
         if st is not None:
             resid = self._fill_resid(self.layers[-1].wd, self._step_acc, WD_ROWS, aux=self._step_res)
         else:
             resid = self._fill_resid(self.layers[-1].wd, self.acc_wd, WD_ROWS)
+        if greedy is not None and self.use_logits and self._logits_fit(fh.desc):
+            # finish, norm, quant, lm_head and the greedy step in one launch
+            tok, posp, step, ring_rows, ring_ld, ring_tok, ring_cap = greedy
+            _lib.call("llhip_dec_logits", ctypes.byref(fh.desc), _vp(self._head_panel(fh.desc)), resid, m.vocab,
+                      _vp(self.logit_keys), tok, posp, step, ring_rows, ring_ld, ring_tok, ring_cap,
+                      _vp(m._dt["embed"]), self.dim, _vp(m._act[m.q.input_name]), s)
+            return
+        # the last down projection finished, normalised and quantised once; the lm_head workgroups
+        # read the quantised row
         _lib.call("llhip_dec_finish", ctypes.byref(fh.desc.pre), resid, s)
         fh.desc.pre.prequant = 1
         if greedy is None:
@@ -275,6 +287,31 @@ class Chain:
         _lib.call("llhip_dec_greedy", _vp(self.keys), self.keys.numel(), tok, posp, step, ring_tok, ring_cap,
                   _vp(m._dt["embed"]), self.dim, _vp(m._act[m.q.input_name]), s)
 
+    def prepare_head(self):
+        """What the greedy head needs made before a capture: the tile-order lm_head."""
+        fh = self.head
+        fh.fill(fh.desc, 1, 0, None)
+        if self.use_logits and self._logits_fit(fh.desc):
+            self._head_panel(fh.desc)
+
+    def _head_panel(self, d):
+        """The lm_head weights in llhip_dec_logits' tile order (built once, on the model's stream)."""
+        if self._panel is None:
+            torch = _torch()
+            N, K = int(d.N), int(d.pre.K)
+            panel = torch.empty(-(-N // 16) * 16 * K, dtype=torch.int8, device=self.model.device)
+            _lib.call("llhip_dec_logits_panel", d.W, N, K, _vp(panel), self.model._stream_handle())
+            self._panel = panel
+        return self._panel
+
+    @staticmethod
+    def _logits_fit(d):
+        """llhip_dec_logits' shape: one row, plain epilogue, K a multiple of 64 up to 1024, 16-byte
+        aligned weights."""
+        K = int(d.pre.K)
+        return (d.M == 1 and d.epilogue == 0 and not d.out_i8 and K % 64 == 0 and K <= 1024
+                and int(d.W or 0) % 16 == 0 and d.N >= 16)
+
     # ---- measurement ------------------------------------------------------------------------
     FAMILIES = ("dec_attn_in", "dec_attention", "dec_mlp", "dec_head")  # the three-launch chain
     STEP_FAMILIES = ("dec_step", "dec_head")  # the one-launch step: every layer, then the head
@@ -285,24 +322,36 @@ class Chain:
         return self.STEP_FAMILIES if self.step(pd) is not None else self.FAMILIES
 
     def launches(self, family: str) -> int:
-        if family == "dec_head":
-            return 2  # the finish and the lm_head
+        if family == "dec_head":  # with the greedy step: one launch, or the finish, lm_head and greedy
+            return 1 if self._one_launch_head() else 3
         return 1 if family == "dec_step" else len(self.layers)
+
+    def _one_launch_head(self) -> bool:
+        fh = self.head
+        fh.fill(fh.desc, 1, 0, None)
+        return self.use_logits and self._logits_fit(fh.desc)
 
     def capture_family(self, family: str | None, pos: int):
         """A HIP graph of one decode step's launches of `family` at the device position `pos` (for
-        timing them in isolation: the values are then meaningless), or with family None the whole
-        step's layers and head (without the greedy step), which can be replayed at one position."""
+        timing them in isolation: the values are then meaningless; dec_head with the decode loop's
+        greedy step), or with family None the whole step's layers and head (without the greedy
+        step), which can be replayed at one position."""
         m = self.model
         torch = _torch()
         m._decode_state(1)
         m._st.copy_(torch.tensor([0, pos, 0], dtype=torch.int32))
-        pd = ctypes.c_void_p(m._st.data_ptr() + 4)
+        base = m._st.data_ptr()
+        pd = ctypes.c_void_p(base + 4)
+        greedy = None
+        if family == "dec_head":
+            greedy = (ctypes.c_void_p(base), pd, ctypes.c_void_p(base + 8), _vp(m._ring_rows), m.vocab,
+                      _vp(m._ring_tok), m._ring_cap)
+        self.prepare_head()
         from .golden import capture_graph
 
         g = torch.cuda.CUDAGraph()
         with capture_graph(g):
-            self.run(0, pd, only=family)
+            self.run(0, pd, greedy=greedy, only=family)
         return g
 
     def step_bytes(self, T: int):

@@ -1463,6 +1463,216 @@ extern "C" int llhip_dec_head(const llhip_norm_linear_desc* d, int64_t vocab, vo
   return norm_linear_launch(p, stream);
 }
 
+// ---------------------------------------------------------------------------------------
+// dec_logits: the decode head in ONE persistent launch -- every workgroup finishes the last down
+// projection from its partial sums and normalises + quantises the row into LDS (workgroup 0 also
+// stores the row's outputs), then streams its share of the lm_head's 16-column tiles (8 waves, each
+// tile's weights loaded straight into registers one tile ahead) with the requant epilogue, the
+// record row and the running (value, lowest index) key; each workgroup writes its best key through
+// to memory and counts itself, and the last one takes the greedy step (token, record, position,
+// step, next input row).  One workgroup per CU, so each waits for its stores once per launch.
+// ---------------------------------------------------------------------------------------
+constexpr int DL_THREADS = 512;
+constexpr int DL_MAXG = 256;            // workgroups at most (one per CU)
+constexpr int DL_KEYS = DL_MAXG + 1;    // key words of a launch: the keys, then the arrival counter
+
+struct DecLogitsArgs {
+  NormQuant pre;
+  ResidArgs res;
+  const int8_t* W;     // [N][K], or in tile order (PANEL): [ceil(N/16)][K/64][64 lanes][16]
+  const int32_t* rq;   // [N][2]
+  const int32_t* bias; // [N] or null
+  int16_t* out;        // [N] logits, or null
+  uint64_t* keys;      // [DL_KEYS]: one key per workgroup, then the arrival counter at DL_MAXG
+  const int32_t* step;
+  int16_t* ring;
+  int64_t ring_ld;
+  int32_t* token;
+  int32_t* pos;
+  int32_t* ring_tok;
+  const int16_t* embed;
+  int16_t* row;
+  int N, K, vocab, ring_cap, dim;
+};
+
+template <int KS, bool PANEL>
+__global__ __launch_bounds__(DL_THREADS) void dec_logits_kernel(DecLogitsArgs p) {
+  kernarg_warm<sizeof(DecLogitsArgs)>();
+  extern __shared__ __attribute__((aligned(16))) int8_t xq[];  // the quantised row, zeros to 64 KS bytes
+  __shared__ uint64_t red64[8];
+  __shared__ uint64_t best[8];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, kg = lane >> 4;
+  const int b = (int)blockIdx.x;
+  const int tiles = (p.N + 15) / 16;
+  const int tb0 = (int)((int64_t)b * tiles / gridDim.x), tb1 = (int)((int64_t)(b + 1) * tiles / gridDim.x);
+  const Rsrc wr = rsrc(p.W, (int64_t)(PANEL ? 16 * tiles : p.N) * p.K), qr = rsrc(p.rq, (int64_t)p.N * 8),
+             br = rsrc(p.bias, (int64_t)p.N * 4);
+  const int nst = p.K / 64;
+  // tile t's weights (lane (col, kg): bytes [64 s + 16 kg, +16) of column col for each K step s),
+  // requant pair and bias; tiles past the workgroup's range read zeros
+  auto load_tile = [&](int t, v4i* w, v2i& rq, int32_t& bias) {
+    const int n = 16 * t + col;
+    const bool in = t < tb1;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      // in tile order each load is 1 KiB in one piece; row-major, 16 pieces of 64 bytes
+      const uint32_t off = PANEL ? (uint32_t)(((t * nst + s) * 64 + lane) * 16) : (uint32_t)(n * p.K + s * 64 + kg * 16);
+      w[s] = ld16(wr, in && s < nst ? off : LD_OOB);
+    }
+    rq = ld8(qr, in && kg == 0 ? 8u * n : LD_OOB);
+    bias = ld4(br, in && kg == 0 ? 4u * n : LD_OOB);
+  };
+  // three tiles' weights per wave in registers: two in flight while the third is multiplied
+  v4i w0[KS], w1[KS], w2[KS];
+  v2i q0{0, 0}, q1{0, 0}, q2{0, 0};
+  int32_t b0 = 0, b1 = 0, b2 = 0;
+  int t = tb0 + wave;
+  load_tile(t, w0, q0, b0);  // requested before the row's finish (they do not depend on it)
+  load_tile(t + 8, w1, q1, b1);
+  // the finished, normalised, quantised row (golden.py:316-342, 124-137, 119-120)
+  ResidRegs rr;
+  resid_prefetch(p.pre, p.res, rr);
+  for (int i = p.K + 4 * tid; i < 64 * KS; i += 4 * DL_THREADS) *reinterpret_cast<int32_t*>(xq + i) = 0;
+  resid_norm_quant(p.pre, p.res, rr, xq, b == 0, red64);  // ends with a barrier
+  const int32_t stepv = ld4(rsrc(p.step, 4), 0);
+  uint64_t key = 0;
+  auto tile = [&](int tt, const v4i* w, v2i rq, int32_t bias) {
+    v4i acc = {0, 0, 0, 0};
+    // the row is read from LDS for each tile (an offset the compiler cannot see through keeps the
+    // reads in the loop): registers held for it would leave too few for three tiles of weights
+    uint32_t xo = 16u * kg;
+    __asm__ volatile("" : "+v"(xo));
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {  // steps past K: zero weights times the zeroed tail of xq
+      const v4i xa = *reinterpret_cast<const v4i*>(xq + s * 64 + xo);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, w[s], acc, 0, 0, 0);
+    }
+    if (lane < 16) {  // one input row: every output row equals row 0
+      const int n = 16 * tt + lane;
+      if (n < p.N) {
+        const int16_t y = (int16_t)sat16(mulshift((int64_t)acc.x + bias, rq.x, rq.y));
+        if (p.out) p.out[n] = y;
+        if (n < p.vocab) {
+          const uint64_t k = amax_key((int)y, n);
+          key = k > key ? k : key;
+          if (stepv < p.ring_cap) p.ring[(int64_t)stepv * p.ring_ld + n] = y;
+        }
+      }
+    }
+  };
+  for (; t < tb1; t += 24) {
+    load_tile(t + 16, w2, q2, b2);
+    tile(t, w0, q0, b0);
+    if (t + 8 >= tb1) break;
+    load_tile(t + 24, w0, q0, b0);
+    tile(t + 8, w1, q1, b1);
+    if (t + 16 >= tb1) break;
+    load_tile(t + 32, w1, q1, b1);
+    tile(t + 16, w2, q2, b2);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)key, off), hi = __shfl_xor((uint32_t)(key >> 32), off);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    key = o > key ? o : key;
+  }
+  if (lane == 0) best[wave] = key;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t k = best[0];
+    for (int w = 1; w < 8; ++w) k = best[w] > k ? best[w] : k;
+    // through to memory: the last workgroup reads it
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2i, k), rsrc(p.keys, DL_KEYS * 8), 8u * b, 0, 16);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the key landed
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(p.keys + DL_MAXG);
+    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1u;
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
+  }
+  __syncthreads();
+  if (!last) return;
+  // the greedy step (golden.py:376-377, record golden.py:411-414, next row golden.py:369-373)
+  if (wave == 0) {
+    const Rsrc kr = rsrc(p.keys, DL_KEYS * 8);
+    uint64_t k = 0;
+    for (int i = lane; i < (int)gridDim.x; i += 64) {
+      const uint64_t v = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(kr, 8u * i, 0, 16));
+      k = v > k ? v : k;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint32_t lo = __shfl_xor((uint32_t)k, off), hi = __shfl_xor((uint32_t)(k >> 32), off);
+      const uint64_t o = ((uint64_t)hi << 32) | lo;
+      k = o > k ? o : k;
+    }
+    if (lane == 0) {
+      // every column below vocab made a nonzero key; a zero maximum cannot occur
+      const int32_t idx = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : 0;
+      last = idx;
+      *p.token = idx;
+      if (stepv < p.ring_cap) p.ring_tok[stepv] = idx;
+      *p.pos = *p.pos + 1;
+      *const_cast<int32_t*>(p.step) = stepv + 1;
+    }
+  }
+  __syncthreads();
+  const int16_t* src = p.embed + (int64_t)last * p.dim;
+  for (int i = tid; i < p.dim; i += blockDim.x) p.row[i] = src[i];
+}
+
+extern "C" int llhip_dec_logits(const llhip_norm_linear_desc* d, const void* panel, const llhip_resid_desc* r,
+                                int64_t vocab, void* keys,
+                                int32_t* token, int32_t* pos, int32_t* step, int16_t* ring, int64_t ring_ld,
+                                int32_t* ring_tokens, int64_t ring_cap, const int16_t* embed, int64_t dim, int16_t* row,
+                                void* stream) {
+  if (!d) return fail(-EINVAL, "dec_logits: null descriptor");
+  DecLogitsArgs p{};
+  int rc = fill_pre(p.pre, d->pre);
+  if (rc) return rc;
+  if (d->pre.prequant || d->M != 1 || d->epilogue != 0 || d->out_i8) return fail(-EINVAL, "dec_logits: one row, plain epilogue");
+  rc = fill_resid(p.res, r, p.pre);
+  if (rc) return rc;
+  const int64_t N = d->N, K = d->pre.K;
+  if (N < 16 || K % 64 || K > NORM_MAX_K || !w_ok(ceil_div(N, 16) * 16, K) || (uintptr_t)d->W % 16 ||
+      (uintptr_t)panel % 16)
+    return fail(-EINVAL, "dec_logits: lm_head geometry (K a multiple of 64, at most %d; W 16-byte aligned)", NORM_MAX_K);
+  const int G = std::min(current_cu_count(), DL_MAXG);
+  if (!keys || (uintptr_t)keys % 8 || vocab < 1 || vocab > N || !step || !token || !pos || ring_cap < 0 ||
+      (ring_cap && (!ring || ring_ld < vocab || !ring_tokens)) || !embed || dim < 1 || dim > INT32_MAX || !row)
+    return fail(-EINVAL, "dec_logits: bad greedy-step operands");
+  p.W = static_cast<const int8_t*>(panel ? panel : d->W);
+  p.rq = static_cast<const int32_t*>(d->rq);
+  p.bias = static_cast<const int32_t*>(d->bias);
+  p.out = static_cast<int16_t*>(d->out);
+  p.keys = static_cast<uint64_t*>(keys);
+  p.step = step;
+  p.ring = ring;
+  p.ring_ld = ring_ld;
+  p.token = token;
+  p.pos = pos;
+  p.ring_tok = ring_tokens;
+  p.embed = embed;
+  p.row = row;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.vocab = (int)vocab;
+  p.ring_cap = (int)std::min<int64_t>(ring_cap, INT32_MAX);
+  p.dim = (int)dim;
+  const hipStream_t st = (hipStream_t)stream;
+  if (K <= 576)
+    hipLaunchKernelGGL((panel ? dec_logits_kernel<9, true> : dec_logits_kernel<9, false>), dim3(G), dim3(DL_THREADS),
+                       64 * 9, st, p);
+  else if (K <= 896)
+    hipLaunchKernelGGL((panel ? dec_logits_kernel<14, true> : dec_logits_kernel<14, false>), dim3(G), dim3(DL_THREADS),
+                       64 * 14, st, p);
+  else
+    hipLaunchKernelGGL((panel ? dec_logits_kernel<16, true> : dec_logits_kernel<16, false>), dim3(G), dim3(DL_THREADS),
+                       64 * 16, st, p);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
 // The greedy step of a decode chain (golden.py:376-377 and the record of golden.py:411-414): the
 // best of the tiles' keys is the first argmax; then token, record, position and step updates, and
 // the next launch's input row = embed[token] (golden.py:369-373).
@@ -1523,3 +1733,28 @@ extern "C" int llhip_dec_greedy(const void* keys, int64_t nkeys, int32_t* token,
 }
 
 extern "C" int64_t llhip_dec_head_keys(int64_t N) { return ceil_div(N, 16); }
+
+extern "C" int64_t llhip_dec_logits_keys(void) { return DL_KEYS; }
+
+// one 16-byte piece per thread: piece i = (tile t, K step s, lane l = 16 kg + c)
+__global__ __launch_bounds__(256) void dec_logits_panel_kernel(const int8_t* __restrict__ W, int N, int K,
+                                                               int64_t pieces, v4i* __restrict__ panel) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pieces) return;
+  const int nst = K / 64, l = (int)(i & 63);
+  const int64_t ts = i >> 6;
+  const int t = (int)(ts / nst), s = (int)(ts % nst);
+  const int n = 16 * t + (l & 15);
+  panel[i] = n < N ? *reinterpret_cast<const v4i*>(W + (int64_t)n * K + 64 * s + 16 * (l >> 4)) : v4i{0, 0, 0, 0};
+}
+
+extern "C" int llhip_dec_logits_panel(const void* W, int64_t N, int64_t K, void* panel, void* stream) {
+  if (!W || !panel || N < 1 || K < 64 || K % 64 || !w_ok(ceil_div(N, 16) * 16, K) || (uintptr_t)W % 16 ||
+      (uintptr_t)panel % 16)
+    return fail(-EINVAL, "dec_logits_panel: bad operands (K a multiple of 64, 16-byte aligned)");
+  const int64_t pieces = ceil_div(N, 16) * (K / 64) * 64;
+  hipLaunchKernelGGL(dec_logits_panel_kernel, dim3((unsigned)ceil_div(pieces, 256)), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const int8_t*>(W), (int)N, (int)K, pieces, static_cast<v4i*>(panel));
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}

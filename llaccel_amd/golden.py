@@ -1047,8 +1047,9 @@ class GoldenModel:
         if self._chained(1):  # the chain's launches gather their next input row themselves
             _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim,
                       ctypes.c_void_p(self._st.data_ptr()), 1, 1, _ptr(self._act[self.q.input_name]), _stream())
-        if self._chained(1):  # the decode step's handle is made outside any capture
+        if self._chained(1):  # the decode step's handle and the head's panel are made outside any capture
             self._chain.step(ctypes.c_void_p(self._st.data_ptr() + 4))
+            self._chain.prepare_head()
         if self.use_graph and (self._graph is None or self._graph_chained != self._graph_key()):
             self._capture()
         for _ in range(n):

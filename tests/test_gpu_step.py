@@ -38,6 +38,7 @@ def test_step_equals_chain_and_oracle(tmp_path_factory, cfg):
     assert g._chain._step is not None, g._chain.step_unsupported  # the decode loop ran the one-launch step
     c = G.GoldenModel(qdir)
     c._chain.use_step = False
+    c._chain.use_logits = False  # and the head as finish + lm_head + greedy launches
     assert c.generate(prompt, 12) == rec
     assert c._chain._step is None
     _kv_equal(g, c)
