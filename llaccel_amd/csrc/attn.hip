@@ -535,22 +535,29 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
     for (int c = 0; c < DK; ++c)
       qf[c] = ld16(qr, (m < p.M && 64 * c + 16 * lg < D) ? (uint32_t)(lr * p.ldq + 64 * c + 16 * lg) : LD_OOB);
   }
+  // the LUT words (words tid, tid + blockDim.x, ..., at least 64 threads; stored to LDS once the tile
+  // loads below are issued, so the two round trips overlap)
+  constexpr int LUTW = (LUT_DW + 63) / 64;
+  uint32_t lutw[LUTW];
   {
     const Rsrc ir = rsrc(kExpI, sizeof(kExpI)), fr = rsrc(kExpF, sizeof(kExpF));
-    for (int idx = tid; idx < LUT_DW; idx += blockDim.x)
-      lut32[idx] = (uint32_t)ld4(ir, idx < 8 ? 4 * idx : LD_OOB) | (uint32_t)ld4(fr, idx >= 8 ? 4 * (idx - 8) : LD_OOB);
-    for (int idx = tid; idx < AT_ROWS * D; idx += blockDim.x) (&osum[0][0])[idx] = 0;
+#pragma unroll
+    for (int i = 0; i < LUTW; ++i) {
+      const int idx = tid + i * (int)blockDim.x;
+      lutw[i] = (uint32_t)ld4(ir, idx < 8 ? 4 * idx : LD_OOB) | (uint32_t)ld4(fr, idx >= 8 && idx < LUT_DW ? 4 * (idx - 8) : LD_OOB);
+    }
   }
   // K (or V) fragment of 16-key block j of tile kt: key kt*64 + 16j + lr, bytes [64c + 16lg, +16)
   auto frag_off = [&](int kt, int j, int c) -> uint32_t {
     return 64 * c + 16 * lg < D ? (uint32_t)((kt * 64 + 16 * j + lr) * D + 64 * c + 16 * lg) : LD_OOB;
   };
-  auto scores = [&](int kt, v4i (&st)[4]) {
-    v4i kf[4][DK];
+  auto kfrags = [&](int kt, v4i (&kf)[4][DK]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int c = 0; c < DK; ++c) kf[j][c] = ld16(kr, frag_off(kt, j, c));
+  };
+  auto score_mfmas = [&](const v4i (&kf)[4][DK], v4i (&st)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       st[j] = v4i{0, 0, 0, 0};
@@ -558,20 +565,47 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
       for (int c = 0; c < DK; ++c) st[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[j][c], qf[c], st[j], 0, 0, 0);
     }
   };
+  auto scores = [&](int kt, v4i (&st)[4]) {
+    v4i kf[4][DK];
+    kfrags(kt, kf);
+    score_mfmas(kf, st);
+  };
   // key of subtile j, register r of tile kt in this lane
   auto key = [&](int kt, int j, int r) { return kt * 64 + 16 * j + 4 * lg + r; };
 
   // Tiles wave + it * nw (it < SC) keep their scores, later their probabilities, in registers
   // across the three passes; further tiles are recomputed in each pass.
   v4i cache[SC][4];
+  // values of the cached tiles, requested with their keys (used in pass 3)
+  v4i vcache[SC][4][DK];
 
-  // pass 1: row maxima
+  // pass 1: row maxima.  The cached tiles' keys and values are requested first, then the LUT and
+  // the output sums are staged in LDS (visible after the first barrier).
   int32_t vmax = INT32_MIN;
+  v4i kfc[SC][4][DK];
+#pragma unroll
+  for (int it = 0; it < SC; ++it) {
+    const int kt = wave + it * nw;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) kfc[it][j][c] = ld16(kr, kt < ntiles ? frag_off(kt, j, c) : LD_OOB);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int c = 0; c < DK; ++c) vcache[it][j][c] = ld16(vr, kt < ntiles ? frag_off(kt, j, c) : LD_OOB);
+  }
+#pragma unroll
+  for (int i = 0; i < LUTW; ++i) {
+    const int idx = tid + i * (int)blockDim.x;
+    if (idx < LUT_DW) lut32[idx] = lutw[i];
+  }
+  for (int idx = tid; idx < AT_ROWS * D; idx += blockDim.x) (&osum[0][0])[idx] = 0;
 #pragma unroll
   for (int it = 0; it < SC; ++it) {
     const int kt = wave + it * nw;
     if (kt < ntiles) {
-      scores(kt, cache[it]);
+      score_mfmas(kfc[it], cache[it]);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -596,17 +630,6 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
   for (int w = 1; w < nw; ++w) mx = max(mx, red[w][lr]);
   __syncthreads();
 
-  // values of the cached tiles: loaded now, used in pass 3
-  v4i vcache[SC][4][DK];
-#pragma unroll
-  for (int it = 0; it < SC; ++it) {
-    const int kt = wave + it * nw;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int c = 0; c < DK; ++c) vcache[it][b][c] = ld16(vr, kt < ntiles ? frag_off(kt, b, c) : LD_OOB);
-  }
-
   // pass 2: sums of the LUT exponentials (cached tiles keep p in place of s)
   const uint16_t* ei = reinterpret_cast<const uint16_t*>(lut32);
   const uint16_t* ef = ei + 16;
@@ -614,29 +637,46 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
   pq.Ms = (uint32_t)p.Ms;
   pq.Ss = p.Ss;
   pq.zc = p.Ss > 0 ? 1ull << (p.Ss - 1) : 0ull;
+  // a tile's 16 scores -> probabilities in place (0 at or past the row's T), returning their sum:
+  // branch-free, all 32 LUT reads issued before the first is used
+  auto tile_probs = [&](int kt, v4i (&st)[4]) -> uint32_t {
+    uint32_t zi[16], lo[16], hi[16];
+    bool ok[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint64_t z = ((uint64_t)(uint32_t)(mx - st[j][r]) * pq.Ms + pq.zc) >> pq.Ss;
+        ok[4 * j + r] = key(kt, j, r) < tlim && z < 4096;
+        zi[4 * j + r] = ok[4 * j + r] ? (uint32_t)z : 0u;
+      }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      hi[k] = ei[zi[k] >> 8];
+      lo[k] = ef[zi[k] & 255];
+    }
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int k = 4 * j + r;
+        const uint32_t pr = ok[k] ? (hi[k] * lo[k] + 32768u) >> 16 : 0u;
+        st[j][r] = (int32_t)pr;
+        sum += pr;
+      }
+    return sum;
+  };
   uint32_t vsum = 0;
 #pragma unroll
   for (int it = 0; it < SC; ++it) {
     const int kt = wave + it * nw;
-    if (kt < ntiles) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t pr = key(kt, j, r) < tlim ? prob_lds(mx - cache[it][j][r], pq, ei, ef) : 0u;
-          cache[it][j][r] = (int32_t)pr;
-          vsum += pr;
-        }
-    }
+    if (kt < ntiles) vsum += tile_probs(kt, cache[it]);
   }
   for (int kt = wave + SC * nw; kt < ntiles; kt += nw) {
     v4i st[4];
     scores(kt, st);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (key(kt, j, r) < tlim) vsum += prob_lds(mx - st[j][r], pq, ei, ef);
+    vsum += tile_probs(kt, st);
   }
   vsum += (uint32_t)__shfl_xor((int)vsum, 16);
   vsum += (uint32_t)__shfl_xor((int)vsum, 32);
@@ -705,11 +745,7 @@ __global__ __launch_bounds__(64 * AttnTileCfg<D>::MAXW) void attention_tiled(Att
       for (int c = 0; c < DK; ++c) vf[b][c] = ld16(vr, frag_off(kt, b, c));
     v4i st[4];
     scores(kt, st);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        st[j][r] = key(kt, j, r) < tlim ? (int32_t)prob_lds(mx - st[j][r], pq, ei, ef) : 0;
+    tile_probs(kt, st);
     pv_tile(st, vf);
   }
   // C layout of O: lane (lg, lr) register r = row 4lg + r, column 16e + lr
