@@ -154,6 +154,15 @@ typedef struct llhip_linear_problem {
 } llhip_linear_problem;
 int llhip_linear_group(const int8_t* A, int64_t M, int64_t K, int64_t lda, int64_t count,
                        const llhip_linear_problem* probs, void* ws, void* stream);
+/* golden.py:316-342 + 141-158 + 119-120 + 344-351 -- the q, k, v projections of a prompt chunk
+ * (probs[0..2]: q and k with i16 outputs, v with i8 output, N multiples of 64) and the rope -> quant
+ * of the query rows (rq) and of the key rows with the K/V cache write (rk, its v = probs[2].out) in
+ * ONE launch: llhip_linear_group followed by llhip_rope_quant2 with x = the q and k outputs, every
+ * output of both written.  head_dim 64, K a multiple of 128, 16-byte aligned rows, tables and
+ * caches, slot_stride a multiple of 16.  rq and rk give the same positions and tables. */
+int llhip_linear_group_rope(const int8_t* A, int64_t M, int64_t K, int64_t lda, const llhip_linear_problem* probs,
+                            const llhip_rope_quant_desc* rq, const llhip_rope_quant_desc* rk, void* ws,
+                            void* stream);
 
 /* golden.py:217-240  exact integer A[M][K] (int64) . W[N][K]^T (int8) -> int64 [M][N] */
 int llhip_exact_matmul(const int64_t* A, int64_t M, int64_t K, const int8_t* W, int64_t N, int64_t* out,

@@ -209,6 +209,8 @@ _SIGS.update({
     "llhip_dec_logits": [ctypes.POINTER(NormLinearDesc), _p, ctypes.POINTER(ResidDesc), _i64, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _p, _p],
     "llhip_dec_logits_keys": [],
     "llhip_dec_logits_panel": [_p, _i64, _i64, _p, _p],
+    "llhip_linear_group_rope": [_p, _i64, _i64, _i64, _p, ctypes.POINTER(RopeQuantDesc),
+                                ctypes.POINTER(RopeQuantDesc), _p, _p],
 })
 _RESTYPES["llhip_dec_head_keys"] = _i64
 _RESTYPES["llhip_dec_logits_keys"] = _i64

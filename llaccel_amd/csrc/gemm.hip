@@ -23,7 +23,7 @@ namespace llhip {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-enum Epi : int { EPI_NONE = 0, EPI_RESADD = 1, EPI_SILU = 2, EPI_MUL = 3 };
+enum Epi : int { EPI_NONE = 0, EPI_RESADD = 1, EPI_SILU = 2, EPI_MUL = 3, EPI_ROPE = 4 };
 
 
 struct LinearArgs {
@@ -682,6 +682,134 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// RoPE epilogue of the q/k/v projections of a prompt chunk (llhip_linear_group_rope): the tile's
+// requantised values go through LDS (the ring is free after the K loop of a one-tile workgroup),
+// then every thread takes 8 rotation pairs of one row and head -- columns i0..i0+7 and 32+i0.. of
+// the 64-column head -- and applies the rope_quant kernel's arithmetic (golden.py:141-158, 119-120)
+// with 16-byte table loads and 16- and 8-byte stores; key tiles also write the quantised keys into
+// the K cache, value tiles their i8 rows into the V cache (golden.py:344-351).  Positions and cache
+// slots as the rope_quant kernel's.
+// ---------------------------------------------------------------------------------------
+struct RopeShared {
+  const int16_t* cos_tab;
+  const int16_t* sin_tab;
+  const int32_t* pos_dev;
+  const int32_t* row_pos;
+  int64_t table_rows, max_seq, slot_stride, seq_rows;
+  int pos;
+};
+// one problem's part: kind 1 rope + quant [+ K cache], kind 2 V cache
+struct RopeSel {
+  int kind, qS;
+  int64_t qM;
+  int16_t* y;
+  int8_t* yq;
+  int8_t* cache;
+};
+
+__device__ __forceinline__ v4i rope_pack16x8(const int32_t (&v)[8]) {
+  return v4i{pack16(v[0], v[1]), pack16(v[2], v[3]), pack16(v[4], v[5]), pack16(v[6], v[7])};
+}
+__device__ __forceinline__ v2i rope_pack8x8(const int32_t (&v)[8]) {
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e >> 2] |= (uint32_t)(v[e] & 255) << (8 * (e & 3));
+  return v2i{(int)w[0], (int)w[1]};
+}
+
+// row m's position and cache slot (as the rope_quant kernel's)
+__device__ __forceinline__ void rope_position(const RopeShared& rs, int64_t m, int64_t& pm, int64_t& slot) {
+  pm = rs.row_pos ? (int64_t)rs.row_pos[m] : rs.seq_rows ? (int64_t)rs.pos + m % rs.seq_rows
+                                                           : (int64_t)(rs.pos_dev ? *rs.pos_dev : rs.pos) + m;
+  slot = rs.row_pos ? m * rs.slot_stride : (rs.seq_rows ? m / rs.seq_rows * rs.slot_stride : 0);
+}
+
+template <int GM, int GN, int NT, bool FAST, int WM, int WN>
+__device__ __forceinline__ void rope_tile_epilogue(const LinearArgs& p, const v16i (&acc)[WM][WN],
+                                                   const ColRq (&cq)[WN], int m0, int n0, int wm, int wn, int8_t* ring,
+                                                   const RopeShared& rs, const RopeSel& sel, bool out8) {
+  int16_t* X = reinterpret_cast<int16_t*>(ring);  // [GM][GN] requantised (i8 outputs: already clamped to i8)
+  const int tid = threadIdx.x, lane = tid & 63;
+#pragma unroll
+  for (int j = 0; j < WN; ++j)
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm + 32 * i + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), col = wn + 32 * j + (lane & 31);
+        const int32_t v = requant_col<FAST>(acc[i][j][r], cq[j]);
+        X[row * GN + col] = (int16_t)(out8 ? clamp32(v, -128, 127) : clamp32(v, -32768, 32767));
+      }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  lds_barrier();
+  if (sel.kind == 1) {
+    // item = (row, head of the tile, 8-pair group): GM x GN/64 x 4
+    const double sq = mulshift_scale(sel.qM, sel.qS);
+    constexpr int ITEMS = GM * (GN / 64) * 4;
+#pragma unroll
+    for (int k = 0; k < (ITEMS + NT - 1) / NT; ++k) {
+      const int t = tid + k * NT;
+      if (t >= ITEMS) break;
+      const int row = t / ((GN / 64) * 4), rem = t % ((GN / 64) * 4), hh = rem >> 2, i0 = (rem & 3) * 8;
+      const int64_t m = m0 + row;
+      const int n = n0 + 64 * hh;  // the head's first column
+      if (m >= p.M || n >= p.N) continue;
+      const int16_t* xr = X + row * GN + 64 * hh + i0;
+      const v4i a8 = *reinterpret_cast<const v4i*>(xr), b8 = *reinterpret_cast<const v4i*>(xr + 32);
+      int16_t* out = static_cast<int16_t*>(p.out) + m * p.ldo + n + i0;  // the linear's own output
+      *reinterpret_cast<v4i*>(out) = a8;
+      *reinterpret_cast<v4i*>(out + 32) = b8;
+      int64_t pm, slot;
+      rope_position(rs, m, pm, slot);
+      if (pm < 0 || pm >= rs.table_rows) continue;  // as the rope_quant kernel: no rotated output
+      const int64_t trow = pm * 32 + i0;
+      const v4i c8 = *reinterpret_cast<const v4i*>(rs.cos_tab + trow), s8 = *reinterpret_cast<const v4i*>(rs.sin_tab + trow);
+      int32_t y1[8], y2[8], q1[8], q2[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int32_t c = (e & 1) ? hi16(c8[e >> 1]) : lo16(c8[e >> 1]), sn = (e & 1) ? hi16(s8[e >> 1]) : lo16(s8[e >> 1]);
+        const int32_t a = (e & 1) ? hi16(a8[e >> 1]) : lo16(a8[e >> 1]), b = (e & 1) ? hi16(b8[e >> 1]) : lo16(b8[e >> 1]);
+        y1[e] = (int32_t)sat16(rshr((int64_t)a * c - (int64_t)b * sn, 14));
+        y2[e] = (int32_t)sat16(rshr((int64_t)b * c + (int64_t)a * sn, 14));
+        q1[e] = mulshift_small_sat(y1[e], sq, -128.0, 127.0);
+        q2[e] = mulshift_small_sat(y2[e], sq, -128.0, 127.0);
+      }
+      const int64_t o = m * p.N + n + i0;  // rope and quant outputs: [M][H*D]
+      if (sel.y) {
+        *reinterpret_cast<v4i*>(sel.y + o) = rope_pack16x8(y1);
+        *reinterpret_cast<v4i*>(sel.y + o + 32) = rope_pack16x8(y2);
+      }
+      const v2i w1 = rope_pack8x8(q1), w2 = rope_pack8x8(q2);
+      *reinterpret_cast<v2i*>(sel.yq + o) = w1;
+      *reinterpret_cast<v2i*>(sel.yq + o + 32) = w2;
+      if (sel.cache && pm < rs.max_seq) {
+        const int64_t dst = slot + ((int64_t)(n / 64) * rs.max_seq + pm) * 64 + i0;
+        *reinterpret_cast<v2i*>(sel.cache + dst) = w1;
+        *reinterpret_cast<v2i*>(sel.cache + dst + 32) = w2;
+      }
+    }
+  } else {
+    // value tile: item = (row, 16 columns); the i8 output and the V cache row
+    for (int t = tid; t < GM * (GN / 16); t += NT) {
+      const int row = t / (GN / 16), c0 = (t % (GN / 16)) * 16;
+      const int64_t m = m0 + row;
+      const int n = n0 + c0;
+      if (m >= p.M || n >= p.N) continue;
+      const int16_t* xr = X + row * GN + c0;
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) w[e >> 2] |= (uint32_t)(xr[e] & 255) << (8 * (e & 3));
+      const v4i v16 = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      *reinterpret_cast<v4i*>(static_cast<int8_t*>(p.out) + m * p.ldo + n) = v16;
+      int64_t pm, slot;
+      rope_position(rs, m, pm, slot);
+      if (sel.cache && pm >= 0 && pm < rs.table_rows && pm < rs.max_seq)
+        *reinterpret_cast<v4i*>(sel.cache + slot + ((int64_t)(n / 64) * rs.max_seq + pm) * 64 + (n % 64)) = v16;
+    }
+  }
+}
+
 // Output tiles l = l0, l0 + lstep, ... < lend (logical index: M-block l % mblocks, N-block
 // l / mblocks), one after another.  The first stages of the next tile are issued as soon as the
 // K loop of this one has finished reading the ring, so their memory latency passes during this
@@ -694,7 +822,7 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
 // sum) and applies the epilogue.
 template <int EPI, bool OUT8, int GM, int GN, int NW, int KT, int NS_>
 __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int l0, int lstep, int lend, int kps,
-                                           int32_t* part) {
+                                           int32_t* part, const RopeShared* rs = nullptr, RopeSel rsel = RopeSel{}) {
   using T = MfmaTile<GM, GN, NW, KT, NS_>;
   constexpr int NS = T::NS;
   extern __shared__ __attribute__((aligned(1024))) int8_t ring[];  // [NS][A GM x KT | W GN x KT]
@@ -846,6 +974,15 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
     for (int j = 0; j < T::WN; ++j) col_fast = col_fast && colrq_fast(cq[j]);
     const bool fast = __all(col_fast);
 
+    if constexpr (EPI == EPI_ROPE) {  // one tile per workgroup: the ring is free (its reads returned above)
+      lds_barrier();
+      if (fast)
+        rope_tile_epilogue<GM, GN, T::NT, true>(p, acc, cq, m0, n0, wm, wn, ring, *rs, rsel, OUT8);
+      else
+        rope_tile_epilogue<GM, GN, T::NT, false>(p, acc, cq, m0, n0, wm, wn, ring, *rs, rsel, OUT8);
+      return;
+    }
+
     if constexpr (OUT8) {
       const bool full = m0 + GM <= p.M && n0 + GN <= p.N && p.ldo % 4 == 0 && (uintptr_t)p.out % 4 == 0;
       if (fast)
@@ -899,9 +1036,12 @@ struct LinearGroup {
   int64_t ldo[GROUP_MAX];
   int N[GROUP_MAX];
   int out8[GROUP_MAX];
+  // the RoPE epilogue (linear_mfma_group<..., true>): per problem, and shared
+  RopeSel rope[GROUP_MAX];
+  RopeShared rs;
 };
 
-template <int GM, int GN, int NW, int KT, int NS>
+template <int GM, int GN, int NW, int KT, int NS, bool ROPE = false>
 __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, LinearGroup g, int mblocks) {
   const int b = blockIdx.x;
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
@@ -918,6 +1058,18 @@ __global__ __launch_bounds__(64 * NW) void linear_mfma_group(LinearArgs p, Linea
   pp.N = g.N[q];
   nbk -= g.nb0[q];
   const int l = nbk * mblocks + mb;
+  if constexpr (ROPE) {
+    // the problem's epilogue fields picked with a wave-uniform select (no indexed kernel argument)
+    RopeSel sel = g.rope[0];
+#pragma unroll
+    for (int i = 1; i < GROUP_MAX; ++i)
+      if (q == i) sel = g.rope[i];
+    if (g.out8[q])
+      mfma_tiles<EPI_ROPE, true, GM, GN, NW, KT, NS>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr, &g.rs, sel);
+    else
+      mfma_tiles<EPI_ROPE, false, GM, GN, NW, KT, NS>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr, &g.rs, sel);
+    return;
+  }
   if (g.out8[q])
     mfma_tiles<EPI_NONE, true, GM, GN, NW, KT, NS>(pp, mblocks, l, 1, l + 1, p.K / KT, nullptr);
   else
@@ -1683,6 +1835,121 @@ extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {
   else
     hipLaunchKernelGGL((linear_mfma_dual<64, GSTAGES>), grid, dim3(512), GSTAGES * (64 + 2 * 128) * 64, s, p, a, mblocks,
                        nblocks);
+  LLHIP_LAUNCH_CHECK();
+  return 0;
+}
+
+// one rope descriptor of llhip_linear_group_rope: the checks of llhip_rope_quant for rows produced by
+// problem pr (x = pr.out, D = 64, the problem's N = H D), plus the alignments of the 16- and 8-byte
+// accesses of the epilogue
+static int rope_group_part(const llhip_rope_quant_desc& d, const llhip_linear_problem& pr, int64_t M, bool key) {
+  if (d.D != 64 || d.H < 1 || d.H * 64 != pr.N || d.x != pr.out || d.M != M || d.ldx != pr.ldo || pr.out_i8)
+    return fail(-EINVAL, "linear_group_rope: the rope rows must be problem %s's i16 output, head_dim 64", key ? "k" : "q");
+  if (!u32_ok(d.qM) || !shift_ok(d.qS)) return fail(-EINVAL, "linear_group_rope: quant multiplier must be u32, shift in [0,63]");
+  if (!d.yq || !d.cos_tab || !d.sin_tab) return fail(-EINVAL, "linear_group_rope: null operand");
+  if (d.seq_rows < 0 || (d.seq_rows > 0 && (d.pos_dev || d.row_pos || M % d.seq_rows)))
+    return fail(-EINVAL, "linear_group_rope: sequences of seq_rows rows need M %% seq_rows == 0 and no row positions");
+  const int64_t span = d.seq_rows > 0 ? d.seq_rows : M;
+  if (!d.pos_dev && !d.row_pos && (d.pos < 0 || d.pos + span > d.table_rows))
+    return fail(-ERANGE, "rope: positions exceed the table");
+  const auto al = [](const void* p, uintptr_t a) { return (uintptr_t)p % a == 0; };
+  if (!al(pr.out, 16) || pr.ldo % 8 || !al(d.y, 16) || !al(d.yq, 8) || !al(d.cos_tab, 16) || !al(d.sin_tab, 16))
+    return fail(-EINVAL, "linear_group_rope: misaligned rows or tables");
+  if (!key) {
+    if (d.kc || d.vc) return fail(-EINVAL, "linear_group_rope: the query rows write no cache");
+    return 0;
+  }
+  if (!d.kc != !d.vc) return fail(-EINVAL, "linear_group_rope: the key rows write both caches or neither");
+  if (d.kc) {
+    if (!d.pos_dev && !d.row_pos && d.pos + span > d.max_seq)
+      return fail(-ERANGE, "positions %lld..%lld exceed max_seq=%lld", (long long)d.pos, (long long)(d.pos + span - 1),
+                  (long long)d.max_seq);
+    if ((d.row_pos || d.seq_rows > 0) && d.slot_stride < d.H * d.max_seq * 64)
+      return fail(-EINVAL, "linear_group_rope: cache slots overlap");
+    if (!al(d.kc, 16) || !al(d.vc, 16) || d.slot_stride % 16) return fail(-EINVAL, "linear_group_rope: misaligned caches");
+  }
+  return 0;
+}
+
+extern "C" int llhip_linear_group_rope(const int8_t* A, int64_t M, int64_t K, int64_t lda, const llhip_linear_problem* probs,
+                                       const llhip_rope_quant_desc* rq, const llhip_rope_quant_desc* rk, void* ws,
+                                       void* stream) {
+  (void)ws;
+  if (!probs || !rq || !rk || !A) return fail(-EINVAL, "linear_group_rope: null argument");
+  if (M < 1 || M > INT32_MAX || K < 128 || K % 128 || K > 65535 || lda < K || lda % 16 || (uintptr_t)A % 16)
+    return fail(-EINVAL, "linear_group_rope: rows of K %% 128 == 0 bytes, 16-byte aligned");
+  for (int q = 0; q < 3; ++q) {
+    const llhip_linear_problem& r = probs[q];
+    if (r.N < 64 || r.N % 64 || r.N > INT32_MAX || r.ldo < r.N || !r.W || !r.rq || !r.out || (uintptr_t)r.W % 16)
+      return fail(-EINVAL, "linear_group_rope: bad problem %d (N a multiple of 64, 16-byte aligned weights)", q);
+  }
+  const llhip_linear_problem& pv = probs[2];
+  if (!pv.out_i8 || pv.N != probs[1].N || (uintptr_t)pv.out % 16 || pv.ldo % 16)
+    return fail(-EINVAL, "linear_group_rope: the v problem writes i8 rows of the k problem's width, 16-byte aligned");
+  int rc = rope_group_part(*rq, probs[0], M, false);
+  if (!rc) rc = rope_group_part(*rk, probs[1], M, true);
+  if (rc) return rc;
+  if (rk->kc && (rk->v != pv.out || rk->ldv != pv.ldo))
+    return fail(-EINVAL, "linear_group_rope: the V cache rows must be problem v's output");
+  if (rq->pos != rk->pos || rq->pos_dev != rk->pos_dev || rq->row_pos != rk->row_pos || rq->seq_rows != rk->seq_rows ||
+      rq->cos_tab != rk->cos_tab || rq->sin_tab != rk->sin_tab || rq->table_rows != rk->table_rows)
+    return fail(-EINVAL, "linear_group_rope: q and k rows at different positions");
+  LinearArgs p{};
+  p.A = A;
+  p.lda = lda;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.steps = (int)ceil_div(K, 64);
+  const int mblocks = (int)ceil_div(M, 64), cus = current_cu_count();
+  const int64_t n64 = (probs[0].N + probs[1].N + probs[2].N) / 64;
+  const bool narrow = mblocks * n64 <= cus;
+  const int gn = narrow ? 64 : 128;
+  LinearGroup g{};
+  g.count = 3;
+  g.nb0[0] = 0;
+  for (int q = 0; q < 3; ++q) {
+    g.W[q] = static_cast<const int8_t*>(probs[q].W);
+    g.rq[q] = static_cast<const int32_t*>(probs[q].rq);
+    g.bias[q] = static_cast<const int32_t*>(probs[q].bias);
+    g.out[q] = probs[q].out;
+    g.ldo[q] = probs[q].ldo;
+    g.N[q] = (int)probs[q].N;
+    g.out8[q] = probs[q].out_i8 ? 1 : 0;
+    g.nb0[q + 1] = g.nb0[q] + (int)ceil_div(probs[q].N, gn);
+  }
+  const llhip_rope_quant_desc* rd[2] = {rq, rk};
+  for (int q = 0; q < 2; ++q) {
+    g.rope[q].kind = 1;
+    g.rope[q].qM = rd[q]->qM;
+    g.rope[q].qS = (int)rd[q]->qS;
+    g.rope[q].y = static_cast<int16_t*>(rd[q]->y);
+    g.rope[q].yq = static_cast<int8_t*>(rd[q]->yq);
+    g.rope[q].cache = static_cast<int8_t*>(rd[q]->kc);
+  }
+  g.rope[2].kind = 2;
+  g.rope[2].cache = static_cast<int8_t*>(rk->vc);
+  g.rs.cos_tab = static_cast<const int16_t*>(rk->cos_tab);
+  g.rs.sin_tab = static_cast<const int16_t*>(rk->sin_tab);
+  g.rs.pos_dev = static_cast<const int32_t*>(rk->pos_dev);
+  g.rs.row_pos = static_cast<const int32_t*>(rk->row_pos);
+  g.rs.table_rows = rk->table_rows;
+  g.rs.max_seq = rk->max_seq;
+  g.rs.slot_stride = rk->slot_stride;
+  g.rs.seq_rows = rk->seq_rows;
+  g.rs.pos = (int)rk->pos;
+  const dim3 grid((unsigned)(ceil_div((int64_t)mblocks * g.nb0[3], 8) * 8));
+  const hipStream_t s = (hipStream_t)stream;
+  if (narrow) {
+    using T = MfmaTile<64, 64, 4, 128, 3>;
+    hipLaunchKernelGGL((linear_mfma_group<64, 64, 4, 128, 3, true>), grid, dim3(T::NT), T::LDS_BYTES, s, p, g, mblocks);
+  } else if (grid.x < (unsigned)cus) {
+    using T = MfmaTile<64, 128, 4, 128, 3>;
+    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 128, 3, true>), grid, dim3(T::NT), T::LDS_BYTES, s, p, g, mblocks);
+  } else {
+    using T = MfmaTile<64, 128, 4, 128>;
+    hipLaunchKernelGGL((linear_mfma_group<64, 128, 4, 128, T::NS, true>), grid, dim3(T::NT), T::LDS_BYTES, s, p, g,
+                       mblocks);
+  }
   LLHIP_LAUNCH_CHECK();
   return 0;
 }

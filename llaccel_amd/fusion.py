@@ -156,16 +156,48 @@ class _GroupLinearStep:
         self.model, self.lins = model, lins
         self.probs = (_lib.LinearProblem * len(lins))()
 
-    def __call__(self, M, pos, pd=None):
+    def fill(self):
         m = self.model
         for pr, o in zip(self.probs, self.lins):
             out = m._buf(o["out"])
             pr.W, pr.N, pr.rq = _vp(m._dt[o["w"]]), int(o["N"]), _vp(m._dt[o["rq"]])
             pr.bias = _vp(m._dt[o["bias"]]) if o.get("bias") else None
             pr.out, pr.ldo, pr.out_i8 = _vp(out), out.shape[1], int(o.get("out_dtype", "i16") == "i8")
+
+    def __call__(self, M, pos, pd=None):
+        m = self.model
+        self.fill()
         a = self.lins[0]
         _lib.call("llhip_linear_group", _vp(m._buf(a["in"])), M, int(a["K"]), int(a["K"]), len(self.lins), self.probs,
                   _vp(m._ws), m._stream_handle())
+
+
+class _GroupRopeStep:
+    """The q, k, v linears and the rope -> quant of the q and k rows with the layer's kv_write in ONE
+    llhip_linear_group_rope launch (head_dim 64: a 64-column GEMM tile is one head, the rotation
+    is the GEMM's epilogue); shapes or alignments it refuses run the two launches instead."""
+
+    def __init__(self, model, group, rope):
+        self.model, self.group, self.rope = model, group, rope
+        self.fused = True   # cleared once the fused entry refuses this graph's operands
+        self.launched = 0   # fused launches made (a test hook)
+
+    def __call__(self, M, pos, pd=None):
+        if self.fused:
+            g, r, m = self.group, self.rope, self.model
+            g.fill()
+            for d, (ro, qu, kvw) in zip(r.desc, r.parts):
+                r._fill(d, ro, qu, kvw, M, pos, pd)
+            a = g.lins[0]
+            try:
+                _lib.call("llhip_linear_group_rope", _vp(m._buf(a["in"])), M, int(a["K"]), int(a["K"]), g.probs,
+                          ctypes.byref(r.desc[0]), ctypes.byref(r.desc[1]), _vp(m._ws), m._stream_handle())
+                self.launched += 1
+                return
+            except ValueError:
+                self.fused = False  # checked before any launch: nothing ran
+        self.group(M, pos, pd)
+        self.rope(M, pos, pd)
 
 
 class _GateUpStep:
@@ -255,7 +287,13 @@ def wide_steps(model, ops, steps):
                     and _is(kvw, "kv_write") and qq_["in"] == rq_["out"] and kq_["in"] == rk_["out"]
                     and kvw["k"] == kq_["out"] and int(kvw["Hkv"]) == int(rk_["H"]) and int(kvw["D"]) == int(rk_["D"])
                     and model._act_spec[kvw["v"]][1] >= int(rk_["H"]) * int(rk_["D"])):
-                out.append(_RopeQuantStep(model, rq_, qq_, rk_, kq_, kvw))
+                rope = _RopeQuantStep(model, rq_, qq_, rk_, kq_, kvw)
+                prev = out[-1] if out else None
+                if (isinstance(prev, _GroupLinearStep) and int(rq_["D"]) == 64
+                        and [o["out"] for o in prev.lins] == [rq_["in"], rk_["in"], kvw["v"]]):
+                    out[-1] = _GroupRopeStep(model, prev, rope)  # q, k, v, rope, quant, kv_write: one launch
+                else:
+                    out.append(rope)
                 i += 5
                 continue
         out.append(steps[i])

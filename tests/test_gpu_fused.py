@@ -97,8 +97,9 @@ def test_qwen3_preinitialised_long_context(tmp_path_factory):
 
 @pytest.mark.parametrize("cfg", ["smol", "qwen25", "qwen3"])
 def test_whole_prompt_prefill_large_models(tmp_path_factory, cfg):
-    """Config 3-5 shapes: one M = 64 prefill launch (tiled MFMA GEMM, M-row attention) == the
-    chunked M = 16 launches (fused kernels), logits and KV."""
+    """Config 3-5 shapes: one M = 64 prefill launch (tiled MFMA GEMM, M-row attention; at head_dim 64
+    the q/k/v GEMM with the rope/quant/kv_write epilogue) == the chunked M = 16 launches (fused
+    kernels), logits and KV."""
     qdir = _qgraph(tmp_path_factory, cfg, True)
     prompt = synth.seeded_prompt(cfg, 61, 3)
     g1, g2 = G.GoldenModel(qdir), G.GoldenModel(qdir)
@@ -107,6 +108,13 @@ def test_whole_prompt_prefill_large_models(tmp_path_factory, cfg):
     assert all(np.array_equal(a, b) for a, b in zip(r1, r2))
     for layer in (0, g1.n_layers // 2, g1.n_layers - 1):
         assert np.array_equal(g1.kv[layer][0], g2.kv[layer][0]) and np.array_equal(g1.kv[layer][1], g2.kv[layer][1])
+    from llaccel_amd.fusion import _GroupRopeStep
+
+    gr = [w for st in g1._plan for w in getattr(st, "wide", None) or [] if isinstance(w, _GroupRopeStep)]
+    if cfg == "qwen25":  # head_dim 64, K % 128 == 0: q, k, v with their rope, quant and kv_write in one launch
+        assert gr and all(w.fused and w.launched > 0 for w in gr)
+    if cfg == "smol":  # K = 576: the fused launch refuses and the two launches run
+        assert gr and not any(w.fused for w in gr)
 
 
 def test_prefill_graph_replays_equal_eager_launches(tmp_path_factory):
