@@ -662,7 +662,11 @@ __device__ __forceinline__ void store_i16_tile(const LinearArgs& p, const v16i (
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[e] = silu16_i16(o[e], (uint32_t)p.Mi, p.Si, p.sh, sig);
           }
-          *reinterpret_cast<v2i*>(out + (int64_t)m * p.ldo + nq) = v2i{pack16(o[0], o[1]), pack16(o[2], o[3])};
+          // streamed past the caches (non-temporal): nothing in this launch reads the output, and
+          // kept out of L2 it leaves the A and W panels there (512 x 896 x 151936: 152.6 -> 135.9
+          // us; the same for the i8 stores above: 119 -> 160 us, not kept)
+          __builtin_nontemporal_store(v2i{pack16(o[0], o[1]), pack16(o[2], o[3])},
+                                      reinterpret_cast<v2i*>(out + (int64_t)m * p.ldo + nq));
         } else if (m < p.M) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
