@@ -37,6 +37,7 @@ SIG = sigmoid_lut().astype(I64)
 EXPI = exp_int_lut().astype(I64)
 EXPF = exp_frac_lut().astype(I64)
 PREFILL_M = 16
+DECODE_GRAPH_STEPS = 8  # decode launches per replay of the run graph (decode_loop)
 
 _torch = None
 
@@ -1017,11 +1018,18 @@ class GoldenModel:
                   _ptr(self._ring_rows), self.vocab, _ptr(self._ring_tok), self._ring_cap, _ptr(self._ws), _stream())
 
     def _capture(self) -> None:
+        """The decode graphs: one launch, and DECODE_GRAPH_STEPS launches in a row (each launch reads
+        and advances the device position and step, so the copies run consecutive positions; one
+        replay of the run graph instead of several saves the gaps between replays)."""
         torch = _t()
         g = torch.cuda.CUDAGraph()
         with capture_graph(g):
             self._decode_launch()
-        self._graph = g
+        run = torch.cuda.CUDAGraph()
+        with capture_graph(run):
+            for _ in range(DECODE_GRAPH_STEPS):
+                self._decode_launch()
+        self._graph, self._graph_run = g, run
         self._graph_chained = self._graph_key()
 
     def _graph_key(self):
@@ -1052,10 +1060,13 @@ class GoldenModel:
             self._chain.prepare_head()
         if self.use_graph and (self._graph is None or self._graph_chained != self._graph_key()):
             self._capture()
-        for _ in range(n):
-            if self.use_graph:
+        if self.use_graph:
+            for _ in range(n // DECODE_GRAPH_STEPS):
+                self._graph_run.replay()
+            for _ in range(n % DECODE_GRAPH_STEPS):
                 self._graph.replay()
-            else:
+        else:
+            for _ in range(n):
                 self._decode_launch()
         if not sync:
             return None
