@@ -1131,18 +1131,11 @@ class GoldenModel:
             g = torch.cuda.CUDAGraph()
             with capture_graph(g):
                 self._decode_batch_launch()
-            run = torch.cuda.CUDAGraph()  # DECODE_GRAPH_STEPS launches in a row, as decode_loop's
-            with capture_graph(run):
-                for _ in range(DECODE_GRAPH_STEPS):
-                    self._decode_batch_launch()
-            self._graph_b, self._graph_b_run = g, run
-        if self.use_graph:
-            for _ in range(n // DECODE_GRAPH_STEPS):
-                self._graph_b_run.replay()
-            for _ in range(n % DECODE_GRAPH_STEPS):
+            self._graph_b = g
+        for _ in range(n):
+            if self.use_graph:
                 self._graph_b.replay()
-        else:
-            for _ in range(n):
+            else:
                 self._decode_batch_launch()
         if not sync:
             return None
