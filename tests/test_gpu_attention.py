@@ -46,6 +46,11 @@ CASES = [
     (20, 8, 2, 64, 3000, 4096),
     (3, 4, 2, 32, 2500, 3000),
     (1, 2, 1, 16, 2047, 2048),
+    # launches of more waves than fit three to a SIMD (a batched prefill's size; at D = 64 the
+    # register-capped instance of the multi-row kernel)
+    (2048, 14, 2, 64, 0, 2048),
+    (1024, 8, 2, 16, 0, 1024),
+    (1024, 8, 4, 32, 0, 1024),
 ]
 
 
