@@ -1170,8 +1170,10 @@ class GoldenModel:
 
     def _prefill_seqs(self, prompts, Lp: int):
         """The one-launch batch prefill: embedding gathers of every prompt into its Lp rows (pad rows
-        zero), then the op list over B x Lp rows in the sequence-major position context.  Returns a
-        device copy of the B x Lp logits rows."""
+        zero), then the op list over B x Lp rows in the sequence-major position context.  Returns the
+        B x Lp logits rows: a buffer of their own that the lm_head writes directly (no device copy of
+        the B x Lp x vocab rows; this launch is not captured, so the output buffer may change)."""
+        torch = _t()
         B = len(prompts)
         M = B * Lp
         self._ensure_capacity(M)
@@ -1181,14 +1183,19 @@ class GoldenModel:
             _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, _ptr(td),
                       len(prompts[b]), Lp, _ptr(x[b * Lp]), _stream())
         kc0 = next(iter(self._kv.values()))[0]
+        out_name = self.q.output_name
+        shared = self._act[out_name]
+        rows = torch.empty((M, shared.shape[1]), dtype=shared.dtype, device=self.device)
+        self._act[out_name] = rows
         self._lean = True  # no activation is collected: dead intermediates go unwritten
         try:
             self._execute(M, 0, _SeqRows(Lp, kc0[0].numel()))
         finally:
             self._lean = False
+            self._act[out_name] = shared
         # freed in stream order: the caching allocator reuses the token buffers only after the gathers
         del toks
-        return self._act[self.q.output_name][:M].clone()
+        return rows
 
     def generate_batch(self, prompts, n_tokens: int) -> list[dict]:
         """Greedy generation of B = len(prompts) independent sequences of one prompt length: each
