@@ -195,7 +195,14 @@ class _GroupRopeStep:
                 self.launched += 1
                 return
             except ValueError:
-                self.fused = False  # checked before any launch: nothing ran
+                # refused before any launch.  The two launches run instead; only when they take these
+                # operands was the refusal a property of the graph (then the fused entry is not tried
+                # again) -- an error of this call (positions past the table, say) propagates from them
+                # and leaves the fused entry on for later calls
+                self.group(M, pos, pd)
+                self.rope(M, pos, pd)
+                self.fused = False
+                return
         self.group(M, pos, pd)
         self.rope(M, pos, pd)
 
