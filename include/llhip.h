@@ -420,7 +420,8 @@ int llhip_dec_greedy(const void* keys, int64_t nkeys, int32_t* token, int32_t* p
  * hq_out), computes its share of d's 16-column tiles (logits to d->out when non-NULL, the record
  * row at ring[*step] when *step < ring_cap) and its best (value, lowest index) key; the last
  * workgroup to finish takes the greedy step (token, ring_tokens, pos, step, row = embed[token]).
- * d->pre.prequant = 0, d->M = 1, plain epilogue, K a multiple of 64 up to 1024.  keys: the
+ * d->pre.prequant = 0, d->M = 1, plain epilogue, K a multiple of 64 up to 1024, vocab <= N; embed
+ * holds at least vocab rows of dim i16 values (the token is below vocab).  keys: the
  * launch's llhip_dec_logits_keys() uint64 words, zero-filled before the first launch -- the
  * arrival counter returns to zero at the end of each launch.  Launches sharing keys run in order.
  * panel: NULL, or d->W in tile order, which streams in whole 1 KiB pieces: for 16-column tile t, K
