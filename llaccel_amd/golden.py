@@ -903,14 +903,27 @@ class GoldenModel:
 
     # ---- host side --------------------------------------------------------------------------
     def _token_rows(self, tokens) -> np.ndarray:
-        rows = []
+        """Embedding row of each token id, numpy indexing rules (golden.py:369-373 indexes the table
+        with the ids: negative ids count from the end, out-of-range ids raise IndexError)."""
         n = self.embed.shape[0]
-        for t in tokens:
-            t = int(t)
-            if not -n <= t < n:
-                raise IndexError(f"index {t} is out of bounds for axis 0 with size {n}")
-            rows.append(t % n)
-        return np.array(rows, dtype=np.int32)
+        arr = np.asarray(tokens)
+        if arr.dtype.kind == "u" and arr.size and int(arr.max()) >= n:
+            bad_u = arr.reshape(-1) >= n
+            raise IndexError(f"index {int(arr.reshape(-1)[int(np.argmax(bad_u))])} is out of bounds for axis 0 with size {n}")
+        if arr.dtype.kind in "iu":
+            a = arr.astype(np.int64).reshape(-1)
+        else:  # Python ints of any size, or values int() accepts
+            try:
+                a = np.asarray([int(t) for t in tokens], dtype=np.int64)
+            except OverflowError:  # an id beyond int64: report it as numpy would
+                for t in tokens:
+                    if not -n <= int(t) < n:
+                        raise IndexError(f"index {int(t)} is out of bounds for axis 0 with size {n}") from None
+                raise
+        bad = (a < -n) | (a >= n)
+        if bad.any():
+            raise IndexError(f"index {int(a[int(np.argmax(bad))])} is out of bounds for axis 0 with size {n}")
+        return (a % n).astype(np.int32)
 
     def embed_rows(self, tokens, M: int) -> np.ndarray:
         """Embedding rows of `tokens`, zero pad rows up to M (golden.py:369-373)."""
@@ -1178,10 +1191,17 @@ class GoldenModel:
         M = B * Lp
         self._ensure_capacity(M)
         x = self._act[self.q.input_name]
-        toks = [_up(self._token_rows(p), np.int32) for p in prompts]  # alive until the launches ran
-        for b, td in enumerate(toks):
-            _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, _ptr(td),
-                      len(prompts[b]), Lp, _ptr(x[b * Lp]), _stream())
+        # every prompt's token rows in one upload (alive until the gathers ran); prompts that fill
+        # their Lp rows exactly are gathered by one launch, else one launch per prompt pads its rows
+        L = len(prompts[0])
+        toks = _up(np.concatenate([self._token_rows(p) for p in prompts]), np.int32)
+        if L == Lp:
+            _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim, _ptr(toks), M, M,
+                      _ptr(x), _stream())
+        else:
+            for b in range(B):
+                _lib.call("llhip_embed_rows", _ptr(self._dt["embed"]), self.embed.shape[0], self.dim,
+                          ctypes.c_void_p(toks.data_ptr() + 4 * b * L), L, Lp, _ptr(x[b * Lp]), _stream())
         kc0 = next(iter(self._kv.values()))[0]
         out_name = self.q.output_name
         shared = self._act[out_name]
