@@ -535,12 +535,16 @@ class GoldenModel:
         self._slot = 0
         self._kv_gen = getattr(self, "_kv_gen", 0) + 1  # new cache addresses (llaccel_amd.chain keys on it)
         self._kv: dict[int, tuple] = {}
-        for op in self.q.ops:
-            if op["op"] == "kv_write":
-                L, Hkv, D = int(op["layer"]), int(op["Hkv"]), int(op["D"])
-                shape = (slots, Hkv, self.max_seq, D)
-                self._kv[L] = (torch.zeros(shape, dtype=torch.int8, device=self.device),
-                               torch.zeros(shape, dtype=torch.int8, device=self.device))
+        # every layer's K and V as views of ONE zero-filled allocation (one fill launch, not two per
+        # layer); each view starts at a multiple of its (slots, Hkv, max_seq, D) size
+        shapes = [(int(op["layer"]), (slots, int(op["Hkv"]), self.max_seq, int(op["D"])))
+                  for op in self.q.ops if op["op"] == "kv_write"]
+        sizes = [math.prod(sh) for _, sh in shapes]
+        flat = torch.zeros(2 * sum(sizes), dtype=torch.int8, device=self.device)
+        off = 0
+        for (L, sh), n in zip(shapes, sizes):
+            self._kv[L] = (flat[off:off + n].view(sh), flat[off + n:off + 2 * n].view(sh))
+            off += 2 * n
 
     @property
     def kv(self) -> dict[int, tuple[np.ndarray, np.ndarray]]:
