@@ -441,7 +441,7 @@ int64_t llhip_dec_logits_keys(void);
  * golden.py:392-397 (decode) running golden.py:275-314 over the layers of a fused graph whose every
  * layer is  rmsnorm, quant, linear q/k/v (+bias), rope q/k, quant q/k, kv_write, attention,
  * linear o (resadd), rmsnorm, quant, linear gate (silu), linear up (mul), quant, linear down
- * (resadd)  -- the layers of the decode chain above, without Q/K norm, head_dim 64 or 128.
+ * (resadd)  -- the layers of the decode chain above, without Q/K norm, head_dim 64.
  * One persistent workgroup per CU computes its fixed share of each stage (q/k/v columns, an
  * attention head slice with its output-projection partial sums, FFN columns with their
  * down-projection partial sums) and hands results to the next stage's workgroups through

@@ -22,9 +22,9 @@ plan.  The kernels read the output projections in panel layouts made once on the
 wo as [H][dim][D] (a head's K range contiguous) and wd as [FFN/16][dim][16].
 
 Decode step: for a launch at a device position (the decode loop) whose layers have no Q/K norm and
-head_dim 64 or 128, all layers run as one persistent launch instead (llhip_dec_step: the same three
-stages per layer, handed between workgroups inside the launch), followed by the same finish, head
-and greedy launches.  It writes the KV caches and the last layer's residual row and partial sums,
+head_dim 64, all layers run as one persistent launch instead (llhip_dec_step: the same three stages
+per layer, handed between workgroups inside the launch), followed by the one-launch greedy head
+(llhip_dec_logits) where it applies, else the same finish, head and greedy launches.  It writes the KV caches and the last layer's residual row and partial sums,
 not the other activations, so launches that collect activations keep the three launches per layer.
 """
 from __future__ import annotations
