@@ -249,13 +249,15 @@ def test_gate_up_equals_the_three_ops(M, K, N, pad, par):
 
 
 @pytest.mark.parametrize("M,K,N", [(512, 4864, 896), (300, 2048, 576), (300, 896, 896), (40, 896, 896), (16, 896, 896),
-                                   (16, 4864, 896), (5, 2048, 576), (2, 896, 1024)])
+                                   (16, 4864, 896), (5, 2048, 576), (2, 896, 1024), (512, 896, 896), (256, 1024, 576),
+                                   (128, 896, 1024)])
 def test_linear_norm_equals_linear_then_rmsnorm_quant(M, K, N):
     """llhip_linear_norm (a resadd linear, then rmsnorm + quant of its output rows) equals the resadd
     linear checked against the oracle followed by the oracle's rmsnorm and quant: with the split-K
     finishing kernel (512 x 4864 x 896, 300 x 2048 x 576) and with the separate launches (unsplit
-    300 x 896 x 896, the 40-row tiled path, the GEMV rows of a batch decode launch, M <= 16), each
-    twice in a row."""
+    300 x 896 x 896, the 40-row tiled path, the GEMV rows of a batch decode launch, M <= 16, and the
+    prompt's o_proj shapes 512 x 896 x 896, 256 x 1024 x 576, 128 x 896 x 1024), each twice in a row,
+    the first call with another residual."""
     import math
 
     from llaccel_amd import _lib
@@ -276,8 +278,9 @@ def test_linear_norm_equals_linear_then_rmsnorm_quant(M, K, N):
     d = _lib.NormQuantDesc()
     d.x, d.gamma, d.h_out, d.hq_out, d.ldx, d.K = ptr(xd), ptr(gd), ptr(hd), ptr(hqd), N, N
     d.eps_t, d.C, d.sh_post, d.Mq, d.Sq, d.prequant = eps_t, C, sh, qM, qS, 0
-    for _ in range(2):
-        _lib.call("llhip_linear_norm", ptr(ad), M, K, K, ptr(wd), N, ptr(rqd), ptr(bd), ptr(auxd), N, ptr(xd), N,
+    aux_other = up(rng.integers(-20000, 20000, (M, N)), np.int16)
+    for ax in (aux_other, auxd):
+        _lib.call("llhip_linear_norm", ptr(ad), M, K, K, ptr(wd), N, ptr(rqd), ptr(bd), ptr(ax), N, ptr(xd), N,
                   ctypes.byref(d), ptr(workspace()), stream())
     x_want = O.linear_c(a, w, rq, bias, False, "resadd", aux, 0, None)
     assert np.array_equal(down(xd), x_want)
