@@ -152,6 +152,23 @@ def test_split_k_gemm(M, K, N, epilogue, out_i8):
     assert np.array_equal(got[rows], want)
 
 
+@pytest.mark.parametrize("epilogue,out_i8", [("none", True), ("resadd", False)])
+@pytest.mark.parametrize("M,K,N", [(4100, 256, 1000), (8192, 896, 896), (2100, 4864, 300), (16384, 128, 4096)])
+def test_tall_gemm_tile_order(M, K, N, epilogue, out_i8):
+    """GEMMs with at least four times as many rows as columns walk their tiles N-block fastest (an
+    XCD's run of tiles shares A rows): ragged M and N on 128x128 tiles, 448 tiles of 128x128, a split
+    along K on 64x64 tiles, and persistent workgroups (4096 tiles) -- sampled rows against the oracle,
+    all columns."""
+    rng = np.random.default_rng(M + K + N + out_i8)
+    a, w, rq = _operands(rng, M, K, N, out_i8=out_i8)
+    bias = rng.integers(-(2**31), 2**31 - 1, N)
+    aux = rng.integers(-32768, 32768, (M, N)) if epilogue == "resadd" else None
+    got = gpu_linear(a, w, rq, bias=bias, out_i8=out_i8, epilogue=epilogue, aux=aux)
+    rows = np.unique(np.concatenate([np.arange(4), np.arange(M - 70, M), rng.choice(M, 24, replace=False)]))
+    want = O.linear_c(a[rows], w, rq, bias, out_i8, epilogue, None if aux is None else aux[rows], 0, None)
+    assert np.array_equal(got[rows], want)
+
+
 @pytest.mark.parametrize("M,K", [(2048, 896), (512, 896), (300, 896), (300, 576), (37, 128), (64, 100)])
 def test_linear_group_equals_separate_launches(M, K):
     """llhip_linear_group (q, k, v of a prompt chunk in one launch: i16, i16 and i8 outputs, bias
