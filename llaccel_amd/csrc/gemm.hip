@@ -39,9 +39,28 @@ struct LinearArgs {
   int aux_shift, Si, sh;
   int steps;  // ceil(K / 64)
   int cpb;    // linear_gemv: output columns per workgroup (16, or 8 / 4 to spread narrow outputs)
-  int nfast;  // linear_mfma: tiles in N-fastest order (N-block l % nblk), else M-fastest
+  int nfast;   // linear_mfma: tiles in N-fastest order (N-block l % nblk), else M-fastest
   int nblk;
+  int mgroup;  // M-fastest order within groups of mgroup M-blocks (0: one group of all)
 };
+
+// M-block and N-block of logical tile l: N-block fastest (nfast), or M-block fastest within groups
+// of mgroup M-blocks whose A rows fit an L2 together (the groups one after another), or M-block
+// fastest over all of them
+__device__ __forceinline__ void tile_mn(const LinearArgs& p, int mblocks, int l, int& mb, int& nb) {
+  if (p.nfast) {
+    mb = l / p.nblk;
+    nb = l % p.nblk;
+  } else if (p.mgroup && mblocks > p.mgroup) {
+    const int gsz = p.mgroup * p.nblk, g = l / gsz, r = l % gsz;
+    const int gm = min(p.mgroup, mblocks - g * p.mgroup);
+    mb = g * p.mgroup + r % gm;
+    nb = r / gm;
+  } else {
+    mb = l % mblocks;
+    nb = l / mblocks;
+  }
+}
 
 // requant + epilogue of one output element (golden.py:323-342)
 template <int EPI, bool OUT8>
@@ -816,8 +835,8 @@ __device__ __forceinline__ void rope_tile_epilogue(const LinearArgs& p, const v1
   }
 }
 
-// Output tiles l = l0, l0 + lstep, ... < lend (logical index: M-block l % mblocks, N-block
-// l / mblocks; with p.nfast M-block l / p.nblk, N-block l % p.nblk), one after another.  The first stages of the next tile are issued as soon as the
+// Output tiles l = l0, l0 + lstep, ... < lend (logical index l to M- and N-block by tile_mn), one
+// after another.  The first stages of the next tile are issued as soon as the
 // K loop of this one has finished reading the ring, so their memory latency passes during this
 // tile's epilogue (which works from registers only).  The K-loop waits stay correct with the
 // epilogue's stores in flight: vector loads complete in order, so at most n tiles' loads
@@ -842,7 +861,9 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
   const int8_t* wsrc[4];
   const int kbase = (int)blockIdx.y * kps * KT;  // first K byte of this split
   auto sources = [&](int l) {
-    const int m0 = (p.nfast ? l / p.nblk : l % mblocks) * GM, n0 = (p.nfast ? l % p.nblk : l / mblocks) * GN;
+    int mbi, nbi;
+    tile_mn(p, mblocks, l, mbi, nbi);
+    const int m0 = mbi * GM, n0 = nbi * GN;
     const int rl = lane / T::CPR, slot = lane % T::CPR;
 #pragma unroll
     for (int i = 0; i < T::LA; ++i) {
@@ -894,7 +915,9 @@ __device__ __forceinline__ void mfma_tiles(const LinearArgs& p, int mblocks, int
   for (int s0 = 0; s0 < NS; ++s0)
     if (s0 < ktiles) issue(s0);
   for (int l = l0;;) {
-    const int m0 = (p.nfast ? l / p.nblk : l % mblocks) * GM, n0 = (p.nfast ? l % p.nblk : l / mblocks) * GN;
+    int mbi, nbi;
+    tile_mn(p, mblocks, l, mbi, nbi);
+    const int m0 = mbi * GM, n0 = nbi * GN;
     // epilogue column parameters, loaded while the first K tiles stream in
     ColRq cq[T::WN];
 #pragma unroll
@@ -1509,6 +1532,10 @@ static int launch_mfma(LinearArgs& p, void* ws, hipStream_t stream, const NormQu
   // 46.7 -> 41.4 us; at M / N = 2.3 (2048 rows) within +-2 %, so only from four times N
   p.nfast = p.M >= 4ll * p.N ? 1 : 0;
   p.nblk = nblocks;
+  // M-fastest with more A than an XCD's 4 MiB L2 holds (a prompt batch's lm_head): groups of
+  // M-blocks whose A rows take ~2 MiB, so an XCD's run of tiles keeps both its A group and its W
+  // panels in L2
+  p.mgroup = (int64_t)p.M * p.K > (4ll << 20) ? (int)std::max<int64_t>(1, (2ll << 20) / ((int64_t)GM * p.K)) : 0;
   int32_t* part = splits > 1 ? reinterpret_cast<int32_t*>(static_cast<char*>(ws) + WS_SCRATCH) : nullptr;
   if constexpr (deep_ring_fits<GM, GN, KT>()) {
     if (tiles * splits < cus)

@@ -153,12 +153,15 @@ def test_split_k_gemm(M, K, N, epilogue, out_i8):
 
 
 @pytest.mark.parametrize("epilogue,out_i8", [("none", True), ("resadd", False)])
-@pytest.mark.parametrize("M,K,N", [(4100, 256, 1000), (8192, 896, 896), (2100, 4864, 300), (16384, 128, 4096)])
-def test_tall_gemm_tile_order(M, K, N, epilogue, out_i8):
-    """GEMMs with at least four times as many rows as columns walk their tiles N-block fastest (an
-    XCD's run of tiles shares A rows): ragged M and N on 128x128 tiles, 448 tiles of 128x128, a split
-    along K on 64x64 tiles, and persistent workgroups (4096 tiles) -- sampled rows against the oracle,
-    all columns."""
+@pytest.mark.parametrize("M,K,N", [(4100, 256, 1000), (8192, 896, 896), (2100, 4864, 300), (16384, 128, 4096),
+                                   (3000, 2048, 1000), (4608, 1024, 32768)])
+def test_gemm_tile_orders(M, K, N, epilogue, out_i8):
+    """The MFMA GEMM's tile orders.  At least four times as many rows as columns: N-block fastest (an
+    XCD's run of tiles shares A rows) -- ragged M and N on 128x128 tiles, 448 tiles of 128x128, a split
+    along K on 64x64 tiles, persistent workgroups (4096 tiles).  More A than an L2 holds otherwise:
+    M-block fastest within groups of M-blocks -- a partial last group (3000 rows) and persistent
+    workgroups (4608 x 1024 x 32768: groups of 8 256-row or 16 128-row blocks).  Sampled rows against the
+    oracle, all columns."""
     rng = np.random.default_rng(M + K + N + out_i8)
     a, w, rq = _operands(rng, M, K, N, out_i8=out_i8)
     bias = rng.integers(-(2**31), 2**31 - 1, N)
