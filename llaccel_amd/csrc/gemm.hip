@@ -1142,7 +1142,8 @@ __global__ __launch_bounds__(512) void linear_mfma_dual(LinearArgs p, DualArgs d
   const int b = blockIdx.x;
   const int logical = (b % 8) * (int)(gridDim.x / 8) + b / 8;
   if (logical >= mblocks * nblocks) return;
-  const int mb = logical % mblocks, nbk = logical / mblocks;
+  int mb, nbk;
+  tile_mn(p, mblocks, logical, mb, nbk);  // M-block fastest, in groups when A exceeds an L2
   const int m0 = mb * GM, n0 = nbk * GN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool upw = wave >= 4;  // wave-uniform role: waves 0-3 gate (and the A loads), 4-7 up
@@ -1859,10 +1860,14 @@ extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {
   a.fqS = (int)d->fq_S;
   a.mul_sh = (int)d->mul_sh;
   const int mblocks = (int)ceil_div(M, 64);
+  // tiles M-block fastest (consecutive workgroups share the gate and up panels), the M-blocks in
+  // groups of ~2 MiB of A rows when A exceeds an XCD's 4 MiB L2 (a prompt batch)
+  p.mgroup = M * K > (4ll << 20) ? (int)std::max<int64_t>(1, (2ll << 20) / (64 * K)) : 0;
   // 64x64 tiles (48 KB rings) while they number at most three per CU (512 x 896 x 4864
   // 18.6 -> 17.6 us, 256 rows 14.1 -> 12.6 us), else 64x128
   if (p.K % 128 == 0 && (int64_t)mblocks * ceil_div(N, 64) <= 3ll * current_cu_count()) {
     const int nblocks = (int)ceil_div(N, 64);
+    p.nblk = nblocks;
     const dim3 grid((unsigned)(ceil_div((int64_t)mblocks * nblocks, 8) * 8));
     hipLaunchKernelGGL((linear_mfma_dual<128, 2, 64>), grid, dim3(512), 2 * (64 + 2 * 64) * 128, s, p, a, mblocks,
                        nblocks);
@@ -1870,6 +1875,7 @@ extern "C" int llhip_gate_up(const llhip_gate_up_desc* d, void* stream) {
     return 0;
   }
   const int nblocks = (int)ceil_div(N, 128);
+  p.nblk = nblocks;
   const dim3 grid((unsigned)(ceil_div((int64_t)mblocks * nblocks, 8) * 8));
   if (p.K % 128 == 0)
     hipLaunchKernelGGL((linear_mfma_dual<128, 2>), grid, dim3(512), 2 * (64 + 2 * 128) * 128, s, p, a, mblocks, nblocks);

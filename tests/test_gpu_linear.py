@@ -217,12 +217,14 @@ PARAMS = [(1 << 30, 30, 16, 11, 1518500250, 38), ((1 << 32) - 1, 0, 31, 31, (1 <
 @pytest.mark.parametrize("M,K,N,pad,par", [(512, 896, 4864, 0, 0), (512, 896, 4864, 5, 0), (1024, 256, 4864, 0, 0),
                                            (300, 128, 200, 4, 0),
                                            (200, 192, 256, 0, 0),
-                                           (40, 100, 64, 5, 0)] + [(70, 128, 256, 0, i) for i in range(1, 5)])
+                                           (40, 100, 64, 5, 0), (5000, 1024, 1000, 4, 0)]
+                         + [(70, 128, 256, 0, i) for i in range(1, 5)])
 def test_gate_up_equals_the_three_ops(M, K, N, pad, par):
     """llhip_gate_up (gate linear with the silu epilogue, up linear with the mul epilogue on the
     gate's output, quant of the product, in one launch) equals the three ops run one by one; output
     rows of N + pad elements (pad 0 and 4: the word stores, 5: element stores); 64x64 tiles up to
-    three workgroups per CU, 64x128 beyond (1024 rows) and for 64-byte K tiles; K = 100 runs the
+    three workgroups per CU, 64x128 beyond (1024 rows) and for 64-byte K tiles, their M-blocks in groups
+    when A exceeds an L2 (5000 x 1024: groups of 32, 32 and 15 64-row blocks); K = 100 runs the
     op-by-op fallback inside the entry point; PARAMS[1:] put every shift at its extremes."""
     from llaccel_amd import _lib
     from oracle import golden_np as OO
