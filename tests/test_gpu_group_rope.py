@@ -2,8 +2,9 @@
 and k rows and the layer's K/V cache write as the GEMM's epilogue, one launch) against
 llhip_linear_group followed by llhip_rope_quant2, bit-exact in every output: the three linear outputs,
 the rotated and quantised q and k rows and both caches -- 64x64 tiles (512 and 40 rows) and 64x128
-tiles (2100 rows), positions from the argument, from a device word, per row (own cache slots) and
-per sequence of a batched prefill -- and the oracle's rope and quant on one case."""
+tiles (2100 and 4608 rows, the latter more A than an L2 holds), positions from the
+argument, from a device word, per row (own cache slots) and per sequence of a batched prefill -- and
+the oracle's rope and quant on one case."""
 from __future__ import annotations
 
 import ctypes
@@ -45,7 +46,7 @@ class _Run:
 
 
 @pytest.mark.parametrize("M,K,mode", [(512, 896, "pos"), (40, 896, "pos"), (2100, 1024, "pos"), (100, 896, "pos_dev"),
-                                      (64, 896, "row_pos"), (128, 896, "seq_rows")])
+                                      (64, 896, "row_pos"), (128, 896, "seq_rows"), (4608, 1024, "seq_rows")])
 def test_group_rope_equals_group_then_rope_quant2(M, K, mode):
     t = torch()
     rng = np.random.default_rng(M + K)

@@ -172,7 +172,7 @@ def test_gemm_tile_orders(M, K, N, epilogue, out_i8):
     assert np.array_equal(got[rows], want)
 
 
-@pytest.mark.parametrize("M,K", [(2048, 896), (512, 896), (300, 896), (300, 576), (37, 128), (64, 100)])
+@pytest.mark.parametrize("M,K", [(2048, 896), (512, 896), (300, 896), (300, 576), (37, 128), (64, 100), (5000, 1024)])
 def test_linear_group_equals_separate_launches(M, K):
     """llhip_linear_group (q, k, v of a prompt chunk in one launch: i16, i16 and i8 outputs, bias
     on two of them) equals one llhip_linear launch per problem: 64x64 tiles (512 and 300 rows,
