@@ -180,6 +180,54 @@ def test_argmax_row_lengths_and_tails(vocab):
         assert idx.cpu().numpy().tolist() == [int(np.argmax(r)) for r in rows], ld
 
 
+@pytest.mark.parametrize("vocab", [1, 7, 8, 9, 2047, 65537, 151936])
+def test_greedy_rows_argmax_record_and_positions(vocab):
+    """llhip_greedy_rows (the batch decode's greedy step) against numpy's argmax per row (the first
+    index of the maximum, golden.py's greedy choice): every tail length of the 16-byte chunks, ties
+    across chunks and threads, values past vocab never chosen; row r recorded at ring slot
+    s = positions[r] - base[r] only when 0 <= s < ring_cap (rows and tokens elsewhere untouched),
+    at a record stride that is a multiple of 8 (16-byte stores) and at an odd one; positions + 1."""
+    from llaccel_amd import _lib
+    from tests.gpu_helpers import ptr, stream, torch, up
+
+    t = torch()
+    R, cap = 5, 3
+    rows = RNG.integers(-32768, 32767, (R, vocab))
+    rows[1, -1] = 32767  # the last value
+    rows[2, :] = -5
+    rows[2, [vocab // 3, vocab - 1]] = 9  # a tie: the lower index wins
+    rows[3, :] = 32767  # all equal: index 0
+    want = [int(np.argmax(r)) for r in rows]
+    base = np.array([100, 7, 0, 50, 3], np.int32)
+    pos = base + np.array([0, 2, cap, -1, 1], np.int32)  # slots 0, 2, none (= cap), none (< 0), 1
+    ld = vocab + (vocab & 1)
+    for ring_ld in (vocab + (-vocab) % 8, vocab + 1 + vocab % 2):  # a multiple of 8, odd
+        buf = np.full((R, ld), 32767, np.int64)
+        buf[:, :vocab] = rows  # past vocab: never chosen
+        d = up(buf, np.int16)
+        tok = t.full((R,), -1, dtype=t.int32, device="cuda")
+        posd = t.tensor(pos, dtype=t.int32, device="cuda")
+        based = t.tensor(base, dtype=t.int32, device="cuda")
+        ring = t.full((cap * R * ring_ld,), -7, dtype=t.int16, device="cuda")
+        ring_tok = t.full((cap * R,), -3, dtype=t.int32, device="cuda")
+        _lib.call("llhip_greedy_rows", ptr(d), R, ld, vocab, ptr(tok), ptr(posd), ptr(based), ptr(ring), ring_ld,
+                  ptr(ring_tok), cap, stream())
+        t.cuda.synchronize()
+        assert tok.cpu().numpy().tolist() == want, ring_ld
+        assert np.array_equal(posd.cpu().numpy(), pos + 1)
+        got_ring = ring.cpu().numpy().reshape(cap, R, ring_ld)
+        got_tok = ring_tok.cpu().numpy().reshape(cap, R)
+        exp_ring = np.full((cap, R, ring_ld), -7, np.int64)
+        exp_tok = np.full((cap, R), -3, np.int64)
+        for r in range(R):
+            s = int(pos[r] - base[r])
+            if 0 <= s < cap:
+                exp_ring[s, r, :vocab] = rows[r]
+                exp_tok[s, r] = want[r]
+        assert np.array_equal(got_ring, exp_ring), ring_ld
+        assert np.array_equal(got_tok, exp_tok), ring_ld
+
+
 def test_argmax_lowest_index_on_ties():
     row = np.zeros(151936, np.int64)
     row[[5, 100, 151935]] = 7
